@@ -1,0 +1,342 @@
+// IMI cell index on gfx950: stable cell order, CSR over global cells, compact
+// metadata and the K/V row permutation.
+//
+// Reference: library/AdaptiveIMI/cpp_extensions/src/reorganize_core.cpp
+//   build_compact_reorg_input   18-85 (2-way), 87-176 (4-way)
+//   reorganize_single_head      234-311 (stable counting sort by compact cell,
+//                               then the K/V row copy)
+// and the padded metadata of pipeline_bindings.cpp:206-276 /
+// indexing.py:108-174.
+//
+// The cell order is produced by an LSD sort with one stable counting pass per
+// subspace label (last subspace first), which yields tokens ordered by
+// (l0, l1, ..., token) = (global cell id, token): the reference's CSR order,
+// because compact ids are ranks of global ids.
+#include "imi_common.hpp"
+#include "imi_sort.hpp"
+
+namespace imi {
+namespace {
+
+struct IxParams {
+    const int32_t* labels;  // [H][P][T]
+    int H, T, P, kmax;
+    int k[4];
+    int64_t ncells;
+    int nblk;
+    int32_t* hist;   // [H][kmax][nblk]
+    int32_t* rank;   // [H][T]
+    int32_t* cid;    // [H][ncells] compact id scratch
+};
+
+__host__ __device__ inline int bits_for(int n) {
+    int b = 0;
+    while ((1 << b) < n) ++b;
+    return b;
+}
+
+__global__ __launch_bounds__(256) void ix_rank_kernel(IxParams a, int p, const int32_t* in) {
+    __shared__ int wcnt[4 * 256];
+    const int h = blockIdx.y, blk = blockIdx.x;
+    const int pos = blk * 256 + threadIdx.x;
+    const bool valid = pos < a.T;
+    const int64_t hT = static_cast<int64_t>(h) * a.T;
+    int digit = 0;
+    if (valid) {
+        const int item = in ? in[hT + pos] : pos;
+        digit = a.labels[(static_cast<int64_t>(h) * a.P + p) * a.T + item];
+    }
+    const int r = block_digit_rank(digit, valid, a.k[p], bits_for(a.k[p]), wcnt,
+                                   a.hist + static_cast<int64_t>(h) * a.kmax * a.nblk, a.nblk, blk);
+    if (valid) a.rank[hT + pos] = r;
+}
+
+__global__ __launch_bounds__(1024) void ix_scan_kernel(IxParams a, int p) {
+    __shared__ int sh[40];
+    const int h = blockIdx.x;
+    block_exclusive_scan_1024(a.hist + static_cast<int64_t>(h) * a.kmax * a.nblk,
+                              static_cast<int64_t>(a.k[p]) * a.nblk, sh);
+}
+
+__global__ __launch_bounds__(256) void ix_scatter_kernel(IxParams a, int p, const int32_t* in, int32_t* out) {
+    const int h = blockIdx.y, blk = blockIdx.x;
+    const int pos = blk * 256 + threadIdx.x;
+    if (pos >= a.T) return;
+    const int64_t hT = static_cast<int64_t>(h) * a.T;
+    const int item = in ? in[hT + pos] : pos;
+    const int digit = a.labels[(static_cast<int64_t>(h) * a.P + p) * a.T + item];
+    const int dst = a.hist[(static_cast<int64_t>(h) * a.kmax + digit) * a.nblk + blk] + a.rank[hT + pos];
+    out[hT + dst] = item;
+}
+
+__device__ __forceinline__ int64_t cell_of(const IxParams& a, int h, int t) {
+    int64_t g = 0;
+    for (int p = 0; p < a.P; ++p) g = g * a.k[p] + a.labels[(static_cast<int64_t>(h) * a.P + p) * a.T + t];
+    return g;
+}
+
+__global__ void ix_zero_kernel(int32_t* x, int64_t n) {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        x[i] = 0;
+}
+
+__global__ __launch_bounds__(256) void ix_count_kernel(IxParams a, int32_t* count) {
+    const int h = blockIdx.y;
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= a.T) return;
+    atomicAdd(&count[static_cast<int64_t>(h) * a.ncells + cell_of(a, h, t)], 1);
+}
+
+// offsets[h][g] = exclusive prefix of count (offsets[h][ncells] = T); when
+// compact metadata is requested also cid[h][g] = exclusive prefix of the
+// occupied flags and n_active[h].
+__global__ __launch_bounds__(1024) void ix_offsets_kernel(IxParams a, const int32_t* count, int32_t* offset,
+                                                          int32_t* n_active) {
+    __shared__ int sh[40];
+    const int h = blockIdx.x;
+    const int32_t* c = count + static_cast<int64_t>(h) * a.ncells;
+    int32_t* o = offset + static_cast<int64_t>(h) * (a.ncells + 1);
+    for (int64_t g = threadIdx.x; g < a.ncells; g += 1024) o[g] = c[g];
+    __syncthreads();
+    const int total = block_exclusive_scan_1024(o, a.ncells, sh);
+    if (threadIdx.x == 0) o[a.ncells] = total;
+    if (a.cid == nullptr) return;
+    int32_t* id = a.cid + static_cast<int64_t>(h) * a.ncells;
+    for (int64_t g = threadIdx.x; g < a.ncells; g += 1024) id[g] = c[g] > 0 ? 1 : 0;
+    __syncthreads();
+    const int act = block_exclusive_scan_1024(id, a.ncells, sh);
+    if (threadIdx.x == 0) n_active[h] = act;
+}
+
+struct CompactOut {
+    int n_c;
+    const float* cent;  // [H][P][kmax][DP]
+    int DP, D;
+    int32_t* gid;
+    int32_t* size;
+    int32_t* offset;
+    float* merged;
+    uint8_t* mask;
+};
+
+// One wave per global cell: occupied cells write their compact slot.
+__global__ __launch_bounds__(256) void ix_compact_fill_kernel(IxParams a, CompactOut o, const int32_t* count,
+                                                              const int32_t* offset) {
+    const int h = blockIdx.y;
+    const int64_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (g >= a.ncells) return;
+    const int cnt = count[static_cast<int64_t>(h) * a.ncells + g];
+    if (cnt == 0) return;
+    const int c = a.cid[static_cast<int64_t>(h) * a.ncells + g];
+    const int64_t hc = static_cast<int64_t>(h) * o.n_c + c;
+    const int lane = lane_id();
+    if (lane == 0) {
+        o.gid[hc] = static_cast<int32_t>(g);
+        o.size[hc] = cnt;
+        o.offset[static_cast<int64_t>(h) * (o.n_c + 1) + c] = offset[static_cast<int64_t>(h) * (a.ncells + 1) + g];
+        o.mask[hc] = 0;
+    }
+    // merged centroid = [C_0[l0] | C_1[l1] | ...]
+    int64_t rem = g;
+    int lab[4] = {0, 0, 0, 0};
+    for (int p = a.P - 1; p >= 0; --p) {
+        lab[p] = static_cast<int>(rem % a.k[p]);
+        rem /= a.k[p];
+    }
+    for (int d = lane; d < o.D; d += 64) {
+        const int p = d / o.DP;
+        o.merged[hc * o.D + d] =
+            o.cent[((static_cast<int64_t>(h) * a.P + p) * a.kmax + lab[p]) * o.DP + (d - p * o.DP)];
+    }
+}
+
+// Padding slots c >= n_active (and the closing offset).
+__global__ __launch_bounds__(256) void ix_compact_pad_kernel(IxParams a, CompactOut o, const int32_t* n_active) {
+    const int h = blockIdx.y;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    const int na = n_active[h];
+    if (c == 0) o.offset[static_cast<int64_t>(h) * (o.n_c + 1) + o.n_c] = a.T;
+    if (c >= o.n_c || c < na) return;
+    const int64_t hc = static_cast<int64_t>(h) * o.n_c + c;
+    o.gid[hc] = -1;
+    o.size[hc] = 0;
+    o.offset[static_cast<int64_t>(h) * (o.n_c + 1) + c] = a.T;
+    o.mask[hc] = 1;
+    for (int d = 0; d < o.D; ++d) o.merged[hc * o.D + d] = 0.0f;
+}
+
+// list[h][pos] = src[h][perm[h][pos]] for keys and values; 16 lanes per
+// 256-byte row, 16 rows per wave.
+__global__ __launch_bounds__(256) void ix_permute_kernel(const uint16_t* keys, const uint16_t* values, int64_t hs,
+                                                         int64_t ts, int T, const int32_t* perm, uint16_t* lk,
+                                                         uint16_t* lv, int64_t list_rows) {
+    const int h = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = lane_id();
+    const int rg = lane >> 4, li = lane & 15;
+    const int base = blockIdx.x * 64 + wave * 16;
+    uint4 kv[4], vv[4];
+    int dst[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int pos = base + it * 4 + rg;
+        dst[it] = pos;
+        if (pos < T) {
+            const int t = perm[static_cast<int64_t>(h) * T + pos];
+            const int64_t so = h * hs + static_cast<int64_t>(t) * ts + li * 8;
+            kv[it] = *reinterpret_cast<const uint4*>(keys + so);
+            vv[it] = *reinterpret_cast<const uint4*>(values + so);
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        if (dst[it] < T) {
+            const int64_t dofs = (static_cast<int64_t>(h) * list_rows + dst[it]) * 128 + li * 8;
+            *reinterpret_cast<uint4*>(lk + dofs) = kv[it];
+            *reinterpret_cast<uint4*>(lv + dofs) = vv[it];
+        }
+    }
+}
+
+int validate(const imi_index_args* a, int& kmax, int64_t& ncells) {
+    IMI_REQUIRE(a != nullptr, IMI_ERR_INVALID, "imi_build_index: null args");
+    IMI_REQUIRE(a->keys && a->values && a->labels && a->cell_count && a->cell_offset && a->perm &&
+                    a->list_keys && a->list_values,
+                IMI_ERR_INVALID, "imi_build_index: null pointer argument");
+    IMI_REQUIRE(a->kv_heads > 0 && a->n_tokens > 0, IMI_ERR_INVALID, "imi_build_index: empty input");
+    IMI_REQUIRE(a->dim == 128, IMI_ERR_UNSUPPORTED, "imi_build_index: head_dim must be 128 (got %d)", a->dim);
+    IMI_REQUIRE(a->parts == 2 || a->parts == 4, IMI_ERR_UNSUPPORTED, "imi_build_index: parts must be 2 or 4");
+    IMI_REQUIRE(a->list_rows >= a->n_tokens, IMI_ERR_INVALID, "imi_build_index: list_rows %lld < n_tokens %d",
+                static_cast<long long>(a->list_rows), a->n_tokens);
+    IMI_REQUIRE((a->token_stride % 8) == 0 && (a->head_stride % 8) == 0, IMI_ERR_INVALID,
+                "imi_build_index: strides must be multiples of 8 elements");
+    kmax = 0;
+    ncells = 1;
+    for (int p = 0; p < a->parts; ++p) {
+        IMI_REQUIRE(a->k[p] >= 1 && a->k[p] <= 256, IMI_ERR_UNSUPPORTED, "imi_build_index: k[%d]=%d outside [1,256]",
+                    p, a->k[p]);
+        kmax = a->k[p] > kmax ? a->k[p] : kmax;
+        ncells *= a->k[p];
+    }
+    IMI_REQUIRE(ncells <= (int64_t(1) << 26), IMI_ERR_UNSUPPORTED, "imi_build_index: %lld cells exceed 2^26",
+                static_cast<long long>(ncells));
+    const bool compact = a->compact_gid || a->compact_size || a->compact_offset || a->compact_centroids ||
+                         a->compact_mask || a->n_active;
+    if (compact) {
+        IMI_REQUIRE(a->compact_gid && a->compact_size && a->compact_offset && a->compact_centroids &&
+                        a->compact_mask && a->n_active && a->centroids,
+                    IMI_ERR_INVALID, "imi_build_index: compact outputs must be all set or all NULL");
+        const int64_t max_active = ncells < a->n_tokens ? ncells : a->n_tokens;
+        IMI_REQUIRE(a->n_centroids >= max_active, IMI_ERR_INVALID,
+                    "imi_build_index: n_centroids %d < possible occupied cells %lld", a->n_centroids,
+                    static_cast<long long>(max_active));
+    }
+    return IMI_OK;
+}
+
+size_t workspace_bytes(const imi_index_args* a, int kmax, int64_t ncells, IxParams* p, int32_t** tmp) {
+    const int nblk = (a->n_tokens + 255) / 256;
+    Carver cv(a->workspace);
+    IxParams q{};
+    q.hist = cv.take<int32_t>(static_cast<size_t>(a->kv_heads) * kmax * nblk);
+    q.rank = cv.take<int32_t>(static_cast<size_t>(a->kv_heads) * a->n_tokens);
+    q.cid = cv.take<int32_t>(static_cast<size_t>(a->kv_heads) * ncells);
+    int32_t* t = cv.take<int32_t>(static_cast<size_t>(a->kv_heads) * a->n_tokens);
+    if (p) *p = q;
+    if (tmp) *tmp = t;
+    return cv.used();
+}
+
+}  // namespace
+}  // namespace imi
+
+using namespace imi;
+
+extern "C" int imi_index_workspace_size(const imi_index_args* a, size_t* bytes) {
+    clear_error();
+    int kmax;
+    int64_t ncells;
+    int rc = validate(a, kmax, ncells);
+    if (rc) return rc;
+    IMI_REQUIRE(bytes != nullptr, IMI_ERR_INVALID, "imi_index_workspace_size: null output");
+    imi_index_args tmp = *a;
+    tmp.workspace = nullptr;
+    *bytes = workspace_bytes(&tmp, kmax, ncells, nullptr, nullptr);
+    return IMI_OK;
+}
+
+extern "C" int imi_build_index(const imi_index_args* a, imi_stream_t stream_) {
+    clear_error();
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    int kmax;
+    int64_t ncells;
+    int rc = validate(a, kmax, ncells);
+    if (rc) return rc;
+    imi_index_args tmp = *a;
+    tmp.workspace = nullptr;
+    const size_t need = workspace_bytes(&tmp, kmax, ncells, nullptr, nullptr);
+    IMI_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= need, IMI_ERR_WORKSPACE,
+                "imi_build_index: workspace %zu bytes < %zu required", a->workspace_bytes, need);
+    IxParams p;
+    int32_t* scratch;
+    workspace_bytes(a, kmax, ncells, &p, &scratch);
+    p.labels = a->labels;
+    p.H = a->kv_heads;
+    p.T = a->n_tokens;
+    p.P = a->parts;
+    p.kmax = kmax;
+    for (int i = 0; i < 4; ++i) p.k[i] = i < a->parts ? a->k[i] : 1;
+    p.ncells = ncells;
+    p.nblk = (a->n_tokens + 255) / 256;
+    const bool compact = a->compact_gid != nullptr;
+    if (!compact) p.cid = nullptr;
+
+    // LSD passes: last subspace first; the final pass lands in a->perm.
+    const int32_t* in = nullptr;
+    for (int pass = 0; pass < a->parts; ++pass) {
+        const int part = a->parts - 1 - pass;
+        int32_t* out = ((a->parts - 1 - pass) % 2 == 0) ? a->perm : scratch;
+        hipLaunchKernelGGL(ix_rank_kernel, dim3(p.nblk, p.H), dim3(256), 0, stream, p, part, in);
+        IMI_LAUNCH_CHECK("ix_rank_kernel");
+        hipLaunchKernelGGL(ix_scan_kernel, dim3(p.H), dim3(1024), 0, stream, p, part);
+        IMI_LAUNCH_CHECK("ix_scan_kernel");
+        hipLaunchKernelGGL(ix_scatter_kernel, dim3(p.nblk, p.H), dim3(256), 0, stream, p, part, in, out);
+        IMI_LAUNCH_CHECK("ix_scatter_kernel");
+        in = out;
+    }
+
+    const int64_t cells_total = ncells * p.H;
+    hipLaunchKernelGGL(ix_zero_kernel, dim3(static_cast<unsigned>((cells_total + 255) / 256 < 65535 ? (cells_total + 255) / 256 : 65535)),
+                       dim3(256), 0, stream, a->cell_count, cells_total);
+    IMI_LAUNCH_CHECK("ix_zero_kernel");
+    hipLaunchKernelGGL(ix_count_kernel, dim3(p.nblk, p.H), dim3(256), 0, stream, p, a->cell_count);
+    IMI_LAUNCH_CHECK("ix_count_kernel");
+    hipLaunchKernelGGL(ix_offsets_kernel, dim3(p.H), dim3(1024), 0, stream, p, a->cell_count, a->cell_offset,
+                       a->n_active);
+    IMI_LAUNCH_CHECK("ix_offsets_kernel");
+
+    if (compact) {
+        CompactOut o;
+        o.n_c = a->n_centroids;
+        o.cent = a->centroids;
+        o.D = a->dim;
+        o.DP = a->dim / a->parts;
+        o.gid = a->compact_gid;
+        o.size = a->compact_size;
+        o.offset = a->compact_offset;
+        o.merged = a->compact_centroids;
+        o.mask = a->compact_mask;
+        hipLaunchKernelGGL(ix_compact_fill_kernel, dim3(static_cast<unsigned>((ncells + 3) / 4), p.H), dim3(256), 0,
+                           stream, p, o, a->cell_count, a->cell_offset);
+        IMI_LAUNCH_CHECK("ix_compact_fill_kernel");
+        hipLaunchKernelGGL(ix_compact_pad_kernel, dim3((o.n_c + 256) / 256, p.H), dim3(256), 0, stream, p, o,
+                           a->n_active);
+        IMI_LAUNCH_CHECK("ix_compact_pad_kernel");
+    }
+
+    hipLaunchKernelGGL(ix_permute_kernel, dim3((a->n_tokens + 63) / 64, p.H), dim3(256), 0, stream, a->keys,
+                       a->values, a->head_stride, a->token_stride, a->n_tokens, a->perm, a->list_keys,
+                       a->list_values, a->list_rows);
+    IMI_LAUNCH_CHECK("ix_permute_kernel");
+    return IMI_OK;
+}

@@ -1,0 +1,427 @@
+// Per-(head, subspace) Lloyd k-means on gfx950.
+//
+// Reference: library/AdaptiveIMI/cpp_extensions/src/kmeans_core.cpp
+//   distance     22-44   (8 FMA lanes, lane sums left to right)
+//   E-step       222-242 (argmin, strict '<': lowest index wins ties)
+//   early stop   244-262
+//   M-step       265-312 (members summed in ascending token order, times
+//                          1.0f/size; empty cluster <- x[uniform draw])
+//   executor     384-501 (one independent run per (head, subspace))
+//
+// Work layout: every kernel covers all H*P (head, subspace) segments at once.
+// The E-step keeps one token's subvector in registers (Dp fp32) and streams
+// the segment's centroids from LDS (broadcast reads); it also emits the block
+// histogram of labels and each token's stable rank inside its block, so the
+// M-step's member lists come from one scan + one scatter, and the M-step sums
+// each cluster sequentially in ascending token order (the reference's order
+// with one thread per subspace run).
+#include <random>
+#include <vector>
+
+#include "imi_common.hpp"
+#include "imi_sort.hpp"
+
+namespace imi {
+namespace {
+
+struct KmParams {
+    const uint16_t* keys;
+    int64_t hs, ts;
+    int H, T, P, kmax, DP;
+    int k[4];
+    float* cent;       // [seg][kmax][DP]
+    int32_t* labels;   // [seg][T]
+    float* mind;       // [seg][T] or null
+    int32_t* hist;     // [seg][kmax][nblk] or null
+    int32_t* rank;     // [seg][T]
+    float* ipart;      // [seg][nblk]
+    int32_t* sorted;   // [seg][T]
+    int32_t* off;      // [seg][kmax + 1]
+    int32_t* empties;  // [seg][kmax]
+    float* prev;       // [seg]
+    int32_t* done;     // [seg] or null
+    int32_t* iters;    // [seg] or null
+    int nblk;
+    int max_iters;
+    float tol;
+    int es_min;
+    float es_rel;
+};
+
+struct Draws {
+    int32_t v[256];  // uniform draws for the empty clusters of one iteration
+};
+
+__host__ __device__ inline int bits_for(int n) {
+    int b = 0;
+    while ((1 << b) < n) ++b;
+    return b;
+}
+
+__global__ __launch_bounds__(64) void km_init_first_kernel(KmParams a) {
+    const int c = blockIdx.x, seg = blockIdx.y;
+    const int h = seg / a.P, p = seg % a.P;
+    if (c >= a.k[p]) return;
+    for (int d = threadIdx.x; d < a.DP; d += 64)
+        a.cent[(static_cast<int64_t>(seg) * a.kmax + c) * a.DP + d] =
+            bf16_to_f32(a.keys[h * a.hs + static_cast<int64_t>(c) * a.ts + p * a.DP + d]);
+}
+
+// Reference distance between the register-resident subvector x and centroid
+// row cr (LDS): lane j accumulates dims j, j+8, ... with fused multiply-add,
+// then the eight lane sums are added left to right.
+template <int DP>
+__device__ __forceinline__ float l2_lanes8(const float (&x)[DP], const float* cr) {
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < DP; i += 8) {
+        const float4 c0 = *reinterpret_cast<const float4*>(cr + i);
+        const float4 c1 = *reinterpret_cast<const float4*>(cr + i + 4);
+        float d;
+        d = x[i + 0] - c0.x; acc[0] = __builtin_fmaf(d, d, acc[0]);
+        d = x[i + 1] - c0.y; acc[1] = __builtin_fmaf(d, d, acc[1]);
+        d = x[i + 2] - c0.z; acc[2] = __builtin_fmaf(d, d, acc[2]);
+        d = x[i + 3] - c0.w; acc[3] = __builtin_fmaf(d, d, acc[3]);
+        d = x[i + 4] - c1.x; acc[4] = __builtin_fmaf(d, d, acc[4]);
+        d = x[i + 5] - c1.y; acc[5] = __builtin_fmaf(d, d, acc[5]);
+        d = x[i + 6] - c1.z; acc[6] = __builtin_fmaf(d, d, acc[6]);
+        d = x[i + 7] - c1.w; acc[7] = __builtin_fmaf(d, d, acc[7]);
+    }
+    float t = acc[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) t = t + acc[j];
+    return t;
+}
+
+// E-step over one block of 256 tokens of one segment.
+template <int DP>
+__global__ __launch_bounds__(256) void km_assign_kernel(KmParams a) {
+    extern __shared__ float smem[];
+    const int seg = blockIdx.y, blk = blockIdx.x;
+    if (a.done && a.done[seg]) return;
+    const int h = seg / a.P, p = seg % a.P;
+    const int k = a.k[p];
+    const int tid = threadIdx.x;
+    float* cs = smem;                                   // [k][DP]
+    int* wcnt = reinterpret_cast<int*>(smem + a.kmax * DP);  // [4][kmax]
+    float* red = reinterpret_cast<float*>(wcnt + 4 * a.kmax);  // [4]
+
+    const float* cg = a.cent + static_cast<int64_t>(seg) * a.kmax * DP;
+    for (int i = tid; i < k * DP; i += 256) cs[i] = cg[i];
+
+    const int t = blk * 256 + tid;
+    const bool valid = t < a.T;
+    float x[DP];
+    if (valid) {
+        const uint4* src = reinterpret_cast<const uint4*>(a.keys + h * a.hs + static_cast<int64_t>(t) * a.ts + p * DP);
+#pragma unroll
+        for (int i = 0; i < DP / 8; ++i) {
+            const uint4 v = src[i];
+            x[8 * i + 0] = bf16_lo(v.x); x[8 * i + 1] = bf16_hi(v.x);
+            x[8 * i + 2] = bf16_lo(v.y); x[8 * i + 3] = bf16_hi(v.y);
+            x[8 * i + 4] = bf16_lo(v.z); x[8 * i + 5] = bf16_hi(v.z);
+            x[8 * i + 6] = bf16_lo(v.w); x[8 * i + 7] = bf16_hi(v.w);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < DP; ++i) x[i] = 0.0f;
+    }
+    __syncthreads();
+
+    float best = 3.402823466e38f;  // FLT_MAX
+    int arg = 0;
+    for (int c = 0; c < k; ++c) {
+        const float dist = l2_lanes8<DP>(x, cs + c * DP);
+        if (dist < best) {
+            best = dist;
+            arg = c;
+        }
+    }
+    if (valid) {
+        a.labels[static_cast<int64_t>(seg) * a.T + t] = arg;
+        if (a.mind) a.mind[static_cast<int64_t>(seg) * a.T + t] = best;
+    }
+    if (a.hist == nullptr) return;
+
+    // inertia partial of this block (fixed reduction order)
+    float part = wave_sum(valid ? best : 0.0f);
+    if (lane_id() == 0) red[tid >> 6] = part;
+    const int r = block_digit_rank(arg, valid, k, bits_for(k), wcnt,
+                                   a.hist + static_cast<int64_t>(seg) * a.kmax * a.nblk, a.nblk, blk);
+    if (valid) a.rank[static_cast<int64_t>(seg) * a.T + t] = r;
+    if (tid == 0) a.ipart[static_cast<int64_t>(seg) * a.nblk + blk] = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// Per segment: exclusive scan of the [label][block] counts, cluster offsets,
+// empty-cluster ordinals, inertia and the early-stop test.
+__global__ __launch_bounds__(1024) void km_scan_kernel(KmParams a, int it) {
+    __shared__ int sh[40];
+    __shared__ int stop;
+    const int seg = blockIdx.x;
+    if (a.done && a.done[seg]) return;
+    const int p = seg % a.P;
+    const int k = a.k[p];
+    int32_t* hist = a.hist + static_cast<int64_t>(seg) * a.kmax * a.nblk;
+    block_exclusive_scan_1024(hist, static_cast<int64_t>(k) * a.nblk, sh);
+    int32_t* off = a.off + static_cast<int64_t>(seg) * (a.kmax + 1);
+    for (int c = threadIdx.x; c < k; c += 1024) off[c] = hist[static_cast<int64_t>(c) * a.nblk];
+    if (threadIdx.x == 0) off[k] = a.T;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int e = 0;
+        int32_t* emp = a.empties + static_cast<int64_t>(seg) * a.kmax;
+        for (int c = 0; c < k; ++c) {
+            emp[c] = e;
+            if (off[c + 1] == off[c]) ++e;
+        }
+        float inertia = 0.0f;
+        const float* ip = a.ipart + static_cast<int64_t>(seg) * a.nblk;
+        for (int b = 0; b < a.nblk; ++b) inertia += ip[b];
+        if (a.iters) a.iters[seg] = it + 1;
+        const float prev = a.prev[seg];
+        const float change = fabsf(prev - inertia);
+        const float rel = prev > 0.0f ? change / prev : 0.0f;
+        const bool min_ok = (it + 1) >= (a.es_min > 1 ? a.es_min : 1);
+        stop = min_ok && (rel <= fmaxf(0.0f, a.es_rel) || change <= fmaxf(0.0f, a.tol));
+        if (!stop) a.prev[seg] = inertia;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0 && stop && a.done) a.done[seg] = 1;
+}
+
+__global__ __launch_bounds__(256) void km_scatter_kernel(KmParams a) {
+    const int seg = blockIdx.y, blk = blockIdx.x;
+    if (a.done && a.done[seg]) return;
+    const int t = blk * 256 + threadIdx.x;
+    if (t >= a.T) return;
+    const int64_t so = static_cast<int64_t>(seg) * a.T;
+    const int lab = a.labels[so + t];
+    const int pos = a.hist[(static_cast<int64_t>(seg) * a.kmax + lab) * a.nblk + blk] + a.rank[so + t];
+    a.sorted[so + pos] = t;
+}
+
+// M-step for one cluster: thread d sums dim d of the members in ascending
+// token order (dependent fp32 adds, loads batched 16 ahead).
+__global__ __launch_bounds__(64) void km_update_kernel(KmParams a, int it, Draws draws) {
+    const int c = blockIdx.x, seg = blockIdx.y;
+    const int h = seg / a.P, p = seg % a.P;
+    if (c >= a.k[p]) return;
+    if (a.done && a.done[seg]) return;
+    const int d = threadIdx.x;
+    const bool live = d < a.DP;
+    const int32_t* off = a.off + static_cast<int64_t>(seg) * (a.kmax + 1);
+    const int lo = off[c], hi = off[c + 1];
+    const uint16_t* base = a.keys + h * a.hs + p * a.DP + (live ? d : 0);
+    float out;
+    if (hi > lo) {
+        const int32_t* srt = a.sorted + static_cast<int64_t>(seg) * a.T;
+        float acc = 0.0f;
+        for (int i0 = lo; i0 < hi; i0 += 64) {
+            const int n = min(64, hi - i0);
+            const int my_tok = d < n ? srt[i0 + d] : 0;
+            for (int u0 = 0; u0 < n; u0 += 16) {
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const int tok = __shfl(my_tok, u0 + u);
+                    v[u] = (u0 + u < n) ? bf16_to_f32(base[static_cast<int64_t>(tok) * a.ts]) : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < 16; ++u)
+                    if (u0 + u < n) acc = acc + v[u];
+            }
+        }
+        const float inv = 1.0f / static_cast<float>(hi - lo);
+        out = acc * inv;
+    } else {
+        const int e = a.empties[static_cast<int64_t>(seg) * a.kmax + c];
+        const int tok = draws.v[e];
+        out = bf16_to_f32(base[static_cast<int64_t>(tok) * a.ts]);
+    }
+    if (live) a.cent[(static_cast<int64_t>(seg) * a.kmax + c) * a.DP + d] = out;
+}
+
+__global__ void km_reset_kernel(KmParams a) {
+    const int seg = blockIdx.x * blockDim.x + threadIdx.x;
+    if (seg >= a.H * a.P) return;
+    a.prev[seg] = 3.402823466e38f;
+    if (a.done) a.done[seg] = 0;
+    if (a.iters) a.iters[seg] = 0;
+}
+
+int validate(const imi_kmeans_args* a, int& kmax, int& dp) {
+    IMI_REQUIRE(a != nullptr, IMI_ERR_INVALID, "imi_kmeans: null args");
+    IMI_REQUIRE(a->keys && a->centroids && a->labels, IMI_ERR_INVALID, "imi_kmeans: null pointer argument");
+    IMI_REQUIRE(a->kv_heads > 0 && a->n_tokens > 0, IMI_ERR_INVALID, "imi_kmeans: empty input (H=%d T=%d)",
+                a->kv_heads, a->n_tokens);
+    IMI_REQUIRE(a->parts == 2 || a->parts == 4, IMI_ERR_UNSUPPORTED, "imi_kmeans: parts must be 2 or 4 (got %d)",
+                a->parts);
+    IMI_REQUIRE(a->dim % a->parts == 0, IMI_ERR_INVALID, "imi_kmeans: dim %d not divisible by parts %d", a->dim,
+                a->parts);
+    dp = a->dim / a->parts;
+    IMI_REQUIRE(dp == 32 || dp == 64, IMI_ERR_UNSUPPORTED, "imi_kmeans: subspace width %d unsupported (32 or 64)",
+                dp);
+    IMI_REQUIRE(a->max_iters >= 1, IMI_ERR_INVALID, "imi_kmeans: max_iters must be >= 1");
+    kmax = 0;
+    for (int p = 0; p < a->parts; ++p) {
+        IMI_REQUIRE(a->k[p] >= 1 && a->k[p] <= 256, IMI_ERR_UNSUPPORTED, "imi_kmeans: k[%d]=%d outside [1,256]", p,
+                    a->k[p]);
+        kmax = a->k[p] > kmax ? a->k[p] : kmax;
+    }
+    if (a->init_mode == 0)
+        IMI_REQUIRE(kmax <= a->n_tokens, IMI_ERR_INVALID,
+                    "imi_kmeans: first-k initialisation needs n_tokens (%d) >= k (%d)", a->n_tokens, kmax);
+    IMI_REQUIRE((a->token_stride % 8) == 0 && (a->head_stride % 8) == 0, IMI_ERR_INVALID,
+                "imi_kmeans: strides must be multiples of 8 elements (16-byte rows)");
+    IMI_REQUIRE((reinterpret_cast<uintptr_t>(a->keys) & 15) == 0, IMI_ERR_INVALID,
+                "imi_kmeans: keys must be 16-byte aligned");
+    return IMI_OK;
+}
+
+size_t workspace_bytes(const imi_kmeans_args* a, int kmax, KmParams* out) {
+    const int segs = a->kv_heads * a->parts;
+    const int nblk = (a->n_tokens + 255) / 256;
+    Carver cv(a->workspace);
+    KmParams p{};
+    p.hist = cv.take<int32_t>(static_cast<size_t>(segs) * kmax * nblk);
+    p.rank = cv.take<int32_t>(static_cast<size_t>(segs) * a->n_tokens);
+    p.ipart = cv.take<float>(static_cast<size_t>(segs) * nblk);
+    p.sorted = cv.take<int32_t>(static_cast<size_t>(segs) * a->n_tokens);
+    p.off = cv.take<int32_t>(static_cast<size_t>(segs) * (kmax + 1));
+    p.empties = cv.take<int32_t>(static_cast<size_t>(segs) * kmax);
+    p.prev = cv.take<float>(segs);
+    p.done = cv.take<int32_t>(segs);
+    if (out) *out = p;
+    return cv.used();
+}
+
+template <int DP>
+int run_assign(const KmParams& p, int segs, hipStream_t stream) {
+    const size_t lds = static_cast<size_t>(p.kmax) * DP * sizeof(float) + 4 * p.kmax * sizeof(int) + 64;
+    if (lds > 64 * 1024) IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_assign_kernel<DP>),
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                           static_cast<int>(lds)));
+    hipLaunchKernelGGL(km_assign_kernel<DP>, dim3(p.nblk, segs), dim3(256), lds, stream, p);
+    IMI_LAUNCH_CHECK("km_assign_kernel");
+    return IMI_OK;
+}
+
+}  // namespace
+}  // namespace imi
+
+using namespace imi;
+
+extern "C" int imi_kmeans_workspace_size(const imi_kmeans_args* a, size_t* bytes) {
+    clear_error();
+    int kmax, dp;
+    int rc = validate(a, kmax, dp);
+    if (rc) return rc;
+    IMI_REQUIRE(bytes != nullptr, IMI_ERR_INVALID, "imi_kmeans_workspace_size: null output");
+    imi_kmeans_args tmp = *a;
+    tmp.workspace = nullptr;
+    *bytes = workspace_bytes(&tmp, kmax, nullptr);
+    return IMI_OK;
+}
+
+extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_) {
+    clear_error();
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    int kmax, dp;
+    int rc = validate(a, kmax, dp);
+    if (rc) return rc;
+    imi_kmeans_args tmp = *a;
+    tmp.workspace = nullptr;
+    const size_t need = workspace_bytes(&tmp, kmax, nullptr);
+    IMI_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= need, IMI_ERR_WORKSPACE,
+                "imi_kmeans_execute: workspace %zu bytes < %zu required", a->workspace_bytes, need);
+
+    KmParams p;
+    workspace_bytes(a, kmax, &p);
+    p.keys = a->keys;
+    p.hs = a->head_stride;
+    p.ts = a->token_stride;
+    p.H = a->kv_heads;
+    p.T = a->n_tokens;
+    p.P = a->parts;
+    p.kmax = kmax;
+    p.DP = dp;
+    for (int i = 0; i < 4; ++i) p.k[i] = i < a->parts ? a->k[i] : 0;
+    p.cent = a->centroids;
+    p.labels = a->labels;
+    p.mind = nullptr;
+    p.iters = a->iters_run;
+    p.nblk = (a->n_tokens + 255) / 256;
+    p.max_iters = a->max_iters;
+    p.tol = a->tol;
+    p.es_min = a->early_stop_min_iter;
+    p.es_rel = a->early_stop_rel_tol;
+    const int segs = a->kv_heads * a->parts;
+    const bool early_stop = a->early_stop_min_iter <= a->max_iters;
+    if (!early_stop) p.done = nullptr;  // no test can fire: skip the flag reads
+
+    hipLaunchKernelGGL(km_reset_kernel, dim3((segs + 63) / 64), dim3(64), 0, stream, p);
+    IMI_LAUNCH_CHECK("km_reset_kernel");
+    if (a->init_mode == 0) {
+        hipLaunchKernelGGL(km_init_first_kernel, dim3(kmax, segs), dim3(64), 0, stream, p);
+        IMI_LAUNCH_CHECK("km_init_first_kernel");
+    }
+    for (int it = 0; it < a->max_iters; ++it) {
+        rc = dp == 64 ? run_assign<64>(p, segs, stream) : run_assign<32>(p, segs, stream);
+        if (rc) return rc;
+        hipLaunchKernelGGL(km_scan_kernel, dim3(segs), dim3(1024), 0, stream, p, it);
+        IMI_LAUNCH_CHECK("km_scan_kernel");
+        hipLaunchKernelGGL(km_scatter_kernel, dim3(p.nblk, segs), dim3(256), 0, stream, p);
+        IMI_LAUNCH_CHECK("km_scatter_kernel");
+        // Empty-cluster draws of this iteration: std::mt19937(it + 12345) with
+        // uniform_int_distribution<int32_t>(0, T-1), one per empty cluster in
+        // ascending cluster order (kmeans_core.cpp:299-311).
+        Draws dr;
+        std::mt19937 rng(static_cast<unsigned>(it + 12345));
+        std::uniform_int_distribution<int32_t> dist(0, a->n_tokens - 1);
+        for (int e = 0; e < kmax; ++e) dr.v[e] = dist(rng);
+        hipLaunchKernelGGL(km_update_kernel, dim3(kmax, segs), dim3(64), 0, stream, p, it, dr);
+        IMI_LAUNCH_CHECK("km_update_kernel");
+    }
+    return IMI_OK;
+}
+
+extern "C" int imi_kmeans_assign(const uint16_t* keys, int64_t head_stride, int64_t token_stride, int32_t kv_heads,
+                                 int32_t n_tokens, int32_t dim, int32_t parts, const int32_t* k,
+                                 const float* centroids, int32_t* labels, float* mind, imi_stream_t stream_) {
+    clear_error();
+    imi_kmeans_args a{};
+    a.keys = keys;
+    a.head_stride = head_stride;
+    a.token_stride = token_stride;
+    a.kv_heads = kv_heads;
+    a.n_tokens = n_tokens;
+    a.dim = dim;
+    a.parts = parts;
+    IMI_REQUIRE(k != nullptr, IMI_ERR_INVALID, "imi_kmeans_assign: null k");
+    for (int i = 0; i < parts && i < 4; ++i) a.k[i] = k[i];
+    a.max_iters = 1;
+    a.init_mode = 1;
+    a.centroids = const_cast<float*>(centroids);
+    a.labels = labels;
+    int kmax, dp;
+    int rc = validate(&a, kmax, dp);
+    if (rc) return rc;
+    KmParams p{};
+    p.keys = keys;
+    p.hs = head_stride;
+    p.ts = token_stride;
+    p.H = kv_heads;
+    p.T = n_tokens;
+    p.P = parts;
+    p.kmax = kmax;
+    p.DP = dp;
+    for (int i = 0; i < 4; ++i) p.k[i] = i < parts ? k[i] : 0;
+    p.cent = const_cast<float*>(centroids);
+    p.labels = labels;
+    p.mind = mind;
+    p.nblk = (n_tokens + 255) / 256;
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    return dp == 64 ? run_assign<64>(p, kv_heads * parts, stream) : run_assign<32>(p, kv_heads * parts, stream);
+}

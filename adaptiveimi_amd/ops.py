@@ -1,0 +1,368 @@
+"""torch-facing wrappers over the C ABI (include/imi_hip.h).
+
+All tensors must live on a HIP device; every call enqueues on the current
+torch stream and returns without a host synchronisation.  Workspaces come
+from the torch caching allocator and are zero-filled once on allocation (the
+kernels leave them reusable).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+from typing import Dict, Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import AttentionArgs, DecodeArgs, IndexArgs, KmeansArgs, SelectArgs, check
+
+_WS: Dict[Tuple[str, int], torch.Tensor] = {}
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_device(*ts: torch.Tensor) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError("adaptiveimi_amd kernels need HIP device tensors (no CPU path)")
+        dev = t.device if dev is None else dev
+    return dev
+
+
+def workspace(name: str, nbytes: int, device: torch.device) -> torch.Tensor:
+    """Zero-filled byte buffer reused across calls (grown on demand)."""
+    key = (name, device.index if device.index is not None else torch.cuda.current_device())
+    buf = _WS.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        _WS[key] = buf
+    return buf
+
+
+def _ks(ks: Sequence[int]):
+    arr = (ctypes.c_int32 * 4)()
+    for i, k in enumerate(ks):
+        arr[i] = int(k)
+    return arr
+
+
+def _as_bits(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"expected bfloat16 tensor, got {t.dtype}")
+    return t
+
+
+def _head_token_strides(x: torch.Tensor) -> Tuple[int, int]:
+    if x.dim() != 3 or x.stride(2) != 1:
+        raise ValueError("expected a [heads, tokens, dim] view with unit stride on dim")
+    return x.stride(0), x.stride(1)
+
+
+# ----------------------------------------------------------------- k-means --
+
+def kmeans(keys: torch.Tensor, ks: Sequence[int], max_iters: int, tol: float = 5e-4,
+           early_stop_min_iter: Optional[int] = None, early_stop_rel_tol: float = 5e-4,
+           init_centroids: Optional[torch.Tensor] = None):
+    """Per-(head, subspace) Lloyd k-means (kmeans_core.cpp:384-501).
+    keys: bf16 [H, T, D] view.  Returns (centroids f32 [H, P, kmax, D/P],
+    labels i32 [H, P, T], iters i32 [H, P])."""
+    dev = _require_device(keys, init_centroids)
+    _as_bits(keys)
+    H, T, D = keys.shape
+    P = len(ks)
+    kmax = max(ks)
+    hs, ts = _head_token_strides(keys)
+    if init_centroids is not None:
+        cent = init_centroids.to(device=dev, dtype=torch.float32).contiguous().clone()
+        if cent.shape != (H, P, kmax, D // P):
+            raise ValueError(f"init_centroids must be [{H}, {P}, {kmax}, {D // P}]")
+    else:
+        cent = torch.zeros((H, P, kmax, D // P), dtype=torch.float32, device=dev)
+    labels = torch.empty((H, P, T), dtype=torch.int32, device=dev)
+    iters = torch.zeros((H, P), dtype=torch.int32, device=dev)
+    a = KmeansArgs(keys=keys.data_ptr(), head_stride=hs, token_stride=ts, kv_heads=H, n_tokens=T, dim=D,
+                   parts=P, k=_ks(ks), max_iters=int(max_iters), tol=float(tol),
+                   early_stop_min_iter=int(max_iters + 1 if early_stop_min_iter is None else early_stop_min_iter),
+                   early_stop_rel_tol=float(early_stop_rel_tol), init_mode=0 if init_centroids is None else 1,
+                   centroids=cent.data_ptr(), labels=labels.data_ptr(), iters_run=iters.data_ptr())
+    need = ctypes.c_size_t()
+    check(_lib.lib().imi_kmeans_workspace_size(ctypes.byref(a), ctypes.byref(need)), "imi_kmeans_workspace_size")
+    ws = workspace("kmeans", need.value, dev)
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = ws.numel()
+    check(_lib.lib().imi_kmeans_execute(ctypes.byref(a), _stream(dev)), "imi_kmeans_execute")
+    return cent, labels, iters
+
+
+def kmeans_assign(keys: torch.Tensor, centroids: torch.Tensor, ks: Sequence[int]):
+    """One E-step with given centroids [H, P, kmax, D/P] (kmeans_core.cpp:222-242).
+    Returns (labels i32 [H, P, T], min distance f32 [H, P, T])."""
+    dev = _require_device(keys, centroids)
+    _as_bits(keys)
+    H, T, D = keys.shape
+    P = len(ks)
+    hs, ts = _head_token_strides(keys)
+    cent = centroids.to(torch.float32).contiguous()
+    labels = torch.empty((H, P, T), dtype=torch.int32, device=dev)
+    mind = torch.empty((H, P, T), dtype=torch.float32, device=dev)
+    check(_lib.lib().imi_kmeans_assign(keys.data_ptr(), hs, ts, H, T, D, P, ctypes.cast(_ks(ks), ctypes.c_void_p),
+                                       cent.data_ptr(), labels.data_ptr(), mind.data_ptr(), _stream(dev)),
+          "imi_kmeans_assign")
+    return labels, mind
+
+
+# -------------------------------------------------------------- cell index --
+
+def build_index(keys: torch.Tensor, values: torch.Tensor, centroids: torch.Tensor, labels: torch.Tensor,
+                ks: Sequence[int], n_centroids: Optional[int] = None, list_rows: Optional[int] = None,
+                list_keys: Optional[torch.Tensor] = None, list_values: Optional[torch.Tensor] = None,
+                compact: bool = True) -> Dict[str, torch.Tensor]:
+    """Cell order + CSR + K/V permutation (reorganize_core.cpp:18-394)."""
+    dev = _require_device(keys, values, centroids, labels)
+    _as_bits(keys)
+    _as_bits(values)
+    H, T, D = keys.shape
+    if values.shape != keys.shape or values.stride() != keys.stride():
+        raise ValueError("keys and values must share shape and strides")
+    hs, ts = _head_token_strides(keys)
+    P = len(ks)
+    ncells = 1
+    for k in ks:
+        ncells *= int(k)
+    rows = int(list_rows or T)
+    out: Dict[str, torch.Tensor] = {}
+    out["cell_count"] = torch.empty((H, ncells), dtype=torch.int32, device=dev)
+    out["cell_offset"] = torch.empty((H, ncells + 1), dtype=torch.int32, device=dev)
+    out["perm"] = torch.empty((H, T), dtype=torch.int32, device=dev)
+    out["list_keys"] = list_keys if list_keys is not None else torch.empty((H, rows, D), dtype=keys.dtype, device=dev)
+    out["list_values"] = (list_values if list_values is not None
+                          else torch.empty((H, rows, D), dtype=keys.dtype, device=dev))
+    for name in ("list_keys", "list_values"):
+        t = out[name]
+        if t.shape[0] != H or t.shape[2] != D or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous [H, rows, D]")
+    rows = out["list_keys"].shape[1]
+    a = IndexArgs(keys=keys.data_ptr(), values=values.data_ptr(), head_stride=hs, token_stride=ts, kv_heads=H,
+                  n_tokens=T, dim=D, parts=P, k=_ks(ks), centroids=centroids.data_ptr(), labels=labels.data_ptr(),
+                  cell_count=out["cell_count"].data_ptr(), cell_offset=out["cell_offset"].data_ptr(),
+                  perm=out["perm"].data_ptr(), list_keys=out["list_keys"].data_ptr(),
+                  list_values=out["list_values"].data_ptr(), list_rows=rows)
+    if compact:
+        n_c = int(n_centroids if n_centroids is not None else ncells + 1)
+        out["n_active"] = torch.empty((H,), dtype=torch.int32, device=dev)
+        out["compact_gid"] = torch.empty((H, n_c), dtype=torch.int32, device=dev)
+        out["compact_size"] = torch.empty((H, n_c), dtype=torch.int32, device=dev)
+        out["compact_offset"] = torch.empty((H, n_c + 1), dtype=torch.int32, device=dev)
+        out["compact_centroids"] = torch.empty((H, n_c, D), dtype=torch.float32, device=dev)
+        out["compact_mask"] = torch.empty((H, n_c), dtype=torch.bool, device=dev)
+        a.n_centroids = n_c
+        a.n_active = out["n_active"].data_ptr()
+        a.compact_gid = out["compact_gid"].data_ptr()
+        a.compact_size = out["compact_size"].data_ptr()
+        a.compact_offset = out["compact_offset"].data_ptr()
+        a.compact_centroids = out["compact_centroids"].data_ptr()
+        a.compact_mask = out["compact_mask"].data_ptr()
+    need = ctypes.c_size_t()
+    check(_lib.lib().imi_index_workspace_size(ctypes.byref(a), ctypes.byref(need)), "imi_index_workspace_size")
+    ws = workspace("index", need.value, dev)
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = ws.numel()
+    check(_lib.lib().imi_build_index(ctypes.byref(a), _stream(dev)), "imi_build_index")
+    return out
+
+
+# ------------------------------------------------------------------ decode --
+
+def fused_query_group_similarities(query_grouped: torch.Tensor, centroids: torch.Tensor,
+                                   out: Optional[torch.Tensor] = None,
+                                   mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """gpu_bindings.cpp:21-43 signature; optional mask fuses retrieval.py:357."""
+    dev = _require_device(query_grouped, centroids, out, mask)
+    _as_bits(query_grouped)
+    if query_grouped.dim() != 3 or centroids.dim() != 3:
+        raise ValueError("query_grouped and centroids must be 3D tensors")
+    H, G, D = query_grouped.shape
+    if centroids.shape[0] != H or centroids.shape[2] != D:
+        raise ValueError("kv_heads / head_dim mismatch between query_grouped and centroids")
+    if centroids.dtype != torch.float32:
+        raise TypeError("centroids must be float32")
+    q = query_grouped.contiguous()
+    c = centroids.contiguous()
+    N = c.shape[1]
+    if out is None:
+        res = torch.empty((H, N), dtype=torch.float32, device=dev)
+    else:
+        if out.dtype != torch.float32 or out.dim() != 2 or out.shape[0] < H or out.shape[1] < N:
+            raise ValueError("out tensor shape insufficient")
+        res = out.narrow(0, 0, H).narrow(1, 0, N)
+        if res.stride(1) != 1:
+            raise ValueError("out must have unit stride on its last dim")
+    m = None if mask is None else mask.to(torch.bool).contiguous()
+    check(_lib.lib().imi_fused_query_group_similarities(q.data_ptr(), c.data_ptr(), res.data_ptr(), res.stride(0),
+                                                        _ptr(m), H, G, N, D, _stream(dev)),
+          "imi_fused_query_group_similarities")
+    return res
+
+
+@dataclass
+class Budget:
+    nprobe: int
+    max_tokens: int
+    buffer_pages: int
+    page_size: int = 8
+
+    @property
+    def sel_cap(self) -> int:
+        return max(1, min(self.nprobe, self.buffer_pages))
+
+    @property
+    def max_rows(self) -> int:
+        return self.buffer_pages * self.page_size
+
+
+def select(query: torch.Tensor, centroids: torch.Tensor, cell_count: torch.Tensor, cell_offset: torch.Tensor,
+           ks: Sequence[int], budget: Budget) -> Dict[str, torch.Tensor]:
+    """Scores + top-nprobe + token prefix + page rule, per KV head
+    (retrieval.py:295-303,357; wave_buffer_cpu_hotcold.cpp:303-371)."""
+    dev = _require_device(query, centroids, cell_count, cell_offset)
+    _as_bits(query)
+    H, G, D = query.shape
+    cap = budget.sel_cap
+    out = {
+        "sel_cell": torch.full((H, cap), -1, dtype=torch.int32, device=dev),
+        "sel_offset": torch.zeros((H, cap), dtype=torch.int32, device=dev),
+        "sel_count": torch.zeros((H, cap), dtype=torch.int32, device=dev),
+        "sel_prefix": torch.zeros((H, cap + 1), dtype=torch.int32, device=dev),
+        "n_selected": torch.zeros((H,), dtype=torch.int32, device=dev),
+        "n_rows": torch.zeros((H,), dtype=torch.int32, device=dev),
+    }
+    q = query.contiguous()
+    a = SelectArgs(query=q.data_ptr(), centroids=centroids.data_ptr(), cell_count=cell_count.data_ptr(),
+                   cell_offset=cell_offset.data_ptr(), kv_heads=H, groups=G, dim=D, parts=len(ks), k=_ks(ks),
+                   nprobe=budget.nprobe, max_tokens=budget.max_tokens, buffer_pages=budget.buffer_pages,
+                   page_size=budget.page_size, sel_cell=out["sel_cell"].data_ptr(),
+                   sel_offset=out["sel_offset"].data_ptr(), sel_count=out["sel_count"].data_ptr(),
+                   sel_prefix=out["sel_prefix"].data_ptr(), n_selected=out["n_selected"].data_ptr(),
+                   n_rows=out["n_rows"].data_ptr(), sel_cap=cap)
+    check(_lib.lib().imi_select(ctypes.byref(a), _stream(dev)), "imi_select")
+    return out
+
+
+def sparse_attention(query: torch.Tensor, steady_keys: Optional[torch.Tensor], steady_values: Optional[torch.Tensor],
+                     static_len: int, list_keys: torch.Tensor, list_values: torch.Tensor, sel: Dict[str, torch.Tensor],
+                     max_rows: int, scale: Optional[float] = None, return_lse: bool = False):
+    """Gather + GQA decode attention over [static rows | selected rows]."""
+    dev = _require_device(query, list_keys, list_values)
+    _as_bits(query)
+    H, G, D = query.shape
+    out = torch.empty((H * G, D), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((H * G,), dtype=torch.float32, device=dev) if return_lse else None
+    ss = steady_keys.shape[1] if steady_keys is not None else 0
+    cap = sel["sel_cell"].shape[1]
+    a = AttentionArgs(query=query.contiguous().data_ptr(), steady_keys=_ptr(steady_keys),
+                      steady_values=_ptr(steady_values), steady_stride=ss, static_len=int(static_len),
+                      list_keys=list_keys.data_ptr(), list_values=list_values.data_ptr(),
+                      list_rows=list_keys.shape[1], sel_offset=sel["sel_offset"].data_ptr(),
+                      sel_count=sel["sel_count"].data_ptr(), sel_prefix=sel["sel_prefix"].data_ptr(),
+                      n_selected=sel["n_selected"].data_ptr(), n_rows=sel["n_rows"].data_ptr(), sel_cap=cap,
+                      max_rows=int(max_rows), kv_heads=H, groups=G, dim=D,
+                      scale=float(scale if scale is not None else 1.0 / math.sqrt(D)), out=out.data_ptr(),
+                      out_lse=_ptr(lse))
+    need = ctypes.c_size_t()
+    check(_lib.lib().imi_attention_workspace_size(ctypes.byref(a), ctypes.byref(need)),
+          "imi_attention_workspace_size")
+    ws = workspace("attention", need.value, dev)
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = ws.numel()
+    check(_lib.lib().imi_sparse_attention(ctypes.byref(a), _stream(dev)), "imi_sparse_attention")
+    return (out, lse) if return_lse else out
+
+
+class DecodePlan:
+    """Pre-built arguments of imi_decode_step for one layer: only the query,
+    output and static_len change between steps, so a step costs one ctypes
+    call.  The plan owns its workspace (zero-filled once)."""
+
+    def __init__(self, centroids: torch.Tensor, cell_count: torch.Tensor, cell_offset: torch.Tensor,
+                 ks: Sequence[int], budget: Budget, list_keys: torch.Tensor, list_values: torch.Tensor,
+                 steady_keys: Optional[torch.Tensor], steady_values: Optional[torch.Tensor], groups: int,
+                 scale: Optional[float] = None, query: Optional[torch.Tensor] = None,
+                 out: Optional[torch.Tensor] = None, out_lse: Optional[torch.Tensor] = None):
+        dev = _require_device(centroids, cell_count, cell_offset, list_keys, list_values)
+        self.device = dev
+        H, _, D = list_keys.shape
+        self.H, self.G, self.D = H, groups, D
+        self.budget = budget
+        self.query = query if query is not None else torch.zeros((H, groups, D), dtype=torch.bfloat16, device=dev)
+        self.out = out if out is not None else torch.empty((H * groups, D), dtype=torch.bfloat16, device=dev)
+        self._keep = (centroids, cell_count, cell_offset, list_keys, list_values, steady_keys, steady_values,
+                      out_lse)
+        a = DecodeArgs()
+        s = a.sel
+        s.query = self.query.data_ptr()
+        s.centroids = centroids.data_ptr()
+        s.cell_count = cell_count.data_ptr()
+        s.cell_offset = cell_offset.data_ptr()
+        s.kv_heads, s.groups, s.dim, s.parts = H, groups, D, len(ks)
+        s.k = _ks(ks)
+        s.nprobe, s.max_tokens = budget.nprobe, budget.max_tokens
+        s.buffer_pages, s.page_size = budget.buffer_pages, budget.page_size
+        s.sel_cap = budget.sel_cap
+        t = a.attn
+        t.query = self.query.data_ptr()
+        t.steady_keys = _ptr(steady_keys)
+        t.steady_values = _ptr(steady_values)
+        t.steady_stride = steady_keys.shape[1] if steady_keys is not None else 0
+        t.static_len = 0
+        t.list_keys, t.list_values = list_keys.data_ptr(), list_values.data_ptr()
+        t.list_rows = list_keys.shape[1]
+        t.max_rows = budget.max_rows
+        t.kv_heads, t.groups, t.dim = H, groups, D
+        t.scale = float(scale if scale is not None else 1.0 / math.sqrt(D))
+        t.out = self.out.data_ptr()
+        t.out_lse = _ptr(out_lse)
+        need = ctypes.c_size_t()
+        check(_lib.lib().imi_decode_workspace_size(ctypes.byref(a), ctypes.byref(need)), "imi_decode_workspace_size")
+        self.ws = torch.zeros(max(need.value, 256), dtype=torch.uint8, device=dev)
+        t.workspace = self.ws.data_ptr()
+        t.workspace_bytes = self.ws.numel()
+        self.args = a
+        self._fn = _lib.lib().imi_decode_step
+        self._ref = ctypes.byref(a)
+        self.selection = self._selection_views()
+
+    def _selection_views(self) -> Dict[str, torch.Tensor]:
+        """Views of the workspace where the selection outputs land."""
+        H, cap = self.H, self.budget.sel_cap
+        i32 = self.ws.view(torch.int32)
+        off = 0
+        views = {}
+        for name, n in (("sel_cell", H * cap), ("sel_offset", H * cap), ("sel_count", H * cap),
+                        ("sel_prefix", H * (cap + 1)), ("n_selected", H), ("n_rows", H)):
+            off = (off + 63) // 64 * 64  # 256-byte alignment in int32 units
+            views[name] = i32[off:off + n]
+            off += n
+        views["sel_cell"] = views["sel_cell"].view(H, cap)
+        views["sel_offset"] = views["sel_offset"].view(H, cap)
+        views["sel_count"] = views["sel_count"].view(H, cap)
+        views["sel_prefix"] = views["sel_prefix"].view(H, cap + 1)
+        return views
+
+    def set_static_len(self, static_len: int) -> None:
+        self.args.attn.static_len = int(static_len)
+
+    def step(self, stream: Optional[int] = None, phases: int = 3) -> torch.Tensor:
+        """Enqueue one step; phases 1 = selection only, 2 = attention only."""
+        self.args.phases = phases
+        check(self._fn(self._ref, stream if stream is not None else _stream(self.device)), "imi_decode_step")
+        return self.out

@@ -1,0 +1,227 @@
+/*
+ * imi_hip.h — C ABI of the MI355X (gfx950) AdaptiveIMI sparse-decode path.
+ *
+ * Plain pointers and sizes only.  Every pointer named "device" is HIP device
+ * memory owned by the caller; the library keeps no pointer after a call
+ * returns.  Every entry point enqueues work on the caller's stream and returns
+ * without a host synchronisation; a non-zero return is an error whose text
+ * imi_last_error() gives (thread-local), with nothing enqueued.
+ *
+ * Layout conventions (H = kv heads, T = indexed tokens, D = head_dim = 128,
+ * P = subspace parts, Dp = D / P, G = query heads per kv head):
+ *   keys/values  bf16 bit patterns, element (h, t, d) at
+ *                base[h * head_stride + t * token_stride + d]
+ *   centroids    fp32 [H][P][kmax][Dp]   (subspace centroids)
+ *   labels       int32 [H][P][T]          (subspace labels)
+ *   cell index   global cell id g = ((l0 * k1 + l1) * k2 + l2) * k3 + l3
+ *                (mixed radix, reorganize_core.cpp:33-35, 112-118)
+ *   cell_count / cell_offset   int32 [H][ncells] / [H][ncells + 1]: CSR over
+ *                global cell ids (empty cells have count 0)
+ *   list_keys / list_values    bf16 [H][list_stride_rows][D]: rows in CSR order
+ *   perm         int32 [H][T]: CSR position -> original token index
+ */
+#ifndef IMI_HIP_H_
+#define IMI_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* imi_stream_t; /* == hipStream_t */
+
+enum {
+    IMI_OK = 0,
+    IMI_ERR_INVALID = 1,     /* bad argument / shape */
+    IMI_ERR_HIP = 2,         /* HIP runtime error */
+    IMI_ERR_UNSUPPORTED = 3, /* shape outside what the kernels implement */
+    IMI_ERR_WORKSPACE = 4    /* workspace too small */
+};
+
+/* Thread-local text of the last error (empty string when none). */
+const char* imi_last_error(void);
+/* ABI version of this library (bumped on any signature change). */
+int imi_version(void);
+
+/* ------------------------------------------------------------------ k-means
+ * Replaces the CPU k-means of the index build:
+ *   kmeans_execute / kmeans_execute_4 / kmeans_execute_ivf
+ *     (library/AdaptiveIMI/cpp_extensions/src/kmeans_core.cpp:822-1174),
+ *   KmeansExecutor::execute (kmeans_core.cpp:384-501),
+ *   lloyd_iteration (kmeans_core.cpp:190-314).
+ * Assignments use the reference distance order exactly (8 FMA lanes then a
+ * left-to-right lane sum, strict '<' so ties go to the lower centroid); the
+ * M-step sums each cluster's members in ascending token order and multiplies
+ * by 1.0f/size (the reference with one thread per (head, subspace), which is
+ * what it runs on hosts with fewer than 32 cores); empty clusters are
+ * re-seeded from std::mt19937(iter + 12345) exactly as the reference does.
+ */
+typedef struct {
+    const uint16_t* keys;     /* device, bf16 bits, see layout above */
+    int64_t head_stride;      /* elements between heads */
+    int64_t token_stride;     /* elements between tokens */
+    int32_t kv_heads;         /* H */
+    int32_t n_tokens;         /* T */
+    int32_t dim;              /* D (128) */
+    int32_t parts;            /* P: 2 or 4 (IMI subspaces) */
+    int32_t k[4];             /* centroids per subspace, each in [1, 256] */
+    int32_t max_iters;        /* >= 1 */
+    float tol;                /* absolute inertia tolerance */
+    int32_t early_stop_min_iter; /* early stop disabled when > max_iters */
+    float early_stop_rel_tol;
+    int32_t init_mode;        /* 0: first k rows of each subspace;
+                                 1: centroids already hold the initial values */
+    float* centroids;         /* device [H][P][kmax][Dp] in/out */
+    int32_t* labels;          /* device [H][P][T] out (last E-step) */
+    int32_t* iters_run;       /* device [H][P] out (E-steps executed), may be NULL */
+    void* workspace;          /* device, >= imi_kmeans_workspace_size() bytes */
+    size_t workspace_bytes;
+} imi_kmeans_args;
+
+int imi_kmeans_workspace_size(const imi_kmeans_args* a, size_t* bytes);
+int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream);
+
+/* One assignment pass with given centroids (the E-step of
+ * kmeans_core.cpp:222-242), for parity checks with injected centroids.
+ * mind (optional) receives each token's minimum distance. */
+int imi_kmeans_assign(const uint16_t* keys, int64_t head_stride, int64_t token_stride, int32_t kv_heads,
+                      int32_t n_tokens, int32_t dim, int32_t parts, const int32_t* k, const float* centroids,
+                      int32_t* labels, float* mind, imi_stream_t stream);
+
+/* ------------------------------------------------------------ cell index
+ * Replaces reorganize_from_kmeans / _4 (reorganize_core.cpp:313-394,
+ * 477-569) with build_compact_reorg_input (18-176) and reorganize_single_head
+ * (234-311): stable order of tokens by (cell, token), CSR over global cells,
+ * compact metadata padded to n_centroids (pipeline_bindings.cpp:206-276,
+ * indexing.py:108-174) and the K/V row permutation into the list.
+ */
+typedef struct {
+    const uint16_t* keys;     /* device bf16, layout above */
+    const uint16_t* values;   /* device bf16, same strides as keys */
+    int64_t head_stride;
+    int64_t token_stride;
+    int32_t kv_heads, n_tokens, dim, parts;
+    int32_t k[4];
+    const float* centroids;   /* device [H][P][kmax][Dp] (from imi_kmeans_execute) */
+    const int32_t* labels;    /* device [H][P][T] */
+    /* outputs (device) */
+    int32_t* cell_count;      /* [H][ncells] */
+    int32_t* cell_offset;     /* [H][ncells + 1] */
+    int32_t* perm;            /* [H][T] */
+    uint16_t* list_keys;      /* [H][list_rows][D] */
+    uint16_t* list_values;    /* [H][list_rows][D] */
+    int64_t list_rows;        /* >= T */
+    /* compact metadata (optional: all NULL to skip) */
+    int32_t n_centroids;      /* padded slot count (>= occupied cells + 0) */
+    int32_t* n_active;        /* [H] occupied cells */
+    int32_t* compact_gid;     /* [H][n_centroids], -1 for padding slots */
+    int32_t* compact_size;    /* [H][n_centroids] */
+    int32_t* compact_offset;  /* [H][n_centroids + 1] */
+    float* compact_centroids; /* [H][n_centroids][D] merged, zero padding */
+    uint8_t* compact_mask;    /* [H][n_centroids] 1 = masked (padding) */
+    void* workspace;
+    size_t workspace_bytes;
+} imi_index_args;
+
+int imi_index_workspace_size(const imi_index_args* a, size_t* bytes);
+int imi_build_index(const imi_index_args* a, imi_stream_t stream);
+
+/* ------------------------------------------------------ decode: scoring
+ * fused_query_group_similarities (src/gpu_bindings.cpp:21-43,
+ * cuda/compute_impl.cu:62-103): scores[h][c] = fp32 FMA chain over d of
+ * qsum[h][d] * centroids[h][c][d], qsum = sum over the G grouped queries.
+ * query: bf16 [H][G][D]; centroids fp32 [H][N][D]; out fp32 [H][out_stride].
+ * mask (optional, [H][N], 1 = masked) writes -inf (retrieval.py:357).
+ */
+int imi_fused_query_group_similarities(const uint16_t* query, const float* centroids, float* out,
+                                       int64_t out_stride, const uint8_t* mask, int32_t kv_heads,
+                                       int32_t groups, int32_t n_clusters, int32_t dim, imi_stream_t stream);
+
+/* -------------------------------------------------- decode: selection
+ * _select_clusters (retrieval.py:295-303) after the -inf mask (357), plus
+ * the page-budget truncation of BufferManager::batch_access
+ * (wave_buffer_cpu_hotcold.cpp:303-371), computed without a host round trip:
+ * per head, cells ranked by (score desc, cell id asc) over occupied cells;
+ * the first m kept where m = min(nprobe, rank at which the exclusive token
+ * prefix reaches max_tokens, rank at which the page count exceeds
+ * buffer_pages).  Scores follow compute_impl.cu:80-101 bit for bit (the
+ * 128-term chain is split at the subspace boundary, which leaves the
+ * arithmetic unchanged).
+ */
+typedef struct {
+    const uint16_t* query;    /* device bf16 [H][G][D] (q heads h*G..h*G+G-1) */
+    const float* centroids;   /* device [H][P][kmax][Dp] */
+    const int32_t* cell_count;  /* device [H][ncells] */
+    const int32_t* cell_offset; /* device [H][ncells + 1] */
+    int32_t kv_heads, groups, dim, parts;
+    int32_t k[4];
+    int32_t nprobe, max_tokens, buffer_pages, page_size;
+    /* outputs (device) */
+    int32_t* sel_cell;        /* [H][sel_cap] global cell ids in rank order */
+    int32_t* sel_offset;      /* [H][sel_cap] CSR row of each selected cell */
+    int32_t* sel_count;       /* [H][sel_cap] rows of each selected cell */
+    int32_t* sel_prefix;      /* [H][sel_cap + 1] exclusive row prefix */
+    int32_t* n_selected;      /* [H] m */
+    int32_t* n_rows;          /* [H] selected rows (sum of sel_count) */
+    int32_t sel_cap;          /* >= min(nprobe, buffer_pages) */
+} imi_select_args;
+
+int imi_select(const imi_select_args* a, imi_stream_t stream);
+
+/* ------------------------------------------ decode: gather + attention
+ * Replaces concat_gather_copy (include/copy_kernel.cuh:220-335, launched by
+ * cuda/gather_copy.cu:100-213) and the unvendored weighted_flash_decoding
+ * called at retrieval.py:439-447: for kv head h and each of its G query
+ * heads, softmax(scale * q.k) v over [the first static_len rows of the steady
+ * zone | the rows of the selected cells], read in place from the list (no
+ * execution buffer).  fp32 accumulation, bf16 output [H*G][D].
+ */
+typedef struct {
+    const uint16_t* query;        /* device bf16 [H][G][D] */
+    const uint16_t* steady_keys;  /* device bf16 [H][steady_stride][D] */
+    const uint16_t* steady_values;
+    int64_t steady_stride;        /* rows per head in the steady zone */
+    int32_t static_len;           /* rows attended from the steady zone */
+    const uint16_t* list_keys;    /* device bf16 [H][list_rows][D] */
+    const uint16_t* list_values;
+    int64_t list_rows;
+    const int32_t* sel_offset;    /* from imi_select */
+    const int32_t* sel_count;
+    const int32_t* sel_prefix;
+    const int32_t* n_selected;
+    const int32_t* n_rows;
+    int32_t sel_cap;
+    int32_t max_rows;             /* bound on n_rows (buffer_pages * page_size) */
+    int32_t kv_heads, groups, dim;
+    float scale;                  /* softmax scale (1/sqrt(D)) */
+    uint16_t* out;                /* device bf16 [H*G][D] */
+    float* out_lse;               /* device fp32 [H*G] natural-log LSE, may be NULL */
+    void* workspace;              /* zero-filled before first use */
+    size_t workspace_bytes;       /* >= imi_attention_workspace_size() */
+} imi_attention_args;
+
+int imi_attention_workspace_size(const imi_attention_args* a, size_t* bytes);
+int imi_sparse_attention(const imi_attention_args* a, imi_stream_t stream);
+
+/* One decode step of one layer (retrieval.py:320-602, tile mode off):
+ * imi_select followed by the gather + attention kernel on the same stream.
+ * The selection outputs (and a per-row location table) live in
+ * attn.workspace, which must be zero-filled before its first use; every call
+ * leaves it reusable.  Calls that share a workspace must not overlap.
+ * phases: 0 or 3 = both halves; 1 = selection only; 2 = attention only
+ * (reads the selection the previous phase-1 call left in the workspace). */
+typedef struct {
+    imi_select_args sel;          /* output pointers may be NULL: workspace used */
+    imi_attention_args attn;      /* sel_* fields are filled in by the call */
+    int32_t phases;
+} imi_decode_args;
+
+int imi_decode_workspace_size(const imi_decode_args* a, size_t* bytes);
+int imi_decode_step(const imi_decode_args* a, imi_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IMI_HIP_H_ */

@@ -1,0 +1,117 @@
+"""Host-side checks of the C ABI that need no GPU: the library loads, exports
+every entry point declared in include/imi_hip.h, and rejects bad arguments
+with a status code and a message (no kernel is launched on these paths)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_functions():
+    text = (ROOT / "include" / "imi_hip.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(imi_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from adaptiveimi_amd import _lib
+
+    return _lib.lib()
+
+
+def test_exports_every_declared_symbol(L):
+    names = declared_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(L, n), n
+    from adaptiveimi_amd import _lib
+
+    assert set(names) == set(_lib.EXPORTS), "ctypes prototypes out of sync with the header"
+
+
+def test_version(L):
+    assert L.imi_version() == 1
+
+
+def _kmeans_args(**over):
+    from adaptiveimi_amd._lib import KmeansArgs
+
+    a = KmeansArgs(keys=16, head_stride=4096 * 128, token_stride=128, kv_heads=8, n_tokens=4096, dim=128, parts=2,
+                   max_iters=10, early_stop_min_iter=11, init_mode=0, centroids=16, labels=16)
+    a.k[0] = a.k[1] = 64
+    for k, v in over.items():
+        if k == "k":
+            for i, x in enumerate(v):
+                a.k[i] = x
+        else:
+            setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("over,code,text", [
+    (dict(parts=3), 3, "parts"),
+    (dict(k=(0, 64)), 3, "k[0]"),
+    (dict(k=(300, 64)), 3, "k[0]"),
+    (dict(n_tokens=0), 1, "empty"),
+    (dict(n_tokens=32), 1, "first-k"),
+    (dict(max_iters=0), 1, "max_iters"),
+    (dict(token_stride=100), 1, "strides"),
+    (dict(dim=96, parts=2), 3, "subspace width"),
+])
+def test_kmeans_rejects_bad_arguments(L, over, code, text):
+    a = _kmeans_args(**over)
+    need = ctypes.c_size_t()
+    rc = L.imi_kmeans_workspace_size(ctypes.byref(a), ctypes.byref(need))
+    assert rc == code
+    assert text in L.imi_last_error().decode()
+
+
+def test_kmeans_workspace_and_too_small_workspace(L):
+    a = _kmeans_args()
+    need = ctypes.c_size_t()
+    assert L.imi_kmeans_workspace_size(ctypes.byref(a), ctypes.byref(need)) == 0
+    assert need.value > 8 * 2 * 4096 * 4
+    a.workspace = 256
+    a.workspace_bytes = need.value - 1
+    assert L.imi_kmeans_execute(ctypes.byref(a), None) == 4
+    assert "workspace" in L.imi_last_error().decode()
+
+
+def test_select_and_decode_argument_checks(L):
+    from adaptiveimi_amd._lib import AttentionArgs, DecodeArgs, SelectArgs
+
+    s = SelectArgs(query=16, centroids=16, cell_count=16, cell_offset=16, kv_heads=8, groups=4, dim=128, parts=4,
+                   nprobe=410, max_tokens=3276, buffer_pages=410, page_size=8, sel_cap=410)
+    s.k[0] = s.k[1] = 64
+    assert L.imi_select(ctypes.byref(s), None) == 3          # 4-way selection not implemented
+    assert "2-way" in L.imi_last_error().decode()
+    s.parts = 2
+    s.sel_cap = 100
+    assert L.imi_select(ctypes.byref(s), None) == 1
+    assert "sel_cap" in L.imi_last_error().decode()
+    d = DecodeArgs()
+    d.sel = s
+    d.sel.sel_cap = 410
+    d.attn = AttentionArgs(query=16, out=16, list_keys=16, list_values=16, kv_heads=8, groups=4, dim=128,
+                           max_rows=100)
+    need = ctypes.c_size_t()
+    assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == 1
+    assert "max_rows" in L.imi_last_error().decode()
+    d.attn.max_rows = 410 * 8
+    assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == 0
+    d.attn.groups = 5
+    d.sel.groups = 5
+    assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == 3
+
+
+def test_ops_refuse_cpu_tensors():
+    import torch
+
+    from adaptiveimi_amd import ops
+
+    k = torch.zeros((2, 64, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="HIP device"):
+        ops.kmeans(k, [8, 8], 2)
