@@ -281,8 +281,16 @@ int nsplit_for(const imi_attention_args* a) {
     return rows <= 0 ? 1 : (rows + kRowsPerBlock - 1) / kRowsPerBlock;
 }
 
+// Splits the workspace is sized for: any static_len up to steady_stride, so a
+// workspace sized once stays valid while the steady zone grows.
+int nsplit_bound(const imi_attention_args* a) {
+    const int64_t srows = a->steady_stride > a->static_len ? a->steady_stride : a->static_len;
+    const int64_t rows = srows + a->max_rows;
+    return rows <= 0 ? 1 : static_cast<int>((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+}
+
 size_t attn_workspace(const imi_attention_args* a, AttnParams* p) {
-    const int nsplit = nsplit_for(a);
+    const int nsplit = nsplit_bound(a);
     Carver cv(a->workspace);
     float* acc = cv.take<float>(static_cast<size_t>(a->kv_heads) * nsplit * a->groups * 128);
     float* ml = cv.take<float>(static_cast<size_t>(a->kv_heads) * nsplit * a->groups * 2);
@@ -291,7 +299,7 @@ size_t attn_workspace(const imi_attention_args* a, AttnParams* p) {
         p->part_acc = acc;
         p->part_ml = ml;
         p->counter = cnt;
-        p->nsplit = nsplit;
+        p->nsplit = nsplit_for(a);
     }
     return cv.used();
 }
@@ -312,7 +320,7 @@ int attn_validate(const imi_attention_args* a, bool need_sel) {
     IMI_REQUIRE(a->max_rows >= 0, IMI_ERR_INVALID, "imi_sparse_attention: max_rows must be >= 0");
     if (need_sel)
         IMI_REQUIRE(a->n_rows != nullptr, IMI_ERR_INVALID, "imi_sparse_attention: null n_rows");
-    IMI_REQUIRE(nsplit_for(a) * a->groups <= kMaxSplitG, IMI_ERR_UNSUPPORTED,
+    IMI_REQUIRE(nsplit_bound(a) * a->groups <= kMaxSplitG, IMI_ERR_UNSUPPORTED,
                 "imi_sparse_attention: %d rows x %d groups exceed the split table", a->static_len + a->max_rows,
                 a->groups);
     return IMI_OK;

@@ -401,18 +401,25 @@ def decode_step(q_bits: np.ndarray, heads: List[dict], steady_k: np.ndarray, ste
                 static_len: int, n_centroids: int, nprobe: int, max_tokens: int, buffer_pages: int,
                 page_size: int = 8):
     """One sparse_attention call (retrieval.py:320-602, tile mode off):
-    scores -> mask -> select -> [static rows | selected rows] -> attention.
-    steady_k/v: bf16 bits [H, static_cap, D].  Returns (out f64 [H,G,D], sel, m,
-    rows per head as indices into the per-head CSR list)."""
+    scores -> mask -> select -> execution buffer [static rows | selected rows]
+    (copy_kernel.cuh:220-335) -> attention.  steady_k/v: bf16 bits
+    [H, static_cap, D].  Returns (out f64 [H,G,D], sel, m, rows per head as
+    indices into the per-head CSR list)."""
     H, G, D = q_bits.shape
     sizes, offsets, cent, mask = pad_metadata(heads, n_centroids, D)
     sc = scores(q_bits, cent)
     sel, m, tok = select(sc, sizes, mask, nprobe, max_tokens, buffer_pages, page_size)
     rows = selected_rows(sel, m, offsets)
-    L = heads[0]["list_keys"].shape[0]
-    kcat = np.concatenate([steady_k[:, :static_len], np.stack([hd["list_keys"] for hd in heads])], axis=1)
-    vcat = np.concatenate([steady_v[:, :static_len], np.stack([hd["list_values"] for hd in heads])], axis=1)
-    full_rows = [np.concatenate([np.arange(static_len, dtype=np.int64), r + static_len]) for r in rows]
-    out = attention(q_bits, kcat, vcat, full_rows)
-    del L
+    width = max(static_len + len(r) for r in rows)
+    ek = np.zeros((H, max(width, 1), D), np.uint16)
+    ev = np.zeros_like(ek)
+    nr = []
+    for h, hd in enumerate(heads):
+        n = static_len + len(rows[h])
+        ek[h, :static_len] = steady_k[h, :static_len]
+        ev[h, :static_len] = steady_v[h, :static_len]
+        ek[h, static_len:n] = hd["list_keys"][rows[h]]
+        ev[h, static_len:n] = hd["list_values"][rows[h]]
+        nr.append(np.arange(n, dtype=np.int64))
+    out = attention(q_bits, ek, ev, nr)
     return out, sel, m, rows
