@@ -26,9 +26,8 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax);
 
 namespace {
 
-constexpr int kRowsPerWave = 32;
-constexpr int kRowsPerBlock = 4 * kRowsPerWave;
-constexpr int kMaxSplitG = 4096;
+constexpr int kWaves = 8;            // waves per workgroup (512 threads)
+constexpr int kMaxSplitG = 8192;     // splits * groups the final merge can index
 
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 
@@ -45,6 +44,7 @@ struct AttnParams {
     int max_rows;
     const int32_t* n_rows;   // [H]
     int H, nsplit;
+    int rows_per_block;
     float scale_log2;        // scale * log2(e)
     float* part_acc;         // [H][nsplit][G][128]
     float* part_ml;          // [H][nsplit][G][2]
@@ -62,11 +62,9 @@ __device__ __forceinline__ float dot8(const uint4& k, const uint32_t (&q)[4]) {
     return s;
 }
 
-__device__ __forceinline__ void unpack8(const uint4& v, float (&f)[8]) {
-    f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x);
-    f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
-    f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z);
-    f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
+__device__ __forceinline__ float bf16_at(const uint4& v, int u) {
+    const uint32_t w = u < 2 ? v.x : u < 4 ? v.y : u < 6 ? v.z : v.w;
+    return (u & 1) ? bf16_hi(w) : bf16_lo(w);
 }
 
 __device__ __forceinline__ float safe_exp2(float x) { return x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(x); }
@@ -75,12 +73,17 @@ __device__ __forceinline__ float safe_exp2(float x) { return x == -INFINITY ? 0.
 // is M; an empty state (m = -inf) weighs 0 even when M is -inf too.
 __device__ __forceinline__ float wexp(float m, float M) { return m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M); }
 
-template <int G>
-__global__ __launch_bounds__(256) void attention_kernel(AttnParams a) {
-    __shared__ float s_acc[4][G][128];
-    __shared__ float s_ml[4][G][2];
+// One workgroup = 8 waves over rows [split * rows_per_block, +rows_per_block)
+// of head h; each wave owns TILES * 16 consecutive rows, read as tiles of 4
+// rows x 4 iterations (16 lanes x 16 bytes per row).
+template <int G, int TILES>
+__global__ __launch_bounds__(512) void attention_kernel(AttnParams a) {
+    constexpr int RW = TILES * 16;
+    __shared__ float s_acc[kWaves][G][128];
+    __shared__ float s_ml[kWaves][G][2];
     __shared__ float s_w[kMaxSplitG];
     __shared__ float s_ML[G][2];
+    __shared__ float s_red[4][G * 128];
     __shared__ int s_last;
 
     const int b = blockIdx.x;
@@ -89,13 +92,20 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int rg = lane >> 4, li = lane & 15;
     const int N = a.static_len + a.n_rows[h];
-    const int row0 = split * kRowsPerBlock + wave * kRowsPerWave;
+    const int row0 = split * a.rows_per_block + wave * RW;
 
+    // q and the row locations of this wave, loaded together up front
     uint32_t qp[G][4];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const uint4 v = *reinterpret_cast<const uint4*>(a.q + (static_cast<int64_t>(h) * G + g) * 128 + li * 8);
         qp[g][0] = v.x; qp[g][1] = v.y; qp[g][2] = v.z; qp[g][3] = v.w;
+    }
+    int myloc = 0;
+    {
+        const int n = row0 + lane;
+        if (lane < RW && n < N && n >= a.static_len)
+            myloc = a.row_loc[static_cast<int64_t>(h) * a.max_rows + (n - a.static_len)];
     }
     float m_[G], l_[G], acc[G][8];
 #pragma unroll
@@ -105,51 +115,44 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams a) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc[g][u] = 0.0f;
     }
-
     const uint16_t* skh = a.sk + static_cast<int64_t>(h) * a.s_stride * 128;
     const uint16_t* svh = a.sv + static_cast<int64_t>(h) * a.s_stride * 128;
     const uint16_t* lkh = a.lk + static_cast<int64_t>(h) * a.list_rows * 128;
     const uint16_t* lvh = a.lv + static_cast<int64_t>(h) * a.list_rows * 128;
-    const int32_t* rl = a.row_loc + static_cast<int64_t>(h) * a.max_rows;
 
     if (row0 < N) {
+        uint4 kk[TILES][4], vv[TILES][4];
+        bool ok[TILES][4];
 #pragma unroll
-        for (int tile = 0; tile < kRowsPerWave / 16; ++tile) {
-            uint4 kk[4], vv[4];
-            bool ok[4];
+        for (int t = 0; t < TILES; ++t)
 #pragma unroll
             for (int it = 0; it < 4; ++it) {
-                const int n = row0 + tile * 16 + it * 4 + rg;
-                ok[it] = n < N;
-                const uint16_t* kp;
-                const uint16_t* vp;
-                if (n < a.static_len) {
-                    kp = skh + static_cast<int64_t>(n) * 128;
-                    vp = svh + static_cast<int64_t>(n) * 128;
+                const int j = t * 16 + it * 4 + rg;
+                const int n = row0 + j;
+                const int loc = __shfl(myloc, j);
+                ok[t][it] = n < N;
+                const uint16_t* kp = n < a.static_len ? skh + static_cast<int64_t>(n) * 128
+                                                      : lkh + static_cast<int64_t>(loc) * 128;
+                const uint16_t* vp = n < a.static_len ? svh + static_cast<int64_t>(n) * 128
+                                                      : lvh + static_cast<int64_t>(loc) * 128;
+                if (ok[t][it]) {
+                    kk[t][it] = *reinterpret_cast<const uint4*>(kp + li * 8);
+                    vv[t][it] = *reinterpret_cast<const uint4*>(vp + li * 8);
                 } else {
-                    const int loc = ok[it] ? rl[n - a.static_len] : 0;
-                    kp = lkh + static_cast<int64_t>(loc) * 128;
-                    vp = lvh + static_cast<int64_t>(loc) * 128;
-                }
-                if (ok[it]) {
-                    kk[it] = *reinterpret_cast<const uint4*>(kp + li * 8);
-                    vv[it] = *reinterpret_cast<const uint4*>(vp + li * 8);
-                } else {
-                    kk[it] = make_uint4(0, 0, 0, 0);
-                    vv[it] = make_uint4(0, 0, 0, 0);
+                    kk[t][it] = make_uint4(0, 0, 0, 0);
+                    vv[t][it] = make_uint4(0, 0, 0, 0);
                 }
             }
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) {
             float s[4][G];
 #pragma unroll
             for (int it = 0; it < 4; ++it)
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
-                    const float d = row16_sum(dot8(kk[it], qp[g]));
-                    s[it][g] = ok[it] ? d * a.scale_log2 : -INFINITY;
+                    const float d = row16_sum(dot8(kk[t][it], qp[g]));
+                    s[it][g] = ok[t][it] ? d * a.scale_log2 : -INFINITY;
                 }
-            float vf[4][8];
-#pragma unroll
-            for (int it = 0; it < 4; ++it) unpack8(vv[it], vf[it]);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 const float tm = fmaxf(fmaxf(s[0][g], s[1][g]), fmaxf(s[2][g], s[3][g]));
@@ -163,10 +166,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams a) {
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
                     float x = acc[g][u] * corr;
-                    x = __builtin_fmaf(p[0], vf[0][u], x);
-                    x = __builtin_fmaf(p[1], vf[1][u], x);
-                    x = __builtin_fmaf(p[2], vf[2][u], x);
-                    x = __builtin_fmaf(p[3], vf[3][u], x);
+#pragma unroll
+                    for (int it = 0; it < 4; ++it) x = __builtin_fmaf(p[it], bf16_at(vv[t][it], u), x);
                     acc[g][u] = x;
                 }
                 m_[g] = mn;
@@ -203,16 +204,16 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams a) {
         }
     }
     __syncthreads();
-    // block partial
+    // block partial (waves merged in order)
     const int64_t pbase = static_cast<int64_t>(h) * a.nsplit + split;
-    for (int o = tid; o < G * 128; o += 256) {
+    for (int o = tid; o < G * 128; o += 64 * kWaves) {
         const int g = o >> 7, d = o & 127;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][g][0]);
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_ml[w][g][0]);
         float L = 0.0f, A = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < kWaves; ++w) {
             const float wt = wexp(s_ml[w][g][0], M);
             L += s_ml[w][g][1] * wt;
             A += s_acc[w][g][d] * wt;
@@ -230,63 +231,79 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams a) {
     if (!s_last) return;
     __threadfence();
 
-    // final merge for head h, splits in order
+    // ---- final merge of head h's nsplit partials (deterministic order) ----
     const float* pml = a.part_ml + static_cast<int64_t>(h) * a.nsplit * G * 2;
-    if (tid < G) {
-        const int g = tid;
+    for (int i = tid; i < a.nsplit * G; i += 64 * kWaves) s_w[i] = pml[2 * i];
+    __syncthreads();
+    if (wave < G) {
+        const int g = wave;
         float M = -INFINITY;
-        for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, pml[(s * G + g) * 2]);
+        for (int s = lane; s < a.nsplit; s += 64) M = fmaxf(M, s_w[s * G + g]);
+        M = wave_max(M);
         float L = 0.0f;
-        for (int s = 0; s < a.nsplit; ++s) {
-            const float ms = pml[(s * G + g) * 2];
-            const float w = (ms == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
-            s_w[s * G + g] = w;
-            L += pml[(s * G + g) * 2 + 1] * w;
+        for (int s = lane; s < a.nsplit; s += 64) L += pml[(s * G + g) * 2 + 1] * wexp(s_w[s * G + g], M);
+        L = wave_sum(L);
+        if (lane == 0) {
+            s_ML[g][0] = M;
+            s_ML[g][1] = L;
         }
-        s_ML[g][0] = M;
-        s_ML[g][1] = L;
     }
     __syncthreads();
+    for (int i = tid; i < a.nsplit * G; i += 64 * kWaves) s_w[i] = wexp(s_w[i], s_ML[i % G][0]);
+    __syncthreads();
+    // thread -> 4 consecutive outputs x one quarter of the splits
     const float* pacc = a.part_acc + static_cast<int64_t>(h) * a.nsplit * G * 128;
-    for (int o = tid; o < G * 128; o += 256) {
-        const int g = o >> 7, d = o & 127;
-        float A = 0.0f;
-        int s = 0;
-        for (; s + 8 <= a.nsplit; s += 8) {
-            float v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = pacc[((s + u) * G + g) * 128 + d];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float w = s_w[(s + u) * G + g];
-                if (w != 0.0f) A = __builtin_fmaf(v[u], w, A);
-            }
-        }
-        for (; s < a.nsplit; ++s) {
+    const int o4 = (tid & 127) * 4;  // output index (g * 128 + d), 4 at a time
+    const int quarter = tid >> 7;    // 0..3
+    for (int o = o4; o < G * 128; o += 512) {
+        const int g = o >> 7;
+        float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s = quarter; s < a.nsplit; s += 4) {
             const float w = s_w[s * G + g];
-            if (w != 0.0f) A = __builtin_fmaf(pacc[(s * G + g) * 128 + d], w, A);
+            if (w == 0.0f) continue;
+            const float4 v = *reinterpret_cast<const float4*>(pacc + static_cast<int64_t>(s) * G * 128 + o);
+            A.x = __builtin_fmaf(v.x, w, A.x);
+            A.y = __builtin_fmaf(v.y, w, A.y);
+            A.z = __builtin_fmaf(v.z, w, A.z);
+            A.w = __builtin_fmaf(v.w, w, A.w);
         }
+        s_red[quarter][o + 0] = A.x;
+        s_red[quarter][o + 1] = A.y;
+        s_red[quarter][o + 2] = A.z;
+        s_red[quarter][o + 3] = A.w;
+    }
+    __syncthreads();
+    for (int o = tid; o < G * 128; o += 64 * kWaves) {
+        const int g = o >> 7;
+        const float A = ((s_red[0][o] + s_red[1][o]) + s_red[2][o]) + s_red[3][o];
         const float L = s_ML[g][1];
-        const float r = L > 0.0f ? A / L : 0.0f;
-        a.out[(static_cast<int64_t>(h) * G + g) * 128 + d] = f32_to_bf16(r);
-        if (a.lse && d == 0)
+        a.out[static_cast<int64_t>(h) * G * 128 + o] = f32_to_bf16(L > 0.0f ? A / L : 0.0f);
+        if (a.lse && (o & 127) == 0)
             a.lse[static_cast<int64_t>(h) * G + g] =
                 L > 0.0f ? (s_ML[g][0] + log2f(L)) * 0.69314718055994530942f : -INFINITY;
     }
     if (tid == 0) a.counter[h] = 0;
 }
 
+// Rows per wave: two tiles when the head has enough rows to give every CU
+// about two workgroups, otherwise one.
+int tiles_for(int rows, int H) {
+    const int blocks_one_tile = (rows + kWaves * 16 - 1) / (kWaves * 16);
+    return blocks_one_tile * H > 512 ? 2 : 1;
+}
+
 int nsplit_for(const imi_attention_args* a) {
     const int rows = a->static_len + a->max_rows;
-    return rows <= 0 ? 1 : (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    const int rb = kWaves * 16 * tiles_for(rows, a->kv_heads);
+    return rows <= 0 ? 1 : (rows + rb - 1) / rb;
 }
 
 // Splits the workspace is sized for: any static_len up to steady_stride, so a
 // workspace sized once stays valid while the steady zone grows.
 int nsplit_bound(const imi_attention_args* a) {
     const int64_t srows = a->steady_stride > a->static_len ? a->steady_stride : a->static_len;
-    const int64_t rows = srows + a->max_rows;
-    return rows <= 0 ? 1 : static_cast<int>((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+    const int rows = static_cast<int>(srows + a->max_rows);
+    return rows <= 0 ? 1 : (rows + kWaves * 16 - 1) / (kWaves * 16);
 }
 
 size_t attn_workspace(const imi_attention_args* a, AttnParams* p) {
@@ -300,6 +317,8 @@ size_t attn_workspace(const imi_attention_args* a, AttnParams* p) {
         p->part_ml = ml;
         p->counter = cnt;
         p->nsplit = nsplit_for(a);
+        const int rows = a->static_len + a->max_rows;
+        p->rows_per_block = kWaves * 16 * tiles_for(rows, a->kv_heads);
     }
     return cv.used();
 }
@@ -328,7 +347,10 @@ int attn_validate(const imi_attention_args* a, bool need_sel) {
 
 template <int G>
 void launch_g(const AttnParams& p, int blocks, hipStream_t stream) {
-    hipLaunchKernelGGL(attention_kernel<G>, dim3(blocks), dim3(256), 0, stream, p);
+    if (p.rows_per_block == kWaves * 32)
+        hipLaunchKernelGGL((attention_kernel<G, 2>), dim3(blocks), dim3(64 * kWaves), 0, stream, p);
+    else
+        hipLaunchKernelGGL((attention_kernel<G, 1>), dim3(blocks), dim3(64 * kWaves), 0, stream, p);
 }
 
 int attn_launch(const imi_attention_args* a, const int32_t* row_loc, hipStream_t stream) {

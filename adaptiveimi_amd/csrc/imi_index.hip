@@ -167,31 +167,35 @@ __global__ __launch_bounds__(256) void ix_compact_pad_kernel(IxParams a, Compact
 }
 
 // list[h][pos] = src[h][perm[h][pos]] for keys and values; 16 lanes per
-// 256-byte row, 16 rows per wave.
+// 256-byte row, 32 rows per wave with every load issued before any store.
+constexpr int kPermRowsPerWave = 32;
+
 __global__ __launch_bounds__(256) void ix_permute_kernel(const uint16_t* keys, const uint16_t* values, int64_t hs,
                                                          int64_t ts, int T, const int32_t* perm, uint16_t* lk,
                                                          uint16_t* lv, int64_t list_rows) {
     const int h = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = lane_id();
     const int rg = lane >> 4, li = lane & 15;
-    const int base = blockIdx.x * 64 + wave * 16;
-    uint4 kv[4], vv[4];
-    int dst[4];
+    const int base = (blockIdx.x * 4 + wave) * kPermRowsPerWave;
+    const int my = base + lane;
+    const int tok = (lane < kPermRowsPerWave && my < T) ? perm[static_cast<int64_t>(h) * T + my] : 0;
+    constexpr int IT = kPermRowsPerWave / 4;
+    uint4 kv[IT], vv[IT];
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int pos = base + it * 4 + rg;
-        dst[it] = pos;
-        if (pos < T) {
-            const int t = perm[static_cast<int64_t>(h) * T + pos];
+    for (int it = 0; it < IT; ++it) {
+        const int j = it * 4 + rg;
+        const int t = __shfl(tok, j);
+        if (base + j < T) {
             const int64_t so = h * hs + static_cast<int64_t>(t) * ts + li * 8;
             kv[it] = *reinterpret_cast<const uint4*>(keys + so);
             vv[it] = *reinterpret_cast<const uint4*>(values + so);
         }
     }
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        if (dst[it] < T) {
-            const int64_t dofs = (static_cast<int64_t>(h) * list_rows + dst[it]) * 128 + li * 8;
+    for (int it = 0; it < IT; ++it) {
+        const int pos = base + it * 4 + rg;
+        if (pos < T) {
+            const int64_t dofs = (static_cast<int64_t>(h) * list_rows + pos) * 128 + li * 8;
             *reinterpret_cast<uint4*>(lk + dofs) = kv[it];
             *reinterpret_cast<uint4*>(lv + dofs) = vv[it];
         }
@@ -334,7 +338,8 @@ extern "C" int imi_build_index(const imi_index_args* a, imi_stream_t stream_) {
         IMI_LAUNCH_CHECK("ix_compact_pad_kernel");
     }
 
-    hipLaunchKernelGGL(ix_permute_kernel, dim3((a->n_tokens + 63) / 64, p.H), dim3(256), 0, stream, a->keys,
+    hipLaunchKernelGGL(ix_permute_kernel, dim3((a->n_tokens + 4 * kPermRowsPerWave - 1) / (4 * kPermRowsPerWave), p.H),
+                       dim3(256), 0, stream, a->keys,
                        a->values, a->head_stride, a->token_stride, a->n_tokens, a->perm, a->list_keys,
                        a->list_values, a->list_rows);
     IMI_LAUNCH_CHECK("ix_permute_kernel");

@@ -155,30 +155,47 @@ __global__ __launch_bounds__(256) void km_assign_kernel(KmParams a) {
 }
 
 // Per segment: exclusive scan of the [label][block] counts, cluster offsets,
-// empty-cluster ordinals, inertia and the early-stop test.
+// empty-cluster ordinals, inertia (fixed reduction order) and the early-stop
+// test of kmeans_core.cpp:244-262.
 __global__ __launch_bounds__(1024) void km_scan_kernel(KmParams a, int it) {
     __shared__ int sh[40];
+    __shared__ int soff[257];
+    __shared__ float sred[16];
     __shared__ int stop;
     const int seg = blockIdx.x;
     if (a.done && a.done[seg]) return;
     const int p = seg % a.P;
     const int k = a.k[p];
+    const int tid = threadIdx.x;
+    // inertia partials: contiguous chunk per thread, then waves in order
+    const float* ip = a.ipart + static_cast<int64_t>(seg) * a.nblk;
+    const int per = (a.nblk + 1023) / 1024;
+    float part = 0.0f;
+    for (int b = tid * per; b < (tid + 1) * per && b < a.nblk; ++b) part += ip[b];
+    part = wave_sum(part);
+    if ((tid & 63) == 0) sred[tid >> 6] = part;
     int32_t* hist = a.hist + static_cast<int64_t>(seg) * a.kmax * a.nblk;
     block_exclusive_scan_1024(hist, static_cast<int64_t>(k) * a.nblk, sh);
     int32_t* off = a.off + static_cast<int64_t>(seg) * (a.kmax + 1);
-    for (int c = threadIdx.x; c < k; c += 1024) off[c] = hist[static_cast<int64_t>(c) * a.nblk];
-    if (threadIdx.x == 0) off[k] = a.T;
+    for (int c = tid; c < k; c += 1024) {
+        const int o = hist[static_cast<int64_t>(c) * a.nblk];
+        off[c] = o;
+        soff[c] = o;
+    }
+    if (tid == 0) {
+        off[k] = a.T;
+        soff[k] = a.T;
+    }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         int e = 0;
         int32_t* emp = a.empties + static_cast<int64_t>(seg) * a.kmax;
         for (int c = 0; c < k; ++c) {
             emp[c] = e;
-            if (off[c + 1] == off[c]) ++e;
+            if (soff[c + 1] == soff[c]) ++e;
         }
         float inertia = 0.0f;
-        const float* ip = a.ipart + static_cast<int64_t>(seg) * a.nblk;
-        for (int b = 0; b < a.nblk; ++b) inertia += ip[b];
+        for (int w = 0; w < 16; ++w) inertia += sred[w];
         if (a.iters) a.iters[seg] = it + 1;
         const float prev = a.prev[seg];
         const float change = fabsf(prev - inertia);
@@ -188,7 +205,7 @@ __global__ __launch_bounds__(1024) void km_scan_kernel(KmParams a, int it) {
         if (!stop) a.prev[seg] = inertia;
     }
     __syncthreads();
-    if (threadIdx.x == 0 && stop && a.done) a.done[seg] = 1;
+    if (tid == 0 && stop && a.done) a.done[seg] = 1;
 }
 
 __global__ __launch_bounds__(256) void km_scatter_kernel(KmParams a) {
@@ -202,45 +219,109 @@ __global__ __launch_bounds__(256) void km_scatter_kernel(KmParams a) {
     a.sorted[so + pos] = t;
 }
 
-// M-step for one cluster: thread d sums dim d of the members in ascending
-// token order (dependent fp32 adds, loads batched 16 ahead).
-__global__ __launch_bounds__(64) void km_update_kernel(KmParams a, int it, Draws draws) {
+// M-step for one cluster.  The sum must follow the reference's order (members
+// in ascending token order, one dependent fp32 add each), so it is a single
+// chain per dimension; wave 0 runs the chains (lane d = dimension d) out of
+// LDS while waves 1..15 gather the next round of member rows into the other
+// half of a double-buffered ring (member ids are prefetched one round ahead).
+constexpr int kMsRows = 256;
+
+template <int DP>
+__global__ __launch_bounds__(1024) void km_update_kernel(KmParams a, int it, Draws draws) {
+    __shared__ uint4 buf[2][kMsRows * DP / 8];   // bf16 rows, 16-byte parts
+    __shared__ int ids[2][kMsRows];
     const int c = blockIdx.x, seg = blockIdx.y;
     const int h = seg / a.P, p = seg % a.P;
     if (c >= a.k[p]) return;
     if (a.done && a.done[seg]) return;
-    const int d = threadIdx.x;
-    const bool live = d < a.DP;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int32_t* off = a.off + static_cast<int64_t>(seg) * (a.kmax + 1);
     const int lo = off[c], hi = off[c + 1];
-    const uint16_t* base = a.keys + h * a.hs + p * a.DP + (live ? d : 0);
-    float out;
-    if (hi > lo) {
-        const int32_t* srt = a.sorted + static_cast<int64_t>(seg) * a.T;
-        float acc = 0.0f;
-        for (int i0 = lo; i0 < hi; i0 += 64) {
-            const int n = min(64, hi - i0);
-            const int my_tok = d < n ? srt[i0 + d] : 0;
-            for (int u0 = 0; u0 < n; u0 += 16) {
-                float v[16];
-#pragma unroll
-                for (int u = 0; u < 16; ++u) {
-                    const int tok = __shfl(my_tok, u0 + u);
-                    v[u] = (u0 + u < n) ? bf16_to_f32(base[static_cast<int64_t>(tok) * a.ts]) : 0.0f;
-                }
-#pragma unroll
-                for (int u = 0; u < 16; ++u)
-                    if (u0 + u < n) acc = acc + v[u];
-            }
+    const uint16_t* kbase = a.keys + h * a.hs + p * DP;
+    float* dst = a.cent + (static_cast<int64_t>(seg) * a.kmax + c) * DP;
+    if (hi == lo) {
+        if (tid < DP) {
+            const int e = a.empties[static_cast<int64_t>(seg) * a.kmax + c];
+            const int tok = draws.v[e];
+            dst[tid] = bf16_to_f32(kbase[static_cast<int64_t>(tok) * a.ts + tid]);
         }
-        const float inv = 1.0f / static_cast<float>(hi - lo);
-        out = acc * inv;
-    } else {
-        const int e = a.empties[static_cast<int64_t>(seg) * a.kmax + c];
-        const int tok = draws.v[e];
-        out = bf16_to_f32(base[static_cast<int64_t>(tok) * a.ts]);
+        return;
     }
-    if (live) a.cent[(static_cast<int64_t>(seg) * a.kmax + c) * a.DP + d] = out;
+    const int32_t* srt = a.sorted + static_cast<int64_t>(seg) * a.T;
+    const int n = hi - lo;
+    const int rounds = (n + kMsRows - 1) / kMsRows;
+    constexpr int PARTS = DP / 8;               // 16-byte parts per row
+    const int ltid = tid - 64;                   // loader index (waves 1..15)
+    // prologue: ids of rounds 0 and 1, rows of round 0
+    for (int i = tid; i < 2 * kMsRows; i += 1024) {
+        const int r = i / kMsRows, j = i - r * kMsRows;
+        const int pos = lo + r * kMsRows + j;
+        ids[r][j] = pos < hi ? srt[pos] : 0;
+    }
+    __syncthreads();
+    {
+        const int cnt = n < kMsRows ? n : kMsRows;
+        for (int i = tid; i < cnt * PARTS; i += 1024) {
+            const int row = i / PARTS, part = i - row * PARTS;
+            buf[0][row * PARTS + part] =
+                *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(ids[0][row]) * a.ts + part * 8);
+        }
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    for (int r = 0; r < rounds; ++r) {
+        const int b = r & 1;
+        if (wave == 0) {
+            const int cnt = (n - r * kMsRows) < kMsRows ? (n - r * kMsRows) : kMsRows;
+            if (lane < DP) {
+                const uint16_t* rows = reinterpret_cast<const uint16_t*>(buf[b]);
+                int row = 0;
+                for (; row + 8 <= cnt; row += 8) {
+                    float v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) v[u] = bf16_to_f32(rows[(row + u) * DP + lane]);
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) acc = acc + v[u];
+                }
+                for (; row < cnt; ++row) acc = acc + bf16_to_f32(rows[row * DP + lane]);
+            }
+        } else {
+            // rows of round r + 1 (ids in ids[b ^ 1]) and ids of round r + 2
+            // (into ids[b], free since round r's rows are already in LDS):
+            // every global load is issued before any LDS store.
+            constexpr int PER = (kMsRows * PARTS + 959) / 960;
+            uint4 v[PER];
+            int slot[PER];
+            int nid = -1;
+            if (r + 1 < rounds) {
+                const int base = (r + 1) * kMsRows;
+                const int cnt = (n - base) < kMsRows ? (n - base) : kMsRows;
+#pragma unroll
+                for (int u = 0; u < PER; ++u) {
+                    const int i = ltid + u * 960;
+                    slot[u] = -1;
+                    if (i < cnt * PARTS) {
+                        const int row = i / PARTS, part = i - row * PARTS;
+                        v[u] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(ids[b ^ 1][row]) * a.ts +
+                                                               part * 8);
+                        slot[u] = i;
+                    }
+                }
+            }
+            if (r + 2 < rounds && ltid < kMsRows) {
+                const int pos = lo + (r + 2) * kMsRows + ltid;
+                nid = pos < hi ? srt[pos] : 0;
+            }
+            if (r + 1 < rounds) {
+#pragma unroll
+                for (int u = 0; u < PER; ++u)
+                    if (slot[u] >= 0) buf[b ^ 1][slot[u]] = v[u];
+            }
+            if (nid >= 0) ids[b][ltid] = nid;
+        }
+        __syncthreads();
+    }
+    if (tid < DP) dst[tid] = acc * (1.0f / static_cast<float>(n));
 }
 
 __global__ void km_reset_kernel(KmParams a) {
@@ -381,7 +462,10 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
         std::mt19937 rng(static_cast<unsigned>(it + 12345));
         std::uniform_int_distribution<int32_t> dist(0, a->n_tokens - 1);
         for (int e = 0; e < kmax; ++e) dr.v[e] = dist(rng);
-        hipLaunchKernelGGL(km_update_kernel, dim3(kmax, segs), dim3(64), 0, stream, p, it, dr);
+        if (dp == 64)
+            hipLaunchKernelGGL(km_update_kernel<64>, dim3(kmax, segs), dim3(1024), 0, stream, p, it, dr);
+        else
+            hipLaunchKernelGGL(km_update_kernel<32>, dim3(kmax, segs), dim3(1024), 0, stream, p, it, dr);
         IMI_LAUNCH_CHECK("km_update_kernel");
     }
     return IMI_OK;

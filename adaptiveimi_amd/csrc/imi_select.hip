@@ -29,16 +29,15 @@ namespace imi {
 namespace {
 
 constexpr int kSelThreads = 1024;
-constexpr int kMaxE = 16;      // cells per thread -> up to 16384 cells
 constexpr int kBins = 2048;
-constexpr int kCap = 4096;     // candidate capacity (power of two)
+constexpr int kCap = 2048;     // candidate capacity
 
 struct SelParams {
     const uint16_t* q;
     const float* cent;
     const int32_t* cnt;
     const int32_t* off;
-    int H, G, D, P, kmax, DP;
+    int H, G, D, P, kmax;
     int k[4];
     int ncells;
     int nprobe, max_tokens, buffer_pages, page_size;
@@ -76,79 +75,112 @@ __device__ __forceinline__ uint64_t cell_key(uint32_t okey, int g) {
     return (static_cast<uint64_t>(okey) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(g));
 }
 
+__device__ __forceinline__ int cell_of_key(uint64_t key) {
+    return static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(key & 0xFFFFFFFFull));
+}
+
+__device__ __forceinline__ int bucket_of(float s, float gmax, float inv) {
+    const float t = (gmax - s) * inv;
+    return t < static_cast<float>(kBins - 1) ? static_cast<int>(t) : kBins - 1;
+}
+
+// DP: subspace width (64 for 2-way IMI at D = 128); EPT: cells per thread.
+template <int DP, int EPT>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
-    extern __shared__ float smem[];
+    extern __shared__ uint64_t dyn[];
     __shared__ float qs[128];
     __shared__ float p1[256];
-    __shared__ int hist[kBins];
+    __shared__ int hist[kBins];         // bucket counts, then fill cursors
+    __shared__ int binbase[kBins + 1];  // first candidate slot of each bucket
+    __shared__ int xh[256];
     __shared__ int sh[48];
     __shared__ int shv[8];
-    __shared__ float shf[32];
+    __shared__ float shf[40];
 
     const int h = blockIdx.x;
     const int tid = threadIdx.x;
     const int k0 = a.k[0], k1 = a.k[1];
-    const int DP = a.DP;
-    float* cT = smem;  // [DP][k1] during scoring; reused for candidates
-    uint64_t* ck = reinterpret_cast<uint64_t*>(smem);
-    int* cs = reinterpret_cast<int*>(ck + kCap);
+    // LDS regions: c1T during scoring, candidates afterwards
+    float* c1T = reinterpret_cast<float*>(dyn);          // [DP][k1]
+    uint64_t* ck = dyn;                                  // [kCap] keys by bucket
+    int* cs = reinterpret_cast<int*>(ck + kCap);         // [kCap] sizes
+    int* co = cs + kCap;                                 // [kCap] CSR offsets
+    int* sg = co + kCap;                                 // [kCap] cell id in rank order
+    int* ss = sg + kCap;                                 // [kCap] size in rank order
+    int* so = ss + kCap;                                 // [kCap] offset in rank order
 
-    // 1. grouped-query sum (compute_impl.cu:80-87)
-    if (tid < a.D) {
-        float acc = 0.0f;
-        for (int g = 0; g < a.G; ++g) acc += bf16_to_f32(a.q[(static_cast<int64_t>(h) * a.G + g) * a.D + tid]);
-        qs[tid] = acc;
+    // ---- loads, all issued before the first wait ----
+    const int32_t* cntp = a.cnt + static_cast<int64_t>(h) * a.ncells;
+    int sz[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int g = e * kSelThreads + tid;
+        sz[e] = g < a.ncells ? cntp[g] : 0;
     }
     const float* c0 = a.cent + (static_cast<int64_t>(h) * a.P + 0) * a.kmax * DP;
     const float* c1 = a.cent + (static_cast<int64_t>(h) * a.P + 1) * a.kmax * DP;
+    float row[DP];
+    if (tid < k0) {
+        const float4* r4 = reinterpret_cast<const float4*>(c0 + static_cast<int64_t>(tid) * DP);
+#pragma unroll
+        for (int i = 0; i < DP / 4; ++i) {
+            const float4 v = r4[i];
+            row[4 * i] = v.x; row[4 * i + 1] = v.y; row[4 * i + 2] = v.z; row[4 * i + 3] = v.w;
+        }
+    }
     for (int i = tid; i < k1 * DP; i += kSelThreads) {
         const int j = i / DP, d = i - (i / DP) * DP;
-        cT[d * k1 + j] = c1[static_cast<int64_t>(j) * DP + d];
+        c1T[d * k1 + j] = c1[i];
     }
+    if (tid < a.D) {
+        float acc = 0.0f;   // grouped-query sum, g ascending (compute_impl.cu:80-87)
+        for (int g = 0; g < a.G; ++g) acc += bf16_to_f32(a.q[(static_cast<int64_t>(h) * a.G + g) * a.D + tid]);
+        qs[tid] = acc;
+    }
+    for (int i = tid; i < kBins; i += kSelThreads) hist[i] = 0;
+    if (tid == 0) shv[0] = 0;
     __syncthreads();
-    // 2. chain over the first subspace, once per l0
+    // chain over the first subspace, once per l0
     if (tid < k0) {
         float acc = 0.0f;
-        const float* row = c0 + static_cast<int64_t>(tid) * DP;
+#pragma unroll
         for (int d = 0; d < DP; ++d) acc = __builtin_fmaf(qs[d], row[d], acc);
         p1[tid] = acc;
     }
     __syncthreads();
 
-    // 3. scores of occupied cells (cell g = e * 1024 + tid)
-    const int E = (a.ncells + kSelThreads - 1) / kSelThreads;
-    const int32_t* cnt = a.cnt + static_cast<int64_t>(h) * a.ncells;
-    float sc[kMaxE];
-    int sz[kMaxE];
+    // ---- scores: the chain continues over the second subspace ----
+    float sc[EPT];
+    int jj[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int g = e * kSelThreads + tid;
+        const int gi = g < a.ncells ? g : 0;
+        const int i = gi / k1;
+        jj[e] = gi - i * k1;
+        sc[e] = p1[i];
+    }
+#pragma unroll
+    for (int d = 0; d < DP; ++d) {
+        const float qd = qs[DP + d];
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) sc[e] = __builtin_fmaf(qd, c1T[d * k1 + jj[e]], sc[e]);
+    }
     int nvalid = 0;
     float smax = -INFINITY, smin = INFINITY;
 #pragma unroll
-    for (int e = 0; e < kMaxE; ++e) {
-        sz[e] = 0;
-        sc[e] = 0.0f;
-        const int g = e * kSelThreads + tid;
-        if (e < E && g < a.ncells) {
-            const int n = cnt[g];
-            if (n > 0) {
-                const int i = g / k1, j = g - (g / k1) * k1;
-                float s = p1[i];
-                for (int d = 0; d < DP; ++d) s = __builtin_fmaf(qs[DP + d], cT[d * k1 + j], s);
-                sc[e] = s;
-                sz[e] = n;
-                ++nvalid;
-                smax = fmaxf(smax, s);
-                smin = fminf(smin, s);
-            }
+    for (int e = 0; e < EPT; ++e)
+        if (sz[e] > 0) {
+            ++nvalid;
+            smax = fmaxf(smax, sc[e]);
+            smin = fminf(smin, sc[e]);
         }
-    }
-    // block reductions
     {
         const int w = tid >> 6;
         const int nv = wave_sum_i(nvalid);
         const float mx = wave_max(smax);
         const float mn = -wave_max(-smin);
         if (lane_id() == 0) {
-            shv[0] = 0;
             sh[w] = nv;
             shf[w] = mx;
             shf[16 + w] = mn;
@@ -164,13 +196,12 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
             mn = fminf(mn, shf[16 + w]);
         }
         shv[1] = nv;
-        shf[0] = mx;
-        shf[1] = mn;
+        shf[32] = mx;
+        shf[33] = mn;
     }
-    for (int i = tid; i < kBins; i += kSelThreads) hist[i] = 0;
     __syncthreads();
     const int n_valid = shv[1];
-    const float gmax = shf[0], gmin = shf[1];
+    const float gmax = shf[32], gmin = shf[33];
     int kp = a.nprobe < a.buffer_pages ? a.nprobe : a.buffer_pages;
     kp = kp < n_valid ? kp : n_valid;
     int32_t* prefix_out = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
@@ -183,28 +214,22 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         return;
     }
 
-    // 4. linear buckets: higher score -> lower or equal bucket
+    // ---- linear buckets: higher score -> lower or equal bucket ----
     const float range = gmax - gmin;
     const float inv = range > 0.0f ? static_cast<float>(kBins) / range : 0.0f;
-    int bin[kMaxE];
 #pragma unroll
-    for (int e = 0; e < kMaxE; ++e) {
-        int b = 0;
-        if (sz[e] > 0) {
-            const float t = (gmax - sc[e]) * inv;
-            b = t < static_cast<float>(kBins - 1) ? static_cast<int>(t) : kBins - 1;
-            atomicAdd(&hist[b], 1);
-        }
-        bin[e] = b;
-    }
+    for (int e = 0; e < EPT; ++e)
+        if (sz[e] > 0) atomicAdd(&hist[bucket_of(sc[e], gmax, inv)], 1);
     __syncthreads();
-    // bucket holding the kp-th best cell
     {
         const int b0 = 2 * tid, b1 = 2 * tid + 1;
         const int h0 = hist[b0], h1 = hist[b1];
         int total;
         const int incl = block_incl_scan(h0 + h1, sh, total);
         const int excl = incl - h0 - h1;
+        binbase[b0] = excl;
+        binbase[b1] = excl + h0;
+        if (tid == kSelThreads - 1) binbase[kBins] = incl;
         if (excl < kp && excl + h0 >= kp) {
             shv[2] = b0;
             shv[3] = excl;
@@ -217,28 +242,27 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     }
     __syncthreads();
     const int bK = shv[2], c_lt = shv[3], c_le = shv[4];
-    uint64_t tau = 0;  // candidates of bucket bK need key >= tau
-    if (c_le > kCap) {
-        // exact: the (kp - c_lt)-th largest 64-bit key inside bucket bK
+    const bool exact = c_le > kCap;
+    uint64_t tau = 0;  // exact path: bucket-bK candidates need key >= tau
+    if (exact) {
         int remaining = kp - c_lt;
         uint64_t prefix = 0, mask = 0;
         for (int pass = 0; pass < 8; ++pass) {
             const int shift = 56 - 8 * pass;
-            for (int i = tid; i < 256; i += kSelThreads) hist[i] = 0;
+            for (int i = tid; i < 256; i += kSelThreads) xh[i] = 0;
             __syncthreads();
 #pragma unroll
-            for (int e = 0; e < kMaxE; ++e) {
-                if (sz[e] > 0 && bin[e] == bK) {
+            for (int e = 0; e < EPT; ++e) {
+                if (sz[e] > 0 && bucket_of(sc[e], gmax, inv) == bK) {
                     const uint64_t key = cell_key(order_key(sc[e]), e * kSelThreads + tid);
-                    if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
+                    if ((key & mask) == prefix) atomicAdd(&xh[(key >> shift) & 255], 1);
                 }
             }
             __syncthreads();
             if (tid < 64) {
-                // lane l owns digits 255-4l .. 252-4l (descending order)
                 int v[4], s = 0;
                 for (int u = 0; u < 4; ++u) {
-                    v[u] = hist[255 - 4 * tid - u];
+                    v[u] = xh[255 - 4 * tid - u];
                     s += v[u];
                 }
                 const int incl = wave_incl_scan(s);
@@ -252,117 +276,129 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
                 }
             }
             __syncthreads();
-            const int digit = shv[5];
             remaining -= shv[6];
-            prefix |= static_cast<uint64_t>(digit) << shift;
+            prefix |= static_cast<uint64_t>(shv[5]) << shift;
             mask |= static_cast<uint64_t>(255) << shift;
             __syncthreads();
         }
         tau = prefix;
     }
+    for (int i = tid; i < kBins; i += kSelThreads) hist[i] = 0;   // fill cursors
+    __syncthreads();
 
-    // 5. gather candidates
+    // ---- candidates, grouped by bucket ----
+    const int32_t* offs = a.off + static_cast<int64_t>(h) * (a.ncells + 1);
 #pragma unroll
-    for (int e = 0; e < kMaxE; ++e) {
+    for (int e = 0; e < EPT; ++e) {
         if (sz[e] > 0) {
+            const int b = bucket_of(sc[e], gmax, inv);
             const int g = e * kSelThreads + tid;
             const uint64_t key = cell_key(order_key(sc[e]), g);
-            bool take = bin[e] < bK || (bin[e] == bK && (c_le <= kCap || key >= tau));
-            if (take) {
-                const int slot = atomicAdd(&shv[0], 1);
+            if (b < bK || (b == bK && (!exact || key >= tau))) {
+                const int slot = binbase[b] + atomicAdd(&hist[b], 1);
                 ck[slot] = key;
                 cs[slot] = sz[e];
+                co[slot] = offs[g];
             }
         }
     }
     __syncthreads();
-    const int C = shv[0];
-    int NP = 1;
-    while (NP < C) NP <<= 1;
-    for (int i = C + tid; i < NP; i += kSelThreads) {
-        ck[i] = 0;
-        cs[i] = 0;
+    const int C = exact ? kp : c_le;
+    // rank inside the bucket by counting larger keys (buckets hold few cells)
+    for (int s = tid; s < C; s += kSelThreads) {
+        const uint64_t key = ck[s];
+        int lo = 0, hi2 = kBins;  // find bucket: last binbase <= s with non-empty segment
+        while (hi2 - lo > 1) {
+            const int mid = (lo + hi2) >> 1;
+            if (binbase[mid] <= s) lo = mid; else hi2 = mid;
+        }
+        const int seg_lo = binbase[lo];
+        const int seg_hi = (lo == bK && exact) ? binbase[lo] + (kp - c_lt) : binbase[lo + 1];
+        int r = 0;
+        for (int i = seg_lo; i < seg_hi; ++i) r += ck[i] > key;
+        const int pos = seg_lo + r;
+        sg[pos] = cell_of_key(key);
+        ss[pos] = cs[s];
+        so[pos] = co[s];
     }
     __syncthreads();
-    // 6. bitonic sort, descending by key
-    for (int kk = 2; kk <= NP; kk <<= 1) {
-        for (int j = kk >> 1; j > 0; j >>= 1) {
-            for (int i = tid; i < NP; i += kSelThreads) {
-                const int l = i ^ j;
-                if (l > i) {
-                    const uint64_t x = ck[i], y = ck[l];
-                    const bool up = (i & kk) == 0;
-                    if (up ? (x < y) : (x > y)) {
-                        ck[i] = y;
-                        ck[l] = x;
-                        const int t = cs[i];
-                        cs[i] = cs[l];
-                        cs[l] = t;
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
 
-    // 7. budget rules in rank order (ranks 4*tid .. 4*tid+3)
-    int s4[4], pg4[4];
+    // ---- budget rules in rank order (ranks 2*tid, 2*tid+1) ----
+    int s2[2], pg2[2];
     int tsum = 0, psum = 0;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int r = 4 * tid + u;
-        s4[u] = r < C ? cs[r] : 0;
-        pg4[u] = (s4[u] + a.page_size - 1) / a.page_size;
-        tsum += s4[u];
-        psum += pg4[u];
+    for (int u = 0; u < 2; ++u) {
+        const int r = 2 * tid + u;
+        s2[u] = r < C ? ss[r] : 0;
+        pg2[u] = (s2[u] + a.page_size - 1) / a.page_size;
+        tsum += s2[u];
+        psum += pg2[u];
     }
     int ttot, ptot;
     const int tincl = block_incl_scan(tsum, sh, ttot);
     const int pincl = block_incl_scan(psum, sh, ptot);
     int texcl = tincl - tsum, pexcl = pincl - psum;
     int kept = 0;
-    int excl_tok[4];
+    int excl_tok[2];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int r = 4 * tid + u;
+    for (int u = 0; u < 2; ++u) {
+        const int r = 2 * tid + u;
         excl_tok[u] = texcl;
-        pexcl += pg4[u];
+        pexcl += pg2[u];
         const bool keep = r < C && r < a.nprobe && texcl < a.max_tokens && pexcl <= a.buffer_pages;
         kept += keep ? 1 : 0;
-        texcl += s4[u];
+        texcl += s2[u];
     }
     int m;
     block_incl_scan(kept, sh, m);
-    // outputs for ranks < m
     int32_t* out_cell = a.sel_cell + static_cast<int64_t>(h) * a.sel_cap;
     int32_t* out_off = a.sel_offset + static_cast<int64_t>(h) * a.sel_cap;
     int32_t* out_cnt = a.sel_count + static_cast<int64_t>(h) * a.sel_cap;
-    const int32_t* offs = a.off + static_cast<int64_t>(h) * (a.ncells + 1);
+    int* sp = cs;  // exclusive row prefix in rank order (cs is free now)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int r = 4 * tid + u;
+    for (int u = 0; u < 2; ++u) {
+        const int r = 2 * tid + u;
         if (r < m) {
-            const int g = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(ck[r] & 0xFFFFFFFFull));
-            const int o = offs[g];
-            out_cell[r] = g;
-            out_off[r] = o;
-            out_cnt[r] = s4[u];
+            out_cell[r] = sg[r];
+            out_off[r] = so[r];
+            out_cnt[r] = s2[u];
             prefix_out[r] = excl_tok[u];
-            if (a.row_loc) {
-                int32_t* rl = a.row_loc + static_cast<int64_t>(h) * a.max_rows + excl_tok[u];
-                for (int i = 0; i < s4[u]; ++i) rl[i] = o + i;
-            }
+            sp[r] = excl_tok[u];
         }
         if (r == m - 1) {
-            prefix_out[m] = excl_tok[u] + s4[u];
+            const int total = excl_tok[u] + s2[u];
+            prefix_out[m] = total;
+            sp[m] = total;
             a.n_sel[h] = m;
-            a.n_rows[h] = excl_tok[u] + s4[u];
+            a.n_rows[h] = total;
+            shv[7] = total;
         }
     }
     if (m == 0 && tid == 0) {
         a.n_sel[h] = 0;
         a.n_rows[h] = 0;
         prefix_out[0] = 0;
+        shv[7] = 0;
+    }
+    if (a.row_loc == nullptr) return;
+    __syncthreads();
+    // ---- row-location table: thread t expands a contiguous run of rows ----
+    const int total = shv[7];
+    const int per = (total + kSelThreads - 1) / kSelThreads;
+    const int j0 = tid * per;
+    if (j0 < total) {
+        int lo = 0, hi2 = m;  // last r with sp[r] <= j0
+        while (hi2 - lo > 1) {
+            const int mid = (lo + hi2) >> 1;
+            if (sp[mid] <= j0) lo = mid; else hi2 = mid;
+        }
+        int r = lo;
+        int32_t* rl = a.row_loc + static_cast<int64_t>(h) * a.max_rows;
+        const int j1 = j0 + per < total ? j0 + per : total;
+        for (int j = j0; j < j1; ++j) {
+            while (j >= sp[r + 1]) ++r;
+            rl[j] = so[r] + (j - sp[r]);
+        }
     }
 }
 
@@ -403,16 +439,30 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     kmax = a->k[0] > a->k[1] ? a->k[0] : a->k[1];
     IMI_REQUIRE(a->k[0] >= 1 && a->k[1] >= 1 && kmax <= 256, IMI_ERR_UNSUPPORTED, "imi_select: k outside [1,256]");
     ncells = static_cast<int64_t>(a->k[0]) * a->k[1];
-    IMI_REQUIRE(ncells <= static_cast<int64_t>(kMaxE) * kSelThreads, IMI_ERR_UNSUPPORTED,
-                "imi_select: %lld cells exceed %d", static_cast<long long>(ncells), kMaxE * kSelThreads);
+    IMI_REQUIRE(ncells <= 16 * kSelThreads, IMI_ERR_UNSUPPORTED, "imi_select: %lld cells exceed %d",
+                static_cast<long long>(ncells), 16 * kSelThreads);
     const int kprime = a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages;
     IMI_REQUIRE(kprime <= kCap, IMI_ERR_UNSUPPORTED, "imi_select: min(nprobe, buffer_pages)=%d exceeds %d", kprime,
                 kCap);
     IMI_REQUIRE(a->sel_cap >= kprime, IMI_ERR_INVALID, "imi_select: sel_cap %d < min(nprobe, buffer_pages) %d",
                 a->sel_cap, kprime);
-    const int dp = a->dim / a->parts;
-    const size_t lds = static_cast<size_t>(dp) * a->k[1] * 4;
-    IMI_REQUIRE(lds <= kCap * 12, IMI_ERR_UNSUPPORTED, "imi_select: k too large for the LDS layout");
+    return IMI_OK;
+}
+
+template <int EPT>
+int launch_ept(const SelParams& p, int H, hipStream_t stream) {
+    constexpr int DP = 64;
+    const size_t cand = static_cast<size_t>(kCap) * (sizeof(uint64_t) + 5 * sizeof(int));
+    const size_t ct = static_cast<size_t>(DP) * p.k[1] * sizeof(float);
+    const size_t lds = cand > ct ? cand : ct;
+    static bool attr_set = false;
+    if (!attr_set) {
+        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&select_kernel<DP, EPT>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((select_kernel<DP, EPT>), dim3(H), dim3(kSelThreads), lds, stream, p);
+    IMI_LAUNCH_CHECK("select_kernel");
     return IMI_OK;
 }
 
@@ -433,7 +483,6 @@ int select_launch(const imi_select_args* a, int32_t* row_loc, int max_rows, hipS
     p.D = a->dim;
     p.P = a->parts;
     p.kmax = kmax;
-    p.DP = a->dim / a->parts;
     for (int i = 0; i < 4; ++i) p.k[i] = a->k[i];
     p.ncells = static_cast<int>(ncells);
     p.nprobe = a->nprobe;
@@ -449,16 +498,12 @@ int select_launch(const imi_select_args* a, int32_t* row_loc, int max_rows, hipS
     p.sel_cap = a->sel_cap;
     p.row_loc = row_loc;
     p.max_rows = max_rows;
-    const size_t lds = kCap * 12;
-    static bool attr_set = false;
-    if (!attr_set) {
-        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&select_kernel),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-        attr_set = true;
-    }
-    hipLaunchKernelGGL(select_kernel, dim3(a->kv_heads), dim3(kSelThreads), lds, stream, p);
-    IMI_LAUNCH_CHECK("select_kernel");
-    return IMI_OK;
+    const int ept = static_cast<int>((ncells + kSelThreads - 1) / kSelThreads);
+    if (ept <= 1) return launch_ept<1>(p, a->kv_heads, stream);
+    if (ept <= 2) return launch_ept<2>(p, a->kv_heads, stream);
+    if (ept <= 4) return launch_ept<4>(p, a->kv_heads, stream);
+    if (ept <= 8) return launch_ept<8>(p, a->kv_heads, stream);
+    return launch_ept<16>(p, a->kv_heads, stream);
 }
 
 }  // namespace imi
