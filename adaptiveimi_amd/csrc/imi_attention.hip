@@ -69,6 +69,17 @@ __device__ __forceinline__ float bf16_at(const uint4& v, int u) {
 
 __device__ __forceinline__ float safe_exp2(float x) { return x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(x); }
 
+// Agent-scope relaxed atomic store / load: encoded with the coherence bit, so
+// other XCDs see the value without an L2 write-back / invalidate.
+__device__ __forceinline__ void coherent_store(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float coherent_load(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// s_waitcnt vmcnt(0): this thread's stores have been acknowledged.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Weight exp2(m - M) of a state with running max m inside a merge whose max
 // is M; an empty state (m = -inf) weighs 0 even when M is -inf too.
 __device__ __forceinline__ float wexp(float m, float M) { return m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M); }
@@ -121,6 +132,9 @@ __global__ __launch_bounds__(512) void attention_kernel(AttnParams a) {
     const uint16_t* lvh = a.lv + static_cast<int64_t>(h) * a.list_rows * 128;
 
     if (row0 < N) {
+        // Branch-free gather: rows past N read row 0 of the list (always in
+        // bounds) and get a -inf score, so all 2 * 4 * TILES loads issue
+        // back to back.
         uint4 kk[TILES][4], vv[TILES][4];
         bool ok[TILES][4];
 #pragma unroll
@@ -131,17 +145,12 @@ __global__ __launch_bounds__(512) void attention_kernel(AttnParams a) {
                 const int n = row0 + j;
                 const int loc = __shfl(myloc, j);
                 ok[t][it] = n < N;
-                const uint16_t* kp = n < a.static_len ? skh + static_cast<int64_t>(n) * 128
-                                                      : lkh + static_cast<int64_t>(loc) * 128;
-                const uint16_t* vp = n < a.static_len ? svh + static_cast<int64_t>(n) * 128
-                                                      : lvh + static_cast<int64_t>(loc) * 128;
-                if (ok[t][it]) {
-                    kk[t][it] = *reinterpret_cast<const uint4*>(kp + li * 8);
-                    vv[t][it] = *reinterpret_cast<const uint4*>(vp + li * 8);
-                } else {
-                    kk[t][it] = make_uint4(0, 0, 0, 0);
-                    vv[t][it] = make_uint4(0, 0, 0, 0);
-                }
+                const bool st = n < a.static_len;
+                const int64_t roff = (st ? static_cast<int64_t>(n) : static_cast<int64_t>(ok[t][it] ? loc : 0)) * 128;
+                const uint16_t* kp = (st ? skh : lkh) + roff + li * 8;
+                const uint16_t* vp = (st ? svh : lvh) + roff + li * 8;
+                kk[t][it] = *reinterpret_cast<const uint4*>(kp);
+                vv[t][it] = *reinterpret_cast<const uint4*>(vp);
             }
 #pragma unroll
         for (int t = 0; t < TILES; ++t) {
@@ -157,7 +166,6 @@ __global__ __launch_bounds__(512) void attention_kernel(AttnParams a) {
             for (int g = 0; g < G; ++g) {
                 const float tm = fmaxf(fmaxf(s[0][g], s[1][g]), fmaxf(s[2][g], s[3][g]));
                 const float mn = fmaxf(m_[g], tm);
-                if (mn == -INFINITY) continue;
                 const float corr = wexp(m_[g], mn);
                 float p[4];
 #pragma unroll
@@ -204,7 +212,8 @@ __global__ __launch_bounds__(512) void attention_kernel(AttnParams a) {
         }
     }
     __syncthreads();
-    // block partial (waves merged in order)
+    // block partial (waves merged in order), published with agent-coherent
+    // stores (write-through past the XCD's L2) instead of a device fence
     const int64_t pbase = static_cast<int64_t>(h) * a.nsplit + split;
     for (int o = tid; o < G * 128; o += 64 * kWaves) {
         const int g = o >> 7, d = o & 127;
@@ -218,22 +227,21 @@ __global__ __launch_bounds__(512) void attention_kernel(AttnParams a) {
             L += s_ml[w][g][1] * wt;
             A += s_acc[w][g][d] * wt;
         }
-        a.part_acc[(pbase * G + g) * 128 + d] = A;
+        coherent_store(a.part_acc + (pbase * G + g) * 128 + d, A);
         if (d == 0) {
-            a.part_ml[(pbase * G + g) * 2 + 0] = M;
-            a.part_ml[(pbase * G + g) * 2 + 1] = L;
+            coherent_store(a.part_ml + (pbase * G + g) * 2 + 0, M);
+            coherent_store(a.part_ml + (pbase * G + g) * 2 + 1, L);
         }
     }
-    __threadfence();
+    wait_stores();
     __syncthreads();
     if (tid == 0) s_last = atomicAdd(&a.counter[h], 1) == a.nsplit - 1;
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
 
     // ---- final merge of head h's nsplit partials (deterministic order) ----
     const float* pml = a.part_ml + static_cast<int64_t>(h) * a.nsplit * G * 2;
-    for (int i = tid; i < a.nsplit * G; i += 64 * kWaves) s_w[i] = pml[2 * i];
+    for (int i = tid; i < a.nsplit * G; i += 64 * kWaves) s_w[i] = coherent_load(pml + 2 * i);
     __syncthreads();
     if (wave < G) {
         const int g = wave;
@@ -241,7 +249,7 @@ __global__ __launch_bounds__(512) void attention_kernel(AttnParams a) {
         for (int s = lane; s < a.nsplit; s += 64) M = fmaxf(M, s_w[s * G + g]);
         M = wave_max(M);
         float L = 0.0f;
-        for (int s = lane; s < a.nsplit; s += 64) L += pml[(s * G + g) * 2 + 1] * wexp(s_w[s * G + g], M);
+        for (int s = lane; s < a.nsplit; s += 64) L += coherent_load(pml + (s * G + g) * 2 + 1) * wexp(s_w[s * G + g], M);
         L = wave_sum(L);
         if (lane == 0) {
             s_ML[g][0] = M;
@@ -251,26 +259,32 @@ __global__ __launch_bounds__(512) void attention_kernel(AttnParams a) {
     __syncthreads();
     for (int i = tid; i < a.nsplit * G; i += 64 * kWaves) s_w[i] = wexp(s_w[i], s_ML[i % G][0]);
     __syncthreads();
-    // thread -> 4 consecutive outputs x one quarter of the splits
+    // thread -> 4 consecutive outputs x one quarter of the splits; loads of
+    // 4 splits are issued together
     const float* pacc = a.part_acc + static_cast<int64_t>(h) * a.nsplit * G * 128;
     const int o4 = (tid & 127) * 4;  // output index (g * 128 + d), 4 at a time
     const int quarter = tid >> 7;    // 0..3
     for (int o = o4; o < G * 128; o += 512) {
         const int g = o >> 7;
-        float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int s = quarter; s < a.nsplit; s += 4) {
-            const float w = s_w[s * G + g];
-            if (w == 0.0f) continue;
-            const float4 v = *reinterpret_cast<const float4*>(pacc + static_cast<int64_t>(s) * G * 128 + o);
-            A.x = __builtin_fmaf(v.x, w, A.x);
-            A.y = __builtin_fmaf(v.y, w, A.y);
-            A.z = __builtin_fmaf(v.z, w, A.z);
-            A.w = __builtin_fmaf(v.w, w, A.w);
+        float A[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int s0 = quarter; s0 < a.nsplit; s0 += 16) {
+            float v[4][4], w[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int s = s0 + 4 * u;
+                const bool in = s < a.nsplit;
+                w[u] = in ? s_w[s * G + g] : 0.0f;
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+                    v[u][x] = in ? coherent_load(pacc + static_cast<int64_t>(s) * G * 128 + o + x) : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int x = 0; x < 4; ++x) A[x] = __builtin_fmaf(v[u][x], w[u], A[x]);
         }
-        s_red[quarter][o + 0] = A.x;
-        s_red[quarter][o + 1] = A.y;
-        s_red[quarter][o + 2] = A.z;
-        s_red[quarter][o + 3] = A.w;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) s_red[quarter][o + x] = A[x];
     }
     __syncthreads();
     for (int o = tid; o < G * 128; o += 64 * kWaves) {

@@ -92,7 +92,6 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     __shared__ float p1[256];
     __shared__ int hist[kBins];         // bucket counts, then fill cursors
     __shared__ int binbase[kBins + 1];  // first candidate slot of each bucket
-    __shared__ int xh[256];
     __shared__ int sh[48];
     __shared__ int shv[8];
     __shared__ float shf[40];
@@ -108,6 +107,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     int* sg = co + kCap;                                 // [kCap] cell id in rank order
     int* ss = sg + kCap;                                 // [kCap] size in rank order
     int* so = ss + kCap;                                 // [kCap] offset in rank order
+    int* seg = so + kCap;                                // [kCap] segment (start | len << 16)
 
     // ---- loads, all issued before the first wait ----
     const int32_t* cntp = a.cnt + static_cast<int64_t>(h) * a.ncells;
@@ -214,112 +214,132 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         return;
     }
 
-    // ---- linear buckets: higher score -> lower or equal bucket ----
-    const float range = gmax - gmin;
-    const float inv = range > 0.0f ? static_cast<float>(kBins) / range : 0.0f;
+    // ---- candidates: iterative linear-bucket refinement ----
+    // st: 0 = dropped, 1 = in play, 2 = placed.  Each level buckets the
+    // in-play scores linearly over their [lo, hi] (higher score -> lower or
+    // equal bucket), places every bucket wholly above the one holding the
+    // kp-th best cell and, when that bucket still does not fit in kCap
+    // slots, refines inside it.  Placed cells form segments (one per bucket)
+    // that are already in rank order relative to each other.
+    int st[EPT];
 #pragma unroll
-    for (int e = 0; e < EPT; ++e)
-        if (sz[e] > 0) atomicAdd(&hist[bucket_of(sc[e], gmax, inv)], 1);
-    __syncthreads();
-    {
-        const int b0 = 2 * tid, b1 = 2 * tid + 1;
-        const int h0 = hist[b0], h1 = hist[b1];
-        int total;
-        const int incl = block_incl_scan(h0 + h1, sh, total);
-        const int excl = incl - h0 - h1;
-        binbase[b0] = excl;
-        binbase[b1] = excl + h0;
-        if (tid == kSelThreads - 1) binbase[kBins] = incl;
-        if (excl < kp && excl + h0 >= kp) {
-            shv[2] = b0;
-            shv[3] = excl;
-            shv[4] = excl + h0;
-        } else if (excl + h0 < kp && incl >= kp) {
-            shv[2] = b1;
-            shv[3] = excl + h0;
-            shv[4] = incl;
-        }
-    }
-    __syncthreads();
-    const int bK = shv[2], c_lt = shv[3], c_le = shv[4];
-    const bool exact = c_le > kCap;
-    uint64_t tau = 0;  // exact path: bucket-bK candidates need key >= tau
-    if (exact) {
-        int remaining = kp - c_lt;
-        uint64_t prefix = 0, mask = 0;
-        for (int pass = 0; pass < 8; ++pass) {
-            const int shift = 56 - 8 * pass;
-            for (int i = tid; i < 256; i += kSelThreads) xh[i] = 0;
-            __syncthreads();
-#pragma unroll
-            for (int e = 0; e < EPT; ++e) {
-                if (sz[e] > 0 && bucket_of(sc[e], gmax, inv) == bK) {
-                    const uint64_t key = cell_key(order_key(sc[e]), e * kSelThreads + tid);
-                    if ((key & mask) == prefix) atomicAdd(&xh[(key >> shift) & 255], 1);
-                }
-            }
-            __syncthreads();
-            if (tid < 64) {
-                int v[4], s = 0;
-                for (int u = 0; u < 4; ++u) {
-                    v[u] = xh[255 - 4 * tid - u];
-                    s += v[u];
-                }
-                const int incl = wave_incl_scan(s);
-                int run = incl - s;
-                for (int u = 0; u < 4; ++u) {
-                    if (run < remaining && run + v[u] >= remaining) {
-                        shv[5] = 255 - 4 * tid - u;
-                        shv[6] = run;
-                    }
-                    run += v[u];
-                }
-            }
-            __syncthreads();
-            remaining -= shv[6];
-            prefix |= static_cast<uint64_t>(shv[5]) << shift;
-            mask |= static_cast<uint64_t>(255) << shift;
-            __syncthreads();
-        }
-        tau = prefix;
-    }
-    for (int i = tid; i < kBins; i += kSelThreads) hist[i] = 0;   // fill cursors
-    __syncthreads();
-
-    // ---- candidates, grouped by bucket ----
+    for (int e = 0; e < EPT; ++e) st[e] = sz[e] > 0 ? 1 : 0;
     const int32_t* offs = a.off + static_cast<int64_t>(h) * (a.ncells + 1);
+    int c_sel = 0;
+    float lo = gmin, hi = gmax;
+    for (int level = 0; level < 16; ++level) {
+        const float range = hi - lo;
+        const float inv = range > 0.0f ? static_cast<float>(kBins) / range : 0.0f;
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-        if (sz[e] > 0) {
-            const int b = bucket_of(sc[e], gmax, inv);
-            const int g = e * kSelThreads + tid;
-            const uint64_t key = cell_key(order_key(sc[e]), g);
-            if (b < bK || (b == bK && (!exact || key >= tau))) {
-                const int slot = binbase[b] + atomicAdd(&hist[b], 1);
-                ck[slot] = key;
+        for (int e = 0; e < EPT; ++e)
+            if (st[e] == 1) atomicAdd(&hist[bucket_of(sc[e], hi, inv)], 1);
+        __syncthreads();
+        const int need = kp - c_sel;
+        {
+            const int b0 = 2 * tid, b1 = 2 * tid + 1;
+            const int h0 = hist[b0], h1 = hist[b1];
+            int total;
+            const int incl = block_incl_scan(h0 + h1, sh, total);
+            const int excl = incl - h0 - h1;
+            binbase[b0] = excl;
+            binbase[b1] = excl + h0;
+            if (tid == kSelThreads - 1) binbase[kBins] = incl;
+            if (excl < need && excl + h0 >= need) {
+                shv[2] = b0;
+                shv[3] = excl;
+                shv[4] = excl + h0;
+            } else if (excl + h0 < need && incl >= need) {
+                shv[2] = b1;
+                shv[3] = excl + h0;
+                shv[4] = incl;
+            }
+        }
+        for (int i = tid; i < kBins; i += kSelThreads) hist[i] = 0;   // fill cursors
+        __syncthreads();
+        const int bK = shv[2], c_lt = shv[3], c_le = shv[4];
+        const bool fits = c_sel + c_le <= kCap;
+        const bool flat = !(range > 0.0f);
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+            if (st[e] != 1) continue;
+            const int b = bucket_of(sc[e], hi, inv);
+            if (b < bK || (fits && b == bK)) {
+                const int g = e * kSelThreads + tid;
+                const int slot = c_sel + binbase[b] + atomicAdd(&hist[b], 1);
+                ck[slot] = cell_key(order_key(sc[e]), g);
                 cs[slot] = sz[e];
                 co[slot] = offs[g];
+                seg[slot] = (c_sel + binbase[b]) | ((binbase[b + 1] - binbase[b]) << 16);
+                st[e] = 2;
+            } else if (b > bK) {
+                st[e] = 0;
             }
         }
+        if (fits) {
+            c_sel += c_le;
+            break;
+        }
+        c_sel += c_lt;
+        __syncthreads();
+        for (int i = tid; i < kBins; i += kSelThreads) hist[i] = 0;
+        if (flat) {
+            // every cell still in play has the same score: the best are the
+            // lowest cell ids, i.e. the first `need` in cell-id order
+            const int keep = kp - c_sel;
+            int base = 0;
+#pragma unroll
+            for (int e = 0; e < EPT; ++e) {
+                const int f = st[e] == 1 ? 1 : 0;
+                int tot;
+                const int r = block_incl_scan(f, sh, tot) - f + base;
+                if (f && r < keep) {
+                    const int g = e * kSelThreads + tid;
+                    const int slot = c_sel + r;
+                    ck[slot] = cell_key(order_key(sc[e]), g);
+                    cs[slot] = sz[e];
+                    co[slot] = offs[g];
+                    seg[slot] = c_sel | (keep << 16);
+                }
+                base += tot;
+            }
+            c_sel += keep;
+            break;
+        }
+        // next level: range of the cells still in play
+        float mx = -INFINITY, mn = INFINITY;
+#pragma unroll
+        for (int e = 0; e < EPT; ++e)
+            if (st[e] == 1) {
+                mx = fmaxf(mx, sc[e]);
+                mn = fminf(mn, sc[e]);
+            }
+        mx = wave_max(mx);
+        mn = -wave_max(-mn);
+        if (lane_id() == 0) {
+            shf[tid >> 6] = mx;
+            shf[16 + (tid >> 6)] = mn;
+        }
+        __syncthreads();
+        hi = -INFINITY;
+        lo = INFINITY;
+        for (int w = 0; w < 16; ++w) {
+            hi = fmaxf(hi, shf[w]);
+            lo = fminf(lo, shf[16 + w]);
+        }
+        __syncthreads();
     }
     __syncthreads();
-    const int C = exact ? kp : c_le;
-    // rank inside the bucket by counting larger keys (buckets hold few cells)
-    for (int s = tid; s < C; s += kSelThreads) {
-        const uint64_t key = ck[s];
-        int lo = 0, hi2 = kBins;  // find bucket: last binbase <= s with non-empty segment
-        while (hi2 - lo > 1) {
-            const int mid = (lo + hi2) >> 1;
-            if (binbase[mid] <= s) lo = mid; else hi2 = mid;
-        }
-        const int seg_lo = binbase[lo];
-        const int seg_hi = (lo == bK && exact) ? binbase[lo] + (kp - c_lt) : binbase[lo + 1];
+    const int C = c_sel;
+    // rank inside each segment by counting larger keys (segments are short)
+    for (int sl = tid; sl < C; sl += kSelThreads) {
+        const uint64_t key = ck[sl];
+        const int sg0 = seg[sl] & 0xFFFF, sgn = seg[sl] >> 16;
         int r = 0;
-        for (int i = seg_lo; i < seg_hi; ++i) r += ck[i] > key;
-        const int pos = seg_lo + r;
+        for (int i = sg0; i < sg0 + sgn; ++i) r += ck[i] > key;
+        const int pos = sg0 + r;
         sg[pos] = cell_of_key(key);
-        ss[pos] = cs[s];
-        so[pos] = co[s];
+        ss[pos] = cs[sl];
+        so[pos] = co[sl];
     }
     __syncthreads();
 
@@ -452,13 +472,13 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
 template <int EPT>
 int launch_ept(const SelParams& p, int H, hipStream_t stream) {
     constexpr int DP = 64;
-    const size_t cand = static_cast<size_t>(kCap) * (sizeof(uint64_t) + 5 * sizeof(int));
+    const size_t cand = static_cast<size_t>(kCap) * (sizeof(uint64_t) + 6 * sizeof(int));
     const size_t ct = static_cast<size_t>(DP) * p.k[1] * sizeof(float);
     const size_t lds = cand > ct ? cand : ct;
     static bool attr_set = false;
     if (!attr_set) {
         IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&select_kernel<DP, EPT>),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
         attr_set = true;
     }
     hipLaunchKernelGGL((select_kernel<DP, EPT>), dim3(H), dim3(kSelThreads), lds, stream, p);

@@ -404,3 +404,34 @@ def test_full_size_properties_128k(ops):
     kd = keys.to(DEV)
     for h in range(H):
         assert torch.equal(out["list_keys"][h], kd[h][perm[h].long()])
+
+
+@pytest.mark.parametrize("case", ["outlier", "zero_query"])
+def test_select_refinement_paths(ops, oracle, case):
+    """Skewed scores (one subspace centroid blown up -> a few huge scores)
+    force the bucket refinement; a zero query makes every score equal, so
+    ranking falls back to cell ids alone."""
+    note(f"[select] {case}")
+    H, T, ks = 4, 12000, (32, 32)
+    keys, values = _kv(H, T, seed=17)
+    kd, vd = keys.to(DEV), values.to(DEV)
+    cent, labels, _ = ops.kmeans(kd, list(ks), 3)
+    if case == "outlier":
+        cent[:, 1, 0] *= 300.0
+    out = ops.build_index(kd, vd, cent, labels, list(ks), n_centroids=ks[0] * ks[1] + 1)
+    from adaptiveimi_amd import synthetic
+
+    q = synthetic.make_queries(keys, 4, seed=3)[0]
+    if case == "zero_query":
+        q.zero_()
+    for bud in (ops.Budget(102, 1200, 150), ops.Budget(400, 5000, 800)):
+        sel = ops.select(q.to(DEV), cent, out["cell_count"], out["cell_offset"], ks, bud)
+        sc = oracle.scores(bits(q), out["compact_centroids"].cpu().numpy())
+        rs, rm, rtok = oracle.select(sc, out["compact_size"].cpu().numpy(), out["compact_mask"].cpu().numpy(),
+                                     bud.nprobe, bud.max_tokens, bud.buffer_pages)
+        gids = out["compact_gid"].cpu().numpy()
+        m = sel["n_selected"].cpu().numpy()
+        assert np.array_equal(m, rm)
+        for h in range(H):
+            assert np.array_equal(sel["sel_cell"].cpu().numpy()[h, : m[h]], gids[h][rs[h, : rm[h]]]), h
+        assert np.array_equal(sel["n_rows"].cpu().numpy(), rtok)
