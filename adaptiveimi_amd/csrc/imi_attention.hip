@@ -169,7 +169,7 @@ __global__ __launch_bounds__(512) void attention_kernel(AttnParams a) {
                 const float corr = wexp(m_[g], mn);
                 float p[4];
 #pragma unroll
-                for (int it = 0; it < 4; ++it) p[it] = safe_exp2(s[it][g] - mn);
+                for (int it = 0; it < 4; ++it) p[it] = wexp(s[it][g], mn);   // 0 for rows past the end
                 l_[g] = l_[g] * corr + ((p[0] + p[1]) + (p[2] + p[3]));
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
