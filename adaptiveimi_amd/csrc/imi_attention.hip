@@ -5,29 +5,31 @@
 // rows = [static_len steady rows | miss pages | hit pages]) followed by the
 // unvendored weighted_flash_decoding (retrieval.py:439-447).  Here the rows
 // are read in place: the steady zone for the first static_len rows, then the
-// CSR list rows of the selected cells (row_loc table written by the
-// selection kernel) -- no execution buffer.
+// CSR list rows of the selected cells (each workgroup stages the head's
+// selection in LDS and binary-searches its rows) -- no execution buffer.
 //
-// Grid: H * nsplit workgroups of 4 waves, block b -> head b % H, split b / H,
+// Grid: H * nsplit workgroups of 8 waves, block b -> head b % H, split b / H,
 // so with 8 KV heads each head's splits run on one XCD (dispatch is round
-// robin over the 8 XCDs) and its partials stay in that XCD's L2.  Each wave
-// owns 32 consecutive rows; a row is read by 16 lanes x 16 bytes (fully
-// coalesced 1 KiB per wave instruction for 4 rows).  q.k uses v_dot2_f32_bf16
-// and a 16-lane DPP reduction; softmax is online in base 2 with fp32 state;
-// the 16 (wave, row-group) states merge in LDS into one partial per block.
-// The last block of each head (device-scope counter) merges the nsplit
-// partials in split order (deterministic) and writes bf16 output and LSE.
+// robin over the 8 XCDs).  Each wave owns 16 or 32 consecutive rows; a row is
+// read by 16 lanes x 16 bytes (fully coalesced 1 KiB per wave instruction for
+// 4 rows).  q.k uses v_dot2_f32_bf16 and a 16-lane DPP reduction; softmax is
+// online in base 2 with fp32 state; the 32 (wave, row-group) states of a
+// workgroup merge in LDS into one partial, written with plain stores.  A
+// second kernel merges each head's partials in split order (deterministic)
+// and writes the bf16 output and the LSE: the kernel boundary makes the
+// partials visible across XCDs without any device-scope fence.
 #include "imi_common.hpp"
 
 namespace imi {
 
-int select_launch(const imi_select_args* a, int32_t* row_loc, int max_rows, hipStream_t stream);
+int select_launch(const imi_select_args* a, hipStream_t stream);
 int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax);
 
 namespace {
 
 constexpr int kWaves = 8;            // waves per workgroup (512 threads)
-constexpr int kMaxSplitG = 8192;     // splits * groups the final merge can index
+constexpr int kMaxSplit = 1024;      // splits per head the merge kernel handles
+constexpr int kSelCapMax = 2048;     // selected cells per head the gather indexes
 
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 
@@ -40,15 +42,16 @@ struct AttnParams {
     const uint16_t* lk;
     const uint16_t* lv;
     int64_t list_rows;
-    const int32_t* row_loc;  // [H][max_rows]
-    int max_rows;
-    const int32_t* n_rows;   // [H]
+    const int32_t* sel_offset;  // [H][sel_cap]
+    const int32_t* sel_prefix;  // [H][sel_cap + 1]
+    const int32_t* n_selected;  // [H]
+    int sel_cap;
+    const int32_t* n_rows;      // [H]
     int H, nsplit;
     int rows_per_block;
     float scale_log2;        // scale * log2(e)
     float* part_acc;         // [H][nsplit][G][128]
     float* part_ml;          // [H][nsplit][G][2]
-    int32_t* counter;        // [H]
     uint16_t* out;           // [H*G][128]
     float* lse;              // [H*G] or null
 };
@@ -69,55 +72,63 @@ __device__ __forceinline__ float bf16_at(const uint4& v, int u) {
 
 __device__ __forceinline__ float safe_exp2(float x) { return x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(x); }
 
-// Agent-scope relaxed atomic store / load: encoded with the coherence bit, so
-// other XCDs see the value without an L2 write-back / invalidate.
-__device__ __forceinline__ void coherent_store(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float coherent_load(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// s_waitcnt vmcnt(0): this thread's stores have been acknowledged.
-__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
 // Weight exp2(m - M) of a state with running max m inside a merge whose max
 // is M; an empty state (m = -inf) weighs 0 even when M is -inf too.
 __device__ __forceinline__ float wexp(float m, float M) { return m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M); }
 
 // One workgroup = 8 waves over rows [split * rows_per_block, +rows_per_block)
 // of head h; each wave owns TILES * 16 consecutive rows, read as tiles of 4
-// rows x 4 iterations (16 lanes x 16 bytes per row).
+// rows x 4 iterations (16 lanes x 16 bytes per row).  The workgroup writes
+// one partial (max, sum, unnormalised output) with plain stores; merge_kernel
+// combines the partials after the kernel boundary.
 template <int G, int TILES>
-__global__ __launch_bounds__(512) void attention_kernel(AttnParams a) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnParams a) {
     constexpr int RW = TILES * 16;
     __shared__ float s_acc[kWaves][G][128];
     __shared__ float s_ml[kWaves][G][2];
-    __shared__ float s_w[kMaxSplitG];
-    __shared__ float s_ML[G][2];
-    __shared__ float s_red[4][G * 128];
-    __shared__ int s_last;
+    __shared__ int s_pre[kSelCapMax + 1];
+    __shared__ int s_off[kSelCapMax];
 
     const int b = blockIdx.x;
     const int h = b % a.H;
     const int split = b / a.H;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int rg = lane >> 4, li = lane & 15;
-    const int N = a.static_len + a.n_rows[h];
     const int row0 = split * a.rows_per_block + wave * RW;
 
-    // q and the row locations of this wave, loaded together up front
+    // One round trip for everything the gather needs: q, the row and cell
+    // counts, and the head's selection (CSR offset and row prefix per cell).
     uint32_t qp[G][4];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const uint4 v = *reinterpret_cast<const uint4*>(a.q + (static_cast<int64_t>(h) * G + g) * 128 + li * 8);
         qp[g][0] = v.x; qp[g][1] = v.y; qp[g][2] = v.z; qp[g][3] = v.w;
     }
+    const int nrows = a.n_rows[h];
+    const int m = a.n_selected[h];
+    {
+        const int32_t* pre = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
+        const int32_t* off = a.sel_offset + static_cast<int64_t>(h) * a.sel_cap;
+        for (int i = tid; i <= a.sel_cap; i += 64 * kWaves) {
+            s_pre[i] = pre[i];
+            if (i < a.sel_cap) s_off[i] = off[i];
+        }
+    }
+    __syncthreads();
+    // row location of lane < RW: cell r with pre[r] <= j < pre[r + 1]
     int myloc = 0;
     {
-        const int n = row0 + lane;
-        if (lane < RW && n < N && n >= a.static_len)
-            myloc = a.row_loc[static_cast<int64_t>(h) * a.max_rows + (n - a.static_len)];
+        const int j = row0 + lane - a.static_len;
+        if (lane < RW && j >= 0 && j < nrows) {
+            int lo = 0, hi = m;
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (s_pre[mid] <= j) lo = mid; else hi = mid;
+            }
+            myloc = s_off[lo] + (j - s_pre[lo]);
+        }
     }
+    const int N = a.static_len + nrows;
     float m_[G], l_[G], acc[G][8];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -183,18 +194,19 @@ __global__ __launch_bounds__(512) void attention_kernel(AttnParams a) {
         }
     }
     // merge the four row groups of the wave (lanes li, li+16, li+32, li+48)
+    // with the permlane swaps: first across rows 0<->1, 2<->3, then halves
 #pragma unroll
-    for (int o = 16; o <= 32; o <<= 1) {
+    for (int step = 0; step < 2; ++step) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const float mo = __shfl_xor(m_[g], o);
-            const float lo = __shfl_xor(l_[g], o);
+            const float mo = step == 0 ? xor16(m_[g]) : xor32(m_[g]);
+            const float lo = step == 0 ? xor16(l_[g]) : xor32(l_[g]);
             const float mn = fmaxf(m_[g], mo);
             const float wa = wexp(m_[g], mn), wb = wexp(mo, mn);
             l_[g] = l_[g] * wa + lo * wb;
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const float ao = __shfl_xor(acc[g][u], o);
+                const float ao = step == 0 ? xor16(acc[g][u]) : xor32(acc[g][u]);
                 acc[g][u] = acc[g][u] * wa + ao * wb;
             }
             m_[g] = mn;
@@ -212,8 +224,7 @@ __global__ __launch_bounds__(512) void attention_kernel(AttnParams a) {
         }
     }
     __syncthreads();
-    // block partial (waves merged in order), published with agent-coherent
-    // stores (write-through past the XCD's L2) instead of a device fence
+    // block partial (waves merged in order)
     const int64_t pbase = static_cast<int64_t>(h) * a.nsplit + split;
     for (int o = tid; o < G * 128; o += 64 * kWaves) {
         const int g = o >> 7, d = o & 127;
@@ -227,76 +238,82 @@ __global__ __launch_bounds__(512) void attention_kernel(AttnParams a) {
             L += s_ml[w][g][1] * wt;
             A += s_acc[w][g][d] * wt;
         }
-        coherent_store(a.part_acc + (pbase * G + g) * 128 + d, A);
+        a.part_acc[(pbase * G + g) * 128 + d] = A;
         if (d == 0) {
-            coherent_store(a.part_ml + (pbase * G + g) * 2 + 0, M);
-            coherent_store(a.part_ml + (pbase * G + g) * 2 + 1, L);
+            a.part_ml[(pbase * G + g) * 2 + 0] = M;
+            a.part_ml[(pbase * G + g) * 2 + 1] = L;
         }
     }
-    wait_stores();
-    __syncthreads();
-    if (tid == 0) s_last = atomicAdd(&a.counter[h], 1) == a.nsplit - 1;
-    __syncthreads();
-    if (!s_last) return;
+}
 
-    // ---- final merge of head h's nsplit partials (deterministic order) ----
-    const float* pml = a.part_ml + static_cast<int64_t>(h) * a.nsplit * G * 2;
-    for (int i = tid; i < a.nsplit * G; i += 64 * kWaves) s_w[i] = coherent_load(pml + 2 * i);
-    __syncthreads();
-    if (wave < G) {
-        const int g = wave;
+// Merge of the nsplit partials of one head for 64 outputs (query head
+// g = chunk / 2, dims (chunk % 2) * 64 ..).  Each of the four waves sums a
+// quarter of the splits (s = q, q + 4, ...); its first 16 loads are issued
+// before wave 0 has derived the split weights, so the common case needs one
+// round trip.  Quarters are added in a fixed order (deterministic).
+__global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
+    __shared__ float s_w[kMaxSplit];
+    __shared__ float s_red[4][64];
+    __shared__ float s_ML[2];
+    const int h = blockIdx.y, chunk = blockIdx.x;
+    const int g = chunk >> 1;
+    const int tid = threadIdx.x, q = tid >> 6, lane = tid & 63;
+    const int o = chunk * 64 + lane;  // g * 128 + d
+    const int ns = a.nsplit;
+    const int64_t stride = static_cast<int64_t>(G) * 128;
+    const float* pacc = a.part_acc + static_cast<int64_t>(h) * ns * stride + o;
+    const float* pml = a.part_ml + (static_cast<int64_t>(h) * ns * G + g) * 2;
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int s = q + 4 * u;
+        v[u] = s < ns ? pacc[s * stride] : 0.0f;
+    }
+    if (q == 0) {
         float M = -INFINITY;
-        for (int s = lane; s < a.nsplit; s += 64) M = fmaxf(M, s_w[s * G + g]);
+        for (int s = lane; s < ns; s += 64) M = fmaxf(M, pml[static_cast<int64_t>(s) * G * 2]);
         M = wave_max(M);
         float L = 0.0f;
-        for (int s = lane; s < a.nsplit; s += 64) L += coherent_load(pml + (s * G + g) * 2 + 1) * wexp(s_w[s * G + g], M);
+        for (int s = lane; s < ns; s += 64) {
+            const float w = wexp(pml[static_cast<int64_t>(s) * G * 2], M);
+            s_w[s] = w;
+            L += pml[static_cast<int64_t>(s) * G * 2 + 1] * w;
+        }
         L = wave_sum(L);
         if (lane == 0) {
-            s_ML[g][0] = M;
-            s_ML[g][1] = L;
+            s_ML[0] = M;
+            s_ML[1] = L;
         }
     }
     __syncthreads();
-    for (int i = tid; i < a.nsplit * G; i += 64 * kWaves) s_w[i] = wexp(s_w[i], s_ML[i % G][0]);
-    __syncthreads();
-    // thread -> 4 consecutive outputs x one quarter of the splits; loads of
-    // 4 splits are issued together
-    const float* pacc = a.part_acc + static_cast<int64_t>(h) * a.nsplit * G * 128;
-    const int o4 = (tid & 127) * 4;  // output index (g * 128 + d), 4 at a time
-    const int quarter = tid >> 7;    // 0..3
-    for (int o = o4; o < G * 128; o += 512) {
-        const int g = o >> 7;
-        float A[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int s0 = quarter; s0 < a.nsplit; s0 += 16) {
-            float v[4][4], w[4];
+    float acc = 0.0f;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int s = s0 + 4 * u;
-                const bool in = s < a.nsplit;
-                w[u] = in ? s_w[s * G + g] : 0.0f;
+    for (int u = 0; u < 16; ++u) {
+        const int s = q + 4 * u;
+        if (s < ns) acc = __builtin_fmaf(v[u], s_w[s], acc);
+    }
+    for (int s0 = q + 64; s0 < ns; s0 += 64) {
 #pragma unroll
-                for (int x = 0; x < 4; ++x)
-                    v[u][x] = in ? coherent_load(pacc + static_cast<int64_t>(s) * G * 128 + o + x) : 0.0f;
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-#pragma unroll
-                for (int x = 0; x < 4; ++x) A[x] = __builtin_fmaf(v[u][x], w[u], A[x]);
+        for (int u = 0; u < 16; ++u) {
+            const int s = s0 + 4 * u;
+            v[u] = s < ns ? pacc[s * stride] : 0.0f;
         }
 #pragma unroll
-        for (int x = 0; x < 4; ++x) s_red[quarter][o + x] = A[x];
+        for (int u = 0; u < 16; ++u) {
+            const int s = s0 + 4 * u;
+            if (s < ns) acc = __builtin_fmaf(v[u], s_w[s], acc);
+        }
     }
+    s_red[q][lane] = acc;
     __syncthreads();
-    for (int o = tid; o < G * 128; o += 64 * kWaves) {
-        const int g = o >> 7;
-        const float A = ((s_red[0][o] + s_red[1][o]) + s_red[2][o]) + s_red[3][o];
-        const float L = s_ML[g][1];
+    if (q == 0) {
+        const float A = ((s_red[0][lane] + s_red[1][lane]) + s_red[2][lane]) + s_red[3][lane];
+        const float L = s_ML[1];
         a.out[static_cast<int64_t>(h) * G * 128 + o] = f32_to_bf16(L > 0.0f ? A / L : 0.0f);
-        if (a.lse && (o & 127) == 0)
+        if (a.lse && lane == 0 && (chunk & 1) == 0)
             a.lse[static_cast<int64_t>(h) * G + g] =
-                L > 0.0f ? (s_ML[g][0] + log2f(L)) * 0.69314718055994530942f : -INFINITY;
+                L > 0.0f ? (s_ML[0] + log2f(L)) * 0.69314718055994530942f : -INFINITY;
     }
-    if (tid == 0) a.counter[h] = 0;
 }
 
 // Rows per wave: two tiles when the head has enough rows to give every CU
@@ -325,11 +342,9 @@ size_t attn_workspace(const imi_attention_args* a, AttnParams* p) {
     Carver cv(a->workspace);
     float* acc = cv.take<float>(static_cast<size_t>(a->kv_heads) * nsplit * a->groups * 128);
     float* ml = cv.take<float>(static_cast<size_t>(a->kv_heads) * nsplit * a->groups * 2);
-    int32_t* cnt = cv.take<int32_t>(a->kv_heads);
     if (p) {
         p->part_acc = acc;
         p->part_ml = ml;
-        p->counter = cnt;
         p->nsplit = nsplit_for(a);
         const int rows = a->static_len + a->max_rows;
         p->rows_per_block = kWaves * 16 * tiles_for(rows, a->kv_heads);
@@ -353,9 +368,11 @@ int attn_validate(const imi_attention_args* a, bool need_sel) {
     IMI_REQUIRE(a->max_rows >= 0, IMI_ERR_INVALID, "imi_sparse_attention: max_rows must be >= 0");
     if (need_sel)
         IMI_REQUIRE(a->n_rows != nullptr, IMI_ERR_INVALID, "imi_sparse_attention: null n_rows");
-    IMI_REQUIRE(nsplit_bound(a) * a->groups <= kMaxSplitG, IMI_ERR_UNSUPPORTED,
-                "imi_sparse_attention: %d rows x %d groups exceed the split table", a->static_len + a->max_rows,
-                a->groups);
+    IMI_REQUIRE(a->sel_cap >= 0 && a->sel_cap <= kSelCapMax, IMI_ERR_UNSUPPORTED,
+                "imi_sparse_attention: sel_cap %d exceeds %d", a->sel_cap, kSelCapMax);
+    IMI_REQUIRE(nsplit_bound(a) <= kMaxSplit, IMI_ERR_UNSUPPORTED,
+                "imi_sparse_attention: %d rows need more than %d splits per head", a->static_len + a->max_rows,
+                kMaxSplit);
     return IMI_OK;
 }
 
@@ -367,7 +384,7 @@ void launch_g(const AttnParams& p, int blocks, hipStream_t stream) {
         hipLaunchKernelGGL((attention_kernel<G, 1>), dim3(blocks), dim3(64 * kWaves), 0, stream, p);
 }
 
-int attn_launch(const imi_attention_args* a, const int32_t* row_loc, hipStream_t stream) {
+int attn_launch(const imi_attention_args* a, hipStream_t stream) {
     AttnParams p;
     attn_workspace(a, &p);
     p.q = a->query;
@@ -378,8 +395,10 @@ int attn_launch(const imi_attention_args* a, const int32_t* row_loc, hipStream_t
     p.lk = a->list_keys;
     p.lv = a->list_values;
     p.list_rows = a->list_rows;
-    p.row_loc = row_loc;
-    p.max_rows = a->max_rows;
+    p.sel_offset = a->sel_offset;
+    p.sel_prefix = a->sel_prefix;
+    p.n_selected = a->n_selected;
+    p.sel_cap = a->sel_cap;
     p.n_rows = a->n_rows;
     p.H = a->kv_heads;
     p.scale_log2 = a->scale * 1.44269504088896340736f;
@@ -394,34 +413,15 @@ int attn_launch(const imi_attention_args* a, const int32_t* row_loc, hipStream_t
         default: launch_g<8>(p, blocks, stream); break;
     }
     IMI_LAUNCH_CHECK("attention_kernel");
+    hipLaunchKernelGGL(merge_kernel, dim3(2 * a->groups, a->kv_heads), dim3(256), 0, stream, p, a->groups);
+    IMI_LAUNCH_CHECK("merge_kernel");
     return IMI_OK;
-}
-
-// Row-location table for a caller-supplied selection (imi_sparse_attention
-// without imi_decode_step): one wave per selected cell.
-__global__ __launch_bounds__(256) void expand_rows_kernel(const int32_t* sel_offset, const int32_t* sel_count,
-                                                          const int32_t* sel_prefix, const int32_t* n_selected,
-                                                          int sel_cap, int32_t* row_loc, int max_rows) {
-    const int h = blockIdx.y;
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (r >= n_selected[h]) return;
-    const int o = sel_offset[static_cast<int64_t>(h) * sel_cap + r];
-    const int c = sel_count[static_cast<int64_t>(h) * sel_cap + r];
-    const int base = sel_prefix[static_cast<int64_t>(h) * (sel_cap + 1) + r];
-    for (int i = lane_id(); i < c; i += 64)
-        if (base + i < max_rows) row_loc[static_cast<int64_t>(h) * max_rows + base + i] = o + i;
 }
 
 }  // namespace
 }  // namespace imi
 
 using namespace imi;
-
-namespace {
-size_t rowloc_bytes(const imi_attention_args* a) {
-    return align_up(static_cast<size_t>(a->kv_heads) * (a->max_rows > 0 ? a->max_rows : 1) * sizeof(int32_t), 256);
-}
-}  // namespace
 
 extern "C" int imi_attention_workspace_size(const imi_attention_args* a, size_t* bytes) {
     clear_error();
@@ -430,7 +430,7 @@ extern "C" int imi_attention_workspace_size(const imi_attention_args* a, size_t*
     IMI_REQUIRE(bytes != nullptr, IMI_ERR_INVALID, "imi_attention_workspace_size: null output");
     imi_attention_args t = *a;
     t.workspace = nullptr;
-    *bytes = rowloc_bytes(a) + attn_workspace(&t, nullptr);
+    *bytes = attn_workspace(&t, nullptr);
     return IMI_OK;
 }
 
@@ -439,28 +439,19 @@ extern "C" int imi_sparse_attention(const imi_attention_args* a, imi_stream_t st
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
     int rc = attn_validate(a, true);
     if (rc) return rc;
-    IMI_REQUIRE(a->sel_offset && a->sel_count && a->sel_prefix && a->n_selected, IMI_ERR_INVALID,
+    IMI_REQUIRE(a->sel_offset && a->sel_prefix && a->n_selected, IMI_ERR_INVALID,
                 "imi_sparse_attention: null selection arrays");
     size_t need;
     rc = imi_attention_workspace_size(a, &need);
     if (rc) return rc;
     IMI_REQUIRE(a->workspace && a->workspace_bytes >= need, IMI_ERR_WORKSPACE,
                 "imi_sparse_attention: workspace %zu bytes < %zu required", a->workspace_bytes, need);
-    int32_t* row_loc = static_cast<int32_t*>(a->workspace);
-    imi_attention_args t = *a;
-    t.workspace = static_cast<char*>(a->workspace) + rowloc_bytes(a);
-    if (a->sel_cap > 0) {
-        hipLaunchKernelGGL(expand_rows_kernel, dim3((a->sel_cap + 3) / 4, a->kv_heads), dim3(256), 0, stream,
-                           a->sel_offset, a->sel_count, a->sel_prefix, a->n_selected, a->sel_cap, row_loc,
-                           a->max_rows);
-        IMI_LAUNCH_CHECK("expand_rows_kernel");
-    }
-    return attn_launch(&t, row_loc, stream);
+    return attn_launch(a, stream);
 }
 
 namespace {
 struct DecodeLayout {
-    int32_t *cell, *off, *cnt, *prefix, *nsel, *nrows, *row_loc;
+    int32_t *cell, *off, *cnt, *prefix, *nsel, *nrows;
     char* attn_ws;
     size_t attn_bytes;
     size_t total;
@@ -476,7 +467,6 @@ DecodeLayout decode_layout(const imi_decode_args* a, void* ws) {
     L.prefix = cv.take<int32_t>(static_cast<size_t>(H) * (cap + 1));
     L.nsel = cv.take<int32_t>(H);
     L.nrows = cv.take<int32_t>(H);
-    L.row_loc = cv.take<int32_t>(static_cast<size_t>(H) * (a->attn.max_rows > 0 ? a->attn.max_rows : 1));
     imi_attention_args t = a->attn;
     t.workspace = nullptr;
     L.attn_bytes = attn_workspace(&t, nullptr);
@@ -523,7 +513,7 @@ extern "C" int imi_decode_step(const imi_decode_args* a, imi_stream_t stream_) {
     if (!s.n_selected) s.n_selected = L.nsel;
     if (!s.n_rows) s.n_rows = L.nrows;
     if (phases & 1) {
-        rc = select_launch(&s, L.row_loc, a->attn.max_rows, stream);
+        rc = select_launch(&s, stream);
         if (rc) return rc;
     } else {
         int64_t nc;
@@ -541,5 +531,5 @@ extern "C" int imi_decode_step(const imi_decode_args* a, imi_stream_t stream_) {
     t.sel_cap = s.sel_cap;
     t.workspace = L.attn_ws;
     t.workspace_bytes = L.attn_bytes;
-    return attn_launch(&t, L.row_loc, stream);
+    return attn_launch(&t, stream);
 }

@@ -9,7 +9,7 @@
 #include <cstring>
 #include <string>
 
-#include "../../include/imi_hip.h"
+#include "imi_hip.h"
 
 namespace imi {
 
@@ -118,28 +118,59 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+// Lane exchanges across the halves / rows of the wave with the gfx950
+// permlane swaps (VALU, no LDS crossbar): value of lane ^ 32 and lane ^ 16.
+__device__ __forceinline__ float xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(lane_id() < 32 ? r[1] : r[0]);
+}
+__device__ __forceinline__ float xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(((lane_id() >> 4) & 1) == 0 ? r[1] : r[0]);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+// DPP controls used below: row_shr:n = 0x110 + n, row_bcast:15 = 0x142,
+// row_bcast:31 = 0x143.  update_dpp(0, v, ...) returns 0 in lanes whose
+// source is outside the row (or whose row is masked off).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, false);
+}
+
+// Inclusive prefix sum across the 64 lanes (row scans, then row carries).
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += dpp_i<0x111>(v);
+    v += dpp_i<0x112>(v);
+    v += dpp_i<0x114>(v);
+    v += dpp_i<0x118>(v);
+    v += dpp_i<0x142, 0xA>(v);
+    v += dpp_i<0x143, 0xC>(v);
     return v;
 }
 
 __device__ __forceinline__ int wave_sum_i(int v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return __builtin_amdgcn_readlane(wave_incl_scan(v), 63);
+}
+
+// Butterfly reductions (every lane gets the result; fixed order, so the
+// result is the same on every call).
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    v += xor16(v);
+    v += xor32(v);
     return v;
 }
 
-// Inclusive prefix sum across the 64 lanes of a wave.
-__device__ __forceinline__ int wave_incl_scan(int v) {
-    const int l = lane_id();
-    for (int o = 1; o < 64; o <<= 1) {
-        int t = __shfl_up(v, o);
-        if (l >= o) v += t;
-    }
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    v = fmaxf(v, xor16(v));
+    v = fmaxf(v, xor32(v));
     return v;
 }
 

@@ -48,8 +48,6 @@ struct SelParams {
     int32_t* n_sel;
     int32_t* n_rows;
     int sel_cap;
-    int32_t* row_loc;  // [H][max_rows] or null
-    int max_rows;
 };
 
 // Block-wide inclusive scan of one int per thread (1024 threads).
@@ -110,12 +108,21 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     int* seg = so + kCap;                                // [kCap] segment (start | len << 16)
 
     // ---- loads, all issued before the first wait ----
+    // Cell (i, j), g = i * k1 + j, lives in thread t = r * k1 + j with
+    // i = r + R * e (R = 1024 / k1 rows of cells in flight): lanes run over j,
+    // so one LDS read of C1[j][d] feeds EPT fused multiply-adds.
+    const int R = kSelThreads / k1;
+    const int jcell = tid % k1, rcell = tid / k1;
     const int32_t* cntp = a.cnt + static_cast<int64_t>(h) * a.ncells;
-    int sz[EPT];
+    const int32_t* offs = a.off + static_cast<int64_t>(h) * (a.ncells + 1);
+    int sz[EPT], co_[EPT];
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-        const int g = e * kSelThreads + tid;
-        sz[e] = g < a.ncells ? cntp[g] : 0;
+        const int i = rcell + R * e;
+        const bool in = rcell < R && i < k0;
+        const int g = i * k1 + jcell;
+        sz[e] = in ? cntp[g] : 0;
+        co_[e] = in ? offs[g] : 0;
     }
     const float* c0 = a.cent + (static_cast<int64_t>(h) * a.P + 0) * a.kmax * DP;
     const float* c1 = a.cent + (static_cast<int64_t>(h) * a.P + 1) * a.kmax * DP;
@@ -129,8 +136,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         }
     }
     for (int i = tid; i < k1 * DP; i += kSelThreads) {
-        const int j = i / DP, d = i - (i / DP) * DP;
-        c1T[d * k1 + j] = c1[i];
+        const int d = i / k1, j = i - (i / k1) * k1;   // consecutive lanes -> consecutive LDS words
+        c1T[i] = c1[static_cast<int64_t>(j) * DP + d];
     }
     if (tid < a.D) {
         float acc = 0.0f;   // grouped-query sum, g ascending (compute_impl.cu:80-87)
@@ -151,20 +158,19 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
 
     // ---- scores: the chain continues over the second subspace ----
     float sc[EPT];
-    int jj[EPT];
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-        const int g = e * kSelThreads + tid;
-        const int gi = g < a.ncells ? g : 0;
-        const int i = gi / k1;
-        jj[e] = gi - i * k1;
-        sc[e] = p1[i];
+        const int i = rcell + R * e;
+        sc[e] = p1[i < k0 ? i : 0];
     }
+    if (rcell < R) {
 #pragma unroll
-    for (int d = 0; d < DP; ++d) {
-        const float qd = qs[DP + d];
+        for (int d = 0; d < DP; ++d) {
+            const float qd = qs[DP + d];
+            const float cv = c1T[d * k1 + jcell];
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) sc[e] = __builtin_fmaf(qd, c1T[d * k1 + jj[e]], sc[e]);
+            for (int e = 0; e < EPT; ++e) sc[e] = __builtin_fmaf(qd, cv, sc[e]);
+        }
     }
     int nvalid = 0;
     float smax = -INFINITY, smin = INFINITY;
@@ -224,7 +230,6 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     int st[EPT];
 #pragma unroll
     for (int e = 0; e < EPT; ++e) st[e] = sz[e] > 0 ? 1 : 0;
-    const int32_t* offs = a.off + static_cast<int64_t>(h) * (a.ncells + 1);
     int c_sel = 0;
     float lo = gmin, hi = gmax;
     for (int level = 0; level < 16; ++level) {
@@ -264,11 +269,11 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
             if (st[e] != 1) continue;
             const int b = bucket_of(sc[e], hi, inv);
             if (b < bK || (fits && b == bK)) {
-                const int g = e * kSelThreads + tid;
+                const int g = (rcell + R * e) * k1 + jcell;
                 const int slot = c_sel + binbase[b] + atomicAdd(&hist[b], 1);
                 ck[slot] = cell_key(order_key(sc[e]), g);
                 cs[slot] = sz[e];
-                co[slot] = offs[g];
+                co[slot] = co_[e];
                 seg[slot] = (c_sel + binbase[b]) | ((binbase[b + 1] - binbase[b]) << 16);
                 st[e] = 2;
             } else if (b > bK) {
@@ -293,11 +298,11 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
                 int tot;
                 const int r = block_incl_scan(f, sh, tot) - f + base;
                 if (f && r < keep) {
-                    const int g = e * kSelThreads + tid;
+                    const int g = (rcell + R * e) * k1 + jcell;
                     const int slot = c_sel + r;
                     ck[slot] = cell_key(order_key(sc[e]), g);
                     cs[slot] = sz[e];
-                    co[slot] = offs[g];
+                    co[slot] = co_[e];
                     seg[slot] = c_sel | (keep << 16);
                 }
                 base += tot;
@@ -374,7 +379,6 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     int32_t* out_cell = a.sel_cell + static_cast<int64_t>(h) * a.sel_cap;
     int32_t* out_off = a.sel_offset + static_cast<int64_t>(h) * a.sel_cap;
     int32_t* out_cnt = a.sel_count + static_cast<int64_t>(h) * a.sel_cap;
-    int* sp = cs;  // exclusive row prefix in rank order (cs is free now)
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int r = 2 * tid + u;
@@ -383,42 +387,18 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
             out_off[r] = so[r];
             out_cnt[r] = s2[u];
             prefix_out[r] = excl_tok[u];
-            sp[r] = excl_tok[u];
         }
         if (r == m - 1) {
             const int total = excl_tok[u] + s2[u];
             prefix_out[m] = total;
-            sp[m] = total;
             a.n_sel[h] = m;
             a.n_rows[h] = total;
-            shv[7] = total;
         }
     }
     if (m == 0 && tid == 0) {
         a.n_sel[h] = 0;
         a.n_rows[h] = 0;
         prefix_out[0] = 0;
-        shv[7] = 0;
-    }
-    if (a.row_loc == nullptr) return;
-    __syncthreads();
-    // ---- row-location table: thread t expands a contiguous run of rows ----
-    const int total = shv[7];
-    const int per = (total + kSelThreads - 1) / kSelThreads;
-    const int j0 = tid * per;
-    if (j0 < total) {
-        int lo = 0, hi2 = m;  // last r with sp[r] <= j0
-        while (hi2 - lo > 1) {
-            const int mid = (lo + hi2) >> 1;
-            if (sp[mid] <= j0) lo = mid; else hi2 = mid;
-        }
-        int r = lo;
-        int32_t* rl = a.row_loc + static_cast<int64_t>(h) * a.max_rows;
-        const int j1 = j0 + per < total ? j0 + per : total;
-        for (int j = j0; j < j1; ++j) {
-            while (j >= sp[r + 1]) ++r;
-            rl[j] = so[r] + (j - sp[r]);
-        }
     }
 }
 
@@ -459,8 +439,8 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     kmax = a->k[0] > a->k[1] ? a->k[0] : a->k[1];
     IMI_REQUIRE(a->k[0] >= 1 && a->k[1] >= 1 && kmax <= 256, IMI_ERR_UNSUPPORTED, "imi_select: k outside [1,256]");
     ncells = static_cast<int64_t>(a->k[0]) * a->k[1];
-    IMI_REQUIRE(ncells <= 16 * kSelThreads, IMI_ERR_UNSUPPORTED, "imi_select: %lld cells exceed %d",
-                static_cast<long long>(ncells), 16 * kSelThreads);
+    IMI_REQUIRE(a->k[1] <= 128 && a->k[0] <= 16 * (kSelThreads / a->k[1]), IMI_ERR_UNSUPPORTED,
+                "imi_select: k = (%d, %d) exceeds the cells one workgroup holds", a->k[0], a->k[1]);
     const int kprime = a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages;
     IMI_REQUIRE(kprime <= kCap, IMI_ERR_UNSUPPORTED, "imi_select: min(nprobe, buffer_pages)=%d exceeds %d", kprime,
                 kCap);
@@ -486,7 +466,7 @@ int launch_ept(const SelParams& p, int H, hipStream_t stream) {
     return IMI_OK;
 }
 
-int select_launch(const imi_select_args* a, int32_t* row_loc, int max_rows, hipStream_t stream) {
+int select_launch(const imi_select_args* a, hipStream_t stream) {
     int64_t ncells;
     int kmax;
     int rc = select_validate(a, ncells, kmax);
@@ -516,9 +496,8 @@ int select_launch(const imi_select_args* a, int32_t* row_loc, int max_rows, hipS
     p.n_sel = a->n_selected;
     p.n_rows = a->n_rows;
     p.sel_cap = a->sel_cap;
-    p.row_loc = row_loc;
-    p.max_rows = max_rows;
-    const int ept = static_cast<int>((ncells + kSelThreads - 1) / kSelThreads);
+    const int rows_in_flight = kSelThreads / a->k[1];
+    const int ept = (a->k[0] + rows_in_flight - 1) / rows_in_flight;
     if (ept <= 1) return launch_ept<1>(p, a->kv_heads, stream);
     if (ept <= 2) return launch_ept<2>(p, a->kv_heads, stream);
     if (ept <= 4) return launch_ept<4>(p, a->kv_heads, stream);
@@ -532,7 +511,7 @@ using namespace imi;
 
 extern "C" int imi_select(const imi_select_args* a, imi_stream_t stream) {
     clear_error();
-    return select_launch(a, nullptr, 0, reinterpret_cast<hipStream_t>(stream));
+    return select_launch(a, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int imi_fused_query_group_similarities(const uint16_t* query, const float* centroids, float* out,
