@@ -8,16 +8,26 @@
 // CSR list rows of the selected cells (each workgroup stages the head's
 // selection in LDS and binary-searches its rows) -- no execution buffer.
 //
-// Grid: H * nsplit workgroups of 8 waves, block b -> head b % H, split b / H,
-// so with 8 KV heads each head's splits run on one XCD (dispatch is round
-// robin over the 8 XCDs).  Each wave owns 16 or 32 consecutive rows; a row is
-// read by 16 lanes x 16 bytes (fully coalesced 1 KiB per wave instruction for
-// 4 rows).  q.k uses v_dot2_f32_bf16 and a 16-lane DPP reduction; softmax is
-// online in base 2 with fp32 state; the 32 (wave, row-group) states of a
-// workgroup merge in LDS into one partial, written with plain stores.  A
-// second kernel merges each head's partials in split order (deterministic)
-// and writes the bf16 output and the LSE: the kernel boundary makes the
-// partials visible across XCDs without any device-scope fence.
+// Grid: H * nsplit workgroups of 4 waves; workgroup b takes split b / H of
+// head (b + b / H) % H, so consecutive workgroups (which the dispatcher deals
+// round robin to the 8 XCDs) rotate over the heads and every XCD gets a
+// share of every head's rows.  A wave owns NT tiles of 16 consecutive rows
+// and keeps two tiles in flight ahead of the one it computes.
+//
+// Per tile, on the matrix cores:
+//   S = K Q^T   4 x v_mfma_f32_16x16x32_bf16: A = the K tile (lane -> token
+//               lane % 16, 8 dims per lane), B = Q with column n holding
+//               query n % G; lane l gets S[token 4(l/16)+i][query (l%16)%G].
+//   O += P V    8 x v_mfma_f32_16x16x16_bf16: A = P, which is exactly the S
+//               layout above (row = query slot, k = token) after exp2 and a
+//               bf16 pack; B = V^T, read from a per-wave LDS copy of the V
+//               tile with ds_read_b64_tr_b16 (4 tokens x 1 dim per lane).
+// Softmax is online in base 2 with fp32 state per query slot; the rescale
+// of O is skipped when no running max moved.  The waves of a workgroup merge
+// in LDS into one partial (plain stores); a second kernel merges each
+// head's partials in split order (deterministic) and writes the bf16 output
+// and the LSE: the kernel boundary makes the partials visible across XCDs
+// without any device-scope fence.
 #include "imi_common.hpp"
 
 namespace imi {
@@ -27,11 +37,17 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax);
 
 namespace {
 
-constexpr int kWaves = 8;            // waves per workgroup (512 threads)
-constexpr int kMaxSplit = 1024;      // splits per head the merge kernel handles
+constexpr int kWaves = 4;            // waves per workgroup (256 threads)
+constexpr int kMaxSplit = 4096;      // splits per head the merge kernel handles
 constexpr int kSelCapMax = 2048;     // selected cells per head the gather indexes
+constexpr int kVStride = 144;        // u16 per LDS row of a wave's V tile (288 B)
 
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2_t;
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
 struct AttnParams {
     const uint16_t* q;
@@ -56,172 +72,192 @@ struct AttnParams {
     float* lse;              // [H*G] or null
 };
 
-__device__ __forceinline__ float dot8(const uint4& k, const uint32_t (&q)[4]) {
-    float s = 0.0f;
-    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, k.x), __builtin_bit_cast(bf16x2_t, q[0]), s, false);
-    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, k.y), __builtin_bit_cast(bf16x2_t, q[1]), s, false);
-    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, k.z), __builtin_bit_cast(bf16x2_t, q[2]), s, false);
-    s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, k.w), __builtin_bit_cast(bf16x2_t, q[3]), s, false);
-    return s;
-}
-
-__device__ __forceinline__ float bf16_at(const uint4& v, int u) {
-    const uint32_t w = u < 2 ? v.x : u < 4 ? v.y : u < 6 ? v.z : v.w;
-    return (u & 1) ? bf16_hi(w) : bf16_lo(w);
-}
-
-__device__ __forceinline__ float safe_exp2(float x) { return x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(x); }
-
 // Weight exp2(m - M) of a state with running max m inside a merge whose max
 // is M; an empty state (m = -inf) weighs 0 even when M is -inf too.
 __device__ __forceinline__ float wexp(float m, float M) { return m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M); }
 
-// One workgroup = 8 waves over rows [split * rows_per_block, +rows_per_block)
-// of head h; each wave owns TILES * 16 consecutive rows, read as tiles of 4
-// rows x 4 iterations (16 lanes x 16 bytes per row).  The workgroup writes
-// one partial (max, sum, unnormalised output) with plain stores; merge_kernel
-// combines the partials after the kernel boundary.
-template <int G, int TILES>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnParams a) {
-    constexpr int RW = TILES * 16;
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// One workgroup = 4 waves over rows [split * rows_per_block, +rows_per_block)
+// of its head; the workgroup writes one partial (max, sum, unnormalised
+// output) with plain stores and merge_kernel combines the partials after the
+// kernel boundary.  Workgroups past the end of their head write nothing.
+template <int G, int NT>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) void attention_kernel(AttnParams a) {
+    constexpr int RW = NT * 16;                       // rows per wave
+    constexpr int NR = (RW + 63) / 64;                // row locations per lane
+    constexpr int SU = (kSelCapMax + 1 + 64 * kWaves - 1) / (64 * kWaves);
     __shared__ float s_acc[kWaves][G][128];
     __shared__ float s_ml[kWaves][G][2];
     __shared__ int s_pre[kSelCapMax + 1];
     __shared__ int s_off[kSelCapMax];
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[kWaves][16 * kVStride];
 
     const int b = blockIdx.x;
-    const int h = b % a.H;
     const int split = b / a.H;
+    const int h = (b % a.H + split) % a.H;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int rg = lane >> 4, li = lane & 15;
+    const int lg = lane >> 4, ln = lane & 15;
     const int row0 = split * a.rows_per_block + wave * RW;
 
-    // One round trip for everything the gather needs: q, the row and cell
-    // counts, and the head's selection (CSR offset and row prefix per cell).
-    uint32_t qp[G][4];
+    // One round trip for everything the gather needs: q (as the MFMA B
+    // operand: column ln = query ln % G, dims 32c + 8lg..), the row and cell
+    // counts, and the head's selection (row prefix and CSR offset per cell).
+    u32x4_t qb[4];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const uint4 v = *reinterpret_cast<const uint4*>(a.q + (static_cast<int64_t>(h) * G + g) * 128 + li * 8);
-        qp[g][0] = v.x; qp[g][1] = v.y; qp[g][2] = v.z; qp[g][3] = v.w;
-    }
+    for (int c = 0; c < 4; ++c)
+        qb[c] = *reinterpret_cast<const u32x4_t*>(a.q + (static_cast<int64_t>(h) * G + ln % G) * 128 + c * 32 + lg * 8);
     const int nrows = a.n_rows[h];
     const int m = a.n_selected[h];
     {
         const int32_t* pre = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
         const int32_t* off = a.sel_offset + static_cast<int64_t>(h) * a.sel_cap;
-        for (int i = tid; i <= a.sel_cap; i += 64 * kWaves) {
-            s_pre[i] = pre[i];
-            if (i < a.sel_cap) s_off[i] = off[i];
+        int pv[SU], ov[SU];
+#pragma unroll
+        for (int u = 0; u < SU; ++u) {
+            const int i = tid + u * 64 * kWaves;
+            pv[u] = i <= a.sel_cap ? pre[i] : 0;
+            ov[u] = i < a.sel_cap ? off[i] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < SU; ++u) {
+            const int i = tid + u * 64 * kWaves;
+            if (i <= a.sel_cap) s_pre[i] = pv[u];
+            if (i < a.sel_cap) s_off[i] = ov[u];
         }
     }
     __syncthreads();
-    // row location of lane < RW: cell r with pre[r] <= j < pre[r + 1]
-    int myloc = 0;
-    {
-        const int j = row0 + lane - a.static_len;
-        if (lane < RW && j >= 0 && j < nrows) {
-            int lo = 0, hi = m;
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (s_pre[mid] <= j) lo = mid; else hi = mid;
-            }
-            myloc = s_off[lo] + (j - s_pre[lo]);
-        }
-    }
     const int N = a.static_len + nrows;
-    float m_[G], l_[G], acc[G][8];
+    if (split * a.rows_per_block >= N) return;   // the merge ignores this split
+
+    // List row of rows row0 + lane + 64r: cell c = the last with pre[c] <= j
+    // (branch-free search over the m selected cells, pre[0] = 0).
+    int loc[NR];
+    {
+        int lo[NR], jj[NR];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m_[g] = -INFINITY;
-        l_[g] = 0.0f;
+        for (int r = 0; r < NR; ++r) {
+            lo[r] = 0;
+            jj[r] = row0 + lane + 64 * r - a.static_len;
+        }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc[g][u] = 0.0f;
+        for (int step = kSelCapMax / 2; step >= 1; step >>= 1)
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                const int c = lo[r] + step;
+                if (c < m && s_pre[c] <= jj[r]) lo[r] = c;
+            }
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+            loc[r] = (jj[r] >= 0 && jj[r] < nrows) ? s_off[lo[r]] + (jj[r] - s_pre[lo[r]]) : 0;
     }
+
     const uint16_t* skh = a.sk + static_cast<int64_t>(h) * a.s_stride * 128;
     const uint16_t* svh = a.sv + static_cast<int64_t>(h) * a.s_stride * 128;
     const uint16_t* lkh = a.lk + static_cast<int64_t>(h) * a.list_rows * 128;
     const uint16_t* lvh = a.lv + static_cast<int64_t>(h) * a.list_rows * 128;
+    f32x4_t acc[8];   // acc[d][r] = O[query slot 4lg + r][dim 16d + ln]
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[d] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_own = -INFINITY, l_own = 0.0f;   // softmax state of query slot ln
+    uint16_t* sv = s_v[wave];
 
     if (row0 < N) {
-        // Branch-free gather: rows past N read row 0 of the list (always in
-        // bounds) and get a -inf score, so all 2 * 4 * TILES loads issue
-        // back to back.
-        uint4 kk[TILES][4], vv[TILES][4];
-        bool ok[TILES][4];
+        // Tile t: lane loads token t*16 + ln (16 bytes at dims 32c + 8lg).
+        // Rows past N read list row 0 (in bounds) and are masked below.
+        u32x4_t kb[2][4], vb[2][4];
+        auto load = [&](int t, int slot) {
+            const int jt = t * 16 + ln;
+            const int n = row0 + jt;
+            const int lr = __shfl(loc[(t * 16) >> 6], jt & 63);
+            const bool st = n < a.static_len;
+            const int64_t roff = (st ? static_cast<int64_t>(n) : static_cast<int64_t>(n < N ? lr : 0)) * 128;
+            const uint16_t* kp = (st ? skh : lkh) + roff + lg * 8;
+            const uint16_t* vp = (st ? svh : lvh) + roff + lg * 8;
 #pragma unroll
-        for (int t = 0; t < TILES; ++t)
-#pragma unroll
-            for (int it = 0; it < 4; ++it) {
-                const int j = t * 16 + it * 4 + rg;
-                const int n = row0 + j;
-                const int loc = __shfl(myloc, j);
-                ok[t][it] = n < N;
-                const bool st = n < a.static_len;
-                const int64_t roff = (st ? static_cast<int64_t>(n) : static_cast<int64_t>(ok[t][it] ? loc : 0)) * 128;
-                const uint16_t* kp = (st ? skh : lkh) + roff + li * 8;
-                const uint16_t* vp = (st ? svh : lvh) + roff + li * 8;
-                kk[t][it] = *reinterpret_cast<const uint4*>(kp);
-                vv[t][it] = *reinterpret_cast<const uint4*>(vp);
+            for (int c = 0; c < 4; ++c) {
+                kb[slot][c] = *reinterpret_cast<const u32x4_t*>(kp + c * 32);
+                vb[slot][c] = *reinterpret_cast<const u32x4_t*>(vp + c * 32);
             }
+        };
+        load(0, 0);
+        if (NT > 1) load(1, 1);
 #pragma unroll
-        for (int t = 0; t < TILES; ++t) {
-            float s[4][G];
+        for (int t = 0; t < NT; ++t) {
+            const int slot = t & 1;
+            // V tile -> LDS, row-major [token][dim]
 #pragma unroll
-            for (int it = 0; it < 4; ++it)
+            for (int c = 0; c < 4; ++c)
+                *reinterpret_cast<u32x4_t*>(sv + ln * kVStride + c * 32 + lg * 8) = vb[slot][c];
+            f32x4_t s4 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const float d = row16_sum(dot8(kk[t][it], qp[g]));
-                    s[it][g] = ok[t][it] ? d * a.scale_log2 : -INFINITY;
+            for (int c = 0; c < 4; ++c)
+                s4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kb[slot][c]),
+                                                             __builtin_bit_cast(bf16x8_t, qb[c]), s4, 0, 0, 0);
+            if (t + 2 < NT) load(t + 2, slot);
+            float s[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                s[i] = (row0 + t * 16 + 4 * lg + i < N) ? s4[i] * a.scale_log2 : -INFINITY;
+            float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+            tm = fmaxf(tm, xor16(tm));
+            tm = fmaxf(tm, xor32(tm));
+            const float mn = fmaxf(m_own, tm);
+            const float corr = wexp(m_own, mn);
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[i] = wexp(s[i], mn);   // 0 for masked rows
+            l_own = l_own * corr + ((p[0] + p[1]) + (p[2] + p[3]));
+            m_own = mn;
+            if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
+                // O row 4lg + r belongs to query slot 4lg + r: its factor sits
+                // in lane 16lg + 4lg + r (any lane of that slot would do).
+                float cr[4];
+                if (4 % G == 0) {
+                    cr[0] = dpp_f32<0x00>(corr);
+                    cr[1] = dpp_f32<0x55>(corr);
+                    cr[2] = dpp_f32<0xAA>(corr);
+                    cr[3] = dpp_f32<0xFF>(corr);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 16 * lg + 4 * lg + r);
                 }
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float tm = fmaxf(fmaxf(s[0][g], s[1][g]), fmaxf(s[2][g], s[3][g]));
-                const float mn = fmaxf(m_[g], tm);
-                const float corr = wexp(m_[g], mn);
-                float p[4];
-#pragma unroll
-                for (int it = 0; it < 4; ++it) p[it] = wexp(s[it][g], mn);   // 0 for rows past the end
-                l_[g] = l_[g] * corr + ((p[0] + p[1]) + (p[2] + p[3]));
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    float x = acc[g][u] * corr;
-#pragma unroll
-                    for (int it = 0; it < 4; ++it) x = __builtin_fmaf(p[it], bf16_at(vv[t][it], u), x);
-                    acc[g][u] = x;
+                for (int d = 0; d < 8; ++d) {
+                    acc[d][0] *= cr[0];
+                    acc[d][1] *= cr[1];
+                    acc[d][2] *= cr[2];
+                    acc[d][3] *= cr[3];
                 }
-                m_[g] = mn;
+            }
+            u32x2_t pa;
+            pa.x = pack_bf16(p[0], p[1]);
+            pa.y = pack_bf16(p[2], p[3]);
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                // lane (lg, ln) gets V[token 4lg + e][dim 16d + ln], e = 0..3
+                const s16x4_t vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4_t*)(sv + (4 * lg + (ln >> 2)) * kVStride + d * 16 + 4 * (ln & 3)));
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, pa), vt, acc[d], 0,
+                                                                   0, 0);
             }
         }
     }
-    // merge the four row groups of the wave (lanes li, li+16, li+32, li+48)
-    // with the permlane swaps: first across rows 0<->1, 2<->3, then halves
+    // sum over the four lane groups (different tokens, shared max)
+    l_own += xor16(l_own);
+    l_own += xor32(l_own);
+    // query g: O row g (lane group g / 4, register g % 4), state of slot g
 #pragma unroll
-    for (int step = 0; step < 2; ++step) {
+    for (int g = 0; g < G; ++g)
+        if (lg == g / 4) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float mo = step == 0 ? xor16(m_[g]) : xor32(m_[g]);
-            const float lo = step == 0 ? xor16(l_[g]) : xor32(l_[g]);
-            const float mn = fmaxf(m_[g], mo);
-            const float wa = wexp(m_[g], mn), wb = wexp(mo, mn);
-            l_[g] = l_[g] * wa + lo * wb;
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float ao = step == 0 ? xor16(acc[g][u]) : xor32(acc[g][u]);
-                acc[g][u] = acc[g][u] * wa + ao * wb;
-            }
-            m_[g] = mn;
+            for (int d = 0; d < 8; ++d) s_acc[wave][g][d * 16 + ln] = acc[d][g % 4];
         }
-    }
-    if (rg == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-#pragma unroll
-            for (int u = 0; u < 8; ++u) s_acc[wave][g][li * 8 + u] = acc[g][u];
-            if (li == 0) {
-                s_ml[wave][g][0] = m_[g];
-                s_ml[wave][g][1] = l_[g];
-            }
-        }
+    if (lg == 0 && ln < G) {
+        s_ml[wave][ln][0] = m_own;
+        s_ml[wave][ln][1] = l_own;
     }
     __syncthreads();
     // block partial (waves merged in order)
@@ -246,11 +282,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
     }
 }
 
-// Merge of the nsplit partials of one head for 64 outputs (query head
-// g = chunk / 2, dims (chunk % 2) * 64 ..).  Each of the four waves sums a
-// quarter of the splits (s = q, q + 4, ...); its first 16 loads are issued
-// before wave 0 has derived the split weights, so the common case needs one
-// round trip.  Quarters are added in a fixed order (deterministic).
+// Merge of the partials of one head for 64 outputs (query head
+// g = chunk / 2, dims (chunk % 2) * 64 ..).  Only splits that hold rows of
+// the head (ceil((static_len + n_rows) / rows_per_block)) take part.  Each of
+// the four waves sums a quarter of the splits (s = q, q + 4, ...); its first
+// 16 loads are issued before wave 0 has derived the split weights, so the
+// common case needs one round trip.  Quarters are added in a fixed order
+// (deterministic).
 __global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
     __shared__ float s_w[kMaxSplit];
     __shared__ float s_red[4][64];
@@ -259,15 +297,17 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
     const int g = chunk >> 1;
     const int tid = threadIdx.x, q = tid >> 6, lane = tid & 63;
     const int o = chunk * 64 + lane;  // g * 128 + d
-    const int ns = a.nsplit;
+    const int nsm = a.nsplit;
+    const int rows = a.static_len + a.n_rows[h];
+    const int ns = min(nsm, (rows + a.rows_per_block - 1) / a.rows_per_block);
     const int64_t stride = static_cast<int64_t>(G) * 128;
-    const float* pacc = a.part_acc + static_cast<int64_t>(h) * ns * stride + o;
-    const float* pml = a.part_ml + (static_cast<int64_t>(h) * ns * G + g) * 2;
+    const float* pacc = a.part_acc + static_cast<int64_t>(h) * nsm * stride + o;
+    const float* pml = a.part_ml + (static_cast<int64_t>(h) * nsm * G + g) * 2;
     float v[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
         const int s = q + 4 * u;
-        v[u] = s < ns ? pacc[s * stride] : 0.0f;
+        v[u] = s < nsm ? pacc[s * stride] : 0.0f;
     }
     if (q == 0) {
         float M = -INFINITY;
@@ -316,25 +356,42 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
     }
 }
 
-// Rows per wave: two tiles when the head has enough rows to give every CU
-// about two workgroups, otherwise one.
-int tiles_for(int rows, int H) {
-    const int blocks_one_tile = (rows + kWaves * 16 - 1) / (kWaves * 16);
-    return blocks_one_tile * H > 512 ? 2 : 1;
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
 }
 
-int nsplit_for(const imi_attention_args* a) {
-    const int rows = a->static_len + a->max_rows;
-    const int rb = kWaves * 16 * tiles_for(rows, a->kv_heads);
-    return rows <= 0 ? 1 : (rows + rb - 1) / rb;
-}
-
-// Splits the workspace is sized for: any static_len up to steady_stride, so a
-// workspace sized once stays valid while the steady zone grows.
-int nsplit_bound(const imi_attention_args* a) {
+// Rows the workspace and the tile size are fixed for: any static_len up to
+// steady_stride, so one workspace (and one captured launch shape) stays valid
+// while the steady zone grows.
+int64_t rows_bound(const imi_attention_args* a) {
     const int64_t srows = a->steady_stride > a->static_len ? a->steady_stride : a->static_len;
-    const int rows = static_cast<int>(srows + a->max_rows);
-    return rows <= 0 ? 1 : (rows + kWaves * 16 - 1) / (kWaves * 16);
+    return srows + a->max_rows;
+}
+
+// Tiles per wave: the most (up to 8) that still gives at least 3/4 of the
+// CUs a workgroup; short row counts use one tile per wave.
+int tiles_per_wave(const imi_attention_args* a) {
+    const int64_t rows = rows_bound(a);
+    const int64_t want = device_cus() * 3 / 4;
+    for (int nt = 8; nt > 1; nt >>= 1) {
+        const int64_t rpb = 64 * nt;
+        if (a->kv_heads * ((rows + rpb - 1) / rpb) >= want) return nt;
+    }
+    return 1;
+}
+
+int nsplit_bound(const imi_attention_args* a) {
+    const int64_t rpb = 64 * tiles_per_wave(a);
+    const int64_t rows = rows_bound(a);
+    return rows <= 0 ? 1 : static_cast<int>((rows + rpb - 1) / rpb);
 }
 
 size_t attn_workspace(const imi_attention_args* a, AttnParams* p) {
@@ -345,9 +402,8 @@ size_t attn_workspace(const imi_attention_args* a, AttnParams* p) {
     if (p) {
         p->part_acc = acc;
         p->part_ml = ml;
-        p->nsplit = nsplit_for(a);
-        const int rows = a->static_len + a->max_rows;
-        p->rows_per_block = kWaves * 16 * tiles_for(rows, a->kv_heads);
+        p->nsplit = nsplit;
+        p->rows_per_block = 64 * tiles_per_wave(a);
     }
     return cv.used();
 }
@@ -378,10 +434,12 @@ int attn_validate(const imi_attention_args* a, bool need_sel) {
 
 template <int G>
 void launch_g(const AttnParams& p, int blocks, hipStream_t stream) {
-    if (p.rows_per_block == kWaves * 32)
-        hipLaunchKernelGGL((attention_kernel<G, 2>), dim3(blocks), dim3(64 * kWaves), 0, stream, p);
-    else
-        hipLaunchKernelGGL((attention_kernel<G, 1>), dim3(blocks), dim3(64 * kWaves), 0, stream, p);
+    switch (p.rows_per_block / 64) {
+        case 8: hipLaunchKernelGGL((attention_kernel<G, 8>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
+        case 4: hipLaunchKernelGGL((attention_kernel<G, 4>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
+        case 2: hipLaunchKernelGGL((attention_kernel<G, 2>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
+        default: hipLaunchKernelGGL((attention_kernel<G, 1>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
+    }
 }
 
 int attn_launch(const imi_attention_args* a, hipStream_t stream) {
@@ -404,7 +462,9 @@ int attn_launch(const imi_attention_args* a, hipStream_t stream) {
     p.scale_log2 = a->scale * 1.44269504088896340736f;
     p.out = a->out;
     p.lse = a->out_lse;
-    const int blocks = a->kv_heads * p.nsplit;
+    const int64_t rows = static_cast<int64_t>(a->static_len) + a->max_rows;
+    const int splits = rows <= 0 ? 1 : static_cast<int>((rows + p.rows_per_block - 1) / p.rows_per_block);
+    const int blocks = a->kv_heads * splits;
     switch (a->groups) {
         case 1: launch_g<1>(p, blocks, stream); break;
         case 2: launch_g<2>(p, blocks, stream); break;

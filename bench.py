@@ -118,18 +118,20 @@ def main():
             p.step()
 
     # -------------------------------------------------- graph of one step
-    graph = None
-    if not args.no_graph:
-        run_step()
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
+    def capture(fn):
+        g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            with torch.cuda.graph(graph, stream=s):
-                run_step()
+            with torch.cuda.graph(g, stream=s):
+                fn()
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
+        return g
+
+    run_step()
+    torch.cuda.synchronize()
+    graph = None if args.no_graph else capture(run_step)
 
     def one_step():
         if graph is not None:
@@ -137,11 +139,11 @@ def main():
         else:
             run_step()
 
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
     for _ in range(args.warmup):
         one_step()
     torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
     t0.record()
     for _ in range(args.steps):
         one_step()
@@ -157,23 +159,27 @@ def main():
     bytes_per_step = rows * 2 * D * 2
     bytes_per_layer = bytes_per_step / L
 
-    # --------------------------- per-kernel durations (eager, HIP events)
-    sel_ms, att_ms = [], []
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    for rep in range(3):
-        for p in plans:
-            evs[0].record()
-            p.step(phases=1)
-            evs[1].record()
-            p.step(phases=2)
-            evs[2].record()
-            torch.cuda.synchronize()
-            sel_ms.append(evs[0].elapsed_time(evs[1]))
-            att_ms.append(evs[1].elapsed_time(evs[2]))
-    att_avg_ms = statistics.mean(att_ms)
-    sel_avg_ms = statistics.mean(sel_ms)
-    achieved = bytes_per_layer / (att_avg_ms * 1e-3) / 1e9
+    # ------------------- per-launch durations: HIP events around graphs that
+    # hold only one phase of every layer (back-to-back launches on one stream,
+    # so host launch gaps do not enter); the selection the attention graph
+    # reads is the one the last full step left in each plan's workspace.
+    def per_launch_us(phase, reps):
+        g = capture(lambda: [p.step(phases=phase) for p in plans])
+        g.replay()
+        torch.cuda.synchronize()
+        t0.record()
+        for _ in range(reps):
+            g.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) * 1e3 / (reps * L)
+
+    reps = max(args.steps, 5)
+    sel_us = per_launch_us(1, reps)
+    att_us = per_launch_us(2, reps)
+    achieved = bytes_per_layer / (att_us * 1e-6) / 1e9
     step_gbps = bytes_per_layer / (ms_per_step / L * 1e-3) / 1e9
+    log(f"[bench] per launch: select {sel_us:.2f} us, attention+merge {att_us:.2f} us")
 
     # ----------------------------------------------------- CPU baseline
     cpu = None
@@ -205,10 +211,10 @@ def main():
         "us_per_layer_step": round(ms_per_step / L * 1e3, 3),
         "attended_rows_per_layer": rows / L,
         "hbm_frac_step": round(step_gbps / HBM_PEAK_GBPS, 4),
-        "kernels_us": {"select": round(sel_avg_ms * 1e3, 2), "gather_attention": round(att_avg_ms * 1e3, 2)},
+        "kernels_us": {"select_kernel": round(sel_us, 2), "attention_kernel+merge_kernel": round(att_us, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "attention_kernel (gather + GQA split-K attention)",
+                     "kernel": "attention_kernel + merge_kernel (gather, GQA split-K attention, split merge)",
                      "bytes_per_launch": int(bytes_per_layer)},
         "cpu_baseline": cpu,
     }
