@@ -31,6 +31,7 @@ namespace {
 constexpr int kSelThreads = 1024;
 constexpr int kBins = 2048;
 constexpr int kCap = 2048;     // candidate capacity
+constexpr int kMaxGroups = 8;  // query heads per KV head
 
 struct SelParams {
     const uint16_t* q;
@@ -69,6 +70,36 @@ __device__ __forceinline__ int block_incl_scan(int v, int* sh, int& total) {
     return r;
 }
 
+// Two block-wide inclusive scans at once (same three barriers as one).
+__device__ __forceinline__ void block_incl_scan2(int& a, int& b, int* sh, int& ta, int& tb) {
+    const int ia = wave_incl_scan(a), ib = wave_incl_scan(b);
+    const int wave = threadIdx.x >> 6;
+    if (lane_id() == 63) {
+        sh[wave] = ia;
+        sh[16 + wave] = ib;
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int xa = threadIdx.x < 16 ? sh[threadIdx.x] : 0;
+        const int xb = threadIdx.x < 16 ? sh[16 + threadIdx.x] : 0;
+        const int va = wave_incl_scan(xa), vb = wave_incl_scan(xb);
+        if (threadIdx.x < 16) {
+            sh[32 + threadIdx.x] = va - xa;
+            sh[48 + threadIdx.x] = vb - xb;
+        }
+        if (threadIdx.x == 15) {
+            sh[64] = va;
+            sh[65] = vb;
+        }
+    }
+    __syncthreads();
+    a = sh[32 + wave] + ia;
+    b = sh[48 + wave] + ib;
+    ta = sh[64];
+    tb = sh[65];
+    __syncthreads();
+}
+
 __device__ __forceinline__ uint64_t cell_key(uint32_t okey, int g) {
     return (static_cast<uint64_t>(okey) << 32) | static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(g));
 }
@@ -86,19 +117,20 @@ __device__ __forceinline__ int bucket_of(float s, float gmax, float inv) {
 template <int DP, int EPT>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     extern __shared__ uint64_t dyn[];
-    __shared__ float qs[128];
+    __shared__ __attribute__((aligned(16))) float qs[128];
     __shared__ float p1[256];
     __shared__ int hist[kBins];         // bucket counts, then fill cursors
     __shared__ int binbase[kBins + 1];  // first candidate slot of each bucket
-    __shared__ int sh[48];
+    __shared__ int sh[82];
     __shared__ int shv[8];
     __shared__ float shf[40];
 
     const int h = blockIdx.x;
     const int tid = threadIdx.x;
     const int k0 = a.k[0], k1 = a.k[1];
-    // LDS regions: c1T during scoring, candidates afterwards
-    float* c1T = reinterpret_cast<float*>(dyn);          // [DP][k1]
+    // LDS regions: centroids during scoring, candidates afterwards
+    float* c1T = reinterpret_cast<float*>(dyn);          // [DP][k1 + 1]
+    float* c0s = c1T + DP * (k1 + 1);                    // [k0][DP + 1]
     uint64_t* ck = dyn;                                  // [kCap] keys by bucket
     int* cs = reinterpret_cast<int*>(ck + kCap);         // [kCap] sizes
     int* co = cs + kCap;                                 // [kCap] CSR offsets
@@ -124,24 +156,46 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         sz[e] = in ? cntp[g] : 0;
         co_[e] = in ? offs[g] : 0;
     }
+    // C0 and C1 rows [k][DP] are read coalesced (float4 per thread) and
+    // stored in LDS with padded strides (conflict-free word reads): C0
+    // row-major [l0][DP + 1] for the per-l0 chain, C1 transposed
+    // [d][k1 + 1] so that lanes over l1 read consecutive words.
     const float* c0 = a.cent + (static_cast<int64_t>(h) * a.P + 0) * a.kmax * DP;
     const float* c1 = a.cent + (static_cast<int64_t>(h) * a.P + 1) * a.kmax * DP;
-    float row[DP];
-    if (tid < k0) {
-        const float4* r4 = reinterpret_cast<const float4*>(c0 + static_cast<int64_t>(tid) * DP);
+    constexpr int kV4 = 128 * DP / 4 / kSelThreads;   // float4 per thread per subspace (k <= 128)
+    float4 c0v[kV4], c1v[kV4];
 #pragma unroll
-        for (int i = 0; i < DP / 4; ++i) {
-            const float4 v = r4[i];
-            row[4 * i] = v.x; row[4 * i + 1] = v.y; row[4 * i + 2] = v.z; row[4 * i + 3] = v.w;
-        }
+    for (int u = 0; u < kV4; ++u) {
+        const int i4 = tid + u * kSelThreads;          // float4 index: row i4 / (DP/4)
+        c0v[u] = i4 * 4 < k0 * DP ? reinterpret_cast<const float4*>(c0)[i4] : make_float4(0, 0, 0, 0);
+        c1v[u] = i4 * 4 < k1 * DP ? reinterpret_cast<const float4*>(c1)[i4] : make_float4(0, 0, 0, 0);
     }
-    for (int i = tid; i < k1 * DP; i += kSelThreads) {
-        const int d = i / k1, j = i - (i / k1) * k1;   // consecutive lanes -> consecutive LDS words
-        c1T[i] = c1[static_cast<int64_t>(j) * DP + d];
+    uint16_t qv[kMaxGroups];
+    if (tid < a.D) {
+#pragma unroll
+        for (int g = 0; g < kMaxGroups; ++g)
+            qv[g] = g < a.G ? a.q[(static_cast<int64_t>(h) * a.G + g) * a.D + tid] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kV4; ++u) {
+        const int i4 = tid + u * kSelThreads;
+        const int r = (i4 * 4) / DP, d = (i4 * 4) % DP;
+        const float e0[4] = {c0v[u].x, c0v[u].y, c0v[u].z, c0v[u].w};
+        const float e1[4] = {c1v[u].x, c1v[u].y, c1v[u].z, c1v[u].w};
+        if (r < k0) {
+#pragma unroll
+            for (int x = 0; x < 4; ++x) c0s[r * (DP + 1) + d + x] = e0[x];
+        }
+        if (r < k1) {
+#pragma unroll
+            for (int x = 0; x < 4; ++x) c1T[(d + x) * (k1 + 1) + r] = e1[x];
+        }
     }
     if (tid < a.D) {
         float acc = 0.0f;   // grouped-query sum, g ascending (compute_impl.cu:80-87)
-        for (int g = 0; g < a.G; ++g) acc += bf16_to_f32(a.q[(static_cast<int64_t>(h) * a.G + g) * a.D + tid]);
+#pragma unroll
+        for (int g = 0; g < kMaxGroups; ++g)
+            if (g < a.G) acc += bf16_to_f32(qv[g]);
         qs[tid] = acc;
     }
     for (int i = tid; i < kBins; i += kSelThreads) hist[i] = 0;
@@ -151,7 +205,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     if (tid < k0) {
         float acc = 0.0f;
 #pragma unroll
-        for (int d = 0; d < DP; ++d) acc = __builtin_fmaf(qs[d], row[d], acc);
+        for (int d = 0; d < DP; ++d) acc = __builtin_fmaf(qs[d], c0s[tid * (DP + 1) + d], acc);
         p1[tid] = acc;
     }
     __syncthreads();
@@ -167,7 +221,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
 #pragma unroll
         for (int d = 0; d < DP; ++d) {
             const float qd = qs[DP + d];
-            const float cv = c1T[d * k1 + jcell];
+            const float cv = c1T[d * (k1 + 1) + jcell];
 #pragma unroll
             for (int e = 0; e < EPT; ++e) sc[e] = __builtin_fmaf(qd, cv, sc[e]);
         }
@@ -360,8 +414,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         psum += pg2[u];
     }
     int ttot, ptot;
-    const int tincl = block_incl_scan(tsum, sh, ttot);
-    const int pincl = block_incl_scan(psum, sh, ptot);
+    int tincl = tsum, pincl = psum;
+    block_incl_scan2(tincl, pincl, sh, ttot, ptot);
     int texcl = tincl - tsum, pexcl = pincl - psum;
     int kept = 0;
     int excl_tok[2];
@@ -374,8 +428,16 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         kept += keep ? 1 : 0;
         texcl += s2[u];
     }
-    int m;
-    block_incl_scan(kept, sh, m);
+    // the rules are monotone in rank (prefixes only grow), so the kept ranks
+    // are exactly the first m: count them per wave, then over the 16 waves
+    {
+        const int wk = wave_sum_i(kept);
+        if (lane_id() == 0) sh[66 + (tid >> 6)] = wk;
+    }
+    __syncthreads();
+    int m = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) m += sh[66 + w];
     int32_t* out_cell = a.sel_cell + static_cast<int64_t>(h) * a.sel_cap;
     int32_t* out_off = a.sel_offset + static_cast<int64_t>(h) * a.sel_cap;
     int32_t* out_cnt = a.sel_count + static_cast<int64_t>(h) * a.sel_cap;
@@ -431,6 +493,8 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     IMI_REQUIRE(a->query && a->centroids && a->cell_count && a->cell_offset, IMI_ERR_INVALID,
                 "imi_select: null input pointer");
     IMI_REQUIRE(a->kv_heads > 0 && a->groups > 0, IMI_ERR_INVALID, "imi_select: empty shape");
+    IMI_REQUIRE(a->groups <= kMaxGroups, IMI_ERR_UNSUPPORTED, "imi_select: %d query heads per kv head exceed %d",
+                a->groups, kMaxGroups);
     IMI_REQUIRE(a->dim == 128, IMI_ERR_UNSUPPORTED, "imi_select: head_dim must be 128");
     IMI_REQUIRE(a->parts == 2, IMI_ERR_UNSUPPORTED, "imi_select: only 2-way IMI is implemented (parts=%d)",
                 a->parts);
@@ -439,7 +503,7 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     kmax = a->k[0] > a->k[1] ? a->k[0] : a->k[1];
     IMI_REQUIRE(a->k[0] >= 1 && a->k[1] >= 1 && kmax <= 256, IMI_ERR_UNSUPPORTED, "imi_select: k outside [1,256]");
     ncells = static_cast<int64_t>(a->k[0]) * a->k[1];
-    IMI_REQUIRE(a->k[1] <= 128 && a->k[0] <= 16 * (kSelThreads / a->k[1]), IMI_ERR_UNSUPPORTED,
+    IMI_REQUIRE(a->k[0] <= 128 && a->k[1] <= 128 && a->k[0] <= 16 * (kSelThreads / a->k[1]), IMI_ERR_UNSUPPORTED,
                 "imi_select: k = (%d, %d) exceeds the cells one workgroup holds", a->k[0], a->k[1]);
     const int kprime = a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages;
     IMI_REQUIRE(kprime <= kCap, IMI_ERR_UNSUPPORTED, "imi_select: min(nprobe, buffer_pages)=%d exceeds %d", kprime,
@@ -453,7 +517,7 @@ template <int EPT>
 int launch_ept(const SelParams& p, int H, hipStream_t stream) {
     constexpr int DP = 64;
     const size_t cand = static_cast<size_t>(kCap) * (sizeof(uint64_t) + 6 * sizeof(int));
-    const size_t ct = static_cast<size_t>(DP) * p.k[1] * sizeof(float);
+    const size_t ct = (static_cast<size_t>(DP) * (p.k[1] + 1) + static_cast<size_t>(p.k[0]) * (DP + 1)) * sizeof(float);
     const size_t lds = cand > ct ? cand : ct;
     static bool attr_set = false;
     if (!attr_set) {
