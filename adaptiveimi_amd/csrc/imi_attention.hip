@@ -284,11 +284,12 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
 
 // Merge of the partials of one head for 64 outputs (query head
 // g = chunk / 2, dims (chunk % 2) * 64 ..).  Only splits that hold rows of
-// the head (ceil((static_len + n_rows) / rows_per_block)) take part.  Each of
-// the four waves sums a quarter of the splits (s = q, q + 4, ...); its first
-// 16 loads are issued before wave 0 has derived the split weights, so the
-// common case needs one round trip.  Quarters are added in a fixed order
-// (deterministic).
+// the head (ceil((static_len + n_rows) / rows_per_block)) take part.  Every
+// load of the first 64 splits (partial sums, and the max / sum pairs that
+// wave 0 turns into split weights) is issued before the row count is known,
+// so the common case needs one round trip.  Each of the four waves sums a
+// quarter of the splits (s = q, q + 4, ...); quarters are added in a fixed
+// order (deterministic).
 __global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
     __shared__ float s_w[kMaxSplit];
     __shared__ float s_red[4][64];
@@ -298,8 +299,6 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
     const int tid = threadIdx.x, q = tid >> 6, lane = tid & 63;
     const int o = chunk * 64 + lane;  // g * 128 + d
     const int nsm = a.nsplit;
-    const int rows = a.static_len + a.n_rows[h];
-    const int ns = min(nsm, (rows + a.rows_per_block - 1) / a.rows_per_block);
     const int64_t stride = static_cast<int64_t>(G) * 128;
     const float* pacc = a.part_acc + static_cast<int64_t>(h) * nsm * stride + o;
     const float* pml = a.part_ml + (static_cast<int64_t>(h) * nsm * G + g) * 2;
@@ -309,15 +308,24 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
         const int s = q + 4 * u;
         v[u] = s < nsm ? pacc[s * stride] : 0.0f;
     }
+    float pm = -INFINITY, pl = 0.0f;
+    if (q == 0 && lane < nsm) {
+        pm = pml[static_cast<int64_t>(lane) * G * 2];
+        pl = pml[static_cast<int64_t>(lane) * G * 2 + 1];
+    }
+    const int rows = a.static_len + a.n_rows[h];
+    const int ns = min(nsm, (rows + a.rows_per_block - 1) / a.rows_per_block);
     if (q == 0) {
-        float M = -INFINITY;
-        for (int s = lane; s < ns; s += 64) M = fmaxf(M, pml[static_cast<int64_t>(s) * G * 2]);
+        float M = lane < ns ? pm : -INFINITY;
+        for (int s = lane + 64; s < ns; s += 64) M = fmaxf(M, pml[static_cast<int64_t>(s) * G * 2]);
         M = wave_max(M);
-        float L = 0.0f;
-        for (int s = lane; s < ns; s += 64) {
-            const float w = wexp(pml[static_cast<int64_t>(s) * G * 2], M);
-            s_w[s] = w;
-            L += pml[static_cast<int64_t>(s) * G * 2 + 1] * w;
+        float w = lane < ns ? wexp(pm, M) : 0.0f;
+        if (lane < nsm) s_w[lane] = w;
+        float L = pl * w;
+        for (int s = lane + 64; s < ns; s += 64) {
+            const float ws = wexp(pml[static_cast<int64_t>(s) * G * 2], M);
+            s_w[s] = ws;
+            L += pml[static_cast<int64_t>(s) * G * 2 + 1] * ws;
         }
         L = wave_sum(L);
         if (lane == 0) {

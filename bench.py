@@ -48,6 +48,9 @@ def parse():
     p.add_argument("--cpu-baseline", type=int, default=1)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-graph", action="store_true")
+    p.add_argument("--copy-probe-mb", type=int, default=0,
+                   help="run a device-to-device copy of this many MiB (3 times) before the timed region, as the "
+                        "known-size reference for FETCH_SIZE / WRITE_SIZE counter runs")
     return p.parse_args()
 
 
@@ -112,6 +115,14 @@ def main():
         if layer % 8 == 7:
             log(f"[bench] built {layer + 1}/{L} layers, last build {build_ms[-1]:.2f} ms")
     torch.cuda.synchronize()
+
+    if args.copy_probe_mb > 0:
+        src = torch.empty(args.copy_probe_mb << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     def run_step():
         for p in plans:
@@ -213,12 +224,25 @@ def main():
         "hbm_frac_step": round(step_gbps / HBM_PEAK_GBPS, 4),
         "kernels_us": {"select_kernel": round(sel_us, 2), "attention_kernel+merge_kernel": round(att_us, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
                      "kernel": "attention_kernel + merge_kernel (gather, GQA split-K attention, split merge)",
                      "bytes_per_launch": int(bytes_per_layer)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per attention launch from the committed counter summary
+    (FETCH_SIZE + WRITE_SIZE of attention_kernel + merge_kernel, scaled by the
+    copy-probe calibration), or None when no summary is present."""
+    f = ROOT / "profiles" / "attention_kernel_traffic_128k.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
 
 
 def cpu_baseline(first, ks, bud, static_len, seconds):
