@@ -361,8 +361,66 @@ class DecodePlan:
     def set_static_len(self, static_len: int) -> None:
         self.args.attn.static_len = int(static_len)
 
+    def run(self, query: torch.Tensor, out: torch.Tensor, static_len: int, stream: Optional[int] = None) -> torch.Tensor:
+        """One full step on caller-owned query [H, G, D] and out [H * G, D]
+        buffers (no copies: the plan's pointers are redirected)."""
+        _as_bits(query)
+        if not query.is_contiguous() or tuple(query.shape) != (self.H, self.G, self.D):
+            raise ValueError(f"query must be a contiguous [{self.H}, {self.G}, {self.D}] tensor")
+        if not out.is_contiguous() or out.numel() != self.H * self.G * self.D or out.dtype != torch.bfloat16:
+            raise ValueError("out must be a contiguous bf16 tensor of H * G * D elements")
+        a = self.args
+        a.sel.query = a.attn.query = query.data_ptr()
+        a.attn.out = out.data_ptr()
+        a.attn.static_len = int(static_len)
+        a.phases = 3
+        try:
+            check(self._fn(self._ref, stream if stream is not None else _stream(self.device)), "imi_decode_step")
+        finally:
+            a.sel.query = a.attn.query = self.query.data_ptr()
+            a.attn.out = self.out.data_ptr()
+        return out
+
     def step(self, stream: Optional[int] = None, phases: int = 3) -> torch.Tensor:
         """Enqueue one step; phases 1 = selection only, 2 = attention only."""
         self.args.phases = phases
         check(self._fn(self._ref, stream if stream is not None else _stream(self.device)), "imi_decode_step")
         return self.out
+
+
+def dense_attention(query: torch.Tensor, steady_keys: torch.Tensor, steady_values: torch.Tensor, static_len: int,
+                    scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """GQA decode attention over the first static_len rows of the steady zone
+    only (runtime.py:393-402): the gather kernel with an empty selection."""
+    dev = _require_device(query, steady_keys, steady_values)
+    _as_bits(query)
+    H, G, D = query.shape
+    if steady_keys.shape[0] != H or steady_keys.shape[2] != D or not steady_keys.is_contiguous():
+        raise ValueError("steady_keys must be contiguous [H, rows, D]")
+    if steady_values.shape != steady_keys.shape or not steady_values.is_contiguous():
+        raise ValueError("steady_values must match steady_keys")
+    key = ("dense_sel", dev.index if dev.index is not None else torch.cuda.current_device(), H)
+    zeros = _WS.get(key)
+    if zeros is None:
+        # sel_offset [H][1], sel_count [H][1], sel_prefix [H][2], counts [H]: all zero
+        zeros = torch.zeros((4, 2 * H + 2), dtype=torch.int32, device=dev)
+        _WS[key] = zeros
+    if out is None:
+        out = torch.empty((H * G, D), dtype=torch.bfloat16, device=dev)
+    a = AttentionArgs(query=query.contiguous().data_ptr(), steady_keys=steady_keys.data_ptr(),
+                      steady_values=steady_values.data_ptr(), steady_stride=steady_keys.shape[1],
+                      static_len=int(static_len), list_keys=steady_keys.data_ptr(),
+                      list_values=steady_values.data_ptr(), list_rows=steady_keys.shape[1],
+                      sel_offset=zeros[0].data_ptr(), sel_count=zeros[1].data_ptr(), sel_prefix=zeros[2].data_ptr(),
+                      n_selected=zeros[3].data_ptr(), n_rows=zeros[3].data_ptr(), sel_cap=1, max_rows=0,
+                      kv_heads=H, groups=G, dim=D,
+                      scale=float(scale if scale is not None else 1.0 / math.sqrt(D)), out=out.data_ptr(),
+                      out_lse=None)
+    need = ctypes.c_size_t()
+    check(_lib.lib().imi_attention_workspace_size(ctypes.byref(a), ctypes.byref(need)),
+          "imi_attention_workspace_size")
+    ws = workspace("dense_attention", need.value, dev)
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = ws.numel()
+    check(_lib.lib().imi_sparse_attention(ctypes.byref(a), _stream(dev)), "imi_sparse_attention")
+    return out

@@ -207,9 +207,9 @@ int imi_sparse_attention(const imi_attention_args* a, imi_stream_t stream);
 
 /* One decode step of one layer (retrieval.py:320-602, tile mode off):
  * imi_select followed by the gather + attention kernel on the same stream.
- * The selection outputs (and a per-row location table) live in
- * attn.workspace, which must be zero-filled before its first use; every call
- * leaves it reusable.  Calls that share a workspace must not overlap.
+ * The selection outputs and the split partials live in attn.workspace,
+ * which must be zero-filled before its first use; every call leaves it
+ * reusable.  Calls that share a workspace must not overlap.
  * phases: 0 or 3 = both halves; 1 = selection only; 2 = attention only
  * (reads the selection the previous phase-1 call left in the workspace). */
 typedef struct {

@@ -1,0 +1,185 @@
+"""The reference-named drop-in: adpimi_cache + imi_decode_attn.
+
+CPU tests check the cache contract (sizes, errors, static_len rule, reuse
+rules) against the reference formulas (cache.py:133-153, 380-395;
+attn_hub/sparse_imi.py:1-10).  GPU tests run a small model-shaped prefill and
+decode through the cache exactly as model_hub does (prefill_update_kv_cache
+per layer, prepare_cache, decode_update_kv_cache + imi_decode_attn per layer)
+and compare every layer with the oracle: selected cells bit-exact, output
+within 2e-2 abs + 1e-2 rel of fp64 attention."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import gpu_available
+
+DEV = "cuda:0"
+
+
+def _cache(layer_mapping=None, **kw):
+    from adaptiveimi_amd.cache_hub.adaptive_imi import adpimi_cache
+
+    args = dict(valid_start=[0], layer_num=2, batch_size=1, max_length=6100, num_key_value_heads=8, num_heads=32,
+                head_dim=128, dtype=torch.bfloat16, layer_mapping=layer_mapping or {"0": "cpu", "1": "cpu"},
+                max_new_length=4, input_length=6096, static_pattern_start=32, static_pattern_end=64, core=4,
+                pages_per_cluster=2, retrieval_budget=0.1, cache_ratio=0.05, buffer_cluster_num=32, prefill_bsz=1,
+                num_gpus=1, model_size=8, subspace_parts=2,
+                runtime_config={"kmeans": {"k1": 32, "k2": 32, "max_iters": 6, "early_stop_min_iter": 6}})
+    args.update(kw)
+    return adpimi_cache(**args)
+
+
+def test_cache_sizes_follow_reference():
+    c = _cache()
+    # cache.py:133-153 with input 6096, max_length 6100, max_new_length 4
+    assert c.input_length == 6096 and c.capacity_input_length == 6096
+    assert c.list_capacity == 6096 - 96 and c.list_stride == 6000
+    assert c.static_capacity == 96 + 3 and c.static_stride == 99
+    assert c.build_index_when_prefilling
+    assert c.static_pattern_total == 96 and c.group_size == 4 and c.batch_groups == 8
+    assert tuple(c.steady_zone_keys[0].shape) == (1, 8, 99, 128)
+    assert c.attn_func == c.dense_attention
+
+
+def test_cache_rejects_what_the_reference_rejects():
+    with pytest.raises(ValueError, match="batch_size=1"):
+        _cache(batch_size=2)
+    with pytest.raises(ValueError, match="subspace_parts"):
+        _cache(subspace_parts=3)
+    with pytest.raises(ValueError, match="input length"):
+        _cache(input_length=0)
+    with pytest.raises(NotImplementedError, match="IVF"):
+        _cache(subspace_parts=0)
+
+
+def test_async_update_warns():
+    with pytest.warns(RuntimeWarning, match="async_update"):
+        _cache(runtime_config={"async_update": {"enabled": True}})
+
+
+def test_static_len_rule():
+    from adaptiveimi_amd.attn_hub.sparse_imi import imi_decode_attn
+
+    class Stub:
+        static_pattern_total = 100
+        layer_num = 3
+
+        def attn_func(self, q, layer_idx, static_len):
+            return (layer_idx, static_len, q.is_contiguous())
+
+    q = torch.zeros(1, 4, 1, 8).transpose(1, 2)   # non-contiguous [1, 1, 4, 8]
+    assert imi_decode_attn(q, None, None, 0, Stub()) == (0, 101, True)
+    assert imi_decode_attn(q, None, None, 2, Stub()) == (2, 100, True)
+
+
+def test_reuse_rules():
+    c = _cache()
+    assert c.can_reuse_for_next_sequence([0], 4, 6096)
+    assert not c.can_reuse_for_next_sequence([0], 4, 7000)       # list too long
+    assert not c.can_reuse_for_next_sequence([0], 10, 6096)      # steady zone too short
+    assert not c.can_reuse_for_next_sequence([0, 0], 4, 6096)
+    c.reset_for_next_sequence([0], 3, 5000)
+    assert c.context == 0 and c.list_stride == 5000 - 96 and c.attn_func == c.dense_attention
+    with pytest.raises(ValueError, match="cannot reuse"):
+        c.reset_for_next_sequence([0], 4, 9000)
+
+
+def test_index_stats_before_build():
+    s = _cache().get_index_stats()
+    assert s["ready_layers"] == 0 and s["non_empty_clusters_total"] == 0
+    assert s["total_heads"] == 16 and math.isclose(s["ideal_clusters_per_head"], 6000 / 16)
+
+
+# ----------------------------------------------------------------- GPU --
+
+def _bits(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a HIP device")
+def test_model_shaped_prefill_and_decode_match_oracle():
+    from adaptiveimi_amd import synthetic
+    from adaptiveimi_amd.attn_hub.sparse_imi import imi_decode_attn
+    from oracle import oracle as orc
+
+    print("[dropin] 2 layers, S=6096, ks=(32,32), 2 decode steps", flush=True)
+    L, S, H, G, D = 2, 6096, 8, 4, 128
+    cache = _cache(layer_mapping={"0": DEV, "1": DEV})
+    kv = []
+    for layer in range(L):
+        k, v = synthetic.make_kv(H, S + 2, seed=40 + layer)
+        kv.append((k, v))
+        ks = k[:, :S].transpose(0, 1).unsqueeze(0).contiguous().to(DEV)   # [1, S, H, D]
+        vs = v[:, :S].transpose(0, 1).unsqueeze(0).contiguous().to(DEV)
+        rk, rv = cache.prefill_update_kv_cache(None, ks, vs, layer, 0)
+        assert rk.shape == ks.shape
+        cache.sync(layer, 0)
+    assert cache.context == S and cache.attn_func == cache.sparse_attention
+    cache.prepare_cache()
+    assert cache.nprobe == round(1024 * 0.1) and cache.max_retrieval_tokens == int(0.1 * 6000)
+
+    # oracle index of each layer
+    heads_by_layer = []
+    for layer in range(L):
+        k, v = kv[layer]
+        mid_k, mid_v = _bits(k[:, 32:S - 64]), _bits(v[:, 32:S - 64])
+        heads = []
+        for h in range(H):
+            labs, cents, _ = orc.kmeans_head(orc.bf16_to_f32(mid_k[h]), [32, 32], 6, early_stop_min_iter=6)
+            r = orc.compact_reorg(labs, [32, 32])
+            assert np.array_equal(cache.token_perm[layer][h].cpu().numpy(), r["perm"]), "cell order differs"
+            heads.append(dict(n_active=r["n_active"], offsets=r["offsets"],
+                              merged=orc.merged_centroids(cents, r["gids"], [32, 32]),
+                              list_keys=mid_k[h][r["perm"]], list_values=mid_v[h][r["perm"]]))
+        heads_by_layer.append(heads)
+
+    for step in range(2):
+        for layer in range(L):
+            k, v = kv[layer]
+            nk = k[:, S + step].reshape(1, 1, H, D).to(DEV)
+            nv = v[:, S + step].reshape(1, 1, H, D).to(DEV)
+            cache.decode_update_kv_cache(nk, nv, layer)
+            q = synthetic.make_queries(k[:, :S], G, seed=10 * step + layer)[0]      # [H, G, D]
+            qs = q.reshape(1, 1, H * G, D).to(DEV)
+            out = imi_decode_attn(qs, nk, nv, layer, cache)
+            assert tuple(out.shape) == (1, 1, H * G, D)
+            static_len = cache.static_pattern_total + (1 if layer < L - 1 else 0)
+            sk = _bits(cache.steady_zone_keys[layer][0])
+            sv = _bits(cache.steady_zone_values[layer][0])
+            ref, _, rm, _ = orc.decode_step(_bits(q), heads_by_layer[layer], sk, sv, static_len,
+                                            cache.n_centroids, cache.nprobe, cache.max_retrieval_tokens,
+                                            cache.buffer_size)
+            plan = cache._plans[layer]
+            assert np.array_equal(plan.selection["n_selected"].cpu().numpy(), rm), "selected cell counts differ"
+            got = out.float().cpu().numpy().reshape(H, G, D)
+            err = np.abs(got - ref)
+            assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)), f"layer {layer} step {step}: max err {err.max()}"
+    assert cache.static_pattern_total == 96 + 2
+    stats = cache.get_index_stats()
+    assert stats["ready_layers"] == 2 and stats["non_empty_clusters_total"] > 0
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a HIP device")
+def test_dense_attention_before_index():
+    """runtime.py:393-402: before the last layer's prefill the cache attends
+    the steady zone only."""
+    print("[dropin] dense attention over the steady zone", flush=True)
+    from adaptiveimi_amd import synthetic
+    from oracle import oracle as orc
+
+    cache = _cache(layer_mapping={"0": DEV, "1": DEV})
+    k, v = synthetic.make_kv(8, 99, seed=3)
+    cache.steady_zone_keys[0][0].copy_(k.to(DEV))
+    cache.steady_zone_values[0][0].copy_(v.to(DEV))
+    q = synthetic.make_queries(k, 4, seed=1)[0]
+    for static_len in (1, 57, 99):
+        out = cache.attn_func(q.reshape(1, 1, 32, 128).to(DEV), 0, static_len)
+        rows = [np.arange(static_len)] * 8
+        ref = orc.attention(_bits(q), _bits(k), _bits(v), rows)
+        got = out.float().cpu().numpy().reshape(8, 4, 128)
+        err = np.abs(got - ref)
+        assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)), f"static_len {static_len}: {err.max()}"
