@@ -12,11 +12,13 @@
 // head (b + b / H) % H, so consecutive workgroups (which the dispatcher deals
 // round robin to the 8 XCDs) rotate over the heads and every XCD gets a
 // share of every head's rows.  A wave owns NT tiles of 16 consecutive rows
-// and keeps two tiles in flight ahead of the one it computes.
+// and keeps two tiles in flight ahead of the one it computes.  Rows are read
+// whole (16 lanes x 16 bytes per 256-byte row) and staged through LDS, which
+// hands K back in the MFMA operand layout and V transposed.
 //
 // Per tile, on the matrix cores:
-//   S = K Q^T   4 x v_mfma_f32_16x16x32_bf16: A = the K tile (lane -> token
-//               lane % 16, 8 dims per lane), B = Q with column n holding
+//   S = K Q^T   4 x v_mfma_f32_16x16x32_bf16: A = the K tile read back from
+//               LDS (lane -> token lane % 16, 8 dims), B = Q with column n holding
 //               query n % G; lane l gets S[token 4(l/16)+i][query (l%16)%G].
 //   O += P V    8 x v_mfma_f32_16x16x16_bf16: A = P, which is exactly the S
 //               layout above (row = query slot, k = token) after exp2 and a
@@ -94,6 +96,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     __shared__ int s_pre[kSelCapMax + 1];
     __shared__ int s_off[kSelCapMax];
     __shared__ __attribute__((aligned(16))) uint16_t s_v[kWaves][16 * kVStride];
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[kWaves][16 * kVStride];
 
     const int b = blockIdx.x;
     const int split = b / a.H;
@@ -163,23 +166,24 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     for (int d = 0; d < 8; ++d) acc[d] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     float m_own = -INFINITY, l_own = 0.0f;   // softmax state of query slot ln
     uint16_t* sv = s_v[wave];
+    uint16_t* sk = s_k[wave];
 
     if (row0 < N) {
-        // Tile t: lane loads token t*16 + ln (16 bytes at dims 32c + 8lg).
-        // Rows past N read list row 0 (in bounds) and are masked below.
+        // Tile t, load it: rows t*16 + 4it + rg, 16 lanes x 16 bytes per row
+        // (whole 256-byte rows per 16 lanes).  Rows past N read list row 0
+        // (in bounds) and are masked below.
+        const int rg = lane >> 4, li = lane & 15;
         u32x4_t kb[2][4], vb[2][4];
         auto load = [&](int t, int slot) {
-            const int jt = t * 16 + ln;
-            const int n = row0 + jt;
-            const int lr = __shfl(loc[(t * 16) >> 6], jt & 63);
-            const bool st = n < a.static_len;
-            const int64_t roff = (st ? static_cast<int64_t>(n) : static_cast<int64_t>(n < N ? lr : 0)) * 128;
-            const uint16_t* kp = (st ? skh : lkh) + roff + lg * 8;
-            const uint16_t* vp = (st ? svh : lvh) + roff + lg * 8;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                kb[slot][c] = *reinterpret_cast<const u32x4_t*>(kp + c * 32);
-                vb[slot][c] = *reinterpret_cast<const u32x4_t*>(vp + c * 32);
+            for (int it = 0; it < 4; ++it) {
+                const int jt = t * 16 + it * 4 + rg;
+                const int n = row0 + jt;
+                const int lr = __shfl(loc[(t * 16) >> 6], jt & 63);
+                const bool st = n < a.static_len;
+                const int64_t roff = (st ? static_cast<int64_t>(n) : static_cast<int64_t>(n < N ? lr : 0)) * 128;
+                kb[slot][it] = *reinterpret_cast<const u32x4_t*>((st ? skh : lkh) + roff + li * 8);
+                vb[slot][it] = *reinterpret_cast<const u32x4_t*>((st ? svh : lvh) + roff + li * 8);
             }
         };
         load(0, 0);
@@ -187,14 +191,20 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const int slot = t & 1;
-            // V tile -> LDS, row-major [token][dim]
+            // K and V tiles -> LDS, row-major [token][dim]; K comes back in
+            // the MFMA A layout (lane -> token ln, dims 32c + 8lg)
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                *reinterpret_cast<u32x4_t*>(sv + ln * kVStride + c * 32 + lg * 8) = vb[slot][c];
+            for (int it = 0; it < 4; ++it) {
+                *reinterpret_cast<u32x4_t*>(sv + (4 * it + rg) * kVStride + li * 8) = vb[slot][it];
+                *reinterpret_cast<u32x4_t*>(sk + (4 * it + rg) * kVStride + li * 8) = kb[slot][it];
+            }
+            u32x4_t ka[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) ka[c] = *reinterpret_cast<const u32x4_t*>(sk + ln * kVStride + c * 32 + lg * 8);
             f32x4_t s4 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-                s4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kb[slot][c]),
+                s4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka[c]),
                                                              __builtin_bit_cast(bf16x8_t, qb[c]), s4, 0, 0, 0);
             if (t + 2 < NT) load(t + 2, slot);
             float s[4];
