@@ -35,6 +35,7 @@ _KMEANS_DEFAULTS = {  # LayerPipelineRuntimeConfig defaults (layer_pipeline.hpp:
     "early_stop_min_iter": 5,
     "early_stop_rel_tol": 5e-4,
     "target_cluster_size": 16,
+    "init": "kmeans++",   # kmeans_plusplus_init_inplace, as the reference; "first" = first k rows
 }
 
 
@@ -185,11 +186,11 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         cfg = self.runtime_config["kmeans"]
         H, T, D = middle_k.shape
         ks = self._layer_ks(T)
-        if T < max(ks):
+        if T < max(ks) and cfg["init"] == "first":
             raise ValueError(f"IMI layer {layer_idx}: {T} middle tokens < k = {max(ks)} (first-k initialisation)")
         cent, labels, _ = ops.kmeans(middle_k, ks, int(cfg["max_iters"]), tol=float(cfg["tol"]),
                                      early_stop_min_iter=int(cfg["early_stop_min_iter"]),
-                                     early_stop_rel_tol=float(cfg["early_stop_rel_tol"]))
+                                     early_stop_rel_tol=float(cfg["early_stop_rel_tol"]), init=str(cfg["init"]))
         dev = middle_k.device
         rows = max(self.list_capacity, T)
         lk = torch.empty((1, H, rows, D), dtype=middle_k.dtype, device=dev)

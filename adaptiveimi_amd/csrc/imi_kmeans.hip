@@ -15,6 +15,7 @@
 // M-step's member lists come from one scan + one scatter, and the M-step sums
 // each cluster sequentially in ascending token order (the reference's order
 // with one thread per subspace run).
+#include <limits>
 #include <random>
 #include <vector>
 
@@ -152,6 +153,154 @@ __global__ __launch_bounds__(256) void km_assign_kernel(KmParams a) {
                                    a.hist + static_cast<int64_t>(seg) * a.kmax * a.nblk, a.nblk, blk);
     if (valid) a.rank[static_cast<int64_t>(seg) * a.T + t] = r;
     if (tid == 0) a.ipart[static_cast<int64_t>(seg) * a.nblk + blk] = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// ---------------------------------------------------------------- kmeans++
+// kmeans_plusplus_init_inplace (kmeans_core.cpp:138-186), one workgroup per
+// (head, subspace).  The random draws do not depend on the data: the host
+// replays std::mt19937_64(seed) for the first index
+// (uniform_int_distribution<int32_t>(0, T-1)) and for one
+// generate_canonical<double, 53> per pick, which is what
+// uniform_real_distribution<double>(0, total) consumes; target = canon *
+// total.  min_dists are updated with the reference distance.  The reference
+// sums them sequentially in double (total, then the running sum that picks
+// the first index with cumsum >= target).  When every value is a multiple
+// of the smallest value's ulp and the total stays below 2^53 such units (the
+// exponent spread is checked per pick), no partial sum rounds, so the
+// sequential doubles equal exact integer prefix sums, computed here with a
+// block scan; otherwise one thread replays the sequential loops.
+struct PpDraws {
+    int32_t first;
+    int32_t pad;
+    double canon[256];   // canon[c] for pick c (index 0 unused)
+};
+
+__device__ __forceinline__ long long pp_units(float m, int emin_eff) {
+    const uint32_t u = __float_as_uint(m);
+    const int e = static_cast<int>((u >> 23) & 0xFFu);
+    const long long mant = static_cast<long long>(u & 0x7FFFFFu) | (e > 0 ? (1ll << 23) : 0ll);
+    const int e_eff = e > 0 ? e : 1;
+    return mant << (e_eff - emin_eff);
+}
+
+template <int DP>
+constexpr int pp_threads() { return DP == 64 ? 512 : 1024; }   // keeps x[DP] in registers
+
+template <int DP>
+__global__ __launch_bounds__(pp_threads<DP>()) void km_pp_kernel(KmParams a, int p, PpDraws dr) {
+    constexpr int TPB = pp_threads<DP>();
+    constexpr int NW = TPB / 64;
+    __shared__ __attribute__((aligned(16))) float cur[DP];
+    __shared__ int s_emin, s_emax, s_sel;
+    __shared__ long long s_part[NW];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int seg = h * a.P + p;
+    const int T = a.T, k = a.k[p];
+    float* md = reinterpret_cast<float*>(a.rank) + static_cast<int64_t>(seg) * T;
+    float* cent = a.cent + static_cast<int64_t>(seg) * a.kmax * DP;
+    const uint16_t* xb = a.keys + static_cast<int64_t>(h) * a.hs + p * DP;
+    if (tid < DP) {
+        const float v = bf16_to_f32(xb[static_cast<int64_t>(dr.first) * a.ts + tid]);
+        cur[tid] = v;
+        cent[tid] = v;
+    }
+    for (int i = tid; i < T; i += TPB) md[i] = 3.402823466e38f;
+    const int chunk = (T + TPB - 1) / TPB;
+    const int i0 = tid * chunk, i1 = min(T, i0 + chunk);
+    int logT = 0;
+    while ((1ll << logT) < static_cast<long long>(T)) ++logT;
+    for (int c = 1; c < k; ++c) {
+        if (tid == 0) {
+            s_emin = 0x7FFFFFFF;
+            s_emax = 0;
+            s_sel = T;
+        }
+        __syncthreads();   // cur, md and the LDS scalars are ready
+        int emin = 0x7FFFFFFF, emax = 0;
+        for (int i = tid; i < T; i += TPB) {
+            float x[DP];
+            const uint16_t* row = xb + static_cast<int64_t>(i) * a.ts;
+#pragma unroll
+            for (int d = 0; d < DP; d += 8) {
+                const uint4 v = *reinterpret_cast<const uint4*>(row + d);
+                x[d + 0] = bf16_lo(v.x); x[d + 1] = bf16_hi(v.x);
+                x[d + 2] = bf16_lo(v.y); x[d + 3] = bf16_hi(v.y);
+                x[d + 4] = bf16_lo(v.z); x[d + 5] = bf16_hi(v.z);
+                x[d + 6] = bf16_lo(v.w); x[d + 7] = bf16_hi(v.w);
+            }
+            const float dist = l2_lanes8<DP>(x, cur);
+            float m = md[i];
+            if (dist < m) {
+                m = dist;
+                md[i] = m;
+            }
+            if (m > 0.0f) {
+                const int e = static_cast<int>((__float_as_uint(m) >> 23) & 0xFFu);
+                const int ee = e > 0 ? e : 1;
+                emin = min(emin, ee);
+                emax = max(emax, ee);
+            }
+        }
+        if (emin != 0x7FFFFFFF) atomicMin(&s_emin, emin);
+        if (emax != 0) atomicMax(&s_emax, emax);
+        __syncthreads();   // md complete, exponent range known
+        const int e_lo = s_emin, e_hi = s_emax;
+        const bool any = e_lo != 0x7FFFFFFF;
+        const bool exact = !any || (e_hi - e_lo) + 24 + logT <= 53;
+        if (exact) {
+            const int emin_eff = any ? e_lo : 1;
+            long long sum = 0;
+            for (int i = i0; i < i1; ++i) sum += pp_units(md[i], emin_eff);
+            // block exclusive scan of the chunk sums (thread order = index order)
+            long long incl = sum;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const long long y = __shfl_up(incl, o);
+                if (lane_id() >= o) incl += y;
+            }
+            const int w = tid >> 6;
+            if (lane_id() == 63) s_part[w] = incl;
+            __syncthreads();
+            long long base = 0, total_u = 0;
+            for (int j = 0; j < NW; ++j) {
+                if (j < w) base += s_part[j];
+                total_u += s_part[j];
+            }
+            const double scale = ldexp(1.0, emin_eff - 150);
+            const double total = static_cast<double>(total_u) * scale;
+            const double target = dr.canon[c] * total + 0.0;
+            const double tu = target / scale;
+            long long run = base + incl - sum;
+            for (int i = i0; i < i1; ++i) {
+                run += pp_units(md[i], emin_eff);
+                if (static_cast<double>(run) >= tu) {
+                    atomicMin(&s_sel, i);
+                    break;
+                }
+            }
+        } else if (tid == 0) {
+            double tw = 0.0;
+            for (int i = 0; i < T; ++i) tw += static_cast<double>(md[i]);
+            const double target = dr.canon[c] * tw + 0.0;
+            double cs = 0.0;
+            int sel = 0;
+            for (int i = 0; i < T; ++i) {
+                cs += static_cast<double>(md[i]);
+                if (cs >= target) {
+                    sel = i;
+                    break;
+                }
+            }
+            s_sel = sel;
+        }
+        __syncthreads();   // selection known; every read of cur is done
+        if (tid < DP) {   // wave 0 only: tid 0 resets s_sel after these reads
+            const int sel = s_sel < T ? s_sel : 0;
+            const float v = bf16_to_f32(xb[static_cast<int64_t>(sel) * a.ts + tid]);
+            cur[tid] = v;
+            cent[static_cast<int64_t>(c) * DP + tid] = v;
+        }
+    }
 }
 
 // Per segment: exclusive scan of the [label][block] counts, cluster offsets,
@@ -351,6 +500,8 @@ int validate(const imi_kmeans_args* a, int& kmax, int& dp) {
                     a->k[p]);
         kmax = a->k[p] > kmax ? a->k[p] : kmax;
     }
+    IMI_REQUIRE(a->init_mode >= 0 && a->init_mode <= 2, IMI_ERR_INVALID,
+                "imi_kmeans: init_mode %d (0 first-k, 1 given, 2 kmeans++)", a->init_mode);
     if (a->init_mode == 0)
         IMI_REQUIRE(kmax <= a->n_tokens, IMI_ERR_INVALID,
                     "imi_kmeans: first-k initialisation needs n_tokens (%d) >= k (%d)", a->n_tokens, kmax);
@@ -447,6 +598,22 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
     if (a->init_mode == 0) {
         hipLaunchKernelGGL(km_init_first_kernel, dim3(kmax, segs), dim3(64), 0, stream, p);
         IMI_LAUNCH_CHECK("km_init_first_kernel");
+    } else if (a->init_mode == 2) {
+        // kmeans++ seeds 42, 43, 44, 45 by subspace, the same for every head
+        // (kmeans_core.cpp:459, 469)
+        for (int part = 0; part < a->parts; ++part) {
+            PpDraws dr{};
+            std::mt19937_64 rng(static_cast<uint64_t>(42 + part));
+            std::uniform_int_distribution<int32_t> first(0, a->n_tokens - 1);
+            dr.first = first(rng);
+            for (int c = 1; c < a->k[part]; ++c)
+                dr.canon[c] = std::generate_canonical<double, std::numeric_limits<double>::digits>(rng);
+            if (dp == 64)
+                hipLaunchKernelGGL(km_pp_kernel<64>, dim3(a->kv_heads), dim3(pp_threads<64>()), 0, stream, p, part, dr);
+            else
+                hipLaunchKernelGGL(km_pp_kernel<32>, dim3(a->kv_heads), dim3(pp_threads<32>()), 0, stream, p, part, dr);
+            IMI_LAUNCH_CHECK("km_pp_kernel");
+        }
     }
     for (int it = 0; it < a->max_iters; ++it) {
         rc = dp == 64 ? run_assign<64>(p, segs, stream) : run_assign<32>(p, segs, stream);

@@ -70,10 +70,16 @@ def _head_token_strides(x: torch.Tensor) -> Tuple[int, int]:
 
 # ----------------------------------------------------------------- k-means --
 
+_INIT_MODES = {"first": 0, "kmeans++": 2}
+
+
 def kmeans(keys: torch.Tensor, ks: Sequence[int], max_iters: int, tol: float = 5e-4,
            early_stop_min_iter: Optional[int] = None, early_stop_rel_tol: float = 5e-4,
-           init_centroids: Optional[torch.Tensor] = None):
+           init_centroids: Optional[torch.Tensor] = None, init: str = "first"):
     """Per-(head, subspace) Lloyd k-means (kmeans_core.cpp:384-501).
+    init: 'first' (first k rows of each subspace), 'kmeans++' (the
+    reference's kmeans_plusplus_init_inplace, seeds 42 + subspace) or, when
+    init_centroids is given, those centroids.
     keys: bf16 [H, T, D] view.  Returns (centroids f32 [H, P, kmax, D/P],
     labels i32 [H, P, T], iters i32 [H, P])."""
     dev = _require_device(keys, init_centroids)
@@ -93,7 +99,8 @@ def kmeans(keys: torch.Tensor, ks: Sequence[int], max_iters: int, tol: float = 5
     a = KmeansArgs(keys=keys.data_ptr(), head_stride=hs, token_stride=ts, kv_heads=H, n_tokens=T, dim=D,
                    parts=P, k=_ks(ks), max_iters=int(max_iters), tol=float(tol),
                    early_stop_min_iter=int(max_iters + 1 if early_stop_min_iter is None else early_stop_min_iter),
-                   early_stop_rel_tol=float(early_stop_rel_tol), init_mode=0 if init_centroids is None else 1,
+                   early_stop_rel_tol=float(early_stop_rel_tol),
+                   init_mode=1 if init_centroids is not None else _INIT_MODES[init],
                    centroids=cent.data_ptr(), labels=labels.data_ptr(), iters_run=iters.data_ptr())
     need = ctypes.c_size_t()
     check(_lib.lib().imi_kmeans_workspace_size(ctypes.byref(a), ctypes.byref(need)), "imi_kmeans_workspace_size")

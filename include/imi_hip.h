@@ -72,7 +72,9 @@ typedef struct {
     int32_t early_stop_min_iter; /* early stop disabled when > max_iters */
     float early_stop_rel_tol;
     int32_t init_mode;        /* 0: first k rows of each subspace;
-                                 1: centroids already hold the initial values */
+                                 1: centroids already hold the initial values;
+                                 2: kmeans++ (kmeans_core.cpp:138-186, seeds
+                                    42 + subspace, same for every head) */
     float* centroids;         /* device [H][P][kmax][Dp] in/out */
     int32_t* labels;          /* device [H][P][T] out (last E-step) */
     int32_t* iters_run;       /* device [H][P] out (E-steps executed), may be NULL */

@@ -26,7 +26,8 @@ def _cache(layer_mapping=None, **kw):
                 max_new_length=4, input_length=6096, static_pattern_start=32, static_pattern_end=64, core=4,
                 pages_per_cluster=2, retrieval_budget=0.1, cache_ratio=0.05, buffer_cluster_num=32, prefill_bsz=1,
                 num_gpus=1, model_size=8, subspace_parts=2,
-                runtime_config={"kmeans": {"k1": 32, "k2": 32, "max_iters": 6, "early_stop_min_iter": 6}})
+                runtime_config={"kmeans": {"k1": 32, "k2": 32, "max_iters": 6, "early_stop_min_iter": 6,
+                                            "init": "first"}})
     args.update(kw)
     return adpimi_cache(**args)
 

@@ -84,6 +84,62 @@ def test_kmeans_full_run_bit_exact(ops, oracle, T, k, iters):
             assert np.array_equal(cent[h, p], cents[p]), (h, p)
 
 
+@pytest.mark.parametrize("T,ks,iters", [(3000, (32, 32), 4), (2049, (16, 16, 16, 16), 3), (700, (64, 64), 2)])
+def test_kmeans_plusplus_bit_exact(ops, oracle, T, ks, iters):
+    """kmeans++ initialisation (kmeans_core.cpp:138-186, seeds 42 + subspace):
+    the GPU picks the same rows as the oracle, which runs the reference's
+    sequential double sums with std::mt19937_64, so centroids and labels
+    after the Lloyd iterations are identical."""
+    note(f"[kmeans++] T={T} ks={ks} iters={iters}")
+    H = 3
+    keys, _ = _kv(H, T, seed=21 + T)
+    cent, labels, _ = ops.kmeans(keys.to(DEV), list(ks), iters, init="kmeans++")
+    cent, labels = cent.cpu().numpy(), labels.cpu().numpy()
+    kf = oracle.bf16_to_f32(bits(keys))
+    for h in range(H):
+        labs, cents, _ = oracle.kmeans_head(kf[h], list(ks), iters, init="kmeans++")
+        for p in range(len(ks)):
+            assert np.array_equal(cent[h, p, :ks[p]], cents[p]), (h, p)
+            assert np.array_equal(labels[h, p], labs[p]), (h, p)
+
+
+def test_kmeans_plusplus_init_only_with_duplicates(ops, oracle):
+    """Initial centroids alone (one Lloyd iteration is compared through its
+    labels) on data with many duplicate rows, so min distances of 0 occur and
+    picks can repeat."""
+    note("[kmeans++] duplicates")
+    H, T, k = 2, 1200, 32
+    keys, _ = _kv(H, T, seed=5)
+    keys[:, 600:] = keys[:, :600]
+    cent, labels, _ = ops.kmeans(keys.to(DEV), [k, k], 1, init="kmeans++")
+    kf = oracle.bf16_to_f32(bits(keys))
+    for h in range(H):
+        labs, cents, _ = oracle.kmeans_head(kf[h], [k, k], 1, init="kmeans++")
+        for p in range(2):
+            assert np.array_equal(labels.cpu().numpy()[h, p], labs[p]), (h, p)
+            assert np.array_equal(cent.cpu().numpy()[h, p], cents[p]), (h, p)
+
+
+def test_kmeans_plusplus_wide_range_sequential_path(ops, oracle):
+    """Min distances spanning more than 53 bits (near-duplicate rows next
+    to far outliers): the per-pick exactness test fails and the kernel
+    replays the reference's sequential double sums; the picks still match."""
+    note("[kmeans++] wide exponent range")
+    H, T, k = 1, 2048, 16
+    rng = np.random.default_rng(9)
+    base = rng.integers(-4, 5, size=(T, 128)).astype(np.float32)
+    base[1::2] = base[0::2]
+    base[1::2, 0] += 1.0 / 64        # neighbours one small step apart
+    base[::97] *= 256.0              # far outliers
+    keys = torch.from_numpy(base).to(torch.bfloat16).unsqueeze(0).contiguous()
+    cent, labels, _ = ops.kmeans(keys.to(DEV), [k, k], 2, init="kmeans++")
+    kf = oracle.bf16_to_f32(bits(keys))
+    labs, cents, _ = oracle.kmeans_head(kf[0], [k, k], 2, init="kmeans++")
+    for p in range(2):
+        assert np.array_equal(cent.cpu().numpy()[0, p], cents[p]), p
+        assert np.array_equal(labels.cpu().numpy()[0, p], labs[p]), p
+
+
 def test_kmeans_empty_cluster_reseed(ops, oracle):
     """Duplicate first rows make clusters empty in iteration 0; the GPU must
     re-seed them from the same mt19937 draws as the reference."""
