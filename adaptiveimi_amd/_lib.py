@@ -50,6 +50,8 @@ class SelectArgs(ctypes.Structure):
         ("k", _i32 * 4), ("nprobe", _i32), ("max_tokens", _i32), ("buffer_pages", _i32), ("page_size", _i32),
         ("sel_cell", _vp), ("sel_offset", _vp), ("sel_count", _vp), ("sel_prefix", _vp),
         ("n_selected", _vp), ("n_rows", _vp), ("sel_cap", _i32),
+        ("compact_gid", _vp), ("compact_size", _vp), ("compact_offset", _vp), ("n_active", _vp),
+        ("compact_cap", _i32), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -77,6 +79,7 @@ EXPORTS = {
     "imi_index_workspace_size": (ctypes.c_int, [ctypes.POINTER(IndexArgs), ctypes.POINTER(ctypes.c_size_t)]),
     "imi_build_index": (ctypes.c_int, [ctypes.POINTER(IndexArgs), _vp]),
     "imi_fused_query_group_similarities": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp]),
+    "imi_select_workspace_size": (ctypes.c_int, [ctypes.POINTER(SelectArgs), ctypes.POINTER(ctypes.c_size_t)]),
     "imi_select": (ctypes.c_int, [ctypes.POINTER(SelectArgs), _vp]),
     "imi_attention_workspace_size": (ctypes.c_int, [ctypes.POINTER(AttentionArgs), ctypes.POINTER(ctypes.c_size_t)]),
     "imi_sparse_attention": (ctypes.c_int, [ctypes.POINTER(AttentionArgs), _vp]),

@@ -163,6 +163,8 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         self.cell_count: List[Optional[torch.Tensor]] = [None] * layer_num     # [H, ncells]
         self.cell_offset: List[Optional[torch.Tensor]] = [None] * layer_num    # [H, ncells + 1]
         self.token_perm: List[Optional[torch.Tensor]] = [None] * layer_num     # [H, T] list row -> token
+        # 4-way only: the occupied cells in cell order (n_active, gid, size, offset)
+        self.compact_cells: List[Optional[Dict[str, torch.Tensor]]] = [None] * layer_num
         self.list_keys: List[Optional[torch.Tensor]] = [None] * layer_num      # [1, H, list_capacity, D]
         self.list_values: List[Optional[torch.Tensor]] = [None] * layer_num
         self._plans: List[Optional[ops.DecodePlan]] = [None] * layer_num
@@ -195,8 +197,15 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         rows = max(self.list_capacity, T)
         lk = torch.empty((1, H, rows, D), dtype=middle_k.dtype, device=dev)
         lv = torch.empty_like(lk)
+        four_way = self.subspace_parts == 4
+        ncells = 1
+        for k in ks:
+            ncells *= int(k)
+        # 4-way scoring walks the occupied cells only (at most min(T, k^4) of them)
         idx = ops.build_index(middle_k, middle_v, cent, labels, ks, list_keys=lk[0], list_values=lv[0],
-                              compact=False)
+                              compact=four_way, merged=False, n_centroids=min(T, ncells) + 1)
+        self.compact_cells[layer_idx] = (
+            {n: idx[n] for n in ("n_active", "compact_gid", "compact_size", "compact_offset")} if four_way else None)
         self.layer_ks[layer_idx] = ks
         self.centroids[layer_idx] = cent
         self.cell_count[layer_idx] = idx["cell_count"]
@@ -262,9 +271,8 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         ks = next((k for k in self.layer_ks if k is not None), None)
         if ks is None:
             raise RuntimeError("prepare_cache: no layer index has been built")
-        if self.subspace_parts != 2:
-            raise NotImplementedError("decode selection over a 4-way IMI is not implemented on this path")
-        explicit = all(int(self.runtime_config["kmeans"].get(n, 0) or 0) > 0 for n in ("k1", "k2"))
+        names = ("k1", "k2") if self.subspace_parts == 2 else ("k1", "k2", "k3", "k4")
+        explicit = all(int(self.runtime_config["kmeans"].get(n, 0) or 0) > 0 for n in names)
         sz = decode_sizing(self.list_capacity, self.retrieval_budget, self.subspace_parts, self.buffer_cluster_num,
                            self.page_size, k_override=ks if explicit else None)
         self.n_centroids = sz["n_centroids"]
@@ -285,7 +293,8 @@ class adpimi_cache:  # noqa: N801  (reference class name)
             plan = ops.DecodePlan(self.centroids[layer_idx], self.cell_count[layer_idx], self.cell_offset[layer_idx],
                                   self.layer_ks[layer_idx], bud, self.list_keys[layer_idx][0],
                                   self.list_values[layer_idx][0], self.steady_zone_keys[layer_idx][0],
-                                  self.steady_zone_values[layer_idx][0], self.group_size)
+                                  self.steady_zone_values[layer_idx][0], self.group_size,
+                                  compact=self.compact_cells[layer_idx])
             self._plans[layer_idx] = plan
         return plan
 
@@ -391,6 +400,7 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         self.cell_count = [None] * n
         self.cell_offset = [None] * n
         self.token_perm = [None] * n
+        self.compact_cells = [None] * n
         self.list_keys = [None] * n
         self.list_values = [None] * n
         self.layer_ks = [None] * n

@@ -36,6 +36,7 @@ namespace imi {
 
 int select_launch(const imi_select_args* a, hipStream_t stream);
 int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax);
+size_t select4_workspace_size(const imi_select_args* a);
 
 namespace {
 
@@ -530,6 +531,8 @@ extern "C" int imi_sparse_attention(const imi_attention_args* a, imi_stream_t st
 namespace {
 struct DecodeLayout {
     int32_t *cell, *off, *cnt, *prefix, *nsel, *nrows;
+    char* sel_ws;            // 4-way selection scratch (empty for 2-way)
+    size_t sel_bytes;
     char* attn_ws;
     size_t attn_bytes;
     size_t total;
@@ -545,6 +548,8 @@ DecodeLayout decode_layout(const imi_decode_args* a, void* ws) {
     L.prefix = cv.take<int32_t>(static_cast<size_t>(H) * (cap + 1));
     L.nsel = cv.take<int32_t>(H);
     L.nrows = cv.take<int32_t>(H);
+    L.sel_bytes = a->sel.parts == 4 ? select4_workspace_size(&a->sel) : 0;
+    L.sel_ws = cv.take<char>(L.sel_bytes > 0 ? L.sel_bytes : 1);
     imi_attention_args t = a->attn;
     t.workspace = nullptr;
     L.attn_bytes = attn_workspace(&t, nullptr);
@@ -590,6 +595,10 @@ extern "C" int imi_decode_step(const imi_decode_args* a, imi_stream_t stream_) {
     if (!s.sel_prefix) s.sel_prefix = L.prefix;
     if (!s.n_selected) s.n_selected = L.nsel;
     if (!s.n_rows) s.n_rows = L.nrows;
+    if (s.parts == 4 && !s.workspace) {
+        s.workspace = L.sel_ws;
+        s.workspace_bytes = L.sel_bytes;
+    }
     if (phases & 1) {
         rc = select_launch(&s, stream);
         if (rc) return rc;

@@ -135,8 +135,9 @@ __global__ __launch_bounds__(256) void ix_compact_fill_kernel(IxParams a, Compac
         o.gid[hc] = static_cast<int32_t>(g);
         o.size[hc] = cnt;
         o.offset[static_cast<int64_t>(h) * (o.n_c + 1) + c] = offset[static_cast<int64_t>(h) * (a.ncells + 1) + g];
-        o.mask[hc] = 0;
+        if (o.mask) o.mask[hc] = 0;
     }
+    if (!o.merged) return;
     // merged centroid = [C_0[l0] | C_1[l1] | ...]
     int64_t rem = g;
     int lab[4] = {0, 0, 0, 0};
@@ -162,8 +163,9 @@ __global__ __launch_bounds__(256) void ix_compact_pad_kernel(IxParams a, Compact
     o.gid[hc] = -1;
     o.size[hc] = 0;
     o.offset[static_cast<int64_t>(h) * (o.n_c + 1) + c] = a.T;
-    o.mask[hc] = 1;
-    for (int d = 0; d < o.D; ++d) o.merged[hc * o.D + d] = 0.0f;
+    if (o.mask) o.mask[hc] = 1;
+    if (o.merged)
+        for (int d = 0; d < o.D; ++d) o.merged[hc * o.D + d] = 0.0f;
 }
 
 // list[h][pos] = src[h][perm[h][pos]] for keys and values; 16 lanes per
@@ -227,9 +229,10 @@ int validate(const imi_index_args* a, int& kmax, int64_t& ncells) {
     const bool compact = a->compact_gid || a->compact_size || a->compact_offset || a->compact_centroids ||
                          a->compact_mask || a->n_active;
     if (compact) {
-        IMI_REQUIRE(a->compact_gid && a->compact_size && a->compact_offset && a->compact_centroids &&
-                        a->compact_mask && a->n_active && a->centroids,
-                    IMI_ERR_INVALID, "imi_build_index: compact outputs must be all set or all NULL");
+        IMI_REQUIRE(a->compact_gid && a->compact_size && a->compact_offset && a->n_active, IMI_ERR_INVALID,
+                    "imi_build_index: compact gid, size, offset and n_active must be all set or all NULL");
+        IMI_REQUIRE(!a->compact_centroids || a->centroids, IMI_ERR_INVALID,
+                    "imi_build_index: merged compact centroids need the subspace centroids");
         const int64_t max_active = ncells < a->n_tokens ? ncells : a->n_tokens;
         IMI_REQUIRE(a->n_centroids >= max_active, IMI_ERR_INVALID,
                     "imi_build_index: n_centroids %d < possible occupied cells %lld", a->n_centroids,

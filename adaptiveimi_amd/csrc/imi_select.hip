@@ -488,6 +488,10 @@ __global__ __launch_bounds__(256) void similarity_kernel(const uint16_t* q, cons
 
 }  // namespace
 
+int select4_validate(const imi_select_args* a);
+size_t select4_workspace_size(const imi_select_args* a);
+int select4_launch(const imi_select_args* a, hipStream_t stream);
+
 int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     IMI_REQUIRE(a != nullptr, IMI_ERR_INVALID, "imi_select: null args");
     IMI_REQUIRE(a->query && a->centroids && a->cell_count && a->cell_offset, IMI_ERR_INVALID,
@@ -496,8 +500,19 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     IMI_REQUIRE(a->groups <= kMaxGroups, IMI_ERR_UNSUPPORTED, "imi_select: %d query heads per kv head exceed %d",
                 a->groups, kMaxGroups);
     IMI_REQUIRE(a->dim == 128, IMI_ERR_UNSUPPORTED, "imi_select: head_dim must be 128");
-    IMI_REQUIRE(a->parts == 2, IMI_ERR_UNSUPPORTED, "imi_select: only 2-way IMI is implemented (parts=%d)",
+    IMI_REQUIRE(a->parts == 2 || a->parts == 4, IMI_ERR_UNSUPPORTED, "imi_select: parts must be 2 or 4 (got %d)",
                 a->parts);
+    if (a->parts == 4) {
+        IMI_REQUIRE(a->page_size > 0 && a->nprobe > 0 && a->max_tokens > 0 && a->buffer_pages > 0, IMI_ERR_INVALID,
+                    "imi_select: budgets must be positive");
+        kmax = 0;
+        ncells = 1;
+        for (int p = 0; p < 4; ++p) {
+            kmax = a->k[p] > kmax ? a->k[p] : kmax;
+            ncells *= a->k[p];
+        }
+        return select4_validate(a);
+    }
     IMI_REQUIRE(a->page_size > 0 && a->nprobe > 0 && a->max_tokens > 0 && a->buffer_pages > 0, IMI_ERR_INVALID,
                 "imi_select: budgets must be positive");
     kmax = a->k[0] > a->k[1] ? a->k[0] : a->k[1];
@@ -537,6 +552,7 @@ int select_launch(const imi_select_args* a, hipStream_t stream) {
     if (rc) return rc;
     IMI_REQUIRE(a->sel_cell && a->sel_offset && a->sel_count && a->sel_prefix && a->n_selected && a->n_rows,
                 IMI_ERR_INVALID, "imi_select: null output pointer");
+    if (a->parts == 4) return select4_launch(a, stream);
     SelParams p;
     p.q = a->query;
     p.cent = a->centroids;
@@ -572,6 +588,17 @@ int select_launch(const imi_select_args* a, hipStream_t stream) {
 }  // namespace imi
 
 using namespace imi;
+
+extern "C" int imi_select_workspace_size(const imi_select_args* a, size_t* bytes) {
+    clear_error();
+    int64_t ncells;
+    int kmax;
+    int rc = select_validate(a, ncells, kmax);
+    if (rc) return rc;
+    IMI_REQUIRE(bytes != nullptr, IMI_ERR_INVALID, "imi_select_workspace_size: null output");
+    *bytes = a->parts == 4 ? select4_workspace_size(a) : 0;
+    return IMI_OK;
+}
 
 extern "C" int imi_select(const imi_select_args* a, imi_stream_t stream) {
     clear_error();

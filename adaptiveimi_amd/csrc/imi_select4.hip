@@ -1,0 +1,501 @@
+// Per-step cell scoring and budget-bounded selection for a 4-way IMI on gfx950.
+//
+// Reference: the same path as the 2-way selection (compute_impl.cu:62-103
+// scores over the padded compact cells, retrieval.py:295-303 and 357,
+// wave_buffer_cpu_hotcold.cpp:303-371), with n_centroids = k^4 + 1 cells
+// (runtime.py:35-38).  With k = 32 that is 1,048,576 cells, most of them
+// empty, so the work runs over the occupied (compact) cells that
+// imi_build_index lists in ascending global id:
+//
+//   sel4_score_kernel   one thread per occupied cell: qsum (g ascending) and
+//                       the 128-term FMA chain over [C0[l0] | C1[l1] | C2[l2]
+//                       | C3[l3]] (the merged centroid, never materialised);
+//                       key = (score, ~gid) so that key order is the reference
+//                       rank order; per-head score range
+//   sel4_hist_kernel    2048 linear buckets over the range
+//   sel4_gather_kernel  the bucket holding the K'-th best cell, where
+//                       K' = min(nprobe, buffer_pages, occupied cells);
+//                       every cell in or above it becomes a candidate
+//   sel4_final_kernel   one workgroup per head: bitonic sort of the
+//                       candidates (or, when more than 4096 cells share the
+//                       top buckets, an exact radix select of the K'-th key),
+//                       then the token and page budgets in rank order
+//
+// Outputs have the 2-way layout (cells in rank order, CSR offset, count,
+// exclusive row prefix, m, rows), so the gather kernel is shared.  The final
+// kernel zeroes the histogram and counters again for the next call.
+#include "imi_common.hpp"
+
+namespace imi {
+namespace {
+
+constexpr int kBins4 = 2048;
+constexpr int kCand4 = 4096;     // candidate capacity per head
+constexpr int kK4 = 64;          // centroids per subspace the kernels hold
+constexpr int kDp4 = 32;         // subspace width (D = 128, 4 parts)
+constexpr int kMaxG4 = 8;        // query heads per KV head
+constexpr int kScoreThreads = 256;
+constexpr int kFinalThreads = 1024;
+constexpr int kSelCap4 = 2048;   // min(nprobe, buffer_pages) bound
+
+struct Sel4 {
+    const uint16_t* q;
+    const float* cent;       // [H][4][kmax][32]
+    int H, G, kmax;
+    int k[4];
+    const int32_t* gid;      // [H][cap]
+    const int32_t* csize;    // [H][cap]
+    const int32_t* coff;     // [H][cap + 1]
+    const int32_t* nact;     // [H]
+    int cap;
+    int nprobe, max_tokens, buffer_pages, page_size;
+    int32_t* sel_cell;
+    int32_t* sel_offset;
+    int32_t* sel_count;
+    int32_t* sel_prefix;
+    int32_t* n_sel;
+    int32_t* n_rows;
+    int sel_cap;
+    uint64_t* keys;          // [H][cap]
+    uint32_t* hist;          // [H][kBins4]
+    uint32_t* ext;           // [H][4]: max order key, ~min order key, candidate count, unused
+    uint64_t* cand;          // [H][kCand4]
+    int32_t* cidx;           // [H][kCand4]
+};
+
+__device__ __forceinline__ float key_score(uint64_t key) {
+    const uint32_t o = static_cast<uint32_t>(key >> 32);
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+}
+
+__device__ __forceinline__ int bucket4(float s, float gmax, float inv) {
+    const float t = (gmax - s) * inv;
+    return t < static_cast<float>(kBins4 - 1) ? static_cast<int>(t) : kBins4 - 1;
+}
+
+// occupied cells of head h, clamped to the compact array width
+__device__ __forceinline__ int n_active(const Sel4& a, int h) {
+    const int na = a.nact[h];
+    return na < 0 ? 0 : (na < a.cap ? na : a.cap);
+}
+
+__device__ __forceinline__ int kprime(const Sel4& a, int na) {
+    int kp = a.nprobe < a.buffer_pages ? a.nprobe : a.buffer_pages;
+    return kp < na ? kp : na;
+}
+
+__global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
+    __shared__ float qs[128];
+    __shared__ float cs[4][kK4][kDp4 + 1];   // padded rows: lanes hit different banks
+    const int h = blockIdx.y, tid = threadIdx.x;
+    if (tid < 128) {
+        uint16_t qv[kMaxG4];
+#pragma unroll
+        for (int g = 0; g < kMaxG4; ++g) qv[g] = g < a.G ? a.q[(static_cast<int64_t>(h) * a.G + g) * 128 + tid] : 0;
+        float acc = 0.0f;   // grouped-query sum, g ascending (compute_impl.cu:80-87)
+#pragma unroll
+        for (int g = 0; g < kMaxG4; ++g)
+            if (g < a.G) acc += bf16_to_f32(qv[g]);
+        qs[tid] = acc;
+    }
+    for (int p = 0; p < 4; ++p) {
+        const float* cp = a.cent + (static_cast<int64_t>(h) * 4 + p) * a.kmax * kDp4;
+        for (int i = tid; i < a.k[p] * kDp4; i += kScoreThreads) cs[p][i / kDp4][i % kDp4] = cp[i];
+    }
+    __syncthreads();
+    const int c = blockIdx.x * kScoreThreads + tid;
+    const int na = n_active(a, h);
+    uint32_t okmax = 0, nokmin = 0;
+    if (c < na) {
+        uint32_t g = static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c]);
+        int l[4];
+#pragma unroll
+        for (int p = 3; p >= 0; --p) {
+            l[p] = static_cast<int>(g % static_cast<uint32_t>(a.k[p]));
+            g /= static_cast<uint32_t>(a.k[p]);
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+#pragma unroll
+            for (int d = 0; d < kDp4; ++d) s = __builtin_fmaf(qs[p * kDp4 + d], cs[p][l[p]][d], s);
+        const uint32_t ok = order_key(s);
+        const uint32_t gv = static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c]);
+        a.keys[static_cast<int64_t>(h) * a.cap + c] = (static_cast<uint64_t>(ok) << 32) | (0xFFFFFFFFu - gv);
+        okmax = ok;
+        nokmin = ~ok;
+    }
+    // per-head range: max of the order key and max of its complement
+    uint32_t m1 = okmax, m2 = nokmin;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        m1 = max(m1, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m1), o)));
+        m2 = max(m2, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m2), o)));
+    }
+    if (lane_id() == 0 && m1 != 0) {
+        atomicMax(&a.ext[h * 4 + 0], m1);
+        atomicMax(&a.ext[h * 4 + 1], m2);
+    }
+}
+
+__global__ __launch_bounds__(kScoreThreads) void sel4_hist_kernel(Sel4 a) {
+    __shared__ uint32_t lh[kBins4];
+    const int h = blockIdx.y, tid = threadIdx.x;
+    for (int i = tid; i < kBins4; i += kScoreThreads) lh[i] = 0;
+    __syncthreads();
+    const int c = blockIdx.x * kScoreThreads + tid;
+    const int na = n_active(a, h);
+    const uint32_t okmax = a.ext[h * 4 + 0], okmin = ~a.ext[h * 4 + 1];
+    const float gmax = key_score(static_cast<uint64_t>(okmax) << 32);
+    const float gmin = key_score(static_cast<uint64_t>(okmin) << 32);
+    const float range = gmax - gmin;
+    const float inv = range > 0.0f ? static_cast<float>(kBins4) / range : 0.0f;
+    if (c < na) atomicAdd(&lh[bucket4(key_score(a.keys[static_cast<int64_t>(h) * a.cap + c]), gmax, inv)], 1u);
+    __syncthreads();
+    for (int i = tid; i < kBins4; i += kScoreThreads)
+        if (lh[i]) atomicAdd(&a.hist[static_cast<int64_t>(h) * kBins4 + i], lh[i]);
+}
+
+// Bucket holding the kp-th best cell (buckets run from the best score down).
+__device__ int find_bucket(const Sel4& a, int h, int kp, int* sh) {
+    constexpr int PER = kBins4 / kScoreThreads;
+    const int tid = threadIdx.x;
+    int v[PER], loc = 0;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        v[u] = static_cast<int>(a.hist[static_cast<int64_t>(h) * kBins4 + tid * PER + u]);
+        loc += v[u];
+    }
+    const int incl = wave_incl_scan(loc);
+    const int w = tid >> 6;
+    if (lane_id() == 63) sh[w] = incl;
+    if (tid == 0) sh[8] = kBins4 - 1;
+    __syncthreads();
+    int base = 0;
+    for (int j = 0; j < w; ++j) base += sh[j];
+    int run = base + incl - loc;
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        if (run < kp && run + v[u] >= kp) sh[8] = tid * PER + u;
+        run += v[u];
+    }
+    __syncthreads();
+    return sh[8];
+}
+
+__global__ __launch_bounds__(kScoreThreads) void sel4_gather_kernel(Sel4 a) {
+    __shared__ int sh[16];
+    const int h = blockIdx.y, tid = threadIdx.x;
+    const int na = n_active(a, h);
+    const int kp = kprime(a, na);
+    if (kp <= 0) return;
+    const int bK = find_bucket(a, h, kp, sh);
+    const int c = blockIdx.x * kScoreThreads + tid;
+    if (c >= na) return;
+    const uint32_t okmax = a.ext[h * 4 + 0], okmin = ~a.ext[h * 4 + 1];
+    const float gmax = key_score(static_cast<uint64_t>(okmax) << 32);
+    const float gmin = key_score(static_cast<uint64_t>(okmin) << 32);
+    const float range = gmax - gmin;
+    const float inv = range > 0.0f ? static_cast<float>(kBins4) / range : 0.0f;
+    const uint64_t key = a.keys[static_cast<int64_t>(h) * a.cap + c];
+    if (bucket4(key_score(key), gmax, inv) <= bK) {
+        const uint32_t slot = atomicAdd(&a.ext[h * 4 + 2], 1u);
+        if (slot < static_cast<uint32_t>(kCand4)) {
+            a.cand[static_cast<int64_t>(h) * kCand4 + slot] = key;
+            a.cidx[static_cast<int64_t>(h) * kCand4 + slot] = c;
+        }
+    }
+}
+
+__device__ __forceinline__ void block_scan2(int& x, int& y, int* sh, int& tx, int& ty) {
+    const int ix = wave_incl_scan(x), iy = wave_incl_scan(y);
+    const int w = threadIdx.x >> 6;
+    if (lane_id() == 63) {
+        sh[w] = ix;
+        sh[16 + w] = iy;
+    }
+    __syncthreads();
+    int bx = 0, by = 0;
+    tx = 0;
+    ty = 0;
+    for (int j = 0; j < kFinalThreads / 64; ++j) {
+        if (j < w) {
+            bx += sh[j];
+            by += sh[16 + j];
+        }
+        tx += sh[j];
+        ty += sh[16 + j];
+    }
+    x = bx + ix;
+    y = by + iy;
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
+    __shared__ uint64_t sk[kCand4];
+    __shared__ int si[kCand4];
+    __shared__ int sh[48];
+    __shared__ uint32_t h256[256];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int na = n_active(a, h);
+    const int kp = kprime(a, na);
+    int32_t* prefix_out = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
+    const uint32_t count = a.ext[h * 4 + 2];
+    int n = 0;   // sorted candidates in sk / si, best first
+    if (kp > 0 && count <= static_cast<uint32_t>(kCand4)) {
+        n = static_cast<int>(count);
+        int N = 1;
+        while (N < n) N <<= 1;
+        for (int i = tid; i < N; i += kFinalThreads) {
+            sk[i] = i < n ? a.cand[static_cast<int64_t>(h) * kCand4 + i] : 0ull;
+            si[i] = i < n ? a.cidx[static_cast<int64_t>(h) * kCand4 + i] : -1;
+        }
+        __syncthreads();
+        for (int kk = 2; kk <= N; kk <<= 1) {
+            for (int j = kk >> 1; j > 0; j >>= 1) {
+                for (int i = tid; i < N; i += kFinalThreads) {
+                    const int ixj = i ^ j;
+                    if (ixj > i) {
+                        const bool desc = (i & kk) == 0;
+                        const uint64_t x = sk[i], y = sk[ixj];
+                        if ((x < y) == desc) {
+                            sk[i] = y;
+                            sk[ixj] = x;
+                            const int t = si[i];
+                            si[i] = si[ixj];
+                            si[ixj] = t;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        }
+    } else if (kp > 0) {
+        // Exact radix select of the kp-th largest key (keys are unique),
+        // then every key at or above it.
+        const uint64_t* keys = a.keys + static_cast<int64_t>(h) * a.cap;
+        uint64_t prefix = 0, mask = 0;
+        int remaining = kp;
+        for (int pass = 0; pass < 8; ++pass) {
+            const int shift = 8 * (7 - pass);
+            for (int i = tid; i < 256; i += kFinalThreads) h256[i] = 0;
+            __syncthreads();
+            for (int c = tid; c < na; c += kFinalThreads) {
+                const uint64_t key = keys[c];
+                if ((key & mask) == prefix) atomicAdd(&h256[(key >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                int acc = 0;
+                for (int d = 255; d >= 0; --d) {
+                    const int hv = static_cast<int>(h256[d]);
+                    if (acc + hv >= remaining) {
+                        sh[40] = d;
+                        sh[41] = remaining - acc;
+                        break;
+                    }
+                    acc += hv;
+                }
+            }
+            __syncthreads();
+            prefix |= static_cast<uint64_t>(sh[40]) << shift;
+            mask |= 255ull << shift;
+            remaining = sh[41];
+            __syncthreads();
+        }
+        if (tid == 0) sh[42] = 0;
+        __syncthreads();
+        for (int c = tid; c < na; c += kFinalThreads) {
+            const uint64_t key = keys[c];
+            if (key >= prefix) {
+                const int slot = atomicAdd(&sh[42], 1);
+                sk[slot] = key;
+                si[slot] = c;
+            }
+        }
+        __syncthreads();
+        n = sh[42];   // == kp
+        int N = 1;
+        while (N < n) N <<= 1;
+        for (int i = n + tid; i < N; i += kFinalThreads) {
+            sk[i] = 0ull;
+            si[i] = -1;
+        }
+        __syncthreads();
+        for (int kk = 2; kk <= N; kk <<= 1) {
+            for (int j = kk >> 1; j > 0; j >>= 1) {
+                for (int i = tid; i < N; i += kFinalThreads) {
+                    const int ixj = i ^ j;
+                    if (ixj > i) {
+                        const bool desc = (i & kk) == 0;
+                        const uint64_t x = sk[i], y = sk[ixj];
+                        if ((x < y) == desc) {
+                            sk[i] = y;
+                            sk[ixj] = x;
+                            const int t = si[i];
+                            si[i] = si[ixj];
+                            si[ixj] = t;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        }
+    }
+
+    // budget rules in rank order over the best kp cells (ranks 2*tid, 2*tid+1)
+    const int C = n < kp ? n : kp;
+    int s2[2] = {0, 0}, pg2[2] = {0, 0}, c2[2] = {-1, -1};
+    int tsum = 0, psum = 0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int r = 2 * tid + u;
+        if (r < C) {
+            c2[u] = si[r];
+            s2[u] = a.csize[static_cast<int64_t>(h) * a.cap + c2[u]];
+        }
+        pg2[u] = (s2[u] + a.page_size - 1) / a.page_size;
+        tsum += s2[u];
+        psum += pg2[u];
+    }
+    int ttot, ptot;
+    int tincl = tsum, pincl = psum;
+    block_scan2(tincl, pincl, sh, ttot, ptot);
+    int texcl = tincl - tsum, pexcl = pincl - psum;
+    int kept = 0;
+    int excl_tok[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int r = 2 * tid + u;
+        excl_tok[u] = texcl;
+        pexcl += pg2[u];
+        const bool keep = r < C && r < a.nprobe && texcl < a.max_tokens && pexcl <= a.buffer_pages;
+        kept += keep ? 1 : 0;
+        texcl += s2[u];
+    }
+    // the rules are monotone in rank, so the kept ranks are the first m
+    {
+        const int wk = wave_sum_i(kept);
+        if (lane_id() == 0) sh[32 + (tid >> 6)] = wk;
+    }
+    __syncthreads();
+    int m = 0;
+    for (int w = 0; w < kFinalThreads / 64; ++w) m += sh[32 + w];
+    int32_t* out_cell = a.sel_cell + static_cast<int64_t>(h) * a.sel_cap;
+    int32_t* out_off = a.sel_offset + static_cast<int64_t>(h) * a.sel_cap;
+    int32_t* out_cnt = a.sel_count + static_cast<int64_t>(h) * a.sel_cap;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int r = 2 * tid + u;
+        if (r < m) {
+            out_cell[r] = static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(sk[r] & 0xFFFFFFFFull));
+            out_off[r] = a.coff[static_cast<int64_t>(h) * (a.cap + 1) + c2[u]];
+            out_cnt[r] = s2[u];
+            prefix_out[r] = excl_tok[u];
+        }
+        if (r == m - 1) {
+            const int total = excl_tok[u] + s2[u];
+            prefix_out[m] = total;
+            a.n_sel[h] = m;
+            a.n_rows[h] = total;
+        }
+    }
+    if (m == 0 && tid == 0) {
+        a.n_sel[h] = 0;
+        a.n_rows[h] = 0;
+        prefix_out[0] = 0;
+    }
+    // leave the workspace zeroed for the next call
+    for (int i = tid; i < kBins4; i += kFinalThreads) a.hist[static_cast<int64_t>(h) * kBins4 + i] = 0;
+    if (tid < 4) a.ext[h * 4 + tid] = 0;
+}
+
+size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
+    Carver cv(a->workspace);
+    const size_t H = a->kv_heads;
+    uint64_t* keys = cv.take<uint64_t>(H * a->compact_cap);
+    uint32_t* hist = cv.take<uint32_t>(H * kBins4);
+    uint32_t* ext = cv.take<uint32_t>(H * 4);
+    uint64_t* cand = cv.take<uint64_t>(H * kCand4);
+    int32_t* cidx = cv.take<int32_t>(H * kCand4);
+    if (p) {
+        p->keys = keys;
+        p->hist = hist;
+        p->ext = ext;
+        p->cand = cand;
+        p->cidx = cidx;
+    }
+    return cv.used();
+}
+
+}  // namespace
+
+int select4_validate(const imi_select_args* a) {
+    IMI_REQUIRE(a->dim == 128 && a->parts == 4, IMI_ERR_UNSUPPORTED, "imi_select: 4-way path needs D=128, parts=4");
+    IMI_REQUIRE(a->groups >= 1 && a->groups <= kMaxG4, IMI_ERR_UNSUPPORTED,
+                "imi_select: %d query heads per kv head exceed %d", a->groups, kMaxG4);
+    for (int p = 0; p < 4; ++p)
+        IMI_REQUIRE(a->k[p] >= 1 && a->k[p] <= kK4, IMI_ERR_UNSUPPORTED,
+                    "imi_select: 4-way k[%d]=%d outside [1,%d]", p, a->k[p], kK4);
+    IMI_REQUIRE(a->compact_gid && a->compact_size && a->compact_offset && a->n_active && a->compact_cap > 0,
+                IMI_ERR_INVALID, "imi_select: 4-way selection needs the compact cell arrays");
+    const int kprime_max = a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages;
+    IMI_REQUIRE(kprime_max <= kSelCap4, IMI_ERR_UNSUPPORTED, "imi_select: min(nprobe, buffer_pages)=%d exceeds %d",
+                kprime_max, kSelCap4);
+    IMI_REQUIRE(a->sel_cap >= kprime_max, IMI_ERR_INVALID, "imi_select: sel_cap %d < min(nprobe, buffer_pages) %d",
+                a->sel_cap, kprime_max);
+    return IMI_OK;
+}
+
+size_t select4_workspace_size(const imi_select_args* a) {
+    imi_select_args t = *a;
+    t.workspace = nullptr;
+    return sel4_workspace(&t, nullptr);
+}
+
+int select4_launch(const imi_select_args* a, hipStream_t stream) {
+    int rc = select4_validate(a);
+    if (rc) return rc;
+    IMI_REQUIRE(a->workspace && a->workspace_bytes >= select4_workspace_size(a), IMI_ERR_WORKSPACE,
+                "imi_select: workspace %zu bytes < %zu required", a->workspace_bytes, select4_workspace_size(a));
+    Sel4 p{};
+    sel4_workspace(a, &p);
+    p.q = a->query;
+    p.cent = a->centroids;
+    p.H = a->kv_heads;
+    p.G = a->groups;
+    p.kmax = 0;
+    for (int i = 0; i < 4; ++i) {
+        p.k[i] = a->k[i];
+        p.kmax = a->k[i] > p.kmax ? a->k[i] : p.kmax;
+    }
+    p.gid = a->compact_gid;
+    p.csize = a->compact_size;
+    p.coff = a->compact_offset;
+    p.nact = a->n_active;
+    p.cap = a->compact_cap;
+    p.nprobe = a->nprobe;
+    p.max_tokens = a->max_tokens;
+    p.buffer_pages = a->buffer_pages;
+    p.page_size = a->page_size;
+    p.sel_cell = a->sel_cell;
+    p.sel_offset = a->sel_offset;
+    p.sel_count = a->sel_count;
+    p.sel_prefix = a->sel_prefix;
+    p.n_sel = a->n_selected;
+    p.n_rows = a->n_rows;
+    p.sel_cap = a->sel_cap;
+    const dim3 grid((a->compact_cap + kScoreThreads - 1) / kScoreThreads, a->kv_heads);
+    hipLaunchKernelGGL(sel4_score_kernel, grid, dim3(kScoreThreads), 0, stream, p);
+    IMI_LAUNCH_CHECK("sel4_score_kernel");
+    hipLaunchKernelGGL(sel4_hist_kernel, grid, dim3(kScoreThreads), 0, stream, p);
+    IMI_LAUNCH_CHECK("sel4_hist_kernel");
+    hipLaunchKernelGGL(sel4_gather_kernel, grid, dim3(kScoreThreads), 0, stream, p);
+    IMI_LAUNCH_CHECK("sel4_gather_kernel");
+    hipLaunchKernelGGL(sel4_final_kernel, dim3(a->kv_heads), dim3(kFinalThreads), 0, stream, p);
+    IMI_LAUNCH_CHECK("sel4_final_kernel");
+    return IMI_OK;
+}
+
+}  // namespace imi

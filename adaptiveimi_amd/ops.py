@@ -133,8 +133,11 @@ def kmeans_assign(keys: torch.Tensor, centroids: torch.Tensor, ks: Sequence[int]
 def build_index(keys: torch.Tensor, values: torch.Tensor, centroids: torch.Tensor, labels: torch.Tensor,
                 ks: Sequence[int], n_centroids: Optional[int] = None, list_rows: Optional[int] = None,
                 list_keys: Optional[torch.Tensor] = None, list_values: Optional[torch.Tensor] = None,
-                compact: bool = True) -> Dict[str, torch.Tensor]:
-    """Cell order + CSR + K/V permutation (reorganize_core.cpp:18-394)."""
+                compact: bool = True, merged: bool = True) -> Dict[str, torch.Tensor]:
+    """Cell order + CSR + K/V permutation (reorganize_core.cpp:18-394).
+    compact: also list the occupied cells (gid, size, offset, n_active);
+    merged: with them the padded merged centroids and mask (the metadata the
+    reference uploads; not needed by the decode kernels)."""
     dev = _require_device(keys, values, centroids, labels)
     _as_bits(keys)
     _as_bits(values)
@@ -170,15 +173,16 @@ def build_index(keys: torch.Tensor, values: torch.Tensor, centroids: torch.Tenso
         out["compact_gid"] = torch.empty((H, n_c), dtype=torch.int32, device=dev)
         out["compact_size"] = torch.empty((H, n_c), dtype=torch.int32, device=dev)
         out["compact_offset"] = torch.empty((H, n_c + 1), dtype=torch.int32, device=dev)
-        out["compact_centroids"] = torch.empty((H, n_c, D), dtype=torch.float32, device=dev)
-        out["compact_mask"] = torch.empty((H, n_c), dtype=torch.bool, device=dev)
         a.n_centroids = n_c
         a.n_active = out["n_active"].data_ptr()
         a.compact_gid = out["compact_gid"].data_ptr()
         a.compact_size = out["compact_size"].data_ptr()
         a.compact_offset = out["compact_offset"].data_ptr()
-        a.compact_centroids = out["compact_centroids"].data_ptr()
-        a.compact_mask = out["compact_mask"].data_ptr()
+        if merged:
+            out["compact_centroids"] = torch.empty((H, n_c, D), dtype=torch.float32, device=dev)
+            out["compact_mask"] = torch.empty((H, n_c), dtype=torch.bool, device=dev)
+            a.compact_centroids = out["compact_centroids"].data_ptr()
+            a.compact_mask = out["compact_mask"].data_ptr()
     need = ctypes.c_size_t()
     check(_lib.lib().imi_index_workspace_size(ctypes.byref(a), ctypes.byref(need)), "imi_index_workspace_size")
     ws = workspace("index", need.value, dev)
@@ -237,10 +241,23 @@ class Budget:
         return self.buffer_pages * self.page_size
 
 
+def _compact_fields(a, compact: Optional[Dict[str, torch.Tensor]]) -> None:
+    """Point SelectArgs at the occupied-cell arrays of build_index (4-way)."""
+    if compact is None:
+        return
+    a.compact_gid = compact["compact_gid"].data_ptr()
+    a.compact_size = compact["compact_size"].data_ptr()
+    a.compact_offset = compact["compact_offset"].data_ptr()
+    a.n_active = compact["n_active"].data_ptr()
+    a.compact_cap = compact["compact_gid"].shape[1]
+
+
 def select(query: torch.Tensor, centroids: torch.Tensor, cell_count: torch.Tensor, cell_offset: torch.Tensor,
-           ks: Sequence[int], budget: Budget) -> Dict[str, torch.Tensor]:
+           ks: Sequence[int], budget: Budget, compact: Optional[Dict[str, torch.Tensor]] = None
+           ) -> Dict[str, torch.Tensor]:
     """Scores + top-nprobe + token prefix + page rule, per KV head
-    (retrieval.py:295-303,357; wave_buffer_cpu_hotcold.cpp:303-371)."""
+    (retrieval.py:295-303,357; wave_buffer_cpu_hotcold.cpp:303-371).
+    A 4-way IMI needs ``compact`` (the build_index outputs with compact=True)."""
     dev = _require_device(query, centroids, cell_count, cell_offset)
     _as_bits(query)
     H, G, D = query.shape
@@ -261,6 +278,13 @@ def select(query: torch.Tensor, centroids: torch.Tensor, cell_count: torch.Tenso
                    sel_offset=out["sel_offset"].data_ptr(), sel_count=out["sel_count"].data_ptr(),
                    sel_prefix=out["sel_prefix"].data_ptr(), n_selected=out["n_selected"].data_ptr(),
                    n_rows=out["n_rows"].data_ptr(), sel_cap=cap)
+    _compact_fields(a, compact)
+    need = ctypes.c_size_t()
+    check(_lib.lib().imi_select_workspace_size(ctypes.byref(a), ctypes.byref(need)), "imi_select_workspace_size")
+    if need.value:
+        ws = workspace("select", need.value, dev)
+        a.workspace = ws.data_ptr()
+        a.workspace_bytes = ws.numel()
     check(_lib.lib().imi_select(ctypes.byref(a), _stream(dev)), "imi_select")
     return out
 
@@ -304,7 +328,8 @@ class DecodePlan:
                  ks: Sequence[int], budget: Budget, list_keys: torch.Tensor, list_values: torch.Tensor,
                  steady_keys: Optional[torch.Tensor], steady_values: Optional[torch.Tensor], groups: int,
                  scale: Optional[float] = None, query: Optional[torch.Tensor] = None,
-                 out: Optional[torch.Tensor] = None, out_lse: Optional[torch.Tensor] = None):
+                 out: Optional[torch.Tensor] = None, out_lse: Optional[torch.Tensor] = None,
+                 compact: Optional[Dict[str, torch.Tensor]] = None):
         dev = _require_device(centroids, cell_count, cell_offset, list_keys, list_values)
         self.device = dev
         H, _, D = list_keys.shape
@@ -313,7 +338,7 @@ class DecodePlan:
         self.query = query if query is not None else torch.zeros((H, groups, D), dtype=torch.bfloat16, device=dev)
         self.out = out if out is not None else torch.empty((H * groups, D), dtype=torch.bfloat16, device=dev)
         self._keep = (centroids, cell_count, cell_offset, list_keys, list_values, steady_keys, steady_values,
-                      out_lse)
+                      out_lse, compact)
         a = DecodeArgs()
         s = a.sel
         s.query = self.query.data_ptr()
@@ -325,6 +350,7 @@ class DecodePlan:
         s.nprobe, s.max_tokens = budget.nprobe, budget.max_tokens
         s.buffer_pages, s.page_size = budget.buffer_pages, budget.page_size
         s.sel_cap = budget.sel_cap
+        _compact_fields(s, compact)
         t = a.attn
         t.query = self.query.data_ptr()
         t.steady_keys = _ptr(steady_keys)

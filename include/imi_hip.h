@@ -121,8 +121,8 @@ typedef struct {
     int32_t* compact_gid;     /* [H][n_centroids], -1 for padding slots */
     int32_t* compact_size;    /* [H][n_centroids] */
     int32_t* compact_offset;  /* [H][n_centroids + 1] */
-    float* compact_centroids; /* [H][n_centroids][D] merged, zero padding */
-    uint8_t* compact_mask;    /* [H][n_centroids] 1 = masked (padding) */
+    float* compact_centroids; /* [H][n_centroids][D] merged, zero padding (may be NULL) */
+    uint8_t* compact_mask;    /* [H][n_centroids] 1 = masked (padding) (may be NULL) */
     void* workspace;
     size_t workspace_bytes;
 } imi_index_args;
@@ -168,8 +168,20 @@ typedef struct {
     int32_t* n_selected;      /* [H] m */
     int32_t* n_rows;          /* [H] selected rows (sum of sel_count) */
     int32_t sel_cap;          /* >= min(nprobe, buffer_pages) */
+    /* 4-way IMI (parts == 4) only: occupied cells in ascending global id,
+     * the compact outputs of imi_build_index, and a zero-filled workspace
+     * (every call leaves it zero again). */
+    const int32_t* compact_gid;     /* [H][compact_cap] */
+    const int32_t* compact_size;    /* [H][compact_cap] */
+    const int32_t* compact_offset;  /* [H][compact_cap + 1] */
+    const int32_t* n_active;        /* [H] */
+    int32_t compact_cap;
+    void* workspace;
+    size_t workspace_bytes;         /* >= imi_select_workspace_size() */
 } imi_select_args;
 
+/* Workspace imi_select needs (0 for 2-way IMI). */
+int imi_select_workspace_size(const imi_select_args* a, size_t* bytes);
 int imi_select(const imi_select_args* a, imi_stream_t stream);
 
 /* ------------------------------------------ decode: gather + attention

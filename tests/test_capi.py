@@ -33,7 +33,7 @@ def test_exports_every_declared_symbol(L):
 
 
 def test_version(L):
-    assert L.imi_version() == 1
+    assert L.imi_version() == 2
 
 
 def _kmeans_args(**over):
@@ -86,9 +86,24 @@ def test_select_and_decode_argument_checks(L):
     s = SelectArgs(query=16, centroids=16, cell_count=16, cell_offset=16, kv_heads=8, groups=4, dim=128, parts=4,
                    nprobe=410, max_tokens=3276, buffer_pages=410, page_size=8, sel_cap=410)
     s.k[0] = s.k[1] = 64
-    assert L.imi_select(ctypes.byref(s), None) == 3          # 4-way selection not implemented
-    assert "2-way" in L.imi_last_error().decode()
+    assert L.imi_select(ctypes.byref(s), None) == 3          # 4-way needs every k in [1, 64]
+    assert "k[2]=0" in L.imi_last_error().decode()
+    s.k[2] = s.k[3] = 64
+    assert L.imi_select(ctypes.byref(s), None) == 1          # ... and the occupied-cell arrays
+    assert "compact cell arrays" in L.imi_last_error().decode()
+    s.compact_gid = s.compact_size = s.compact_offset = s.n_active = 16
+    s.compact_cap = 4096
+    s.nprobe = s.buffer_pages = 3000
+    assert L.imi_select(ctypes.byref(s), None) == 3          # top-k beyond the 4-way bound
+    assert "exceeds 2048" in L.imi_last_error().decode()
+    s.nprobe = s.buffer_pages = 410
+    s.sel_cell = s.sel_offset = s.sel_count = s.sel_prefix = s.n_selected = s.n_rows = 16
+    need = ctypes.c_size_t()
+    assert L.imi_select_workspace_size(ctypes.byref(s), ctypes.byref(need)) == 0 and need.value > 0
+    assert L.imi_select(ctypes.byref(s), None) == 4          # no workspace given
+    assert "workspace" in L.imi_last_error().decode()
     s.parts = 2
+    assert L.imi_select_workspace_size(ctypes.byref(s), ctypes.byref(need)) == 0 and need.value == 0
     s.sel_cap = 100
     assert L.imi_select(ctypes.byref(s), None) == 1
     assert "sel_cap" in L.imi_last_error().decode()

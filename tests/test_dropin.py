@@ -101,26 +101,31 @@ def _bits(t):
 
 @pytest.mark.gpu
 @pytest.mark.skipif(not gpu_available(), reason="needs a HIP device")
-def test_model_shaped_prefill_and_decode_match_oracle():
+@pytest.mark.parametrize("ks", [(32, 32), (6, 6, 6, 6)])
+def test_model_shaped_prefill_and_decode_match_oracle(ks):
     from adaptiveimi_amd import synthetic
     from adaptiveimi_amd.attn_hub.sparse_imi import imi_decode_attn
     from oracle import oracle as orc
 
-    print("[dropin] 2 layers, S=6096, ks=(32,32), 2 decode steps", flush=True)
+    print(f"[dropin] 2 layers, S=6096, ks={ks}, 2 decode steps", flush=True)
     L, S, H, G, D = 2, 6096, 8, 4, 128
-    cache = _cache(layer_mapping={"0": DEV, "1": DEV})
+    kcfg = {f"k{i + 1}": k for i, k in enumerate(ks)}
+    kcfg.update(max_iters=6, early_stop_min_iter=6, init="first")
+    cache = _cache(layer_mapping={"0": DEV, "1": DEV}, subspace_parts=len(ks), runtime_config={"kmeans": kcfg})
     kv = []
     for layer in range(L):
         k, v = synthetic.make_kv(H, S + 2, seed=40 + layer)
         kv.append((k, v))
-        ks = k[:, :S].transpose(0, 1).unsqueeze(0).contiguous().to(DEV)   # [1, S, H, D]
-        vs = v[:, :S].transpose(0, 1).unsqueeze(0).contiguous().to(DEV)
-        rk, rv = cache.prefill_update_kv_cache(None, ks, vs, layer, 0)
-        assert rk.shape == ks.shape
+        pk = k[:, :S].transpose(0, 1).unsqueeze(0).contiguous().to(DEV)   # [1, S, H, D]
+        pv = v[:, :S].transpose(0, 1).unsqueeze(0).contiguous().to(DEV)
+        rk, rv = cache.prefill_update_kv_cache(None, pk, pv, layer, 0)
+        assert rk.shape == pk.shape
         cache.sync(layer, 0)
     assert cache.context == S and cache.attn_func == cache.sparse_attention
     cache.prepare_cache()
-    assert cache.nprobe == round(1024 * 0.1) and cache.max_retrieval_tokens == int(0.1 * 6000)
+    ncells = int(np.prod(ks))
+    assert cache.n_centroids == ncells + 1
+    assert cache.nprobe == round(ncells * 0.1) and cache.max_retrieval_tokens == int(0.1 * 6000)
 
     # oracle index of each layer
     heads_by_layer = []
@@ -129,11 +134,11 @@ def test_model_shaped_prefill_and_decode_match_oracle():
         mid_k, mid_v = _bits(k[:, 32:S - 64]), _bits(v[:, 32:S - 64])
         heads = []
         for h in range(H):
-            labs, cents, _ = orc.kmeans_head(orc.bf16_to_f32(mid_k[h]), [32, 32], 6, early_stop_min_iter=6)
-            r = orc.compact_reorg(labs, [32, 32])
+            labs, cents, _ = orc.kmeans_head(orc.bf16_to_f32(mid_k[h]), list(ks), 6, early_stop_min_iter=6)
+            r = orc.compact_reorg(labs, list(ks))
             assert np.array_equal(cache.token_perm[layer][h].cpu().numpy(), r["perm"]), "cell order differs"
             heads.append(dict(n_active=r["n_active"], offsets=r["offsets"],
-                              merged=orc.merged_centroids(cents, r["gids"], [32, 32]),
+                              merged=orc.merged_centroids(cents, r["gids"], list(ks)),
                               list_keys=mid_k[h][r["perm"]], list_values=mid_v[h][r["perm"]]))
         heads_by_layer.append(heads)
 

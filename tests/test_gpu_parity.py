@@ -299,6 +299,79 @@ def test_select_bit_exact(ops, oracle, T, ks, budget, G, seed):
         assert n_c == sizes.shape[1]
 
 
+@pytest.mark.parametrize("T,ks,budget,G,seed", [
+    (20000, (8, 8, 8, 8), 0.1, 8, 0),
+    (30000, (16, 16, 16, 16), 0.05, 4, 1),
+    (12000, (5, 7, 6, 4), 0.2, 7, 2),
+])
+def test_select_4way_bit_exact(ops, oracle, T, ks, budget, G, seed):
+    """4-way IMI selection over the occupied cells (the reference scores the
+    padded k^4 + 1 compact cells): same cells, rank order and row counts as
+    the oracle."""
+    note(f"[select4] T={T} ks={ks} budget={budget} G={G}")
+    H = 4
+    keys, values = _kv(H, T, seed=200 + seed)
+    kd, vd = keys.to(DEV), values.to(DEV)
+    cent, labels, _ = ops.kmeans(kd, list(ks), 3)
+    ncells = int(np.prod(ks))
+    out = ops.build_index(kd, vd, cent, labels, list(ks), n_centroids=ncells + 1)
+    from adaptiveimi_amd import synthetic
+
+    sz = oracle.sizing(T, budget, subspace_parts=4, k_override=ks)
+    bud = ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"])
+    qs = synthetic.make_queries(keys, G, seed=seed, n_queries=2)
+    sizes = out["compact_size"].cpu().numpy()
+    mask = out["compact_mask"].cpu().numpy()
+    gids = out["compact_gid"].cpu().numpy()
+    merged = out["compact_centroids"].cpu().numpy()
+    for qi in range(qs.shape[0]):
+        q = qs[qi]
+        sel = ops.select(q.to(DEV), cent, out["cell_count"], out["cell_offset"], ks, bud, compact=out)
+        sc = oracle.scores(bits(q), merged)
+        rs, rm, rtok = oracle.select(sc, sizes, mask, bud.nprobe, bud.max_tokens, bud.buffer_pages)
+        m = sel["n_selected"].cpu().numpy()
+        assert np.array_equal(m, rm), (qi, m, rm)
+        cells = sel["sel_cell"].cpu().numpy()
+        offs = sel["sel_offset"].cpu().numpy()
+        coff = out["compact_offset"].cpu().numpy()
+        for h in range(H):
+            assert np.array_equal(cells[h, : m[h]], gids[h][rs[h, : rm[h]]]), (qi, h)
+            assert np.array_equal(offs[h, : m[h]], coff[h][rs[h, : rm[h]]]), (qi, h)
+        assert np.array_equal(sel["n_rows"].cpu().numpy(), rtok)
+
+
+@pytest.mark.parametrize("qmode", ["zero", "three_dims"])
+def test_select_4way_massive_ties(ops, oracle, qmode):
+    """Integer data with few distinct scores.  qmode "zero": every occupied
+    cell scores 0, so far more than 4096 cells share the threshold bucket and
+    the exact radix-select path runs; "three_dims": scores depend on the first
+    subspace only, a handful of values each shared by hundreds of cells.  Ties
+    go to the lowest cell id either way."""
+    note(f"[select4] massive ties {qmode}")
+    H, T, ks = 2, 40000, (10, 10, 10, 10)
+    keys, values = _kv(H, T, seed=11, integer=True)
+    kd, vd = keys.to(DEV), values.to(DEV)
+    cent, labels, _ = ops.kmeans(kd, list(ks), 2)
+    out = ops.build_index(kd, vd, cent, labels, list(ks), n_centroids=10001)
+    n_active = out["n_active"].cpu().numpy()
+    q = torch.zeros((H, 4, 128), dtype=torch.bfloat16)
+    if qmode == "three_dims":
+        q[:, :, :3] = 1.0
+    else:
+        assert n_active.min() > 4096      # the zero query must overflow the candidate buffer
+    bud = ops.Budget(3000, 30000, 2000)
+    sel = ops.select(q.to(DEV), cent, out["cell_count"], out["cell_offset"], ks, bud, compact=out)
+    sc = oracle.scores(bits(q), out["compact_centroids"].cpu().numpy())
+    rs, rm, rtok = oracle.select(sc, out["compact_size"].cpu().numpy(), out["compact_mask"].cpu().numpy(),
+                                 3000, 30000, 2000)
+    gids = out["compact_gid"].cpu().numpy()
+    m = sel["n_selected"].cpu().numpy()
+    assert np.array_equal(m, rm)
+    for h in range(H):
+        assert np.array_equal(sel["sel_cell"].cpu().numpy()[h, : m[h]], gids[h][rs[h, : rm[h]]])
+    assert np.array_equal(sel["n_rows"].cpu().numpy(), rtok)
+
+
 def test_select_ties_integer_data(ops, oracle):
     """Integer keys/queries: many exactly tied scores; order must be by cell id."""
     note("[select] ties")
