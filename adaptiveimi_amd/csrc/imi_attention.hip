@@ -6,7 +6,8 @@
 // unvendored weighted_flash_decoding (retrieval.py:439-447).  Here the rows
 // are read in place: the steady zone for the first static_len rows, then the
 // CSR list rows of the selected cells (each workgroup stages the head's
-// selection in LDS and binary-searches its rows) -- no execution buffer.
+// selection in LDS and each wave maps its rows to list rows with two ballot
+// rounds and a flag count) -- no execution buffer.
 //
 // Grid: H * nsplit workgroups of 4 waves; workgroup b takes split b / H of
 // head (b + b / H) % H, so consecutive workgroups (which the dispatcher deals
@@ -79,6 +80,22 @@ struct AttnParams {
 // is M; an empty state (m = -inf) weighs 0 even when M is -inf too.
 __device__ __forceinline__ float wexp(float m, float M) { return m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M); }
 
+// Orders this wave's LDS accesses around a hand-off between its own lanes
+// (compiler-only: a wave executes its LDS instructions in order, but without
+// the fences the compiler may reorder or forward them as if each lane ran
+// alone).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Number of set bits of the 128-bit mask (lo, hi) at positions 0..i.
+__device__ __forceinline__ int popc_upto(uint64_t lo, uint64_t hi, int i) {
+    if (i < 64) return __builtin_popcountll(lo & (~0ull >> (63 - i)));
+    return __builtin_popcountll(lo) + __builtin_popcountll(hi & (~0ull >> (127 - i)));
+}
+
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
 }
@@ -91,11 +108,13 @@ template <int G, int NT>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) void attention_kernel(AttnParams a) {
     constexpr int RW = NT * 16;                       // rows per wave
     constexpr int NR = (RW + 63) / 64;                // row locations per lane
+    static_assert(NR <= 2, "the row lookup covers windows of at most 128 rows");
     constexpr int SU = (kSelCapMax + 1 + 64 * kWaves - 1) / (64 * kWaves);
     __shared__ float s_acc[kWaves][G][128];
     __shared__ float s_ml[kWaves][G][2];
     __shared__ int s_pre[kSelCapMax + 1];
     __shared__ int s_off[kSelCapMax];
+    __shared__ int s_flag[kWaves][NR * 64];
     __shared__ __attribute__((aligned(16))) uint16_t s_v[kWaves][16 * kVStride];
     __shared__ __attribute__((aligned(16))) uint16_t s_k[kWaves][16 * kVStride];
 
@@ -136,26 +155,52 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     const int N = a.static_len + nrows;
     if (split * a.rows_per_block >= N) return;   // the merge ignores this split
 
-    // List row of rows row0 + lane + 64r: cell c = the last with pre[c] <= j
-    // (branch-free search over the m selected cells, pre[0] = 0).
+    // List row of window row i (rows row0 + i, i = lane + 64r): the wave
+    // finds the cell c0 that holds its first list row j0 (two ballot rounds
+    // over the staged prefix), flags the window offsets where the following
+    // cells start, and counts the flags up to each row.  Selected cells hold
+    // at least one row, so their starts are distinct; locations are clamped
+    // to the list.
     int loc[NR];
     {
-        int lo[NR], jj[NR];
+        const int j0 = max(row0 - a.static_len, 0);
+        int c0 = 0;
+        if (m > 1) {
+            const int step = (m + 63) >> 6;   // <= 32 cells per lane sample
+            const int cs = lane * step;
+            const uint64_t b1 = __builtin_amdgcn_ballot_w64(cs < m && s_pre[cs] <= j0);
+            const int base = (63 - __builtin_clzll(b1 | 1ull)) * step;
+            const int cc = base + lane;
+            const uint64_t b2 = __builtin_amdgcn_ballot_w64(lane < step && cc < m && s_pre[cc] <= j0);
+            c0 = base + (63 - __builtin_clzll(b2 | 1ull));
+        }
+        int* fl = s_flag[wave];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) fl[lane + 64 * r] = 0;
+        wave_lds_sync();
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-            lo[r] = 0;
-            jj[r] = row0 + lane + 64 * r - a.static_len;
-        }
-#pragma unroll
-        for (int step = kSelCapMax / 2; step >= 1; step >>= 1)
-#pragma unroll
-            for (int r = 0; r < NR; ++r) {
-                const int c = lo[r] + step;
-                if (c < m && s_pre[c] <= jj[r]) lo[r] = c;
+            const int c = c0 + 1 + lane + 64 * r;
+            if (c < m) {
+                const int o = s_pre[c] - j0;
+                if (o > 0 && o < NR * 64) fl[o] = 1;
             }
+        }
+        wave_lds_sync();
+        uint64_t fm[2] = {0ull, 0ull};
 #pragma unroll
-        for (int r = 0; r < NR; ++r)
-            loc[r] = (jj[r] >= 0 && jj[r] < nrows) ? s_off[lo[r]] + (jj[r] - s_pre[lo[r]]) : 0;
+        for (int r = 0; r < NR; ++r) fm[r] = __builtin_amdgcn_ballot_w64(fl[lane + 64 * r] != 0);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int j = row0 + lane + 64 * r - a.static_len;
+            int l = 0;
+            if (j >= 0 && j < nrows) {
+                const int c = c0 + popc_upto(fm[0], fm[1], j - j0);
+                l = s_off[c] + (j - s_pre[c]);
+                l = min(max(l, 0), static_cast<int>(a.list_rows) - 1);
+            }
+            loc[r] = l;
+        }
     }
 
     const uint16_t* skh = a.sk + static_cast<int64_t>(h) * a.s_stride * 128;
@@ -199,6 +244,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
                 *reinterpret_cast<u32x4_t*>(sv + (4 * it + rg) * kVStride + li * 8) = vb[slot][it];
                 *reinterpret_cast<u32x4_t*>(sk + (4 * it + rg) * kVStride + li * 8) = kb[slot][it];
             }
+            wave_lds_sync();
             u32x4_t ka[4];
 #pragma unroll
             for (int c = 0; c < 4; ++c) ka[c] = *reinterpret_cast<const u32x4_t*>(sk + ln * kVStride + c * 32 + lg * 8);
@@ -254,6 +300,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
                 acc[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, pa), vt, acc[d], 0,
                                                                    0, 0);
             }
+            wave_lds_sync();
         }
     }
     // sum over the four lane groups (different tokens, shared max)

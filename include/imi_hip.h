@@ -201,9 +201,9 @@ typedef struct {
     const uint16_t* list_keys;    /* device bf16 [H][list_rows][D] */
     const uint16_t* list_values;
     int64_t list_rows;
-    const int32_t* sel_offset;    /* from imi_select */
-    const int32_t* sel_count;
-    const int32_t* sel_prefix;
+    const int32_t* sel_offset;    /* from imi_select; every selected cell */
+    const int32_t* sel_count;     /*   holds at least one row (imi_select */
+    const int32_t* sel_prefix;    /*   keeps no empty cell) */
     const int32_t* n_selected;
     const int32_t* n_rows;
     int32_t sel_cap;
