@@ -422,18 +422,6 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
     }
 }
 
-int device_cus() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
-    }
-    return cached[dev];
-}
-
 // Rows the workspace and the tile size are fixed for: any static_len up to
 // steady_stride, so one workspace (and one captured launch shape) stays valid
 // while the steady zone grows.

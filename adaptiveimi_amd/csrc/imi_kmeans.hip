@@ -9,12 +9,15 @@
 //   executor     384-501 (one independent run per (head, subspace))
 //
 // Work layout: every kernel covers all H*P (head, subspace) segments at once.
-// The E-step keeps one token's subvector in registers (Dp fp32) and streams
-// the segment's centroids from LDS (broadcast reads); it also emits the block
-// histogram of labels and each token's stable rank inside its block, so the
-// M-step's member lists come from one scan + one scatter, and the M-step sums
-// each cluster sequentially in ascending token order (the reference's order
-// with one thread per subspace run).
+// E-step (k <= 128): distances are screened on the matrix cores (bf16 MFMA
+// with the centroids split into hi + lo bf16 parts, under a proven rounding
+// bound) and only the centroids that can still win get the exact reference
+// distance; k > 128 uses the exact distance to every centroid.  Both emit
+// the block histogram of labels and each token's stable rank inside its
+// block, so the M-step's member lists come from one scan + one scatter.  The
+// M-step sums each cluster sequentially in ascending token order (the
+// reference's order with one thread per subspace run), one wave per cluster
+// with the member rows streamed through a register ring.
 #include <limits>
 #include <random>
 #include <vector>
@@ -153,6 +156,238 @@ __global__ __launch_bounds__(256) void km_assign_kernel(KmParams a) {
                                    a.hist + static_cast<int64_t>(seg) * a.kmax * a.nblk, a.nblk, blk);
     if (valid) a.rank[static_cast<int64_t>(seg) * a.T + t] = r;
     if (tid == 0) a.ipart[static_cast<int64_t>(seg) * a.nblk + blk] = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// E-step with matrix-core screening (k <= 128).  For token x and centroid
+// c the distance is approximated as D~ = |x|^2 + |c|^2 - 2 x.c, with x.c on
+// v_mfma_f32_16x16x32_bf16: x is bf16 already and c enters as two bf16
+// parts (hi = bf16(c), lo = bf16(c - hi), |c - hi - lo| <= 2^-16 |c|).
+// Rounding analysis (unit roundoff u = 2^-24, at most ~256 accumulations
+// per dot product, reference distance = 8 FMA chains + 7 adds):
+//   |D~ - D_ref| <= 2^-14.6 (|x|^2 + |c|^2) <= E = 2^-12 (|x|^2 + max|c|^2)
+// (4x margin, plus 1e-30 for flushed subnormal products).  Any centroid
+// that can win under the reference order satisfies D~(c) <= min D~ + 2E, so
+// only those candidates get the exact reference distance (l2_lanes8, c
+// ascending, strict '<'); usually there is one.  Non-finite or huge values
+// (|x|^2 + max|c|^2 > 1e37) make every centroid a candidate, which is the
+// plain exact E-step.  Outputs (labels, min distances, block ranks, label
+// histogram, inertia partials) are those of km_assign_kernel.
+typedef __attribute__((ext_vector_type(8))) __bf16 km_bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float km_f32x4_t;
+typedef __attribute__((ext_vector_type(4))) unsigned int km_u32x4_t;
+
+constexpr int kScreenMaxK = 128;
+
+__device__ __forceinline__ uint32_t xor16_u(uint32_t v) { return __float_as_uint(xor16(__uint_as_float(v))); }
+__device__ __forceinline__ uint32_t xor32_u(uint32_t v) { return __float_as_uint(xor32(__uint_as_float(v))); }
+
+// Intra-wave LDS hand-off (compiler ordering only; a wave's LDS instructions
+// execute in order).
+__device__ __forceinline__ void km_wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int DP>
+size_t screen_lds_bytes(int kmax) {
+    constexpr int KH = DP / 32;
+    const size_t nct = (kmax + 15) / 16;
+    return static_cast<size_t>(kmax) * (DP + 4) * 4 + nct * KH * 2 * 64 * 16 + nct * 16 * 4 + 256 * 2 * 8 +
+           4 * static_cast<size_t>(kmax) * 4 + 64;
+}
+
+template <int DP>
+__global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int chunks) {
+    constexpr int KH = DP / 32;   // 32-dim K steps per subvector
+    extern __shared__ float smem[];
+    const int seg = blockIdx.y;
+    if (a.done && a.done[seg]) return;
+    const int h = seg / a.P, p = seg % a.P;
+    const int k = a.k[p];
+    const int nct = (k + 15) >> 4;
+    const int nct_max = (a.kmax + 15) >> 4;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    constexpr int CS = DP + 4;
+    float* cs = smem;                                                        // [kmax][DP + 4]
+    km_u32x4_t* apk = reinterpret_cast<km_u32x4_t*>(cs + a.kmax * CS);      // [nct][KH][hi,lo][64 lanes]
+    float* ccs = reinterpret_cast<float*>(apk + nct_max * KH * 2 * 64);     // [nct * 16]
+    uint64_t* cmask = reinterpret_cast<uint64_t*>(ccs + nct_max * 16);      // [256][2] candidate bits
+    int* wcnt = reinterpret_cast<int*>(cmask + 256 * 2);                     // [4][kmax]
+    float* red = reinterpret_cast<float*>(wcnt + 4 * a.kmax);               // [4]
+
+    const float* cg = a.cent + static_cast<int64_t>(seg) * a.kmax * DP;
+    for (int i = tid; i < k * DP; i += 256) cs[(i / DP) * CS + i % DP] = cg[i];
+    __syncthreads();
+    // A operands: lane l of tile ct holds centroid 16ct + l%16, dims
+    // 32kh + 8(l/16) .. +7 (v_mfma_f32_16x16x32_bf16 A layout)
+    for (int e = tid; e < nct * KH * 2 * 64; e += 256) {
+        const int l = e & 63, part = (e >> 6) & 1, t2 = e >> 7;
+        const int kh = t2 % KH, ct = t2 / KH;
+        const int c = ct * 16 + (l & 15);
+        const int d0 = kh * 32 + 8 * (l >> 4);
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        if (c < k) {
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+                const float v0 = cs[c * CS + d0 + i], v1 = cs[c * CS + d0 + i + 1];
+                uint16_t b0 = f32_to_bf16(v0), b1 = f32_to_bf16(v1);
+                if (part) {
+                    b0 = f32_to_bf16(v0 - bf16_to_f32(b0));
+                    b1 = f32_to_bf16(v1 - bf16_to_f32(b1));
+                }
+                w[i / 2] = static_cast<uint32_t>(b0) | (static_cast<uint32_t>(b1) << 16);
+            }
+        }
+        apk[e] = km_u32x4_t{w[0], w[1], w[2], w[3]};
+    }
+    for (int c = tid; c < nct * 16; c += 256) {
+        float sq = 0.0f;
+        if (c < k)
+            for (int d = 0; d < DP; ++d) sq = __builtin_fmaf(cs[c * CS + d], cs[c * CS + d], sq);
+        ccs[c] = sq;
+    }
+    __syncthreads();
+    float ccmax = 0.0f;
+    for (int c = lane; c < k; c += 64) ccmax = fmaxf(ccmax, ccs[c]);
+    ccmax = wave_max(ccmax);
+
+    const uint16_t* kb = a.keys + h * a.hs + p * DP;
+    // 256-token blocks blockIdx.x * chunks .. +chunks-1 (the prologue above is
+    // shared by all of them)
+#pragma unroll 1
+    for (int ci = 0; ci < chunks; ++ci) {
+    const int blk = blockIdx.x * chunks + ci;
+    if (blk >= a.nblk) break;
+    if (ci > 0) __syncthreads();   // the previous block's LDS reads are done
+    // every load of this block of 256 tokens is issued up front: the MFMA B
+    // operands of the wave's four 16-token tiles (lane l: token l%16, dims
+    // 32kh + 8(l/16) .. +7) and the thread's own token row for the exact pass
+    const int tw0 = blk * 256 + wave * 64;
+    const int t = blk * 256 + tid;
+    const bool valid = t < a.T;
+    km_u32x4_t bqa[4][KH];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int tt = tw0 + 16 * j + (lane & 15);
+#pragma unroll
+        for (int kh = 0; kh < KH; ++kh)
+            bqa[j][kh] = tt < a.T ? *reinterpret_cast<const km_u32x4_t*>(kb + static_cast<int64_t>(tt) * a.ts +
+                                                                         kh * 32 + 8 * (lane >> 4))
+                                  : km_u32x4_t{0u, 0u, 0u, 0u};
+    }
+    // screening: token tile j = tokens 16j .. 16j+15 of this wave's 64
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const km_u32x4_t* bq = bqa[j];
+        float xs = 0.0f;
+#pragma unroll
+        for (int kh = 0; kh < KH; ++kh) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float lo = bf16_lo(bq[kh][w]), hi = bf16_hi(bq[kh][w]);
+                xs = __builtin_fmaf(lo, lo, xs);
+                xs = __builtin_fmaf(hi, hi, xs);
+            }
+        }
+        xs += xor16(xs);
+        xs += xor32(xs);
+        float dt[kScreenMaxK / 16][4];
+        float dmin = INFINITY;
+#pragma unroll
+        for (int ct = 0; ct < kScreenMaxK / 16; ++ct) {
+            if (ct < nct) {
+                km_f32x4_t acc = km_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int kh = 0; kh < KH; ++kh) {
+                    const km_u32x4_t ah = apk[((ct * KH + kh) * 2 + 0) * 64 + lane];
+                    const km_u32x4_t al = apk[((ct * KH + kh) * 2 + 1) * 64 + lane];
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(km_bf16x8_t, ah),
+                                                                  __builtin_bit_cast(km_bf16x8_t, bq[kh]), acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(km_bf16x8_t, al),
+                                                                  __builtin_bit_cast(km_bf16x8_t, bq[kh]), acc, 0, 0, 0);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int c = ct * 16 + 4 * (lane >> 4) + r;
+                    const float v = c < k ? (xs + ccs[c]) - 2.0f * acc[r] : INFINITY;
+                    dt[ct][r] = v;
+                    dmin = fminf(dmin, v);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dt[ct][r] = INFINITY;
+            }
+        }
+        dmin = fminf(dmin, xor16(dmin));
+        dmin = fminf(dmin, xor32(dmin));
+        const float mag = xs + ccmax;
+        const float lim = dmin + 2.0f * (0x1p-12f * mag + 1e-30f);
+        const bool all = !(lim < INFINITY) || !(mag <= 1e37f);
+        uint32_t m[kScreenMaxK / 32] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int ct = 0; ct < kScreenMaxK / 16; ++ct)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int c = ct * 16 + 4 * (lane >> 4) + r;
+                if (c < k && (all || dt[ct][r] <= lim)) m[c >> 5] |= 1u << (c & 31);
+            }
+#pragma unroll
+        for (int w = 0; w < kScreenMaxK / 32; ++w) {
+            m[w] |= xor16_u(m[w]);
+            m[w] |= xor32_u(m[w]);
+        }
+        if (lane < 16) {
+            const int slot = wave * 64 + 16 * j + lane;
+            cmask[slot * 2 + 0] = static_cast<uint64_t>(m[0]) | (static_cast<uint64_t>(m[1]) << 32);
+            cmask[slot * 2 + 1] = static_cast<uint64_t>(m[2]) | (static_cast<uint64_t>(m[3]) << 32);
+        }
+    }
+    km_wave_lds_sync();
+
+    // exact reference distance to the candidates, one token per thread
+    float x[DP];
+    km_u32x4_t xr[DP / 8];
+#pragma unroll
+    for (int i = 0; i < DP / 8; ++i)
+        xr[i] = valid ? *reinterpret_cast<const km_u32x4_t*>(kb + static_cast<int64_t>(t) * a.ts + 8 * i)
+                      : km_u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < DP / 8; ++i) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            x[8 * i + 2 * w] = bf16_lo(xr[i][w]);
+            x[8 * i + 2 * w + 1] = bf16_hi(xr[i][w]);
+        }
+    }
+    float best = 3.402823466e38f;  // FLT_MAX
+    int arg = 0;
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        uint64_t mm = cmask[tid * 2 + w];
+        while (mm) {
+            const int c = 64 * w + __builtin_ctzll(mm);
+            mm &= mm - 1;
+            const float dist = l2_lanes8<DP>(x, cs + c * CS);
+            if (dist < best) {
+                best = dist;
+                arg = c;
+            }
+        }
+    }
+    if (valid) {
+        a.labels[static_cast<int64_t>(seg) * a.T + t] = arg;
+        if (a.mind) a.mind[static_cast<int64_t>(seg) * a.T + t] = best;
+    }
+    if (a.hist == nullptr) continue;
+
+    float part = wave_sum(valid ? best : 0.0f);
+    if (lane_id() == 0) red[tid >> 6] = part;
+    const int r = block_digit_rank(arg, valid, k, bits_for(k), wcnt,
+                                   a.hist + static_cast<int64_t>(seg) * a.kmax * a.nblk, a.nblk, blk);
+    if (valid) a.rank[static_cast<int64_t>(seg) * a.T + t] = r;
+    if (tid == 0) a.ipart[static_cast<int64_t>(seg) * a.nblk + blk] = ((red[0] + red[1]) + red[2]) + red[3];
+    }
 }
 
 // ---------------------------------------------------------------- kmeans++
@@ -368,109 +603,98 @@ __global__ __launch_bounds__(256) void km_scatter_kernel(KmParams a) {
     a.sorted[so + pos] = t;
 }
 
-// M-step for one cluster.  The sum must follow the reference's order (members
-// in ascending token order, one dependent fp32 add each), so it is a single
-// chain per dimension; wave 0 runs the chains (lane d = dimension d) out of
-// LDS while waves 1..15 gather the next round of member rows into the other
-// half of a double-buffered ring (member ids are prefetched one round ahead).
-constexpr int kMsRows = 256;
-
+// M-step, one wave per cluster (four clusters per workgroup).  Lane d keeps
+// the chain of dimension d (members in ascending token order, one dependent
+// fp32 add each).  Member rows are gathered in 64-row batches (16-byte parts,
+// every lane loads one part per instruction) into a ring of NB register
+// batches, and the member ids run 2*NB batches ahead, so every wait on a
+// batch leaves the later ones in flight; a batch goes through the wave's LDS
+// tile to reach the dimension-per-lane layout of the chains.
 template <int DP>
-__global__ __launch_bounds__(1024) void km_update_kernel(KmParams a, int it, Draws draws) {
-    __shared__ uint4 buf[2][kMsRows * DP / 8];   // bf16 rows, 16-byte parts
-    __shared__ int ids[2][kMsRows];
-    const int c = blockIdx.x, seg = blockIdx.y;
+__global__ __launch_bounds__(256) void km_update_wave_kernel(KmParams a, int it, Draws draws) {
+    constexpr int PARTS = DP / 8;    // 16-byte parts per row
+    constexpr int RPL = 64 / PARTS;  // rows per load instruction
+    constexpr int LPB = PARTS;       // load instructions per 64-row batch
+    constexpr int NB = 4;            // row batches in flight
+    constexpr int NI = 2 * NB;       // id batches in flight
+    __shared__ km_u32x4_t sbuf[4][64 * PARTS];
+    const int seg = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = blockIdx.x * 4 + wave;
     const int h = seg / a.P, p = seg % a.P;
     if (c >= a.k[p]) return;
     if (a.done && a.done[seg]) return;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int32_t* off = a.off + static_cast<int64_t>(seg) * (a.kmax + 1);
     const int lo = off[c], hi = off[c + 1];
     const uint16_t* kbase = a.keys + h * a.hs + p * DP;
     float* dst = a.cent + (static_cast<int64_t>(seg) * a.kmax + c) * DP;
     if (hi == lo) {
-        if (tid < DP) {
+        if (lane < DP) {
             const int e = a.empties[static_cast<int64_t>(seg) * a.kmax + c];
             const int tok = draws.v[e];
-            dst[tid] = bf16_to_f32(kbase[static_cast<int64_t>(tok) * a.ts + tid]);
+            dst[lane] = bf16_to_f32(kbase[static_cast<int64_t>(tok) * a.ts + lane]);
         }
         return;
     }
-    const int32_t* srt = a.sorted + static_cast<int64_t>(seg) * a.T;
     const int n = hi - lo;
-    const int rounds = (n + kMsRows - 1) / kMsRows;
-    constexpr int PARTS = DP / 8;               // 16-byte parts per row
-    const int ltid = tid - 64;                   // loader index (waves 1..15)
-    // prologue: ids of rounds 0 and 1, rows of round 0
-    for (int i = tid; i < 2 * kMsRows; i += 1024) {
-        const int r = i / kMsRows, j = i - r * kMsRows;
-        const int pos = lo + r * kMsRows + j;
-        ids[r][j] = pos < hi ? srt[pos] : 0;
+    const int nb = (n + 63) >> 6;
+    const int32_t* srt = a.sorted + static_cast<int64_t>(seg) * a.T + lo;
+    const int part = lane % PARTS, rsub = lane / PARTS;
+    // ids of batch b: lane l -> member 64b + l (rows past n read token 0
+    // and are not summed)
+#define KM_LD_ID(b) ((64 * (b) + lane) < n ? srt[64 * (b) + lane] : 0)
+#define KM_LD_ROWS(idv, slot)                                                                          \
+    _Pragma("unroll") for (int u = 0; u < LPB; ++u) {                                                \
+        const int id_ = __shfl((idv), u * RPL + rsub);                                               \
+        rr[slot][u] = *reinterpret_cast<const km_u32x4_t*>(kbase + static_cast<int64_t>(id_) * a.ts + part * 8); \
     }
-    __syncthreads();
-    {
-        const int cnt = n < kMsRows ? n : kMsRows;
-        for (int i = tid; i < cnt * PARTS; i += 1024) {
-            const int row = i / PARTS, part = i - row * PARTS;
-            buf[0][row * PARTS + part] =
-                *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(ids[0][row]) * a.ts + part * 8);
+    int idr[NI];
+    km_u32x4_t rr[NB][LPB];
+#pragma unroll
+    for (int j = 0; j < NI; ++j) idr[j] = j < nb ? KM_LD_ID(j) : 0;
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+        if (j < nb) {
+            KM_LD_ROWS(idr[j], j)
         }
-    }
-    __syncthreads();
+    km_u32x4_t* buf = sbuf[wave];
+    const uint16_t* rows = reinterpret_cast<const uint16_t*>(buf);
     float acc = 0.0f;
-    for (int r = 0; r < rounds; ++r) {
-        const int b = r & 1;
-        if (wave == 0) {
-            const int cnt = (n - r * kMsRows) < kMsRows ? (n - r * kMsRows) : kMsRows;
-            if (lane < DP) {
-                const uint16_t* rows = reinterpret_cast<const uint16_t*>(buf[b]);
-                int row = 0;
-                for (; row + 8 <= cnt; row += 8) {
-                    float v[8];
+#pragma unroll 1
+    for (int b0 = 0; b0 < nb; b0 += NI) {
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) v[u] = bf16_to_f32(rows[(row + u) * DP + lane]);
+        for (int jj = 0; jj < NI; ++jj) {
+            const int b = b0 + jj;
+            if (b < nb) {
+                const int j = jj % NB;
+                // batch b: registers -> LDS tile (row-major, DP bf16 per row)
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) acc = acc + v[u];
+                for (int u = 0; u < LPB; ++u) buf[(u * RPL + rsub) * PARTS + part] = rr[j][u];
+                // refill: rows of batch b + NB (ids loaded NB batches ago),
+                // then ids of batch b + NI into the slot just used
+                if (b + NB < nb) {
+                    KM_LD_ROWS(idr[(jj + NB) % NI], j)
                 }
-                for (; row < cnt; ++row) acc = acc + bf16_to_f32(rows[row * DP + lane]);
-            }
-        } else {
-            // rows of round r + 1 (ids in ids[b ^ 1]) and ids of round r + 2
-            // (into ids[b], free since round r's rows are already in LDS):
-            // every global load is issued before any LDS store.
-            constexpr int PER = (kMsRows * PARTS + 959) / 960;
-            uint4 v[PER];
-            int slot[PER];
-            int nid = -1;
-            if (r + 1 < rounds) {
-                const int base = (r + 1) * kMsRows;
-                const int cnt = (n - base) < kMsRows ? (n - base) : kMsRows;
+                if (b + NI < nb) idr[jj] = KM_LD_ID(b + NI);
+                km_wave_lds_sync();
+                const int cnt = (n - 64 * b) < 64 ? (n - 64 * b) : 64;
+                if (lane < DP) {
+                    if (cnt == 64) {
+                        float v[64];
 #pragma unroll
-                for (int u = 0; u < PER; ++u) {
-                    const int i = ltid + u * 960;
-                    slot[u] = -1;
-                    if (i < cnt * PARTS) {
-                        const int row = i / PARTS, part = i - row * PARTS;
-                        v[u] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(ids[b ^ 1][row]) * a.ts +
-                                                               part * 8);
-                        slot[u] = i;
+                        for (int q = 0; q < 64; ++q) v[q] = bf16_to_f32(rows[q * DP + lane]);
+#pragma unroll
+                        for (int q = 0; q < 64; ++q) acc = acc + v[q];
+                    } else {
+                        for (int r = 0; r < cnt; ++r) acc = acc + bf16_to_f32(rows[r * DP + lane]);
                     }
                 }
+                km_wave_lds_sync();
             }
-            if (r + 2 < rounds && ltid < kMsRows) {
-                const int pos = lo + (r + 2) * kMsRows + ltid;
-                nid = pos < hi ? srt[pos] : 0;
-            }
-            if (r + 1 < rounds) {
-#pragma unroll
-                for (int u = 0; u < PER; ++u)
-                    if (slot[u] >= 0) buf[b ^ 1][slot[u]] = v[u];
-            }
-            if (nid >= 0) ids[b][ltid] = nid;
         }
-        __syncthreads();
     }
-    if (tid < DP) dst[tid] = acc * (1.0f / static_cast<float>(n));
+    if (lane < DP) dst[lane] = acc * (1.0f / static_cast<float>(n));
+#undef KM_LD_ID
+#undef KM_LD_ROWS
 }
 
 __global__ void km_reset_kernel(KmParams a) {
@@ -531,6 +755,24 @@ size_t workspace_bytes(const imi_kmeans_args* a, int kmax, KmParams* out) {
 
 template <int DP>
 int run_assign(const KmParams& p, int segs, hipStream_t stream) {
+    if (p.kmax <= kScreenMaxK) {
+        const size_t lds = screen_lds_bytes<DP>(p.kmax);
+        if (lds > 64 * 1024)
+            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_assign_screen_kernel<DP>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+        // as many workgroups as fit on the device at once, each over `chunks`
+        // consecutive 256-token blocks
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, km_assign_screen_kernel<DP>, 256, lds) != hipSuccess ||
+            per_cu <= 0)
+            per_cu = 1;
+        const int64_t want = static_cast<int64_t>(per_cu) * device_cus();
+        const int chunks = static_cast<int>(std::max<int64_t>(1, (static_cast<int64_t>(p.nblk) * segs + want - 1) / want));
+        const int gx = (p.nblk + chunks - 1) / chunks;
+        hipLaunchKernelGGL(km_assign_screen_kernel<DP>, dim3(gx, segs), dim3(256), lds, stream, p, chunks);
+        IMI_LAUNCH_CHECK("km_assign_screen_kernel");
+        return IMI_OK;
+    }
     const size_t lds = static_cast<size_t>(p.kmax) * DP * sizeof(float) + 4 * p.kmax * sizeof(int) + 64;
     if (lds > 64 * 1024) IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_assign_kernel<DP>),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -630,10 +872,10 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
         std::uniform_int_distribution<int32_t> dist(0, a->n_tokens - 1);
         for (int e = 0; e < kmax; ++e) dr.v[e] = dist(rng);
         if (dp == 64)
-            hipLaunchKernelGGL(km_update_kernel<64>, dim3(kmax, segs), dim3(1024), 0, stream, p, it, dr);
+            hipLaunchKernelGGL(km_update_wave_kernel<64>, dim3((kmax + 3) / 4, segs), dim3(256), 0, stream, p, it, dr);
         else
-            hipLaunchKernelGGL(km_update_kernel<32>, dim3(kmax, segs), dim3(1024), 0, stream, p, it, dr);
-        IMI_LAUNCH_CHECK("km_update_kernel");
+            hipLaunchKernelGGL(km_update_wave_kernel<32>, dim3((kmax + 3) / 4, segs), dim3(256), 0, stream, p, it, dr);
+        IMI_LAUNCH_CHECK("km_update_wave_kernel");
     }
     return IMI_OK;
 }
