@@ -190,9 +190,13 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         ks = self._layer_ks(T)
         if T < max(ks) and cfg["init"] == "first":
             raise ValueError(f"IMI layer {layer_idx}: {T} middle tokens < k = {max(ks)} (first-k initialisation)")
-        cent, labels, _ = ops.kmeans(middle_k, ks, int(cfg["max_iters"]), tol=float(cfg["tol"]),
-                                     early_stop_min_iter=int(cfg["early_stop_min_iter"]),
-                                     early_stop_rel_tol=float(cfg["early_stop_rel_tol"]), init=str(cfg["init"]))
+        km_kw = dict(tol=float(cfg["tol"]), early_stop_min_iter=int(cfg["early_stop_min_iter"]),
+                     early_stop_rel_tol=float(cfg["early_stop_rel_tol"]), init=str(cfg["init"]))
+        sample = int(cfg.get("sample_keys", 0) or 0)
+        if 0 < sample < T:   # 1M-token build: Lloyd on a strided sample, then every key assigned
+            cent, labels, _ = ops.kmeans_sampled(middle_k, ks, int(cfg["max_iters"]), sample, **km_kw)
+        else:
+            cent, labels, _ = ops.kmeans(middle_k, ks, int(cfg["max_iters"]), **km_kw)
         dev = middle_k.device
         rows = max(self.list_capacity, T)
         lk = torch.empty((1, H, rows, D), dtype=middle_k.dtype, device=dev)

@@ -42,6 +42,8 @@ struct SelParams {
     int k[4];
     int ncells;
     int nprobe, max_tokens, buffer_pages, page_size;
+    const int32_t* head_max_tokens;    // [H] or null
+    const int32_t* head_buffer_pages;  // [H] or null
     int32_t* sel_cell;
     int32_t* sel_offset;
     int32_t* sel_count;
@@ -262,7 +264,10 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     __syncthreads();
     const int n_valid = shv[1];
     const float gmax = shf[32], gmin = shf[33];
-    int kp = a.nprobe < a.buffer_pages ? a.nprobe : a.buffer_pages;
+    // this head's budgets (ragged batches), bounded by the launch-wide ones
+    const int max_tokens = a.head_max_tokens ? min(a.head_max_tokens[h], a.max_tokens) : a.max_tokens;
+    const int buffer_pages = a.head_buffer_pages ? min(a.head_buffer_pages[h], a.buffer_pages) : a.buffer_pages;
+    int kp = a.nprobe < buffer_pages ? a.nprobe : buffer_pages;
     kp = kp < n_valid ? kp : n_valid;
     int32_t* prefix_out = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
     if (kp <= 0) {
@@ -424,7 +429,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         const int r = 2 * tid + u;
         excl_tok[u] = texcl;
         pexcl += pg2[u];
-        const bool keep = r < C && r < a.nprobe && texcl < a.max_tokens && pexcl <= a.buffer_pages;
+        const bool keep = r < C && r < a.nprobe && texcl < max_tokens && pexcl <= buffer_pages;
         kept += keep ? 1 : 0;
         texcl += s2[u];
     }
@@ -569,6 +574,8 @@ int select_launch(const imi_select_args* a, hipStream_t stream) {
     p.max_tokens = a->max_tokens;
     p.buffer_pages = a->buffer_pages;
     p.page_size = a->page_size;
+    p.head_max_tokens = a->head_max_tokens;
+    p.head_buffer_pages = a->head_buffer_pages;
     p.sel_cell = a->sel_cell;
     p.sel_offset = a->sel_offset;
     p.sel_count = a->sel_count;

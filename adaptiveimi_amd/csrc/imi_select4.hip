@@ -49,6 +49,8 @@ struct Sel4 {
     const int32_t* nact;     // [H]
     int cap;
     int nprobe, max_tokens, buffer_pages, page_size;
+    const int32_t* head_max_tokens;    // [H] or null
+    const int32_t* head_buffer_pages;  // [H] or null
     int32_t* sel_cell;
     int32_t* sel_offset;
     int32_t* sel_count;
@@ -79,8 +81,17 @@ __device__ __forceinline__ int n_active(const Sel4& a, int h) {
     return na < 0 ? 0 : (na < a.cap ? na : a.cap);
 }
 
-__device__ __forceinline__ int kprime(const Sel4& a, int na) {
-    int kp = a.nprobe < a.buffer_pages ? a.nprobe : a.buffer_pages;
+// this head's budgets (ragged batches), bounded by the launch-wide ones
+__device__ __forceinline__ int head_pages(const Sel4& a, int h) {
+    return a.head_buffer_pages ? min(a.head_buffer_pages[h], a.buffer_pages) : a.buffer_pages;
+}
+__device__ __forceinline__ int head_tokens(const Sel4& a, int h) {
+    return a.head_max_tokens ? min(a.head_max_tokens[h], a.max_tokens) : a.max_tokens;
+}
+
+__device__ __forceinline__ int kprime(const Sel4& a, int h, int na) {
+    const int bp = head_pages(a, h);
+    int kp = a.nprobe < bp ? a.nprobe : bp;
     return kp < na ? kp : na;
 }
 
@@ -188,7 +199,7 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_gather_kernel(Sel4 a) {
     __shared__ int sh[16];
     const int h = blockIdx.y, tid = threadIdx.x;
     const int na = n_active(a, h);
-    const int kp = kprime(a, na);
+    const int kp = kprime(a, h, na);
     if (kp <= 0) return;
     const int bK = find_bucket(a, h, kp, sh);
     const int c = blockIdx.x * kScoreThreads + tid;
@@ -239,7 +250,7 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     __shared__ uint32_t h256[256];
     const int h = blockIdx.x, tid = threadIdx.x;
     const int na = n_active(a, h);
-    const int kp = kprime(a, na);
+    const int kp = kprime(a, h, na);
     int32_t* prefix_out = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
     const uint32_t count = a.ext[h * 4 + 2];
     int n = 0;   // sorted candidates in sk / si, best first
@@ -370,7 +381,7 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
         const int r = 2 * tid + u;
         excl_tok[u] = texcl;
         pexcl += pg2[u];
-        const bool keep = r < C && r < a.nprobe && texcl < a.max_tokens && pexcl <= a.buffer_pages;
+        const bool keep = r < C && r < a.nprobe && texcl < head_tokens(a, h) && pexcl <= head_pages(a, h);
         kept += keep ? 1 : 0;
         texcl += s2[u];
     }
@@ -479,6 +490,8 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     p.max_tokens = a->max_tokens;
     p.buffer_pages = a->buffer_pages;
     p.page_size = a->page_size;
+    p.head_max_tokens = a->head_max_tokens;
+    p.head_buffer_pages = a->head_buffer_pages;
     p.sel_cell = a->sel_cell;
     p.sel_offset = a->sel_offset;
     p.sel_count = a->sel_count;

@@ -128,6 +128,23 @@ def kmeans_assign(keys: torch.Tensor, centroids: torch.Tensor, ks: Sequence[int]
     return labels, mind
 
 
+def kmeans_sampled(keys: torch.Tensor, ks: Sequence[int], max_iters: int, sample_tokens: int, **kw):
+    """K-means on an evenly strided sample of at most ``sample_tokens`` keys
+    per head (a strided view: every ceil(T / sample_tokens)-th token, nothing
+    copied), then one assignment pass of every key with the final centroids
+    (the 1M-token build: 20 iterations on 65536 keys, then all keys).  The
+    batch-1 reference has no sampling; each half is its own reference step
+    (kmeans_core.cpp:190-314, then the E-step 222-242).  Returns
+    (centroids f32 [H, P, kmax, D/P], labels i32 [H, P, T], iters i32 [H, P])."""
+    if sample_tokens <= 0:
+        raise ValueError("sample_tokens must be positive")
+    H, T, D = keys.shape
+    step = max(1, -(-T // int(sample_tokens)))
+    cent, _, iters = kmeans(keys[:, ::step], ks, max_iters, **kw)
+    labels, _ = kmeans_assign(keys, cent, ks)
+    return cent, labels, iters
+
+
 # -------------------------------------------------------------- cell index --
 
 def build_index(keys: torch.Tensor, values: torch.Tensor, centroids: torch.Tensor, labels: torch.Tensor,
@@ -227,10 +244,15 @@ def fused_query_group_similarities(query_grouped: torch.Tensor, centroids: torch
 
 @dataclass
 class Budget:
+    """Decode budgets (runtime.py:31-63).  head_max_tokens / head_buffer_pages
+    give per-KV-head budgets for a ragged batch (the heads of several
+    sequences in one launch); the scalars are then their maxima."""
     nprobe: int
     max_tokens: int
     buffer_pages: int
     page_size: int = 8
+    head_max_tokens: Optional[Sequence[int]] = None
+    head_buffer_pages: Optional[Sequence[int]] = None
 
     @property
     def sel_cap(self) -> int:
@@ -239,6 +261,35 @@ class Budget:
     @property
     def max_rows(self) -> int:
         return self.buffer_pages * self.page_size
+
+    @classmethod
+    def ragged(cls, per_sequence: Sequence["Budget"], heads_per_sequence: int) -> "Budget":
+        """One launch over the KV heads of several sequences (sequence-major):
+        same nprobe and page size, each sequence's own token and page budget."""
+        if not per_sequence:
+            raise ValueError("ragged budget needs at least one sequence")
+        nprobe = {b.nprobe for b in per_sequence}
+        page = {b.page_size for b in per_sequence}
+        if len(nprobe) != 1 or len(page) != 1:
+            raise ValueError("sequences of one ragged launch share nprobe and page_size")
+        mt = [b.max_tokens for b in per_sequence for _ in range(heads_per_sequence)]
+        bp = [b.buffer_pages for b in per_sequence for _ in range(heads_per_sequence)]
+        return cls(nprobe.pop(), max(mt), max(bp), page.pop(), head_max_tokens=mt, head_buffer_pages=bp)
+
+
+def _budget_fields(a, budget: Budget, H: int, dev) -> Tuple[torch.Tensor, ...]:
+    """Per-head budget arrays of a ragged launch (device int32 [H]); the
+    returned tensors must outlive the call."""
+    keep = []
+    for name, vals in (("head_max_tokens", budget.head_max_tokens), ("head_buffer_pages", budget.head_buffer_pages)):
+        if vals is None:
+            continue
+        t = torch.as_tensor(list(vals), dtype=torch.int32).to(dev)
+        if t.numel() != H:
+            raise ValueError(f"{name} has {t.numel()} entries for {H} KV heads")
+        setattr(a, name, t.data_ptr())
+        keep.append(t)
+    return tuple(keep)
 
 
 def _compact_fields(a, compact: Optional[Dict[str, torch.Tensor]]) -> None:
@@ -279,6 +330,7 @@ def select(query: torch.Tensor, centroids: torch.Tensor, cell_count: torch.Tenso
                    sel_prefix=out["sel_prefix"].data_ptr(), n_selected=out["n_selected"].data_ptr(),
                    n_rows=out["n_rows"].data_ptr(), sel_cap=cap)
     _compact_fields(a, compact)
+    keep = _budget_fields(a, budget, H, dev)
     need = ctypes.c_size_t()
     check(_lib.lib().imi_select_workspace_size(ctypes.byref(a), ctypes.byref(need)), "imi_select_workspace_size")
     if need.value:
@@ -351,6 +403,7 @@ class DecodePlan:
         s.buffer_pages, s.page_size = budget.buffer_pages, budget.page_size
         s.sel_cap = budget.sel_cap
         _compact_fields(s, compact)
+        self._keep_budget = _budget_fields(s, budget, H, dev)
         t = a.attn
         t.query = self.query.data_ptr()
         t.steady_keys = _ptr(steady_keys)

@@ -178,6 +178,13 @@ typedef struct {
     int32_t compact_cap;
     void* workspace;
     size_t workspace_bytes;         /* >= imi_select_workspace_size() */
+    /* Ragged batches (the heads of several sequences in one call, no
+     * counterpart in the batch-1 reference): per-head token and page budgets,
+     * device int32 [H], or NULL for max_tokens / buffer_pages on every head.
+     * Each per-head value is clamped to its scalar, so the scalars must be
+     * the largest budgets (they size sel_cap and the attention's max_rows). */
+    const int32_t* head_max_tokens;
+    const int32_t* head_buffer_pages;
 } imi_select_args;
 
 /* Workspace imi_select needs (0 for 2-way IMI). */

@@ -33,7 +33,7 @@ def test_exports_every_declared_symbol(L):
 
 
 def test_version(L):
-    assert L.imi_version() == 2
+    assert L.imi_version() == 3
 
 
 def _kmeans_args(**over):

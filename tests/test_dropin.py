@@ -93,6 +93,17 @@ def test_index_stats_before_build():
     assert s["total_heads"] == 16 and math.isclose(s["ideal_clusters_per_head"], 6000 / 16)
 
 
+def test_ragged_budget_rules():
+    """Per-head budgets of a ragged launch (sequence-major heads)."""
+    from adaptiveimi_amd import ops as o
+
+    b = o.Budget.ragged([o.Budget(102, 300, 38), o.Budget(102, 1200, 150)], 2)
+    assert (b.max_tokens, b.buffer_pages, b.sel_cap) == (1200, 150, 102)
+    assert b.head_max_tokens == [300, 300, 1200, 1200] and b.head_buffer_pages == [38, 38, 150, 150]
+    with pytest.raises(ValueError, match="share nprobe"):
+        o.Budget.ragged([o.Budget(102, 300, 38), o.Budget(50, 1200, 150)], 2)
+
+
 # ----------------------------------------------------------------- GPU --
 
 def _bits(t):

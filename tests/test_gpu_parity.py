@@ -140,6 +140,26 @@ def test_kmeans_plusplus_wide_range_sequential_path(ops, oracle):
         assert np.array_equal(labels.cpu().numpy()[0, p], labs[p]), p
 
 
+@pytest.mark.parametrize("T,sample,ks", [(24000, 6000, (32, 32)), (20001, 4096, (8, 8, 8, 8))])
+def test_kmeans_sampled_then_assign(ops, oracle, T, sample, ks):
+    """The 1M-token build at reduced scale: k-means on every ceil(T/sample)-th
+    key, then every key assigned to the final centroids -- bit-exact with the
+    oracle's Lloyd run on the same sample and its E-step over all keys."""
+    note(f"[kmeans] sampled T={T} sample={sample} ks={ks}")
+    H = 2
+    keys, _ = _kv(H, T, seed=17)
+    cent, labels, _ = ops.kmeans_sampled(keys.to(DEV), list(ks), 4, sample)
+    step = -(-T // sample)
+    kf = oracle.bf16_to_f32(bits(keys))
+    sl = oracle.subspace_slices(128, len(ks))
+    for h in range(H):
+        rl, rc, _ = oracle.kmeans_head(kf[h, ::step], list(ks), 4)
+        for p in range(len(ks)):
+            assert np.array_equal(cent[h, p, : ks[p]].cpu().numpy(), rc[p]), (h, p)
+            lab, _, _ = oracle.estep(np.ascontiguousarray(kf[h][:, sl[p]]), rc[p])
+            assert np.array_equal(labels[h, p].cpu().numpy(), lab), (h, p)
+
+
 def test_kmeans_empty_cluster_reseed(ops, oracle):
     """Duplicate first rows make clusters empty in iteration 0; the GPU must
     re-seed them from the same mt19937 draws as the reference."""
@@ -428,6 +448,75 @@ def test_decode_step_matches_oracle(ops, oracle, T, ks, G, static_len):
     sel = plan.selection
     assert np.array_equal(sel["n_selected"].cpu().numpy(), rm)
     _check_attention(res, ref)
+
+
+@pytest.mark.parametrize("ks", [(32, 32), (6, 6, 6, 6)])
+def test_ragged_batch_decode_matches_oracle(ops, oracle, ks):
+    """Config 2 at reduced scale: the KV heads of four sequences of different
+    lengths (so different token and page budgets) share one selection and
+    attention launch, their lists living in one [B*H, max_len, D] buffer.
+    Every sequence must match its own batch-1 oracle step: same selected
+    cells, attention within 2e-2 + 1e-2 |ref|."""
+    from adaptiveimi_amd import synthetic
+
+    lens = [3000, 6000, 9000, 12000]
+    note(f"[ragged] lens={lens} ks={ks}")
+    H, G, D, static_len = 4, 7, 128, 96
+    B, cap = len(lens), max(lens)
+    lk = torch.zeros((B * H, cap, D), dtype=torch.bfloat16, device=DEV)
+    lv = torch.zeros_like(lk)
+    sk, sv = synthetic.make_kv(B * H, static_len + 4, seed=91)
+    cents, counts, offsets, compacts, buds, per_seq = [], [], [], [], [], []
+    ncells = int(np.prod(ks))
+    for s_, T in enumerate(lens):
+        keys, values = synthetic.make_kv(H, T, seed=300 + s_)
+        kd, vd = keys.to(DEV), values.to(DEV)
+        cent, labels, _ = ops.kmeans(kd, list(ks), 3)
+        out = ops.build_index(kd, vd, cent, labels, list(ks), n_centroids=min(T, ncells) + 1 if len(ks) == 4 else None,
+                              list_keys=lk[s_ * H:(s_ + 1) * H], list_values=lv[s_ * H:(s_ + 1) * H])
+        cents.append(cent)
+        counts.append(out["cell_count"])
+        offsets.append(out["cell_offset"])
+        compacts.append(out)
+        sz = oracle.sizing(T, 0.1, k_override=ks)
+        buds.append(ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"]))
+        per_seq.append((keys, sz))
+    bud = ops.Budget.ragged(buds, H)
+    compact = None
+    if len(ks) == 4:
+        width = max(c["compact_gid"].shape[1] for c in compacts)
+
+        def pad(name, extra=0):
+            return torch.cat([torch.nn.functional.pad(c[name], (0, width + extra - c[name].shape[1])) for c in compacts])
+
+        compact = dict(compact_gid=pad("compact_gid"), compact_size=pad("compact_size"),
+                       compact_offset=pad("compact_offset", 1), n_active=torch.cat([c["n_active"] for c in compacts]))
+    plan = ops.DecodePlan(torch.cat(cents), torch.cat(counts), torch.cat(offsets), ks, bud, lk, lv, sk.to(DEV),
+                          sv.to(DEV), G, compact=compact)
+    plan.set_static_len(static_len)
+    q = torch.cat([synthetic.make_queries(per_seq[s_][0], G, seed=20 + s_)[0] for s_ in range(B)])
+    plan.query.copy_(q.to(DEV))
+    res = plan.step().clone().float().cpu().numpy().reshape(B * H, G, D)
+    sel = plan.selection
+    m_all = sel["n_selected"].cpu().numpy()
+    cells_all = sel["sel_cell"].cpu().numpy()
+    for s_ in range(B):
+        out, (keys, sz) = compacts[s_], per_seq[s_]
+        hs = slice(s_ * H, (s_ + 1) * H)
+        heads = []
+        for h in range(H):
+            na = int(out["n_active"][h])
+            heads.append(dict(n_active=na, offsets=out["compact_offset"][h, : na + 1].cpu().numpy(),
+                              merged=out["compact_centroids"][h, :na].cpu().numpy(),
+                              list_keys=bits(lk[s_ * H + h, : lens[s_]]), list_values=bits(lv[s_ * H + h, : lens[s_]])))
+        ref, rs, rm, _ = oracle.decode_step(bits(q[hs]), heads, bits(sk[hs]), bits(sv[hs]), static_len,
+                                            sz["n_centroids"], sz["nprobe"], sz["max_tokens"], sz["buffer_pages"])
+        assert np.array_equal(m_all[hs], rm), (s_, m_all[hs], rm)
+        gids = out["compact_gid"].cpu().numpy()
+        for h in range(H):
+            assert np.array_equal(cells_all[s_ * H + h, : rm[h]], gids[h][rs[h, : rm[h]]]), (s_, h)
+        err = np.abs(res[hs] - ref)
+        assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)), (s_, float(err.max()))
 
 
 def test_attention_standalone_and_lse(ops, oracle):
