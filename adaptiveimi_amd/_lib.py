@@ -52,7 +52,7 @@ class SelectArgs(ctypes.Structure):
         ("n_selected", _vp), ("n_rows", _vp), ("sel_cap", _i32),
         ("compact_gid", _vp), ("compact_size", _vp), ("compact_offset", _vp), ("n_active", _vp),
         ("compact_cap", _i32), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
-        ("head_max_tokens", _vp), ("head_buffer_pages", _vp),
+        ("head_max_tokens", _vp), ("head_buffer_pages", _vp), ("tile_mode", _i32),
     ]
 
 

@@ -21,6 +21,7 @@ host; their constructor arguments are accepted and recorded.
 from __future__ import annotations
 
 import math
+import os
 import warnings
 from typing import Dict, List, Optional
 
@@ -293,7 +294,10 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         if plan is None:
             if not self.cache_prepared:
                 self.prepare_cache()
-            bud = ops.Budget(self.nprobe, self.max_retrieval_tokens, self.buffer_size, self.page_size)
+            # IMI_MAX_TILES != 0 selects the reference's tile mode (retrieval.py:373-382)
+            tiles = int(os.getenv("IMI_MAX_TILES", "0") or 0) != 0
+            bud = ops.Budget(self.nprobe, self.max_retrieval_tokens, self.buffer_size, self.page_size,
+                             tile_mode=tiles)
             plan = ops.DecodePlan(self.centroids[layer_idx], self.cell_count[layer_idx], self.cell_offset[layer_idx],
                                   self.layer_ks[layer_idx], bud, self.list_keys[layer_idx][0],
                                   self.list_values[layer_idx][0], self.steady_zone_keys[layer_idx][0],

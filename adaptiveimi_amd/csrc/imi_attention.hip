@@ -597,9 +597,12 @@ int decode_validate(const imi_decode_args* a) {
     IMI_REQUIRE(a != nullptr, IMI_ERR_INVALID, "imi_decode_step: null args");
     IMI_REQUIRE(a->sel.kv_heads == a->attn.kv_heads && a->sel.groups == a->attn.groups,
                 IMI_ERR_INVALID, "imi_decode_step: selection and attention shapes differ");
-    IMI_REQUIRE(a->attn.max_rows >= a->sel.buffer_pages * a->sel.page_size, IMI_ERR_INVALID,
-                "imi_decode_step: max_rows %d < buffer_pages * page_size %d", a->attn.max_rows,
-                a->sel.buffer_pages * a->sel.page_size);
+    // selected rows: at most buffer_pages pages, or in tile mode the token
+    // budget plus one cell of at most buffer_pages pages
+    const int64_t need_rows = static_cast<int64_t>(a->sel.buffer_pages) * a->sel.page_size +
+                              (a->sel.tile_mode ? static_cast<int64_t>(a->sel.max_tokens) : 0);
+    IMI_REQUIRE(a->attn.max_rows >= need_rows, IMI_ERR_INVALID, "imi_decode_step: max_rows %d < %lld selectable rows",
+                a->attn.max_rows, static_cast<long long>(need_rows));
     return attn_validate(&a->attn, false);
 }
 }  // namespace

@@ -44,6 +44,7 @@ struct SelParams {
     int nprobe, max_tokens, buffer_pages, page_size;
     const int32_t* head_max_tokens;    // [H] or null
     const int32_t* head_buffer_pages;  // [H] or null
+    int tile_mode;
     int32_t* sel_cell;
     int32_t* sel_offset;
     int32_t* sel_count;
@@ -267,7 +268,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     // this head's budgets (ragged batches), bounded by the launch-wide ones
     const int max_tokens = a.head_max_tokens ? min(a.head_max_tokens[h], a.max_tokens) : a.max_tokens;
     const int buffer_pages = a.head_buffer_pages ? min(a.head_buffer_pages[h], a.buffer_pages) : a.buffer_pages;
-    int kp = a.nprobe < buffer_pages ? a.nprobe : buffer_pages;
+    // every kept cell costs a page, except in tile mode (no running page cut)
+    int kp = a.tile_mode ? a.nprobe : (a.nprobe < buffer_pages ? a.nprobe : buffer_pages);
     kp = kp < n_valid ? kp : n_valid;
     int32_t* prefix_out = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
     if (kp <= 0) {
@@ -415,6 +417,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         const int r = 2 * tid + u;
         s2[u] = r < C ? ss[r] : 0;
         pg2[u] = (s2[u] + a.page_size - 1) / a.page_size;
+        // tile mode counts the cells that alone overflow the page budget
+        if (a.tile_mode) pg2[u] = pg2[u] > buffer_pages ? 1 : 0;
         tsum += s2[u];
         psum += pg2[u];
     }
@@ -429,7 +433,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         const int r = 2 * tid + u;
         excl_tok[u] = texcl;
         pexcl += pg2[u];
-        const bool keep = r < C && r < a.nprobe && texcl < max_tokens && pexcl <= buffer_pages;
+        const bool keep = r < C && r < a.nprobe && texcl < max_tokens && pexcl <= (a.tile_mode ? 0 : buffer_pages);
         kept += keep ? 1 : 0;
         texcl += s2[u];
     }
@@ -525,11 +529,10 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     ncells = static_cast<int64_t>(a->k[0]) * a->k[1];
     IMI_REQUIRE(a->k[0] <= 128 && a->k[1] <= 128 && a->k[0] <= 16 * (kSelThreads / a->k[1]), IMI_ERR_UNSUPPORTED,
                 "imi_select: k = (%d, %d) exceeds the cells one workgroup holds", a->k[0], a->k[1]);
-    const int kprime = a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages;
-    IMI_REQUIRE(kprime <= kCap, IMI_ERR_UNSUPPORTED, "imi_select: min(nprobe, buffer_pages)=%d exceeds %d", kprime,
-                kCap);
-    IMI_REQUIRE(a->sel_cap >= kprime, IMI_ERR_INVALID, "imi_select: sel_cap %d < min(nprobe, buffer_pages) %d",
-                a->sel_cap, kprime);
+    const int kprime = a->tile_mode ? a->nprobe : (a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages);
+    IMI_REQUIRE(kprime <= kCap, IMI_ERR_UNSUPPORTED, "imi_select: %d cells to rank exceed %d", kprime, kCap);
+    IMI_REQUIRE(a->sel_cap >= kprime, IMI_ERR_INVALID, "imi_select: sel_cap %d < %d (%s)", a->sel_cap, kprime,
+                a->tile_mode ? "nprobe" : "min(nprobe, buffer_pages)");
     return IMI_OK;
 }
 
@@ -576,6 +579,7 @@ int select_launch(const imi_select_args* a, hipStream_t stream) {
     p.page_size = a->page_size;
     p.head_max_tokens = a->head_max_tokens;
     p.head_buffer_pages = a->head_buffer_pages;
+    p.tile_mode = a->tile_mode != 0;
     p.sel_cell = a->sel_cell;
     p.sel_offset = a->sel_offset;
     p.sel_count = a->sel_count;

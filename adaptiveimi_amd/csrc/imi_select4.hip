@@ -22,8 +22,11 @@
 //                       then the token and page budgets in rank order
 //
 // Outputs have the 2-way layout (cells in rank order, CSR offset, count,
-// exclusive row prefix, m, rows), so the gather kernel is shared.  The final
-// kernel zeroes the histogram and counters again for the next call.
+// exclusive row prefix, m, rows), so the gather kernel is shared.  The
+// per-head range and counter words live at a fixed place of the workspace
+// and the final kernel zeroes them again, the score kernel clears the
+// histogram and the histogram kernel the candidate counter, so a workspace
+// zero-filled once serves later calls of any shape.
 #include "imi_common.hpp"
 
 namespace imi {
@@ -37,6 +40,7 @@ constexpr int kMaxG4 = 8;        // query heads per KV head
 constexpr int kScoreThreads = 256;
 constexpr int kFinalThreads = 1024;
 constexpr int kSelCap4 = 2048;   // min(nprobe, buffer_pages) bound
+constexpr int kExtHeads = 1024;  // KV heads one call handles (fixed-place counters)
 
 struct Sel4 {
     const uint16_t* q;
@@ -51,6 +55,7 @@ struct Sel4 {
     int nprobe, max_tokens, buffer_pages, page_size;
     const int32_t* head_max_tokens;    // [H] or null
     const int32_t* head_buffer_pages;  // [H] or null
+    int tile_mode;
     int32_t* sel_cell;
     int32_t* sel_offset;
     int32_t* sel_count;
@@ -91,7 +96,7 @@ __device__ __forceinline__ int head_tokens(const Sel4& a, int h) {
 
 __device__ __forceinline__ int kprime(const Sel4& a, int h, int na) {
     const int bp = head_pages(a, h);
-    int kp = a.nprobe < bp ? a.nprobe : bp;
+    int kp = a.tile_mode ? a.nprobe : (a.nprobe < bp ? a.nprobe : bp);
     return kp < na ? kp : na;
 }
 
@@ -113,6 +118,9 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
         const float* cp = a.cent + (static_cast<int64_t>(h) * 4 + p) * a.kmax * kDp4;
         for (int i = tid; i < a.k[p] * kDp4; i += kScoreThreads) cs[p][i / kDp4][i % kDp4] = cp[i];
     }
+    // this head's histogram starts at zero (the histogram kernel is the next launch)
+    for (int i = blockIdx.x * kScoreThreads + tid; i < kBins4; i += gridDim.x * kScoreThreads)
+        a.hist[static_cast<int64_t>(h) * kBins4 + i] = 0;
     __syncthreads();
     const int c = blockIdx.x * kScoreThreads + tid;
     const int na = n_active(a, h);
@@ -156,6 +164,7 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_hist_kernel(Sel4 a) {
     __syncthreads();
     const int c = blockIdx.x * kScoreThreads + tid;
     const int na = n_active(a, h);
+    if (blockIdx.x == 0 && tid == 0) a.ext[h * 4 + 2] = 0;   // candidate counter of the gather kernel
     const uint32_t okmax = a.ext[h * 4 + 0], okmin = ~a.ext[h * 4 + 1];
     const float gmax = key_score(static_cast<uint64_t>(okmax) << 32);
     const float gmin = key_score(static_cast<uint64_t>(okmin) << 32);
@@ -367,6 +376,7 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
             s2[u] = a.csize[static_cast<int64_t>(h) * a.cap + c2[u]];
         }
         pg2[u] = (s2[u] + a.page_size - 1) / a.page_size;
+        if (a.tile_mode) pg2[u] = pg2[u] > head_pages(a, h) ? 1 : 0;   // cells that alone overflow
         tsum += s2[u];
         psum += pg2[u];
     }
@@ -381,7 +391,8 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
         const int r = 2 * tid + u;
         excl_tok[u] = texcl;
         pexcl += pg2[u];
-        const bool keep = r < C && r < a.nprobe && texcl < head_tokens(a, h) && pexcl <= head_pages(a, h);
+        const bool keep = r < C && r < a.nprobe && texcl < head_tokens(a, h) &&
+                          pexcl <= (a.tile_mode ? 0 : head_pages(a, h));
         kept += keep ? 1 : 0;
         texcl += s2[u];
     }
@@ -417,17 +428,19 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
         a.n_rows[h] = 0;
         prefix_out[0] = 0;
     }
-    // leave the workspace zeroed for the next call
-    for (int i = tid; i < kBins4; i += kFinalThreads) a.hist[static_cast<int64_t>(h) * kBins4 + i] = 0;
+    // leave the range words zero for the next call
     if (tid < 4) a.ext[h * 4 + tid] = 0;
 }
 
 size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
     Carver cv(a->workspace);
     const size_t H = a->kv_heads;
-    uint64_t* keys = cv.take<uint64_t>(H * a->compact_cap);
+    // The range/counter words sit at a fixed place for every shape and every
+    // call leaves them zero, so one zero-filled buffer serves calls of any
+    // shape; the histogram is cleared by the score kernel of each call.
+    uint32_t* ext = cv.take<uint32_t>(static_cast<size_t>(kExtHeads) * 4);
     uint32_t* hist = cv.take<uint32_t>(H * kBins4);
-    uint32_t* ext = cv.take<uint32_t>(H * 4);
+    uint64_t* keys = cv.take<uint64_t>(H * a->compact_cap);
     uint64_t* cand = cv.take<uint64_t>(H * kCand4);
     int32_t* cidx = cv.take<int32_t>(H * kCand4);
     if (p) {
@@ -444,6 +457,8 @@ size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
 
 int select4_validate(const imi_select_args* a) {
     IMI_REQUIRE(a->dim == 128 && a->parts == 4, IMI_ERR_UNSUPPORTED, "imi_select: 4-way path needs D=128, parts=4");
+    IMI_REQUIRE(a->kv_heads <= kExtHeads, IMI_ERR_UNSUPPORTED, "imi_select: 4-way path handles at most %d KV heads",
+                kExtHeads);
     IMI_REQUIRE(a->groups >= 1 && a->groups <= kMaxG4, IMI_ERR_UNSUPPORTED,
                 "imi_select: %d query heads per kv head exceed %d", a->groups, kMaxG4);
     for (int p = 0; p < 4; ++p)
@@ -451,11 +466,12 @@ int select4_validate(const imi_select_args* a) {
                     "imi_select: 4-way k[%d]=%d outside [1,%d]", p, a->k[p], kK4);
     IMI_REQUIRE(a->compact_gid && a->compact_size && a->compact_offset && a->n_active && a->compact_cap > 0,
                 IMI_ERR_INVALID, "imi_select: 4-way selection needs the compact cell arrays");
-    const int kprime_max = a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages;
-    IMI_REQUIRE(kprime_max <= kSelCap4, IMI_ERR_UNSUPPORTED, "imi_select: min(nprobe, buffer_pages)=%d exceeds %d",
-                kprime_max, kSelCap4);
-    IMI_REQUIRE(a->sel_cap >= kprime_max, IMI_ERR_INVALID, "imi_select: sel_cap %d < min(nprobe, buffer_pages) %d",
-                a->sel_cap, kprime_max);
+    const int kprime_max =
+        a->tile_mode ? a->nprobe : (a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages);
+    IMI_REQUIRE(kprime_max <= kSelCap4, IMI_ERR_UNSUPPORTED, "imi_select: %d cells to rank exceed %d", kprime_max,
+                kSelCap4);
+    IMI_REQUIRE(a->sel_cap >= kprime_max, IMI_ERR_INVALID, "imi_select: sel_cap %d < %d (%s)", a->sel_cap,
+                kprime_max, a->tile_mode ? "nprobe" : "min(nprobe, buffer_pages)");
     return IMI_OK;
 }
 
@@ -492,6 +508,7 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     p.page_size = a->page_size;
     p.head_max_tokens = a->head_max_tokens;
     p.head_buffer_pages = a->head_buffer_pages;
+    p.tile_mode = a->tile_mode != 0;
     p.sel_cell = a->sel_cell;
     p.sel_offset = a->sel_offset;
     p.sel_count = a->sel_count;

@@ -253,13 +253,18 @@ class Budget:
     page_size: int = 8
     head_max_tokens: Optional[Sequence[int]] = None
     head_buffer_pages: Optional[Sequence[int]] = None
+    tile_mode: bool = False   # IMI_MAX_TILES != 0 (retrieval.py:30-112, 452-527)
 
     @property
     def sel_cap(self) -> int:
+        if self.tile_mode:
+            return max(1, self.nprobe)
         return max(1, min(self.nprobe, self.buffer_pages))
 
     @property
     def max_rows(self) -> int:
+        if self.tile_mode:   # the token budget plus one cell of at most buffer_pages pages
+            return self.max_tokens + self.buffer_pages * self.page_size
         return self.buffer_pages * self.page_size
 
     @classmethod
@@ -274,7 +279,11 @@ class Budget:
             raise ValueError("sequences of one ragged launch share nprobe and page_size")
         mt = [b.max_tokens for b in per_sequence for _ in range(heads_per_sequence)]
         bp = [b.buffer_pages for b in per_sequence for _ in range(heads_per_sequence)]
-        return cls(nprobe.pop(), max(mt), max(bp), page.pop(), head_max_tokens=mt, head_buffer_pages=bp)
+        tiles = {b.tile_mode for b in per_sequence}
+        if len(tiles) != 1:
+            raise ValueError("sequences of one ragged launch share tile_mode")
+        return cls(nprobe.pop(), max(mt), max(bp), page.pop(), head_max_tokens=mt, head_buffer_pages=bp,
+                   tile_mode=tiles.pop())
 
 
 def _budget_fields(a, budget: Budget, H: int, dev) -> Tuple[torch.Tensor, ...]:
@@ -331,6 +340,7 @@ def select(query: torch.Tensor, centroids: torch.Tensor, cell_count: torch.Tenso
                    n_rows=out["n_rows"].data_ptr(), sel_cap=cap)
     _compact_fields(a, compact)
     keep = _budget_fields(a, budget, H, dev)
+    a.tile_mode = int(bool(budget.tile_mode))
     need = ctypes.c_size_t()
     check(_lib.lib().imi_select_workspace_size(ctypes.byref(a), ctypes.byref(need)), "imi_select_workspace_size")
     if need.value:
@@ -404,6 +414,7 @@ class DecodePlan:
         s.sel_cap = budget.sel_cap
         _compact_fields(s, compact)
         self._keep_budget = _budget_fields(s, budget, H, dev)
+        s.tile_mode = int(bool(budget.tile_mode))
         t = a.attn
         t.query = self.query.data_ptr()
         t.steady_keys = _ptr(steady_keys)

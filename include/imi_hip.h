@@ -169,8 +169,9 @@ typedef struct {
     int32_t* n_rows;          /* [H] selected rows (sum of sel_count) */
     int32_t sel_cap;          /* >= min(nprobe, buffer_pages) */
     /* 4-way IMI (parts == 4) only: occupied cells in ascending global id,
-     * the compact outputs of imi_build_index, and a zero-filled workspace
-     * (every call leaves it zero again). */
+     * the compact outputs of imi_build_index, and a workspace zero-filled
+     * before its first use (calls of any shape may then share it; calls
+     * that overlap in time may not).  At most 1024 KV heads. */
     const int32_t* compact_gid;     /* [H][compact_cap] */
     const int32_t* compact_size;    /* [H][compact_cap] */
     const int32_t* compact_offset;  /* [H][compact_cap + 1] */
@@ -185,6 +186,14 @@ typedef struct {
      * the largest budgets (they size sel_cap and the attention's max_rows). */
     const int32_t* head_max_tokens;
     const int32_t* head_buffer_pages;
+    /* Tile mode (IMI_MAX_TILES != 0 in the reference; retrieval.py:30-112,
+     * 452-527): the cells kept by nprobe and the token budget are not cut by
+     * the running page total -- the reference attends them tile by tile
+     * (each tile at most buffer_pages pages, outputs merged by LSE) -- and a
+     * head stops at its first cell that alone needs more than buffer_pages
+     * pages.  Selected rows then reach max_tokens - 1 + buffer_pages *
+     * page_size, and sel_cap must cover nprobe.  0 = off. */
+    int32_t tile_mode;
 } imi_select_args;
 
 /* Workspace imi_select needs (0 for 2-way IMI). */

@@ -366,6 +366,32 @@ def select(sc: np.ndarray, sizes: np.ndarray, mask: np.ndarray, nprobe: int, max
     return sel, m, tok
 
 
+def select_tiles(sc: np.ndarray, sizes: np.ndarray, mask: np.ndarray, nprobe: int, max_tokens: int,
+                 buffer_pages: int, page_size: int = 8):
+    """Tile mode (IMI_MAX_TILES != 0): retrieval.py:295-303 (topk + token
+    budget) then _build_cluster_tiles (retrieval.py:30-112).  Tiles group the
+    kept cells in rank order so that each tile holds at most buffer_pages
+    pages; a cell whose own page count exceeds buffer_pages can join no tile,
+    so its head stops there.  Every tile is attended and the tiles are merged
+    by LSE (retrieval.py:452-527), i.e. the attended set is the union of the
+    tiles.  Returns (sel, m, tokens) like select()."""
+    big = np.iinfo(np.int32).max // 2
+    sel, m, _ = select(sc, sizes, mask, nprobe, max_tokens, big, page_size)
+    H = sel.shape[0]
+    tok = np.zeros(H, np.int64)
+    for h in range(H):
+        cut = int(m[h])
+        for r in range(int(m[h])):
+            pages = (int(sizes[h, sel[h, r]]) + page_size - 1) // page_size
+            if pages > buffer_pages:
+                cut = r
+                break
+        sel[h, cut:] = -1
+        m[h] = cut
+        tok[h] = int(sum(int(sizes[h, c]) for c in sel[h, :cut]))
+    return sel, m, tok
+
+
 def selected_rows(sel: np.ndarray, m: np.ndarray, offsets: np.ndarray) -> List[np.ndarray]:
     """CSR rows of the selected cells per head, in rank order."""
     out = []
@@ -399,16 +425,18 @@ def attention(q_bits: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, rows: 
 
 def decode_step(q_bits: np.ndarray, heads: List[dict], steady_k: np.ndarray, steady_v: np.ndarray,
                 static_len: int, n_centroids: int, nprobe: int, max_tokens: int, buffer_pages: int,
-                page_size: int = 8):
-    """One sparse_attention call (retrieval.py:320-602, tile mode off):
-    scores -> mask -> select -> execution buffer [static rows | selected rows]
+                page_size: int = 8, tile_mode: bool = False):
+    """One sparse_attention call (retrieval.py:320-602): scores -> mask ->
+    select (select_tiles in tile mode) -> execution buffer [static rows |
+    selected rows]
     (copy_kernel.cuh:220-335) -> attention.  steady_k/v: bf16 bits
     [H, static_cap, D].  Returns (out f64 [H,G,D], sel, m, rows per head as
     indices into the per-head CSR list)."""
     H, G, D = q_bits.shape
     sizes, offsets, cent, mask = pad_metadata(heads, n_centroids, D)
     sc = scores(q_bits, cent)
-    sel, m, tok = select(sc, sizes, mask, nprobe, max_tokens, buffer_pages, page_size)
+    pick = select_tiles if tile_mode else select
+    sel, m, tok = pick(sc, sizes, mask, nprobe, max_tokens, buffer_pages, page_size)
     rows = selected_rows(sel, m, offsets)
     width = max(static_len + len(r) for r in rows)
     ek = np.zeros((H, max(width, 1), D), np.uint16)

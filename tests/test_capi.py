@@ -33,7 +33,7 @@ def test_exports_every_declared_symbol(L):
 
 
 def test_version(L):
-    assert L.imi_version() == 3
+    assert L.imi_version() == 4
 
 
 def _kmeans_args(**over):
@@ -95,7 +95,7 @@ def test_select_and_decode_argument_checks(L):
     s.compact_cap = 4096
     s.nprobe = s.buffer_pages = 3000
     assert L.imi_select(ctypes.byref(s), None) == 3          # top-k beyond the 4-way bound
-    assert "exceeds 2048" in L.imi_last_error().decode()
+    assert "exceed 2048" in L.imi_last_error().decode()
     s.nprobe = s.buffer_pages = 410
     s.sel_cell = s.sel_offset = s.sel_count = s.sel_prefix = s.n_selected = s.n_rows = 16
     need = ctypes.c_size_t()

@@ -392,6 +392,62 @@ def test_select_4way_massive_ties(ops, oracle, qmode):
     assert np.array_equal(sel["n_rows"].cpu().numpy(), rtok)
 
 
+def test_select_4way_workspace_reuse_across_shapes(ops, oracle):
+    """ops.select shares one 4-way workspace between calls; calls of a
+    different head count and compact width must not see each other's state."""
+    note("[select4] workspace reuse across shapes")
+    from adaptiveimi_amd import synthetic
+
+    for H, T, ks in ((2, 9000, (8, 8, 8, 8)), (8, 12000, (6, 6, 6, 6)), (3, 20000, (10, 10, 10, 10)),
+                     (2, 9000, (8, 8, 8, 8))):
+        keys, values = _kv(H, T, seed=H + T)
+        kd, vd = keys.to(DEV), values.to(DEV)
+        cent, labels, _ = ops.kmeans(kd, list(ks), 2)
+        ncells = int(np.prod(ks))
+        out = ops.build_index(kd, vd, cent, labels, list(ks), n_centroids=min(T, ncells) + 1)
+        bud = ops.Budget(min(200, ncells), 1500, 60)
+        q = synthetic.make_queries(keys, 4, seed=3)[0]
+        sel = ops.select(q.to(DEV), cent, out["cell_count"], out["cell_offset"], ks, bud, compact=out)
+        sc = oracle.scores(bits(q), out["compact_centroids"].cpu().numpy())
+        rs, rm, rtok = oracle.select(sc, out["compact_size"].cpu().numpy(), out["compact_mask"].cpu().numpy(),
+                                     bud.nprobe, bud.max_tokens, bud.buffer_pages)
+        assert np.array_equal(sel["n_selected"].cpu().numpy(), rm), (H, T, ks)
+        gids = out["compact_gid"].cpu().numpy()
+        for h in range(H):
+            assert np.array_equal(sel["sel_cell"].cpu().numpy()[h, : rm[h]], gids[h][rs[h, : rm[h]]]), (H, h)
+
+
+@pytest.mark.parametrize("ks,pages", [((32, 32), 3), ((32, 32), 40), ((8, 8, 8, 8), 2)])
+def test_select_tile_mode_bit_exact(ops, oracle, ks, pages):
+    """Tile mode (IMI_MAX_TILES != 0): the kept cells are not cut by the
+    running page total, and a head stops at its first cell that alone needs
+    more than buffer_pages pages (retrieval.py:30-112).  Small page budgets
+    make such cells common."""
+    note(f"[select] tile mode ks={ks} pages={pages}")
+    H, T, G = 8, 12000, 4
+    keys, values = _kv(H, T, seed=61)
+    kd, vd = keys.to(DEV), values.to(DEV)
+    cent, labels, _ = ops.kmeans(kd, list(ks), 3)
+    ncells = int(np.prod(ks))
+    out = ops.build_index(kd, vd, cent, labels, list(ks), n_centroids=min(T, ncells) + 1 if len(ks) == 4 else None)
+    bud = ops.Budget(min(300, ncells), 2500, pages, tile_mode=True)
+    from adaptiveimi_amd import synthetic
+
+    q = synthetic.make_queries(keys, G, seed=8)[0]
+    sel = ops.select(q.to(DEV), cent, out["cell_count"], out["cell_offset"], ks, bud,
+                     compact=out if len(ks) == 4 else None)
+    sc = oracle.scores(bits(q), out["compact_centroids"].cpu().numpy())
+    rs, rm, rtok = oracle.select_tiles(sc, out["compact_size"].cpu().numpy(), out["compact_mask"].cpu().numpy(),
+                                       bud.nprobe, bud.max_tokens, bud.buffer_pages)
+    gids = out["compact_gid"].cpu().numpy()
+    m = sel["n_selected"].cpu().numpy()
+    assert np.array_equal(m, rm), (m, rm)
+    for h in range(H):
+        assert np.array_equal(sel["sel_cell"].cpu().numpy()[h, : m[h]], gids[h][rs[h, : rm[h]]]), h
+    assert np.array_equal(sel["n_rows"].cpu().numpy(), rtok)
+    assert rm.max() > 0
+
+
 def test_select_ties_integer_data(ops, oracle):
     """Integer keys/queries: many exactly tied scores; order must be by cell id."""
     note("[select] ties")
@@ -418,17 +474,18 @@ def _check_attention(out, ref):
     assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)), float(err.max())
 
 
-@pytest.mark.parametrize("T,ks,G,static_len", [(32768, (64, 64), 4, 96), (9000, (32, 32), 7, 0),
-                                                (6000, (32, 32), 8, 200)])
-def test_decode_step_matches_oracle(ops, oracle, T, ks, G, static_len):
-    note(f"[decode] T={T} ks={ks} G={G} static={static_len}")
+@pytest.mark.parametrize("T,ks,G,static_len,tiles", [(32768, (64, 64), 4, 96, False), (9000, (32, 32), 7, 0, False),
+                                                      (6000, (32, 32), 8, 200, False), (20000, (32, 32), 4, 96, True)])
+def test_decode_step_matches_oracle(ops, oracle, T, ks, G, static_len, tiles):
+    note(f"[decode] T={T} ks={ks} G={G} static={static_len} tiles={tiles}")
     H = 8
     keys, values, cent, out = _index(ops, H, T, ks, 300 + G)
     from adaptiveimi_amd import synthetic
 
     sk, sv = synthetic.make_kv(H, max(static_len, 1) + 8, seed=77)
     sz = oracle.sizing(T, 0.1, k_override=ks)
-    bud = ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"])
+    # tile mode: a small page budget, so that the tiles (and the oversized-cell stop) matter
+    bud = ops.Budget(sz["nprobe"], sz["max_tokens"], 12 if tiles else sz["buffer_pages"], tile_mode=tiles)
     plan = ops.DecodePlan(cent, out["cell_count"], out["cell_offset"], ks, bud, out["list_keys"],
                           out["list_values"], sk.to(DEV), sv.to(DEV), G)
     plan.set_static_len(static_len)
@@ -444,9 +501,11 @@ def test_decode_step_matches_oracle(ops, oracle, T, ks, G, static_len):
         heads.append(dict(n_active=na, offsets=offs, merged=out["compact_centroids"][h, :na].cpu().numpy(),
                           list_keys=bits(out["list_keys"][h]), list_values=bits(out["list_values"][h])))
     ref, rs, rm, _ = oracle.decode_step(bits(q), heads, bits(sk), bits(sv), static_len, sz["n_centroids"],
-                                        bud.nprobe, bud.max_tokens, bud.buffer_pages)
+                                        bud.nprobe, bud.max_tokens, bud.buffer_pages, tile_mode=tiles)
     sel = plan.selection
     assert np.array_equal(sel["n_selected"].cpu().numpy(), rm)
+    if tiles:   # more rows than one page budget holds
+        assert int(sel["n_rows"].max()) > bud.buffer_pages * bud.page_size
     _check_attention(res, ref)
 
 
