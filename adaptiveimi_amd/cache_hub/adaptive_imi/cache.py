@@ -114,7 +114,15 @@ class adpimi_cache:  # noqa: N801  (reference class name)
             "kmeans": kmeans_cfg,
             "prefetch": dict(runtime_config.get("prefetch") or {}),
             "async_update": dict(runtime_config.get("async_update") or {}),
+            "pipeline": dict(runtime_config.get("pipeline") or {}),
         }
+        # The reference builds each layer's index on host worker threads while
+        # the next layers prefill (LayerPipeline); here the build runs on a
+        # side HIP stream and the first use of the index waits for it on the
+        # device (no host synchronisation).
+        self.async_build = bool(self.runtime_config["pipeline"].get("async_build", True))
+        self._build_stream: Optional[torch.cuda.Stream] = None
+        self._build_events: List[Optional[torch.cuda.Event]] = [None] * layer_num
         self.async_update_enabled = bool(self.runtime_config["async_update"].get("enabled", False))
         if self.async_update_enabled:
             warnings.warn("adpimi_cache: online index maintenance (async_update) is not implemented on this path; "
@@ -238,7 +246,22 @@ class adpimi_cache:  # noqa: N801  (reference class name)
             if not self.layer_started[layer_idx]:
                 mk = key_states[0, middle_start:middle_end].transpose(0, 1)     # [H, T, D] view
                 mv = value_states[0, middle_start:middle_end].transpose(0, 1)
-                self._build_layer_index(layer_idx, mk, mv)
+                if self.async_build and key_states.is_cuda:
+                    main = torch.cuda.current_stream(key_states.device)
+                    if self._build_stream is None:
+                        self._build_stream = torch.cuda.Stream(key_states.device)   # default priority
+                    side = self._build_stream
+                    side.wait_stream(main)
+                    with torch.cuda.stream(side):
+                        self._build_layer_index(layer_idx, mk, mv)
+                    # the prefill tensors stay allocated until the build has read them
+                    key_states.record_stream(side)
+                    value_states.record_stream(side)
+                    ev = torch.cuda.Event()
+                    ev.record(side)
+                    self._build_events[layer_idx] = ev
+                else:
+                    self._build_layer_index(layer_idx, mk, mv)
                 self.layer_started[layer_idx] = True
             ss, se = self.static_pattern_start, self.static_pattern_end
             self.steady_zone_keys[layer_idx][start_bdx:end_bdx, :, :ss, :] = (
@@ -262,15 +285,35 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         return key_states[:, valid_start:, :, :], value_states[:, valid_start:, :, :]
 
     def sync(self, layer_idx, start_bdx):
-        """indexing.py:612: the index build is enqueued on the caller's
-        stream, so there is no background work to wait for."""
+        """indexing.py:612.  Returns at once, as the reference's does once the
+        chunk copy is done: the build keeps running on the side stream, and
+        every use of the index (prepare_cache, the decode plans, the index
+        statistics) first makes the caller's stream wait for it."""
         return None
+
+    def _await_index(self, layer_idx: int) -> None:
+        """Order the caller's stream after layer_idx's side-stream build and
+        tie the layer's tensors to that stream for the allocator."""
+        ev = self._build_events[layer_idx]
+        if ev is None:
+            return
+        main = torch.cuda.current_stream(self.centroids[layer_idx].device)
+        main.wait_event(ev)
+        for t in (self.centroids[layer_idx], self.cell_count[layer_idx], self.cell_offset[layer_idx],
+                  self.token_perm[layer_idx], self.list_keys[layer_idx], self.list_values[layer_idx]):
+            if t is not None:
+                t.record_stream(main)
+        for t in (self.compact_cells[layer_idx] or {}).values():
+            t.record_stream(main)
+        self._build_events[layer_idx] = None
 
     # ------------------------------------------------------------- decode --
     def prepare_cache(self, skip_prefetch: bool = False):
         """runtime.py:11-63: decode budgets, then one decode plan per layer."""
         if not self.build_index_when_prefilling:
             return
+        for layer in range(self.layer_num):
+            self._await_index(layer)
         if self.cache_prepared:
             return
         ks = next((k for k in self.layer_ks if k is not None), None)
@@ -294,6 +337,7 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         if plan is None:
             if not self.cache_prepared:
                 self.prepare_cache()
+            self._await_index(layer_idx)
             # IMI_MAX_TILES != 0 selects the reference's tile mode (retrieval.py:373-382)
             tiles = int(os.getenv("IMI_MAX_TILES", "0") or 0) != 0
             bud = ops.Budget(self.nprobe, self.max_retrieval_tokens, self.buffer_size, self.page_size,
@@ -346,6 +390,8 @@ class adpimi_cache:  # noqa: N801  (reference class name)
     # ----------------------------------------------------------- lifecycle --
     def get_index_stats(self) -> Dict[str, object]:
         """indexing.py:316-350."""
+        for layer in range(self.layer_num):
+            self._await_index(layer)
         ideal_per_head = max(float(self.list_capacity) / 16.0, 0.0)
         total_heads = int(self.layer_num * self.batch_groups)
         ideal_total = ideal_per_head * float(total_heads)
@@ -399,11 +445,15 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         self.layer_started = [False] * self.layer_num
         self._expected_middle_len = [None] * self.layer_num
         self._plans = [None] * self.layer_num
+        for layer in range(self.layer_num):
+            if self.centroids[layer] is not None:
+                self._await_index(layer)
 
     def cleanup(self):
         """indexing.py:453: drop every device buffer the cache holds."""
         n = self.layer_num
         self._plans = [None] * n
+        self._build_events = [None] * n
         self.centroids = [None] * n
         self.cell_count = [None] * n
         self.cell_offset = [None] * n

@@ -40,8 +40,11 @@ def _require_device(*ts: torch.Tensor) -> torch.device:
 
 
 def workspace(name: str, nbytes: int, device: torch.device) -> torch.Tensor:
-    """Zero-filled byte buffer reused across calls (grown on demand)."""
-    key = (name, device.index if device.index is not None else torch.cuda.current_device())
+    """Zero-filled byte buffer reused across calls (grown on demand), one per
+    (name, device, stream): calls on one stream are ordered, calls on two
+    streams (an index build on a side stream) never share a buffer."""
+    key = (name, device.index if device.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(device).cuda_stream)
     buf = _WS.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)

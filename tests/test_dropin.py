@@ -200,3 +200,45 @@ def test_dense_attention_before_index():
         got = out.float().cpu().numpy().reshape(8, 4, 128)
         err = np.abs(got - ref)
         assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)), f"static_len {static_len}: {err.max()}"
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a HIP device")
+def test_side_stream_build_matches_inline_build():
+    """The index build on the side stream (the default, like the reference's
+    background LayerPipeline) gives the same index and decode output as the
+    build on the caller's stream, with the prefill tensors freed right after
+    prefill_update_kv_cache returns."""
+    from adaptiveimi_amd import synthetic
+    from adaptiveimi_amd.attn_hub.sparse_imi import imi_decode_attn
+
+    print("[dropin] side-stream build vs inline build", flush=True)
+    L, S, H, G, D = 2, 6096, 8, 4, 128
+    kv = [synthetic.make_kv(H, S + 1, seed=70 + layer) for layer in range(L)]
+    outs = []
+    for async_build in (False, True):
+        cfg = {"kmeans": {"k1": 32, "k2": 32, "max_iters": 4, "early_stop_min_iter": 4, "init": "first"},
+               "pipeline": {"async_build": async_build}}
+        cache = _cache(layer_mapping={"0": DEV, "1": DEV}, runtime_config=cfg)
+        assert cache.async_build == async_build
+        for layer in range(L):
+            k, v = kv[layer]
+            pk = k[:, :S].transpose(0, 1).unsqueeze(0).contiguous().to(DEV)
+            pv = v[:, :S].transpose(0, 1).unsqueeze(0).contiguous().to(DEV)
+            cache.prefill_update_kv_cache(None, pk, pv, layer, 0)
+            cache.sync(layer, 0)
+            del pk, pv                      # the side stream still reads them
+            torch.empty(8 << 20, dtype=torch.uint8, device=DEV).fill_(0xAB)   # reuse pressure
+        cache.prepare_cache()
+        res = []
+        for layer in range(L):
+            k, v = kv[layer]
+            nk = k[:, S].reshape(1, 1, H, D).to(DEV)
+            cache.decode_update_kv_cache(nk, v[:, S].reshape(1, 1, H, D).to(DEV), layer)
+            q = synthetic.make_queries(k[:, :S], G, seed=layer)[0].reshape(1, 1, H * G, D).to(DEV)
+            res.append(imi_decode_attn(q, nk, None, layer, cache).clone())
+            res += [cache.token_perm[layer].clone(), cache.list_keys[layer].clone(), cache.centroids[layer].clone()]
+        torch.cuda.synchronize()
+        outs.append(res)
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
