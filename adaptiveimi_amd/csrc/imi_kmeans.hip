@@ -16,8 +16,9 @@
 // the block histogram of labels and each token's stable rank inside its
 // block, so the M-step's member lists come from one scan + one scatter.  The
 // M-step sums each cluster sequentially in ascending token order (the
-// reference's order with one thread per subspace run), one wave per cluster
-// with the member rows streamed through a register ring.
+// reference's order with one thread per subspace run): one workgroup per
+// cluster, one wave running the chains while three waves stream the member
+// rows through register rings and an LDS hand-off.
 #include <limits>
 #include <random>
 #include <vector>
@@ -197,7 +198,7 @@ size_t screen_lds_bytes(int kmax) {
            4 * static_cast<size_t>(kmax) * 4 + 64;
 }
 
-template <int DP>
+template <int DP, int MAXK>
 __global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int chunks) {
     constexpr int KH = DP / 32;   // 32-dim K steps per subvector
     extern __shared__ float smem[];
@@ -217,7 +218,21 @@ __global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int c
     float* red = reinterpret_cast<float*>(wcnt + 4 * a.kmax);               // [4]
 
     const float* cg = a.cent + static_cast<int64_t>(seg) * a.kmax * DP;
-    for (int i = tid; i < k * DP; i += 256) cs[(i / DP) * CS + i % DP] = cg[i];
+    {
+        // centroid rows -> LDS (padded rows), every float4 load issued first
+        constexpr int PER = MAXK * DP / 4 / 256;
+        float4 v[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i4 = tid + u * 256;
+            v[u] = i4 * 4 < k * DP ? reinterpret_cast<const float4*>(cg)[i4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = (tid + u * 256) * 4;
+            if (i < k * DP) *reinterpret_cast<float4*>(cs + (i / DP) * CS + i % DP) = v[u];
+        }
+    }
     __syncthreads();
     // A operands: lane l of tile ct holds centroid 16ct + l%16, dims
     // 32kh + 8(l/16) .. +7 (v_mfma_f32_16x16x32_bf16 A layout)
@@ -243,14 +258,18 @@ __global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int c
     }
     for (int c = tid; c < nct * 16; c += 256) {
         float sq = 0.0f;
-        if (c < k)
+        if (c < k) {
+#pragma unroll
             for (int d = 0; d < DP; ++d) sq = __builtin_fmaf(cs[c * CS + d], cs[c * CS + d], sq);
+        }
         ccs[c] = sq;
     }
     __syncthreads();
     float ccmax = 0.0f;
     for (int c = lane; c < k; c += 64) ccmax = fmaxf(ccmax, ccs[c]);
     ccmax = wave_max(ccmax);
+    const int nwords = (nct + 1) >> 1;          // 32-bit candidate words in use
+    const bool partial = nct * 16 > k;          // last centroid tile not full
 
     const uint16_t* kb = a.keys + h * a.hs + p * DP;
     // 256-token blocks blockIdx.x * chunks .. +chunks-1 (the prologue above is
@@ -260,9 +279,8 @@ __global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int c
     const int blk = blockIdx.x * chunks + ci;
     if (blk >= a.nblk) break;
     if (ci > 0) __syncthreads();   // the previous block's LDS reads are done
-    // every load of this block of 256 tokens is issued up front: the MFMA B
-    // operands of the wave's four 16-token tiles (lane l: token l%16, dims
-    // 32kh + 8(l/16) .. +7) and the thread's own token row for the exact pass
+    // the MFMA operands of the wave's four 16-token tiles are loaded up front
+    // (lane l: token l%16, dims 32kh + 8(l/16) .. +7)
     const int tw0 = blk * 256 + wave * 64;
     const int t = blk * 256 + tid;
     const bool valid = t < a.T;
@@ -276,26 +294,34 @@ __global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int c
                                                                          kh * 32 + 8 * (lane >> 4))
                                   : km_u32x4_t{0u, 0u, 0u, 0u};
     }
-    // screening: token tile j = tokens 16j .. 16j+15 of this wave's 64
+    // the thread's own token row for the exact pass, loaded now as well
+    km_u32x4_t xr[DP / 8];
+#pragma unroll
+    for (int i = 0; i < DP / 8; ++i)
+        xr[i] = valid ? *reinterpret_cast<const km_u32x4_t*>(kb + static_cast<int64_t>(t) * a.ts + 8 * i)
+                      : km_u32x4_t{0u, 0u, 0u, 0u};
+    // screening: token tile j = tokens 16j .. 16j+15 of this wave's 64.
+    // e(c) = |c|^2 - 2 x.c orders the centroids like D~ = |x|^2 + e(c).
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const km_u32x4_t* bq = bqa[j];
-        float xs = 0.0f;
+        // |x|^2 from the diagonal of x x^T (the same registers serve as A and
+        // B): token t's entry sits in lane 16(t/4) + t, register t % 4
+        float xs;
+        {
+            km_f32x4_t dg = km_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kh = 0; kh < KH; ++kh) {
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const float lo = bf16_lo(bq[kh][w]), hi = bf16_hi(bq[kh][w]);
-                xs = __builtin_fmaf(lo, lo, xs);
-                xs = __builtin_fmaf(hi, hi, xs);
-            }
+            for (int kh = 0; kh < KH; ++kh)
+                dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(km_bf16x8_t, bq[kh]),
+                                                             __builtin_bit_cast(km_bf16x8_t, bq[kh]), dg, 0, 0, 0);
+            const int tl = lane & 15, rr = tl & 3;
+            const float own = rr == 0 ? dg[0] : rr == 1 ? dg[1] : rr == 2 ? dg[2] : dg[3];
+            xs = __shfl(own, 16 * (tl >> 2) + tl);
         }
-        xs += xor16(xs);
-        xs += xor32(xs);
-        float dt[kScreenMaxK / 16][4];
-        float dmin = INFINITY;
+        float ev[MAXK / 16][4];
+        float emin = INFINITY;
 #pragma unroll
-        for (int ct = 0; ct < kScreenMaxK / 16; ++ct) {
+        for (int ct = 0; ct < MAXK / 16; ++ct) {
             if (ct < nct) {
                 km_f32x4_t acc = km_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -310,32 +336,38 @@ __global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int c
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int c = ct * 16 + 4 * (lane >> 4) + r;
-                    const float v = c < k ? (xs + ccs[c]) - 2.0f * acc[r] : INFINITY;
-                    dt[ct][r] = v;
-                    dmin = fminf(dmin, v);
+                    float v = __builtin_fmaf(-2.0f, acc[r], ccs[c]);
+                    if (partial && ct == nct - 1 && c >= k) v = INFINITY;
+                    ev[ct][r] = v;
+                    emin = fminf(emin, v);
                 }
             } else {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) dt[ct][r] = INFINITY;
+                for (int r = 0; r < 4; ++r) ev[ct][r] = INFINITY;
             }
         }
-        dmin = fminf(dmin, xor16(dmin));
-        dmin = fminf(dmin, xor32(dmin));
+        emin = fminf(emin, xor16(emin));
+        emin = fminf(emin, xor32(emin));
+        // candidates: e(c) <= min e + 2E; non-finite or huge magnitudes make
+        // every finite e a candidate (the exhaustive E-step)
         const float mag = xs + ccmax;
-        const float lim = dmin + 2.0f * (0x1p-12f * mag + 1e-30f);
-        const bool all = !(lim < INFINITY) || !(mag <= 1e37f);
-        uint32_t m[kScreenMaxK / 32] = {0u, 0u, 0u, 0u};
+        const float lim0 = emin + 2.0f * (0x1p-12f * mag + 1e-30f);
+        const bool all = !(mag <= 1e37f) || !(lim0 < INFINITY);
+        const float lim = all ? 3.402823466e38f : lim0;
+        uint32_t m[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int ct = 0; ct < kScreenMaxK / 16; ++ct)
+        for (int ct = 0; ct < MAXK / 16; ++ct) {
+            uint32_t nib = 0u;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int c = ct * 16 + 4 * (lane >> 4) + r;
-                if (c < k && (all || dt[ct][r] <= lim)) m[c >> 5] |= 1u << (c & 31);
+            for (int r = 0; r < 4; ++r) nib |= ev[ct][r] <= lim ? (1u << r) : 0u;
+            m[ct >> 1] |= nib << ((ct & 1) * 16 + 4 * (lane >> 4));
+        }
+#pragma unroll
+        for (int w = 0; w < MAXK / 32; ++w) {
+            if (w < nwords) {
+                m[w] |= xor16_u(m[w]);
+                m[w] |= xor32_u(m[w]);
             }
-#pragma unroll
-        for (int w = 0; w < kScreenMaxK / 32; ++w) {
-            m[w] |= xor16_u(m[w]);
-            m[w] |= xor32_u(m[w]);
         }
         if (lane < 16) {
             const int slot = wave * 64 + 16 * j + lane;
@@ -347,11 +379,6 @@ __global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int c
 
     // exact reference distance to the candidates, one token per thread
     float x[DP];
-    km_u32x4_t xr[DP / 8];
-#pragma unroll
-    for (int i = 0; i < DP / 8; ++i)
-        xr[i] = valid ? *reinterpret_cast<const km_u32x4_t*>(kb + static_cast<int64_t>(t) * a.ts + 8 * i)
-                      : km_u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < DP / 8; ++i) {
 #pragma unroll
@@ -603,32 +630,35 @@ __global__ __launch_bounds__(256) void km_scatter_kernel(KmParams a) {
     a.sorted[so + pos] = t;
 }
 
-// M-step, one wave per cluster (four clusters per workgroup).  Lane d keeps
-// the chain of dimension d (members in ascending token order, one dependent
-// fp32 add each).  Member rows are gathered in 64-row batches (16-byte parts,
-// every lane loads one part per instruction) into a ring of NB register
-// batches, and the member ids run 2*NB batches ahead, so every wait on a
-// batch leaves the later ones in flight; a batch goes through the wave's LDS
-// tile to reach the dimension-per-lane layout of the chains.
+// M-step, one workgroup per cluster: wave 0 keeps the chains (lane d =
+// dimension d, members in ascending token order, one dependent fp32 add
+// each) while waves 1..3 gather the member rows, so a large cluster streams
+// with three waves' worth of loads in flight.  Batch b (64 rows) belongs to
+// loader 1 + b % 3 as its local batch b / 3; round q hands batches 3q ..
+// 3q+2 over through one of two sets of LDS slots (the loaders fill round
+// q+1 while wave 0 sums round q), one barrier per round.  Each loader keeps
+// NB local batches in flight in a register ring and the member ids NI local
+// batches ahead (the same ring discipline as a lone wave).
 template <int DP>
-__global__ __launch_bounds__(256) void km_update_wave_kernel(KmParams a, int it, Draws draws) {
+__global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, int it, Draws draws) {
     constexpr int PARTS = DP / 8;    // 16-byte parts per row
     constexpr int RPL = 64 / PARTS;  // rows per load instruction
     constexpr int LPB = PARTS;       // load instructions per 64-row batch
-    constexpr int NB = 4;            // row batches in flight
-    constexpr int NI = 2 * NB;       // id batches in flight
-    __shared__ km_u32x4_t sbuf[4][64 * PARTS];
-    const int seg = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int c = blockIdx.x * 4 + wave;
+    constexpr int NL = 3;            // loader waves
+    constexpr int NB = 4;            // local batches in flight per loader
+    constexpr int NI = 2 * NB;       // local id batches in flight per loader
+    __shared__ km_u32x4_t ring[2 * NL][64 * PARTS];
+    const int c = blockIdx.x, seg = blockIdx.y;
     const int h = seg / a.P, p = seg % a.P;
     if (c >= a.k[p]) return;
     if (a.done && a.done[seg]) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int32_t* off = a.off + static_cast<int64_t>(seg) * (a.kmax + 1);
     const int lo = off[c], hi = off[c + 1];
     const uint16_t* kbase = a.keys + h * a.hs + p * DP;
     float* dst = a.cent + (static_cast<int64_t>(seg) * a.kmax + c) * DP;
     if (hi == lo) {
-        if (lane < DP) {
+        if (wave == 0 && lane < DP) {
             const int e = a.empties[static_cast<int64_t>(seg) * a.kmax + c];
             const int tok = draws.v[e];
             dst[lane] = bf16_to_f32(kbase[static_cast<int64_t>(tok) * a.ts + lane]);
@@ -636,65 +666,74 @@ __global__ __launch_bounds__(256) void km_update_wave_kernel(KmParams a, int it,
         return;
     }
     const int n = hi - lo;
-    const int nb = (n + 63) >> 6;
+    const int nb = (n + 63) >> 6;              // 64-row batches
+    const int rounds = (nb + NL - 1) / NL;     // = local batches of loader 1
     const int32_t* srt = a.sorted + static_cast<int64_t>(seg) * a.T + lo;
-    const int part = lane % PARTS, rsub = lane / PARTS;
-    // ids of batch b: lane l -> member 64b + l (rows past n read token 0
-    // and are not summed)
-#define KM_LD_ID(b) ((64 * (b) + lane) < n ? srt[64 * (b) + lane] : 0)
-#define KM_LD_ROWS(idv, slot)                                                                          \
+    if (wave > 0) {
+        const int lw = wave - 1;
+        const int part = lane % PARTS, rsub = lane / PARTS;
+        // global batch of local batch q: NL * q + lw; rows past n read token 0
+#define KMB_ID(q) ((NL * (q) + lw) * 64 + lane < n ? srt[(NL * (q) + lw) * 64 + lane] : 0)
+#define KMB_ROWS(idv, slot)                                                                            \
     _Pragma("unroll") for (int u = 0; u < LPB; ++u) {                                                \
         const int id_ = __shfl((idv), u * RPL + rsub);                                               \
         rr[slot][u] = *reinterpret_cast<const km_u32x4_t*>(kbase + static_cast<int64_t>(id_) * a.ts + part * 8); \
     }
-    int idr[NI];
-    km_u32x4_t rr[NB][LPB];
+        int idr[NI];
+        km_u32x4_t rr[NB][LPB];
 #pragma unroll
-    for (int j = 0; j < NI; ++j) idr[j] = j < nb ? KM_LD_ID(j) : 0;
+        for (int j = 0; j < NI; ++j) idr[j] = KMB_ID(j);
 #pragma unroll
-    for (int j = 0; j < NB; ++j)
-        if (j < nb) {
-            KM_LD_ROWS(idr[j], j)
+        for (int j = 0; j < NB; ++j) {
+            KMB_ROWS(idr[j], j)
         }
-    km_u32x4_t* buf = sbuf[wave];
-    const uint16_t* rows = reinterpret_cast<const uint16_t*>(buf);
-    float acc = 0.0f;
 #pragma unroll 1
-    for (int b0 = 0; b0 < nb; b0 += NI) {
+        for (int q0 = 0; q0 < rounds; q0 += NI) {
 #pragma unroll
-        for (int jj = 0; jj < NI; ++jj) {
-            const int b = b0 + jj;
-            if (b < nb) {
-                const int j = jj % NB;
-                // batch b: registers -> LDS tile (row-major, DP bf16 per row)
+            for (int jj = 0; jj < NI; ++jj) {
+                const int q = q0 + jj;
+                if (q < rounds) {
+                    const int j = jj % NB;
+                    km_u32x4_t* slot = ring[(q & 1) * NL + lw];
 #pragma unroll
-                for (int u = 0; u < LPB; ++u) buf[(u * RPL + rsub) * PARTS + part] = rr[j][u];
-                // refill: rows of batch b + NB (ids loaded NB batches ago),
-                // then ids of batch b + NI into the slot just used
-                if (b + NB < nb) {
-                    KM_LD_ROWS(idr[(jj + NB) % NI], j)
-                }
-                if (b + NI < nb) idr[jj] = KM_LD_ID(b + NI);
-                km_wave_lds_sync();
-                const int cnt = (n - 64 * b) < 64 ? (n - 64 * b) : 64;
-                if (lane < DP) {
-                    if (cnt == 64) {
-                        float v[64];
-#pragma unroll
-                        for (int q = 0; q < 64; ++q) v[q] = bf16_to_f32(rows[q * DP + lane]);
-#pragma unroll
-                        for (int q = 0; q < 64; ++q) acc = acc + v[q];
-                    } else {
-                        for (int r = 0; r < cnt; ++r) acc = acc + bf16_to_f32(rows[r * DP + lane]);
+                    for (int u = 0; u < LPB; ++u) slot[(u * RPL + rsub) * PARTS + part] = rr[j][u];
+                    if (q + NB < rounds) {
+                        KMB_ROWS(idr[(jj + NB) % NI], j)
                     }
+                    if (q + NI < rounds) idr[jj] = KMB_ID(q + NI);
                 }
-                km_wave_lds_sync();
+                if (q0 + jj < rounds) __syncthreads();
             }
         }
+#undef KMB_ID
+#undef KMB_ROWS
+    } else {
+        float acc = 0.0f;
+#pragma unroll 1
+        for (int q = 0; q < rounds; ++q) {
+            __syncthreads();   // round q's slots are filled
+#pragma unroll
+            for (int lw = 0; lw < NL; ++lw) {
+                const int b = NL * q + lw;
+                if (b < nb) {
+                    const uint16_t* rows = reinterpret_cast<const uint16_t*>(ring[(q & 1) * NL + lw]);
+                    const int cnt = (n - 64 * b) < 64 ? (n - 64 * b) : 64;
+                    if (lane < DP) {
+                        if (cnt == 64) {
+                            float v[64];
+#pragma unroll
+                            for (int r = 0; r < 64; ++r) v[r] = bf16_to_f32(rows[r * DP + lane]);
+#pragma unroll
+                            for (int r = 0; r < 64; ++r) acc = acc + v[r];
+                        } else {
+                            for (int r = 0; r < cnt; ++r) acc = acc + bf16_to_f32(rows[r * DP + lane]);
+                        }
+                    }
+                }
+            }
+        }
+        if (lane < DP) dst[lane] = acc * (1.0f / static_cast<float>(n));
     }
-    if (lane < DP) dst[lane] = acc * (1.0f / static_cast<float>(n));
-#undef KM_LD_ID
-#undef KM_LD_ROWS
 }
 
 __global__ void km_reset_kernel(KmParams a) {
@@ -753,25 +792,31 @@ size_t workspace_bytes(const imi_kmeans_args* a, int kmax, KmParams* out) {
     return cv.used();
 }
 
+template <int DP, int MAXK>
+int run_screen(const KmParams& p, int segs, hipStream_t stream) {
+    const size_t lds = screen_lds_bytes<DP>(p.kmax);
+    if (lds > 64 * 1024)
+        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_assign_screen_kernel<DP, MAXK>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    // as many workgroups as fit on the device at once, each over `chunks`
+    // consecutive 256-token blocks
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, km_assign_screen_kernel<DP, MAXK>, 256, lds) !=
+            hipSuccess ||
+        per_cu <= 0)
+        per_cu = 1;
+    const int64_t want = static_cast<int64_t>(per_cu) * device_cus();
+    const int chunks = static_cast<int>(std::max<int64_t>(1, (static_cast<int64_t>(p.nblk) * segs + want - 1) / want));
+    const int gx = (p.nblk + chunks - 1) / chunks;
+    hipLaunchKernelGGL((km_assign_screen_kernel<DP, MAXK>), dim3(gx, segs), dim3(256), lds, stream, p, chunks);
+    IMI_LAUNCH_CHECK("km_assign_screen_kernel");
+    return IMI_OK;
+}
+
 template <int DP>
 int run_assign(const KmParams& p, int segs, hipStream_t stream) {
     if (p.kmax <= kScreenMaxK) {
-        const size_t lds = screen_lds_bytes<DP>(p.kmax);
-        if (lds > 64 * 1024)
-            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_assign_screen_kernel<DP>),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-        // as many workgroups as fit on the device at once, each over `chunks`
-        // consecutive 256-token blocks
-        int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, km_assign_screen_kernel<DP>, 256, lds) != hipSuccess ||
-            per_cu <= 0)
-            per_cu = 1;
-        const int64_t want = static_cast<int64_t>(per_cu) * device_cus();
-        const int chunks = static_cast<int>(std::max<int64_t>(1, (static_cast<int64_t>(p.nblk) * segs + want - 1) / want));
-        const int gx = (p.nblk + chunks - 1) / chunks;
-        hipLaunchKernelGGL(km_assign_screen_kernel<DP>, dim3(gx, segs), dim3(256), lds, stream, p, chunks);
-        IMI_LAUNCH_CHECK("km_assign_screen_kernel");
-        return IMI_OK;
+        return p.kmax <= 64 ? run_screen<DP, 64>(p, segs, stream) : run_screen<DP, kScreenMaxK>(p, segs, stream);
     }
     const size_t lds = static_cast<size_t>(p.kmax) * DP * sizeof(float) + 4 * p.kmax * sizeof(int) + 64;
     if (lds > 64 * 1024) IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_assign_kernel<DP>),
@@ -872,10 +917,10 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
         std::uniform_int_distribution<int32_t> dist(0, a->n_tokens - 1);
         for (int e = 0; e < kmax; ++e) dr.v[e] = dist(rng);
         if (dp == 64)
-            hipLaunchKernelGGL(km_update_wave_kernel<64>, dim3((kmax + 3) / 4, segs), dim3(256), 0, stream, p, it, dr);
+            hipLaunchKernelGGL(km_update_block_kernel<64>, dim3(kmax, segs), dim3(256), 0, stream, p, it, dr);
         else
-            hipLaunchKernelGGL(km_update_wave_kernel<32>, dim3((kmax + 3) / 4, segs), dim3(256), 0, stream, p, it, dr);
-        IMI_LAUNCH_CHECK("km_update_wave_kernel");
+            hipLaunchKernelGGL(km_update_block_kernel<32>, dim3(kmax, segs), dim3(256), 0, stream, p, it, dr);
+        IMI_LAUNCH_CHECK("km_update_block_kernel");
     }
     return IMI_OK;
 }
