@@ -53,6 +53,9 @@ class SelectArgs(ctypes.Structure):
         ("compact_gid", _vp), ("compact_size", _vp), ("compact_offset", _vp), ("n_active", _vp),
         ("compact_cap", _i32), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("head_max_tokens", _vp), ("head_buffer_pages", _vp), ("tile_mode", _i32),
+        ("shadow", _vp), ("shadow_rows", _i32), ("upd_slot", _vp), ("upd_row", _vp), ("upd_n", _vp),
+        ("ring_cell", _vp), ("ring_row", _vp), ("ring_n", _vp), ("ring_cap", _i32), ("exec_rows", _i32),
+        ("delta_rows", _vp), ("n_delta", _vp),
     ]
 
 
@@ -63,6 +66,19 @@ class AttentionArgs(ctypes.Structure):
         ("sel_offset", _vp), ("sel_count", _vp), ("sel_prefix", _vp), ("n_selected", _vp), ("n_rows", _vp),
         ("sel_cap", _i32), ("max_rows", _i32), ("kv_heads", _i32), ("groups", _i32), ("dim", _i32),
         ("scale", _f32), ("out", _vp), ("out_lse", _vp),
+        ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("delta_rows", _vp), ("n_delta", _vp), ("delta_cap", _i32),
+    ]
+
+
+class UpdateArgs(ctypes.Structure):
+    _fields_ = [
+        ("steady_keys", _vp), ("steady_stride", _i64), ("row0", _i32), ("count", _i32),
+        ("kv_heads", _i32), ("dim", _i32), ("shadow", _vp), ("n_rows", _i32), ("padding_id", _i32),
+        ("n_active", _vp), ("compact_gid", _vp), ("centroid_counts", _vp), ("delta_counts", _vp),
+        ("delta_sums", _vp), ("threshold", _i32), ("ring_id", _vp), ("ring_cell", _vp), ("ring_row", _vp),
+        ("ring_pos", _vp), ("ring_n", _vp), ("ring_cap", _i32), ("upd_slot", _vp), ("upd_row", _vp),
+        ("upd_n", _vp), ("n_index", _i32), ("index_by_gid", _i32),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
     ]
 
@@ -86,6 +102,9 @@ EXPORTS = {
     "imi_sparse_attention": (ctypes.c_int, [ctypes.POINTER(AttentionArgs), _vp]),
     "imi_decode_workspace_size": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_size_t)]),
     "imi_decode_step": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp]),
+    "imi_update_workspace_size": (ctypes.c_int, [ctypes.POINTER(UpdateArgs), ctypes.POINTER(ctypes.c_size_t)]),
+    "imi_update_assign": (ctypes.c_int, [ctypes.POINTER(UpdateArgs), _vp]),
+    "imi_update_refresh": (ctypes.c_int, [ctypes.POINTER(UpdateArgs), _vp]),
 }
 
 _lib = None

@@ -17,12 +17,21 @@ selection with the page rule, in-place gather and attention) with no host
 round trip.  The host-tier page cache, its thread pool and the prefetch
 warm-up of the reference have no counterpart because nothing lives on the
 host; their constructor arguments are accepted and recorded.
+
+Online index maintenance (runtime_config["async_update"], async_update.py)
+runs on the device as well: every `batch` decode keys of a layer are
+assigned to clusters and enter the delta ring (imi_update_assign, at
+decode_update_kv_cache), the centroids whose delta count reached
+`threshold` are replaced before that layer's next selection
+(imi_update_refresh), and the selection scores replaced centroids over their
+new values and appends the matching ring tokens to the attended rows.  The
+reference applies a finished side-stream update at the next step; here the
+update is stream-ordered and always lands at the next step.
 """
 from __future__ import annotations
 
 import math
 import os
-import warnings
 from typing import Dict, List, Optional
 
 import torch
@@ -123,10 +132,21 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         self.async_build = bool(self.runtime_config["pipeline"].get("async_build", True))
         self._build_stream: Optional[torch.cuda.Stream] = None
         self._build_events: List[Optional[torch.cuda.Event]] = [None] * layer_num
-        self.async_update_enabled = bool(self.runtime_config["async_update"].get("enabled", False))
-        if self.async_update_enabled:
-            warnings.warn("adpimi_cache: online index maintenance (async_update) is not implemented on this path; "
-                          "the index stays as built at prefill", RuntimeWarning, stacklevel=2)
+        # online index maintenance (cache.py:305-311 defaults)
+        acfg = self.runtime_config["async_update"]
+        self.async_update_enabled = bool(acfg.get("enabled", False))
+        self.async_update_batch = max(int(acfg.get("batch", 16)), 1)
+        self.async_update_threshold = max(int(acfg.get("threshold", 16)), 1)
+        self.async_update_delta_tokens = max(int(acfg.get("delta_tokens", 512)), 1)
+        if self.async_update_enabled and self.async_update_batch > min(64, self.async_update_delta_tokens):
+            raise ValueError("async_update: batch must be at most 64 and at most delta_tokens")
+        if self.async_update_enabled and self.async_update_delta_tokens > 1024:
+            raise ValueError("async_update: delta_tokens must be at most 1024")
+        self._updates: List[Optional[ops.OnlineUpdate]] = [None] * layer_num
+        self._upd_count = [0] * layer_num
+        self._upd_pending: List[Optional[int]] = [None] * layer_num   # decode step of an unapplied refresh
+        self._decode_step = 0
+        self.execution_stride = 0
 
         # sizes (cache.py:133-153)
         self.input_length = int(input_length) if input_length is not None else self.max_length - max_new_length
@@ -174,6 +194,8 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         self.token_perm: List[Optional[torch.Tensor]] = [None] * layer_num     # [H, T] list row -> token
         # 4-way only: the occupied cells in cell order (n_active, gid, size, offset)
         self.compact_cells: List[Optional[Dict[str, torch.Tensor]]] = [None] * layer_num
+        # online update only: the compact metadata with merged centroids
+        self.compact_meta: List[Optional[Dict[str, torch.Tensor]]] = [None] * layer_num
         self.list_keys: List[Optional[torch.Tensor]] = [None] * layer_num      # [1, H, list_capacity, D]
         self.list_values: List[Optional[torch.Tensor]] = [None] * layer_num
         self._plans: List[Optional[ops.DecodePlan]] = [None] * layer_num
@@ -214,11 +236,18 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         ncells = 1
         for k in ks:
             ncells *= int(k)
-        # 4-way scoring walks the occupied cells only (at most min(T, k^4) of them)
+        # 4-way scoring walks the occupied cells only (at most min(T, k^4) of
+        # them); the online update keeps merged centroids by compact id (the
+        # reference's padded n_centroids = k^2 + 1 slots for 2-way)
+        online = self.async_update_enabled
         idx = ops.build_index(middle_k, middle_v, cent, labels, ks, list_keys=lk[0], list_values=lv[0],
-                              compact=four_way, merged=False, n_centroids=min(T, ncells) + 1)
+                              compact=four_way or online, merged=online,
+                              n_centroids=min(T, ncells) + 1 if four_way else ncells + 1)
         self.compact_cells[layer_idx] = (
             {n: idx[n] for n in ("n_active", "compact_gid", "compact_size", "compact_offset")} if four_way else None)
+        self.compact_meta[layer_idx] = (
+            {n: idx[n] for n in ("n_active", "compact_gid", "compact_size", "compact_centroids")} if online else None)
+        self._updates[layer_idx] = None
         self.layer_ks[layer_idx] = ks
         self.centroids[layer_idx] = cent
         self.cell_count[layer_idx] = idx["cell_count"]
@@ -303,7 +332,7 @@ class adpimi_cache:  # noqa: N801  (reference class name)
                   self.token_perm[layer_idx], self.list_keys[layer_idx], self.list_values[layer_idx]):
             if t is not None:
                 t.record_stream(main)
-        for t in (self.compact_cells[layer_idx] or {}).values():
+        for t in list((self.compact_cells[layer_idx] or {}).values()) + list((self.compact_meta[layer_idx] or {}).values()):
             t.record_stream(main)
         self._build_events[layer_idx] = None
 
@@ -330,9 +359,32 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         self.budget_tokens = self.max_retrieval_tokens
         self.buffer_size = sz["buffer_pages"]
         self.buffer_budget_pages = self.buffer_size
+        self.execution_stride = self.buffer_size * self.page_size + self.static_capacity   # runtime.py:62
         self.cache_prepared = True
 
+    def _update_state(self, layer_idx: int) -> Optional[ops.OnlineUpdate]:
+        """runtime.py:106-166: the layer's update state, made on first use."""
+        if not self.async_update_enabled or self.compact_meta[layer_idx] is None:
+            return None
+        upd = self._updates[layer_idx]
+        if upd is None:
+            if not self.cache_prepared:
+                self.prepare_cache()
+            self._await_index(layer_idx)
+            meta = self.compact_meta[layer_idx]
+            four_way = self.subspace_parts == 4
+            ncells = int(self.cell_count[layer_idx].shape[1])
+            upd = ops.OnlineUpdate(meta["compact_centroids"], meta["compact_size"], meta["compact_gid"],
+                                   meta["n_active"], self.padding_cluster_id, self.async_update_threshold,
+                                   self.async_update_delta_tokens,
+                                   n_index=meta["compact_gid"].shape[1] if four_way else ncells,
+                                   index_by_gid=not four_way)
+            self._updates[layer_idx] = upd
+            self._plans[layer_idx] = None
+        return upd
+
     def _plan(self, layer_idx: int) -> ops.DecodePlan:
+        upd = self._update_state(layer_idx)   # (re)builds the plan when the state is new
         plan = self._plans[layer_idx]
         if plan is None:
             if not self.cache_prepared:
@@ -346,7 +398,7 @@ class adpimi_cache:  # noqa: N801  (reference class name)
                                   self.layer_ks[layer_idx], bud, self.list_keys[layer_idx][0],
                                   self.list_values[layer_idx][0], self.steady_zone_keys[layer_idx][0],
                                   self.steady_zone_values[layer_idx][0], self.group_size,
-                                  compact=self.compact_cells[layer_idx])
+                                  compact=self.compact_cells[layer_idx], update=upd)
             self._plans[layer_idx] = plan
         return plan
 
@@ -359,12 +411,16 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         token and page budgets, gather and GQA attention in one call."""
         self.ensure_layer_ready(layer_idx)
         plan = self._plan(layer_idx)
+        pending = self._upd_pending[layer_idx]
+        if pending is not None and pending < self._decode_step:   # async_update.py:7-19, one step later
+            self._updates[layer_idx].refresh(self.async_update_batch)
+            self._upd_pending[layer_idx] = None
         q = queries.reshape(self.batch_groups, self.group_size, self.head_dim)
         if not q.is_contiguous():
             q = q.contiguous()
         out = torch.empty((self.batch_size, 1, self.num_heads, self.head_dim), dtype=queries.dtype,
                           device=queries.device)
-        plan.run(q, out, int(static_len))
+        plan.run(q, out, int(static_len), exec_rows=self.execution_stride - int(static_len))
         return out
 
     def dense_attention(self, queries, layer_idx, static_len):
@@ -376,8 +432,21 @@ class adpimi_cache:  # noqa: N801  (reference class name)
 
     def decode_update_kv_cache(self, key_states, value_states, layer_idx):
         """runtime.py:378-392.  key_states / value_states: [1, 1, H, D]."""
-        self.steady_zone_keys[layer_idx][:, :, self.static_pattern_total, :] = key_states[:, 0, :, :]
-        self.steady_zone_values[layer_idx][:, :, self.static_pattern_total, :] = value_states[:, 0, :, :]
+        if layer_idx == 0:
+            self._decode_step += 1
+        row = self.static_pattern_total
+        self.steady_zone_keys[layer_idx][:, :, row, :] = key_states[:, 0, :, :]
+        self.steady_zone_values[layer_idx][:, :, row, :] = value_states[:, 0, :, :]
+        upd = self._update_state(layer_idx) if self.attn_func == self.sparse_attention else None
+        if upd is not None:   # async_update.py:77-162
+            self._upd_count[layer_idx] += 1
+            if self._upd_count[layer_idx] == self.async_update_batch:
+                if self._upd_pending[layer_idx] is not None:   # the previous batch's refresh comes first
+                    upd.refresh(self.async_update_batch)
+                n = self.async_update_batch
+                upd.assign(self.steady_zone_keys[layer_idx][0], row - n + 1, n)
+                self._upd_pending[layer_idx] = self._decode_step
+                self._upd_count[layer_idx] = 0
         if layer_idx == self.layer_num - 1:
             self.context += 1
             self.static_pattern_total += 1
@@ -445,6 +514,9 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         self.layer_started = [False] * self.layer_num
         self._expected_middle_len = [None] * self.layer_num
         self._plans = [None] * self.layer_num
+        self._updates = [None] * self.layer_num
+        self._upd_count = [0] * self.layer_num
+        self._upd_pending = [None] * self.layer_num
         for layer in range(self.layer_num):
             if self.centroids[layer] is not None:
                 self._await_index(layer)
@@ -459,6 +531,10 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         self.cell_offset = [None] * n
         self.token_perm = [None] * n
         self.compact_cells = [None] * n
+        self.compact_meta = [None] * n
+        self._updates = [None] * n
+        self._upd_count = [0] * n
+        self._upd_pending = [None] * n
         self.list_keys = [None] * n
         self.list_values = [None] * n
         self.layer_ks = [None] * n

@@ -44,6 +44,7 @@ namespace {
 constexpr int kWaves = 4;            // waves per workgroup (256 threads)
 constexpr int kMaxSplit = 4096;      // splits per head the merge kernel handles
 constexpr int kSelCapMax = 2048;     // selected cells per head the gather indexes
+constexpr int kDeltaMax = 1024;      // delta rows per head (the delta ring)
 constexpr int kVStride = 144;        // u16 per LDS row of a wave's V tile (288 B)
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
@@ -67,6 +68,9 @@ struct AttnParams {
     const int32_t* n_selected;  // [H]
     int sel_cap;
     const int32_t* n_rows;      // [H]
+    const int32_t* delta_rows;  // [H][delta_cap] steady rows after the selected rows, or null
+    const int32_t* n_delta;     // [H]
+    int delta_cap;
     int H, nsplit;
     int rows_per_block;
     float scale_log2;        // scale * log2(e)
@@ -104,16 +108,19 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 // of its head; the workgroup writes one partial (max, sum, unnormalised
 // output) with plain stores and merge_kernel combines the partials after the
 // kernel boundary.  Workgroups past the end of their head write nothing.
-template <int G, int NT>
+// DELTA: rows appended after the selected rows (a separate instantiation).
+template <int G, int NT, bool DELTA>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) void attention_kernel(AttnParams a) {
     constexpr int RW = NT * 16;                       // rows per wave
     constexpr int NR = (RW + 63) / 64;                // row locations per lane
     static_assert(NR <= 2, "the row lookup covers windows of at most 128 rows");
     constexpr int SU = (kSelCapMax + 1 + 64 * kWaves - 1) / (64 * kWaves);
+    constexpr int DU = kDeltaMax / (64 * kWaves);
     __shared__ float s_acc[kWaves][G][128];
     __shared__ float s_ml[kWaves][G][2];
     __shared__ int s_pre[kSelCapMax + 1];
     __shared__ int s_off[kSelCapMax];
+    __shared__ int s_drow[DELTA ? kDeltaMax : 1];
     __shared__ int s_flag[kWaves][NR * 64];
     __shared__ __attribute__((aligned(16))) uint16_t s_v[kWaves][16 * kVStride];
     __shared__ __attribute__((aligned(16))) uint16_t s_k[kWaves][16 * kVStride];
@@ -134,6 +141,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
         qb[c] = *reinterpret_cast<const u32x4_t*>(a.q + (static_cast<int64_t>(h) * G + ln % G) * 128 + c * 32 + lg * 8);
     const int nrows = a.n_rows[h];
     const int m = a.n_selected[h];
+    const int nd = DELTA ? min(max(a.n_delta[h], 0), a.delta_cap) : 0;
     {
         const int32_t* pre = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
         const int32_t* off = a.sel_offset + static_cast<int64_t>(h) * a.sel_cap;
@@ -144,15 +152,26 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
             pv[u] = i <= a.sel_cap ? pre[i] : 0;
             ov[u] = i < a.sel_cap ? off[i] : 0;
         }
+        int dv[DU];
+#pragma unroll
+        for (int u = 0; u < DU; ++u) {
+            const int i = tid + u * 64 * kWaves;
+            dv[u] = DELTA && i < a.delta_cap ? a.delta_rows[static_cast<int64_t>(h) * a.delta_cap + i] : 0;
+        }
 #pragma unroll
         for (int u = 0; u < SU; ++u) {
             const int i = tid + u * 64 * kWaves;
             if (i <= a.sel_cap) s_pre[i] = pv[u];
             if (i < a.sel_cap) s_off[i] = ov[u];
         }
+        if (DELTA) {
+#pragma unroll
+            for (int u = 0; u < DU; ++u) s_drow[tid + u * 64 * kWaves] = dv[u];
+        }
     }
     __syncthreads();
-    const int N = a.static_len + nrows;
+    // rows: [static_len steady rows | nrows list rows | nd delta rows (steady)]
+    const int N = a.static_len + nrows + nd;
     if (split * a.rows_per_block >= N) return;   // the merge ignores this split
 
     // List row of window row i (rows row0 + i, i = lane + 64r): the wave
@@ -160,7 +179,8 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     // over the staged prefix), flags the window offsets where the following
     // cells start, and counts the flags up to each row.  Selected cells hold
     // at least one row, so their starts are distinct; locations are clamped
-    // to the list.
+    // to the list.  A delta row gets -1 - its steady row (clamped to the
+    // steady zone).
     int loc[NR];
     {
         const int j0 = max(row0 - a.static_len, 0);
@@ -198,6 +218,8 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
                 const int c = c0 + popc_upto(fm[0], fm[1], j - j0);
                 l = s_off[c] + (j - s_pre[c]);
                 l = min(max(l, 0), static_cast<int>(a.list_rows) - 1);
+            } else if (DELTA && j >= nrows && j < nrows + nd) {
+                l = -1 - min(max(s_drow[j - nrows], 0), static_cast<int>(a.s_stride) - 1);
             }
             loc[r] = l;
         }
@@ -227,9 +249,11 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
                 const int n = row0 + jt;
                 const int lr = __shfl(loc[(t * 16) >> 6], jt & 63);
                 const bool st = n < a.static_len;
-                const int64_t roff = (st ? static_cast<int64_t>(n) : static_cast<int64_t>(n < N ? lr : 0)) * 128;
-                kb[slot][it] = *reinterpret_cast<const u32x4_t*>((st ? skh : lkh) + roff + li * 8);
-                vb[slot][it] = *reinterpret_cast<const u32x4_t*>((st ? svh : lvh) + roff + li * 8);
+                const bool dl = DELTA && !st && n < N && lr < 0;   // delta row: steady row -1 - lr
+                const int64_t roff =
+                    (st ? static_cast<int64_t>(n) : static_cast<int64_t>(dl ? -1 - lr : (n < N ? lr : 0))) * 128;
+                kb[slot][it] = *reinterpret_cast<const u32x4_t*>((st || dl ? skh : lkh) + roff + li * 8);
+                vb[slot][it] = *reinterpret_cast<const u32x4_t*>((st || dl ? svh : lvh) + roff + li * 8);
             }
         };
         load(0, 0);
@@ -371,7 +395,7 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
         pm = pml[static_cast<int64_t>(lane) * G * 2];
         pl = pml[static_cast<int64_t>(lane) * G * 2 + 1];
     }
-    const int rows = a.static_len + a.n_rows[h];
+    const int rows = a.static_len + a.n_rows[h] + (a.delta_rows ? min(max(a.n_delta[h], 0), a.delta_cap) : 0);
     const int ns = min(nsm, (rows + a.rows_per_block - 1) / a.rows_per_block);
     if (q == 0) {
         float M = lane < ns ? pm : -INFINITY;
@@ -478,6 +502,16 @@ int attn_validate(const imi_attention_args* a, bool need_sel) {
     IMI_REQUIRE(a->max_rows >= 0, IMI_ERR_INVALID, "imi_sparse_attention: max_rows must be >= 0");
     if (need_sel)
         IMI_REQUIRE(a->n_rows != nullptr, IMI_ERR_INVALID, "imi_sparse_attention: null n_rows");
+    if (a->delta_rows) {
+        IMI_REQUIRE(a->delta_cap > 0 && a->delta_cap <= kDeltaMax, IMI_ERR_UNSUPPORTED,
+                    "imi_sparse_attention: delta_cap %d outside [1, %d]", a->delta_cap, kDeltaMax);
+        IMI_REQUIRE(a->steady_keys && a->steady_values && a->steady_stride > 0, IMI_ERR_INVALID,
+                    "imi_sparse_attention: delta rows need the steady zone");
+        IMI_REQUIRE(a->max_rows >= a->delta_cap, IMI_ERR_INVALID,
+                    "imi_sparse_attention: max_rows %d must cover the %d delta rows", a->max_rows, a->delta_cap);
+        if (need_sel)
+            IMI_REQUIRE(a->n_delta != nullptr, IMI_ERR_INVALID, "imi_sparse_attention: null n_delta");
+    }
     IMI_REQUIRE(a->sel_cap >= 0 && a->sel_cap <= kSelCapMax, IMI_ERR_UNSUPPORTED,
                 "imi_sparse_attention: sel_cap %d exceeds %d", a->sel_cap, kSelCapMax);
     IMI_REQUIRE(nsplit_bound(a) <= kMaxSplit, IMI_ERR_UNSUPPORTED,
@@ -486,14 +520,22 @@ int attn_validate(const imi_attention_args* a, bool need_sel) {
     return IMI_OK;
 }
 
+template <int G, bool DELTA>
+void launch_gd(const AttnParams& p, int blocks, hipStream_t stream) {
+    switch (p.rows_per_block / 64) {
+        case 8: hipLaunchKernelGGL((attention_kernel<G, 8, DELTA>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
+        case 4: hipLaunchKernelGGL((attention_kernel<G, 4, DELTA>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
+        case 2: hipLaunchKernelGGL((attention_kernel<G, 2, DELTA>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
+        default: hipLaunchKernelGGL((attention_kernel<G, 1, DELTA>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
+    }
+}
+
 template <int G>
 void launch_g(const AttnParams& p, int blocks, hipStream_t stream) {
-    switch (p.rows_per_block / 64) {
-        case 8: hipLaunchKernelGGL((attention_kernel<G, 8>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
-        case 4: hipLaunchKernelGGL((attention_kernel<G, 4>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
-        case 2: hipLaunchKernelGGL((attention_kernel<G, 2>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
-        default: hipLaunchKernelGGL((attention_kernel<G, 1>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
-    }
+    if (p.delta_rows)
+        launch_gd<G, true>(p, blocks, stream);
+    else
+        launch_gd<G, false>(p, blocks, stream);
 }
 
 int attn_launch(const imi_attention_args* a, hipStream_t stream) {
@@ -512,6 +554,9 @@ int attn_launch(const imi_attention_args* a, hipStream_t stream) {
     p.n_selected = a->n_selected;
     p.sel_cap = a->sel_cap;
     p.n_rows = a->n_rows;
+    p.delta_rows = a->delta_rows;
+    p.n_delta = a->n_delta;
+    p.delta_cap = a->delta_cap;
     p.H = a->kv_heads;
     p.scale_log2 = a->scale * 1.44269504088896340736f;
     p.out = a->out;
@@ -566,6 +611,7 @@ extern "C" int imi_sparse_attention(const imi_attention_args* a, imi_stream_t st
 namespace {
 struct DecodeLayout {
     int32_t *cell, *off, *cnt, *prefix, *nsel, *nrows;
+    int32_t *drows, *ndelta;   // delta append outputs (ring_cap > 0)
     char* sel_ws;            // 4-way selection scratch (empty for 2-way)
     size_t sel_bytes;
     char* attn_ws;
@@ -583,6 +629,9 @@ DecodeLayout decode_layout(const imi_decode_args* a, void* ws) {
     L.prefix = cv.take<int32_t>(static_cast<size_t>(H) * (cap + 1));
     L.nsel = cv.take<int32_t>(H);
     L.nrows = cv.take<int32_t>(H);
+    const int rc = a->sel.ring_cap > 0 ? a->sel.ring_cap : 0;
+    L.drows = cv.take<int32_t>(static_cast<size_t>(H) * (rc > 0 ? rc : 1));
+    L.ndelta = cv.take<int32_t>(H);
     L.sel_bytes = a->sel.parts == 4 ? select4_workspace_size(&a->sel) : 0;
     L.sel_ws = cv.take<char>(L.sel_bytes > 0 ? L.sel_bytes : 1);
     imi_attention_args t = a->attn;
@@ -598,9 +647,15 @@ int decode_validate(const imi_decode_args* a) {
     IMI_REQUIRE(a->sel.kv_heads == a->attn.kv_heads && a->sel.groups == a->attn.groups,
                 IMI_ERR_INVALID, "imi_decode_step: selection and attention shapes differ");
     // selected rows: at most buffer_pages pages, or in tile mode the token
-    // budget plus one cell of at most buffer_pages pages
+    // budget plus one cell of at most buffer_pages pages; then the delta rows
+    if (a->sel.ring_cap > 0)
+        IMI_REQUIRE(a->sel.ring_cap <= kDeltaMax && a->attn.steady_keys && a->attn.steady_values &&
+                        a->attn.steady_stride > 0,
+                    IMI_ERR_INVALID, "imi_decode_step: the delta append needs ring_cap <= %d and the steady zone",
+                    kDeltaMax);
     const int64_t need_rows = static_cast<int64_t>(a->sel.buffer_pages) * a->sel.page_size +
-                              (a->sel.tile_mode ? static_cast<int64_t>(a->sel.max_tokens) : 0);
+                              (a->sel.tile_mode ? static_cast<int64_t>(a->sel.max_tokens) : 0) +
+                              (a->sel.ring_cap > 0 ? a->sel.ring_cap : 0);
     IMI_REQUIRE(a->attn.max_rows >= need_rows, IMI_ERR_INVALID, "imi_decode_step: max_rows %d < %lld selectable rows",
                 a->attn.max_rows, static_cast<long long>(need_rows));
     return attn_validate(&a->attn, false);
@@ -633,6 +688,10 @@ extern "C" int imi_decode_step(const imi_decode_args* a, imi_stream_t stream_) {
     if (!s.sel_prefix) s.sel_prefix = L.prefix;
     if (!s.n_selected) s.n_selected = L.nsel;
     if (!s.n_rows) s.n_rows = L.nrows;
+    if (s.ring_cap > 0) {
+        if (!s.delta_rows) s.delta_rows = L.drows;
+        if (!s.n_delta) s.n_delta = L.ndelta;
+    }
     if (s.parts == 4 && !s.workspace) {
         s.workspace = L.sel_ws;
         s.workspace_bytes = L.sel_bytes;
@@ -654,6 +713,9 @@ extern "C" int imi_decode_step(const imi_decode_args* a, imi_stream_t stream_) {
     t.n_selected = s.n_selected;
     t.n_rows = s.n_rows;
     t.sel_cap = s.sel_cap;
+    t.delta_rows = s.ring_cap > 0 ? s.delta_rows : nullptr;
+    t.n_delta = s.ring_cap > 0 ? s.n_delta : nullptr;
+    t.delta_cap = s.ring_cap > 0 ? s.ring_cap : 0;
     t.workspace = L.attn_ws;
     t.workspace_bytes = L.attn_bytes;
     return attn_launch(&t, stream);

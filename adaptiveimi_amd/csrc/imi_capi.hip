@@ -21,4 +21,4 @@ void clear_error() { g_error[0] = '\0'; }
 
 extern "C" const char* imi_last_error(void) { return imi::g_error; }
 
-extern "C" int imi_version(void) { return 4; }
+extern "C" int imi_version(void) { return 5; }

@@ -93,6 +93,35 @@ inline int device_cus() {
     return cached[dev];
 }
 
+// ------------------------------------------------- LDS set of cell ids --
+// Open-addressing set of non-negative ints in a kSetSize-int LDS table
+// (empty = -1), filled at most half: inserts and lookups always end.
+constexpr int kSetBits = 12;
+constexpr int kSetSize = 1 << kSetBits;
+
+__device__ __forceinline__ uint32_t set_slot(int key) {
+    return (static_cast<uint32_t>(key) * 2654435761u) >> (32 - kSetBits);
+}
+
+__device__ __forceinline__ void set_insert(int* t, int key) {
+    uint32_t i = set_slot(key);
+    while (true) {
+        const int prev = atomicCAS(&t[i], -1, key);
+        if (prev == -1 || prev == key) return;
+        i = (i + 1) & (kSetSize - 1);
+    }
+}
+
+__device__ __forceinline__ bool set_find(const int* t, int key) {
+    uint32_t i = set_slot(key);
+    while (true) {
+        const int v = t[i];
+        if (v == key) return true;
+        if (v == -1) return false;
+        i = (i + 1) & (kSetSize - 1);
+    }
+}
+
 // ----------------------------------------------------------- wave helpers --
 constexpr int kWave = 64;
 

@@ -32,6 +32,8 @@ constexpr int kSelThreads = 1024;
 constexpr int kBins = 2048;
 constexpr int kCap = 2048;     // candidate capacity
 constexpr int kMaxGroups = 8;  // query heads per KV head
+constexpr int kOvr = 64;       // replaced centroids scored per pass
+constexpr int kRingCap = 1024; // delta ring entries (one per thread)
 
 struct SelParams {
     const uint16_t* q;
@@ -52,6 +54,19 @@ struct SelParams {
     int32_t* n_sel;
     int32_t* n_rows;
     int sel_cap;
+    // online index maintenance: replaced centroids and the delta ring
+    const float* shadow;
+    int shadow_rows;
+    const int32_t* upd_slot;
+    const int32_t* upd_row;
+    const int32_t* upd_n;
+    const int32_t* ring_cell;
+    const int32_t* ring_row;
+    const int32_t* ring_n;
+    int ring_cap;
+    int exec_rows;
+    int32_t* delta_rows;
+    int32_t* n_delta;
 };
 
 // Block-wide inclusive scan of one int per thread (1024 threads).
@@ -116,8 +131,35 @@ __device__ __forceinline__ int bucket_of(float s, float gmax, float inv) {
     return t < static_cast<float>(kBins - 1) ? static_cast<int>(t) : kBins - 1;
 }
 
-// DP: subspace width (64 for 2-way IMI at D = 128); EPT: cells per thread.
-template <int DP, int EPT>
+// Delta append (async_update.py:20-76, called at retrieval.py:420): the
+// ring entries (ring index order, the first ring_n valid) whose cell is in
+// the reference's `selected` -- the m_tok cells that pass nprobe and the
+// token budget (retrieval.py:295-303), plus the padding id when m_tok <
+// nprobe -- up to the execution-buffer rows left after the selected rows.
+// rcode / rrow: this thread's ring entry (thread = ring index).
+__device__ void delta_match(const SelParams& a, int h, int m_tok, int rows_sel, const int* kept, int* table,
+                            int* sh, int rcode, int rrow) {
+    const int tid = threadIdx.x;
+    for (int i = tid; i < kSetSize; i += kSelThreads) table[i] = -1;
+    __syncthreads();
+    for (int r = tid; r < m_tok; r += kSelThreads) set_insert(table, kept[r]);
+    __syncthreads();
+    const int nvalid = min(a.ring_n[h], a.ring_cap);
+    bool match = false;
+    if (tid < nvalid) match = rcode >= 0 ? set_find(table, rcode) : (rcode == -1 && m_tok < a.nprobe);
+    const int f = match ? 1 : 0;
+    int tot;
+    const int pos = block_incl_scan(f, sh, tot) - f;
+    const int avail = max(a.exec_rows - rows_sel, 0);
+    const int nd = min(tot, avail);
+    if (match && pos < nd) a.delta_rows[static_cast<int64_t>(h) * a.ring_cap + pos] = rrow;
+    if (tid == 0) a.n_delta[h] = nd;
+}
+
+// DP: subspace width (64 for 2-way IMI at D = 128); EPT: cells per thread;
+// ONLINE: replaced centroids and the delta ring (a separate instantiation,
+// so the plain kernel carries none of that code).
+template <int DP, int EPT, bool ONLINE>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     extern __shared__ uint64_t dyn[];
     __shared__ __attribute__((aligned(16))) float qs[128];
@@ -126,6 +168,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     __shared__ int binbase[kBins + 1];  // first candidate slot of each bucket
     __shared__ int sh[82];
     __shared__ int shv[8];
+    __shared__ int shk[16];
     __shared__ float shf[40];
 
     const int h = blockIdx.x;
@@ -158,6 +201,32 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         const int g = i * k1 + jcell;
         sz[e] = in ? cntp[g] : 0;
         co_[e] = in ? offs[g] : 0;
+    }
+    // Online index maintenance (async_update.py): the override slot of each
+    // of this thread's cells (-1: merged centroid unchanged), the shadow row
+    // of each of the first kOvr slots (thread t stages float4 t & 31 of slot
+    // t >> 5), and this thread's delta ring entry (thread = ring index).
+    const bool upd = ONLINE && a.upd_slot != nullptr;
+    const int n_upd = upd ? a.upd_n[h] : 0;
+    int us[EPT];
+    int urow[2] = {0, 0};
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int i = rcell + R * e;
+        const bool in = upd && rcell < R && i < k0;
+        us[e] = in ? a.upd_slot[static_cast<int64_t>(h) * a.ncells + i * k1 + jcell] : -1;
+    }
+    if (upd) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int slot = (tid + u * kSelThreads) >> 5;
+            urow[u] = slot < a.shadow_rows ? a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + slot] : 0;
+        }
+    }
+    int rcode = -3, rrow = 0;
+    if (ONLINE && a.ring_cap > 0 && tid < a.ring_cap) {
+        rcode = a.ring_cell[static_cast<int64_t>(h) * a.ring_cap + tid];
+        rrow = a.ring_row[static_cast<int64_t>(h) * a.ring_cap + tid];
     }
     // C0 and C1 rows [k][DP] are read coalesced (float4 per thread) and
     // stored in LDS with padded strides (conflict-free word reads): C0
@@ -213,6 +282,17 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     }
     __syncthreads();
 
+    // shadow rows of the first kOvr override slots, in flight during scoring
+    float4 ovv[2] = {};
+    if (upd) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int row = min(max(urow[u], 0), a.shadow_rows - 1);
+            ovv[u] = reinterpret_cast<const float4*>(a.shadow + (static_cast<int64_t>(h) * a.shadow_rows + row) *
+                                                     128)[(tid + u * kSelThreads) & 31];
+        }
+    }
+
     // ---- scores: the chain continues over the second subspace ----
     float sc[EPT];
 #pragma unroll
@@ -227,6 +307,45 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
             const float cv = c1T[d * (k1 + 1) + jcell];
 #pragma unroll
             for (int e = 0; e < EPT; ++e) sc[e] = __builtin_fmaf(qd, cv, sc[e]);
+        }
+    }
+    // cells whose centroid was replaced: the full 128-term chain over the
+    // shadow row (compute_impl.cu:80-101 on the updated centroid), kOvr
+    // slots per pass, staged in LDS after the C0 rows
+    if (ONLINE && n_upd > 0) {
+        float* ovr = c0s + k0 * (DP + 1);   // [kOvr][129]
+        float* ovs = ovr + kOvr * 129;      // [kOvr]
+        for (int base = 0; base < n_upd; base += kOvr) {
+            if (base > 0) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int slot = base + ((tid + u * kSelThreads) >> 5);
+                    const int row = slot < a.shadow_rows ? a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + slot] : 0;
+                    const int rc = min(max(row, 0), a.shadow_rows - 1);
+                    ovv[u] = reinterpret_cast<const float4*>(
+                        a.shadow + (static_cast<int64_t>(h) * a.shadow_rows + rc) * 128)[(tid + u * kSelThreads) & 31];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int i4 = tid + u * kSelThreads;
+                float* dst = ovr + (i4 >> 5) * 129 + (i4 & 31) * 4;
+                dst[0] = ovv[u].x;
+                dst[1] = ovv[u].y;
+                dst[2] = ovv[u].z;
+                dst[3] = ovv[u].w;
+            }
+            __syncthreads();
+            if (tid < kOvr && base + tid < n_upd) {
+                float acc = 0.0f;
+                for (int d = 0; d < 128; ++d) acc = __builtin_fmaf(qs[d], ovr[tid * 129 + d], acc);
+                ovs[tid] = acc;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < EPT; ++e)
+                if (us[e] >= base && us[e] < base + kOvr) sc[e] = ovs[us[e] - base];
+            __syncthreads();
         }
     }
     int nvalid = 0;
@@ -268,8 +387,9 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     // this head's budgets (ragged batches), bounded by the launch-wide ones
     const int max_tokens = a.head_max_tokens ? min(a.head_max_tokens[h], a.max_tokens) : a.max_tokens;
     const int buffer_pages = a.head_buffer_pages ? min(a.head_buffer_pages[h], a.buffer_pages) : a.buffer_pages;
-    // every kept cell costs a page, except in tile mode (no running page cut)
-    int kp = a.tile_mode ? a.nprobe : (a.nprobe < buffer_pages ? a.nprobe : buffer_pages);
+    // every kept cell costs a page, except in tile mode (no running page cut);
+    // the delta match needs the ranks the page cut drops too
+    int kp = (a.tile_mode || a.ring_cap > 0) ? a.nprobe : (a.nprobe < buffer_pages ? a.nprobe : buffer_pages);
     kp = kp < n_valid ? kp : n_valid;
     int32_t* prefix_out = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
     if (kp <= 0) {
@@ -278,6 +398,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
             a.n_rows[h] = 0;
             prefix_out[0] = 0;
         }
+        if (ONLINE && a.ring_cap > 0) delta_match(a, h, 0, 0, sg, reinterpret_cast<int*>(dyn), sh, rcode, rrow);
         return;
     }
 
@@ -426,27 +547,39 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     int tincl = tsum, pincl = psum;
     block_incl_scan2(tincl, pincl, sh, ttot, ptot);
     int texcl = tincl - tsum, pexcl = pincl - psum;
-    int kept = 0;
+    int kept = 0, kept_tok = 0;
     int excl_tok[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int r = 2 * tid + u;
         excl_tok[u] = texcl;
         pexcl += pg2[u];
-        const bool keep = r < C && r < a.nprobe && texcl < max_tokens && pexcl <= (a.tile_mode ? 0 : buffer_pages);
+        const bool keep_tok = r < C && r < a.nprobe && texcl < max_tokens;
+        const bool keep = keep_tok && pexcl <= (a.tile_mode ? 0 : buffer_pages);
         kept += keep ? 1 : 0;
+        kept_tok += keep_tok ? 1 : 0;
         texcl += s2[u];
     }
     // the rules are monotone in rank (prefixes only grow), so the kept ranks
-    // are exactly the first m: count them per wave, then over the 16 waves
+    // are exactly the first m (the first m_tok before the page cut): count
+    // them per wave, then over the 16 waves
+    const bool ring = ONLINE && a.ring_cap > 0;
     {
         const int wk = wave_sum_i(kept);
-        if (lane_id() == 0) sh[66 + (tid >> 6)] = wk;
+        const int wt = ring ? wave_sum_i(kept_tok) : 0;
+        if (lane_id() == 0) {
+            sh[66 + (tid >> 6)] = wk;
+            if (ONLINE) shk[tid >> 6] = wt;
+        }
     }
     __syncthreads();
-    int m = 0;
+    int m = 0, m_tok = 0;
 #pragma unroll
     for (int w = 0; w < 16; ++w) m += sh[66 + w];
+    if (ring) {
+#pragma unroll
+        for (int w = 0; w < 16; ++w) m_tok += shk[w];
+    }
     int32_t* out_cell = a.sel_cell + static_cast<int64_t>(h) * a.sel_cap;
     int32_t* out_off = a.sel_offset + static_cast<int64_t>(h) * a.sel_cap;
     int32_t* out_cnt = a.sel_count + static_cast<int64_t>(h) * a.sel_cap;
@@ -464,12 +597,18 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
             prefix_out[m] = total;
             a.n_sel[h] = m;
             a.n_rows[h] = total;
+            if (ONLINE) shv[5] = total;
         }
     }
     if (m == 0 && tid == 0) {
         a.n_sel[h] = 0;
         a.n_rows[h] = 0;
         prefix_out[0] = 0;
+    }
+    if (ring) {
+        __syncthreads();
+        const int rows_sel = m > 0 ? shv[5] : 0;
+        delta_match(a, h, m_tok, rows_sel, sg, reinterpret_cast<int*>(dyn), sh, rcode, rrow);
     }
 }
 
@@ -511,6 +650,16 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     IMI_REQUIRE(a->dim == 128, IMI_ERR_UNSUPPORTED, "imi_select: head_dim must be 128");
     IMI_REQUIRE(a->parts == 2 || a->parts == 4, IMI_ERR_UNSUPPORTED, "imi_select: parts must be 2 or 4 (got %d)",
                 a->parts);
+    if (a->ring_cap != 0) {
+        IMI_REQUIRE(a->ring_cap > 0 && a->ring_cap <= kRingCap, IMI_ERR_UNSUPPORTED,
+                    "imi_select: ring_cap %d outside [1, %d]", a->ring_cap, kRingCap);
+        IMI_REQUIRE(!a->tile_mode, IMI_ERR_UNSUPPORTED, "imi_select: the delta append is not available in tile mode");
+        IMI_REQUIRE(a->ring_cell && a->ring_row && a->ring_n, IMI_ERR_INVALID, "imi_select: null delta ring");
+        IMI_REQUIRE(a->exec_rows >= 0, IMI_ERR_INVALID, "imi_select: exec_rows must be >= 0");
+    }
+    if (a->upd_slot)
+        IMI_REQUIRE(a->shadow && a->upd_row && a->upd_n && a->shadow_rows > 0, IMI_ERR_INVALID,
+                    "imi_select: replaced centroids need shadow, shadow_rows, upd_row and upd_n");
     if (a->parts == 4) {
         IMI_REQUIRE(a->page_size > 0 && a->nprobe > 0 && a->max_tokens > 0 && a->buffer_pages > 0, IMI_ERR_INVALID,
                     "imi_select: budgets must be positive");
@@ -529,26 +678,28 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     ncells = static_cast<int64_t>(a->k[0]) * a->k[1];
     IMI_REQUIRE(a->k[0] <= 128 && a->k[1] <= 128 && a->k[0] <= 16 * (kSelThreads / a->k[1]), IMI_ERR_UNSUPPORTED,
                 "imi_select: k = (%d, %d) exceeds the cells one workgroup holds", a->k[0], a->k[1]);
-    const int kprime = a->tile_mode ? a->nprobe : (a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages);
+    const bool rank_all = a->tile_mode || a->ring_cap > 0;
+    const int kprime = rank_all ? a->nprobe : (a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages);
     IMI_REQUIRE(kprime <= kCap, IMI_ERR_UNSUPPORTED, "imi_select: %d cells to rank exceed %d", kprime, kCap);
     IMI_REQUIRE(a->sel_cap >= kprime, IMI_ERR_INVALID, "imi_select: sel_cap %d < %d (%s)", a->sel_cap, kprime,
-                a->tile_mode ? "nprobe" : "min(nprobe, buffer_pages)");
+                rank_all ? "nprobe" : "min(nprobe, buffer_pages)");
     return IMI_OK;
 }
 
-template <int EPT>
+template <int EPT, bool ONLINE>
 int launch_ept(const SelParams& p, int H, hipStream_t stream) {
     constexpr int DP = 64;
     const size_t cand = static_cast<size_t>(kCap) * (sizeof(uint64_t) + 6 * sizeof(int));
-    const size_t ct = (static_cast<size_t>(DP) * (p.k[1] + 1) + static_cast<size_t>(p.k[0]) * (DP + 1)) * sizeof(float);
+    size_t ct = (static_cast<size_t>(DP) * (p.k[1] + 1) + static_cast<size_t>(p.k[0]) * (DP + 1)) * sizeof(float);
+    if (p.upd_slot) ct += static_cast<size_t>(kOvr) * 130 * sizeof(float);   // override rows + scores
     const size_t lds = cand > ct ? cand : ct;
     static bool attr_set = false;
     if (!attr_set) {
-        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&select_kernel<DP, EPT>),
+        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&select_kernel<DP, EPT, ONLINE>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024));
         attr_set = true;
     }
-    hipLaunchKernelGGL((select_kernel<DP, EPT>), dim3(H), dim3(kSelThreads), lds, stream, p);
+    hipLaunchKernelGGL((select_kernel<DP, EPT, ONLINE>), dim3(H), dim3(kSelThreads), lds, stream, p);
     IMI_LAUNCH_CHECK("select_kernel");
     return IMI_OK;
 }
@@ -560,6 +711,8 @@ int select_launch(const imi_select_args* a, hipStream_t stream) {
     if (rc) return rc;
     IMI_REQUIRE(a->sel_cell && a->sel_offset && a->sel_count && a->sel_prefix && a->n_selected && a->n_rows,
                 IMI_ERR_INVALID, "imi_select: null output pointer");
+    IMI_REQUIRE(a->ring_cap == 0 || (a->delta_rows && a->n_delta), IMI_ERR_INVALID,
+                "imi_select: null delta output pointer");
     if (a->parts == 4) return select4_launch(a, stream);
     SelParams p;
     p.q = a->query;
@@ -587,13 +740,32 @@ int select_launch(const imi_select_args* a, hipStream_t stream) {
     p.n_sel = a->n_selected;
     p.n_rows = a->n_rows;
     p.sel_cap = a->sel_cap;
+    p.shadow = a->shadow;
+    p.shadow_rows = a->shadow_rows;
+    p.upd_slot = a->upd_slot;
+    p.upd_row = a->upd_row;
+    p.upd_n = a->upd_n;
+    p.ring_cell = a->ring_cell;
+    p.ring_row = a->ring_row;
+    p.ring_n = a->ring_n;
+    p.ring_cap = a->ring_cap;
+    p.exec_rows = a->exec_rows;
+    p.delta_rows = a->delta_rows;
+    p.n_delta = a->n_delta;
     const int rows_in_flight = kSelThreads / a->k[1];
     const int ept = (a->k[0] + rows_in_flight - 1) / rows_in_flight;
-    if (ept <= 1) return launch_ept<1>(p, a->kv_heads, stream);
-    if (ept <= 2) return launch_ept<2>(p, a->kv_heads, stream);
-    if (ept <= 4) return launch_ept<4>(p, a->kv_heads, stream);
-    if (ept <= 8) return launch_ept<8>(p, a->kv_heads, stream);
-    return launch_ept<16>(p, a->kv_heads, stream);
+    if (p.upd_slot || p.ring_cap > 0) {
+        if (ept <= 1) return launch_ept<1, true>(p, a->kv_heads, stream);
+        if (ept <= 2) return launch_ept<2, true>(p, a->kv_heads, stream);
+        if (ept <= 4) return launch_ept<4, true>(p, a->kv_heads, stream);
+        if (ept <= 8) return launch_ept<8, true>(p, a->kv_heads, stream);
+        return launch_ept<16, true>(p, a->kv_heads, stream);
+    }
+    if (ept <= 1) return launch_ept<1, false>(p, a->kv_heads, stream);
+    if (ept <= 2) return launch_ept<2, false>(p, a->kv_heads, stream);
+    if (ept <= 4) return launch_ept<4, false>(p, a->kv_heads, stream);
+    if (ept <= 8) return launch_ept<8, false>(p, a->kv_heads, stream);
+    return launch_ept<16, false>(p, a->kv_heads, stream);
 }
 
 }  // namespace imi

@@ -68,6 +68,19 @@ struct Sel4 {
     uint32_t* ext;           // [H][4]: max order key, ~min order key, candidate count, unused
     uint64_t* cand;          // [H][kCand4]
     int32_t* cidx;           // [H][kCand4]
+    // online index maintenance: replaced centroids (by compact id) and the
+    // delta ring
+    const float* shadow;
+    int shadow_rows;
+    const int32_t* upd_slot;
+    const int32_t* upd_row;
+    const int32_t* ring_cell;
+    const int32_t* ring_row;
+    const int32_t* ring_n;
+    int ring_cap;
+    int exec_rows;
+    int32_t* delta_rows;
+    int32_t* n_delta;
 };
 
 __device__ __forceinline__ float key_score(uint64_t key) {
@@ -94,12 +107,16 @@ __device__ __forceinline__ int head_tokens(const Sel4& a, int h) {
     return a.head_max_tokens ? min(a.head_max_tokens[h], a.max_tokens) : a.max_tokens;
 }
 
+// cells to rank: every kept cell costs a page except in tile mode, and the
+// delta match needs the ranks the page cut drops
 __device__ __forceinline__ int kprime(const Sel4& a, int h, int na) {
     const int bp = head_pages(a, h);
-    int kp = a.tile_mode ? a.nprobe : (a.nprobe < bp ? a.nprobe : bp);
+    int kp = (a.tile_mode || a.ring_cap > 0) ? a.nprobe : (a.nprobe < bp ? a.nprobe : bp);
     return kp < na ? kp : na;
 }
 
+// ONLINE: replaced centroids / the delta ring (a separate instantiation).
+template <bool ONLINE>
 __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     __shared__ float qs[128];
     __shared__ float cs[4][kK4][kDp4 + 1];   // padded rows: lanes hit different banks
@@ -134,10 +151,26 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
             g /= static_cast<uint32_t>(a.k[p]);
         }
         float s = 0.0f;
+        const int us = ONLINE && a.upd_slot ? a.upd_slot[static_cast<int64_t>(h) * a.cap + c] : -1;
+        if (us < 0) {
 #pragma unroll
-        for (int p = 0; p < 4; ++p)
+            for (int p = 0; p < 4; ++p)
 #pragma unroll
-            for (int d = 0; d < kDp4; ++d) s = __builtin_fmaf(qs[p * kDp4 + d], cs[p][l[p]][d], s);
+                for (int d = 0; d < kDp4; ++d) s = __builtin_fmaf(qs[p * kDp4 + d], cs[p][l[p]][d], s);
+        } else {
+            // replaced centroid (async_update.py:7-19): the chain over its shadow row
+            const int row = min(max(a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + min(us, a.shadow_rows - 1)], 0),
+                                a.shadow_rows - 1);
+            const float4* sr =
+                reinterpret_cast<const float4*>(a.shadow + (static_cast<int64_t>(h) * a.shadow_rows + row) * 128);
+            for (int d4 = 0; d4 < 32; ++d4) {
+                const float4 v = sr[d4];
+                s = __builtin_fmaf(qs[4 * d4 + 0], v.x, s);
+                s = __builtin_fmaf(qs[4 * d4 + 1], v.y, s);
+                s = __builtin_fmaf(qs[4 * d4 + 2], v.z, s);
+                s = __builtin_fmaf(qs[4 * d4 + 3], v.w, s);
+            }
+        }
         const uint32_t ok = order_key(s);
         const uint32_t gv = static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c]);
         a.keys[static_cast<int64_t>(h) * a.cap + c] = (static_cast<uint64_t>(ok) << 32) | (0xFFFFFFFFu - gv);
@@ -252,10 +285,13 @@ __device__ __forceinline__ void block_scan2(int& x, int& y, int* sh, int& tx, in
     __syncthreads();
 }
 
+template <bool ONLINE>
 __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     __shared__ uint64_t sk[kCand4];
     __shared__ int si[kCand4];
     __shared__ int sh[48];
+    __shared__ int shk[kFinalThreads / 64];
+    __shared__ int s_rows;
     __shared__ uint32_t h256[256];
     const int h = blockIdx.x, tid = threadIdx.x;
     const int na = n_active(a, h);
@@ -384,26 +420,35 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     int tincl = tsum, pincl = psum;
     block_scan2(tincl, pincl, sh, ttot, ptot);
     int texcl = tincl - tsum, pexcl = pincl - psum;
-    int kept = 0;
+    int kept = 0, kept_tok = 0;
     int excl_tok[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int r = 2 * tid + u;
         excl_tok[u] = texcl;
         pexcl += pg2[u];
-        const bool keep = r < C && r < a.nprobe && texcl < head_tokens(a, h) &&
-                          pexcl <= (a.tile_mode ? 0 : head_pages(a, h));
+        const bool keep_tok = r < C && r < a.nprobe && texcl < head_tokens(a, h);
+        const bool keep = keep_tok && pexcl <= (a.tile_mode ? 0 : head_pages(a, h));
         kept += keep ? 1 : 0;
+        kept_tok += keep_tok ? 1 : 0;
         texcl += s2[u];
     }
-    // the rules are monotone in rank, so the kept ranks are the first m
+    // the rules are monotone in rank, so the kept ranks are the first m (the
+    // first m_tok before the page cut)
     {
         const int wk = wave_sum_i(kept);
-        if (lane_id() == 0) sh[32 + (tid >> 6)] = wk;
+        const int wt = ONLINE ? wave_sum_i(kept_tok) : 0;
+        if (lane_id() == 0) {
+            sh[32 + (tid >> 6)] = wk;
+            if (ONLINE) shk[tid >> 6] = wt;
+        }
     }
     __syncthreads();
-    int m = 0;
-    for (int w = 0; w < kFinalThreads / 64; ++w) m += sh[32 + w];
+    int m = 0, m_tok = 0;
+    for (int w = 0; w < kFinalThreads / 64; ++w) {
+        m += sh[32 + w];
+        if (ONLINE) m_tok += shk[w];
+    }
     int32_t* out_cell = a.sel_cell + static_cast<int64_t>(h) * a.sel_cap;
     int32_t* out_off = a.sel_offset + static_cast<int64_t>(h) * a.sel_cap;
     int32_t* out_cnt = a.sel_count + static_cast<int64_t>(h) * a.sel_cap;
@@ -421,6 +466,7 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
             prefix_out[m] = total;
             a.n_sel[h] = m;
             a.n_rows[h] = total;
+            if (ONLINE) s_rows = total;
         }
     }
     if (m == 0 && tid == 0) {
@@ -430,6 +476,34 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     }
     // leave the range words zero for the next call
     if (tid < 4) a.ext[h * 4 + tid] = 0;
+    if (ONLINE && a.ring_cap > 0) {
+        // Delta append (async_update.py:20-76): the ring entries whose cell
+        // is one of the m_tok cells that pass nprobe and the token budget
+        // (global ids, in si once the ranks are read), or the padding id when
+        // m_tok < nprobe, up to the execution-buffer rows left.
+        int* table = si;
+        __syncthreads();
+        const int rows_sel = m > 0 ? s_rows : 0;
+        for (int i = tid; i < kSetSize; i += kFinalThreads) table[i] = -1;
+        __syncthreads();
+        for (int r = tid; r < m_tok; r += kFinalThreads)
+            set_insert(table, static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(sk[r] & 0xFFFFFFFFull)));
+        __syncthreads();
+        const int nvalid = min(a.ring_n[h], a.ring_cap);
+        bool match = false;
+        int rrow = 0;
+        if (tid < nvalid) {
+            const int code = a.ring_cell[static_cast<int64_t>(h) * a.ring_cap + tid];
+            rrow = a.ring_row[static_cast<int64_t>(h) * a.ring_cap + tid];
+            match = code >= 0 ? set_find(table, code) : (code == -1 && m_tok < a.nprobe);
+        }
+        int f = match ? 1 : 0, z = 0, tot, ztot;
+        block_scan2(f, z, sh, tot, ztot);
+        const int pos = f - (match ? 1 : 0);
+        const int nd = min(tot, max(a.exec_rows - rows_sel, 0));
+        if (match && pos < nd) a.delta_rows[static_cast<int64_t>(h) * a.ring_cap + pos] = rrow;
+        if (tid == 0) a.n_delta[h] = nd;
+    }
 }
 
 size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
@@ -466,12 +540,12 @@ int select4_validate(const imi_select_args* a) {
                     "imi_select: 4-way k[%d]=%d outside [1,%d]", p, a->k[p], kK4);
     IMI_REQUIRE(a->compact_gid && a->compact_size && a->compact_offset && a->n_active && a->compact_cap > 0,
                 IMI_ERR_INVALID, "imi_select: 4-way selection needs the compact cell arrays");
-    const int kprime_max =
-        a->tile_mode ? a->nprobe : (a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages);
+    const bool rank_all = a->tile_mode || a->ring_cap > 0;
+    const int kprime_max = rank_all ? a->nprobe : (a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages);
     IMI_REQUIRE(kprime_max <= kSelCap4, IMI_ERR_UNSUPPORTED, "imi_select: %d cells to rank exceed %d", kprime_max,
                 kSelCap4);
     IMI_REQUIRE(a->sel_cap >= kprime_max, IMI_ERR_INVALID, "imi_select: sel_cap %d < %d (%s)", a->sel_cap,
-                kprime_max, a->tile_mode ? "nprobe" : "min(nprobe, buffer_pages)");
+                kprime_max, rank_all ? "nprobe" : "min(nprobe, buffer_pages)");
     return IMI_OK;
 }
 
@@ -516,14 +590,32 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     p.n_sel = a->n_selected;
     p.n_rows = a->n_rows;
     p.sel_cap = a->sel_cap;
+    p.shadow = a->shadow;
+    p.shadow_rows = a->shadow_rows;
+    p.upd_slot = a->upd_slot;
+    p.upd_row = a->upd_row;
+    p.ring_cell = a->ring_cell;
+    p.ring_row = a->ring_row;
+    p.ring_n = a->ring_n;
+    p.ring_cap = a->ring_cap;
+    p.exec_rows = a->exec_rows;
+    p.delta_rows = a->delta_rows;
+    p.n_delta = a->n_delta;
     const dim3 grid((a->compact_cap + kScoreThreads - 1) / kScoreThreads, a->kv_heads);
-    hipLaunchKernelGGL(sel4_score_kernel, grid, dim3(kScoreThreads), 0, stream, p);
+    const bool online = p.upd_slot || p.ring_cap > 0;
+    if (online)
+        hipLaunchKernelGGL(sel4_score_kernel<true>, grid, dim3(kScoreThreads), 0, stream, p);
+    else
+        hipLaunchKernelGGL(sel4_score_kernel<false>, grid, dim3(kScoreThreads), 0, stream, p);
     IMI_LAUNCH_CHECK("sel4_score_kernel");
     hipLaunchKernelGGL(sel4_hist_kernel, grid, dim3(kScoreThreads), 0, stream, p);
     IMI_LAUNCH_CHECK("sel4_hist_kernel");
     hipLaunchKernelGGL(sel4_gather_kernel, grid, dim3(kScoreThreads), 0, stream, p);
     IMI_LAUNCH_CHECK("sel4_gather_kernel");
-    hipLaunchKernelGGL(sel4_final_kernel, dim3(a->kv_heads), dim3(kFinalThreads), 0, stream, p);
+    if (online)
+        hipLaunchKernelGGL(sel4_final_kernel<true>, dim3(a->kv_heads), dim3(kFinalThreads), 0, stream, p);
+    else
+        hipLaunchKernelGGL(sel4_final_kernel<false>, dim3(a->kv_heads), dim3(kFinalThreads), 0, stream, p);
     IMI_LAUNCH_CHECK("sel4_final_kernel");
     return IMI_OK;
 }

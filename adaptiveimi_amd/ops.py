@@ -15,7 +15,7 @@ from typing import Dict, Optional, Sequence, Tuple
 import torch
 
 from . import _lib
-from ._lib import AttentionArgs, DecodeArgs, IndexArgs, KmeansArgs, SelectArgs, check
+from ._lib import AttentionArgs, DecodeArgs, IndexArgs, KmeansArgs, SelectArgs, UpdateArgs, check
 
 _WS: Dict[Tuple[str, int], torch.Tensor] = {}
 
@@ -315,16 +315,117 @@ def _compact_fields(a, compact: Optional[Dict[str, torch.Tensor]]) -> None:
     a.compact_cap = compact["compact_gid"].shape[1]
 
 
+class OnlineUpdate:
+    """One layer's online index maintenance: the reference's async centroid
+    update and delta ring (async_update.py:77-162; state of runtime.py:106-166).
+
+    shadow [H, n_rows, D] f32 starts as the merged centroids by compact id
+    (rows past n_active zero), centroid_counts as the cell sizes.  assign()
+    takes a batch of decode keys from the steady zone (cluster = arg-max dot
+    product over the shadow, delta counts and sums, ring entries); refresh()
+    replaces the centroids whose delta count reached the threshold.  The
+    selection reads the shadow rows of replaced cells and matches the ring
+    against the kept cells (select / DecodePlan with ``update=``).  Call
+    refresh() before the next step's selection, and before the next assign().
+    index_by_gid: the override slots are indexed by global cell id (2-way
+    selection) instead of compact id (4-way)."""
+
+    def __init__(self, compact_centroids: torch.Tensor, compact_size: torch.Tensor, compact_gid: torch.Tensor,
+                 n_active: torch.Tensor, padding_id: int, threshold: int, ring_cap: int, n_index: int,
+                 index_by_gid: bool):
+        dev = _require_device(compact_centroids, compact_size, compact_gid, n_active)
+        H, n_rows, D = compact_centroids.shape
+        if D != 128:
+            raise ValueError("online update needs head_dim 128")
+        self.device, self.H, self.n_rows, self.D = dev, H, n_rows, D
+        self.padding_id, self.threshold, self.ring_cap = int(padding_id), int(threshold), int(ring_cap)
+        self.n_index, self.index_by_gid = int(n_index), bool(index_by_gid)
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.shadow = compact_centroids.to(torch.float32).contiguous().clone()
+        self.centroid_counts = compact_size.to(torch.int32).contiguous().clone()
+        self.delta_counts = torch.zeros((H, n_rows), **i32)
+        self.delta_sums = torch.zeros((H, n_rows, D), dtype=torch.float32, device=dev)
+        self.compact_gid = compact_gid.to(torch.int32).contiguous()
+        self.n_active = n_active.to(torch.int32).contiguous()
+        self.ring_id = torch.full((H, ring_cap), int(padding_id), **i32)
+        self.ring_cell = torch.full((H, ring_cap), -2, **i32)
+        self.ring_row = torch.zeros((H, ring_cap), **i32)
+        self.ring_pos = torch.zeros((H,), **i32)
+        self.ring_n = torch.zeros((H,), **i32)
+        self.upd_slot = torch.full((H, self.n_index), -1, **i32)
+        self.upd_row = torch.zeros((H, n_rows), **i32)
+        self.upd_n = torch.zeros((H,), **i32)
+        self._ws: Optional[torch.Tensor] = None
+
+    def _args(self, steady_keys: Optional[torch.Tensor], row0: int, count: int) -> UpdateArgs:
+        a = UpdateArgs(steady_stride=0, row0=int(row0), count=int(count), kv_heads=self.H, dim=self.D,
+                       shadow=self.shadow.data_ptr(), n_rows=self.n_rows, padding_id=self.padding_id,
+                       n_active=self.n_active.data_ptr(), compact_gid=self.compact_gid.data_ptr(),
+                       centroid_counts=self.centroid_counts.data_ptr(), delta_counts=self.delta_counts.data_ptr(),
+                       delta_sums=self.delta_sums.data_ptr(), threshold=self.threshold,
+                       ring_id=self.ring_id.data_ptr(), ring_cell=self.ring_cell.data_ptr(),
+                       ring_row=self.ring_row.data_ptr(), ring_pos=self.ring_pos.data_ptr(),
+                       ring_n=self.ring_n.data_ptr(), ring_cap=self.ring_cap, upd_slot=self.upd_slot.data_ptr(),
+                       upd_row=self.upd_row.data_ptr(), upd_n=self.upd_n.data_ptr(), n_index=self.n_index,
+                       index_by_gid=int(self.index_by_gid))
+        if steady_keys is not None:
+            if steady_keys.dim() != 3 or steady_keys.shape[0] != self.H or not steady_keys.is_contiguous():
+                raise ValueError(f"steady_keys must be a contiguous [{self.H}, rows, {self.D}] tensor")
+            _as_bits(steady_keys)
+            a.steady_keys = steady_keys.data_ptr()
+            a.steady_stride = steady_keys.shape[1]
+        return a
+
+    def assign(self, steady_keys: torch.Tensor, row0: int, count: int) -> None:
+        """async_update.py:119-134, 146-161 for the keys at steady rows
+        [row0, row0 + count) of steady_keys [H, rows, D] (bf16)."""
+        a = self._args(steady_keys, row0, count)
+        need = ctypes.c_size_t()
+        check(_lib.lib().imi_update_workspace_size(ctypes.byref(a), ctypes.byref(need)), "imi_update_workspace_size")
+        if self._ws is None or self._ws.numel() < need.value:
+            self._ws = torch.empty(max(int(need.value), 256), dtype=torch.uint8, device=self.device)
+        a.workspace = self._ws.data_ptr()
+        a.workspace_bytes = self._ws.numel()
+        check(_lib.lib().imi_update_assign(ctypes.byref(a), _stream(self.device)), "imi_update_assign")
+
+    def refresh(self, count: int) -> None:
+        """async_update.py:135-143 for the batch of the last assign(count)."""
+        a = self._args(None, 0, count)
+        check(_lib.lib().imi_update_refresh(ctypes.byref(a), _stream(self.device)), "imi_update_refresh")
+
+    def wire(self, s: SelectArgs, exec_rows: int) -> None:
+        """Point selection arguments at this state (replaced centroids and
+        the delta ring)."""
+        s.shadow = self.shadow.data_ptr()
+        s.shadow_rows = self.n_rows
+        s.upd_slot = self.upd_slot.data_ptr()
+        s.upd_row = self.upd_row.data_ptr()
+        s.upd_n = self.upd_n.data_ptr()
+        s.ring_cell = self.ring_cell.data_ptr()
+        s.ring_row = self.ring_row.data_ptr()
+        s.ring_n = self.ring_n.data_ptr()
+        s.ring_cap = self.ring_cap
+        s.exec_rows = int(exec_rows)
+
+
+def _sel_cap(budget: Budget, update: Optional[OnlineUpdate]) -> int:
+    """Ranks the selection keeps: the delta match needs all of nprobe."""
+    return max(budget.sel_cap, budget.nprobe) if update is not None else budget.sel_cap
+
+
 def select(query: torch.Tensor, centroids: torch.Tensor, cell_count: torch.Tensor, cell_offset: torch.Tensor,
-           ks: Sequence[int], budget: Budget, compact: Optional[Dict[str, torch.Tensor]] = None
-           ) -> Dict[str, torch.Tensor]:
+           ks: Sequence[int], budget: Budget, compact: Optional[Dict[str, torch.Tensor]] = None,
+           update: Optional[OnlineUpdate] = None, exec_rows: int = 0) -> Dict[str, torch.Tensor]:
     """Scores + top-nprobe + token prefix + page rule, per KV head
     (retrieval.py:295-303,357; wave_buffer_cpu_hotcold.cpp:303-371).
-    A 4-way IMI needs ``compact`` (the build_index outputs with compact=True)."""
+    A 4-way IMI needs ``compact`` (the build_index outputs with compact=True).
+    With ``update`` the replaced centroids are scored and the delta ring is
+    matched (outputs delta_rows [H, ring_cap], n_delta [H]); exec_rows =
+    execution-buffer rows after the static rows."""
     dev = _require_device(query, centroids, cell_count, cell_offset)
     _as_bits(query)
     H, G, D = query.shape
-    cap = budget.sel_cap
+    cap = _sel_cap(budget, update)
     out = {
         "sel_cell": torch.full((H, cap), -1, dtype=torch.int32, device=dev),
         "sel_offset": torch.zeros((H, cap), dtype=torch.int32, device=dev),
@@ -344,6 +445,12 @@ def select(query: torch.Tensor, centroids: torch.Tensor, cell_count: torch.Tenso
     _compact_fields(a, compact)
     keep = _budget_fields(a, budget, H, dev)
     a.tile_mode = int(bool(budget.tile_mode))
+    if update is not None:
+        update.wire(a, exec_rows)
+        out["delta_rows"] = torch.zeros((H, update.ring_cap), dtype=torch.int32, device=dev)
+        out["n_delta"] = torch.zeros((H,), dtype=torch.int32, device=dev)
+        a.delta_rows = out["delta_rows"].data_ptr()
+        a.n_delta = out["n_delta"].data_ptr()
     need = ctypes.c_size_t()
     check(_lib.lib().imi_select_workspace_size(ctypes.byref(a), ctypes.byref(need)), "imi_select_workspace_size")
     if need.value:
@@ -357,7 +464,10 @@ def select(query: torch.Tensor, centroids: torch.Tensor, cell_count: torch.Tenso
 def sparse_attention(query: torch.Tensor, steady_keys: Optional[torch.Tensor], steady_values: Optional[torch.Tensor],
                      static_len: int, list_keys: torch.Tensor, list_values: torch.Tensor, sel: Dict[str, torch.Tensor],
                      max_rows: int, scale: Optional[float] = None, return_lse: bool = False):
-    """Gather + GQA decode attention over [static rows | selected rows]."""
+    """Gather + GQA decode attention over [static rows | selected rows |
+    delta rows]; the delta rows (steady-zone rows) come from a selection
+    made with ``update`` (sel["delta_rows"], sel["n_delta"]), and max_rows
+    must then also cover them."""
     dev = _require_device(query, list_keys, list_values)
     _as_bits(query)
     H, G, D = query.shape
@@ -374,6 +484,10 @@ def sparse_attention(query: torch.Tensor, steady_keys: Optional[torch.Tensor], s
                       max_rows=int(max_rows), kv_heads=H, groups=G, dim=D,
                       scale=float(scale if scale is not None else 1.0 / math.sqrt(D)), out=out.data_ptr(),
                       out_lse=_ptr(lse))
+    if "delta_rows" in sel:
+        a.delta_rows = sel["delta_rows"].data_ptr()
+        a.n_delta = sel["n_delta"].data_ptr()
+        a.delta_cap = sel["delta_rows"].shape[1]
     need = ctypes.c_size_t()
     check(_lib.lib().imi_attention_workspace_size(ctypes.byref(a), ctypes.byref(need)),
           "imi_attention_workspace_size")
@@ -394,16 +508,18 @@ class DecodePlan:
                  steady_keys: Optional[torch.Tensor], steady_values: Optional[torch.Tensor], groups: int,
                  scale: Optional[float] = None, query: Optional[torch.Tensor] = None,
                  out: Optional[torch.Tensor] = None, out_lse: Optional[torch.Tensor] = None,
-                 compact: Optional[Dict[str, torch.Tensor]] = None):
+                 compact: Optional[Dict[str, torch.Tensor]] = None, update: Optional[OnlineUpdate] = None):
         dev = _require_device(centroids, cell_count, cell_offset, list_keys, list_values)
         self.device = dev
         H, _, D = list_keys.shape
         self.H, self.G, self.D = H, groups, D
         self.budget = budget
+        self.update = update
+        self.sel_cap = _sel_cap(budget, update)
         self.query = query if query is not None else torch.zeros((H, groups, D), dtype=torch.bfloat16, device=dev)
         self.out = out if out is not None else torch.empty((H * groups, D), dtype=torch.bfloat16, device=dev)
         self._keep = (centroids, cell_count, cell_offset, list_keys, list_values, steady_keys, steady_values,
-                      out_lse, compact)
+                      out_lse, compact, update)
         a = DecodeArgs()
         s = a.sel
         s.query = self.query.data_ptr()
@@ -414,10 +530,12 @@ class DecodePlan:
         s.k = _ks(ks)
         s.nprobe, s.max_tokens = budget.nprobe, budget.max_tokens
         s.buffer_pages, s.page_size = budget.buffer_pages, budget.page_size
-        s.sel_cap = budget.sel_cap
+        s.sel_cap = self.sel_cap
         _compact_fields(s, compact)
         self._keep_budget = _budget_fields(s, budget, H, dev)
         s.tile_mode = int(bool(budget.tile_mode))
+        if update is not None:
+            update.wire(s, 0)
         t = a.attn
         t.query = self.query.data_ptr()
         t.steady_keys = _ptr(steady_keys)
@@ -426,7 +544,7 @@ class DecodePlan:
         t.static_len = 0
         t.list_keys, t.list_values = list_keys.data_ptr(), list_values.data_ptr()
         t.list_rows = list_keys.shape[1]
-        t.max_rows = budget.max_rows
+        t.max_rows = budget.max_rows + (update.ring_cap if update is not None else 0)
         t.kv_heads, t.groups, t.dim = H, groups, D
         t.scale = float(scale if scale is not None else 1.0 / math.sqrt(D))
         t.out = self.out.data_ptr()
@@ -443,15 +561,21 @@ class DecodePlan:
 
     def _selection_views(self) -> Dict[str, torch.Tensor]:
         """Views of the workspace where the selection outputs land."""
-        H, cap = self.H, self.budget.sel_cap
+        H, cap = self.H, self.sel_cap
         i32 = self.ws.view(torch.int32)
         off = 0
         views = {}
+        rc = self.update.ring_cap if self.update is not None else 0
         for name, n in (("sel_cell", H * cap), ("sel_offset", H * cap), ("sel_count", H * cap),
-                        ("sel_prefix", H * (cap + 1)), ("n_selected", H), ("n_rows", H)):
+                        ("sel_prefix", H * (cap + 1)), ("n_selected", H), ("n_rows", H),
+                        ("delta_rows", H * max(rc, 1)), ("n_delta", H)):
             off = (off + 63) // 64 * 64  # 256-byte alignment in int32 units
             views[name] = i32[off:off + n]
             off += n
+        if rc:
+            views["delta_rows"] = views["delta_rows"].view(H, rc)
+        else:
+            del views["delta_rows"], views["n_delta"]
         views["sel_cell"] = views["sel_cell"].view(H, cap)
         views["sel_offset"] = views["sel_offset"].view(H, cap)
         views["sel_count"] = views["sel_count"].view(H, cap)
@@ -461,7 +585,13 @@ class DecodePlan:
     def set_static_len(self, static_len: int) -> None:
         self.args.attn.static_len = int(static_len)
 
-    def run(self, query: torch.Tensor, out: torch.Tensor, static_len: int, stream: Optional[int] = None) -> torch.Tensor:
+    def set_exec_rows(self, exec_rows: int) -> None:
+        """Execution-buffer rows left after the static rows (the delta
+        append's bound, retrieval.py via async_update.py:57-72)."""
+        self.args.sel.exec_rows = int(exec_rows)
+
+    def run(self, query: torch.Tensor, out: torch.Tensor, static_len: int, stream: Optional[int] = None,
+            exec_rows: Optional[int] = None) -> torch.Tensor:
         """One full step on caller-owned query [H, G, D] and out [H * G, D]
         buffers (no copies: the plan's pointers are redirected)."""
         _as_bits(query)
@@ -473,6 +603,8 @@ class DecodePlan:
         a.sel.query = a.attn.query = query.data_ptr()
         a.attn.out = out.data_ptr()
         a.attn.static_len = int(static_len)
+        if exec_rows is not None:
+            a.sel.exec_rows = int(exec_rows)
         a.phases = 3
         try:
             check(self._fn(self._ref, stream if stream is not None else _stream(self.device)), "imi_decode_step")

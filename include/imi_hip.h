@@ -194,6 +194,27 @@ typedef struct {
      * pages.  Selected rows then reach max_tokens - 1 + buffer_pages *
      * page_size, and sel_cap must cover nprobe.  0 = off. */
     int32_t tile_mode;
+    /* Online index maintenance (imi_update_*; async_update.py:7-19): cells
+     * whose merged centroid was replaced are scored over their shadow row
+     * (the same 128-term chain).  upd_slot NULL = no replaced centroids. */
+    const float* shadow;            /* [H][shadow_rows][D] */
+    int32_t shadow_rows;
+    const int32_t* upd_slot;        /* [H][ncells] (2-way) or [H][compact_cap] (4-way) */
+    const int32_t* upd_row;         /* [H][shadow_rows] */
+    const int32_t* upd_n;           /* [H] */
+    /* Delta append (async_update.py:20-76): ring entries whose cell is in the
+     * reference's `selected` (the cells that pass nprobe and the token
+     * budget, before the page cut, plus the padding id when fewer than
+     * nprobe pass) are appended after the selected rows, in ring index
+     * order, up to exec_rows - n_rows.  ring_cap 0 = off; not with
+     * tile_mode; sel_cap must then cover nprobe. */
+    const int32_t* ring_cell;       /* [H][ring_cap] match code (imi_update_args) */
+    const int32_t* ring_row;        /* [H][ring_cap] steady row of each entry */
+    const int32_t* ring_n;          /* [H] valid entries (ring index 0 ..) */
+    int32_t ring_cap;               /* <= 1024 */
+    int32_t exec_rows;              /* execution-buffer rows after the static rows */
+    int32_t* delta_rows;            /* out [H][ring_cap] steady rows appended */
+    int32_t* n_delta;               /* out [H] */
 } imi_select_args;
 
 /* Workspace imi_select needs (0 for 2-way IMI). */
@@ -230,13 +251,82 @@ typedef struct {
     float* out_lse;               /* device fp32 [H*G] natural-log LSE, may be NULL */
     void* workspace;              /* zero-filled before first use */
     size_t workspace_bytes;       /* >= imi_attention_workspace_size() */
+    /* Delta rows (imi_select delta append): steady-zone rows attended after
+     * the selected rows, or NULL.  max_rows must then also cover delta_cap. */
+    const int32_t* delta_rows;    /* [H][delta_cap] */
+    const int32_t* n_delta;       /* [H] */
+    int32_t delta_cap;
 } imi_attention_args;
 
 int imi_attention_workspace_size(const imi_attention_args* a, size_t* bytes);
 int imi_sparse_attention(const imi_attention_args* a, imi_stream_t stream);
 
+/* --------------------------------------------- online index maintenance
+ * The reference's async centroid update and delta append
+ * (cache_hub/adaptive_imi/async_update.py:77-162, state from
+ * runtime.py:106-166), split in two calls on the caller's stream:
+ *
+ * imi_update_assign  (async_update.py:119-134, 146-161) for the batch of
+ *   `count` decode keys at steady rows [row0, row0 + count): each key's
+ *   cluster is the first compact row with the largest dot product over the
+ *   shadow (torch.argmax of keys_fp32 @ shadow^T; the dot products here are
+ *   sequential fp32 FMA chains over d, -0 counted as +0); delta_counts +=
+ *   1 and delta_sums += key per key in batch order; the keys enter the delta
+ *   ring (ring_id = compact row, ring_cell = match code, ring_row = steady
+ *   row) at ring_pos, which advances modulo ring_cap; ring_n saturates at
+ *   ring_cap.
+ * imi_update_refresh (async_update.py:135-143) for the same batch: every
+ *   row the batch touched whose delta count reached `threshold` becomes
+ *   (shadow * centroid_count + delta_sum) / (centroid_count + delta_count),
+ *   its centroid count takes the sum and its delta state is cleared; an
+ *   occupied row (< n_active) so replaced gets an override slot that
+ *   imi_select reads.  The reference copies the shadow into the scored
+ *   centroids when its side stream has finished (async_update.py:7-19);
+ *   callers make that deterministic by calling refresh before the next
+ *   step's selection (and before the next assign).
+ *
+ * Match codes (ring_cell): the global cell id of an occupied row; -1 for
+ * the reference padding id (padding_id, which `selected` holds wherever a
+ * rank was not kept); -2 for any other empty slot (never selected).
+ */
+typedef struct {
+    const uint16_t* steady_keys;   /* device bf16 [H][steady_stride][D] */
+    int64_t steady_stride;
+    int32_t row0;                  /* steady row of the batch's first key */
+    int32_t count;                 /* keys in the batch, 1 .. ring_cap */
+    int32_t kv_heads, dim;         /* D = 128 */
+    float* shadow;                 /* device [H][n_rows][D] merged centroids by compact id */
+    int32_t n_rows;                /* compact rows held (>= n_active + 1) */
+    int32_t padding_id;            /* reference padding cluster id (n_centroids - 1) */
+    const int32_t* n_active;       /* device [H] */
+    const int32_t* compact_gid;    /* device [H][n_rows] global cell id per compact row */
+    int32_t* centroid_counts;      /* device [H][n_rows] */
+    int32_t* delta_counts;         /* device [H][n_rows] */
+    float* delta_sums;             /* device [H][n_rows][D] */
+    int32_t threshold;             /* >= 1 */
+    int32_t* ring_id;              /* device [H][ring_cap] compact row (delta_cluster_ids) */
+    int32_t* ring_cell;            /* device [H][ring_cap] match code */
+    int32_t* ring_row;             /* device [H][ring_cap] steady row */
+    int32_t* ring_pos;             /* device [H] next write position */
+    int32_t* ring_n;               /* device [H] valid entries */
+    int32_t ring_cap;              /* 1 .. 1024 (delta_tokens) */
+    int32_t* upd_slot;             /* device [H][n_index] override slot or -1 */
+    int32_t* upd_row;              /* device [H][n_rows] shadow row of each slot */
+    int32_t* upd_n;                /* device [H] slots in use */
+    int32_t n_index;               /* ncells (2-way, by global id) or n_rows (4-way, by compact id) */
+    int32_t index_by_gid;          /* 1: upd_slot is indexed by global cell id (2-way selection) */
+    void* workspace;               /* device, >= imi_update_workspace_size() bytes */
+    size_t workspace_bytes;
+} imi_update_args;
+
+int imi_update_workspace_size(const imi_update_args* a, size_t* bytes);
+int imi_update_assign(const imi_update_args* a, imi_stream_t stream);
+int imi_update_refresh(const imi_update_args* a, imi_stream_t stream);
+
 /* One decode step of one layer (retrieval.py:320-602, tile mode off):
- * imi_select followed by the gather + attention kernel on the same stream.
+ * imi_select followed by the gather + attention kernel on the same stream;
+ * with sel.ring_cap > 0 the matched delta-ring tokens are attended after the
+ * selected rows (attn.max_rows must also cover ring_cap).
  * The selection outputs and the split partials live in attn.workspace,
  * which must be zero-filled before its first use; every call leaves it
  * reusable.  Calls that share a workspace must not overlap.

@@ -327,6 +327,32 @@ void orc_select(const float* scores, const int32_t* sizes, const uint8_t* masked
     }
 }
 
+// Cluster of each new decode key in the async centroid update,
+// async_update.py:125-127: similarities = keys_fp32 @ shadow^T (torch.bmm),
+// cluster = torch.argmax (first index of the maximum).  The bmm summation
+// order is the BLAS library's and is not pinned by the reference; this
+// restatement fixes it to the sequential fp32 FMA chain over d, with -0
+// counted as +0 so that equal values tie and the lowest row wins.
+// keys [B][D], rows [N][D] fp32; out [B] row index.
+void orc_update_assign(const float* keys, int B, const float* rows, int N, int D, int32_t* out) {
+    for (int b = 0; b < B; ++b) {
+        const float* x = keys + (int64_t)b * D;
+        float best = 0.0f;
+        int32_t arg = 0;
+        for (int r = 0; r < N; ++r) {
+            const float* c = rows + (int64_t)r * D;
+            float s = 0.0f;
+            for (int d = 0; d < D; ++d) s = std::fmaf(x[d], c[d], s);
+            s = s + 0.0f;
+            if (r == 0 || s > best) {
+                best = s;
+                arg = r;
+            }
+        }
+        out[b] = arg;
+    }
+}
+
 // Softmax decode attention in double precision (closed form of the
 // unvendored weighted_flash_decoding called at retrieval.py:439-447):
 // out[h*G+g] = sum_r softmax_r(scale * q.k_r) v_r over the rows listed in

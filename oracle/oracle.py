@@ -18,6 +18,14 @@ Parity status per function (what pins it is in tests/test_oracle.py):
   attention             parity unpinned against the (unvendored)
                         weighted_flash_decoding; pinned against closed-form
                         softmax attention (uniform / one-hot cases)
+  update_assign         the reference's torch.bmm summation order is parity
+                        unpinned; the arg-max and its lowest-row tie rule are
+                        pinned on integer data (exact dot products) and
+                        against an fp64 arg-max away from near-ties
+  OnlineUpdateOracle    pinned: closed-form running means on integer data,
+                        the threshold/reset rule, ring order, and the
+                        delta-match rules (kept cells, padding id) on
+                        constructed cases
 """
 from __future__ import annotations
 
@@ -74,6 +82,8 @@ def lib():
         L.orc_select.restype = None
         L.orc_select.argtypes = [_f32p, _i32p, _u8p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                  ctypes.c_int, ctypes.c_int, _i32p, _i32p, _i64p]
+        L.orc_update_assign.restype = None
+        L.orc_update_assign.argtypes = [_f32p, ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int, _i32p]
         L.orc_attention.restype = None
         L.orc_attention.argtypes = [_u16p, _u16p, _u16p, ctypes.c_int64, _i64p, _i32p, ctypes.c_int64,
                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_double, _f64p]
@@ -451,3 +461,125 @@ def decode_step(q_bits: np.ndarray, heads: List[dict], steady_k: np.ndarray, ste
         nr.append(np.arange(n, dtype=np.int64))
     out = attention(q_bits, ek, ev, nr)
     return out, sel, m, rows
+
+
+# ------------------------------------------------ online index update ----
+
+def update_assign(keys_f32: np.ndarray, rows: np.ndarray) -> np.ndarray:
+    """async_update.py:125-127: arg-max over rows of keys @ rows^T, first
+    index on ties, dot products as sequential fp32 FMA chains (the
+    reference's bmm order is the BLAS library's).  keys [B, D], rows [N, D]."""
+    keys_f32 = np.ascontiguousarray(keys_f32, np.float32)
+    rows = np.ascontiguousarray(rows, np.float32)
+    B, D = keys_f32.shape
+    out = np.empty(B, np.int32)
+    lib().orc_update_assign(_p(keys_f32, _f32p), B, _p(rows, _f32p), rows.shape[0], D, _p(out, _i32p))
+    return out
+
+
+class OnlineUpdateOracle:
+    """The reference's async centroid update and delta ring, per KV head
+    (async_update.py:77-162; state from runtime.py:115-166), with the update
+    applied at the next step (the reference applies it once its side stream
+    has finished, async_update.py:7-19).
+
+    shadow [H, n_c, D] f32: merged centroids by compact id, zero past
+    n_active; sizes [H, n_c]: the cell sizes (centroid_counts)."""
+
+    def __init__(self, shadow: np.ndarray, sizes: np.ndarray, padding_id: int, threshold: int, ring_cap: int):
+        H, n_c, D = shadow.shape
+        self.shadow = np.array(shadow, np.float32)
+        self.cc = np.array(sizes, np.int64)
+        self.dc = np.zeros((H, n_c), np.int64)
+        self.ds = np.zeros((H, n_c, D), np.float32)
+        self.padding_id, self.threshold, self.cap = int(padding_id), int(threshold), int(ring_cap)
+        self.ring_id = np.full((H, ring_cap), padding_id, np.int64)
+        self.ring_row = np.zeros((H, ring_cap), np.int64)
+        self.pos = np.zeros(H, np.int64)
+        self.n = np.zeros(H, np.int64)
+        self.last_ids: Optional[np.ndarray] = None
+        self.replaced: List[List[int]] = [[] for _ in range(H)]   # compact rows, first-replacement order
+
+    def assign(self, keys_bits: np.ndarray, rows: Sequence[int]) -> np.ndarray:
+        """async_update.py:119-134 (scatter_add in batch order) and 146-161
+        (ring write).  keys_bits [H, B, D] bf16 bits; rows: steady rows."""
+        H, B, _ = keys_bits.shape
+        ids = np.empty((H, B), np.int64)
+        for h in range(H):
+            x = bf16_to_f32(keys_bits[h])
+            ids[h] = update_assign(x, self.shadow[h])
+            for s_ in range(B):
+                c = ids[h, s_]
+                self.ds[h, c] = self.ds[h, c] + x[s_]
+                self.dc[h, c] += 1
+            for s_ in range(B):
+                p = (self.pos[h] + s_) % self.cap
+                self.ring_id[h, p] = ids[h, s_]
+                self.ring_row[h, p] = rows[s_]
+            self.pos[h] = (self.pos[h] + B) % self.cap
+            self.n[h] = min(self.n[h] + B, self.cap)
+        self.last_ids = ids
+        return ids
+
+    def refresh(self) -> None:
+        """async_update.py:135-143 for the rows the last batch touched."""
+        ids = self.last_ids
+        if ids is None:
+            return
+        for h in range(ids.shape[0]):
+            for c in dict.fromkeys(int(v) for v in ids[h]):
+                if self.dc[h, c] < self.threshold:
+                    continue
+                total = self.cc[h, c] + self.dc[h, c]
+                num = self.shadow[h, c] * np.float32(self.cc[h, c]) + self.ds[h, c]
+                self.shadow[h, c] = num / np.float32(max(total, 1))
+                self.cc[h, c] = total
+                self.dc[h, c] = 0
+                self.ds[h, c] = 0.0
+                if c not in self.replaced[h]:
+                    self.replaced[h].append(c)
+        self.last_ids = None
+
+    def delta_rows(self, h: int, kept: Sequence[int], nprobe: int, exec_rows: int, rows_sel: int) -> List[int]:
+        """async_update.py:41-76 for one head: ring entries (index order, the
+        first n valid) whose cluster is one of the kept compact ids (the cells
+        passing nprobe and the token budget), or the padding id when fewer
+        than nprobe pass; at most exec_rows - rows_sel of them."""
+        ks = set(int(c) for c in kept)
+        pad = len(ks) < nprobe
+        out = [int(self.ring_row[h, p]) for p in range(int(self.n[h]))
+               if int(self.ring_id[h, p]) in ks or (pad and int(self.ring_id[h, p]) == self.padding_id)]
+        return out[: max(exec_rows - rows_sel, 0)]
+
+
+def decode_step_online(q_bits: np.ndarray, sizes: np.ndarray, offsets: np.ndarray, mask: np.ndarray,
+                       list_keys: np.ndarray, list_values: np.ndarray, steady_k: np.ndarray, steady_v: np.ndarray,
+                       static_len: int, upd: OnlineUpdateOracle, nprobe: int, max_tokens: int, buffer_pages: int,
+                       exec_rows: int, page_size: int = 8):
+    """sparse_attention with the async update on (retrieval.py:320-447 with
+    async_update.py:7-76): scores over the current centroids (the shadow),
+    selection, execution buffer [static rows | selected rows | delta rows]
+    and attention.  sizes/offsets/mask padded per head ([H, n_c(+1)]);
+    list_keys/values [H, L, D] bf16 bits.  Returns (out f64 [H, G, D], sel,
+    m, list rows per head, delta steady rows per head)."""
+    H, G, D = q_bits.shape
+    sc = scores(q_bits, upd.shadow)
+    sel, m, _ = select(sc, sizes, mask, nprobe, max_tokens, buffer_pages, page_size)
+    big = np.iinfo(np.int32).max // 2
+    sel_t, m_t, _ = select(sc, sizes, mask, nprobe, max_tokens, big, page_size)
+    rows = selected_rows(sel, m, offsets)
+    drows = [upd.delta_rows(h, sel_t[h, : m_t[h]], nprobe, exec_rows, len(rows[h])) for h in range(H)]
+    width = max(static_len + len(rows[h]) + len(drows[h]) for h in range(H))
+    ek = np.zeros((H, max(width, 1), D), np.uint16)
+    ev = np.zeros_like(ek)
+    nr = []
+    for h in range(H):
+        a, b = static_len, static_len + len(rows[h])
+        n = b + len(drows[h])
+        ek[h, :a], ev[h, :a] = steady_k[h, :a], steady_v[h, :a]
+        ek[h, a:b], ev[h, a:b] = list_keys[h][rows[h]], list_values[h][rows[h]]
+        ek[h, b:n], ev[h, b:n] = steady_k[h][drows[h]], steady_v[h][drows[h]]
+        nr.append(np.arange(n, dtype=np.int64))
+    out = attention(q_bits, ek, ev, nr)
+    return out, sel, m, rows, drows
+

@@ -33,7 +33,7 @@ def test_exports_every_declared_symbol(L):
 
 
 def test_version(L):
-    assert L.imi_version() == 4
+    assert L.imi_version() == 5
 
 
 def _kmeans_args(**over):
@@ -120,6 +120,56 @@ def test_select_and_decode_argument_checks(L):
     d.attn.groups = 5
     d.sel.groups = 5
     assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == 3
+
+
+def test_online_update_argument_checks(L):
+    from adaptiveimi_amd._lib import AttentionArgs, DecodeArgs, SelectArgs, UpdateArgs
+
+    u = UpdateArgs(steady_keys=16, steady_stride=1000, row0=980, count=16, kv_heads=8, dim=128, shadow=16,
+                   n_rows=4097, padding_id=4096, n_active=16, compact_gid=16, centroid_counts=16, delta_counts=16,
+                   delta_sums=16, threshold=16, ring_id=16, ring_cell=16, ring_row=16, ring_pos=16, ring_n=16,
+                   ring_cap=512, upd_slot=16, upd_row=16, upd_n=16, n_index=4096, index_by_gid=1)
+    need = ctypes.c_size_t()
+    assert L.imi_update_workspace_size(ctypes.byref(u), ctypes.byref(need)) == 0 and need.value >= 8 * 16 * 17 * 8
+    assert L.imi_update_assign(ctypes.byref(u), None) == 4          # no workspace given
+    u.row0 = 990
+    assert L.imi_update_assign(ctypes.byref(u), None) == 1          # rows past the steady zone
+    assert "steady zone" in L.imi_last_error().decode()
+    u.row0, u.count = 0, 65
+    assert L.imi_update_refresh(ctypes.byref(u), None) == 3         # batch above 64 keys
+    u.count, u.ring_cap = 16, 2000
+    assert L.imi_update_refresh(ctypes.byref(u), None) == 3
+    assert "ring_cap" in L.imi_last_error().decode()
+    u.ring_cap, u.delta_sums = 512, None
+    assert L.imi_update_refresh(ctypes.byref(u), None) == 1
+    assert "null state" in L.imi_last_error().decode()
+    # selection: the delta append is not available in tile mode, needs the ring
+    # and must rank all of nprobe
+    s = SelectArgs(query=16, centroids=16, cell_count=16, cell_offset=16, kv_heads=8, groups=4, dim=128, parts=2,
+                   nprobe=410, max_tokens=3276, buffer_pages=300, page_size=8, sel_cap=300, ring_cap=512,
+                   tile_mode=1)
+    s.k[0] = s.k[1] = 64
+    assert L.imi_select(ctypes.byref(s), None) == 3
+    assert "tile mode" in L.imi_last_error().decode()
+    s.tile_mode = 0
+    assert L.imi_select(ctypes.byref(s), None) == 1
+    assert "delta ring" in L.imi_last_error().decode()
+    s.ring_cell = s.ring_row = s.ring_n = 16
+    assert L.imi_select(ctypes.byref(s), None) == 1
+    assert "sel_cap 300 < 410 (nprobe)" in L.imi_last_error().decode()
+    s.sel_cap = 410
+    s.upd_slot = 16
+    assert L.imi_select(ctypes.byref(s), None) == 1
+    assert "shadow" in L.imi_last_error().decode()
+    s.upd_slot = None
+    d = DecodeArgs()
+    d.sel = s
+    d.attn = AttentionArgs(query=16, out=16, list_keys=16, list_values=16, kv_heads=8, groups=4, dim=128,
+                           max_rows=300 * 8, steady_keys=16, steady_values=16, steady_stride=200)
+    assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == 1   # max_rows misses the ring
+    assert "max_rows" in L.imi_last_error().decode()
+    d.attn.max_rows = 300 * 8 + 512
+    assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == 0
 
 
 def test_ops_refuse_cpu_tensors():

@@ -55,9 +55,18 @@ def test_cache_rejects_what_the_reference_rejects():
         _cache(subspace_parts=0)
 
 
-def test_async_update_warns():
-    with pytest.warns(RuntimeWarning, match="async_update"):
-        _cache(runtime_config={"async_update": {"enabled": True}})
+def test_async_update_config():
+    """cache.py:305-311: enabled, batch (16), threshold (16), delta_tokens (512)."""
+    c = _cache(runtime_config={"async_update": {"enabled": True}})
+    assert c.async_update_enabled and (c.async_update_batch, c.async_update_threshold,
+                                       c.async_update_delta_tokens) == (16, 16, 512)
+    c = _cache(runtime_config={"async_update": {"enabled": True, "batch": 4, "threshold": 0, "delta_tokens": 32}})
+    assert (c.async_update_batch, c.async_update_threshold, c.async_update_delta_tokens) == (4, 1, 32)
+    assert not _cache().async_update_enabled
+    with pytest.raises(ValueError, match="batch"):
+        _cache(runtime_config={"async_update": {"enabled": True, "batch": 100}})
+    with pytest.raises(ValueError, match="delta_tokens"):
+        _cache(runtime_config={"async_update": {"enabled": True, "delta_tokens": 4096}})
 
 
 def test_static_len_rule():
