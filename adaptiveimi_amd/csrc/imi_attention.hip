@@ -252,8 +252,8 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
                 const bool dl = DELTA && !st && n < N && lr < 0;   // delta row: steady row -1 - lr
                 const int64_t roff =
                     (st ? static_cast<int64_t>(n) : static_cast<int64_t>(dl ? -1 - lr : (n < N ? lr : 0))) * 128;
-                kb[slot][it] = *reinterpret_cast<const u32x4_t*>((st || dl ? skh : lkh) + roff + li * 8);
-                vb[slot][it] = *reinterpret_cast<const u32x4_t*>((st || dl ? svh : lvh) + roff + li * 8);
+                kb[slot][it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>((st || dl ? skh : lkh) + roff + li * 8));
+                vb[slot][it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>((st || dl ? svh : lvh) + roff + li * 8));
             }
         };
         load(0, 0);
