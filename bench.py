@@ -48,6 +48,9 @@ def parse():
     p.add_argument("--cpu-baseline", type=int, default=1)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-graph", action="store_true")
+    p.add_argument("--online-layers", type=int, default=4,
+                   help="layers of the online-index-maintenance leg (async_update: batch 16, threshold 16, "
+                        "512-token ring, 1024 decode keys); 0 skips it")
     p.add_argument("--copy-probe-mb", type=int, default=0,
                    help="run a device-to-device copy of this many MiB (3 times) before the timed region, as the "
                         "known-size reference for FETCH_SIZE / WRITE_SIZE counter runs")
@@ -192,6 +195,11 @@ def main():
     step_gbps = bytes_per_layer / (ms_per_step / L * 1e-3) / 1e9
     log(f"[bench] per launch: select {sel_us:.2f} us, attention+merge {att_us:.2f} us")
 
+    online = None
+    if args.online_layers > 0:
+        online = online_update_leg(args, ks, bud, static_total, capture)
+        log(f"[bench] online update: {online}")
+
     # ----------------------------------------------------- CPU baseline
     cpu = None
     if keep_first is not None:
@@ -228,8 +236,91 @@ def main():
                      "kernel": "attention_kernel + merge_kernel (gather, GQA split-K attention, split merge)",
                      "bytes_per_launch": int(bytes_per_layer)},
         "cpu_baseline": cpu,
+        "online_update": online,
     }
     print(json.dumps(result), flush=True)
+
+
+def online_update_leg(args, ks, bud, static_total, capture):
+    """The decode step with the reference's async update on (async_update.py:
+    batch 16, threshold 16, 512-token delta ring) after 1024 generated keys,
+    on the first online_layers layers (same seeds as the main run): time of
+    imi_update_assign / imi_update_refresh per call, and the per-layer step
+    with replaced centroids and delta rows against the same layers' plain
+    step.  Decode keys are prompt keys drawn at random (a new token's key
+    resembles the context's)."""
+    import torch
+
+    from adaptiveimi_amd import ops, synthetic
+
+    dev = torch.device("cuda:0")
+    H, G, D, NL = args.kv_heads, args.groups, 128, args.online_layers
+    batch, thr, ring, gen = 16, 16, 512, 1024
+    ncells = ks[0] * ks[1]
+    static_cap = static_total + gen + 8
+    static_len = static_total + gen
+    exec_rows = bud.buffer_pages * bud.page_size + static_cap - static_len
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    plain, online, keep = [], [], []
+    g = torch.Generator(device="cpu").manual_seed(11)
+    for layer in range(NL):
+        keys, values = synthetic.make_kv(H, args.context, seed=1000 + layer, device="cuda")
+        mid_k = keys[:, args.static_start:args.context - args.static_end]
+        mid_v = values[:, args.static_start:args.context - args.static_end]
+        cent, labels, _ = ops.kmeans(mid_k, list(ks), args.iters)
+        idx = ops.build_index(mid_k, mid_v, cent, labels, list(ks), compact=True, merged=True, n_centroids=ncells + 1)
+        sk = torch.zeros((H, static_cap, D), dtype=torch.bfloat16, device=dev)
+        sv = torch.zeros_like(sk)
+        sk[:, :args.static_start] = keys[:, :args.static_start]
+        sk[:, args.static_start:static_total] = keys[:, args.context - args.static_end:]
+        sv[:, :static_total] = torch.cat([values[:, :args.static_start], values[:, args.context - args.static_end:]], 1)
+        pick = torch.randint(0, mid_k.shape[1], (gen,), generator=g).to(dev)
+        sk[:, static_total:static_len] = mid_k[:, pick]
+        sv[:, static_total:static_len] = mid_v[:, pick]
+        upd = ops.OnlineUpdate(idx["compact_centroids"], idx["compact_size"], idx["compact_gid"], idx["n_active"],
+                               ncells, thr, ring, n_index=ncells, index_by_gid=True)
+        for b in range(gen // batch):
+            upd.assign(sk, static_total + b * batch, batch)
+            upd.refresh(batch)
+        q = synthetic.make_queries(mid_k, G, seed=layer)[0].contiguous()
+        for lst, u in ((plain, None), (online, upd)):
+            pl = ops.DecodePlan(cent, idx["cell_count"], idx["cell_offset"], ks, bud, idx["list_keys"],
+                                idx["list_values"], sk, sv, G, query=q, update=u)
+            pl.set_static_len(static_len)
+            pl.set_exec_rows(exec_rows)
+            lst.append(pl)
+        keep.append((upd, idx, cent, sk, sv))
+        del keys, values, labels
+    def graph_us(fn, per):
+        gr = capture(fn)
+        for _ in range(3):
+            gr.replay()
+        torch.cuda.synchronize()
+        ev0.record()
+        for _ in range(20):
+            gr.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) * 1e3 / (20 * per)
+
+    res = {}
+    for name, lst in (("plain", plain), ("online", online)):
+        for p_ in lst:
+            p_.step()
+        res[name] = [round(graph_us(lambda: [p_.step(phases=ph) for p_ in lst], NL), 2) for ph in (3, 1, 2)]
+    repl = sum(int(k[0].upd_n.sum().item()) for k in keep) / (NL * H)
+    drows = sum(int(p_.selection["n_delta"].sum().item()) for p_ in online) / (NL * H)
+    # the update kernels per call (graph replays: no host enqueue gaps); the
+    # replays keep updating the state, which only changes what they time
+    last = static_total + gen - batch
+    assign_us = graph_us(lambda: [k[0].assign(k[3], last, batch) for k in keep], NL)
+    refresh_us = graph_us(lambda: [k[0].refresh(batch) for k in keep], NL)
+    return {"layers": NL, "decode_keys": gen, "batch": batch, "threshold": thr, "ring": ring,
+            "assign_us": round(assign_us, 2), "refresh_us": round(refresh_us, 2),
+            "us_per_layer_step": res["online"][0], "select_us": res["online"][1], "attention_merge_us": res["online"][2],
+            "plain_us_per_layer_step": res["plain"][0], "plain_select_us": res["plain"][1],
+            "plain_attention_merge_us": res["plain"][2],
+            "replaced_cells_per_head": round(repl, 1), "delta_rows_per_head": round(drows, 1)}
 
 
 def measured_traffic():
