@@ -34,6 +34,7 @@ constexpr int kCap = 2048;     // candidate capacity
 constexpr int kMaxGroups = 8;  // query heads per KV head
 constexpr int kOvr = 64;       // replaced centroids scored per pass
 constexpr int kRingCap = 1024; // delta ring entries (one per thread)
+constexpr int kKeepWords = 512;  // bitmap of kept global cells (k0 * k1 <= 16384)
 
 struct SelParams {
     const uint16_t* q;
@@ -132,26 +133,33 @@ __device__ __forceinline__ int bucket_of(float s, float gmax, float inv) {
 }
 
 // Delta append (async_update.py:20-76, called at retrieval.py:420): the
-// ring entries (ring index order, the first ring_n valid) whose cell is in
-// the reference's `selected` -- the m_tok cells that pass nprobe and the
-// token budget (retrieval.py:295-303), plus the padding id when m_tok <
-// nprobe -- up to the execution-buffer rows left after the selected rows.
-// rcode / rrow: this thread's ring entry (thread = ring index).
-__device__ void delta_match(const SelParams& a, int h, int m_tok, int rows_sel, const int* kept, int* table,
-                            int* sh, int rcode, int rrow) {
-    const int tid = threadIdx.x;
-    for (int i = tid; i < kSetSize; i += kSelThreads) table[i] = -1;
-    __syncthreads();
-    for (int r = tid; r < m_tok; r += kSelThreads) set_insert(table, kept[r]);
-    __syncthreads();
-    const int nvalid = min(a.ring_n[h], a.ring_cap);
+// ring entries (ring index order, the first rn valid) whose cell is in the
+// reference's `selected` -- the m_tok cells that pass nprobe and the token
+// budget (retrieval.py:295-303), set in the `keep` bitmap of global cell
+// ids, plus the padding id when m_tok < nprobe -- up to the
+// execution-buffer rows left after the selected rows.  rcode / rrow: this
+// thread's ring entry (thread = ring index).  One barrier, which also
+// publishes *rows_sel (written before the call by the thread that knows it).
+__device__ void delta_match(const SelParams& a, int h, int m_tok, const int* rows_sel, bool have_rows,
+                            const uint32_t* keep, int* wcnt, int rcode, int rrow, int rn) {
+    const int tid = threadIdx.x, wave = tid >> 6;
     bool match = false;
-    if (tid < nvalid) match = rcode >= 0 ? set_find(table, rcode) : (rcode == -1 && m_tok < a.nprobe);
-    const int f = match ? 1 : 0;
-    int tot;
-    const int pos = block_incl_scan(f, sh, tot) - f;
-    const int avail = max(a.exec_rows - rows_sel, 0);
-    const int nd = min(tot, avail);
+    if (tid < rn)
+        match = rcode >= 0 ? (rcode < a.ncells && ((keep[rcode >> 5] >> (rcode & 31)) & 1u) != 0)
+                           : (rcode == -1 && m_tok < a.nprobe);
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(match);
+    if (lane_id() == 0) wcnt[wave] = __builtin_popcountll(bal);
+    __syncthreads();
+    int before = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kSelThreads / 64; ++w) {
+        const int x = wcnt[w];
+        tot += x;
+        before += w < wave ? x : 0;
+    }
+    const int pos = before + __builtin_popcountll(bal & lanemask_lt());
+    const int rsel = have_rows ? *rows_sel : 0;
+    const int nd = min(tot, max(a.exec_rows - rsel, 0));
     if (match && pos < nd) a.delta_rows[static_cast<int64_t>(h) * a.ring_cap + pos] = rrow;
     if (tid == 0) a.n_delta[h] = nd;
 }
@@ -169,6 +177,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     __shared__ int sh[82];
     __shared__ int shv[8];
     __shared__ int shk[16];
+    __shared__ int shk2[16];
+    __shared__ uint32_t s_keep[ONLINE ? kKeepWords : 1];   // kept cells of the delta match
     __shared__ float shf[40];
 
     const int h = blockIdx.x;
@@ -223,8 +233,10 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
             urow[u] = slot < a.shadow_rows ? a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + slot] : 0;
         }
     }
+    const bool ring = ONLINE && a.ring_cap > 0;
     int rcode = -3, rrow = 0;
-    if (ONLINE && a.ring_cap > 0 && tid < a.ring_cap) {
+    const int rn = ring ? min(a.ring_n[h], a.ring_cap) : 0;
+    if (ring && tid < a.ring_cap) {
         rcode = a.ring_cell[static_cast<int64_t>(h) * a.ring_cap + tid];
         rrow = a.ring_row[static_cast<int64_t>(h) * a.ring_cap + tid];
     }
@@ -271,6 +283,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         qs[tid] = acc;
     }
     for (int i = tid; i < kBins; i += kSelThreads) hist[i] = 0;
+    if (ring)
+        for (int i = tid; i < kKeepWords; i += kSelThreads) s_keep[i] = 0;
     if (tid == 0) shv[0] = 0;
     __syncthreads();
     // chain over the first subspace, once per l0
@@ -312,9 +326,10 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     // cells whose centroid was replaced: the full 128-term chain over the
     // shadow row (compute_impl.cu:80-101 on the updated centroid), kOvr
     // slots per pass, staged in LDS after the C0 rows
-    if (ONLINE && n_upd > 0) {
-        float* ovr = c0s + k0 * (DP + 1);   // [kOvr][129]
-        float* ovs = ovr + kOvr * 129;      // [kOvr]
+    float* ovr = c0s + k0 * (DP + 1);   // [kOvr][129] replaced centroids staged in LDS
+    float* ovs = ovr + kOvr * 129;      // [kOvr] their scores
+    if (ONLINE && n_upd > kOvr) {
+        // more than kOvr replaced cells: passes of kOvr slots before the range
         for (int base = 0; base < n_upd; base += kOvr) {
             if (base > 0) {
 #pragma unroll
@@ -348,6 +363,21 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
             __syncthreads();
         }
     }
+    // up to kOvr replaced cells: their rows (loaded during the scoring) go to
+    // LDS now; wave 0 scores them between the two barriers of the range
+    // reduction, whose range then covers both old and new scores
+    const bool ovr_one = ONLINE && n_upd > 0 && n_upd <= kOvr;
+    if (ovr_one) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int i4 = tid + u * kSelThreads;
+            float* dst = ovr + (i4 >> 5) * 129 + (i4 & 31) * 4;
+            dst[0] = ovv[u].x;
+            dst[1] = ovv[u].y;
+            dst[2] = ovv[u].z;
+            dst[3] = ovv[u].w;
+        }
+    }
     int nvalid = 0;
     float smax = -INFINITY, smin = INFINITY;
 #pragma unroll
@@ -369,9 +399,20 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         }
     }
     __syncthreads();
+    float ov_mx = -INFINITY, ov_mn = INFINITY;
+    if (ovr_one && tid < 64) {
+        if (tid < n_upd) {
+            float acc = 0.0f;   // compute_impl.cu:80-101 over the replaced centroid
+            for (int d = 0; d < 128; ++d) acc = __builtin_fmaf(qs[d], ovr[tid * 129 + d], acc);
+            ovs[tid] = acc;
+            ov_mx = ov_mn = acc;
+        }
+        ov_mx = wave_max(ov_mx);
+        ov_mn = -wave_max(-ov_mn);
+    }
     if (tid == 0) {
         int nv = 0;
-        float mx = -INFINITY, mn = INFINITY;
+        float mx = ov_mx, mn = ov_mn;
         for (int w = 0; w < 16; ++w) {
             nv += sh[w];
             mx = fmaxf(mx, shf[w]);
@@ -382,6 +423,11 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         shf[33] = mn;
     }
     __syncthreads();
+    if (ovr_one) {
+#pragma unroll
+        for (int e = 0; e < EPT; ++e)
+            if (us[e] >= 0 && us[e] < kOvr) sc[e] = ovs[us[e]];
+    }
     const int n_valid = shv[1];
     const float gmax = shf[32], gmin = shf[33];
     // this head's budgets (ragged batches), bounded by the launch-wide ones
@@ -398,7 +444,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
             a.n_rows[h] = 0;
             prefix_out[0] = 0;
         }
-        if (ONLINE && a.ring_cap > 0) delta_match(a, h, 0, 0, sg, reinterpret_cast<int*>(dyn), sh, rcode, rrow);
+        if (ring) delta_match(a, h, 0, nullptr, false, s_keep, shk, rcode, rrow, rn);
         return;
     }
 
@@ -558,12 +604,15 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         const bool keep = keep_tok && pexcl <= (a.tile_mode ? 0 : buffer_pages);
         kept += keep ? 1 : 0;
         kept_tok += keep_tok ? 1 : 0;
+        if (ring && keep_tok) {   // the kept cell set of the delta match
+            const int g = sg[r];
+            atomicOr(&s_keep[g >> 5], 1u << (g & 31));
+        }
         texcl += s2[u];
     }
     // the rules are monotone in rank (prefixes only grow), so the kept ranks
     // are exactly the first m (the first m_tok before the page cut): count
     // them per wave, then over the 16 waves
-    const bool ring = ONLINE && a.ring_cap > 0;
     {
         const int wk = wave_sum_i(kept);
         const int wt = ring ? wave_sum_i(kept_tok) : 0;
@@ -605,11 +654,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         a.n_rows[h] = 0;
         prefix_out[0] = 0;
     }
-    if (ring) {
-        __syncthreads();
-        const int rows_sel = m > 0 ? shv[5] : 0;
-        delta_match(a, h, m_tok, rows_sel, sg, reinterpret_cast<int*>(dyn), sh, rcode, rrow);
-    }
+    if (ring) delta_match(a, h, m_tok, &shv[5], m > 0, s_keep, shk2, rcode, rrow, rn);
 }
 
 // fused_query_group_similarities over compact merged centroids

@@ -215,6 +215,44 @@ def test_select_with_replaced_centroids_and_delta(ops, oracle, ks):
     assert hit_replaced > 0, "no replaced centroid was selected: the test covers nothing"
 
 
+def test_select_many_replaced_centroids(ops, oracle):
+    """More than 64 replaced centroids in a head (the selection then scores
+    them in several passes of 64): threshold 1 and batches of 64 keys drawn
+    over the whole prompt."""
+    note("[online] selection with > 64 replaced cells")
+    H, T, B, G, ks = 8, 8000, 64, 4, (32, 32)
+    keys, _, cent, out, ncells = _built(ops, H, T, ks, 91)
+    upd, orc = _state(ops, oracle, out, ks, ncells, threshold=1, ring_cap=256)
+    g = torch.Generator().manual_seed(17)
+    idx = torch.randint(0, T, (H, 4 * B), generator=g)
+    steady = torch.stack([keys[h, idx[h]] for h in range(H)]).contiguous()
+    sd = steady.to(DEV)
+    for b in range(4):
+        upd.assign(sd, b * B, B)
+        orc.assign(bits(steady[:, b * B:(b + 1) * B]), list(range(b * B, (b + 1) * B)))
+        upd.refresh(B)
+        orc.refresh()
+    torch.cuda.synchronize()
+    assert int(upd.upd_n.min()) > 64 and int(upd.upd_n.max()) > 128
+    sz = oracle.sizing(T, 0.1, k_override=ks)
+    bud = ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"])
+    from adaptiveimi_amd import synthetic
+
+    for q in ((steady[:, :G].float() * 2).to(torch.bfloat16), synthetic.make_queries(keys, G, seed=8)[0]):
+        sel = ops.select(q.to(DEV), cent, out["cell_count"], out["cell_offset"], ks, bud, update=upd,
+                         exec_rows=10 ** 6)
+        cells, rm, rtok, dr = _select_oracle(oracle, orc, q, out, sz, bud, 10 ** 6, ncells)
+        m = sel["n_selected"].cpu().numpy()
+        assert np.array_equal(m, rm)
+        got = sel["sel_cell"].cpu().numpy()
+        nd = sel["n_delta"].cpu().numpy()
+        drow = sel["delta_rows"].cpu().numpy()
+        for h in range(H):
+            assert np.array_equal(got[h, : m[h]], cells[h]), h
+            assert list(drow[h, : nd[h]]) == dr[h], h
+        assert np.array_equal(sel["n_rows"].cpu().numpy(), rtok)
+
+
 def test_decode_step_online_matches_oracle(ops, oracle):
     note("[online] decode step")
     H, T, B, G, ks = 8, 9000, 8, 4, (32, 32)
