@@ -3,9 +3,9 @@
 // up at runtime.py:106-166).
 //
 // imi_update_assign, for a batch of decode keys (steady rows row0 ..):
-//   upd_sim_kernel     grid (row chunks of 256, H): one compact row per
-//                      thread, the dot product of every batch key with it as
-//                      a sequential fp32 FMA chain over d (keys broadcast
+//   upd_sim_kernel     grid (row chunks of 256, H, keys / 4): one compact row
+//                      per thread, the dot product of four batch keys with it
+//                      as sequential fp32 FMA chains over d (keys broadcast
 //                      from LDS, the row streamed 32 dims at a time), then a
 //                      workgroup arg-max per key packed as (order key of the
 //                      value, ~row) so that the largest value and, among
@@ -25,7 +25,7 @@ namespace imi {
 namespace {
 
 constexpr int kSimThreads = 256;   // compact rows per workgroup of upd_sim_kernel
-constexpr int kKeyBlock = 16;      // batch keys per pass of upd_sim_kernel
+constexpr int kKeyBlock = 4;       // batch keys per workgroup of upd_sim_kernel
 constexpr int kMaxBatch = 64;      // keys one assign call takes
 constexpr int kRingMax = 1024;     // delta ring capacity bound
 constexpr int kD = 128;
@@ -66,67 +66,69 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
     return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
 }
 
-// Dot products of up to 16 batch keys with one compact row per thread, and
-// the arg-max of each key over the workgroup's 256 rows.
+// Dot products of four batch keys (4 blockIdx.z .. +3) with one compact row
+// per thread, and the arg-max of each key over the workgroup's 256 rows.
 __global__ __launch_bounds__(kSimThreads) void upd_sim_kernel(UpdParams a) {
     __shared__ __attribute__((aligned(16))) float xs[kKeyBlock][kD];
     __shared__ uint64_t red[kSimThreads / 64][kKeyBlock];
     const int h = blockIdx.y, chunk = blockIdx.x, tid = threadIdx.x;
+    const int kb = blockIdx.z * kKeyBlock;
+    const int nk = min(kKeyBlock, a.count - kb);
     const int r = chunk * kSimThreads + tid;
     const bool live = r < a.n_rows;
     const float4* row = reinterpret_cast<const float4*>(a.shadow + (static_cast<int64_t>(h) * a.n_rows + (live ? r : 0)) * kD);
-    for (int kb = 0; kb < a.count; kb += kKeyBlock) {
-        const int nk = min(kKeyBlock, a.count - kb);
-        // the keys of this block (bf16 -> fp32 is exact), zero past the batch
-        for (int i = tid; i < kKeyBlock * kD; i += kSimThreads) {
-            const int j = i / kD, d = i % kD;
-            xs[j][d] = j < nk ? bf16_to_f32(key_row(a, h, kb + j)[d]) : 0.0f;
-        }
-        __syncthreads();
-        float acc[kKeyBlock];
+    // the block's keys (bf16 -> fp32 is exact), zero past the batch
+    for (int i = tid; i < kKeyBlock * kD; i += kSimThreads) {
+        const int j = i / kD, d = i % kD;
+        xs[j][d] = j < nk ? bf16_to_f32(key_row(a, h, kb + j)[d]) : 0.0f;
+    }
+    float acc[kKeyBlock];
 #pragma unroll
-        for (int j = 0; j < kKeyBlock; ++j) acc[j] = 0.0f;
-        // chain over d in order, the row read 32 dims (8 float4) at a time
+    for (int j = 0; j < kKeyBlock; ++j) acc[j] = 0.0f;
+    float4 rv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) rv[u] = row[u];
+    __syncthreads();
+    // chain over d in order, the row read 32 dims (8 float4) at a time
 #pragma unroll 1
-        for (int dc = 0; dc < kD / 32; ++dc) {
-            float4 rv[8];
+    for (int dc = 0; dc < kD / 32; ++dc) {
+        if (dc > 0) {
 #pragma unroll
             for (int u = 0; u < 8; ++u) rv[u] = row[dc * 8 + u];
+        }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < 8; ++u) {
 #pragma unroll
-                for (int j = 0; j < kKeyBlock; ++j) {
-                    const float4 x = *reinterpret_cast<const float4*>(&xs[j][dc * 32 + u * 4]);
-                    acc[j] = __builtin_fmaf(x.x, rv[u].x, acc[j]);
-                    acc[j] = __builtin_fmaf(x.y, rv[u].y, acc[j]);
-                    acc[j] = __builtin_fmaf(x.z, rv[u].z, acc[j]);
-                    acc[j] = __builtin_fmaf(x.w, rv[u].w, acc[j]);
-                }
+            for (int j = 0; j < kKeyBlock; ++j) {
+                const float4 x = *reinterpret_cast<const float4*>(&xs[j][dc * 32 + u * 4]);
+                acc[j] = __builtin_fmaf(x.x, rv[u].x, acc[j]);
+                acc[j] = __builtin_fmaf(x.y, rv[u].y, acc[j]);
+                acc[j] = __builtin_fmaf(x.z, rv[u].z, acc[j]);
+                acc[j] = __builtin_fmaf(x.w, rv[u].w, acc[j]);
             }
         }
-        // (value, ~row) keys: -0 counts as +0, rows past n_rows never win
-        const int wave = tid >> 6;
+    }
+    // (value, ~row) keys: -0 counts as +0, rows past n_rows never win
+    const int wave = tid >> 6;
 #pragma unroll
-        for (int j = 0; j < kKeyBlock; ++j) {
-            const float v = acc[j] + 0.0f;
-            uint64_t key = live ? (static_cast<uint64_t>(order_key(v)) << 32) |
-                                      static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(r))
-                                : 0ull;
+    for (int j = 0; j < kKeyBlock; ++j) {
+        const float v = acc[j] + 0.0f;
+        uint64_t key = live ? (static_cast<uint64_t>(order_key(v)) << 32) |
+                                  static_cast<uint64_t>(0xFFFFFFFFu - static_cast<uint32_t>(r))
+                            : 0ull;
 #pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) {
-                const uint64_t o = shfl_xor_u64(key, m);
-                key = o > key ? o : key;
-            }
-            if (lane_id() == 0) red[wave][j] = key;
+        for (int m = 32; m >= 1; m >>= 1) {
+            const uint64_t o = shfl_xor_u64(key, m);
+            key = o > key ? o : key;
         }
-        __syncthreads();
-        if (tid < nk) {
-            uint64_t best = red[0][tid];
+        if (lane_id() == 0) red[wave][j] = key;
+    }
+    __syncthreads();
+    if (tid < nk) {
+        uint64_t best = red[0][tid];
 #pragma unroll
-            for (int w = 1; w < kSimThreads / 64; ++w) best = red[w][tid] > best ? red[w][tid] : best;
-            a.part[(static_cast<int64_t>(h) * a.count + kb + tid) * a.nchunk + chunk] = best;
-        }
-        __syncthreads();
+        for (int w = 1; w < kSimThreads / 64; ++w) best = red[w][tid] > best ? red[w][tid] : best;
+        a.part[(static_cast<int64_t>(h) * a.count + kb + tid) * a.nchunk + chunk] = best;
     }
 }
 
@@ -169,13 +171,27 @@ __global__ __launch_bounds__(kD) void upd_assign_kernel(UpdParams a) {
     __shared__ int mult[kMaxBatch];
     __shared__ int sh[2];
     __shared__ float acc[kMaxBatch][kD + 1];
+    __shared__ unsigned long long best[kMaxBatch];
     const int h = blockIdx.x, tid = threadIdx.x;
-    for (int s = tid; s < a.count; s += kD) {
-        const uint64_t* p = a.part + (static_cast<int64_t>(h) * a.count + s) * a.nchunk;
-        uint64_t best = 0;
-        for (int c = 0; c < a.nchunk; ++c) best = p[c] > best ? p[c] : best;
-        ids[s] = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best & 0xFFFFFFFFull));
+    if (tid < kMaxBatch) best[tid] = 0ull;
+    __syncthreads();
+    // arg-max over the chunks: every (key, chunk) partial loaded by some
+    // thread, 8 loads in flight, combined with LDS atomics
+    {
+        const uint64_t* p = a.part + static_cast<int64_t>(h) * a.count * a.nchunk;
+        const int total = a.count * a.nchunk;
+        for (int i0 = tid; i0 < total; i0 += 8 * kD) {
+            uint64_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = i0 + u * kD < total ? p[i0 + u * kD] : 0ull;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (i0 + u * kD < total) atomicMax(&best[(i0 + u * kD) / a.nchunk], static_cast<unsigned long long>(v[u]));
+        }
     }
+    __syncthreads();
+    for (int s = tid; s < a.count; s += kD)
+        ids[s] = static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(best[s] & 0xFFFFFFFFull));
     __syncthreads();
     const int nd = group_ids(ids, a.count, grp, cells, sh);
     const int64_t hrow = static_cast<int64_t>(h) * a.n_rows;
@@ -226,14 +242,20 @@ __global__ __launch_bounds__(kD) void upd_assign_kernel(UpdParams a) {
 
 // Threshold update of the rows the last batch touched (async_update.py:
 // 135-143): (shadow * count + sum) / max(count + delta, 1), multiply then add
-// then divide, each rounded to fp32 as the reference's tensor ops are.
+// then divide, each rounded to fp32 as the reference's tensor ops are.  The
+// touched rows' counts are read at once, the replaced rows 8 at a time (thread
+// d owns dimension d), and override slots are handed out in first-touch order.
 __global__ __launch_bounds__(kD) void upd_refresh_kernel(UpdParams a) {
     __shared__ int ids[kMaxBatch];
     __shared__ int grp[kMaxBatch];
     __shared__ int cells[kMaxBatch];
     __shared__ int sh[2];
+    __shared__ int s_cnt[kMaxBatch], s_dlt[kMaxBatch], s_key[kMaxBatch], s_old[kMaxBatch];
+    __shared__ int s_rep[kMaxBatch];
+    __shared__ int s_nrep;
     const int h = blockIdx.x, tid = threadIdx.x;
     const int pos_end = a.ring_pos[h];
+    const int un0 = a.upd_n[h];
     for (int s = tid; s < a.count; s += kD) {
         const int pos = ((pos_end - a.count + s) % a.ring_cap + a.ring_cap) % a.ring_cap;
         ids[s] = a.ring_id[static_cast<int64_t>(h) * a.ring_cap + pos];
@@ -242,34 +264,60 @@ __global__ __launch_bounds__(kD) void upd_refresh_kernel(UpdParams a) {
     const int nd = group_ids(ids, a.count, grp, cells, sh);
     const int64_t hrow = static_cast<int64_t>(h) * a.n_rows;
     const int na = a.n_active[h];
-    for (int i = 0; i < nd; ++i) {
-        const int c = cells[i];
-        if (c < 0 || c >= a.n_rows) continue;   // a ring slot never written (uniform)
-        const int delta = a.dc[hrow + c];
-        if (delta < a.threshold) continue;   // uniform over the workgroup
-        const int cnt = a.cc[hrow + c];
-        const int total = cnt + delta;
-        float* srow = a.shadow + (hrow + c) * kD;
-        float* drow = a.ds + (hrow + c) * kD;
-        const float num = __fadd_rn(__fmul_rn(srow[tid], static_cast<float>(cnt)), drow[tid]);
-        srow[tid] = __fdiv_rn(num, static_cast<float>(total > 1 ? total : 1));
-        drow[tid] = 0.0f;
-        __syncthreads();   // every lane has read the counts before they change
-        if (tid == 0) {
-            a.cc[hrow + c] = total;
-            a.dc[hrow + c] = 0;
-            const int key = c < na ? (a.by_gid ? a.gid[hrow + c] : c) : -1;
-            if (key >= 0 && key < a.n_index) {
-                int32_t* us = a.upd_slot + static_cast<int64_t>(h) * a.n_index + key;
-                if (*us < 0 && a.upd_n[h] < a.n_rows) {
-                    const int slot = a.upd_n[h];
-                    a.upd_row[hrow + slot] = c;
-                    *us = slot;
-                    a.upd_n[h] = slot + 1;
-                }
+    if (tid < nd) {
+        const int c = cells[tid];
+        const bool ok = c >= 0 && c < a.n_rows;   // a ring slot never written is skipped
+        s_dlt[tid] = ok ? a.dc[hrow + c] : -1;
+        s_cnt[tid] = ok ? a.cc[hrow + c] : 0;
+        const int key = ok && c < na ? (a.by_gid ? a.gid[hrow + c] : c) : -1;
+        s_key[tid] = key >= 0 && key < a.n_index ? key : -1;
+        s_old[tid] = s_key[tid] >= 0 ? a.upd_slot[static_cast<int64_t>(h) * a.n_index + s_key[tid]] : 0;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int n = 0;
+        for (int i = 0; i < nd; ++i)
+            if (s_dlt[i] >= a.threshold) s_rep[n++] = i;
+        s_nrep = n;
+    }
+    __syncthreads();
+    const int nrep = s_nrep;
+    for (int i0 = 0; i0 < nrep; i0 += 8) {
+        float sv[8], dv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = i0 + u < nrep ? cells[s_rep[i0 + u]] : 0;
+            sv[u] = i0 + u < nrep ? a.shadow[(hrow + c) * kD + tid] : 0.0f;
+            dv[u] = i0 + u < nrep ? a.ds[(hrow + c) * kD + tid] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (i0 + u < nrep) {
+                const int i = s_rep[i0 + u];
+                const int c = cells[i];
+                const int total = s_cnt[i] + s_dlt[i];
+                const float num = __fadd_rn(__fmul_rn(sv[u], static_cast<float>(s_cnt[i])), dv[u]);
+                a.shadow[(hrow + c) * kD + tid] = __fdiv_rn(num, static_cast<float>(total > 1 ? total : 1));
+                a.ds[(hrow + c) * kD + tid] = 0.0f;
             }
         }
-        __syncthreads();
+    }
+    if (tid < nrep) {
+        const int i = s_rep[tid];
+        a.cc[hrow + cells[i]] = s_cnt[i] + s_dlt[i];
+        a.dc[hrow + cells[i]] = 0;
+    }
+    if (tid == 0) {
+        int n = un0;
+        for (int r = 0; r < nrep; ++r) {
+            const int i = s_rep[r];
+            if (s_key[i] >= 0 && s_old[i] < 0 && n < a.n_rows) {
+                a.upd_row[hrow + n] = cells[i];
+                a.upd_slot[static_cast<int64_t>(h) * a.n_index + s_key[i]] = n;
+                ++n;
+            }
+        }
+        a.upd_n[h] = n;
     }
 }
 
@@ -363,7 +411,8 @@ extern "C" int imi_update_assign(const imi_update_args* a, imi_stream_t stream_)
     UpdParams p{};
     fill_params(a, p);
     update_workspace(a, &p);
-    hipLaunchKernelGGL(upd_sim_kernel, dim3(p.nchunk, a->kv_heads), dim3(kSimThreads), 0, stream, p);
+    hipLaunchKernelGGL(upd_sim_kernel, dim3(p.nchunk, a->kv_heads, (a->count + kKeyBlock - 1) / kKeyBlock),
+                       dim3(kSimThreads), 0, stream, p);
     IMI_LAUNCH_CHECK("upd_sim_kernel");
     hipLaunchKernelGGL(upd_assign_kernel, dim3(a->kv_heads), dim3(kD), 0, stream, p);
     IMI_LAUNCH_CHECK("upd_assign_kernel");
