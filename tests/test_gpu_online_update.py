@@ -296,16 +296,18 @@ def test_decode_step_online_matches_oracle(ops, oracle):
     assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)), float(err.max())
 
 
-@pytest.mark.parametrize("ks", [(32, 32), (6, 6, 6, 6)])
-def test_cache_with_async_update_matches_oracle(ops, oracle, ks):
-    """The drop-in with async_update on (batch 4, threshold 2, 24-token ring),
-    driven like model_hub drives it, against a step-by-step oracle replay
-    (update applied at the next step)."""
+@pytest.mark.parametrize("ks,steps,batch,thr,ring", [((32, 32), 14, 4, 2, 24), ((6, 6, 6, 6), 14, 4, 2, 24),
+                                                      ((32, 32), 50, 16, 3, 40)])
+def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, thr, ring):
+    """The drop-in with async_update on, driven like model_hub drives it,
+    against a step-by-step oracle replay (update applied at the next step);
+    the last case uses the reference's batch of 16 keys over three batches
+    with a ring that wraps."""
     from adaptiveimi_amd import synthetic
     from adaptiveimi_amd.attn_hub.sparse_imi import imi_decode_attn
     from adaptiveimi_amd.cache_hub.adaptive_imi import adpimi_cache
 
-    L, S, H, G, D, steps, batch = 2, 4096, 8, 4, 128, 14, 4
+    L, S, H, G, D = 2, 4096, 8, 4, 128
     note(f"[online] drop-in ks={ks} {steps} decode steps")
     kcfg = {f"k{i + 1}": k for i, k in enumerate(ks)}
     kcfg.update(max_iters=3, early_stop_min_iter=3, init="first")
@@ -316,7 +318,7 @@ def test_cache_with_async_update_matches_oracle(ops, oracle, ks):
                          retrieval_budget=0.1, cache_ratio=0.05, buffer_cluster_num=32, prefill_bsz=1, num_gpus=1,
                          model_size=8, subspace_parts=len(ks),
                          runtime_config={"kmeans": kcfg, "async_update": {"enabled": True, "batch": batch,
-                                                                          "threshold": 2, "delta_tokens": 24}})
+                                                                          "threshold": thr, "delta_tokens": ring}})
     kv = []
     for layer in range(L):
         k, v = synthetic.make_kv(H, S, seed=50 + layer)
@@ -336,7 +338,7 @@ def test_cache_with_async_update_matches_oracle(ops, oracle, ks):
         na = meta["n_active"].cpu().numpy()
         mask = (sizes == 0) | (np.arange(sizes.shape[1])[None, :] >= na[:, None])
         orc = oracle.OnlineUpdateOracle(meta["compact_centroids"].cpu().numpy(), sizes, cache.padding_cluster_id,
-                                        2, 24)
+                                        thr, ring)
         twins.append(dict(sizes=sizes, offs=offs, mask=mask, orc=orc, count=0, pending=None,
                           lk=bits(cache.list_keys[layer][0]), lv=bits(cache.list_values[layer][0])))
     assert cache.padding_cluster_id == ncells
