@@ -41,6 +41,9 @@ constexpr int kScoreThreads = 256;
 constexpr int kFinalThreads = 1024;
 constexpr int kSelCap4 = 2048;   // min(nprobe, buffer_pages) bound
 constexpr int kExtHeads = 1024;  // KV heads one call handles (fixed-place counters)
+constexpr int kCPT = 8;          // occupied cells per thread in the score / histogram / gather kernels
+constexpr int kCS4 = 36;         // LDS row stride of a subspace centroid (16-byte aligned rows)
+constexpr int kCellsPerBlock = kScoreThreads * kCPT;
 
 struct Sel4 {
     const uint16_t* q;
@@ -66,6 +69,8 @@ struct Sel4 {
     uint64_t* keys;          // [H][cap]
     uint32_t* hist;          // [H][kBins4]
     uint32_t* ext;           // [H][4]: max order key, ~min order key, candidate count, unused
+    uint32_t* rpart;         // [H][nbs][2]: per-workgroup max order key and max ~order key
+    int nbs;                 // score workgroups per head
     uint64_t* cand;          // [H][kCand4]
     int32_t* cidx;           // [H][kCand4]
     // online index maintenance: replaced centroids (by compact id) and the
@@ -118,9 +123,26 @@ __device__ __forceinline__ int kprime(const Sel4& a, int h, int na) {
 // ONLINE: replaced centroids / the delta ring (a separate instantiation).
 template <bool ONLINE>
 __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
-    __shared__ float qs[128];
-    __shared__ float cs[4][kK4][kDp4 + 1];   // padded rows: lanes hit different banks
+    __shared__ __attribute__((aligned(16))) float qs[128];
+    __shared__ __attribute__((aligned(16))) float cs[4][kK4][kCS4];
+    __shared__ float p01[kK4 * kK4];   // chain over subspaces 0 and 1, per (l0, l1) pair this block uses
+    __shared__ int s_pair[2];
     const int h = blockIdx.y, tid = threadIdx.x;
+    const int na = n_active(a, h);
+    // the block's cells (ascending global id): their ids, loaded first
+    uint32_t gv[kCPT];
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
+        gv[u] = c < na ? static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c]) : 0u;
+    }
+    const int c_first = blockIdx.x * kCellsPerBlock;
+    const int c_last = min(na, c_first + kCellsPerBlock) - 1;
+    const uint32_t k23 = static_cast<uint32_t>(a.k[2]) * static_cast<uint32_t>(a.k[3]);
+    if (tid == 0 && c_first <= c_last) {
+        s_pair[0] = static_cast<int>(static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c_first]) / k23);
+        s_pair[1] = static_cast<int>(static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c_last]) / k23);
+    }
     if (tid < 128) {
         uint16_t qv[kMaxG4];
 #pragma unroll
@@ -139,11 +161,43 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     for (int i = blockIdx.x * kScoreThreads + tid; i < kBins4; i += gridDim.x * kScoreThreads)
         a.hist[static_cast<int64_t>(h) * kBins4 + i] = 0;
     __syncthreads();
-    const int c = blockIdx.x * kScoreThreads + tid;
-    const int na = n_active(a, h);
+    // The 128-term chain runs over C0[l0], C1[l1], C2[l2], C3[l3] in turn, so
+    // its value after the first 64 terms depends on (l0, l1) only: computed
+    // once per pair in the block's (contiguous) pair range, then continued per
+    // cell over C2 and C3 -- the same multiply-adds in the same order.
+    const int pa = c_first <= c_last ? s_pair[0] : 0;
+    // (ids out of order or out of range would only give wrong scores: both ends are clamped)
+    const int npair = c_first <= c_last ? min(max(s_pair[1] - s_pair[0] + 1, 0), kK4 * kK4) : 0;
+    for (int t = tid; t < npair; t += kScoreThreads) {
+        const int l0 = (pa + t) / a.k[1], l1 = (pa + t) % a.k[1];
+        float s = 0.0f;
+#pragma unroll
+        for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
+            const float4 q4 = *reinterpret_cast<const float4*>(&qs[4 * d4]);
+            const float4 c4 = *reinterpret_cast<const float4*>(&cs[0][l0][4 * d4]);
+            s = __builtin_fmaf(q4.x, c4.x, s);
+            s = __builtin_fmaf(q4.y, c4.y, s);
+            s = __builtin_fmaf(q4.z, c4.z, s);
+            s = __builtin_fmaf(q4.w, c4.w, s);
+        }
+#pragma unroll
+        for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
+            const float4 q4 = *reinterpret_cast<const float4*>(&qs[kDp4 + 4 * d4]);
+            const float4 c4 = *reinterpret_cast<const float4*>(&cs[1][l1][4 * d4]);
+            s = __builtin_fmaf(q4.x, c4.x, s);
+            s = __builtin_fmaf(q4.y, c4.y, s);
+            s = __builtin_fmaf(q4.z, c4.z, s);
+            s = __builtin_fmaf(q4.w, c4.w, s);
+        }
+        p01[t] = s;
+    }
+    __syncthreads();
     uint32_t okmax = 0, nokmin = 0;
-    if (c < na) {
-        uint32_t g = static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c]);
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
+        if (c >= na) break;
+        uint32_t g = gv[u];
         int l[4];
 #pragma unroll
         for (int p = 3; p >= 0; --p) {
@@ -153,10 +207,18 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
         float s = 0.0f;
         const int us = ONLINE && a.upd_slot ? a.upd_slot[static_cast<int64_t>(h) * a.cap + c] : -1;
         if (us < 0) {
+            s = p01[min(max(static_cast<int>(gv[u] / k23) - pa, 0), kK4 * kK4 - 1)];
 #pragma unroll
-            for (int p = 0; p < 4; ++p)
+            for (int p = 2; p < 4; ++p)
 #pragma unroll
-                for (int d = 0; d < kDp4; ++d) s = __builtin_fmaf(qs[p * kDp4 + d], cs[p][l[p]][d], s);
+                for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
+                    const float4 q4 = *reinterpret_cast<const float4*>(&qs[p * kDp4 + 4 * d4]);
+                    const float4 c4 = *reinterpret_cast<const float4*>(&cs[p][l[p]][4 * d4]);
+                    s = __builtin_fmaf(q4.x, c4.x, s);
+                    s = __builtin_fmaf(q4.y, c4.y, s);
+                    s = __builtin_fmaf(q4.z, c4.z, s);
+                    s = __builtin_fmaf(q4.w, c4.w, s);
+                }
         } else {
             // replaced centroid (async_update.py:7-19): the chain over its shadow row
             const int row = min(max(a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + min(us, a.shadow_rows - 1)], 0),
@@ -172,21 +234,68 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
             }
         }
         const uint32_t ok = order_key(s);
-        const uint32_t gv = static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c]);
-        a.keys[static_cast<int64_t>(h) * a.cap + c] = (static_cast<uint64_t>(ok) << 32) | (0xFFFFFFFFu - gv);
-        okmax = ok;
-        nokmin = ~ok;
+        a.keys[static_cast<int64_t>(h) * a.cap + c] = (static_cast<uint64_t>(ok) << 32) | (0xFFFFFFFFu - gv[u]);
+        okmax = max(okmax, ok);
+        nokmin = max(nokmin, ~ok);
     }
-    // per-head range: max of the order key and max of its complement
+    // the workgroup's range partial (max order key, max complement): a plain
+    // store, reduced by the histogram kernel (per-wave atomics on one word per
+    // head serialise when a head has 10^5 cells)
     uint32_t m1 = okmax, m2 = nokmin;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         m1 = max(m1, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m1), o)));
         m2 = max(m2, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m2), o)));
     }
-    if (lane_id() == 0 && m1 != 0) {
-        atomicMax(&a.ext[h * 4 + 0], m1);
-        atomicMax(&a.ext[h * 4 + 1], m2);
+    __shared__ uint32_t red[kScoreThreads / 64][2];
+    if (lane_id() == 0) {
+        red[tid >> 6][0] = m1;
+        red[tid >> 6][1] = m2;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t r1 = 0, r2 = 0;
+#pragma unroll
+        for (int w = 0; w < kScoreThreads / 64; ++w) {
+            r1 = max(r1, red[w][0]);
+            r2 = max(r2, red[w][1]);
+        }
+        a.rpart[(static_cast<int64_t>(h) * a.nbs + blockIdx.x) * 2 + 0] = r1;
+        a.rpart[(static_cast<int64_t>(h) * a.nbs + blockIdx.x) * 2 + 1] = r2;
+    }
+}
+
+// Score range of head h from the score kernel's per-workgroup partials
+// (every thread gets it; the workgroup 0 of each head also leaves it in ext
+// for the gather kernel).
+__device__ void head_range(const Sel4& a, int h, uint32_t* red2, float& gmax, float& gmin) {
+    const int tid = threadIdx.x;
+    uint32_t m1 = 0, m2 = 0;
+    for (int i = tid; i < a.nbs; i += kScoreThreads) {
+        m1 = max(m1, a.rpart[(static_cast<int64_t>(h) * a.nbs + i) * 2 + 0]);
+        m2 = max(m2, a.rpart[(static_cast<int64_t>(h) * a.nbs + i) * 2 + 1]);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        m1 = max(m1, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m1), o)));
+        m2 = max(m2, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m2), o)));
+    }
+    if (lane_id() == 0) {
+        red2[(tid >> 6) * 2 + 0] = m1;
+        red2[(tid >> 6) * 2 + 1] = m2;
+    }
+    __syncthreads();
+    uint32_t r1 = 0, r2 = 0;
+#pragma unroll
+    for (int w = 0; w < kScoreThreads / 64; ++w) {
+        r1 = max(r1, red2[w * 2 + 0]);
+        r2 = max(r2, red2[w * 2 + 1]);
+    }
+    gmax = key_score(static_cast<uint64_t>(r1) << 32);
+    gmin = key_score(static_cast<uint64_t>(~r2) << 32);
+    if (blockIdx.x == 0 && tid == 0) {
+        a.ext[h * 4 + 0] = r1;
+        a.ext[h * 4 + 1] = r2;
     }
 }
 
@@ -195,15 +304,18 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_hist_kernel(Sel4 a) {
     const int h = blockIdx.y, tid = threadIdx.x;
     for (int i = tid; i < kBins4; i += kScoreThreads) lh[i] = 0;
     __syncthreads();
-    const int c = blockIdx.x * kScoreThreads + tid;
+    __shared__ uint32_t red2[kScoreThreads / 64 * 2];
     const int na = n_active(a, h);
     if (blockIdx.x == 0 && tid == 0) a.ext[h * 4 + 2] = 0;   // candidate counter of the gather kernel
-    const uint32_t okmax = a.ext[h * 4 + 0], okmin = ~a.ext[h * 4 + 1];
-    const float gmax = key_score(static_cast<uint64_t>(okmax) << 32);
-    const float gmin = key_score(static_cast<uint64_t>(okmin) << 32);
+    float gmax, gmin;
+    head_range(a, h, red2, gmax, gmin);
     const float range = gmax - gmin;
     const float inv = range > 0.0f ? static_cast<float>(kBins4) / range : 0.0f;
-    if (c < na) atomicAdd(&lh[bucket4(key_score(a.keys[static_cast<int64_t>(h) * a.cap + c]), gmax, inv)], 1u);
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
+        if (c < na) atomicAdd(&lh[bucket4(key_score(a.keys[static_cast<int64_t>(h) * a.cap + c]), gmax, inv)], 1u);
+    }
     __syncthreads();
     for (int i = tid; i < kBins4; i += kScoreThreads)
         if (lh[i]) atomicAdd(&a.hist[static_cast<int64_t>(h) * kBins4 + i], lh[i]);
@@ -244,19 +356,22 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_gather_kernel(Sel4 a) {
     const int kp = kprime(a, h, na);
     if (kp <= 0) return;
     const int bK = find_bucket(a, h, kp, sh);
-    const int c = blockIdx.x * kScoreThreads + tid;
-    if (c >= na) return;
     const uint32_t okmax = a.ext[h * 4 + 0], okmin = ~a.ext[h * 4 + 1];
     const float gmax = key_score(static_cast<uint64_t>(okmax) << 32);
     const float gmin = key_score(static_cast<uint64_t>(okmin) << 32);
     const float range = gmax - gmin;
     const float inv = range > 0.0f ? static_cast<float>(kBins4) / range : 0.0f;
-    const uint64_t key = a.keys[static_cast<int64_t>(h) * a.cap + c];
-    if (bucket4(key_score(key), gmax, inv) <= bK) {
-        const uint32_t slot = atomicAdd(&a.ext[h * 4 + 2], 1u);
-        if (slot < static_cast<uint32_t>(kCand4)) {
-            a.cand[static_cast<int64_t>(h) * kCand4 + slot] = key;
-            a.cidx[static_cast<int64_t>(h) * kCand4 + slot] = c;
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
+        if (c >= na) break;
+        const uint64_t key = a.keys[static_cast<int64_t>(h) * a.cap + c];
+        if (bucket4(key_score(key), gmax, inv) <= bK) {
+            const uint32_t slot = atomicAdd(&a.ext[h * 4 + 2], 1u);
+            if (slot < static_cast<uint32_t>(kCand4)) {
+                a.cand[static_cast<int64_t>(h) * kCand4 + slot] = key;
+                a.cidx[static_cast<int64_t>(h) * kCand4 + slot] = c;
+            }
         }
     }
 }
@@ -513,6 +628,8 @@ size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
     // call leaves them zero, so one zero-filled buffer serves calls of any
     // shape; the histogram is cleared by the score kernel of each call.
     uint32_t* ext = cv.take<uint32_t>(static_cast<size_t>(kExtHeads) * 4);
+    const int nbs = (a->compact_cap + kCellsPerBlock - 1) / kCellsPerBlock;
+    uint32_t* rpart = cv.take<uint32_t>(H * static_cast<size_t>(nbs) * 2);
     uint32_t* hist = cv.take<uint32_t>(H * kBins4);
     uint64_t* keys = cv.take<uint64_t>(H * a->compact_cap);
     uint64_t* cand = cv.take<uint64_t>(H * kCand4);
@@ -521,6 +638,8 @@ size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
         p->keys = keys;
         p->hist = hist;
         p->ext = ext;
+        p->rpart = rpart;
+        p->nbs = nbs;
         p->cand = cand;
         p->cidx = cidx;
     }
@@ -601,7 +720,7 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     p.exec_rows = a->exec_rows;
     p.delta_rows = a->delta_rows;
     p.n_delta = a->n_delta;
-    const dim3 grid((a->compact_cap + kScoreThreads - 1) / kScoreThreads, a->kv_heads);
+    const dim3 grid(p.nbs, a->kv_heads);
     const bool online = p.upd_slot || p.ring_cap > 0;
     if (online)
         hipLaunchKernelGGL(sel4_score_kernel<true>, grid, dim3(kScoreThreads), 0, stream, p);
