@@ -547,7 +547,9 @@ void launch_g(const AttnParams& p, int blocks, hipStream_t stream) {
         launch_gd<G, false>(p, blocks, stream);
 }
 
-int attn_launch(const imi_attention_args* a, hipStream_t stream) {
+// kernels: bit 0 the split pass, bit 1 the merge (which reads the partials
+// the last split pass left in the workspace).
+int attn_launch(const imi_attention_args* a, hipStream_t stream, int kernels = 3) {
     AttnParams p;
     attn_workspace(a, &p);
     p.q = a->query;
@@ -573,16 +575,20 @@ int attn_launch(const imi_attention_args* a, hipStream_t stream) {
     const int64_t rows = static_cast<int64_t>(a->static_len) + a->max_rows;
     const int splits = rows <= 0 ? 1 : static_cast<int>((rows + p.rows_per_block - 1) / p.rows_per_block);
     const int blocks = a->kv_heads * splits;
-    switch (a->groups) {
-        case 1: launch_g<1>(p, blocks, stream); break;
-        case 2: launch_g<2>(p, blocks, stream); break;
-        case 4: launch_g<4>(p, blocks, stream); break;
-        case 7: launch_g<7>(p, blocks, stream); break;
-        default: launch_g<8>(p, blocks, stream); break;
+    if (kernels & 1) {
+        switch (a->groups) {
+            case 1: launch_g<1>(p, blocks, stream); break;
+            case 2: launch_g<2>(p, blocks, stream); break;
+            case 4: launch_g<4>(p, blocks, stream); break;
+            case 7: launch_g<7>(p, blocks, stream); break;
+            default: launch_g<8>(p, blocks, stream); break;
+        }
+        IMI_LAUNCH_CHECK("attention_kernel");
     }
-    IMI_LAUNCH_CHECK("attention_kernel");
-    hipLaunchKernelGGL(merge_kernel, dim3(2 * a->groups, a->kv_heads), dim3(256), 0, stream, p, a->groups);
-    IMI_LAUNCH_CHECK("merge_kernel");
+    if (kernels & 2) {
+        hipLaunchKernelGGL(merge_kernel, dim3(2 * a->groups, a->kv_heads), dim3(256), 0, stream, p, a->groups);
+        IMI_LAUNCH_CHECK("merge_kernel");
+    }
     return IMI_OK;
 }
 
@@ -689,7 +695,10 @@ extern "C" int imi_decode_step(const imi_decode_args* a, imi_stream_t stream_) {
     IMI_REQUIRE(a->attn.workspace && a->attn.workspace_bytes >= need.total, IMI_ERR_WORKSPACE,
                 "imi_decode_step: workspace %zu bytes < %zu required", a->attn.workspace_bytes, need.total);
     const DecodeLayout L = decode_layout(a, a->attn.workspace);
-    const int phases = (a->phases & 3) == 0 ? 3 : (a->phases & 3);
+    IMI_REQUIRE(a->phases >= 0 && a->phases < 16, IMI_ERR_INVALID, "imi_decode_step: phases %d outside [0, 15]",
+                a->phases);
+    const int phases = a->phases == 0 ? 3 : a->phases;
+    const int kernels = ((phases & 2) ? 3 : 0) | ((phases & 4) ? 1 : 0) | ((phases & 8) ? 2 : 0);
     imi_select_args s = a->sel;
     if (!s.sel_cell) s.sel_cell = L.cell;
     if (!s.sel_offset) s.sel_offset = L.off;
@@ -714,7 +723,7 @@ extern "C" int imi_decode_step(const imi_decode_args* a, imi_stream_t stream_) {
         rc = select_validate(&s, nc, km);
         if (rc) return rc;
     }
-    if (!(phases & 2)) return IMI_OK;
+    if (!kernels) return IMI_OK;
     imi_attention_args t = a->attn;
     t.sel_offset = s.sel_offset;
     t.sel_count = s.sel_count;
@@ -727,5 +736,5 @@ extern "C" int imi_decode_step(const imi_decode_args* a, imi_stream_t stream_) {
     t.delta_cap = s.ring_cap > 0 ? s.ring_cap : 0;
     t.workspace = L.attn_ws;
     t.workspace_bytes = L.attn_bytes;
-    return attn_launch(&t, stream);
+    return attn_launch(&t, stream, kernels);
 }

@@ -614,7 +614,8 @@ class DecodePlan:
         return out
 
     def step(self, stream: Optional[int] = None, phases: int = 3) -> torch.Tensor:
-        """Enqueue one step; phases 1 = selection only, 2 = attention only."""
+        """Enqueue one step.  phases (bits): 1 selection, 2 attention (split
+        pass + merge), 4 split pass only, 8 merge only; 3 = the whole step."""
         self.args.phases = phases
         check(self._fn(self._ref, stream if stream is not None else _stream(self.device)), "imi_decode_step")
         return self.out

@@ -9,6 +9,13 @@ one decode token; the metric is decode steps/s per layer.
 
 Prints ONE JSON line (rank 0).  Index-build time, per-kernel durations,
 roofline and the CPU baseline are fields of the same line.
+
+`--workload config3` / `config4` run the same measurement on the other
+single-GPU configurations of BASELINE.json (their parity cases are in the
+tests): a 16-layer slice of a Qwen2.5-72B attention shape, batch 2 x 262144
+tokens, 4-way IMI 4 x 32 centroids, a fixed budget of 4096 tokens; and 32
+Llama-3-8B layers at 1,048,576 tokens, IMI 2 x 128 centroids, 20 Lloyd
+iterations on a 65536-key sample then one full assignment, budget 0.02.
 """
 from __future__ import annotations
 
@@ -31,20 +38,34 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+# BASELINE.json configurations that fit one GPU: layers, context, KV heads per
+# sequence, query heads per KV head, centroids per subspace, Lloyd iterations,
+# budget ratio (None: fixed_tokens), sequences, k-means sample (0: all keys)
+WORKLOADS = {
+    "config1": dict(layers=32, context=131072, kv_heads=8, groups=4, ks=(64, 64), iters=10, budget=0.1,
+                    fixed_tokens=0, batch=1, sample=0),
+    "config3": dict(layers=16, context=262144, kv_heads=8, groups=8, ks=(32, 32, 32, 32), iters=10, budget=None,
+                    fixed_tokens=4096, batch=2, sample=0),
+    "config4": dict(layers=32, context=1048576, kv_heads=8, groups=4, ks=(128, 128), iters=20, budget=0.02,
+                    fixed_tokens=0, batch=1, sample=65536),
+}
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--layers", type=int, default=32)
-    p.add_argument("--context", type=int, default=131072)
+    p.add_argument("--workload", choices=sorted(WORKLOADS), default="config1")
+    p.add_argument("--layers", type=int, default=None)
+    p.add_argument("--context", type=int, default=None)
     p.add_argument("--static-start", type=int, default=32)
     p.add_argument("--static-end", type=int, default=64)
-    p.add_argument("--kv-heads", type=int, default=8)
-    p.add_argument("--groups", type=int, default=4)
-    p.add_argument("--k", type=int, default=64)
-    p.add_argument("--iters", type=int, default=10)
-    p.add_argument("--budget", type=float, default=0.1)
+    p.add_argument("--kv-heads", type=int, default=None)
+    p.add_argument("--groups", type=int, default=None)
+    p.add_argument("--k", type=int, default=None, help="centroids per subspace")
+    p.add_argument("--iters", type=int, default=None)
+    p.add_argument("--budget", type=float, default=None)
     p.add_argument("--cpu-baseline", type=int, default=1)
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-graph", action="store_true")
@@ -54,7 +75,19 @@ def parse():
     p.add_argument("--copy-probe-mb", type=int, default=0,
                    help="run a device-to-device copy of this many MiB (3 times) before the timed region, as the "
                         "known-size reference for FETCH_SIZE / WRITE_SIZE counter runs")
-    return p.parse_args()
+    args = p.parse_args()
+    w = dict(WORKLOADS[args.workload])
+    for name in ("layers", "context", "kv_heads", "groups", "iters", "budget"):
+        if getattr(args, name) is not None:
+            w[name] = getattr(args, name)
+    if args.k is not None:
+        w["ks"] = (args.k,) * len(w["ks"])
+    for name, v in w.items():
+        setattr(args, name, v)
+    if args.workload != "config1":
+        args.cpu_baseline = 0      # the CPU baseline is quoted on the default workload
+        args.online_layers = 0
+    return args
 
 
 def main():
@@ -71,15 +104,21 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    H, G, D, L = args.kv_heads, args.groups, 128, args.layers
+    H, G, D, L = args.kv_heads * args.batch, args.groups, 128, args.layers   # H: KV heads of every sequence
     static_total = args.static_start + args.static_end
     T = args.context - static_total
-    ks = (args.k, args.k)
-    sz = decode_sizing(T, args.budget, k_override=ks)
+    ks = tuple(args.ks)
+    parts = len(ks)
+    ncells = math.prod(ks)
+    ratio = args.budget if args.budget is not None else args.fixed_tokens / T
+    sz = decode_sizing(T, ratio, subspace_parts=parts, k_override=ks)
+    if args.fixed_tokens:
+        sz["max_tokens"] = args.fixed_tokens
+        sz["buffer_pages"] = max(32, -(-args.fixed_tokens // sz["page_size"]))
     bud = ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"])
     static_cap = static_total + 256
     static_len = static_total + 1   # one generated token in the steady zone
-    log(f"[bench] layers={L} context={args.context} T={T} ks={ks} nprobe={bud.nprobe} "
+    log(f"[bench] {args.workload}: layers={L} context={args.context} T={T} heads={H} ks={ks} nprobe={bud.nprobe} "
         f"max_tokens={bud.max_tokens} buffer_pages={bud.buffer_pages}")
 
     # ---------------------------------------------------------- index build
@@ -101,14 +140,22 @@ def main():
         steady_v[:, static_total] = values[:, -1]
         torch.cuda.synchronize()
         start_ev.record()
-        cent, labels, _ = ops.kmeans(mid_k, list(ks), args.iters)
-        idx = ops.build_index(mid_k, mid_v, cent, labels, list(ks), compact=False)
+        if args.sample:
+            cent, labels, _ = ops.kmeans_sampled(mid_k, list(ks), args.iters, args.sample)
+        else:
+            cent, labels, _ = ops.kmeans(mid_k, list(ks), args.iters)
+        if parts == 4:   # selection over the occupied cells (compact ids)
+            idx = ops.build_index(mid_k, mid_v, cent, labels, list(ks), compact=True, merged=False,
+                                  n_centroids=min(T, ncells) + 1)
+        else:
+            idx = ops.build_index(mid_k, mid_v, cent, labels, list(ks), compact=False)
         end_ev.record()
         torch.cuda.synchronize()
         build_ms.append(start_ev.elapsed_time(end_ev))
         q = synthetic.make_queries(mid_k, G, seed=layer)[0]
         plan = ops.DecodePlan(cent, idx["cell_count"], idx["cell_offset"], ks, bud, idx["list_keys"],
-                              idx["list_values"], steady_k, steady_v, G, query=q.contiguous())
+                              idx["list_values"], steady_k, steady_v, G, query=q.contiguous(),
+                              compact=idx if parts == 4 else None)
         plan.set_static_len(static_len)
         plans.append(plan)
         if layer == 0 and args.cpu_baseline:
@@ -190,10 +237,14 @@ def main():
 
     reps = max(args.steps, 5)
     sel_us = per_launch_us(1, reps)
-    att_us = per_launch_us(2, reps)
-    achieved = bytes_per_layer / (att_us * 1e-6) / 1e9
+    att_us = per_launch_us(2, reps)      # split pass + merge
+    split_us = per_launch_us(4, reps)    # attention_kernel alone (the kernel that moves the bytes)
+    merge_us = per_launch_us(8, reps)    # merge_kernel alone
+    achieved = bytes_per_layer / (split_us * 1e-6) / 1e9
+    achieved_am = bytes_per_layer / (att_us * 1e-6) / 1e9
     step_gbps = bytes_per_layer / (ms_per_step / L * 1e-3) / 1e9
-    log(f"[bench] per launch: select {sel_us:.2f} us, attention+merge {att_us:.2f} us")
+    log(f"[bench] per launch: select {sel_us:.2f} us, attention+merge {att_us:.2f} us "
+        f"(attention_kernel {split_us:.2f} us, merge_kernel {merge_us:.2f} us)")
 
     online = None
     if args.online_layers > 0:
@@ -219,8 +270,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (config-0 key/value distributions, seeded)",
         "config": {
-            "workload": f"configs[1] attention path: {L} Llama-3-8B layers ({H} KV heads, GQA {G}, d128) at "
-                        f"{args.context} tokens, IMI 2x{args.k}, {args.iters} Lloyd iters, budget {args.budget}",
+            "workload": workload_name(args, L, H, G, ks),
             "layers": L, "context": args.context, "kv_heads": H, "q_heads": H * G, "static_window": static_total,
             "nprobe": bud.nprobe, "max_tokens": bud.max_tokens, "buffer_pages": bud.buffer_pages,
             "hip_graph": graph is not None,
@@ -230,15 +280,32 @@ def main():
         "us_per_layer_step": round(ms_per_step / L * 1e3, 3),
         "attended_rows_per_layer": rows / L,
         "hbm_frac_step": round(step_gbps / HBM_PEAK_GBPS, 4),
-        "kernels_us": {"select_kernel": round(sel_us, 2), "attention_kernel+merge_kernel": round(att_us, 2)},
+        "kernels_us": {"select_kernel": round(sel_us, 2), "attention_kernel": round(split_us, 2),
+                       "merge_kernel": round(merge_us, 2), "attention_kernel+merge_kernel": round(att_us, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
-                     "kernel": "attention_kernel + merge_kernel (gather, GQA split-K attention, split merge)",
-                     "bytes_per_launch": int(bytes_per_layer)},
+                     "kernel": "attention_kernel (gather + GQA split-K attention)",
+                     "bytes_per_launch": int(bytes_per_layer),
+                     "with_merge": {"achieved": round(achieved_am, 1), "frac": round(achieved_am / HBM_PEAK_GBPS, 4),
+                                    "kernels": "attention_kernel + merge_kernel"}},
         "cpu_baseline": cpu,
         "online_update": online,
     }
     print(json.dumps(result), flush=True)
+
+
+def workload_name(args, L, H, G, ks):
+    imi = "x".join(str(k) for k in ks)
+    budget = f"budget {args.budget}" if args.budget is not None else f"fixed budget {args.fixed_tokens} tokens"
+    sample = f" on a {args.sample}-key sample + full assignment" if args.sample else ""
+    if args.workload == "config1":
+        head = f"configs[1] attention path: {L} Llama-3-8B layers"
+    elif args.workload == "config3":
+        head = f"configs[3] attention path: {L}-layer Qwen2.5-72B attention slice, batch {args.batch}"
+    else:
+        head = f"configs[4] attention path: {L} Llama-3-8B layers"
+    return (f"{head} ({H} KV heads, GQA {G}, d128) at {args.context} tokens, IMI {imi}, {args.iters} Lloyd "
+            f"iters{sample}, {budget}")
 
 
 def online_update_leg(args, ks, bud, static_total, capture):
@@ -324,9 +391,9 @@ def online_update_leg(args, ks, bud, static_total, capture):
 
 
 def measured_traffic():
-    """HBM bytes per attention launch from the committed counter summary
-    (FETCH_SIZE + WRITE_SIZE of attention_kernel + merge_kernel, scaled by the
-    copy-probe calibration), or None when no summary is present."""
+    """HBM bytes per attention_kernel launch from the committed counter
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-probe calibration),
+    or None when no summary is present."""
     f = ROOT / "profiles" / "attention_kernel_traffic_128k.md"
     if not f.exists():
         return None

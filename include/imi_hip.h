@@ -330,8 +330,10 @@ int imi_update_refresh(const imi_update_args* a, imi_stream_t stream);
  * The selection outputs and the split partials live in attn.workspace,
  * which must be zero-filled before its first use; every call leaves it
  * reusable.  Calls that share a workspace must not overlap.
- * phases: 0 or 3 = both halves; 1 = selection only; 2 = attention only
- * (reads the selection the previous phase-1 call left in the workspace). */
+ * phases (bits): 1 = selection, 2 = attention (split pass + merge),
+ * 4 = split pass only, 8 = merge only; 0 = 3 = the whole step.  A phase
+ * run alone reads what the previous call left in the workspace (the
+ * selection, the split partials), e.g. to time one kernel. */
 typedef struct {
     imi_select_args sel;          /* output pointers may be NULL: workspace used */
     imi_attention_args attn;      /* sel_* fields are filled in by the call */

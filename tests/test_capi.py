@@ -117,6 +117,12 @@ def test_select_and_decode_argument_checks(L):
     assert "max_rows" in L.imi_last_error().decode()
     d.attn.max_rows = 410 * 8
     assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == 0
+    d.attn.workspace = 256                                    # never touched: the call stops at the check
+    d.attn.workspace_bytes = need.value
+    d.phases = 16
+    assert L.imi_decode_step(ctypes.byref(d), None) == 1
+    assert "phases" in L.imi_last_error().decode()
+    d.phases = 0
     d.attn.groups = 5
     d.sel.groups = 5
     assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == 3

@@ -578,25 +578,27 @@ def test_ragged_batch_decode_matches_oracle(ops, oracle, ks):
         assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)), (s_, float(err.max()))
 
 
-def test_attention_standalone_and_lse(ops, oracle):
-    """imi_sparse_attention with a caller-made selection, and the LSE output."""
-    note("[attention] standalone")
-    H, G, L = 4, 4, 3000
+@pytest.mark.parametrize("L,cap,span", [(3000, 40, 50), (150000, 1400, 100)])
+def test_attention_standalone_and_lse(ops, oracle, L, cap, span):
+    """imi_sparse_attention with a caller-made selection, and the LSE output.
+    The large case gives heads of 35k-70k rows, i.e. 70-140 splits: the
+    merge's first batch of partials, then chunks of 64 split weights."""
+    note(f"[attention] standalone L={L} cap={cap}")
+    H, G = 4, 4
     from adaptiveimi_amd import synthetic
 
     kl, vl = synthetic.make_kv(H, L, seed=31)
     q = synthetic.make_queries(kl, G, seed=4)[0]
     rng = np.random.default_rng(0)
-    cap = 40
     offs = np.zeros((H, cap), np.int32)
     cnts = np.zeros((H, cap), np.int32)
     pref = np.zeros((H, cap + 1), np.int32)
     nsel = np.zeros(H, np.int32)
     rows = []
     for h in range(H):
-        m = int(rng.integers(0, cap))
-        starts = np.sort(rng.choice(L // 50, m, replace=False)) * 50
-        c = rng.integers(1, 50, m)
+        m = int(rng.integers(0, cap)) if cap < 100 else int(rng.integers(cap // 2, cap))
+        starts = np.sort(rng.choice(L // span, m, replace=False)) * span
+        c = rng.integers(1, span, m)
         offs[h, :m], cnts[h, :m] = starts, c
         pref[h, 1 : m + 1] = np.cumsum(c)
         nsel[h] = m
@@ -605,7 +607,7 @@ def test_attention_standalone_and_lse(ops, oracle):
                sel_offset=torch.from_numpy(offs).to(DEV), sel_count=torch.from_numpy(cnts).to(DEV),
                sel_prefix=torch.from_numpy(pref).to(DEV), n_selected=torch.from_numpy(nsel).to(DEV),
                n_rows=torch.from_numpy(pref[np.arange(H), nsel]).to(DEV))
-    out, lse = ops.sparse_attention(q.to(DEV), None, None, 0, kl.to(DEV), vl.to(DEV), sel, max_rows=cap * 50,
+    out, lse = ops.sparse_attention(q.to(DEV), None, None, 0, kl.to(DEV), vl.to(DEV), sel, max_rows=cap * span,
                                     return_lse=True)
     ref = oracle.attention(bits(q), bits(kl), bits(vl), rows)
     _check_attention(out, ref)
@@ -656,6 +658,15 @@ def test_decode_repeatable_and_graph_capture(ops, oracle):
             g.replay()
             torch.cuda.synchronize()
             assert torch.equal(plan.out, eager[i]), (rep, i)
+    # the step in parts: selection, split pass, merge (each reads what the
+    # previous call left in the workspace) gives the same bytes
+    for i in range(3):
+        plan.query.copy_(qs[i])
+        plan.out.zero_()
+        for ph in (1, 4, 8):
+            plan.step(phases=ph)
+        torch.cuda.synchronize()
+        assert torch.equal(plan.out, eager[i]), ("phases 1, 4, 8", i)
 
 
 def test_full_size_properties_128k(ops):
@@ -683,18 +694,31 @@ def test_full_size_properties_128k(ops):
         assert torch.equal(out["list_keys"][h], kd[h][perm[h].long()])
 
 
-@pytest.mark.parametrize("case", ["outlier", "zero_query"])
+@pytest.mark.parametrize("case", ["outlier", "zero_query", "zero_query_4096", "near_ties", "huge_centroid"])
 def test_select_refinement_paths(ops, oracle, case):
     """Skewed scores (one subspace centroid blown up -> a few huge scores)
     force the bucket refinement; a zero query makes every score equal, so
-    ranking falls back to cell ids alone."""
+    ranking falls back to cell ids alone (with 4096 cells: more candidates
+    than the bound test hands to the exact chain, so every cell's chain is
+    run).  Near ties: the second-subspace centroids differ by ~1e-6
+    relative, so the cells of one first-subspace centroid score within a
+    few ulps of each other and their order is decided by the roundings of
+    the chain, well inside the score bounds.  A centroid of magnitude 1e33
+    puts the bounds' magnitude sums past 2^114 (no pruning) while every
+    chain stays finite."""
     note(f"[select] {case}")
-    H, T, ks = 4, 12000, (32, 32)
+    H, T, ks = 4, 12000, ((64, 64) if case == "zero_query_4096" else (32, 32))
     keys, values = _kv(H, T, seed=17)
     kd, vd = keys.to(DEV), values.to(DEV)
     cent, labels, _ = ops.kmeans(kd, list(ks), 3)
     if case == "outlier":
         cent[:, 1, 0] *= 300.0
+    if case == "near_ties":
+        g = torch.Generator().manual_seed(5)
+        noise = torch.randn(cent[:, 1, : ks[1]].shape, generator=g).to(DEV)
+        cent[:, 1, : ks[1]] = cent[:, 1, :1] * (1.0 + 1e-6 * noise)
+    if case == "huge_centroid":
+        cent[:, 0, 0] *= 1e33
     out = ops.build_index(kd, vd, cent, labels, list(ks), n_centroids=ks[0] * ks[1] + 1)
     from adaptiveimi_amd import synthetic
 
