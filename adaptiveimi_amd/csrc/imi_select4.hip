@@ -124,9 +124,13 @@ __device__ __forceinline__ int kprime(const Sel4& a, int h, int na) {
 template <bool ONLINE>
 __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     __shared__ __attribute__((aligned(16))) float qs[128];
-    __shared__ __attribute__((aligned(16))) float cs[4][kK4][kCS4];
-    __shared__ float p01[kK4 * kK4];   // chain over subspaces 0 and 1, per (l0, l1) pair this block uses
     __shared__ int s_pair[2];
+    // dynamic LDS, sized by the launch: C0..C3 rows [4][kmax][kCS4], then the
+    // chain over subspaces 0 and 1 per (l0, l1) pair this block uses [k0 * k1]
+    extern __shared__ __attribute__((aligned(16))) float s_dyn4[];
+    float* cs = s_dyn4;                      // row r of subspace p at (p * kmax + r) * kCS4
+    float* p01 = s_dyn4 + 4 * a.kmax * kCS4;
+    const int pair_cap = a.k[0] * a.k[1];
     const int h = blockIdx.y, tid = threadIdx.x;
     const int na = n_active(a, h);
     // the block's cells (ascending global id): their ids, loaded first
@@ -155,7 +159,7 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     }
     for (int p = 0; p < 4; ++p) {
         const float* cp = a.cent + (static_cast<int64_t>(h) * 4 + p) * a.kmax * kDp4;
-        for (int i = tid; i < a.k[p] * kDp4; i += kScoreThreads) cs[p][i / kDp4][i % kDp4] = cp[i];
+        for (int i = tid; i < a.k[p] * kDp4; i += kScoreThreads) cs[(p * a.kmax + i / kDp4) * kCS4 + i % kDp4] = cp[i];
     }
     // this head's histogram starts at zero (the histogram kernel is the next launch)
     for (int i = blockIdx.x * kScoreThreads + tid; i < kBins4; i += gridDim.x * kScoreThreads)
@@ -167,14 +171,14 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     // cell over C2 and C3 -- the same multiply-adds in the same order.
     const int pa = c_first <= c_last ? s_pair[0] : 0;
     // (ids out of order or out of range would only give wrong scores: both ends are clamped)
-    const int npair = c_first <= c_last ? min(max(s_pair[1] - s_pair[0] + 1, 0), kK4 * kK4) : 0;
+    const int npair = c_first <= c_last ? min(max(s_pair[1] - s_pair[0] + 1, 0), pair_cap) : 0;
     for (int t = tid; t < npair; t += kScoreThreads) {
         const int l0 = (pa + t) / a.k[1], l1 = (pa + t) % a.k[1];
         float s = 0.0f;
 #pragma unroll
         for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
             const float4 q4 = *reinterpret_cast<const float4*>(&qs[4 * d4]);
-            const float4 c4 = *reinterpret_cast<const float4*>(&cs[0][l0][4 * d4]);
+            const float4 c4 = *reinterpret_cast<const float4*>(&cs[l0 * kCS4 + 4 * d4]);
             s = __builtin_fmaf(q4.x, c4.x, s);
             s = __builtin_fmaf(q4.y, c4.y, s);
             s = __builtin_fmaf(q4.z, c4.z, s);
@@ -183,7 +187,7 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
 #pragma unroll
         for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
             const float4 q4 = *reinterpret_cast<const float4*>(&qs[kDp4 + 4 * d4]);
-            const float4 c4 = *reinterpret_cast<const float4*>(&cs[1][l1][4 * d4]);
+            const float4 c4 = *reinterpret_cast<const float4*>(&cs[(a.kmax + l1) * kCS4 + 4 * d4]);
             s = __builtin_fmaf(q4.x, c4.x, s);
             s = __builtin_fmaf(q4.y, c4.y, s);
             s = __builtin_fmaf(q4.z, c4.z, s);
@@ -192,45 +196,65 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
         p01[t] = s;
     }
     __syncthreads();
+    // every cell's chain continues from its pair prefix over C2[l2], then
+    // C3[l3]; dims outer and the kCPT cells inner, so one broadcast read of
+    // q feeds kCPT multiply-adds (each cell's chain keeps its order)
+    float sv[kCPT];
+    int r2[kCPT], r3[kCPT];   // LDS offsets of the rows C2[l2], C3[l3]
+    const uint32_t k3 = static_cast<uint32_t>(a.k[3]), k2 = static_cast<uint32_t>(a.k[2]);
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        r3[u] = (3 * a.kmax + static_cast<int>(gv[u] % k3)) * kCS4;
+        r2[u] = (2 * a.kmax + static_cast<int>((gv[u] / k3) % k2)) * kCS4;
+        sv[u] = p01[min(max(static_cast<int>(gv[u] / k23) - pa, 0), pair_cap - 1)];
+    }
+#pragma unroll 1
+    for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
+        const float4 q4 = *reinterpret_cast<const float4*>(&qs[2 * kDp4 + 4 * d4]);
+#pragma unroll
+        for (int u = 0; u < kCPT; ++u) {
+            const float4 c4 = *reinterpret_cast<const float4*>(&cs[r2[u] + 4 * d4]);
+            sv[u] = __builtin_fmaf(q4.x, c4.x, sv[u]);
+            sv[u] = __builtin_fmaf(q4.y, c4.y, sv[u]);
+            sv[u] = __builtin_fmaf(q4.z, c4.z, sv[u]);
+            sv[u] = __builtin_fmaf(q4.w, c4.w, sv[u]);
+        }
+    }
+#pragma unroll 1
+    for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
+        const float4 q4 = *reinterpret_cast<const float4*>(&qs[3 * kDp4 + 4 * d4]);
+#pragma unroll
+        for (int u = 0; u < kCPT; ++u) {
+            const float4 c4 = *reinterpret_cast<const float4*>(&cs[r3[u] + 4 * d4]);
+            sv[u] = __builtin_fmaf(q4.x, c4.x, sv[u]);
+            sv[u] = __builtin_fmaf(q4.y, c4.y, sv[u]);
+            sv[u] = __builtin_fmaf(q4.z, c4.z, sv[u]);
+            sv[u] = __builtin_fmaf(q4.w, c4.w, sv[u]);
+        }
+    }
     uint32_t okmax = 0, nokmin = 0;
 #pragma unroll
     for (int u = 0; u < kCPT; ++u) {
         const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
         if (c >= na) break;
-        uint32_t g = gv[u];
-        int l[4];
-#pragma unroll
-        for (int p = 3; p >= 0; --p) {
-            l[p] = static_cast<int>(g % static_cast<uint32_t>(a.k[p]));
-            g /= static_cast<uint32_t>(a.k[p]);
-        }
-        float s = 0.0f;
-        const int us = ONLINE && a.upd_slot ? a.upd_slot[static_cast<int64_t>(h) * a.cap + c] : -1;
-        if (us < 0) {
-            s = p01[min(max(static_cast<int>(gv[u] / k23) - pa, 0), kK4 * kK4 - 1)];
-#pragma unroll
-            for (int p = 2; p < 4; ++p)
-#pragma unroll
-                for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
-                    const float4 q4 = *reinterpret_cast<const float4*>(&qs[p * kDp4 + 4 * d4]);
-                    const float4 c4 = *reinterpret_cast<const float4*>(&cs[p][l[p]][4 * d4]);
-                    s = __builtin_fmaf(q4.x, c4.x, s);
-                    s = __builtin_fmaf(q4.y, c4.y, s);
-                    s = __builtin_fmaf(q4.z, c4.z, s);
-                    s = __builtin_fmaf(q4.w, c4.w, s);
+        float s = sv[u];
+        if (ONLINE && a.upd_slot) {
+            const int us = a.upd_slot[static_cast<int64_t>(h) * a.cap + c];
+            if (us >= 0) {
+                // replaced centroid (async_update.py:7-19): the chain over its shadow row
+                const int row = min(
+                    max(a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + min(us, a.shadow_rows - 1)], 0),
+                    a.shadow_rows - 1);
+                const float4* sr =
+                    reinterpret_cast<const float4*>(a.shadow + (static_cast<int64_t>(h) * a.shadow_rows + row) * 128);
+                s = 0.0f;
+                for (int d4 = 0; d4 < 32; ++d4) {
+                    const float4 v = sr[d4];
+                    s = __builtin_fmaf(qs[4 * d4 + 0], v.x, s);
+                    s = __builtin_fmaf(qs[4 * d4 + 1], v.y, s);
+                    s = __builtin_fmaf(qs[4 * d4 + 2], v.z, s);
+                    s = __builtin_fmaf(qs[4 * d4 + 3], v.w, s);
                 }
-        } else {
-            // replaced centroid (async_update.py:7-19): the chain over its shadow row
-            const int row = min(max(a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + min(us, a.shadow_rows - 1)], 0),
-                                a.shadow_rows - 1);
-            const float4* sr =
-                reinterpret_cast<const float4*>(a.shadow + (static_cast<int64_t>(h) * a.shadow_rows + row) * 128);
-            for (int d4 = 0; d4 < 32; ++d4) {
-                const float4 v = sr[d4];
-                s = __builtin_fmaf(qs[4 * d4 + 0], v.x, s);
-                s = __builtin_fmaf(qs[4 * d4 + 1], v.y, s);
-                s = __builtin_fmaf(qs[4 * d4 + 2], v.z, s);
-                s = __builtin_fmaf(qs[4 * d4 + 3], v.w, s);
             }
         }
         const uint32_t ok = order_key(s);
@@ -721,11 +745,14 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     p.delta_rows = a->delta_rows;
     p.n_delta = a->n_delta;
     const dim3 grid(p.nbs, a->kv_heads);
+    // C0..C3 rows at the padded stride, then one chain prefix per (l0, l1) pair
+    const size_t score_lds = (static_cast<size_t>(4) * p.kmax * kCS4 + static_cast<size_t>(a->k[0]) * a->k[1]) *
+                             sizeof(float);
     const bool online = p.upd_slot || p.ring_cap > 0;
     if (online)
-        hipLaunchKernelGGL(sel4_score_kernel<true>, grid, dim3(kScoreThreads), 0, stream, p);
+        hipLaunchKernelGGL(sel4_score_kernel<true>, grid, dim3(kScoreThreads), score_lds, stream, p);
     else
-        hipLaunchKernelGGL(sel4_score_kernel<false>, grid, dim3(kScoreThreads), 0, stream, p);
+        hipLaunchKernelGGL(sel4_score_kernel<false>, grid, dim3(kScoreThreads), score_lds, stream, p);
     IMI_LAUNCH_CHECK("sel4_score_kernel");
     hipLaunchKernelGGL(sel4_hist_kernel, grid, dim3(kScoreThreads), 0, stream, p);
     IMI_LAUNCH_CHECK("sel4_hist_kernel");
