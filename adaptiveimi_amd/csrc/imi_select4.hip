@@ -34,6 +34,8 @@ namespace {
 
 constexpr int kBins4 = 2048;
 constexpr int kCand4 = 4096;     // candidate capacity per head
+constexpr int kShards = 16;      // candidate counters per head (cell c counts in shard c % kShards)
+constexpr int kShardCap = kCand4 / kShards;
 constexpr int kK4 = 64;          // centroids per subspace the kernels hold
 constexpr int kDp4 = 32;         // subspace width (D = 128, 4 parts)
 constexpr int kMaxG4 = 8;        // query heads per KV head
@@ -44,6 +46,10 @@ constexpr int kExtHeads = 1024;  // KV heads one call handles (fixed-place count
 constexpr int kCPT = 8;          // occupied cells per thread in the score / histogram / gather kernels
 constexpr int kCS4 = 36;         // LDS row stride of a subspace centroid (16-byte aligned rows)
 constexpr int kCellsPerBlock = kScoreThreads * kCPT;
+// the histogram kernel takes 8x more cells per workgroup: its global merge
+// (one atomic per non-empty bin and workgroup) is a per-workgroup cost
+constexpr int kHistCPT = 64;
+constexpr int kHistCellsPerBlock = kScoreThreads * kHistCPT;
 
 struct Sel4 {
     const uint16_t* q;
@@ -68,8 +74,9 @@ struct Sel4 {
     int sel_cap;
     uint64_t* keys;          // [H][cap]
     uint32_t* hist;          // [H][kBins4]
-    uint32_t* ext;           // [H][4]: max order key, ~min order key, candidate count, unused
+    uint32_t* ext;           // [H][4]: max order key, ~min order key, unused, unused
     uint32_t* rpart;         // [H][nbs][2]: per-workgroup max order key and max ~order key
+    uint32_t* ccnt;          // [H][kShards]: candidates per shard (shard s: cand slots s * kShardCap ..)
     int nbs;                 // score workgroups per head
     uint64_t* cand;          // [H][kCand4]
     int32_t* cidx;           // [H][kCand4]
@@ -330,15 +337,23 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_hist_kernel(Sel4 a) {
     __syncthreads();
     __shared__ uint32_t red2[kScoreThreads / 64 * 2];
     const int na = n_active(a, h);
-    if (blockIdx.x == 0 && tid == 0) a.ext[h * 4 + 2] = 0;   // candidate counter of the gather kernel
+    if (blockIdx.x == 0 && tid < kShards) a.ccnt[h * kShards + tid] = 0;   // the gather kernel's counters
+    // every key of this thread in flight before the range reduction
+    const uint64_t* keys = a.keys + static_cast<int64_t>(h) * a.cap;
+    uint64_t kv[kHistCPT];
+#pragma unroll
+    for (int u = 0; u < kHistCPT; ++u) {
+        const int c = blockIdx.x * kHistCellsPerBlock + u * kScoreThreads + tid;
+        kv[u] = c < na ? keys[c] : 0ull;
+    }
     float gmax, gmin;
     head_range(a, h, red2, gmax, gmin);
     const float range = gmax - gmin;
     const float inv = range > 0.0f ? static_cast<float>(kBins4) / range : 0.0f;
 #pragma unroll
-    for (int u = 0; u < kCPT; ++u) {
-        const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
-        if (c < na) atomicAdd(&lh[bucket4(key_score(a.keys[static_cast<int64_t>(h) * a.cap + c]), gmax, inv)], 1u);
+    for (int u = 0; u < kHistCPT; ++u) {
+        const int c = blockIdx.x * kHistCellsPerBlock + u * kScoreThreads + tid;
+        if (c < na) atomicAdd(&lh[bucket4(key_score(kv[u]), gmax, inv)], 1u);
     }
     __syncthreads();
     for (int i = tid; i < kBins4; i += kScoreThreads)
@@ -379,6 +394,14 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_gather_kernel(Sel4 a) {
     const int na = n_active(a, h);
     const int kp = kprime(a, h, na);
     if (kp <= 0) return;
+    // every key of this thread in flight before the bucket search
+    const uint64_t* keys = a.keys + static_cast<int64_t>(h) * a.cap;
+    uint64_t kv[kCPT];
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
+        kv[u] = c < na ? keys[c] : 0ull;
+    }
     const int bK = find_bucket(a, h, kp, sh);
     const uint32_t okmax = a.ext[h * 4 + 0], okmin = ~a.ext[h * 4 + 1];
     const float gmax = key_score(static_cast<uint64_t>(okmax) << 32);
@@ -388,13 +411,16 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_gather_kernel(Sel4 a) {
 #pragma unroll
     for (int u = 0; u < kCPT; ++u) {
         const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
-        if (c >= na) break;
-        const uint64_t key = a.keys[static_cast<int64_t>(h) * a.cap + c];
-        if (bucket4(key_score(key), gmax, inv) <= bK) {
-            const uint32_t slot = atomicAdd(&a.ext[h * 4 + 2], 1u);
-            if (slot < static_cast<uint32_t>(kCand4)) {
-                a.cand[static_cast<int64_t>(h) * kCand4 + slot] = key;
-                a.cidx[static_cast<int64_t>(h) * kCand4 + slot] = c;
+        if (c < na && bucket4(key_score(kv[u]), gmax, inv) <= bK) {
+            // one of kShards counters per head, by cell index (the best cells
+            // cluster in id order): atomics on one word from every workgroup
+            // of a head serialise
+            const int shard = c & (kShards - 1);
+            const uint32_t slot = atomicAdd(&a.ccnt[h * kShards + shard], 1u);
+            if (slot < static_cast<uint32_t>(kShardCap)) {
+                const int64_t at = static_cast<int64_t>(h) * kCand4 + shard * kShardCap + slot;
+                a.cand[at] = kv[u];
+                a.cidx[at] = c;
             }
         }
     }
@@ -424,6 +450,73 @@ __device__ __forceinline__ void block_scan2(int& x, int& y, int* sh, int& tx, in
     __syncthreads();
 }
 
+// Bitonic sort, descending, of the first N entries of sk / si (N a power of
+// two).  N <= kFinalThreads: one entry per thread, held in registers; the
+// compare-exchange stages whose partner lies in the same wave (distance < 64)
+// run on lane shuffles, only the longer ones go through LDS (two barriers
+// each: 10 of the 55 stages at N = 1024).  Larger N: every stage in LDS.
+__device__ void bitonic_desc(uint64_t* sk, int* si, int N) {
+    const int tid = threadIdx.x;
+    if (N <= kFinalThreads) {
+        uint64_t x = tid < N ? sk[tid] : 0ull;
+        int xi = tid < N ? si[tid] : -1;
+        for (int kk = 2; kk <= N; kk <<= 1) {
+            for (int j = kk >> 1; j > 0; j >>= 1) {
+                uint64_t y;
+                int yi;
+                if (j >= 64) {
+                    __syncthreads();
+                    if (tid < N) {
+                        sk[tid] = x;
+                        si[tid] = xi;
+                    }
+                    __syncthreads();
+                    const int p = tid ^ j;
+                    y = p < N ? sk[p] : 0ull;
+                    yi = p < N ? si[p] : -1;
+                } else {
+                    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(x & 0xFFFFFFFFull), j));
+                    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(x >> 32), j));
+                    y = (static_cast<uint64_t>(hi) << 32) | lo;
+                    yi = __shfl_xor(xi, j);
+                }
+                const bool desc = (tid & kk) == 0;
+                const bool lower = (tid & j) == 0;
+                if (lower == desc ? y > x : y < x) {   // the lower slot keeps the larger key when descending
+                    x = y;
+                    xi = yi;
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < N) {
+            sk[tid] = x;
+            si[tid] = xi;
+        }
+        __syncthreads();
+        return;
+    }
+    for (int kk = 2; kk <= N; kk <<= 1) {
+        for (int j = kk >> 1; j > 0; j >>= 1) {
+            for (int i = tid; i < N; i += kFinalThreads) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const bool desc = (i & kk) == 0;
+                    const uint64_t x = sk[i], y = sk[ixj];
+                    if ((x < y) == desc) {
+                        sk[i] = y;
+                        sk[ixj] = x;
+                        const int t = si[i];
+                        si[i] = si[ixj];
+                        si[ixj] = t;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
 template <bool ONLINE>
 __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     __shared__ uint64_t sk[kCand4];
@@ -432,40 +525,43 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     __shared__ int shk[kFinalThreads / 64];
     __shared__ int s_rows;
     __shared__ uint32_t h256[256];
+    __shared__ int s_spre[kShards + 1];
+    __shared__ int s_over;
     const int h = blockIdx.x, tid = threadIdx.x;
     const int na = n_active(a, h);
     const int kp = kprime(a, h, na);
     int32_t* prefix_out = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
-    const uint32_t count = a.ext[h * 4 + 2];
+    // the gather's shard counts: prefix over the shards, overflow of any
+    if (tid < 64) {
+        const uint32_t cnt = tid < kShards ? a.ccnt[h * kShards + tid] : 0u;
+        const int v = static_cast<int>(min(cnt, static_cast<uint32_t>(kShardCap)));
+        const int incl = wave_incl_scan(v);
+        if (tid < kShards) s_spre[tid + 1] = incl;
+        if (tid == 0) s_spre[0] = 0;
+        const bool over = __builtin_amdgcn_ballot_w64(cnt > static_cast<uint32_t>(kShardCap)) != 0;
+        if (tid == 0) s_over = over ? 1 : 0;
+    }
+    __syncthreads();
     int n = 0;   // sorted candidates in sk / si, best first
-    if (kp > 0 && count <= static_cast<uint32_t>(kCand4)) {
-        n = static_cast<int>(count);
+    if (kp > 0 && !s_over) {
+        n = s_spre[kShards];
         int N = 1;
         while (N < n) N <<= 1;
         for (int i = tid; i < N; i += kFinalThreads) {
-            sk[i] = i < n ? a.cand[static_cast<int64_t>(h) * kCand4 + i] : 0ull;
-            si[i] = i < n ? a.cidx[static_cast<int64_t>(h) * kCand4 + i] : -1;
+            uint64_t key = 0ull;
+            int ci = -1;
+            if (i < n) {
+                int sh_ = 0;
+                while (sh_ + 1 < kShards && s_spre[sh_ + 1] <= i) ++sh_;
+                const int64_t at = static_cast<int64_t>(h) * kCand4 + sh_ * kShardCap + (i - s_spre[sh_]);
+                key = a.cand[at];
+                ci = a.cidx[at];
+            }
+            sk[i] = key;
+            si[i] = ci;
         }
         __syncthreads();
-        for (int kk = 2; kk <= N; kk <<= 1) {
-            for (int j = kk >> 1; j > 0; j >>= 1) {
-                for (int i = tid; i < N; i += kFinalThreads) {
-                    const int ixj = i ^ j;
-                    if (ixj > i) {
-                        const bool desc = (i & kk) == 0;
-                        const uint64_t x = sk[i], y = sk[ixj];
-                        if ((x < y) == desc) {
-                            sk[i] = y;
-                            sk[ixj] = x;
-                            const int t = si[i];
-                            si[i] = si[ixj];
-                            si[ixj] = t;
-                        }
-                    }
-                }
-                __syncthreads();
-            }
-        }
+        bitonic_desc(sk, si, N);
     } else if (kp > 0) {
         // Exact radix select of the kp-th largest key (keys are unique),
         // then every key at or above it.
@@ -518,38 +614,24 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
             si[i] = -1;
         }
         __syncthreads();
-        for (int kk = 2; kk <= N; kk <<= 1) {
-            for (int j = kk >> 1; j > 0; j >>= 1) {
-                for (int i = tid; i < N; i += kFinalThreads) {
-                    const int ixj = i ^ j;
-                    if (ixj > i) {
-                        const bool desc = (i & kk) == 0;
-                        const uint64_t x = sk[i], y = sk[ixj];
-                        if ((x < y) == desc) {
-                            sk[i] = y;
-                            sk[ixj] = x;
-                            const int t = si[i];
-                            si[i] = si[ixj];
-                            si[ixj] = t;
-                        }
-                    }
-                }
-                __syncthreads();
-            }
-        }
+        bitonic_desc(sk, si, N);
     }
 
     // budget rules in rank order over the best kp cells (ranks 2*tid, 2*tid+1)
     const int C = n < kp ? n : kp;
-    int s2[2] = {0, 0}, pg2[2] = {0, 0}, c2[2] = {-1, -1};
+    int s2[2] = {0, 0}, pg2[2] = {0, 0}, c2[2] = {-1, -1}, o2[2] = {0, 0};
     int tsum = 0, psum = 0;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int r = 2 * tid + u;
-        if (r < C) {
+        if (r < C) {   // size and CSR offset in one round trip
             c2[u] = si[r];
             s2[u] = a.csize[static_cast<int64_t>(h) * a.cap + c2[u]];
+            o2[u] = a.coff[static_cast<int64_t>(h) * (a.cap + 1) + c2[u]];
         }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
         pg2[u] = (s2[u] + a.page_size - 1) / a.page_size;
         if (a.tile_mode) pg2[u] = pg2[u] > head_pages(a, h) ? 1 : 0;   // cells that alone overflow
         tsum += s2[u];
@@ -596,7 +678,7 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
         const int r = 2 * tid + u;
         if (r < m) {
             out_cell[r] = static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(sk[r] & 0xFFFFFFFFull));
-            out_off[r] = a.coff[static_cast<int64_t>(h) * (a.cap + 1) + c2[u]];
+            out_off[r] = o2[u];
             out_cnt[r] = s2[u];
             prefix_out[r] = excl_tok[u];
         }
@@ -654,6 +736,7 @@ size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
     uint32_t* ext = cv.take<uint32_t>(static_cast<size_t>(kExtHeads) * 4);
     const int nbs = (a->compact_cap + kCellsPerBlock - 1) / kCellsPerBlock;
     uint32_t* rpart = cv.take<uint32_t>(H * static_cast<size_t>(nbs) * 2);
+    uint32_t* ccnt = cv.take<uint32_t>(H * kShards);
     uint32_t* hist = cv.take<uint32_t>(H * kBins4);
     uint64_t* keys = cv.take<uint64_t>(H * a->compact_cap);
     uint64_t* cand = cv.take<uint64_t>(H * kCand4);
@@ -663,6 +746,7 @@ size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
         p->hist = hist;
         p->ext = ext;
         p->rpart = rpart;
+        p->ccnt = ccnt;
         p->nbs = nbs;
         p->cand = cand;
         p->cidx = cidx;
@@ -754,7 +838,8 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     else
         hipLaunchKernelGGL(sel4_score_kernel<false>, grid, dim3(kScoreThreads), score_lds, stream, p);
     IMI_LAUNCH_CHECK("sel4_score_kernel");
-    hipLaunchKernelGGL(sel4_hist_kernel, grid, dim3(kScoreThreads), 0, stream, p);
+    const dim3 grid_h((a->compact_cap + kHistCellsPerBlock - 1) / kHistCellsPerBlock, a->kv_heads);
+    hipLaunchKernelGGL(sel4_hist_kernel, grid_h, dim3(kScoreThreads), 0, stream, p);
     IMI_LAUNCH_CHECK("sel4_hist_kernel");
     hipLaunchKernelGGL(sel4_gather_kernel, grid, dim3(kScoreThreads), 0, stream, p);
     IMI_LAUNCH_CHECK("sel4_gather_kernel");
