@@ -290,6 +290,8 @@ def test_similarities_bit_exact(ops, oracle):
     (8000, (32, 32), 0.1, 4, 1),
     (8000, (32, 32), 0.02, 7, 2),
     (20000, (45, 45), 0.05, 8, 3),
+    (60000, (128, 128), 0.02, 4, 4),     # configs[4]'s 2 x 128 centroids: 16 cells per thread
+    (30000, (100, 90), 0.05, 4, 5),
 ])
 def test_select_bit_exact(ops, oracle, T, ks, budget, G, seed):
     note(f"[select] T={T} ks={ks} budget={budget} G={G}")
