@@ -203,14 +203,17 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     const int jcell = tid % k1, rcell = tid / k1;
     const int32_t* cntp = a.cnt + static_cast<int64_t>(h) * a.ncells;
     const int32_t* offs = a.off + static_cast<int64_t>(h) * (a.ncells + 1);
-    int sz[EPT], co_[EPT];
+    // with 8 or more cells per thread the CSR offsets are read at the end,
+    // for the kept cells only (holding them would spill registers)
+    constexpr bool LATE_OFF = EPT >= 8;
+    int sz[EPT], co_[LATE_OFF ? 1 : EPT];
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
         const int i = rcell + R * e;
         const bool in = rcell < R && i < k0;
         const int g = i * k1 + jcell;
         sz[e] = in ? cntp[g] : 0;
-        co_[e] = in ? offs[g] : 0;
+        if (!LATE_OFF) co_[e] = in ? offs[g] : 0;
     }
     // Online index maintenance (async_update.py): the override slot of each
     // of this thread's cells (-1: merged centroid unchanged), the shadow row
@@ -315,12 +318,27 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         sc[e] = p1[i < k0 ? i : 0];
     }
     if (rcell < R) {
+        if constexpr (EPT >= 8) {
+            // 8+ fused multiply-adds per LDS read already: a rolled loop keeps
+            // the centroid reads from being hoisted into spilled registers
+#pragma unroll 1
+            for (int d0 = 0; d0 < DP; d0 += 8) {
 #pragma unroll
-        for (int d = 0; d < DP; ++d) {
-            const float qd = qs[DP + d];
-            const float cv = c1T[d * (k1 + 1) + jcell];
+                for (int d = d0; d < d0 + 8; ++d) {
+                    const float qd = qs[DP + d];
+                    const float cv = c1T[d * (k1 + 1) + jcell];
 #pragma unroll
-            for (int e = 0; e < EPT; ++e) sc[e] = __builtin_fmaf(qd, cv, sc[e]);
+                    for (int e = 0; e < EPT; ++e) sc[e] = __builtin_fmaf(qd, cv, sc[e]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int d = 0; d < DP; ++d) {
+                const float qd = qs[DP + d];
+                const float cv = c1T[d * (k1 + 1) + jcell];
+#pragma unroll
+                for (int e = 0; e < EPT; ++e) sc[e] = __builtin_fmaf(qd, cv, sc[e]);
+            }
         }
     }
     // cells whose centroid was replaced: the full 128-term chain over the
@@ -501,7 +519,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
                 const int slot = c_sel + binbase[b] + atomicAdd(&hist[b], 1);
                 ck[slot] = cell_key(order_key(sc[e]), g);
                 cs[slot] = sz[e];
-                co[slot] = co_[e];
+                if (!LATE_OFF) co[slot] = co_[e];
                 seg[slot] = (c_sel + binbase[b]) | ((binbase[b + 1] - binbase[b]) << 16);
                 st[e] = 2;
             } else if (b > bK) {
@@ -530,7 +548,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
                     const int slot = c_sel + r;
                     ck[slot] = cell_key(order_key(sc[e]), g);
                     cs[slot] = sz[e];
-                    co[slot] = co_[e];
+                    if (!LATE_OFF) co[slot] = co_[e];
                     seg[slot] = c_sel | (keep << 16);
                 }
                 base += tot;
@@ -572,7 +590,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         const int pos = sg0 + r;
         sg[pos] = cell_of_key(key);
         ss[pos] = cs[sl];
-        so[pos] = co[sl];
+        if (!LATE_OFF) so[pos] = co[sl];
     }
     __syncthreads();
 
@@ -637,7 +655,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         const int r = 2 * tid + u;
         if (r < m) {
             out_cell[r] = sg[r];
-            out_off[r] = so[r];
+            out_off[r] = LATE_OFF ? offs[sg[r]] : so[r];
             out_cnt[r] = s2[u];
             prefix_out[r] = excl_tok[u];
         }
