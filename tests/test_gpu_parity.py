@@ -696,20 +696,22 @@ def test_full_size_properties_128k(ops):
         assert torch.equal(out["list_keys"][h], kd[h][perm[h].long()])
 
 
-@pytest.mark.parametrize("case", ["outlier", "zero_query", "zero_query_4096", "near_ties", "huge_centroid"])
+@pytest.mark.parametrize("case", ["outlier", "zero_query", "zero_query_4096", "near_ties", "huge_centroid",
+                                  "zero_query_16384", "near_ties_16384", "huge_centroid_16384"])
 def test_select_refinement_paths(ops, oracle, case):
     """Skewed scores (one subspace centroid blown up -> a few huge scores)
     force the bucket refinement; a zero query makes every score equal, so
-    ranking falls back to cell ids alone (with 4096 cells: more candidates
-    than the bound test hands to the exact chain, so every cell's chain is
-    run).  Near ties: the second-subspace centroids differ by ~1e-6
-    relative, so the cells of one first-subspace centroid score within a
-    few ulps of each other and their order is decided by the roundings of
-    the chain, well inside the score bounds.  A centroid of magnitude 1e33
-    puts the bounds' magnitude sums past 2^114 (no pruning) while every
-    chain stays finite."""
+    ranking falls back to cell ids alone.  Near ties: the second-subspace
+    centroids differ by ~1e-6 relative, so the cells of one first-subspace
+    centroid score within a few ulps of each other and their order is
+    decided by the roundings of the chain.  A centroid of magnitude 1e33
+    keeps every chain finite but puts the magnitude sums sum |q||c| past
+    2^114.  The _16384 cases repeat them at 2 x 128 centroids (16 cells per
+    thread, the layout of configs[4])."""
     note(f"[select] {case}")
-    H, T, ks = 4, 12000, ((64, 64) if case == "zero_query_4096" else (32, 32))
+    H, T = 4, 12000
+    ks = (128, 128) if case.endswith("_16384") else ((64, 64) if case == "zero_query_4096" else (32, 32))
+    case = case.replace("_16384", "").replace("_4096", "")
     keys, values = _kv(H, T, seed=17)
     kd, vd = keys.to(DEV), values.to(DEV)
     cent, labels, _ = ops.kmeans(kd, list(ks), 3)
