@@ -45,6 +45,7 @@ constexpr int kSelCap4 = 2048;   // min(nprobe, buffer_pages) bound
 constexpr int kExtHeads = 1024;  // KV heads one call handles (fixed-place counters)
 constexpr int kCPT = 8;          // occupied cells per thread in the score / histogram / gather kernels
 constexpr int kCS4 = 36;         // LDS row stride of a subspace centroid (16-byte aligned rows)
+constexpr int kTripCap = 1024;   // (l0, l1, l2) prefixes a score workgroup keeps
 constexpr int kCellsPerBlock = kScoreThreads * kCPT;
 // the histogram kernel takes 8x more cells per workgroup: its global merge
 // (one atomic per non-empty bin and workgroup) is a per-workgroup cost
@@ -132,12 +133,15 @@ template <bool ONLINE>
 __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     __shared__ __attribute__((aligned(16))) float qs[128];
     __shared__ int s_pair[2];
-    // dynamic LDS, sized by the launch: C0..C3 rows [4][kmax][kCS4], then the
-    // chain over subspaces 0 and 1 per (l0, l1) pair this block uses [k0 * k1]
+    __shared__ int s_trip[2];
+    // dynamic LDS, sized by the launch: C0..C3 rows [4][kmax][kCS4], the
+    // chain over subspaces 0 and 1 per (l0, l1) pair this block uses
+    // [k0 * k1], then the chain over subspaces 0..2 per (l0, l1, l2) [kTripCap]
     extern __shared__ __attribute__((aligned(16))) float s_dyn4[];
     float* cs = s_dyn4;                      // row r of subspace p at (p * kmax + r) * kCS4
     float* p01 = s_dyn4 + 4 * a.kmax * kCS4;
     const int pair_cap = a.k[0] * a.k[1];
+    float* p012 = p01 + pair_cap;
     const int h = blockIdx.y, tid = threadIdx.x;
     const int na = n_active(a, h);
     // the block's cells (ascending global id): their ids, loaded first
@@ -150,9 +154,14 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     const int c_first = blockIdx.x * kCellsPerBlock;
     const int c_last = min(na, c_first + kCellsPerBlock) - 1;
     const uint32_t k23 = static_cast<uint32_t>(a.k[2]) * static_cast<uint32_t>(a.k[3]);
+    const uint32_t k3 = static_cast<uint32_t>(a.k[3]), k2 = static_cast<uint32_t>(a.k[2]);
     if (tid == 0 && c_first <= c_last) {
-        s_pair[0] = static_cast<int>(static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c_first]) / k23);
-        s_pair[1] = static_cast<int>(static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c_last]) / k23);
+        const uint32_t g0 = static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c_first]);
+        const uint32_t g1 = static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c_last]);
+        s_pair[0] = static_cast<int>(g0 / k23);
+        s_pair[1] = static_cast<int>(g1 / k23);
+        s_trip[0] = static_cast<int>(g0 / k3);
+        s_trip[1] = static_cast<int>(g1 / k3);
     }
     if (tid < 128) {
         uint16_t qv[kMaxG4];
@@ -203,28 +212,55 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
         p01[t] = s;
     }
     __syncthreads();
-    // every cell's chain continues from its pair prefix over C2[l2], then
+    // Every cell's chain continues from its pair prefix over C2[l2], then
     // C3[l3]; dims outer and the kCPT cells inner, so one broadcast read of
-    // q feeds kCPT multiply-adds (each cell's chain keeps its order)
+    // q feeds kCPT multiply-adds (each cell's chain keeps its order).  When
+    // the block's (l0, l1, l2) range is short (dense heads), the chain
+    // through C2 is also computed once per triple, and cells continue over
+    // C3 only.
     float sv[kCPT];
-    int r2[kCPT], r3[kCPT];   // LDS offsets of the rows C2[l2], C3[l3]
-    const uint32_t k3 = static_cast<uint32_t>(a.k[3]), k2 = static_cast<uint32_t>(a.k[2]);
+    int r3[kCPT];   // LDS offsets of the rows C3[l3]
 #pragma unroll
-    for (int u = 0; u < kCPT; ++u) {
-        r3[u] = (3 * a.kmax + static_cast<int>(gv[u] % k3)) * kCS4;
-        r2[u] = (2 * a.kmax + static_cast<int>((gv[u] / k3) % k2)) * kCS4;
-        sv[u] = p01[min(max(static_cast<int>(gv[u] / k23) - pa, 0), pair_cap - 1)];
-    }
-#pragma unroll 1
-    for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
-        const float4 q4 = *reinterpret_cast<const float4*>(&qs[2 * kDp4 + 4 * d4]);
+    for (int u = 0; u < kCPT; ++u) r3[u] = (3 * a.kmax + static_cast<int>(gv[u] % k3)) * kCS4;
+    const int ta = c_first <= c_last ? s_trip[0] : 0;
+    const int ntrip = c_first <= c_last ? s_trip[1] - s_trip[0] + 1 : 0;
+    if (ntrip > 0 && ntrip <= kTripCap) {
+        for (int t = tid; t < ntrip; t += kScoreThreads) {
+            const int tg = ta + t;
+            float x = p01[min(max(tg / static_cast<int>(k2) - pa, 0), pair_cap - 1)];
+            const float* c2r = &cs[(2 * a.kmax + tg % static_cast<int>(k2)) * kCS4];
+#pragma unroll
+            for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
+                const float4 q4 = *reinterpret_cast<const float4*>(&qs[2 * kDp4 + 4 * d4]);
+                const float4 c4 = *reinterpret_cast<const float4*>(&c2r[4 * d4]);
+                x = __builtin_fmaf(q4.x, c4.x, x);
+                x = __builtin_fmaf(q4.y, c4.y, x);
+                x = __builtin_fmaf(q4.z, c4.z, x);
+                x = __builtin_fmaf(q4.w, c4.w, x);
+            }
+            p012[t] = x;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < kCPT; ++u) sv[u] = p012[min(max(static_cast<int>(gv[u] / k3) - ta, 0), kTripCap - 1)];
+    } else {
+        int r2[kCPT];   // LDS offsets of the rows C2[l2]
 #pragma unroll
         for (int u = 0; u < kCPT; ++u) {
-            const float4 c4 = *reinterpret_cast<const float4*>(&cs[r2[u] + 4 * d4]);
-            sv[u] = __builtin_fmaf(q4.x, c4.x, sv[u]);
-            sv[u] = __builtin_fmaf(q4.y, c4.y, sv[u]);
-            sv[u] = __builtin_fmaf(q4.z, c4.z, sv[u]);
-            sv[u] = __builtin_fmaf(q4.w, c4.w, sv[u]);
+            r2[u] = (2 * a.kmax + static_cast<int>((gv[u] / k3) % k2)) * kCS4;
+            sv[u] = p01[min(max(static_cast<int>(gv[u] / k23) - pa, 0), pair_cap - 1)];
+        }
+#pragma unroll 1
+        for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
+            const float4 q4 = *reinterpret_cast<const float4*>(&qs[2 * kDp4 + 4 * d4]);
+#pragma unroll
+            for (int u = 0; u < kCPT; ++u) {
+                const float4 c4 = *reinterpret_cast<const float4*>(&cs[r2[u] + 4 * d4]);
+                sv[u] = __builtin_fmaf(q4.x, c4.x, sv[u]);
+                sv[u] = __builtin_fmaf(q4.y, c4.y, sv[u]);
+                sv[u] = __builtin_fmaf(q4.z, c4.z, sv[u]);
+                sv[u] = __builtin_fmaf(q4.w, c4.w, sv[u]);
+            }
         }
     }
 #pragma unroll 1
@@ -829,9 +865,9 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     p.delta_rows = a->delta_rows;
     p.n_delta = a->n_delta;
     const dim3 grid(p.nbs, a->kv_heads);
-    // C0..C3 rows at the padded stride, then one chain prefix per (l0, l1) pair
-    const size_t score_lds = (static_cast<size_t>(4) * p.kmax * kCS4 + static_cast<size_t>(a->k[0]) * a->k[1]) *
-                             sizeof(float);
+    // C0..C3 rows at the padded stride, the chain prefixes per (l0, l1) pair and per triple
+    const size_t score_lds =
+        (static_cast<size_t>(4) * p.kmax * kCS4 + static_cast<size_t>(a->k[0]) * a->k[1] + kTripCap) * sizeof(float);
     const bool online = p.upd_slot || p.ring_cap > 0;
     if (online)
         hipLaunchKernelGGL(sel4_score_kernel<true>, grid, dim3(kScoreThreads), score_lds, stream, p);
