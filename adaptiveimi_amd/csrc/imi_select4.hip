@@ -43,7 +43,7 @@ constexpr int kScoreThreads = 256;
 constexpr int kFinalThreads = 1024;
 constexpr int kSelCap4 = 2048;   // min(nprobe, buffer_pages) bound
 constexpr int kExtHeads = 1024;  // KV heads one call handles (fixed-place counters)
-constexpr int kCPT = 8;          // occupied cells per thread in the score / histogram / gather kernels
+constexpr int kCPT = 16;         // occupied cells per thread in the score / histogram / gather kernels
 constexpr int kCS4 = 36;         // LDS row stride of a subspace centroid (16-byte aligned rows)
 constexpr int kTripCap = 1024;   // (l0, l1, l2) prefixes a score workgroup keeps
 constexpr int kCellsPerBlock = kScoreThreads * kCPT;
