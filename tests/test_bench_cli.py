@@ -1,0 +1,55 @@
+"""bench.py's command line and bookkeeping, without a GPU: the one-GPU
+refusal, the workload table and the traffic figure read from the committed
+counter summary."""
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+
+
+def _parse(monkeypatch, argv):
+    import bench
+
+    monkeypatch.setattr(sys, "argv", ["bench.py", *argv])
+    return bench.parse()
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    msg = json.loads(r.stdout.strip().splitlines()[-1])
+    assert "one GPU" in msg["error"]
+
+
+def test_default_workload_is_the_north_star(monkeypatch):
+    a = _parse(monkeypatch, [])
+    assert a.workload == "config1"
+    assert (a.layers, a.context, a.kv_heads, a.groups, tuple(a.ks), a.iters, a.budget) == \
+        (32, 131072, 8, 4, (64, 64), 10, 0.1)
+    assert a.cpu_baseline == 1 and a.online_layers == 4
+    import bench
+
+    name = bench.workload_name(a, 32, 8, 4, tuple(a.ks))
+    assert name.startswith("configs[1]") and "131072" in name and "budget 0.1" in name
+
+
+def test_other_workloads_and_overrides(monkeypatch):
+    a = _parse(monkeypatch, ["--workload", "config3"])
+    assert (a.layers, a.context, a.batch, a.groups, tuple(a.ks), a.fixed_tokens, a.budget) == \
+        (16, 262144, 2, 8, (32, 32, 32, 32), 4096, None)
+    assert a.cpu_baseline == 0 and a.online_layers == 0   # quoted on the default workload only
+    a = _parse(monkeypatch, ["--workload", "config4", "--layers", "2", "--k", "96"])
+    assert (a.layers, a.context, tuple(a.ks), a.sample, a.budget) == (2, 1048576, (96, 96), 65536, 0.02)
+
+
+def test_traffic_comes_from_the_committed_summary():
+    import bench
+
+    t = bench.measured_traffic()
+    text = (ROOT / "profiles" / "attention_kernel_traffic_128k.md").read_text()
+    assert t is not None and f"traffic_bytes_per_launch: {t}" in text
+    assert 40_000_000 < t < 60_000_000
