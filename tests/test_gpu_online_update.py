@@ -170,7 +170,7 @@ def _select_oracle(oracle, orc, q, out, sz, bud, exec_rows, ncells):
     return cells, rm, rtok, dr
 
 
-@pytest.mark.parametrize("ks", [(32, 32), (6, 6, 6, 6)])
+@pytest.mark.parametrize("ks", [(32, 32), (128, 128), (6, 6, 6, 6)])
 def test_select_with_replaced_centroids_and_delta(ops, oracle, ks):
     from adaptiveimi_amd import synthetic
 
