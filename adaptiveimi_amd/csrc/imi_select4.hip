@@ -7,26 +7,30 @@
 // empty, so the work runs over the occupied (compact) cells that
 // imi_build_index lists in ascending global id:
 //
-//   sel4_score_kernel   one thread per occupied cell: qsum (g ascending) and
-//                       the 128-term FMA chain over [C0[l0] | C1[l1] | C2[l2]
-//                       | C3[l3]] (the merged centroid, never materialised);
-//                       key = (score, ~gid) so that key order is the reference
-//                       rank order; per-head score range
-//   sel4_hist_kernel    2048 linear buckets over the range
+//   sel4_score_kernel   16 occupied cells per thread: qsum (g ascending)
+//                       and the 128-term FMA chain over [C0[l0] | C1[l1] |
+//                       C2[l2] | C3[l3]] (the merged centroid, never
+//                       materialised), continued from prefixes shared per
+//                       (l0, l1) and (l0, l1, l2); key = (score, ~gid) so
+//                       that key order is the reference rank order; one
+//                       score range per workgroup
+//   sel4_hist_kernel    the head's range from those, then 2048 linear
+//                       buckets over it
 //   sel4_gather_kernel  the bucket holding the K'-th best cell, where
 //                       K' = min(nprobe, buffer_pages, occupied cells);
 //                       every cell in or above it becomes a candidate
+//                       (16 counters per head, by cell index)
 //   sel4_final_kernel   one workgroup per head: bitonic sort of the
-//                       candidates (or, when more than 4096 cells share the
-//                       top buckets, an exact radix select of the K'-th key),
-//                       then the token and page budgets in rank order
+//                       candidates (or, when a counter overflows, an exact
+//                       radix select of the K'-th key), then the token and
+//                       page budgets in rank order
 //
 // Outputs have the 2-way layout (cells in rank order, CSR offset, count,
 // exclusive row prefix, m, rows), so the gather kernel is shared.  The
-// per-head range and counter words live at a fixed place of the workspace
-// and the final kernel zeroes them again, the score kernel clears the
-// histogram and the histogram kernel the candidate counter, so a workspace
-// zero-filled once serves later calls of any shape.
+// per-head range words live at a fixed place of the workspace and the final
+// kernel zeroes them again, the score kernel clears the histogram and the
+// histogram kernel the candidate counters, so a workspace zero-filled once
+// serves later calls of any shape.
 #include "imi_common.hpp"
 
 namespace imi {
