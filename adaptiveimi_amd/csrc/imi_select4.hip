@@ -571,6 +571,17 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     const int na = n_active(a, h);
     const int kp = kprime(a, h, na);
     int32_t* prefix_out = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
+    // every candidate slot is read before the shard counts are known (one
+    // round trip for both); slots past a shard's count are ignored
+    constexpr int kSlotsPT = kCand4 / kFinalThreads;
+    uint64_t pk[kSlotsPT];
+    int pi[kSlotsPT];
+#pragma unroll
+    for (int u = 0; u < kSlotsPT; ++u) {
+        const int64_t at = static_cast<int64_t>(h) * kCand4 + tid + u * kFinalThreads;
+        pk[u] = a.cand[at];
+        pi[u] = a.cidx[at];
+    }
     // the gather's shard counts: prefix over the shards, overflow of any
     if (tid < 64) {
         const uint32_t cnt = tid < kShards ? a.ccnt[h * kShards + tid] : 0u;
@@ -587,18 +598,18 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
         n = s_spre[kShards];
         int N = 1;
         while (N < n) N <<= 1;
-        for (int i = tid; i < N; i += kFinalThreads) {
-            uint64_t key = 0ull;
-            int ci = -1;
-            if (i < n) {
-                int sh_ = 0;
-                while (sh_ + 1 < kShards && s_spre[sh_ + 1] <= i) ++sh_;
-                const int64_t at = static_cast<int64_t>(h) * kCand4 + sh_ * kShardCap + (i - s_spre[sh_]);
-                key = a.cand[at];
-                ci = a.cidx[at];
+#pragma unroll
+        for (int u = 0; u < kSlotsPT; ++u) {
+            const int i = tid + u * kFinalThreads;
+            const int sh_ = i / kShardCap, j = i % kShardCap;
+            if (j < s_spre[sh_ + 1] - s_spre[sh_]) {
+                sk[s_spre[sh_] + j] = pk[u];
+                si[s_spre[sh_] + j] = pi[u];
             }
-            sk[i] = key;
-            si[i] = ci;
+        }
+        for (int i = n + tid; i < N; i += kFinalThreads) {
+            sk[i] = 0ull;
+            si[i] = -1;
         }
         __syncthreads();
         bitonic_desc(sk, si, N);
