@@ -93,8 +93,8 @@ def parse():
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is a design note "
-                                   "(see DESIGN.md), so --gpus must be 1"}))
+        print(json.dumps({"error": "this build runs on one GPU only (sharding over GPUs is a design, not "
+                                   "code), so --gpus must be 1"}))
         sys.exit(2)
     import numpy as np
     import torch
