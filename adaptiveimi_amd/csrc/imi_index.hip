@@ -172,11 +172,6 @@ __global__ __launch_bounds__(256) void ix_compact_pad_kernel(IxParams a, Compact
 // 256-byte row, 32 rows per wave with every load issued before any store.
 constexpr int kPermRowsPerWave = 32;
 
-typedef __attribute__((ext_vector_type(4))) unsigned int ix_u32x4_t;
-
-// The list rows are written with non-temporal stores: they are read back
-// only by the decode step, long after the build (2.96 vs 3.08 ms per layer
-// at 128k with plain stores).
 __global__ __launch_bounds__(256) void ix_permute_kernel(const uint16_t* keys, const uint16_t* values, int64_t hs,
                                                          int64_t ts, int T, const int32_t* perm, uint16_t* lk,
                                                          uint16_t* lv, int64_t list_rows) {
@@ -187,15 +182,15 @@ __global__ __launch_bounds__(256) void ix_permute_kernel(const uint16_t* keys, c
     const int my = base + lane;
     const int tok = (lane < kPermRowsPerWave && my < T) ? perm[static_cast<int64_t>(h) * T + my] : 0;
     constexpr int IT = kPermRowsPerWave / 4;
-    ix_u32x4_t kv[IT], vv[IT];
+    uint4 kv[IT], vv[IT];
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
         const int j = it * 4 + rg;
         const int t = __shfl(tok, j);
         if (base + j < T) {
             const int64_t so = h * hs + static_cast<int64_t>(t) * ts + li * 8;
-            kv[it] = *reinterpret_cast<const ix_u32x4_t*>(keys + so);
-            vv[it] = *reinterpret_cast<const ix_u32x4_t*>(values + so);
+            kv[it] = *reinterpret_cast<const uint4*>(keys + so);
+            vv[it] = *reinterpret_cast<const uint4*>(values + so);
         }
     }
 #pragma unroll
@@ -203,8 +198,8 @@ __global__ __launch_bounds__(256) void ix_permute_kernel(const uint16_t* keys, c
         const int pos = base + it * 4 + rg;
         if (pos < T) {
             const int64_t dofs = (static_cast<int64_t>(h) * list_rows + pos) * 128 + li * 8;
-            __builtin_nontemporal_store(kv[it], reinterpret_cast<ix_u32x4_t*>(lk + dofs));
-            __builtin_nontemporal_store(vv[it], reinterpret_cast<ix_u32x4_t*>(lv + dofs));
+            *reinterpret_cast<uint4*>(lk + dofs) = kv[it];
+            *reinterpret_cast<uint4*>(lv + dofs) = vv[it];
         }
     }
 }
