@@ -292,6 +292,7 @@ def test_similarities_bit_exact(ops, oracle):
     (20000, (45, 45), 0.05, 8, 3),
     (60000, (128, 128), 0.02, 4, 4),     # configs[4]'s 2 x 128 centroids: 16 cells per thread
     (30000, (100, 90), 0.05, 4, 5),
+    (32768, (64, 64), 0.5, 4, 6),        # nprobe = buffer_pages = 2048: the ranking capacity
 ])
 def test_select_bit_exact(ops, oracle, T, ks, budget, G, seed):
     note(f"[select] T={T} ks={ks} budget={budget} G={G}")
@@ -325,6 +326,7 @@ def test_select_bit_exact(ops, oracle, T, ks, budget, G, seed):
     (20000, (8, 8, 8, 8), 0.1, 8, 0),
     (30000, (16, 16, 16, 16), 0.05, 4, 1),
     (12000, (5, 7, 6, 4), 0.2, 7, 2),
+    (40000, (8, 8, 8, 8), 0.5, 4, 3),    # nprobe = 2048 < buffer_pages: the ranking capacity
 ])
 def test_select_4way_bit_exact(ops, oracle, T, ks, budget, G, seed):
     """4-way IMI selection over the occupied cells (the reference scores the
