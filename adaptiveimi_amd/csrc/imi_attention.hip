@@ -457,7 +457,9 @@ int64_t rows_bound(const imi_attention_args* a) {
 // Tiles per wave: the fewest (1..8) whose grid still fits on the CUs in one
 // round, so that every CU streams and each workgroup's share is as short as
 // possible (at 128k, H = 8: 7 tiles, 240 workgroups, 15.7 us vs 15.9 us with
-// 8 tiles and 208 workgroups); 8 when even that needs more than one round.
+// 8 tiles and 208 workgroups).  When no grid fits, the one (4..8 tiles, so
+// that each wave's ramp stays amortised) whose busiest CU streams the fewest
+// rows: workgroups per CU x rows per workgroup.
 int tiles_per_wave(const imi_attention_args* a) {
     const int64_t rows = rows_bound(a);
     const int64_t cus = device_cus();
@@ -465,7 +467,18 @@ int tiles_per_wave(const imi_attention_args* a) {
         const int64_t rpb = 64 * nt;
         if (a->kv_heads * ((rows + rpb - 1) / rpb) <= cus) return nt;
     }
-    return 8;
+    int best = 8;
+    int64_t best_load = INT64_MAX;
+    for (int nt = 8; nt >= 4; --nt) {
+        const int64_t rpb = 64 * nt;
+        const int64_t wgs = a->kv_heads * ((rows + rpb - 1) / rpb);
+        const int64_t load = (wgs + cus - 1) / cus * rpb;
+        if (load < best_load) {
+            best_load = load;
+            best = nt;
+        }
+    }
+    return best;
 }
 
 int nsplit_bound(const imi_attention_args* a) {
