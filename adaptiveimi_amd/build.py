@@ -51,7 +51,8 @@ def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False, jobs: int = 4) -> Path:
+def build(verbose: bool = False, jobs: int = 4, force: bool = False) -> Path:
+    """Compile every source (force) or the ones newer than their object."""
     BUILD_DIR.mkdir(exist_ok=True)
     hipcc = _hipcc()
     headers = list(CSRC.glob("*.hpp")) + [PKG.parent / "include" / "imi_hip.h"]
@@ -59,7 +60,7 @@ def build(verbose: bool = False, jobs: int = 4) -> Path:
 
     def compile_one(src: Path) -> Path:
         obj = BUILD_DIR / (src.stem + ".o")
-        if obj.exists() and obj.stat().st_mtime > max(src.stat().st_mtime, newest_header):
+        if not force and obj.exists() and obj.stat().st_mtime > max(src.stat().st_mtime, newest_header):
             return obj
         cmd = [hipcc, *HIPCC_FLAGS, "-I", str(PKG.parent / "include"), "-c", str(src), "-o", str(obj)]
         if verbose:
