@@ -601,7 +601,10 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     for (int u = 0; u < 2; ++u) {
         const int r = 2 * tid + u;
         s2[u] = r < C ? ss[r] : 0;
-        pg2[u] = (s2[u] + a.page_size - 1) / a.page_size;
+        // pages = ceil(size / page_size); a power-of-two page size (8 in every
+        // configuration) takes a shift instead of an integer division
+        pg2[u] = (a.page_size & (a.page_size - 1)) == 0 ? (s2[u] + a.page_size - 1) >> (__builtin_ctz(a.page_size))
+                                                        : (s2[u] + a.page_size - 1) / a.page_size;
         // tile mode counts the cells that alone overflow the page budget
         if (a.tile_mode) pg2[u] = pg2[u] > buffer_pages ? 1 : 0;
         tsum += s2[u];

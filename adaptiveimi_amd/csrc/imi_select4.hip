@@ -683,7 +683,10 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-        pg2[u] = (s2[u] + a.page_size - 1) / a.page_size;
+        // pages = ceil(size / page_size); a power-of-two page size (8 in every
+        // configuration) takes a shift instead of an integer division
+        pg2[u] = (a.page_size & (a.page_size - 1)) == 0 ? (s2[u] + a.page_size - 1) >> (__builtin_ctz(a.page_size))
+                                                        : (s2[u] + a.page_size - 1) / a.page_size;
         if (a.tile_mode) pg2[u] = pg2[u] > head_pages(a, h) ? 1 : 0;   // cells that alone overflow
         tsum += s2[u];
         psum += pg2[u];
