@@ -132,8 +132,19 @@ __device__ __forceinline__ int kprime(const Sel4& a, int h, int na) {
     return kp < na ? kp : na;
 }
 
+// Cell-id digits: POW2 (every k a power of two, as in every configuration)
+// takes shifts and masks instead of integer divisions.
+template <bool POW2>
+__device__ __forceinline__ uint32_t kdiv(uint32_t g, uint32_t k) {
+    return POW2 ? g >> __builtin_ctz(k) : g / k;
+}
+template <bool POW2>
+__device__ __forceinline__ uint32_t kmod(uint32_t g, uint32_t k) {
+    return POW2 ? g & (k - 1) : g % k;
+}
+
 // ONLINE: replaced centroids / the delta ring (a separate instantiation).
-template <bool ONLINE>
+template <bool ONLINE, bool POW2>
 __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     __shared__ __attribute__((aligned(16))) float qs[128];
     __shared__ int s_pair[2];
@@ -162,10 +173,10 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     if (tid == 0 && c_first <= c_last) {
         const uint32_t g0 = static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c_first]);
         const uint32_t g1 = static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c_last]);
-        s_pair[0] = static_cast<int>(g0 / k23);
-        s_pair[1] = static_cast<int>(g1 / k23);
-        s_trip[0] = static_cast<int>(g0 / k3);
-        s_trip[1] = static_cast<int>(g1 / k3);
+        s_pair[0] = static_cast<int>(kdiv<POW2>(g0, k23));
+        s_pair[1] = static_cast<int>(kdiv<POW2>(g1, k23));
+        s_trip[0] = static_cast<int>(kdiv<POW2>(g0, k3));
+        s_trip[1] = static_cast<int>(kdiv<POW2>(g1, k3));
     }
     if (tid < 128) {
         uint16_t qv[kMaxG4];
@@ -193,7 +204,8 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     // (ids out of order or out of range would only give wrong scores: both ends are clamped)
     const int npair = c_first <= c_last ? min(max(s_pair[1] - s_pair[0] + 1, 0), pair_cap) : 0;
     for (int t = tid; t < npair; t += kScoreThreads) {
-        const int l0 = (pa + t) / a.k[1], l1 = (pa + t) % a.k[1];
+        const uint32_t pt = static_cast<uint32_t>(pa + t), k1 = static_cast<uint32_t>(a.k[1]);
+        const int l0 = static_cast<int>(kdiv<POW2>(pt, k1)), l1 = static_cast<int>(kmod<POW2>(pt, k1));
         float s = 0.0f;
 #pragma unroll
         for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
@@ -225,14 +237,14 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     float sv[kCPT];
     int r3[kCPT];   // LDS offsets of the rows C3[l3]
 #pragma unroll
-    for (int u = 0; u < kCPT; ++u) r3[u] = (3 * a.kmax + static_cast<int>(gv[u] % k3)) * kCS4;
+    for (int u = 0; u < kCPT; ++u) r3[u] = (3 * a.kmax + static_cast<int>(kmod<POW2>(gv[u], k3))) * kCS4;
     const int ta = c_first <= c_last ? s_trip[0] : 0;
     const int ntrip = c_first <= c_last ? s_trip[1] - s_trip[0] + 1 : 0;
     if (ntrip > 0 && ntrip <= kTripCap) {
         for (int t = tid; t < ntrip; t += kScoreThreads) {
             const int tg = ta + t;
-            float x = p01[min(max(tg / static_cast<int>(k2) - pa, 0), pair_cap - 1)];
-            const float* c2r = &cs[(2 * a.kmax + tg % static_cast<int>(k2)) * kCS4];
+            float x = p01[min(max(static_cast<int>(kdiv<POW2>(tg, k2)) - pa, 0), pair_cap - 1)];
+            const float* c2r = &cs[(2 * a.kmax + static_cast<int>(kmod<POW2>(tg, k2))) * kCS4];
 #pragma unroll
             for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
                 const float4 q4 = *reinterpret_cast<const float4*>(&qs[2 * kDp4 + 4 * d4]);
@@ -246,13 +258,14 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
         }
         __syncthreads();
 #pragma unroll
-        for (int u = 0; u < kCPT; ++u) sv[u] = p012[min(max(static_cast<int>(gv[u] / k3) - ta, 0), kTripCap - 1)];
+        for (int u = 0; u < kCPT; ++u)
+            sv[u] = p012[min(max(static_cast<int>(kdiv<POW2>(gv[u], k3)) - ta, 0), kTripCap - 1)];
     } else {
         int r2[kCPT];   // LDS offsets of the rows C2[l2]
 #pragma unroll
         for (int u = 0; u < kCPT; ++u) {
-            r2[u] = (2 * a.kmax + static_cast<int>((gv[u] / k3) % k2)) * kCS4;
-            sv[u] = p01[min(max(static_cast<int>(gv[u] / k23) - pa, 0), pair_cap - 1)];
+            r2[u] = (2 * a.kmax + static_cast<int>(kmod<POW2>(kdiv<POW2>(gv[u], k3), k2))) * kCS4;
+            sv[u] = p01[min(max(static_cast<int>(kdiv<POW2>(gv[u], k23)) - pa, 0), pair_cap - 1)];
         }
 #pragma unroll 1
         for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
@@ -887,10 +900,16 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     const size_t score_lds =
         (static_cast<size_t>(4) * p.kmax * kCS4 + static_cast<size_t>(a->k[0]) * a->k[1] + kTripCap) * sizeof(float);
     const bool online = p.upd_slot || p.ring_cap > 0;
-    if (online)
-        hipLaunchKernelGGL(sel4_score_kernel<true>, grid, dim3(kScoreThreads), score_lds, stream, p);
+    bool pow2 = true;
+    for (int i = 0; i < 4; ++i) pow2 = pow2 && (a->k[i] & (a->k[i] - 1)) == 0;
+    if (online && pow2)
+        hipLaunchKernelGGL((sel4_score_kernel<true, true>), grid, dim3(kScoreThreads), score_lds, stream, p);
+    else if (online)
+        hipLaunchKernelGGL((sel4_score_kernel<true, false>), grid, dim3(kScoreThreads), score_lds, stream, p);
+    else if (pow2)
+        hipLaunchKernelGGL((sel4_score_kernel<false, true>), grid, dim3(kScoreThreads), score_lds, stream, p);
     else
-        hipLaunchKernelGGL(sel4_score_kernel<false>, grid, dim3(kScoreThreads), score_lds, stream, p);
+        hipLaunchKernelGGL((sel4_score_kernel<false, false>), grid, dim3(kScoreThreads), score_lds, stream, p);
     IMI_LAUNCH_CHECK("sel4_score_kernel");
     const dim3 grid_h((a->compact_cap + kHistCellsPerBlock - 1) / kHistCellsPerBlock, a->kv_heads);
     hipLaunchKernelGGL(sel4_hist_kernel, grid_h, dim3(kScoreThreads), 0, stream, p);
