@@ -102,6 +102,7 @@ EXPORTS = {
     "imi_sparse_attention": (ctypes.c_int, [ctypes.POINTER(AttentionArgs), _vp]),
     "imi_decode_workspace_size": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_size_t)]),
     "imi_decode_step": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp]),
+    "imi_decode_step_noalloc": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp]),
     "imi_update_workspace_size": (ctypes.c_int, [ctypes.POINTER(UpdateArgs), ctypes.POINTER(ctypes.c_size_t)]),
     "imi_update_assign": (ctypes.c_int, [ctypes.POINTER(UpdateArgs), _vp]),
     "imi_update_refresh": (ctypes.c_int, [ctypes.POINTER(UpdateArgs), _vp]),

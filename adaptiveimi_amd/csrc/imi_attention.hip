@@ -31,6 +31,8 @@
 // head's partials in split order (deterministic) and writes the bf16 output
 // and the LSE: the kernel boundary makes the partials visible across XCDs
 // without any device-scope fence.
+#include <mutex>
+
 #include "imi_common.hpp"
 
 namespace imi {
@@ -38,6 +40,7 @@ namespace imi {
 int select_launch(const imi_select_args* a, hipStream_t stream);
 int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax);
 size_t select4_workspace_size(const imi_select_args* a);
+size_t select4_zero_bytes();
 
 namespace {
 
@@ -644,6 +647,8 @@ struct DecodeLayout {
     size_t sel_bytes;
     char* attn_ws;
     size_t attn_bytes;
+    char* zero_at;           // the words the kernels expect zero at the start of a call
+    size_t zero_bytes;
     size_t total;
 };
 
@@ -662,6 +667,8 @@ DecodeLayout decode_layout(const imi_decode_args* a, void* ws) {
     L.ndelta = cv.take<int32_t>(H);
     L.sel_bytes = a->sel.parts == 4 ? select4_workspace_size(&a->sel) : 0;
     L.sel_ws = cv.take<char>(L.sel_bytes > 0 ? L.sel_bytes : 1);
+    L.zero_bytes = a->sel.parts == 4 ? select4_zero_bytes() : 0;
+    L.zero_at = L.sel_ws;
     imi_attention_args t = a->attn;
     t.workspace = nullptr;
     L.attn_bytes = attn_workspace(&t, nullptr);
@@ -699,15 +706,11 @@ extern "C" int imi_decode_workspace_size(const imi_decode_args* a, size_t* bytes
     return IMI_OK;
 }
 
-extern "C" int imi_decode_step(const imi_decode_args* a, imi_stream_t stream_) {
-    clear_error();
-    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-    int rc = decode_validate(a);
-    if (rc) return rc;
-    const DecodeLayout need = decode_layout(a, nullptr);
-    IMI_REQUIRE(a->attn.workspace && a->attn.workspace_bytes >= need.total, IMI_ERR_WORKSPACE,
-                "imi_decode_step: workspace %zu bytes < %zu required", a->attn.workspace_bytes, need.total);
-    const DecodeLayout L = decode_layout(a, a->attn.workspace);
+namespace {
+// One decode step with its workspace at ws (already checked to be large enough).
+int decode_run(const imi_decode_args* a, void* ws, hipStream_t stream) {
+    int rc;
+    const DecodeLayout L = decode_layout(a, ws);
     IMI_REQUIRE(a->phases >= 0 && a->phases < 16, IMI_ERR_INVALID, "imi_decode_step: phases %d outside [0, 15]",
                 a->phases);
     const int phases = a->phases == 0 ? 3 : a->phases;
@@ -750,4 +753,81 @@ extern "C" int imi_decode_step(const imi_decode_args* a, imi_stream_t stream_) {
     t.workspace = L.attn_ws;
     t.workspace_bytes = L.attn_bytes;
     return attn_launch(&t, stream, kernels);
+}
+}  // namespace
+
+extern "C" int imi_decode_step(const imi_decode_args* a, imi_stream_t stream_) {
+    clear_error();
+    int rc = decode_validate(a);
+    if (rc) return rc;
+    const DecodeLayout need = decode_layout(a, nullptr);
+    IMI_REQUIRE(a->attn.workspace && a->attn.workspace_bytes >= need.total, IMI_ERR_WORKSPACE,
+                "imi_decode_step: workspace %zu bytes < %zu required", a->attn.workspace_bytes, need.total);
+    return decode_run(a, a->attn.workspace, reinterpret_cast<hipStream_t>(stream_));
+}
+
+// ------------------------------------------------ decode without allocation
+// imi_decode_step_noalloc keeps its workspace in this file-scope device
+// array instead of a caller buffer.  Host code never passes the array's name
+// to a kernel (on the host it is only a stand-in symbol): the device address
+// comes from hipGetSymbolAddress, once per device, and is kept per device.
+namespace {
+constexpr size_t kScratchBytes = size_t(64) << 20;   // 64 MiB per device
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (resolved on the first
+// call per device, with that device current).
+int scratch_address(void** out) {
+    int dev = 0;
+    IMI_HIP_CHECK(hipGetDevice(&dev));
+    IMI_REQUIRE(dev >= 0 && dev < kMaxDevices, IMI_ERR_UNSUPPORTED, "imi_decode_step_noalloc: device %d beyond %d",
+                dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        IMI_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        IMI_REQUIRE(ptr != nullptr, IMI_ERR_HIP, "imi_decode_step_noalloc: no device address for the scratch array");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return IMI_OK;
+}
+
+// Zero fill with a kernel (no memset node when a caller captures the step).
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, size_t n) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256)
+        p[i] = 0u;
+}
+}  // namespace
+
+extern "C" int imi_decode_step_noalloc(const imi_decode_args* a, imi_stream_t stream_) {
+    clear_error();
+    hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    int rc = decode_validate(a);
+    if (rc) return rc;
+    const DecodeLayout need = decode_layout(a, nullptr);
+    IMI_REQUIRE(need.total <= kScratchBytes, IMI_ERR_UNSUPPORTED,
+                "imi_decode_step_noalloc: this shape needs %zu bytes of scratch, the static scratch holds %zu",
+                need.total, kScratchBytes);
+    void* ws = nullptr;
+    rc = scratch_address(&ws);
+    if (rc) return rc;
+    // The array keeps whatever the previous call (of any shape) left in it:
+    // clear the words this call's kernels expect to find zero.
+    const DecodeLayout L = decode_layout(a, ws);
+    if (L.zero_bytes > 0) {
+        const size_t words = L.zero_bytes / 4;
+        const unsigned blocks = static_cast<unsigned>(words < 256 * 256 ? (words + 255) / 256 : 256);
+        hipLaunchKernelGGL(zero_words_kernel, dim3(blocks), dim3(256), 0, stream,
+                           reinterpret_cast<uint32_t*>(L.zero_at), words);
+        IMI_LAUNCH_CHECK("zero_words_kernel");
+    }
+    return decode_run(a, ws, stream);
 }

@@ -843,6 +843,10 @@ int select4_validate(const imi_select_args* a) {
     return IMI_OK;
 }
 
+// Bytes at the start of the workspace that a call expects zero (the
+// fixed-place range words; every call leaves them zero again).
+size_t select4_zero_bytes() { return static_cast<size_t>(kExtHeads) * 4 * sizeof(uint32_t); }
+
 size_t select4_workspace_size(const imi_select_args* a) {
     imi_select_args t = *a;
     t.workspace = nullptr;

@@ -343,6 +343,19 @@ typedef struct {
 int imi_decode_workspace_size(const imi_decode_args* a, size_t* bytes);
 int imi_decode_step(const imi_decode_args* a, imi_stream_t stream);
 
+/* imi_decode_step without any allocation and without a caller workspace:
+ * no counterpart in the reference.  It is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops).  The
+ * workspace lives in a static device array of 64 MiB per device, held until
+ * the process ends (its address is resolved once per device on the first
+ * call); a shape whose workspace (imi_decode_workspace_size) exceeds it is
+ * rejected with IMI_ERR_UNSUPPORTED.  attn.workspace / workspace_bytes are
+ * ignored.  Every call on a device shares that device's array, so calls
+ * that overlap in time on one device (two streams, two threads) race; calls
+ * in stream order are fine.  Each call first clears the words its kernels
+ * expect zero.  No hipMalloc / hipFree is called. */
+int imi_decode_step_noalloc(const imi_decode_args* a, imi_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -186,3 +186,22 @@ def test_ops_refuse_cpu_tensors():
     k = torch.zeros((2, 64, 128), dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="HIP device"):
         ops.kmeans(k, [8, 8], 2)
+
+
+def test_noalloc_rejects_shapes_beyond_its_scratch(L):
+    """The no-alloc step checks its workspace need against the static array
+    (64 MiB) before touching the device."""
+    from adaptiveimi_amd._lib import AttentionArgs, DecodeArgs, SelectArgs
+
+    s = SelectArgs(query=16, centroids=16, cell_count=16, cell_offset=16, kv_heads=4096, groups=4, dim=128, parts=2,
+                   nprobe=410, max_tokens=3276, buffer_pages=410, page_size=8, sel_cap=410)
+    s.k[0] = s.k[1] = 64
+    d = DecodeArgs()
+    d.sel = s
+    d.attn = AttentionArgs(query=16, out=16, list_keys=16, list_values=16, kv_heads=4096, groups=4, dim=128,
+                           max_rows=410 * 8, steady_stride=512)
+    need = ctypes.c_size_t()
+    assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == 0
+    assert need.value > 64 << 20
+    assert L.imi_decode_step_noalloc(ctypes.byref(d), None) == 3
+    assert "scratch" in L.imi_last_error().decode()
