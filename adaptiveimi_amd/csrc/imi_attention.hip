@@ -4,20 +4,28 @@
 // (include/copy_kernel.cuh:220-335, launched by cuda/gather_copy.cu:100-213:
 // rows = [static_len steady rows | miss pages | hit pages]) followed by the
 // unvendored weighted_flash_decoding (retrieval.py:439-447).  Here the rows
-// are read in place: the steady zone for the first static_len rows, then the
-// CSR list rows of the selected cells (each workgroup stages the head's
-// selection in LDS and each wave maps its rows to list rows with two ballot
-// rounds and a flag count) -- no execution buffer.
+// are read in place -- the steady zone for the first static_len rows, the
+// CSR list rows of the selected cells, then the matched delta-ring rows
+// (steady rows) -- with no execution buffer.
 //
-// Grid: H * nsplit workgroups of 4 waves; workgroup b takes split b / H of
-// head (b + b / H) % H, so consecutive workgroups (which the dispatcher deals
-// round robin to the 8 XCDs) rotate over the heads and every XCD gets a
-// share of every head's rows.  A wave owns NT tiles of 16 consecutive rows
+// Grid: H * S workgroups of 4 waves; workgroup b takes split s = b / H of
+// head (b + s) % H, so consecutive workgroups (which the dispatcher deals
+// round robin to the 8 XCDs) rotate over the heads.  Split s covers rows
+// [R s / S, R (s + 1) / S) of its head's R attended rows, so the work follows
+// the rows each head actually selected, not a bound.
+//
+// Prologue: one round trip brings q, the head's row / cell / delta counts,
+// the first kStageCap cells of its selection (row prefix and CSR offset per
+// cell) and its delta rows into registers, then LDS.  The start of every
+// non-empty cell inside the workgroup's rows is flagged with its rank, an
+// inclusive max-scan gives each row its cell, and row -> list row (or -1 -
+// steady row) goes to an LDS table.  The staged selection shares its LDS
+// with the K / V tiles, which are first written after the table is built.
+//
+// Streaming: a wave owns a quarter of the workgroup's rows in tiles of 16
 // and keeps two tiles in flight ahead of the one it computes.  Rows are read
 // whole (16 lanes x 16 bytes per 256-byte row) and staged through LDS, which
-// hands K back in the MFMA operand layout and V transposed.
-//
-// Per tile, on the matrix cores:
+// hands K back in the MFMA operand layout and V transposed.  Per tile:
 //   S = K Q^T   4 x v_mfma_f32_16x16x32_bf16: A = the K tile read back from
 //               LDS (lane -> token lane % 16, 8 dims), B = Q with column n holding
 //               query n % G; lane l gets S[token 4(l/16)+i][query (l%16)%G].
@@ -27,11 +35,13 @@
 //               tile with ds_read_b64_tr_b16 (4 tokens x 1 dim per lane).
 // Softmax is online in base 2 with fp32 state per query slot; the rescale
 // of O is skipped when no running max moved.  The waves of a workgroup merge
-// in LDS into one partial (plain stores); a second kernel merges each
-// head's partials in split order (deterministic) and writes the bf16 output
-// and the LSE: the kernel boundary makes the partials visible across XCDs
-// without any device-scope fence.
+// in LDS into one partial (plain stores); merge_kernel combines each head's S
+// partials in split order (deterministic) and writes the bf16 output and the
+// LSE: the kernel boundary makes the partials visible across XCDs without any
+// device-scope fence.
+#include <climits>
 #include <mutex>
+#include <type_traits>
 
 #include "imi_common.hpp"
 
@@ -41,14 +51,19 @@ int select_launch(const imi_select_args* a, hipStream_t stream);
 int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax);
 size_t select4_workspace_size(const imi_select_args* a);
 size_t select4_zero_bytes();
+size_t sel2_keys_bytes(const imi_select_args* a);
 
 namespace {
 
 constexpr int kWaves = 4;            // waves per workgroup (256 threads)
+constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxSplit = 4096;      // splits per head the merge kernel handles
-constexpr int kSelCapMax = 2048;     // selected cells per head the gather indexes
+constexpr int kLocCap = 2048;        // attended rows per workgroup (row lookup in LDS)
 constexpr int kDeltaMax = 1024;      // delta rows per head (the delta ring)
-constexpr int kVStride = 144;        // u16 per LDS row of a wave's V tile (288 B)
+constexpr int kVStride = 144;        // u16 per LDS row of a wave's K / V tile (288 B)
+constexpr int kPF = 2;               // K / V tiles in flight per wave
+constexpr int kStageCap = 2048;      // selected cells staged in the prologue's first round trip
+constexpr int kStageMax = 16384;     // selected cells per head (row prefix + offset staged in LDS)
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
@@ -56,8 +71,9 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
 typedef __attribute__((ext_vector_type(2))) unsigned int u32x2_t;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;   // global (not flat) loads
 
-struct AttnParams {
+struct DecParams {
     const uint16_t* q;
     const uint16_t* sk;
     const uint16_t* sv;
@@ -66,21 +82,23 @@ struct AttnParams {
     const uint16_t* lk;
     const uint16_t* lv;
     int64_t list_rows;
-    const int32_t* sel_offset;  // [H][sel_cap]
-    const int32_t* sel_prefix;  // [H][sel_cap + 1]
-    const int32_t* n_selected;  // [H]
-    int sel_cap;
-    const int32_t* n_rows;      // [H]
-    const int32_t* delta_rows;  // [H][delta_cap] steady rows after the selected rows, or null
-    const int32_t* n_delta;     // [H]
-    int delta_cap;
-    int H, nsplit;
-    int rows_per_block;
+    int H, S;
     float scale_log2;        // scale * log2(e)
-    float* part_acc;         // [H][nsplit][G][128]
-    float* part_ml;          // [H][nsplit][G][2]
+    float* part_acc;         // [H][S][G][128]
+    float* part_ml;          // [H][S][G][2]
     uint16_t* out;           // [H*G][128]
     float* lse;              // [H*G] or null
+    // given selection
+    const int32_t* g_prefix;   // [H][g_cap + 1]
+    const int32_t* g_offset;   // [H][g_cap]
+    const int32_t* g_nsel;     // [H]
+    const int32_t* g_nrows;    // [H]
+    int g_cap;
+    const int32_t* g_drows;    // [H][g_dcap] or null
+    const int32_t* g_ndelta;   // [H]
+    int g_dcap;
+    int o_base;                // LDS word of the staged offsets (after the prefix)
+    int stage_words;           // LDS words shared by the staged selection and the K / V tiles
 };
 
 // Weight exp2(m - M) of a state with running max m inside a merge whose max
@@ -97,137 +115,186 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Number of set bits of the 128-bit mask (lo, hi) at positions 0..i.
-__device__ __forceinline__ int popc_upto(uint64_t lo, uint64_t hi, int i) {
-    if (i < 64) return __builtin_popcountll(lo & (~0ull >> (63 - i)));
-    return __builtin_popcountll(lo) + __builtin_popcountll(hi & (~0ull >> (127 - i)));
-}
-
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
 }
 
-// One workgroup = 4 waves over rows [split * rows_per_block, +rows_per_block)
-// of its head; the workgroup writes one partial (max, sum, unnormalised
-// output) with plain stores and merge_kernel combines the partials after the
-// kernel boundary.  Workgroups past the end of their head write nothing.
-// DELTA: rows appended after the selected rows (a separate instantiation).
-template <int G, int NT, bool DELTA>
-__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) void attention_kernel(AttnParams a) {
-    constexpr int RW = NT * 16;                       // rows per wave
-    constexpr int NR = (RW + 63) / 64;                // row locations per lane
-    static_assert(NR <= 2, "the row lookup covers windows of at most 128 rows");
-    constexpr int SU = (kSelCapMax + 1 + 64 * kWaves - 1) / (64 * kWaves);
-    constexpr int DU = kDeltaMax / (64 * kWaves);
-    __shared__ float s_acc[kWaves][G][128];
-    __shared__ float s_ml[kWaves][G][2];
-    __shared__ int s_pre[kSelCapMax + 1];
-    __shared__ int s_off[kSelCapMax];
-    __shared__ int s_drow[DELTA ? kDeltaMax : 1];
-    __shared__ int s_flag[kWaves][NR * 64];
-    __shared__ __attribute__((aligned(16))) uint16_t s_v[kWaves][16 * kVStride];
-    __shared__ __attribute__((aligned(16))) uint16_t s_k[kWaves][16 * kVStride];
+// Inclusive max-scan across the 64 lanes (row shifts, then row broadcasts;
+// lanes without a source keep INT_MIN, the identity).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_imin(int v) {
+    return __builtin_amdgcn_update_dpp(INT_MIN, v, CTRL, ROW_MASK, 0xF, false);
+}
+__device__ __forceinline__ int wave_incl_max_scan(int v) {
+    v = max(v, dpp_imin<0x111>(v));
+    v = max(v, dpp_imin<0x112>(v));
+    v = max(v, dpp_imin<0x114>(v));
+    v = max(v, dpp_imin<0x118>(v));
+    v = max(v, dpp_imin<0x142, 0xA>(v));
+    v = max(v, dpp_imin<0x143, 0xC>(v));
+    return v;
+}
+
+// LDS: [staged selection | K and V tiles] (stage_words), then the wave
+// partials, the row lookup and the delta rows.
+constexpr int kTileU16 = kWaves * 16 * kVStride;   // one of the K / V tiles of all waves
+constexpr int kTileWords = kTileU16;               // both tiles, in 32-bit words
+template <int G>
+constexpr int tail_words() {
+    return kWaves * G * 128 + kWaves * G * 2 + kLocCap + kDeltaMax;
+}
+
+// One workgroup = 4 waves over its split of head h's rows [static | selected
+// | delta]; writes one partial (max, sum, unnormalised output).  The head's
+// selection (row prefix and CSR offset per cell, at most kStageCap cells in
+// the first round trip) is staged in LDS together with q and the row counts.
+template <int G>
+__global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
+    extern __shared__ __attribute__((aligned(16))) int lds[];
+    int* P = lds;                                   // [g_cap + 1] row prefix of the selected cells
+    int* O = lds + a.o_base;                        // [g_cap] CSR offset of each selected cell
+    uint16_t* s_k = reinterpret_cast<uint16_t*>(lds);   // the tiles reuse the staged selection's words
+    uint16_t* s_v = s_k + kTileU16;
+    float* s_acc = reinterpret_cast<float*>(lds + a.stage_words);           // [4][G][128]
+    float* s_ml = s_acc + kWaves * G * 128;                                 // [4][G][2]
+    int* s_loc = reinterpret_cast<int*>(s_ml + kWaves * G * 2);             // [kLocCap]
+    int* s_drow = s_loc + kLocCap;                                          // [kDeltaMax]
 
     const int b = blockIdx.x;
     const int split = b / a.H;
     const int h = (b % a.H + split) % a.H;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lg = lane >> 4, ln = lane & 15;
-    const int row0 = split * a.rows_per_block + wave * RW;
 
-    // One round trip for everything the gather needs: q (as the MFMA B
-    // operand: column ln = query ln % G, dims 32c + 8lg..), the row and cell
-    // counts, and the head's selection (row prefix and CSR offset per cell).
+    // ---- one round trip: q (as the MFMA B operand: column ln = query
+    // ln % G, dims 32c + 8lg ..), the row and cell counts, the first
+    // kStageCap cells of the selection and the delta rows ----
     u32x4_t qb[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
         qb[c] = *reinterpret_cast<const u32x4_t*>(a.q + (static_cast<int64_t>(h) * G + ln % G) * 128 + c * 32 + lg * 8);
-    const int nrows = a.n_rows[h];
-    const int m = a.n_selected[h];
-    const int nd = DELTA ? min(max(a.n_delta[h], 0), a.delta_cap) : 0;
-    {
-        const int32_t* pre = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
-        const int32_t* off = a.sel_offset + static_cast<int64_t>(h) * a.sel_cap;
-        int pv[SU], ov[SU];
+    const int32_t* pre = a.g_prefix + static_cast<int64_t>(h) * (a.g_cap + 1);
+    const int32_t* offg = a.g_offset + static_cast<int64_t>(h) * a.g_cap;
+    const int m_raw = a.g_nsel[h];
+    const int nrows_raw = a.g_nrows[h];
+    const int nd_raw = a.g_drows ? a.g_ndelta[h] : 0;
+    constexpr int SU = (kStageCap + kThreads) / kThreads;   // entries per thread (prefix has one more)
+    int pv[SU], ov[SU];
+    const int c1 = min(a.g_cap, kStageCap);
 #pragma unroll
-        for (int u = 0; u < SU; ++u) {
-            const int i = tid + u * 64 * kWaves;
-            pv[u] = i <= a.sel_cap ? pre[i] : 0;
-            ov[u] = i < a.sel_cap ? off[i] : 0;
-        }
-        int dv[DU];
-#pragma unroll
-        for (int u = 0; u < DU; ++u) {
-            const int i = tid + u * 64 * kWaves;
-            dv[u] = DELTA && i < a.delta_cap ? a.delta_rows[static_cast<int64_t>(h) * a.delta_cap + i] : 0;
-        }
-#pragma unroll
-        for (int u = 0; u < SU; ++u) {
-            const int i = tid + u * 64 * kWaves;
-            if (i <= a.sel_cap) s_pre[i] = pv[u];
-            if (i < a.sel_cap) s_off[i] = ov[u];
-        }
-        if (DELTA) {
-#pragma unroll
-            for (int u = 0; u < DU; ++u) s_drow[tid + u * 64 * kWaves] = dv[u];
-        }
+    for (int u = 0; u < SU; ++u) {
+        const int i = tid + u * kThreads;
+        pv[u] = i <= c1 ? pre[i] : 0;
+        ov[u] = i < c1 ? offg[i] : 0;
     }
+    int dv[kDeltaMax / kThreads];
+#pragma unroll
+    for (int u = 0; u < kDeltaMax / kThreads; ++u) {
+        const int i = tid + u * kThreads;
+        dv[u] = (a.g_drows && i < a.g_dcap) ? a.g_drows[static_cast<int64_t>(h) * a.g_dcap + i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+        const int i = tid + u * kThreads;
+        if (i <= c1) P[i] = pv[u];
+        if (i < c1) O[i] = ov[u];
+    }
+#pragma unroll
+    for (int u = 0; u < kDeltaMax / kThreads; ++u) s_drow[tid + u * kThreads] = dv[u];
+    const int m = min(max(m_raw, 0), a.g_cap);
+    const int nrows = max(nrows_raw, 0);
+    const int nd = min(max(nd_raw, 0), a.g_dcap);
+    // selections above kStageCap cells: the rest in further round trips
+    for (int i = kStageCap + 1 + tid; i <= m; i += kThreads) P[i] = pre[i];
+    for (int i = kStageCap + tid; i < m; i += kThreads) O[i] = offg[i];
     __syncthreads();
-    // rows: [static_len steady rows | nrows list rows | nd delta rows (steady)]
-    const int N = a.static_len + nrows + nd;
-    if (split * a.rows_per_block >= N) return;   // the merge ignores this split
+    const int sl = a.static_len;
+    // split boundaries floor(R s / S) in 32-bit arithmetic: R = q S + rem
+    // (R < 2^32, S <= kMaxSplit, so rem * s < 2^24)
+    const uint32_t R = static_cast<uint32_t>(sl) + static_cast<uint32_t>(nrows) + static_cast<uint32_t>(nd);
+    const uint32_t Rq = R / static_cast<uint32_t>(a.S), Rr = R % static_cast<uint32_t>(a.S);
+    const int64_t r0 = static_cast<int64_t>(Rq) * split + Rr * static_cast<uint32_t>(split) / static_cast<uint32_t>(a.S);
+    const int64_t r1e =
+        static_cast<int64_t>(Rq) * (split + 1) + Rr * static_cast<uint32_t>(split + 1) / static_cast<uint32_t>(a.S);
+    const int64_t r1 = min(r1e, r0 + kLocCap);   // the host sizes S so that this never cuts
 
-    // List row of window row i (rows row0 + i, i = lane + 64r): the wave
-    // finds the cell c0 that holds its first list row j0 (two ballot rounds
-    // over the staged prefix), flags the window offsets where the following
-    // cells start, and counts the flags up to each row.  Selected cells hold
-    // at least one row, so their starts are distinct; locations are clamped
-    // to the list.  A delta row gets -1 - its steady row (clamped to the
-    // steady zone).
-    int loc[NR];
+    // ---- row lookup: s_loc[i] for rows r0 + i of this split.  Each wave
+    // fills the entries of its own quarter (no workgroup barrier): a steady
+    // row gets -1 - its row, a delta row -1 - its ring row, a selected row j
+    // the list row O[c] + j - P[c] of the cell c holding it.  The cell of the
+    // wave's first selected row comes from a 64-ary search over the staged
+    // prefix (ballots); the start of every later non-empty cell inside the
+    // wave's rows is flagged with its rank and an inclusive max-scan gives
+    // every row its cell.  List rows are clamped to the list, steady rows to
+    // the steady zone. ----
+    const int nr = static_cast<int>(r1 - r0);
+    const int wb = nr * wave / kWaves, we = nr * (wave + 1) / kWaves;
+    const int wn = we - wb;   // <= kLocCap / 4 = 512
     {
-        const int j0 = max(row0 - a.static_len, 0);
-        int c0 = 0;
-        if (m > 1) {
-            const int step = (m + 63) >> 6;   // <= 32 cells per lane sample
-            const int cs = lane * step;
-            const uint64_t b1 = __builtin_amdgcn_ballot_w64(cs < m && s_pre[cs] <= j0);
-            const int base = (63 - __builtin_clzll(b1 | 1ull)) * step;
-            const int cc = base + lane;
-            const uint64_t b2 = __builtin_amdgcn_ballot_w64(lane < step && cc < m && s_pre[cc] <= j0);
-            c0 = base + (63 - __builtin_clzll(b2 | 1ull));
-        }
-        int* fl = s_flag[wave];
-#pragma unroll
-        for (int r = 0; r < NR; ++r) fl[lane + 64 * r] = 0;
-        wave_lds_sync();
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            const int c = c0 + 1 + lane + 64 * r;
-            if (c < m) {
-                const int o = s_pre[c] - j0;
-                if (o > 0 && o < NR * 64) fl[o] = 1;
+        const int lmax = max(static_cast<int>(a.list_rows) - 1, 0);
+        const int smax = static_cast<int>(a.s_stride) - 1;
+        const int64_t w0 = r0 + wb;   // first row of this wave
+        // positions [0, pa) steady, [pa, pb) selected, [pb, wn) delta
+        const int pa = static_cast<int>(min(max(sl - w0, int64_t(0)), int64_t(wn)));
+        const int pb = static_cast<int>(min(max(sl + nrows - w0, int64_t(0)), int64_t(wn)));
+        for (int i = lane; i < wn; i += 64) {
+            int v = INT_MIN;
+            if (i < pa) {
+                v = -1 - static_cast<int>(w0 + i);
+            } else if (i >= pb) {
+                const int d = static_cast<int>(w0 + i - sl - nrows);
+                v = -1 - min(max(s_drow[min(d, kDeltaMax - 1)], 0), smax);
             }
+            s_loc[wb + i] = v;
         }
-        wave_lds_sync();
-        uint64_t fm[2] = {0ull, 0ull};
-#pragma unroll
-        for (int r = 0; r < NR; ++r) fm[r] = __builtin_amdgcn_ballot_w64(fl[lane + 64 * r] != 0);
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            const int j = row0 + lane + 64 * r - a.static_len;
-            int l = 0;
-            if (j >= 0 && j < nrows) {
-                const int c = c0 + popc_upto(fm[0], fm[1], j - j0);
-                l = s_off[c] + (j - s_pre[c]);
-                l = min(max(l, 0), static_cast<int>(a.list_rows) - 1);
-            } else if (DELTA && j >= nrows && j < nrows + nd) {
-                l = -1 - min(max(s_drow[j - nrows], 0), static_cast<int>(a.s_stride) - 1);
+        if (pb > pa) {
+            const int jlo = static_cast<int>(w0 + pa - sl), jhi = jlo + (pb - pa);
+            // c0 = the last cell with P[c] <= jlo (P[0] = 0 <= jlo)
+            int lo = 0, len = m;
+            while (len > 1) {
+                const int step = (len + 63) >> 6;
+                const bool ok = lane * step < len && P[lo + lane * step] <= jlo;
+                const int k = 63 - __builtin_clzll(__builtin_amdgcn_ballot_w64(ok) | 1ull);
+                lo += k * step;
+                len = min(step, len - k * step);
             }
-            loc[r] = l;
+            wave_lds_sync();   // the fill above precedes the flags
+            if (lane == 0) s_loc[wb + pa] = lo;
+            // later cells start above jlo: flag those that start below jhi
+            for (int cb = lo + 1; cb < m; cb += 64) {
+                const int c = cb + lane;
+                const int pc = c < m ? P[c] : INT_MAX;
+                const int pn = c < m ? P[c + 1] : 0;
+                if (pc < jhi && pn > pc) s_loc[wb + pa + (pc - jlo)] = c;
+                if (__builtin_amdgcn_readlane(pc, 63) >= jhi) break;
+            }
+            wave_lds_sync();
+            // `per` consecutive selected positions per lane
+            const int per = (pb - pa + 63) >> 6;   // <= 8
+            const int q0 = pa + lane * per;
+            int v[8];
+            int run = INT_MIN;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                v[u] = (u < per && q0 + u < pb) ? s_loc[wb + q0 + u] : INT_MIN;
+                run = max(run, v[u]);
+            }
+            // exclusive max over the lanes below (wave_shr:1 of the inclusive scan)
+            int c = __builtin_amdgcn_update_dpp(INT_MIN, wave_incl_max_scan(run), 0x138, 0xF, 0xF, false);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                c = max(c, v[u]);
+                if (u < per && q0 + u < pb) {
+                    const int cc = max(c, 0);
+                    const int j = jlo + (q0 + u - pa);
+                    s_loc[wb + q0 + u] = min(max(O[cc] + (j - P[cc]), 0), lmax);
+                }
+            }
         }
     }
+    wave_lds_sync();
 
+    // ---- stream this wave's quarter of the rows ----
     const uint16_t* skh = a.sk + static_cast<int64_t>(h) * a.s_stride * 128;
     const uint16_t* svh = a.sv + static_cast<int64_t>(h) * a.s_stride * 128;
     const uint16_t* lkh = a.lk + static_cast<int64_t>(h) * a.list_rows * 128;
@@ -236,40 +303,34 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[d] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     float m_own = -INFINITY, l_own = 0.0f;   // softmax state of query slot ln
-    uint16_t* sv = s_v[wave];
-    uint16_t* sk = s_k[wave];
-
-    if (row0 < N) {
-        // Tile t, load it: rows t*16 + 4it + rg, 16 lanes x 16 bytes per row
-        // (whole 256-byte rows per 16 lanes).  Rows past N read list row 0
-        // (in bounds) and are masked below.
+    uint16_t* sv = s_v + wave * 16 * kVStride;
+    uint16_t* sk = s_k + wave * 16 * kVStride;
+    const int nt = (wn + 15) >> 4;
+    if (nt > 0) {
+        // Tile t: rows wb + t*16 + 4it + rg, 16 lanes x 16 bytes per row.
+        // Rows past the wave's end read list row 0 (in bounds) and are masked.
         const int rg = lane >> 4, li = lane & 15;
-        u32x4_t kb[2][4], vb[2][4];
-        auto load = [&](int t, int slot) {
+        u32x4_t kb[kPF][4], vb[kPF][4];
+        auto load = [&](int t, auto slot_c) {
+            constexpr int SLOT = decltype(slot_c)::value;
 #pragma unroll
             for (int it = 0; it < 4; ++it) {
                 const int jt = t * 16 + it * 4 + rg;
-                const int n = row0 + jt;
-                const int lr = __shfl(loc[(t * 16) >> 6], jt & 63);
-                const bool st = n < a.static_len;
-                const bool dl = DELTA && !st && n < N && lr < 0;   // delta row: steady row -1 - lr
-                const int64_t roff =
-                    (st ? static_cast<int64_t>(n) : static_cast<int64_t>(dl ? -1 - lr : (n < N ? lr : 0))) * 128;
-                kb[slot][it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>((st || dl ? skh : lkh) + roff + li * 8));
-                vb[slot][it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>((st || dl ? svh : lvh) + roff + li * 8));
+                const int lr = jt < wn ? s_loc[wb + jt] : 0;
+                const bool steady = lr < 0;
+                const int64_t roff = static_cast<int64_t>(steady ? -1 - lr : lr) * 128;
+                kb[SLOT][it] = __builtin_nontemporal_load((g_u32x4_t*)((steady ? skh : lkh) + roff + li * 8));
+                vb[SLOT][it] = __builtin_nontemporal_load((g_u32x4_t*)((steady ? svh : lvh) + roff + li * 8));
             }
         };
-        load(0, 0);
-        if (NT > 1) load(1, 1);
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const int slot = t & 1;
-            // K and V tiles -> LDS, row-major [token][dim]; K comes back in
-            // the MFMA A layout (lane -> token ln, dims 32c + 8lg)
+        auto body = [&](int t, auto slot_c, auto prefetch_c) {
+            constexpr int SLOT = decltype(slot_c)::value;
+            // K and V tiles -> LDS, row-major [token][dim]; K comes back in the
+            // MFMA A layout (lane -> token ln, dims 32c + 8lg)
 #pragma unroll
             for (int it = 0; it < 4; ++it) {
-                *reinterpret_cast<u32x4_t*>(sv + (4 * it + rg) * kVStride + li * 8) = vb[slot][it];
-                *reinterpret_cast<u32x4_t*>(sk + (4 * it + rg) * kVStride + li * 8) = kb[slot][it];
+                *reinterpret_cast<u32x4_t*>(sv + (4 * it + rg) * kVStride + li * 8) = vb[SLOT][it];
+                *reinterpret_cast<u32x4_t*>(sk + (4 * it + rg) * kVStride + li * 8) = kb[SLOT][it];
             }
             wave_lds_sync();
             u32x4_t ka[4];
@@ -280,11 +341,10 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
             for (int c = 0; c < 4; ++c)
                 s4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka[c]),
                                                              __builtin_bit_cast(bf16x8_t, qb[c]), s4, 0, 0, 0);
-            if (t + 2 < NT) load(t + 2, slot);
+            if constexpr (decltype(prefetch_c)::value) load(t + kPF, slot_c);
             float s[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                s[i] = (row0 + t * 16 + 4 * lg + i < N) ? s4[i] * a.scale_log2 : -INFINITY;
+            for (int i = 0; i < 4; ++i) s[i] = (t * 16 + 4 * lg + i < wn) ? s4[i] * a.scale_log2 : -INFINITY;
             float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
             tm = fmaxf(tm, xor16(tm));
             tm = fmaxf(tm, xor32(tm));
@@ -328,7 +388,34 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
                                                                    0, 0);
             }
             wave_lds_sync();
+        };
+        // Groups of kPF tiles, every load and body unconditional (so that the
+        // waits before each tile count exactly the loads issued after it):
+        // the tiles past nt in the last group are masked and read list row 0.
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
+        using S3 = std::integral_constant<int, 3>;
+        using Pf = std::true_type;
+        using NoPf = std::false_type;
+        auto group = [&](int t0, auto pf) {
+            body(t0, S0{}, pf);
+            body(t0 + 1, S1{}, pf);
+            if constexpr (kPF == 4) {
+                body(t0 + 2, S2{}, pf);
+                body(t0 + 3, S3{}, pf);
+            }
+        };
+        static_assert(kPF == 2 || kPF == 4, "two or four tile slots");
+        load(0, S0{});
+        load(1, S1{});
+        if constexpr (kPF == 4) {
+            load(2, S2{});
+            load(3, S3{});
         }
+        const int ng = (nt + kPF - 1) / kPF;
+        for (int g = 0; g + 1 < ng; ++g) group(g * kPF, Pf{});
+        group((ng - 1) * kPF, NoPf{});
     }
     // sum over the four lane groups (different tokens, shared max)
     l_own += xor16(l_own);
@@ -338,26 +425,27 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     for (int g = 0; g < G; ++g)
         if (lg == g / 4) {
 #pragma unroll
-            for (int d = 0; d < 8; ++d) s_acc[wave][g][d * 16 + ln] = acc[d][g % 4];
+            for (int d = 0; d < 8; ++d) s_acc[(wave * G + g) * 128 + d * 16 + ln] = acc[d][g % 4];
         }
     if (lg == 0 && ln < G) {
-        s_ml[wave][ln][0] = m_own;
-        s_ml[wave][ln][1] = l_own;
+        s_ml[(wave * G + ln) * 2 + 0] = m_own;
+        s_ml[(wave * G + ln) * 2 + 1] = l_own;
     }
     __syncthreads();
-    // block partial (waves merged in order)
-    const int64_t pbase = static_cast<int64_t>(h) * a.nsplit + split;
-    for (int o = tid; o < G * 128; o += 64 * kWaves) {
+    // workgroup partial (waves merged in order); an empty split writes an
+    // empty state (max -inf, sum 0), which the merge weighs 0
+    const int64_t pbase = static_cast<int64_t>(h) * a.S + split;
+    for (int o = tid; o < G * 128; o += kThreads) {
         const int g = o >> 7, d = o & 127;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_ml[w][g][0]);
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_ml[(w * G + g) * 2]);
         float L = 0.0f, A = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            const float wt = wexp(s_ml[w][g][0], M);
-            L += s_ml[w][g][1] * wt;
-            A += s_acc[w][g][d] * wt;
+            const float wt = wexp(s_ml[(w * G + g) * 2], M);
+            L += s_ml[(w * G + g) * 2 + 1] * wt;
+            A += s_acc[(w * G + g) * 128 + d] * wt;
         }
         a.part_acc[(pbase * G + g) * 128 + d] = A;
         if (d == 0) {
@@ -367,15 +455,13 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))
     }
 }
 
-// Merge of the partials of one head for 64 outputs (query head
-// g = chunk / 2, dims (chunk % 2) * 64 ..).  Only splits that hold rows of
-// the head (ceil((static_len + n_rows) / rows_per_block)) take part.  Every
-// load of the first 64 splits (partial sums, and the max / sum pairs that
-// wave 0 turns into split weights) is issued before the row count is known,
-// so the common case needs one round trip.  Each of the four waves sums a
-// quarter of the splits (s = q, q + 4, ...); quarters are added in a fixed
-// order (deterministic).
-__global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
+// Merge of the S partials of one head for 64 outputs (query head g = chunk
+// / 2, dims (chunk % 2) * 64 ..).  Every load of the first 64 splits
+// (partial sums, and the max / sum pairs that wave 0 turns into split
+// weights) is issued at once; each of the four waves sums a quarter of the
+// splits (s = q, q + 4, ...) and the quarters are added in a fixed order
+// (deterministic).
+__global__ __launch_bounds__(256) void merge_kernel(DecParams a, int G) {
     __shared__ float s_w[kMaxSplit];
     __shared__ float s_red[4][64];
     __shared__ float s_ML[2];
@@ -383,29 +469,27 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
     const int g = chunk >> 1;
     const int tid = threadIdx.x, q = tid >> 6, lane = tid & 63;
     const int o = chunk * 64 + lane;  // g * 128 + d
-    const int nsm = a.nsplit;
+    const int ns = a.S;
     const int64_t stride = static_cast<int64_t>(G) * 128;
-    const float* pacc = a.part_acc + static_cast<int64_t>(h) * nsm * stride + o;
-    const float* pml = a.part_ml + (static_cast<int64_t>(h) * nsm * G + g) * 2;
+    const float* pacc = a.part_acc + static_cast<int64_t>(h) * ns * stride + o;
+    const float* pml = a.part_ml + (static_cast<int64_t>(h) * ns * G + g) * 2;
     float v[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
         const int s = q + 4 * u;
-        v[u] = s < nsm ? pacc[s * stride] : 0.0f;
+        v[u] = s < ns ? pacc[s * stride] : 0.0f;
     }
-    float pm = -INFINITY, pl = 0.0f;
-    if (q == 0 && lane < nsm) {
-        pm = pml[static_cast<int64_t>(lane) * G * 2];
-        pl = pml[static_cast<int64_t>(lane) * G * 2 + 1];
-    }
-    const int rows = a.static_len + a.n_rows[h] + (a.delta_rows ? min(max(a.n_delta[h], 0), a.delta_cap) : 0);
-    const int ns = min(nsm, (rows + a.rows_per_block - 1) / a.rows_per_block);
     if (q == 0) {
-        float M = lane < ns ? pm : -INFINITY;
+        float pm = -INFINITY, pl = 0.0f;
+        if (lane < ns) {
+            pm = pml[static_cast<int64_t>(lane) * G * 2];
+            pl = pml[static_cast<int64_t>(lane) * G * 2 + 1];
+        }
+        float M = pm;
         for (int s = lane + 64; s < ns; s += 64) M = fmaxf(M, pml[static_cast<int64_t>(s) * G * 2]);
         M = wave_max(M);
-        float w = lane < ns ? wexp(pm, M) : 0.0f;
-        if (lane < nsm) s_w[lane] = w;
+        const float w = lane < ns ? wexp(pm, M) : 0.0f;
+        if (lane < ns) s_w[lane] = w;
         float L = pl * w;
         for (int s = lane + 64; s < ns; s += 64) {
             const float ws = wexp(pml[static_cast<int64_t>(s) * G * 2], M);
@@ -419,11 +503,11 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
         }
     }
     __syncthreads();
-    float acc = 0.0f;
+    float accv = 0.0f;
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
         const int s = q + 4 * u;
-        if (s < ns) acc = __builtin_fmaf(v[u], s_w[s], acc);
+        if (s < ns) accv = __builtin_fmaf(v[u], s_w[s], accv);
     }
     for (int s0 = q + 64; s0 < ns; s0 += 64) {
 #pragma unroll
@@ -434,10 +518,10 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
             const int s = s0 + 4 * u;
-            if (s < ns) acc = __builtin_fmaf(v[u], s_w[s], acc);
+            if (s < ns) accv = __builtin_fmaf(v[u], s_w[s], accv);
         }
     }
-    s_red[q][lane] = acc;
+    s_red[q][lane] = accv;
     __syncthreads();
     if (q == 0) {
         const float A = ((s_red[0][lane] + s_red[1][lane]) + s_red[2][lane]) + s_red[3][lane];
@@ -449,57 +533,34 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams a, int G) {
     }
 }
 
-// Rows the workspace and the tile size are fixed for: any static_len up to
-// steady_stride, so one workspace (and one captured launch shape) stays valid
-// while the steady zone grows.
+// Rows one split may hold for any call of this shape: any static_len up to
+// steady_stride (so one workspace and one captured launch shape stay valid
+// while the steady zone grows), the selected rows, the delta rows.
 int64_t rows_bound(const imi_attention_args* a) {
     const int64_t srows = a->steady_stride > a->static_len ? a->steady_stride : a->static_len;
     return srows + a->max_rows;
 }
 
-// Tiles per wave: the fewest (1..8) whose grid still fits on the CUs in one
-// round, so that every CU streams and each workgroup's share is as short as
-// possible (at 128k, H = 8: 7 tiles, 240 workgroups, 15.7 us vs 15.9 us with
-// 8 tiles and 208 workgroups).  When no grid fits, the one (4..8 tiles, so
-// that each wave's ramp stays amortised) whose busiest CU streams the fewest
-// rows: workgroups per CU x rows per workgroup.
-int tiles_per_wave(const imi_attention_args* a) {
-    const int64_t rows = rows_bound(a);
+// Splits per head: about one workgroup per CU in all, and enough that no
+// split holds more than kLocCap rows.
+int splits_per_head(const imi_attention_args* a) {
     const int64_t cus = device_cus();
-    for (int nt = 1; nt < 8; ++nt) {
-        const int64_t rpb = 64 * nt;
-        if (a->kv_heads * ((rows + rpb - 1) / rpb) <= cus) return nt;
-    }
-    int best = 8;
-    int64_t best_load = INT64_MAX;
-    for (int nt = 8; nt >= 4; --nt) {
-        const int64_t rpb = 64 * nt;
-        const int64_t wgs = a->kv_heads * ((rows + rpb - 1) / rpb);
-        const int64_t load = (wgs + cus - 1) / cus * rpb;
-        if (load < best_load) {
-            best_load = load;
-            best = nt;
-        }
-    }
-    return best;
+    int64_t s = (cus + a->kv_heads - 1) / a->kv_heads;
+    const int64_t need = (rows_bound(a) + kLocCap - 1) / kLocCap;
+    if (s < need) s = need;
+    if (s < 1) s = 1;
+    return static_cast<int>(s);
 }
 
-int nsplit_bound(const imi_attention_args* a) {
-    const int64_t rpb = 64 * tiles_per_wave(a);
-    const int64_t rows = rows_bound(a);
-    return rows <= 0 ? 1 : static_cast<int>((rows + rpb - 1) / rpb);
-}
-
-size_t attn_workspace(const imi_attention_args* a, AttnParams* p) {
-    const int nsplit = nsplit_bound(a);
+size_t attn_workspace(const imi_attention_args* a, DecParams* p) {
+    const int S = splits_per_head(a);
     Carver cv(a->workspace);
-    float* acc = cv.take<float>(static_cast<size_t>(a->kv_heads) * nsplit * a->groups * 128);
-    float* ml = cv.take<float>(static_cast<size_t>(a->kv_heads) * nsplit * a->groups * 2);
+    float* acc = cv.take<float>(static_cast<size_t>(a->kv_heads) * S * a->groups * 128);
+    float* ml = cv.take<float>(static_cast<size_t>(a->kv_heads) * S * a->groups * 2);
     if (p) {
         p->part_acc = acc;
         p->part_ml = ml;
-        p->nsplit = nsplit;
-        p->rows_per_block = 64 * tiles_per_wave(a);
+        p->S = S;
     }
     return cv.used();
 }
@@ -516,7 +577,8 @@ int attn_validate(const imi_attention_args* a, bool need_sel) {
                 static_cast<long long>(a->steady_stride));
     IMI_REQUIRE(a->static_len == 0 || (a->steady_keys && a->steady_values), IMI_ERR_INVALID,
                 "imi_sparse_attention: null steady zone");
-    IMI_REQUIRE(a->list_keys && a->list_values, IMI_ERR_INVALID, "imi_sparse_attention: null list");
+    IMI_REQUIRE(a->list_keys && a->list_values && a->list_rows > 0, IMI_ERR_INVALID,
+                "imi_sparse_attention: null or empty list");
     IMI_REQUIRE(a->max_rows >= 0, IMI_ERR_INVALID, "imi_sparse_attention: max_rows must be >= 0");
     if (need_sel)
         IMI_REQUIRE(a->n_rows != nullptr, IMI_ERR_INVALID, "imi_sparse_attention: null n_rows");
@@ -530,82 +592,91 @@ int attn_validate(const imi_attention_args* a, bool need_sel) {
         if (need_sel)
             IMI_REQUIRE(a->n_delta != nullptr, IMI_ERR_INVALID, "imi_sparse_attention: null n_delta");
     }
-    IMI_REQUIRE(a->sel_cap >= 0 && a->sel_cap <= kSelCapMax, IMI_ERR_UNSUPPORTED,
-                "imi_sparse_attention: sel_cap %d exceeds %d", a->sel_cap, kSelCapMax);
-    IMI_REQUIRE(nsplit_bound(a) <= kMaxSplit, IMI_ERR_UNSUPPORTED,
-                "imi_sparse_attention: %d rows need more than %d splits per head", a->static_len + a->max_rows,
-                kMaxSplit);
+    IMI_REQUIRE(a->sel_cap >= 0, IMI_ERR_INVALID, "imi_sparse_attention: sel_cap must be >= 0");
+    IMI_REQUIRE(a->sel_cap <= kStageMax, IMI_ERR_UNSUPPORTED, "imi_sparse_attention: sel_cap %d above %d",
+                a->sel_cap, kStageMax);
+    IMI_REQUIRE(splits_per_head(a) <= kMaxSplit, IMI_ERR_UNSUPPORTED,
+                "imi_sparse_attention: %lld rows need more than %d splits per head",
+                static_cast<long long>(rows_bound(a)), kMaxSplit);
     return IMI_OK;
 }
 
-template <int G, bool DELTA>
-void launch_gd(const AttnParams& p, int blocks, hipStream_t stream) {
-#define IMI_ATT_CASE(N) \
-    case N: hipLaunchKernelGGL((attention_kernel<G, N, DELTA>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
-    switch (p.rows_per_block / 64) {
-        IMI_ATT_CASE(8)
-        IMI_ATT_CASE(7)
-        IMI_ATT_CASE(6)
-        IMI_ATT_CASE(5)
-        IMI_ATT_CASE(4)
-        IMI_ATT_CASE(3)
-        IMI_ATT_CASE(2)
-        default: hipLaunchKernelGGL((attention_kernel<G, 1, DELTA>), dim3(blocks), dim3(64 * kWaves), 0, stream, p); break;
-    }
-#undef IMI_ATT_CASE
+void fill_common(const imi_attention_args* a, DecParams* p) {
+    p->q = a->query;
+    p->sk = a->steady_keys ? a->steady_keys : a->list_keys;   // never read when static_len = 0 and no delta rows
+    p->sv = a->steady_values ? a->steady_values : a->list_values;
+    p->s_stride = a->steady_keys ? a->steady_stride : 1;
+    p->static_len = a->static_len;
+    p->lk = a->list_keys;
+    p->lv = a->list_values;
+    p->list_rows = a->list_rows;
+    p->H = a->kv_heads;
+    p->scale_log2 = a->scale * 1.44269504088896340736f;
+    p->out = a->out;
+    p->lse = a->out_lse;
+}
+
+// Words of the staged selection's region: the row prefix (cap + 1, padded
+// to 4 words) and the offsets, or the two K / V tiles if those are larger.
+int stage_obase(int cap) { return (cap + 1 + 3) & ~3; }
+int stage_words(int cap) {
+    const int w = stage_obase(cap) + ((cap + 3) & ~3);
+    return w > kTileWords ? w : kTileWords;
 }
 
 template <int G>
-void launch_g(const AttnParams& p, int blocks, hipStream_t stream) {
-    if (p.delta_rows)
-        launch_gd<G, true>(p, blocks, stream);
-    else
-        launch_gd<G, false>(p, blocks, stream);
+int launch_att(const DecParams& p, hipStream_t stream) {
+    const size_t lds = static_cast<size_t>(p.stage_words + tail_words<G>()) * 4;
+    static bool attr_set = false;
+    if (!attr_set) {
+        constexpr size_t lds_max = static_cast<size_t>(2 * (kStageMax + 4) + tail_words<G>()) * 4;
+        static_assert(lds_max <= 160 * 1024, "LDS of one workgroup");
+        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<G>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_max)));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((attention_kernel<G>), dim3(p.H * p.S), dim3(kThreads), lds, stream, p);
+    IMI_LAUNCH_CHECK("attention_kernel");
+    return IMI_OK;
 }
 
 // kernels: bit 0 the split pass, bit 1 the merge (which reads the partials
 // the last split pass left in the workspace).
-int attn_launch(const imi_attention_args* a, hipStream_t stream, int kernels = 3) {
-    AttnParams p;
-    attn_workspace(a, &p);
-    p.q = a->query;
-    p.sk = a->steady_keys;
-    p.sv = a->steady_values;
-    p.s_stride = a->steady_stride;
-    p.static_len = a->static_len;
-    p.lk = a->list_keys;
-    p.lv = a->list_values;
-    p.list_rows = a->list_rows;
-    p.sel_offset = a->sel_offset;
-    p.sel_prefix = a->sel_prefix;
-    p.n_selected = a->n_selected;
-    p.sel_cap = a->sel_cap;
-    p.n_rows = a->n_rows;
-    p.delta_rows = a->delta_rows;
-    p.n_delta = a->n_delta;
-    p.delta_cap = a->delta_cap;
-    p.H = a->kv_heads;
-    p.scale_log2 = a->scale * 1.44269504088896340736f;
-    p.out = a->out;
-    p.lse = a->out_lse;
-    const int64_t rows = static_cast<int64_t>(a->static_len) + a->max_rows;
-    const int splits = rows <= 0 ? 1 : static_cast<int>((rows + p.rows_per_block - 1) / p.rows_per_block);
-    const int blocks = a->kv_heads * splits;
+int attn_run(const DecParams& p, int groups, hipStream_t stream, int kernels) {
+    int rc = IMI_OK;
     if (kernels & 1) {
-        switch (a->groups) {
-            case 1: launch_g<1>(p, blocks, stream); break;
-            case 2: launch_g<2>(p, blocks, stream); break;
-            case 4: launch_g<4>(p, blocks, stream); break;
-            case 7: launch_g<7>(p, blocks, stream); break;
-            default: launch_g<8>(p, blocks, stream); break;
+        switch (groups) {
+            case 1: rc = launch_att<1>(p, stream); break;
+            case 2: rc = launch_att<2>(p, stream); break;
+            case 4: rc = launch_att<4>(p, stream); break;
+            case 7: rc = launch_att<7>(p, stream); break;
+            default: rc = launch_att<8>(p, stream); break;
         }
-        IMI_LAUNCH_CHECK("attention_kernel");
+        if (rc) return rc;
     }
     if (kernels & 2) {
-        hipLaunchKernelGGL(merge_kernel, dim3(2 * a->groups, a->kv_heads), dim3(256), 0, stream, p, a->groups);
+        hipLaunchKernelGGL(merge_kernel, dim3(2 * groups, p.H), dim3(256), 0, stream, p, groups);
         IMI_LAUNCH_CHECK("merge_kernel");
     }
     return IMI_OK;
+}
+
+// Attention over a selection held in global memory.
+int attn_launch_given(const imi_attention_args* a, hipStream_t stream, int kernels) {
+    DecParams p{};
+    attn_workspace(a, &p);
+    fill_common(a, &p);
+    p.g_prefix = a->sel_prefix;
+    p.g_offset = a->sel_offset;
+    p.g_nsel = a->n_selected;
+    p.g_nrows = a->n_rows;
+    p.g_cap = a->sel_cap;
+    p.g_drows = a->delta_rows;
+    p.g_ndelta = a->n_delta;
+    p.g_dcap = a->delta_cap;
+    p.o_base = stage_obase(a->sel_cap);
+    p.stage_words = stage_words(a->sel_cap);
+    return attn_run(p, a->groups, stream, kernels);
 }
 
 }  // namespace
@@ -636,18 +707,19 @@ extern "C" int imi_sparse_attention(const imi_attention_args* a, imi_stream_t st
     if (rc) return rc;
     IMI_REQUIRE(a->workspace && a->workspace_bytes >= need, IMI_ERR_WORKSPACE,
                 "imi_sparse_attention: workspace %zu bytes < %zu required", a->workspace_bytes, need);
-    return attn_launch(a, stream);
+    return attn_launch_given(a, stream, 3);
 }
 
 namespace {
 struct DecodeLayout {
     int32_t *cell, *off, *cnt, *prefix, *nsel, *nrows;
     int32_t *drows, *ndelta;   // delta append outputs (ring_cap > 0)
-    char* sel_ws;            // 4-way selection scratch (empty for 2-way)
+    uint32_t* keys;            // 2-way score keys [H][npad]
+    char* sel_ws;              // 4-way selection scratch (empty for 2-way)
     size_t sel_bytes;
     char* attn_ws;
     size_t attn_bytes;
-    char* zero_at;           // the words the kernels expect zero at the start of a call
+    char* zero_at;             // the words the kernels expect zero at the start of a call
     size_t zero_bytes;
     size_t total;
 };
@@ -665,6 +737,7 @@ DecodeLayout decode_layout(const imi_decode_args* a, void* ws) {
     const int rc = a->sel.ring_cap > 0 ? a->sel.ring_cap : 0;
     L.drows = cv.take<int32_t>(static_cast<size_t>(H) * (rc > 0 ? rc : 1));
     L.ndelta = cv.take<int32_t>(H);
+    L.keys = a->sel.parts == 2 ? cv.take<uint32_t>(sel2_keys_bytes(&a->sel) / sizeof(uint32_t)) : nullptr;
     L.sel_bytes = a->sel.parts == 4 ? select4_workspace_size(&a->sel) : 0;
     L.sel_ws = cv.take<char>(L.sel_bytes > 0 ? L.sel_bytes : 1);
     L.zero_bytes = a->sel.parts == 4 ? select4_zero_bytes() : 0;
@@ -693,6 +766,12 @@ int decode_validate(const imi_decode_args* a) {
                               (a->sel.ring_cap > 0 ? a->sel.ring_cap : 0);
     IMI_REQUIRE(a->attn.max_rows >= need_rows, IMI_ERR_INVALID, "imi_decode_step: max_rows %d < %lld selectable rows",
                 a->attn.max_rows, static_cast<long long>(need_rows));
+    IMI_REQUIRE(a->sel.sel_cap <= kStageMax, IMI_ERR_UNSUPPORTED, "imi_decode_step: sel_cap %d above %d",
+                a->sel.sel_cap, kStageMax);
+    int64_t nc;
+    int km;
+    int rc = select_validate(&a->sel, nc, km);
+    if (rc) return rc;
     return attn_validate(&a->attn, false);
 }
 }  // namespace
@@ -707,9 +786,11 @@ extern "C" int imi_decode_workspace_size(const imi_decode_args* a, size_t* bytes
 }
 
 namespace {
-// One decode step with its workspace at ws (already checked to be large enough).
+// One decode step with its workspace at ws (already checked to be large
+// enough): imi_select's kernels -> attention_kernel (given selection) ->
+// merge_kernel.  phases (bits): 1 the selection, 4 attention_kernel, 8
+// merge_kernel, 2 both of those.
 int decode_run(const imi_decode_args* a, void* ws, hipStream_t stream) {
-    int rc;
     const DecodeLayout L = decode_layout(a, ws);
     IMI_REQUIRE(a->phases >= 0 && a->phases < 16, IMI_ERR_INVALID, "imi_decode_step: phases %d outside [0, 15]",
                 a->phases);
@@ -726,21 +807,21 @@ int decode_run(const imi_decode_args* a, void* ws, hipStream_t stream) {
         if (!s.delta_rows) s.delta_rows = L.drows;
         if (!s.n_delta) s.n_delta = L.ndelta;
     }
-    if (s.parts == 4 && !s.workspace) {
+    if (s.parts == 4) {
         s.workspace = L.sel_ws;
         s.workspace_bytes = L.sel_bytes;
+    } else {
+        s.workspace = L.keys;
+        s.workspace_bytes = sel2_keys_bytes(&s);
     }
     if (phases & 1) {
-        rc = select_launch(&s, stream);
-        if (rc) return rc;
-    } else {
-        int64_t nc;
-        int km;
-        rc = select_validate(&s, nc, km);
+        const int rc = select_launch(&s, stream);
         if (rc) return rc;
     }
     if (!kernels) return IMI_OK;
     imi_attention_args t = a->attn;
+    t.workspace = L.attn_ws;
+    t.workspace_bytes = L.attn_bytes;
     t.sel_offset = s.sel_offset;
     t.sel_count = s.sel_count;
     t.sel_prefix = s.sel_prefix;
@@ -750,9 +831,7 @@ int decode_run(const imi_decode_args* a, void* ws, hipStream_t stream) {
     t.delta_rows = s.ring_cap > 0 ? s.delta_rows : nullptr;
     t.n_delta = s.ring_cap > 0 ? s.n_delta : nullptr;
     t.delta_cap = s.ring_cap > 0 ? s.ring_cap : 0;
-    t.workspace = L.attn_ws;
-    t.workspace_bytes = L.attn_bytes;
-    return attn_launch(&t, stream, kernels);
+    return attn_launch_given(&t, stream, kernels);
 }
 }  // namespace
 

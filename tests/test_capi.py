@@ -102,16 +102,21 @@ def test_select_and_decode_argument_checks(L):
     assert L.imi_select_workspace_size(ctypes.byref(s), ctypes.byref(need)) == 0 and need.value > 0
     assert L.imi_select(ctypes.byref(s), None) == 4          # no workspace given
     assert "workspace" in L.imi_last_error().decode()
-    s.parts = 2
+    s.parts = 2   # 2-way within the one-kernel bounds (k <= 128, K' <= 2048): no workspace
     assert L.imi_select_workspace_size(ctypes.byref(s), ctypes.byref(need)) == 0 and need.value == 0
+    s.k[0], s.nprobe, s.buffer_pages = 200, 3000, 3000   # beyond them: one score key per cell, padded to 1024
+    s.sel_cap = 3000
+    assert L.imi_select_workspace_size(ctypes.byref(s), ctypes.byref(need)) == 0
+    assert need.value == 8 * 16 * 1024 * 4   # 12800 cells: 13 blocks, padded to 16
+    s.k[0], s.nprobe, s.buffer_pages, s.sel_cap = 64, 410, 410, 410
     s.sel_cap = 100
     assert L.imi_select(ctypes.byref(s), None) == 1
     assert "sel_cap" in L.imi_last_error().decode()
     d = DecodeArgs()
     d.sel = s
     d.sel.sel_cap = 410
-    d.attn = AttentionArgs(query=16, out=16, list_keys=16, list_values=16, kv_heads=8, groups=4, dim=128,
-                           max_rows=100)
+    d.attn = AttentionArgs(query=16, out=16, list_keys=16, list_values=16, list_rows=4096, kv_heads=8, groups=4,
+                           dim=128, max_rows=100)
     need = ctypes.c_size_t()
     assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == 1
     assert "max_rows" in L.imi_last_error().decode()
@@ -170,8 +175,8 @@ def test_online_update_argument_checks(L):
     s.upd_slot = None
     d = DecodeArgs()
     d.sel = s
-    d.attn = AttentionArgs(query=16, out=16, list_keys=16, list_values=16, kv_heads=8, groups=4, dim=128,
-                           max_rows=300 * 8, steady_keys=16, steady_values=16, steady_stride=200)
+    d.attn = AttentionArgs(query=16, out=16, list_keys=16, list_values=16, list_rows=4096, kv_heads=8, groups=4,
+                           dim=128, max_rows=300 * 8, steady_keys=16, steady_values=16, steady_stride=200)
     assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == 1   # max_rows misses the ring
     assert "max_rows" in L.imi_last_error().decode()
     d.attn.max_rows = 300 * 8 + 512
@@ -193,13 +198,13 @@ def test_noalloc_rejects_shapes_beyond_its_scratch(L):
     (64 MiB) before touching the device."""
     from adaptiveimi_amd._lib import AttentionArgs, DecodeArgs, SelectArgs
 
-    s = SelectArgs(query=16, centroids=16, cell_count=16, cell_offset=16, kv_heads=4096, groups=4, dim=128, parts=2,
+    s = SelectArgs(query=16, centroids=16, cell_count=16, cell_offset=16, kv_heads=16384, groups=4, dim=128, parts=2,
                    nprobe=410, max_tokens=3276, buffer_pages=410, page_size=8, sel_cap=410)
     s.k[0] = s.k[1] = 64
     d = DecodeArgs()
     d.sel = s
-    d.attn = AttentionArgs(query=16, out=16, list_keys=16, list_values=16, kv_heads=4096, groups=4, dim=128,
-                           max_rows=410 * 8, steady_stride=512)
+    d.attn = AttentionArgs(query=16, out=16, list_keys=16, list_values=16, list_rows=4096, kv_heads=16384, groups=4,
+                           dim=128, max_rows=410 * 8, steady_stride=512)
     need = ctypes.c_size_t()
     assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == 0
     assert need.value > 64 << 20

@@ -292,7 +292,10 @@ def test_similarities_bit_exact(ops, oracle):
     (20000, (45, 45), 0.05, 8, 3),
     (60000, (128, 128), 0.02, 4, 4),     # configs[4]'s 2 x 128 centroids: 16 cells per thread
     (30000, (100, 90), 0.05, 4, 5),
-    (32768, (64, 64), 0.5, 4, 6),        # nprobe = buffer_pages = 2048: the ranking capacity
+    (32768, (64, 64), 0.5, 4, 6),        # nprobe = buffer_pages = 2048: the one-kernel ranking capacity
+    (60000, (256, 64), 0.05, 4, 7),      # k0 = 256: score + rank kernels
+    (100000, (128, 128), 0.2, 4, 8),     # K' = 2500 pages > 2048: score + rank kernels
+    (50000, (200, 80), 0.3, 8, 9),       # 16000 cells, K' = 4096 nprobe < 4688 pages
 ])
 def test_select_bit_exact(ops, oracle, T, ks, budget, G, seed):
     note(f"[select] T={T} ks={ks} budget={budget} G={G}")
@@ -478,16 +481,19 @@ def _check_attention(out, ref):
     assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)), float(err.max())
 
 
-@pytest.mark.parametrize("T,ks,G,static_len,tiles", [(32768, (64, 64), 4, 96, False), (9000, (32, 32), 7, 0, False),
-                                                      (6000, (32, 32), 8, 200, False), (20000, (32, 32), 4, 96, True)])
-def test_decode_step_matches_oracle(ops, oracle, T, ks, G, static_len, tiles):
-    note(f"[decode] T={T} ks={ks} G={G} static={static_len} tiles={tiles}")
+@pytest.mark.parametrize("T,ks,G,static_len,tiles,budget", [
+    (32768, (64, 64), 4, 96, False, 0.1), (9000, (32, 32), 7, 0, False, 0.1), (6000, (32, 32), 8, 200, False, 0.1),
+    (20000, (32, 32), 4, 96, True, 0.1),
+    (100000, (128, 128), 4, 96, False, 0.2),   # score + rank kernels; over 2048 selected cells per head
+])
+def test_decode_step_matches_oracle(ops, oracle, T, ks, G, static_len, tiles, budget):
+    note(f"[decode] T={T} ks={ks} G={G} static={static_len} tiles={tiles} budget={budget}")
     H = 8
     keys, values, cent, out = _index(ops, H, T, ks, 300 + G)
     from adaptiveimi_amd import synthetic
 
     sk, sv = synthetic.make_kv(H, max(static_len, 1) + 8, seed=77)
-    sz = oracle.sizing(T, 0.1, k_override=ks)
+    sz = oracle.sizing(T, budget, k_override=ks)
     # tile mode: a small page budget, so that the tiles (and the oversized-cell stop) matter
     bud = ops.Budget(sz["nprobe"], sz["max_tokens"], 12 if tiles else sz["buffer_pages"], tile_mode=tiles)
     plan = ops.DecodePlan(cent, out["cell_count"], out["cell_offset"], ks, bud, out["list_keys"],
@@ -510,6 +516,8 @@ def test_decode_step_matches_oracle(ops, oracle, T, ks, G, static_len, tiles):
     assert np.array_equal(sel["n_selected"].cpu().numpy(), rm)
     if tiles:   # more rows than one page budget holds
         assert int(sel["n_rows"].max()) > bud.buffer_pages * bud.page_size
+    if budget > 0.1:   # the attention prologue stages its selection in more than one round trip
+        assert int(sel["n_selected"].max()) > 2048
     _check_attention(res, ref)
 
 
@@ -582,12 +590,15 @@ def test_ragged_batch_decode_matches_oracle(ops, oracle, ks):
         assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)), (s_, float(err.max()))
 
 
-@pytest.mark.parametrize("L,cap,span", [(3000, 40, 50), (150000, 1400, 100)])
-def test_attention_standalone_and_lse(ops, oracle, L, cap, span):
+@pytest.mark.parametrize("L,cap,span,holes", [(3000, 40, 50, False), (150000, 1400, 100, False),
+                                              (150000, 6000, 20, False), (20000, 300, 50, True)])
+def test_attention_standalone_and_lse(ops, oracle, L, cap, span, holes):
     """imi_sparse_attention with a caller-made selection, and the LSE output.
-    The large case gives heads of 35k-70k rows, i.e. 70-140 splits: the
-    merge's first batch of partials, then chunks of 64 split weights."""
-    note(f"[attention] standalone L={L} cap={cap}")
+    The 1400-cell case gives heads of 35k-70k rows, i.e. 70-140 splits: the
+    merge's first batch of partials, then chunks of 64 split weights.  The
+    6000-cell case selects more cells than the prologue's first round trip
+    stages (2048); holes: every third selected cell holds no rows."""
+    note(f"[attention] standalone L={L} cap={cap} holes={holes}")
     H, G = 4, 4
     from adaptiveimi_amd import synthetic
 
@@ -603,6 +614,8 @@ def test_attention_standalone_and_lse(ops, oracle, L, cap, span):
         m = int(rng.integers(0, cap)) if cap < 100 else int(rng.integers(cap // 2, cap))
         starts = np.sort(rng.choice(L // span, m, replace=False)) * span
         c = rng.integers(1, span, m)
+        if holes:
+            c[::3] = 0
         offs[h, :m], cnts[h, :m] = starts, c
         pref[h, 1 : m + 1] = np.cumsum(c)
         nsel[h] = m
@@ -731,7 +744,8 @@ def test_select_refinement_paths(ops, oracle, case):
     q = synthetic.make_queries(keys, 4, seed=3)[0]
     if case == "zero_query":
         q.zero_()
-    for bud in (ops.Budget(102, 1200, 150), ops.Budget(400, 5000, 800)):
+    # the third budget ranks 3000 cells: the score + rank kernels
+    for bud in (ops.Budget(102, 1200, 150), ops.Budget(400, 5000, 800), ops.Budget(3000, 11000, 3000)):
         sel = ops.select(q.to(DEV), cent, out["cell_count"], out["cell_offset"], ks, bud)
         sc = oracle.scores(bits(q), out["compact_centroids"].cpu().numpy())
         rs, rm, rtok = oracle.select(sc, out["compact_size"].cpu().numpy(), out["compact_mask"].cpu().numpy(),
