@@ -32,7 +32,7 @@ from __future__ import annotations
 
 import math
 import os
-from typing import Dict, List, Optional
+from typing import Dict, List, Optional, Sequence
 
 import torch
 
@@ -213,6 +213,22 @@ class adpimi_cache:  # noqa: N801  (reference class name)
             return ks
         return adaptive_k(n_tokens, int(cfg.get("target_cluster_size", 16)), self.subspace_parts)
 
+    def _decode_budget(self, ks: Sequence[int]) -> Dict[str, int]:
+        """runtime.py:31-63 with this cache's list capacity and budget."""
+        names = ("k1", "k2") if self.subspace_parts == 2 else ("k1", "k2", "k3", "k4")
+        explicit = all(int(self.runtime_config["kmeans"].get(n, 0) or 0) > 0 for n in names)
+        return decode_sizing(self.list_capacity, self.retrieval_budget, self.subspace_parts, self.buffer_cluster_num,
+                             self.page_size, k_override=ks if explicit else None)
+
+    def _check_decode_limits(self, ks: Sequence[int]) -> None:
+        """Fail before the index build, not at the first decode step, when the
+        selection kernels cannot rank this shape (e.g. too many cells to
+        rank for the 4-way path)."""
+        sz = self._decode_budget(ks)
+        tiles = int(os.getenv("IMI_MAX_TILES", "0") or 0) != 0
+        bud = ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"], self.page_size, tile_mode=tiles)
+        ops.check_decode_limits(self.batch_groups, self.group_size, ks, bud, online=self.async_update_enabled)
+
     def _build_layer_index(self, layer_idx: int, middle_k: torch.Tensor, middle_v: torch.Tensor) -> None:
         """k-means + reorganisation of one layer's middle keys ([H, T, D]
         strided views of the prefill tensors; nothing is copied first)."""
@@ -221,6 +237,7 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         ks = self._layer_ks(T)
         if T < max(ks) and cfg["init"] == "first":
             raise ValueError(f"IMI layer {layer_idx}: {T} middle tokens < k = {max(ks)} (first-k initialisation)")
+        self._check_decode_limits(ks)
         km_kw = dict(tol=float(cfg["tol"]), early_stop_min_iter=int(cfg["early_stop_min_iter"]),
                      early_stop_rel_tol=float(cfg["early_stop_rel_tol"]), init=str(cfg["init"]))
         sample = int(cfg.get("sample_keys", 0) or 0)
@@ -348,10 +365,8 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         ks = next((k for k in self.layer_ks if k is not None), None)
         if ks is None:
             raise RuntimeError("prepare_cache: no layer index has been built")
-        names = ("k1", "k2") if self.subspace_parts == 2 else ("k1", "k2", "k3", "k4")
-        explicit = all(int(self.runtime_config["kmeans"].get(n, 0) or 0) > 0 for n in names)
-        sz = decode_sizing(self.list_capacity, self.retrieval_budget, self.subspace_parts, self.buffer_cluster_num,
-                           self.page_size, k_override=ks if explicit else None)
+        sz = self._decode_budget(ks)
+        self._check_decode_limits(ks)
         self.n_centroids = sz["n_centroids"]
         self.padding_cluster_id = sz["padding_cluster_id"]
         self.nprobe = sz["nprobe"]
@@ -479,7 +494,11 @@ class adpimi_cache:  # noqa: N801  (reference class name)
             "ideal_clusters_total": float(ideal_total),
             "non_empty_clusters_total": int(non_empty),
             "non_empty_ratio": float(non_empty) / float(ideal_total) if ideal_total > 0 else 0.0,
-            "total_centroid_bytes_gpu": int(sum(c.numel() * 4 for c in self.centroids if c is not None)),
+            # indexing.py:333-334: padded merged centroids (n_centroids x head_dim fp32 per KV head) per ready
+            # layer, the metadata the reference keeps on the GPU; the decode kernels here read the
+            # subspace centroids instead (subspace_centroid_bytes_gpu)
+            "total_centroid_bytes_gpu": int(ready * self.batch_groups * self.n_centroids * self.head_dim * 4),
+            "subspace_centroid_bytes_gpu": int(sum(c.numel() * 4 for c in self.centroids if c is not None)),
         }
 
     def can_reuse_for_next_sequence(self, valid_start, max_new_length: int, input_length: int) -> bool:

@@ -132,8 +132,10 @@ __device__ __forceinline__ int kprime(const Sel4& a, int h, int na) {
     return kp < na ? kp : na;
 }
 
-// Cell-id digits: POW2 (every k a power of two, as in every configuration)
-// takes shifts and masks instead of integer divisions.
+// Cell-id digits: POW2 (every k a power of two, as when a runtime config
+// sets k explicitly, e.g. 4 x 32; the adaptive k of
+// layer_pipeline.cpp:177-228 usually is not, e.g. 7, 10, 11 or 13 for
+// 32k-512k tokens) takes shifts and masks instead of integer divisions.
 template <bool POW2>
 __device__ __forceinline__ uint32_t kdiv(uint32_t g, uint32_t k) {
     return POW2 ? g >> __builtin_ctz(k) : g / k;

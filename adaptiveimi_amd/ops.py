@@ -408,6 +408,32 @@ class OnlineUpdate:
         s.exec_rows = int(exec_rows)
 
 
+def check_decode_limits(kv_heads: int, groups: int, ks: Sequence[int], budget: Budget,
+                        online: bool = False) -> None:
+    """Raise IMIError now if the selection kernels cannot rank this shape
+    (cells per head, cells to rank, heads, groups), before any index is built:
+    imi_select_workspace_size validates the same limits a decode step would.
+    online: the delta match ranks all of nprobe (async update on)."""
+    ncells = 1
+    for k in ks:
+        ncells *= int(k)
+    a = SelectArgs(query=16, centroids=16, cell_count=16, cell_offset=16, kv_heads=int(kv_heads),
+                   groups=int(groups), dim=128, parts=len(ks), nprobe=budget.nprobe, max_tokens=budget.max_tokens,
+                   buffer_pages=budget.buffer_pages, page_size=budget.page_size,
+                   tile_mode=int(bool(budget.tile_mode)))
+    a.k = _ks(ks)
+    rank_all = online or budget.tile_mode
+    a.sel_cap = budget.nprobe if rank_all else min(budget.nprobe, budget.buffer_pages)
+    if online:
+        a.ring_cap, a.ring_cell, a.ring_row, a.ring_n, a.exec_rows = 1, 16, 16, 16, 0
+    if len(ks) == 4:
+        a.compact_gid = a.compact_size = a.compact_offset = a.n_active = 16
+        a.compact_cap = ncells + 1
+    need = ctypes.c_size_t()
+    check(_lib.lib().imi_select_workspace_size(ctypes.byref(a), ctypes.byref(need)),
+          f"decode selection for k={list(ks)}, nprobe={budget.nprobe}, buffer_pages={budget.buffer_pages}")
+
+
 def _sel_cap(budget: Budget, update: Optional[OnlineUpdate]) -> int:
     """Ranks the selection keeps: the delta match needs all of nprobe."""
     return max(budget.sel_cap, budget.nprobe) if update is not None else budget.sel_cap

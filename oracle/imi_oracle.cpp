@@ -117,6 +117,19 @@ float orc_estep(const float* data, int64_t n, int dim, const float* cent, int k,
     return inertia;
 }
 
+// Raw engine outputs (the first n after seeding): std::mt19937 and
+// std::mt19937_64, the engines of kmeans_core.cpp:150 and :293.  They let the
+// tests pin the engines against the outputs the C++ standard fixes
+// ([rand.predef]: the 10000th output of a default-seeded engine).
+void orc_mt32_outputs(uint32_t seed, int64_t n, uint32_t* out) {
+    std::mt19937 rng(seed);
+    for (int64_t i = 0; i < n; ++i) out[i] = static_cast<uint32_t>(rng());
+}
+void orc_mt64_outputs(uint64_t seed, int64_t n, uint64_t* out) {
+    std::mt19937_64 rng(seed);
+    for (int64_t i = 0; i < n; ++i) out[i] = rng();
+}
+
 // Uniform draws used by the empty-cluster reseed of iteration `iter`:
 // std::mt19937(iter + 12345) and uniform_int_distribution<int32_t>(0, n-1),
 // drawn once per empty cluster in ascending cluster order

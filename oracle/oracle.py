@@ -84,6 +84,10 @@ def lib():
                                  ctypes.c_int, ctypes.c_int, _i32p, _i32p, _i64p]
         L.orc_update_assign.restype = None
         L.orc_update_assign.argtypes = [_f32p, ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int, _i32p]
+        L.orc_mt32_outputs.restype = None
+        L.orc_mt32_outputs.argtypes = [ctypes.c_uint32, ctypes.c_int64, ctypes.POINTER(ctypes.c_uint32)]
+        L.orc_mt64_outputs.restype = None
+        L.orc_mt64_outputs.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.POINTER(ctypes.c_uint64)]
         L.orc_attention.restype = None
         L.orc_attention.argtypes = [_u16p, _u16p, _u16p, ctypes.c_int64, _i64p, _i32p, ctypes.c_int64,
                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_double, _f64p]
@@ -210,6 +214,18 @@ def mstep(data: np.ndarray, labels: np.ndarray, k: int, iteration: int, nthreads
 def reseed_draws(iteration: int, n: int, count: int) -> np.ndarray:
     out = np.empty(count, np.int32)
     lib().orc_reseed_draws(iteration, n, count, _p(out, _i32p))
+    return out
+
+
+def mt_outputs(seed: int, n: int, bits: int = 64) -> np.ndarray:
+    """The first n outputs of std::mt19937 (bits=32) or std::mt19937_64 seeded
+    with `seed` (the engines of kmeans_core.cpp:150 and :293)."""
+    if bits == 64:
+        out = np.empty(n, np.uint64)
+        lib().orc_mt64_outputs(seed, n, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)))
+    else:
+        out = np.empty(n, np.uint32)
+        lib().orc_mt32_outputs(seed, n, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
     return out
 
 

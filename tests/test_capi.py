@@ -210,3 +210,19 @@ def test_noalloc_rejects_shapes_beyond_its_scratch(L):
     assert need.value > 64 << 20
     assert L.imi_decode_step_noalloc(ctypes.byref(d), None) == 3
     assert "scratch" in L.imi_last_error().decode()
+
+
+def test_check_decode_limits_rejects_before_any_build(L):
+    """ops.check_decode_limits runs the selection's argument checks alone (no
+    device, no index), so a cache can refuse an unsupported shape before it
+    spends the prefill on an index build."""
+    from adaptiveimi_amd import ops
+    from adaptiveimi_amd._lib import IMIError
+
+    ops.check_decode_limits(8, 4, (64, 64), ops.Budget(410, 13097, 1638))
+    ops.check_decode_limits(8, 4, (181, 90), ops.Budget(1638, 52000, 1638))      # 2-way k above 128
+    ops.check_decode_limits(8, 4, (32, 32, 32, 32), ops.Budget(16390, 4096, 512))
+    with pytest.raises(IMIError, match="cells"):
+        ops.check_decode_limits(8, 4, (256, 128), ops.Budget(410, 13097, 1638))   # 32768 cells per head
+    with pytest.raises(IMIError, match="rank"):
+        ops.check_decode_limits(8, 4, (128, 128), ops.Budget(5000, 60000, 5000))  # K' above the ranking capacity

@@ -121,7 +121,7 @@ def _bits(t):
 
 @pytest.mark.gpu
 @pytest.mark.skipif(not gpu_available(), reason="needs a HIP device")
-@pytest.mark.parametrize("ks", [(32, 32), (6, 6, 6, 6)])
+@pytest.mark.parametrize("ks", [(32, 32), (6, 6, 6, 6), (8, 8, 8, 8)])
 def test_model_shaped_prefill_and_decode_match_oracle(ks):
     from adaptiveimi_amd import synthetic
     from adaptiveimi_amd.attn_hub.sparse_imi import imi_decode_attn
@@ -157,7 +157,7 @@ def test_model_shaped_prefill_and_decode_match_oracle(ks):
             labs, cents, _ = orc.kmeans_head(orc.bf16_to_f32(mid_k[h]), list(ks), 6, early_stop_min_iter=6)
             r = orc.compact_reorg(labs, list(ks))
             assert np.array_equal(cache.token_perm[layer][h].cpu().numpy(), r["perm"]), "cell order differs"
-            heads.append(dict(n_active=r["n_active"], offsets=r["offsets"],
+            heads.append(dict(n_active=r["n_active"], offsets=r["offsets"], gids=r["gids"],
                               merged=orc.merged_centroids(cents, r["gids"], list(ks)),
                               list_keys=mid_k[h][r["perm"]], list_values=mid_v[h][r["perm"]]))
         heads_by_layer.append(heads)
@@ -175,11 +175,17 @@ def test_model_shaped_prefill_and_decode_match_oracle(ks):
             static_len = cache.static_pattern_total + (1 if layer < L - 1 else 0)
             sk = _bits(cache.steady_zone_keys[layer][0])
             sv = _bits(cache.steady_zone_values[layer][0])
-            ref, _, rm, _ = orc.decode_step(_bits(q), heads_by_layer[layer], sk, sv, static_len,
-                                            cache.n_centroids, cache.nprobe, cache.max_retrieval_tokens,
-                                            cache.buffer_size)
+            ref, rs, rm, rrows = orc.decode_step(_bits(q), heads_by_layer[layer], sk, sv, static_len,
+                                                 cache.n_centroids, cache.nprobe, cache.max_retrieval_tokens,
+                                                 cache.buffer_size)
             plan = cache._plans[layer]
             assert np.array_equal(plan.selection["n_selected"].cpu().numpy(), rm), "selected cell counts differ"
+            cells = plan.selection["sel_cell"].cpu().numpy()
+            nrows = plan.selection["n_rows"].cpu().numpy()
+            for h in range(H):   # same cells in rank order (compact id -> global id), same row totals
+                gid = heads_by_layer[layer][h]["gids"]
+                assert np.array_equal(cells[h, : rm[h]], gid[rs[h, : rm[h]]]), f"layer {layer} head {h}: cells"
+                assert nrows[h] == len(rrows[h]), f"layer {layer} head {h}: rows"
             got = out.float().cpu().numpy().reshape(H, G, D)
             err = np.abs(got - ref)
             assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)), f"layer {layer} step {step}: max err {err.max()}"

@@ -93,7 +93,7 @@ def _compare_state(upd, orc, out, four, ncells):
         assert (uslot[h] >= 0).sum() == len(rep)
 
 
-@pytest.mark.parametrize("ks", [(32, 32), (6, 6, 6, 6)])
+@pytest.mark.parametrize("ks", [(32, 32), (6, 6, 6, 6), (8, 8, 8, 8)])   # (8,8,8,8): power-of-two digit path
 def test_update_kernels_match_oracle(ops, oracle, ks):
     note(f"[online] update kernels ks={ks}")
     H, T, B = 8, 5000, 8
@@ -170,7 +170,7 @@ def _select_oracle(oracle, orc, q, out, sz, bud, exec_rows, ncells):
     return cells, rm, rtok, dr
 
 
-@pytest.mark.parametrize("ks", [(32, 32), (128, 128), (6, 6, 6, 6)])
+@pytest.mark.parametrize("ks", [(32, 32), (128, 128), (6, 6, 6, 6), (8, 8, 8, 8)])
 def test_select_with_replaced_centroids_and_delta(ops, oracle, ks):
     from adaptiveimi_amd import synthetic
 
@@ -297,7 +297,7 @@ def test_decode_step_online_matches_oracle(ops, oracle):
 
 
 @pytest.mark.parametrize("ks,steps,batch,thr,ring", [((32, 32), 14, 4, 2, 24), ((6, 6, 6, 6), 14, 4, 2, 24),
-                                                      ((32, 32), 50, 16, 3, 40)])
+                                                      ((8, 8, 8, 8), 14, 4, 2, 24), ((32, 32), 50, 16, 3, 40)])
 def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, thr, ring):
     """The drop-in with async_update on, driven like model_hub drives it,
     against a step-by-step oracle replay (update applied at the next step);

@@ -43,7 +43,8 @@ def _kv(H, T, seed=0, integer=False):
 # ------------------------------------------------------------- k-means ----
 
 @pytest.mark.parametrize("T,k,parts,integer", [(3000, 64, 2, False), (1000, 16, 2, True), (2049, 32, 4, False),
-                                                (777, 7, 2, False)])
+                                                (777, 7, 2, False),
+                                                (1000, 128, 2, False), (1500, 128, 2, True)])   # configs[4]: k = 128
 def test_assign_bit_exact(ops, oracle, T, k, parts, integer):
     note(f"[assign] T={T} k={k} parts={parts} integer={integer}")
     H = 4
@@ -140,7 +141,8 @@ def test_kmeans_plusplus_wide_range_sequential_path(ops, oracle):
         assert np.array_equal(labels.cpu().numpy()[0, p], labs[p]), p
 
 
-@pytest.mark.parametrize("T,sample,ks", [(24000, 6000, (32, 32)), (20001, 4096, (8, 8, 8, 8))])
+@pytest.mark.parametrize("T,sample,ks", [(24000, 6000, (32, 32)), (20001, 4096, (8, 8, 8, 8)),
+                                         (60000, 16384, (128, 128))])   # configs[4]: 2 x 128 centroids
 def test_kmeans_sampled_then_assign(ops, oracle, T, sample, ks):
     """The 1M-token build at reduced scale: k-means on every ceil(T/sample)-th
     key, then every key assigned to the final centroids -- bit-exact with the
@@ -174,6 +176,49 @@ def test_kmeans_empty_cluster_reseed(ops, oracle):
         for p in range(2):
             assert np.array_equal(labels.cpu().numpy()[h, p], labs[p])
             assert np.array_equal(cent.cpu().numpy()[h, p], cents[p])
+
+
+def _exact_cluster_keys(H, k=4, per=64, seed=0):
+    """bf16 keys whose E-step distances and inertia are exact integers in any
+    summation order: per 64-dim subspace, k clusters of `per` integer rows
+    symmetric around integer centres (a power-of-two size, so the M-step
+    mean is the exact centre), the first k rows off-centre members."""
+    rng = np.random.default_rng(seed)
+    out = np.zeros((H, k * per, 128), np.float32)
+    for h in range(H):
+        for p in range(2):
+            centres = rng.integers(-7, 8, (k, 64)) * 16
+            rows = []
+            for c in range(k):
+                half = rng.integers(-3, 4, (per // 2, 64))
+                rows.append(np.concatenate([centres[c] + half, centres[c] - half]))
+            x = np.concatenate(rows)
+            firsts = np.array([c * per for c in range(k)])
+            order = np.concatenate([firsts, np.setdiff1d(np.arange(k * per), firsts)])
+            out[h, :, p * 64:(p + 1) * 64] = x[order]
+    return torch.from_numpy(out).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("min_iter,rel_tol,tol", [(1, 1e-6, 0.0), (2, 0.0, 0.0), (1, 0.9, 0.0), (5, 0.0, 0.0),
+                                                  (1, 0.0, 1e9)])
+def test_kmeans_early_stop_matches_oracle(ops, oracle, min_iter, rel_tol, tol):
+    """kmeans_core.cpp:244-262 on data whose inertia is exact in any order, so
+    the GPU's summation order cannot move the stop: the iteration count, the
+    labels and the centroids equal the oracle's."""
+    note(f"[kmeans] early stop min_iter={min_iter} rel_tol={rel_tol} tol={tol}")
+    H, k = 2, 4
+    keys = _exact_cluster_keys(H, k)
+    kf = oracle.bf16_to_f32(bits(keys))
+    assert np.array_equal(kf, np.round(kf))
+    cent, labels, it = ops.kmeans(keys.to(DEV), [k, k], 10, tol=tol, early_stop_min_iter=min_iter,
+                                  early_stop_rel_tol=rel_tol)
+    for h in range(H):
+        labs, cents, iters = oracle.kmeans_head(kf[h], [k, k], 10, tol=tol, early_stop_min_iter=min_iter,
+                                                early_stop_rel_tol=rel_tol)
+        for p in range(2):
+            assert int(it[h, p]) == iters[p], (h, p)
+            assert np.array_equal(labels[h, p].cpu().numpy(), labs[p]), (h, p)
+            assert np.array_equal(cent[h, p].cpu().numpy(), cents[p]), (h, p)
 
 
 def test_kmeans_early_stop_semantics(ops, oracle):
@@ -485,6 +530,7 @@ def _check_attention(out, ref):
     (32768, (64, 64), 4, 96, False, 0.1), (9000, (32, 32), 7, 0, False, 0.1), (6000, (32, 32), 8, 200, False, 0.1),
     (20000, (32, 32), 4, 96, True, 0.1),
     (100000, (128, 128), 4, 96, False, 0.2),   # score + rank kernels; over 2048 selected cells per head
+    (131072 - 96, (64, 64), 4, 97, False, 0.1),   # configs[1], the bench shape: nprobe 410, 1638 pages
 ])
 def test_decode_step_matches_oracle(ops, oracle, T, ks, G, static_len, tiles, budget):
     note(f"[decode] T={T} ks={ks} G={G} static={static_len} tiles={tiles} budget={budget}")
@@ -510,14 +556,73 @@ def test_decode_step_matches_oracle(ops, oracle, T, ks, G, static_len, tiles, bu
         offs = out["compact_offset"][h, : na + 1].cpu().numpy()
         heads.append(dict(n_active=na, offsets=offs, merged=out["compact_centroids"][h, :na].cpu().numpy(),
                           list_keys=bits(out["list_keys"][h]), list_values=bits(out["list_values"][h])))
-    ref, rs, rm, _ = oracle.decode_step(bits(q), heads, bits(sk), bits(sv), static_len, sz["n_centroids"],
-                                        bud.nprobe, bud.max_tokens, bud.buffer_pages, tile_mode=tiles)
+    ref, rs, rm, rrows = oracle.decode_step(bits(q), heads, bits(sk), bits(sv), static_len, sz["n_centroids"],
+                                            bud.nprobe, bud.max_tokens, bud.buffer_pages, tile_mode=tiles)
     sel = plan.selection
     assert np.array_equal(sel["n_selected"].cpu().numpy(), rm)
+    # the same cells in the same rank order (compact id -> global cell id) and row totals
+    gids = out["compact_gid"].cpu().numpy()
+    cells = sel["sel_cell"].cpu().numpy()
+    nrows = sel["n_rows"].cpu().numpy()
+    for h in range(H):
+        assert np.array_equal(cells[h, : rm[h]], gids[h][rs[h, : rm[h]]]), h
+        assert nrows[h] == len(rrows[h]), h
     if tiles:   # more rows than one page budget holds
         assert int(sel["n_rows"].max()) > bud.buffer_pages * bud.page_size
     if budget > 0.1:   # the attention prologue stages its selection in more than one round trip
         assert int(sel["n_selected"].max()) > 2048
+    _check_attention(res, ref)
+
+
+def test_config3_shape_decode_matches_oracle(ops, oracle):
+    """configs[3] per sequence: 4-way IMI with 32 centroids per subspace (a
+    1,048,576-cell space), 262,048 listed tokens per KV head (over 200k
+    occupied cells each), G = 8, the fixed budget of 4096 tokens (nprobe
+    16390, 512 pages).  Selection (cells in rank order, row totals) is
+    bit-exact with the oracle; attention within the usual tolerance."""
+    from adaptiveimi_amd import synthetic
+
+    H, G, ks = 2, 8, (32, 32, 32, 32)
+    T = 262144 - 96
+    note(f"[config3] H={H} T={T} ks={ks} G={G}")
+    keys, values = _kv(H, T, seed=333)
+    kd, vd = keys.to(DEV), values.to(DEV)
+    cent, labels, _ = ops.kmeans(kd, list(ks), 3)
+    ncells = int(np.prod(ks))
+    out = ops.build_index(kd, vd, cent, labels, list(ks), n_centroids=ncells + 1, merged=False)
+    n_active = out["n_active"].cpu().numpy()
+    assert (n_active > 200000).all(), n_active
+    sz = oracle.sizing(T, 4096 / T, subspace_parts=4, k_override=ks)
+    sz["max_tokens"] = 4096
+    sz["buffer_pages"] = max(32, -(-4096 // sz["page_size"]))
+    bud = ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"])
+    assert (bud.nprobe, bud.buffer_pages) == (16390, 512)
+    static_len = 97
+    sk, sv = synthetic.make_kv(H, static_len + 8, seed=78)
+    plan = ops.DecodePlan(cent, out["cell_count"], out["cell_offset"], ks, bud, out["list_keys"],
+                          out["list_values"], sk.to(DEV), sv.to(DEV), G, compact=out)
+    plan.set_static_len(static_len)
+    q = synthetic.make_queries(keys, G, seed=6)[0]
+    plan.query.copy_(q.to(DEV))
+    res = plan.step().clone()
+    torch.cuda.synchronize()
+    cents = cent.cpu().numpy()
+    heads = []
+    gids = out["compact_gid"].cpu().numpy()
+    for h in range(H):
+        na = int(n_active[h])
+        merged = oracle.merged_centroids([cents[h, p, : ks[p]] for p in range(4)], gids[h, :na], list(ks))
+        heads.append(dict(n_active=na, offsets=out["compact_offset"][h, : na + 1].cpu().numpy(), merged=merged,
+                          list_keys=bits(out["list_keys"][h]), list_values=bits(out["list_values"][h])))
+    ref, rs, rm, rrows = oracle.decode_step(bits(q), heads, bits(sk), bits(sv), static_len, int(n_active.max()) + 1,
+                                            bud.nprobe, bud.max_tokens, bud.buffer_pages)
+    sel = plan.selection
+    assert np.array_equal(sel["n_selected"].cpu().numpy(), rm)
+    cells = sel["sel_cell"].cpu().numpy()
+    nrows = sel["n_rows"].cpu().numpy()
+    for h in range(H):
+        assert np.array_equal(cells[h, : rm[h]], gids[h][rs[h, : rm[h]]]), h
+        assert nrows[h] == len(rrows[h]), h
     _check_attention(res, ref)
 
 

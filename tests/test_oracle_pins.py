@@ -1,0 +1,440 @@
+"""Further pins of the CPU oracle, each against something the oracle does not
+contain: outputs fixed by the C++ standard, published algorithms restated
+here from their specifications, exact rational arithmetic, and literal
+restatements of reference code paths.
+
+  * mt19937 / mt19937_64: the engines of kmeans_core.cpp:150 (kmeans++) and
+    :293 (empty-cluster reseed), restated from Matsumoto-Nishimura's
+    published recurrences and checked against the 10000th outputs that the
+    C++ standard fixes ([rand.predef]).
+  * uniform_int_distribution / uniform_real_distribution: restated from
+    libstdc++ of GCC 11.4 (the toolchain of this image and of the
+    reference's build): Lemire's nearly divisionless reduction for 32- and
+    64-bit engines, and generate_canonical<double, 53>.
+  * kmeans++ (kmeans_core.cpp:138-186) and the reseed draws
+    (kmeans_core.cpp:292-310) rebuilt from those pieces.
+  * the Lloyd early-stop rule (kmeans_core.cpp:244-262) replayed on data
+    whose inertia is exact in any summation order.
+  * the score chain (compute_impl.cu:80-101): `sim += q[d] * c[d]` compiled
+    by nvcc with its default -fmad=true contracts to fmaf(q[d], c[d], sim),
+    a sequential chain over d; checked against exact rational arithmetic
+    on inputs where an unfused or reordered chain gives another result.
+  * tile mode: _build_cluster_tiles (retrieval.py:30-112) restated with
+    torch ops on top of _select_clusters (retrieval.py:295-303); the union
+    of its tiles must equal oracle.select_tiles.
+"""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+U32 = (1 << 32) - 1
+U64 = (1 << 64) - 1
+
+
+# ---------------------------------------------------------------- engines ----
+
+class MT19937:
+    """32-bit Mersenne Twister (Matsumoto & Nishimura 1998)."""
+    n, m = 624, 397
+
+    def __init__(self, seed: int):
+        self.mt = [seed & U32]
+        for i in range(1, self.n):
+            prev = self.mt[-1]
+            self.mt.append((1812433253 * (prev ^ (prev >> 30)) + i) & U32)
+        self.i = self.n
+
+    def _twist(self):
+        mt = self.mt
+        for k in range(self.n):
+            x = (mt[k] & 0x80000000) | (mt[(k + 1) % self.n] & 0x7FFFFFFF)
+            xa = (x >> 1) ^ (0x9908B0DF if x & 1 else 0)
+            mt[k] = mt[(k + self.m) % self.n] ^ xa
+        self.i = 0
+
+    def __call__(self) -> int:
+        if self.i >= self.n:
+            self._twist()
+        y = self.mt[self.i]
+        self.i += 1
+        y ^= y >> 11
+        y ^= (y << 7) & 0x9D2C5680
+        y ^= (y << 15) & 0xEFC60000
+        y ^= y >> 18
+        return y & U32
+
+    bits = 32
+
+
+class MT19937_64:
+    """64-bit Mersenne Twister (Nishimura 2000)."""
+    n, m = 312, 156
+
+    def __init__(self, seed: int):
+        self.mt = [seed & U64]
+        for i in range(1, self.n):
+            prev = self.mt[-1]
+            self.mt.append((6364136223846793005 * (prev ^ (prev >> 62)) + i) & U64)
+        self.i = self.n
+
+    def _twist(self):
+        mt = self.mt
+        for k in range(self.n):
+            x = (mt[k] & 0xFFFFFFFF80000000) | (mt[(k + 1) % self.n] & 0x7FFFFFFF)
+            xa = (x >> 1) ^ (0xB5026F5AA96619E9 if x & 1 else 0)
+            mt[k] = mt[(k + self.m) % self.n] ^ xa
+        self.i = 0
+
+    def __call__(self) -> int:
+        if self.i >= self.n:
+            self._twist()
+        y = self.mt[self.i]
+        self.i += 1
+        y ^= (y >> 29) & 0x5555555555555555
+        y ^= (y << 17) & 0x71D67FFFEDA60000
+        y ^= (y << 37) & 0xFFF7EEE000000000
+        y ^= y >> 43
+        return y & U64
+
+    bits = 64
+
+
+def test_engines_match_the_standard_and_the_oracle(oracle):
+    # [rand.predef]: the 10000th consecutive invocation of a default-seeded
+    # (5489) object produces these values
+    for cls, want in ((MT19937, 4123659995), (MT19937_64, 9981545732273789042)):
+        e = cls(5489)
+        for _ in range(9999):
+            e()
+        assert e() == want
+    assert int(oracle.mt_outputs(5489, 10000, 64)[-1]) == 9981545732273789042
+    assert int(oracle.mt_outputs(5489, 10000, 32)[-1]) == 4123659995
+    for seed in (0, 42, 43, 12345, 12352, 2 ** 63 + 5):
+        e64 = MT19937_64(seed)
+        assert [e64() for _ in range(700)] == [int(x) for x in oracle.mt_outputs(seed, 700, 64)]
+        e32 = MT19937(seed & U32)
+        assert [e32() for _ in range(700)] == [int(x) for x in oracle.mt_outputs(seed & U32, 700, 32)]
+
+
+# ---------------------------------------------------------- distributions ----
+
+def uniform_int(eng, a: int, b: int) -> int:
+    """libstdc++ (GCC 11) uniform_int_distribution<int32_t>(a, b) with a
+    32- or 64-bit engine: Lemire's reduction of one engine word."""
+    erange = b - a + 1
+    w = eng.bits
+    mask = (1 << w) - 1
+    product = eng() * erange
+    low = product & mask
+    if low < erange:
+        threshold = ((1 << w) - erange) % erange
+        while low < threshold:
+            product = eng() * erange
+            low = product & mask
+    return a + (product >> w)
+
+
+def canonical_double(eng) -> float:
+    """generate_canonical<double, 53> over a 64-bit engine: one word, rounded
+    to double (round-to-nearest-even) and scaled by 2^-64; 1.0 maps to the
+    largest double below 1."""
+    r = float(eng()) / 18446744073709551616.0
+    return r if r < 1.0 else np.nextafter(1.0, 0.0)
+
+
+def test_reseed_draws_match_restated_distribution(oracle):
+    for it in (0, 1, 9, 19):
+        for n in (1, 2, 3, 97, 1000, 65536, 131072, 2 ** 31 - 1):
+            got = oracle.reseed_draws(it, n, 40)
+            eng = MT19937(it + 12345)
+            want = [uniform_int(eng, 0, n - 1) for _ in range(40)]
+            assert got.tolist() == want, (it, n)
+
+
+def test_uniform_int_rejection_branch_is_exercised(oracle):
+    """A range of 2^31 + 1 values rejects about half of the words: the
+    restated threshold loop must then consume extra engine words (the
+    reseed test above compares the restatement with the real library)."""
+    e1, e2 = MT19937(7), MT19937(7)
+    draws = [uniform_int(e1, 0, 2 ** 31) for _ in range(50)]
+
+    class Count:
+        bits = 32
+
+        def __init__(self):
+            self.n = 0
+
+        def __call__(self):
+            self.n += 1
+            return e2()
+    c = Count()
+    assert [uniform_int(c, 0, 2 ** 31) for _ in range(50)] == draws
+    assert c.n > 50
+
+
+# ---------------------------------------------------------------- kmeans++ ----
+
+def _l2(oracle, a, b):
+    return np.float32(oracle.lib().orc_l2(a.ctypes.data_as(oracle._f32p), b.ctypes.data_as(oracle._f32p),
+                                          a.shape[0]))
+
+
+def kmeanspp_restated(oracle, x, k, seed):
+    """kmeans_core.cpp:138-186 with the restated engine and distributions
+    (distances through the oracle's lane-ordered L2, pinned separately)."""
+    n = x.shape[0]
+    eng = MT19937_64(seed)
+    picks = [uniform_int(eng, 0, n - 1)]
+    mind = np.full(n, np.finfo(np.float32).max, np.float32)
+    for c in range(1, k):
+        prev = x[picks[-1]]
+        for i in range(n):
+            d = _l2(oracle, x[i], prev)
+            if d < mind[i]:
+                mind[i] = d
+        total = 0.0
+        for i in range(n):
+            total += float(mind[i])
+        target = canonical_double(eng) * (total - 0.0) + 0.0
+        run, pick = 0.0, 0
+        for i in range(n):
+            run += float(mind[i])
+            if run >= target:
+                pick = i
+                break
+        picks.append(pick)
+    return picks
+
+
+@pytest.mark.parametrize("seed", [42, 43, 7])
+def test_kmeanspp_matches_restated_algorithm(oracle, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((240, 16)) * rng.lognormal(0, 1, (240, 1))).astype(np.float32)
+    picks = kmeanspp_restated(oracle, x, 10, seed)
+    c = oracle.kmeanspp_init(x, 10, seed)
+    assert np.array_equal(c, x[picks])
+
+
+def test_kmeanspp_degenerate_distances(oracle):
+    """All rows equal: after the first pick every D^2 weight is 0, the target
+    is 0 and the scan takes index 0.  Two distinct rows: the second pick must
+    be the other row, then only zero weights remain."""
+    x = np.tile(np.arange(16, dtype=np.float32), (50, 1))
+    picks = kmeanspp_restated(oracle, x, 5, 42)
+    assert picks[1:] == [0, 0, 0, 0]
+    assert np.array_equal(oracle.kmeanspp_init(x, 5, 42), x[picks])
+    y = x.copy()
+    y[30:] += 1.0
+    picks = kmeanspp_restated(oracle, y, 4, 43)
+    first_half = picks[0] < 30
+    assert (picks[1] < 30) != first_half
+    assert np.array_equal(oracle.kmeanspp_init(y, 4, 43), y[picks])
+
+
+# ------------------------------------------------------------ early stop ----
+
+def _exact_clusters(k=4, per=64, dim=16, seed=0):
+    """Integer rows symmetric around integer centres, cluster sizes a power
+    of two (so 1.0f/size is exact and every mean is the exact centre); the
+    first k rows are off-centre members of each cluster, so iteration 0
+    moves the centroids and iteration 1 lowers the inertia."""
+    rng = np.random.default_rng(seed)
+    centres = rng.integers(-40, 40, (k, dim)) * 8
+    rows = []
+    for c in range(k):
+        half = rng.integers(-3, 4, (per // 2, dim))
+        rows.append(np.concatenate([centres[c] + half, centres[c] - half]))
+    x = np.concatenate(rows).astype(np.float32)
+    firsts = np.array([c * per for c in range(k)])
+    order = np.concatenate([firsts, np.setdiff1d(np.arange(k * per), firsts)])
+    return x[order]
+
+
+def lloyd_iterations_restated(oracle, x, k, max_iters, tol, min_iter, rel_tol):
+    """kmeans_core.cpp:219-262: E-step, then the stop test on the fp32
+    inertia (|prev - inertia|, relative to prev), then the M-step."""
+    cent = x[:k].copy()
+    prev = np.float32(np.finfo(np.float32).max)
+    iters = 0
+    for it in range(max_iters):
+        iters += 1
+        lab, mind, _ = oracle.estep(x, cent)
+        inertia = np.float32(0.0)
+        for v in mind:
+            inertia = np.float32(inertia + v)
+        change = np.float32(abs(prev - inertia))
+        rel = np.float32(change / prev) if prev > 0 else np.float32(0.0)
+        if iters >= max(1, min_iter) and (rel <= max(0.0, rel_tol) or change <= max(0.0, tol)):
+            break
+        prev = inertia
+        cent = oracle.mstep(x, lab, k, it)
+    return iters, cent
+
+
+@pytest.mark.parametrize("min_iter,rel_tol,tol", [(1, 1e-6, 0.0), (2, 0.0, 0.0), (1, 0.9, 0.0), (5, 0.0, 0.0),
+                                                  (1, 0.0, 1e9)])
+def test_lloyd_early_stop_rule_exact(oracle, min_iter, rel_tol, tol):
+    x = _exact_clusters()
+    # every distance and partial sum is an integer below 2^24: any order is exact
+    _, mind, _ = oracle.estep(x, x[:4].copy())
+    assert mind.astype(np.float64).sum() < 2 ** 24 and np.all(mind == np.round(mind))
+    want_iters, want_cent = lloyd_iterations_restated(oracle, x, 4, 10, tol, min_iter, rel_tol)
+    cent, lab, iters = oracle.lloyd(x, x[:4].copy(), 10, tol=tol, early_stop_min_iter=min_iter,
+                                    early_stop_rel_tol=rel_tol)
+    assert iters == want_iters
+    assert np.array_equal(cent, want_cent)
+    # the expected stop points of this data: prev starts at FLT_MAX, so the
+    # first test never stops; iteration 0 moves the centroids to the exact
+    # centres, so iteration 2 repeats iteration 1's inertia (change 0)
+    expect = {(1, 1e-6, 0.0): 3, (2, 0.0, 0.0): 3, (1, 0.9, 0.0): 2, (5, 0.0, 0.0): 5, (1, 0.0, 1e9): 2}
+    assert iters == expect[(min_iter, rel_tol, tol)]
+
+
+# ---------------------------------------------------------------- scoring ----
+
+def _fma_f32(a, b, c):
+    """fmaf with one rounding: the exact rational a*b + c rounded to binary32
+    (round to nearest, ties to even)."""
+    x = Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))
+    return np.float32(_round_f32(x))
+
+
+def _round_f32(x: Fraction) -> float:
+    if x == 0:
+        return 0.0
+    sign = -1 if x < 0 else 1
+    x = abs(x)
+    e = x.numerator.bit_length() - x.denominator.bit_length()
+    if Fraction(2) ** e > x:
+        e -= 1
+    e = max(e, -126)
+    scale = Fraction(2) ** (23 - e)
+    m = x * scale
+    q, r = divmod(m.numerator, m.denominator)
+    if 2 * r > m.denominator or (2 * r == m.denominator and q & 1):
+        q += 1
+    return sign * float(Fraction(q) / scale)
+
+
+def _chain(qs, c, order, fused=True):
+    s = np.float32(0.0)
+    for d in order:
+        s = _fma_f32(qs[d], c[d], s) if fused else np.float32(s + np.float32(qs[d] * c[d]))
+    return s
+
+
+def test_score_chain_order_is_pinned(oracle):
+    """q[1] * c[1] = 1 + 2^-7 + 2^-20 + 2^-27 needs 28 significant bits: a
+    fused chain after s = -1 keeps the 2^-27, an unfused one rounds it away,
+    and the reversed chain rounds the product before -1 is added."""
+    D = 128
+    q = np.zeros((1, 1, D), np.float32)
+    c = np.zeros((1, 1, D), np.float32)
+    q[0, 0, 0], c[0, 0, 0] = 1.0, -1.0
+    q[0, 0, 1], c[0, 0, 1] = 1.0 + 2.0 ** -7, 1.0 + 2.0 ** -20
+    qs = q[0].sum(0)
+    fwd = _chain(qs, c[0, 0], range(D))
+    assert fwd == np.float32(2.0 ** -7 + 2.0 ** -20 + 2.0 ** -27)
+    assert _chain(qs, c[0, 0], range(D), fused=False) != fwd
+    assert _chain(qs, c[0, 0], range(D - 1, -1, -1)) != fwd
+    got = oracle.scores(oracle.f32_to_bf16(q), c)
+    assert got[0, 0] == fwd
+
+
+def test_scores_random_match_exact_sequential_fma(oracle):
+    """Random bf16 queries (G = 4, summed in fp32 in g order as
+    compute_impl.cu:81-86 does) and fp32 centroids: every score equals the
+    exact-rational sequential FMA chain."""
+    rng = np.random.default_rng(21)
+    H, G, N, D = 2, 4, 6, 128
+    qb = oracle.f32_to_bf16((rng.standard_normal((H, G, D)) * rng.lognormal(0, 2, (H, G, 1))).astype(np.float32))
+    c = (rng.standard_normal((H, N, D)) * rng.lognormal(0, 2, (H, N, 1))).astype(np.float32)
+    got = oracle.scores(qb, c)
+    qf = oracle.bf16_to_f32(qb)
+    for h in range(H):
+        qs = np.zeros(D, np.float32)
+        for g in range(G):
+            qs = (qs + qf[h, g]).astype(np.float32)
+        for n in range(N):
+            assert got[h, n] == _chain(qs, c[h, n], range(D)), (h, n)
+
+
+# -------------------------------------------------------------- tile mode ----
+
+def _tiles_literal(sims, cluster_sizes, pad, nprobe, max_tokens, buffer_size, page_size):
+    """_select_clusters (retrieval.py:295-303) and _build_cluster_tiles
+    (retrieval.py:30-112) in torch ops.  cluster_sizes: [B, pad + 1] with the
+    padding cluster last (size 0)."""
+    B = sims.shape[0]
+    topk = torch.topk(sims, nprobe, dim=-1, largest=True, sorted=True)
+    sizes = torch.gather(cluster_sizes, 1, topk.indices)
+    valid = sizes > 0
+    cumsum = torch.cumsum(sizes, dim=-1, dtype=torch.int32)
+    keep = valid & ((cumsum - sizes) < max_tokens)
+    selected = topk.indices.masked_fill(~keep, pad).to(torch.int64)
+
+    sel_sizes = torch.gather(cluster_sizes.to(torch.int64), 1, selected.clamp_max(pad))
+    sel_sizes = torch.where(selected == pad, 0, sel_sizes)
+    sel_pages = torch.div(sel_sizes + page_size - 1, page_size, rounding_mode="floor")
+    sel_pages = torch.where(sel_sizes > 0, torch.clamp(sel_pages, min=1), 0)
+    prefix = torch.cumsum(sel_pages, dim=1)
+    positions = torch.arange(nprobe, dtype=torch.int64).unsqueeze(0).expand(B, -1)
+    offsets = torch.zeros(B, dtype=torch.int64)
+    counts = (selected != pad).sum(dim=1, dtype=torch.int64)
+    tiles = []
+    while torch.any(offsets < counts):
+        start_valid = offsets < counts
+        start_prefix = torch.gather(prefix, 1, torch.clamp(offsets - 1, min=0).unsqueeze(1)).squeeze(1)
+        start_prefix = torch.where(offsets > 0, start_prefix, torch.zeros_like(start_prefix))
+        rel = prefix - start_prefix.unsqueeze(1)
+        cand = (positions >= offsets.unsqueeze(1)) & (positions < counts.unsqueeze(1)) & (rel <= buffer_size)
+        take = cand.sum(dim=1, dtype=torch.int64)
+        force = start_valid & (take == 0)
+        if torch.any(force):
+            cur = torch.minimum(offsets.unsqueeze(1), torch.full_like(offsets.unsqueeze(1), nprobe - 1))
+            cur_pages = torch.gather(sel_pages, 1, cur).squeeze(1)
+            force = force & (cur_pages <= buffer_size)
+            take = torch.where(force, torch.ones_like(take), take)
+        take = torch.minimum(take, counts - offsets)
+        max_take = int(take.max().item())
+        if max_take <= 0:
+            break
+        gpos = offsets.unsqueeze(1) + torch.arange(max_take, dtype=torch.int64).unsqueeze(0)
+        payload = torch.gather(selected, 1, torch.minimum(gpos, torch.full_like(gpos, nprobe - 1)))
+        pmask = torch.arange(max_take, dtype=torch.int64).unsqueeze(0) < take.unsqueeze(1)
+        tile = torch.full((B, max_take), pad, dtype=torch.int64)
+        tile[pmask] = payload[pmask]
+        tiles.append(tile)
+        offsets = offsets + take
+    return tiles
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_select_tiles_matches_literal_tiles(oracle, seed):
+    rng = np.random.default_rng(300 + seed)
+    B, N, page = 4, 400, 8
+    sizes = rng.integers(1, 60, (B, N)).astype(np.int32)
+    n_active = rng.integers(250, N + 1, B)
+    mask = np.zeros((B, N), bool)
+    for b in range(B):
+        sizes[b, n_active[b]:] = 0
+        mask[b, n_active[b]:] = True
+    buffer_pages = int(rng.integers(2, 12))
+    big = rng.random((B, N)) < 0.04          # cells with more pages than one tile holds
+    sizes[big & ~mask] = rng.integers(page * buffer_pages + 1, page * buffer_pages + 90, int((big & ~mask).sum()))
+    sc = rng.standard_normal((B, N)).astype(np.float32)   # distinct: topk order is the rank order
+    nprobe = int(rng.integers(20, 200))
+    max_tokens = int(rng.integers(100, 4000))
+    sims = torch.from_numpy(sc).masked_fill(torch.from_numpy(mask), float("-inf"))
+    cs = torch.from_numpy(np.concatenate([sizes, np.zeros((B, 1), np.int32)], 1))
+    tiles = _tiles_literal(sims, cs, N, nprobe, max_tokens, buffer_pages, page)
+    sel, m, tok = oracle.select_tiles(sc, sizes, mask, nprobe, max_tokens, buffer_pages, page)
+    for b in range(B):
+        attended = [int(c) for t in tiles for c in t[b].tolist() if c != N]
+        assert sel[b, : m[b]].tolist() == attended, b
+        assert tok[b] == sizes[b, attended].sum()
+        for t in tiles:   # each tile holds at most buffer_pages pages
+            cells = [c for c in t[b].tolist() if c != N]
+            assert sum((int(sizes[b, c]) + page - 1) // page for c in cells) <= buffer_pages
