@@ -32,6 +32,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, vendor figure
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, vendor figure (no sparsity)
 
 
 def log(msg):
@@ -67,7 +68,8 @@ def parse():
     p.add_argument("--iters", type=int, default=None)
     p.add_argument("--budget", type=float, default=None)
     p.add_argument("--cpu-baseline", type=int, default=1)
-    p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--cpu-seconds", type=float, default=40.0,
+                   help="time bound of the CPU baseline leg (decode steps, then full index builds of layer 0)")
     p.add_argument("--no-graph", action="store_true")
     p.add_argument("--online-layers", type=int, default=4,
                    help="layers of the online-index-maintenance leg (async_update: batch 16, threshold 16, "
@@ -254,7 +256,7 @@ def main():
     # ----------------------------------------------------- CPU baseline
     cpu = None
     if keep_first is not None:
-        cpu = cpu_baseline(keep_first, ks, bud, static_len, args.cpu_seconds)
+        cpu = cpu_baseline(keep_first, ks, bud, static_len, args.cpu_seconds, args.iters)
 
     result = {
         "metric": "sparse-decode steps/s per layer @128k, budget 0.1; index-build ms; % HBM peak",
@@ -277,13 +279,15 @@ def main():
         },
         "index_build_ms": {"per_layer_median": round(statistics.median(build_ms), 3),
                            "per_layer_min": round(min(build_ms), 3), "layers": L},
+        "index_build_roofline": build_roofline(args, H, T, ks, statistics.median(build_ms)),
         "us_per_layer_step": round(ms_per_step / L * 1e3, 3),
         "attended_rows_per_layer": rows / L,
         "hbm_frac_step": round(step_gbps / HBM_PEAK_GBPS, 4),
         "kernels_us": {"select_kernel": round(sel_us, 2), "attention_kernel": round(split_us, 2),
                        "merge_kernel": round(merge_us, 2), "attention_kernel+merge_kernel": round(att_us, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": measured_traffic(workload_name(args, L, H, G, ks)),
                      "kernel": "attention_kernel (gather + GQA split-K attention)",
                      "bytes_per_launch": int(bytes_per_layer),
                      "with_merge": {"achieved": round(achieved_am, 1), "frac": round(achieved_am / HBM_PEAK_GBPS, 4),
@@ -390,23 +394,90 @@ def online_update_leg(args, ks, bud, static_total, capture):
             "replaced_cells_per_head": round(repl, 1), "delta_rows_per_head": round(drows, 1)}
 
 
-def measured_traffic():
+def measured_traffic(workload):
     """HBM bytes per attention_kernel launch from the committed counter
-    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-probe calibration),
-    or None when no summary is present."""
-    f = ROOT / "profiles" / "attention_kernel_traffic_128k.md"
+    summary of this exact workload (FETCH_SIZE + WRITE_SIZE per dispatch,
+    each scaled by what the counter reads for a copy of known size), or
+    None when no summary of this workload is committed."""
+    f = ROOT / "profiles" / "attention_kernel_traffic_config1.md"
     if not f.exists():
         return None
+    fields = {}
     for line in f.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
-            return int(line.split(":", 1)[1].strip())
-    return None
+        if ":" in line and not line.startswith(("#", " ", "|")):
+            k, v = line.split(":", 1)
+            fields[k.strip()] = v.strip()
+    if fields.get("workload") != workload or "traffic_bytes_per_launch" not in fields:
+        return None
+    return int(fields["traffic_bytes_per_launch"])
 
 
-def cpu_baseline(first, ks, bud, static_len, seconds):
-    """Oracle (C restatement of the reference CPU path) on the host: decode
-    steps of layer 0 (scores, selection, gather, attention) and, bounded, the
-    k-means + reorganisation of one KV head."""
+def build_roofline(args, H, T, ks, build_ms):
+    """Index-build fractions over the whole per-layer build (k-means +
+    cell lists + K/V permutation, median wall time):
+      E-step FLOPs = 2 T k D per Lloyd iteration per KV head (every key
+        against the k centroids of each of the P subspaces of D/P dims), on
+        the k-means sample for the iterations plus one full assignment when
+        the build samples; against the dense bf16 MFMA peak (the E-step
+        screens distances with bf16 MFMA and rechecks them in fp32);
+      bytes >= the keys once plus the K/V permutation (read and write K
+        and V), 5 T D 2 B per KV head; against the HBM peak."""
+    D = 128
+    k = max(ks)
+    n_it = min(args.sample, T) if args.sample else T
+    flops = 2.0 * k * D * H * (n_it * args.iters + (T if args.sample else 0))
+    nbytes = 5.0 * T * D * 2 * H
+    t = build_ms * 1e-3
+    return {"estep_gflop": round(flops / 1e9, 2), "mfma_tflops": round(flops / t / 1e12, 2),
+            "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS, "mfma_frac": round(flops / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, 5),
+            "bytes_min": int(nbytes), "hbm_gbps": round(nbytes / t / 1e9, 1),
+            "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBPS, 4),
+            "basis": "whole build wall time per layer (median); E-step FLOPs 2*T*k*D per iteration per KV head"}
+
+
+def cpu_build_layer(orc, kbits, vbits, ks, iters, cores):
+    """The reference's CPU index build of one layer (kmeans_core.cpp:384-501,
+    reorganize_core.cpp:18-311), restated by the oracle: bf16 -> fp32,
+    subvector split, per-(head, subspace) Lloyd runs (first-k init, no early
+    stop) on max_concurrent tasks of threads_per_phase OpenMP threads each
+    (kmeans_core.cpp:433-443, cache.py:113-124), then the compaction and the
+    stable K/V permutation per head."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+
+    H, T, D = kbits.shape
+    parts = len(ks)
+    tasks = H * parts
+    tpp = orc.reference_threads_per_phase(cores, H, parts)
+    min_threads = max(1, min(max(1, cores // tasks), cores))
+    max_conc = max(1, min(tasks, cores // min_threads))
+    kf = orc.bf16_to_f32(kbits)
+    sl = orc.subspace_slices(D, parts)
+    subs = [[np.ascontiguousarray(kf[h][:, sl[p]]) for p in range(parts)] for h in range(H)]
+
+    def run(hp):
+        h, p = hp
+        sub = subs[h][p]
+        _, lab, _ = orc.lloyd(sub, sub[: ks[p]], iters, mstep_threads=tpp, estep_threads=tpp)
+        return hp, lab
+
+    labels = {}
+    with ThreadPoolExecutor(max_conc) as ex:
+        for hp, lab in ex.map(run, [(h, p) for h in range(H) for p in range(parts)]):
+            labels[hp] = lab
+    lists = []
+    for h in range(H):
+        r = orc.compact_reorg([labels[(h, p)] for p in range(parts)], ks)
+        lists.append((kbits[h][r["perm"]], vbits[h][r["perm"]]))
+    return lists, max_conc, tpp
+
+
+def cpu_baseline(first, ks, bud, static_len, seconds, iters):
+    """CPU baseline on the host cores (the oracle's C restatement of the
+    reference's CPU path, OpenMP over every core in the affinity mask):
+    decode steps of layer 0 in fp32 (median of >= 20), and the full index
+    build of layer 0 (median of >= 5 runs when they fit the time bound)."""
     import numpy as np
     import torch
 
@@ -415,6 +486,8 @@ def cpu_baseline(first, ks, bud, static_len, seconds):
     def bits(t):
         return t.contiguous().view(torch.int16).numpy().view(np.uint16)
 
+    cores = len(os.sched_getaffinity(0))
+    os.environ.setdefault("OMP_NUM_THREADS", str(cores))
     idx = first["idx"]
     H = first["keys"].shape[0]
     heads = []
@@ -426,29 +499,35 @@ def cpu_baseline(first, ks, bud, static_len, seconds):
         gids = np.flatnonzero(cnt[h])
         offsets = np.concatenate([off[h][gids], [off[h][-1]]]).astype(np.int32)
         heads.append(dict(n_active=len(gids), offsets=offsets,
-                          merged=orc.merged_centroids([cent[h, 0, :ks[0]], cent[h, 1, :ks[1]]], gids, ks),
-                          list_keys=lk[h], list_values=lv[h]))
+                          merged=orc.merged_centroids([cent[h, 0, :ks[0]], cent[h, 1, :ks[1]]], gids, ks)))
     n_c = ks[0] * ks[1] + 1
     q = bits(first["q"])
-    sk, sv = bits(first["steady_k"]), bits(first["steady_v"])
-    orc.decode_step(q, heads, sk, sv, static_len, n_c, bud.nprobe, bud.max_tokens, bud.buffer_pages)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds * 0.5 and n < 200:
-        orc.decode_step(q, heads, sk, sv, static_len, n_c, bud.nprobe, bud.max_tokens, bud.buffer_pages)
-        n += 1
-    dec_s = (time.perf_counter() - t0) / n
-    # index build of one KV head (k-means both subspaces + reorganisation)
-    kf = orc.bf16_to_f32(bits(first["keys"][0]))
-    threads = len(os.sched_getaffinity(0))
+    base = orc.DecodeBaselineF32(heads, lk, lv, bits(first["steady_k"]), bits(first["steady_v"]), n_c)
+    args = (static_len, bud.nprobe, bud.max_tokens, bud.buffer_pages)
+    for _ in range(3):
+        base.step(q, *args)
+    dec = []
     t0 = time.perf_counter()
-    labs, cents, _ = orc.kmeans_head(kf, list(ks), 10, init="first")
-    orc.compact_reorg(labs, ks)
-    head_s = time.perf_counter() - t0
-    return {"value": round(1.0 / dec_s, 2), "unit": "decode steps/s per layer", "cores": 1, "kind": "port",
-            "sample": f"{n} decode steps of layer 0 ({H} KV heads, fp64 attention) in one thread; "
-                      f"index build of 1 of {H} KV heads (E-step on {threads} OpenMP threads, M-step 1 thread) "
-                      f"took {head_s * 1e3:.0f} ms (x{H} heads = {head_s * H * 1e3:.0f} ms per layer)",
-            "index_build_ms_per_layer_est": round(head_s * H * 1e3, 1), "estep_threads": threads}
+    while len(dec) < 20 or (time.perf_counter() - t0 < seconds * 0.3 and len(dec) < 200):
+        t1 = time.perf_counter()
+        base.step(q, *args)
+        dec.append(time.perf_counter() - t1)
+    dec_s = statistics.median(dec)
+    kb, vb = bits(first["keys"]), bits(first["values"])
+    build = []
+    t0 = time.perf_counter()
+    while len(build) < 5 and (len(build) == 0 or time.perf_counter() - t0 < seconds * 0.8):
+        t1 = time.perf_counter()
+        _, max_conc, tpp = cpu_build_layer(orc, kb, vb, ks, iters, cores)
+        build.append(time.perf_counter() - t1)
+    build_ms = statistics.median(build) * 1e3
+    return {"value": round(1.0 / dec_s, 2), "unit": "decode steps/s per layer", "cores": cores, "kind": "port",
+            "sample": f"layer 0 of the same workload: {len(dec)} decode steps ({H} KV heads, scores + selection + "
+                      f"fp32 attention, OpenMP on {cores} cores), median; {len(build)} full index builds of the "
+                      f"layer ({H} heads x {len(ks)} subspaces, {iters} Lloyd iterations, {max_conc} concurrent "
+                      f"runs x {tpp} threads as the reference splits them, compaction, K/V permutation), median",
+            "decode_us_per_layer_median": round(dec_s * 1e6, 1), "decode_runs": len(dec),
+            "index_build_ms_per_layer_median": round(build_ms, 1), "index_build_runs": len(build)}
 
 
 if __name__ == "__main__":

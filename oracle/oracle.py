@@ -88,6 +88,11 @@ def lib():
         L.orc_mt32_outputs.argtypes = [ctypes.c_uint32, ctypes.c_int64, ctypes.POINTER(ctypes.c_uint32)]
         L.orc_mt64_outputs.restype = None
         L.orc_mt64_outputs.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.POINTER(ctypes.c_uint64)]
+        L.orc_decode_step_f32.restype = None
+        L.orc_decode_step_f32.argtypes = [_u16p, _f32p, _i32p, _u8p, _i32p, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_int, _u16p, _u16p, ctypes.c_int64, _u16p, _u16p,
+                                          ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_float, _f32p, _i32p]
         L.orc_attention.restype = None
         L.orc_attention.argtypes = [_u16p, _u16p, _u16p, ctypes.c_int64, _i64p, _i32p, ctypes.c_int64,
                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_double, _f64p]
@@ -477,6 +482,37 @@ def decode_step(q_bits: np.ndarray, heads: List[dict], steady_k: np.ndarray, ste
         nr.append(np.arange(n, dtype=np.int64))
     out = attention(q_bits, ek, ev, nr)
     return out, sel, m, rows
+
+
+class DecodeBaselineF32:
+    """CPU BASELINE, not a checker: the decode step of every KV head in fp32
+    with OpenMP (orc_decode_step_f32), on metadata padded once
+    (pad_metadata).  list_keys / values: [H, L, D] bf16 bits; steady_k / v:
+    [H, S, D] bf16 bits."""
+
+    def __init__(self, heads: List[dict], list_keys: np.ndarray, list_values: np.ndarray, steady_k: np.ndarray,
+                 steady_v: np.ndarray, n_centroids: int, D: int = 128):
+        self.sizes, self.offsets, self.cent, mask = pad_metadata(heads, n_centroids, D)
+        self.mask = np.ascontiguousarray(mask, np.uint8)
+        self.lk = np.ascontiguousarray(list_keys, np.uint16)
+        self.lv = np.ascontiguousarray(list_values, np.uint16)
+        self.sk = np.ascontiguousarray(steady_k, np.uint16)
+        self.sv = np.ascontiguousarray(steady_v, np.uint16)
+        self.H, self.N, self.D = self.cent.shape
+
+    def step(self, q_bits: np.ndarray, static_len: int, nprobe: int, max_tokens: int, buffer_pages: int,
+             page_size: int = 8, scale: Optional[float] = None):
+        q_bits = np.ascontiguousarray(q_bits, np.uint16)
+        G = q_bits.shape[1]
+        out = np.empty((self.H, G, self.D), np.float32)
+        m = np.empty(self.H, np.int32)
+        sc = 1.0 / math.sqrt(self.D) if scale is None else scale
+        lib().orc_decode_step_f32(_p(q_bits, _u16p), _p(self.cent, _f32p), _p(self.sizes, _i32p),
+                                  _p(self.mask, _u8p), _p(self.offsets, _i32p), self.H, G, self.N, self.D,
+                                  _p(self.lk, _u16p), _p(self.lv, _u16p), self.lk.shape[1], _p(self.sk, _u16p),
+                                  _p(self.sv, _u16p), self.sk.shape[1], static_len, nprobe, max_tokens,
+                                  buffer_pages, page_size, sc, _p(out, _f32p), _p(m, _i32p))
+        return out, m
 
 
 # ------------------------------------------------ online index update ----

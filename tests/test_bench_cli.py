@@ -46,10 +46,32 @@ def test_other_workloads_and_overrides(monkeypatch):
     assert (a.layers, a.context, tuple(a.ks), a.sample, a.budget) == (2, 1048576, (96, 96), 65536, 0.02)
 
 
-def test_traffic_comes_from_the_committed_summary():
+def test_traffic_comes_from_the_committed_summary_of_the_same_workload(monkeypatch):
+    """roofline.traffic is the counter figure of the summary whose workload
+    line names this exact workload, and null for any other workload."""
     import bench
 
-    t = bench.measured_traffic()
-    text = (ROOT / "profiles" / "attention_kernel_traffic_128k.md").read_text()
-    assert t is not None and f"traffic_bytes_per_launch: {t}" in text
+    a = _parse(monkeypatch, [])
+    name = bench.workload_name(a, 32, 8, 4, tuple(a.ks))
+    f = ROOT / "profiles" / "attention_kernel_traffic_config1.md"
+    assert bench.measured_traffic(name + " (other)") is None
+    if not f.exists():
+        assert bench.measured_traffic(name) is None
+        return
+    text = f.read_text()
+    t = bench.measured_traffic(name)
+    assert t is not None and f"traffic_bytes_per_launch: {t}" in text and f"workload: {name}" in text
     assert 40_000_000 < t < 60_000_000
+    c3 = _parse(monkeypatch, ["--workload", "config3"])
+    assert bench.measured_traffic(bench.workload_name(c3, 16, 16, 8, tuple(c3.ks))) is None
+
+
+def test_build_roofline_fields(monkeypatch):
+    import bench
+
+    a = _parse(monkeypatch, [])
+    r = bench.build_roofline(a, 8, 131072 - 96, (64, 64), 3.0)
+    # 2 T k D per iteration per head: 2 * 130976 * 64 * 128 * 8 * 10
+    assert r["estep_gflop"] == round(2 * 130976 * 64 * 128 * 8 * 10 / 1e9, 2)
+    assert r["bytes_min"] == 5 * 130976 * 128 * 2 * 8
+    assert abs(r["hbm_frac"] - r["bytes_min"] / 3e-3 / 8e12) < 1e-4

@@ -438,3 +438,30 @@ def test_select_tiles_matches_literal_tiles(oracle, seed):
         for t in tiles:   # each tile holds at most buffer_pages pages
             cells = [c for c in t[b].tolist() if c != N]
             assert sum((int(sizes[b, c]) + page - 1) // page for c in cells) <= buffer_pages
+
+
+# ------------------------------------------------------ CPU baseline step ----
+
+def test_cpu_baseline_step_matches_oracle_decode(oracle):
+    """The fp32 OpenMP decode step that bench.py times as the CPU baseline
+    computes what the oracle's decode_step computes: the same selection and
+    the same attention up to fp32 rounding."""
+    rng = np.random.default_rng(31)
+    H, G, D, L, S, N = 3, 4, 128, 3000, 40, 120
+    heads = []
+    lk = oracle.f32_to_bf16(rng.standard_normal((H, L, D)).astype(np.float32))
+    lv = oracle.f32_to_bf16(rng.standard_normal((H, L, D)).astype(np.float32))
+    for h in range(H):
+        na = int(rng.integers(80, N))
+        cuts = np.sort(rng.choice(np.arange(1, L), na - 1, replace=False))
+        offs = np.concatenate([[0], cuts, [L]]).astype(np.int32)
+        heads.append(dict(n_active=na, offsets=offs, merged=rng.standard_normal((na, D)).astype(np.float32),
+                          list_keys=lk[h], list_values=lv[h]))
+    sk = oracle.f32_to_bf16(rng.standard_normal((H, S, D)).astype(np.float32))
+    sv = oracle.f32_to_bf16(rng.standard_normal((H, S, D)).astype(np.float32))
+    q = oracle.f32_to_bf16(rng.standard_normal((H, G, D)).astype(np.float32))
+    ref, sel, m, _ = oracle.decode_step(q, heads, sk, sv, 33, N + 1, 30, 600, 70)
+    base = oracle.DecodeBaselineF32(heads, lk, lv, sk, sv, N + 1)
+    out, mb = base.step(q, 33, 30, 600, 70)
+    assert np.array_equal(mb, m)
+    assert np.allclose(out, ref, rtol=1e-4, atol=1e-5)
