@@ -49,9 +49,9 @@ namespace imi {
 
 int select_launch(const imi_select_args* a, hipStream_t stream);
 int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax);
-size_t select4_workspace_size(const imi_select_args* a);
 size_t select4_zero_bytes();
 size_t sel2_keys_bytes(const imi_select_args* a);
+size_t select4_workspace_size(const imi_select_args* a);
 
 namespace {
 
@@ -714,7 +714,6 @@ namespace {
 struct DecodeLayout {
     int32_t *cell, *off, *cnt, *prefix, *nsel, *nrows;
     int32_t *drows, *ndelta;   // delta append outputs (ring_cap > 0)
-    uint32_t* keys;            // 2-way score keys [H][npad]
     char* sel_ws;              // 4-way selection scratch (empty for 2-way)
     size_t sel_bytes;
     char* attn_ws;
@@ -737,10 +736,10 @@ DecodeLayout decode_layout(const imi_decode_args* a, void* ws) {
     const int rc = a->sel.ring_cap > 0 ? a->sel.ring_cap : 0;
     L.drows = cv.take<int32_t>(static_cast<size_t>(H) * (rc > 0 ? rc : 1));
     L.ndelta = cv.take<int32_t>(H);
-    L.keys = a->sel.parts == 2 ? cv.take<uint32_t>(sel2_keys_bytes(&a->sel) / sizeof(uint32_t)) : nullptr;
-    L.sel_bytes = a->sel.parts == 4 ? select4_workspace_size(&a->sel) : 0;
+    // the ranking pipeline's workspace (4-way, and 2-way beyond the one-kernel selection)
+    L.sel_bytes = a->sel.parts == 4 ? select4_workspace_size(&a->sel) : sel2_keys_bytes(&a->sel);
     L.sel_ws = cv.take<char>(L.sel_bytes > 0 ? L.sel_bytes : 1);
-    L.zero_bytes = a->sel.parts == 4 ? select4_zero_bytes() : 0;
+    L.zero_bytes = L.sel_bytes > 0 ? select4_zero_bytes() : 0;
     L.zero_at = L.sel_ws;
     imi_attention_args t = a->attn;
     t.workspace = nullptr;
@@ -807,13 +806,8 @@ int decode_run(const imi_decode_args* a, void* ws, hipStream_t stream) {
         if (!s.delta_rows) s.delta_rows = L.drows;
         if (!s.n_delta) s.n_delta = L.ndelta;
     }
-    if (s.parts == 4) {
-        s.workspace = L.sel_ws;
-        s.workspace_bytes = L.sel_bytes;
-    } else {
-        s.workspace = L.keys;
-        s.workspace_bytes = sel2_keys_bytes(&s);
-    }
+    s.workspace = L.sel_ws;
+    s.workspace_bytes = L.sel_bytes;
     if (phases & 1) {
         const int rc = select_launch(&s, stream);
         if (rc) return rc;

@@ -17,227 +17,19 @@
 //   select_kernel      (k0, k1 <= 128, K' <= 2048) one 1024-thread workgroup
 //                      per head scores every cell and ranks the candidates in
 //                      one pass
-//   sel2_score_kernel  (up to 16384 cells, K' <= 4096) many workgroups per
-//   + sel2_rank_kernel head score one cell per thread into order keys; one
-//                      workgroup per head then applies the ranking and budget
-//                      rules of imi_rank.hpp, the outputs and the delta match.
+//   otherwise          (k <= 256, K' <= 8192) the ranking pipeline of
+//                      imi_select4.hip over every global cell: a score
+//                      kernel of one cell per thread and many workgroups
+//                      per head, a histogram, the candidates, the ranks and
+//                      budgets in one workgroup per head.
 #include "imi_common.hpp"
-#include "imi_rank.hpp"
 
 namespace imi {
-
-constexpr int kSel2MaxCells = 16384;   // k0 * k1 one ranking workgroup holds (64 per thread)
-constexpr int kSel2Cap = 4096;         // ranked candidates of the standalone kernel
-constexpr int kSel2Block = 1024;       // keys are padded per head to a multiple of this
 
 namespace {
 
 constexpr int kMaxGroups = 8;  // query heads per KV head
 constexpr int kRingCap = 1024; // delta ring entries (4 per thread)
-constexpr int kScoreThreads = 256;
-
-struct Sel2Params {
-    const uint16_t* q;
-    const float* cent;
-    const int32_t* cnt;
-    const int32_t* off;
-    int H, G, kmax, k0, k1, ncells, npad;
-    uint32_t* keys;                    // [H][npad] order keys, 0 = empty
-    rank::Budget bud;
-    const int32_t* head_max_tokens;    // [H] or null
-    const int32_t* head_buffer_pages;  // [H] or null
-    int32_t* sel_cell;
-    int32_t* sel_offset;
-    int32_t* sel_count;
-    int32_t* sel_prefix;
-    int32_t* n_sel;
-    int32_t* n_rows;
-    int sel_cap;
-    // online index maintenance: replaced centroids and the delta ring
-    const float* shadow;
-    int shadow_rows;
-    const int32_t* upd_slot;   // [H][ncells]
-    const int32_t* upd_row;    // [H][shadow_rows]
-    const int32_t* ring_cell;
-    const int32_t* ring_row;
-    const int32_t* ring_n;
-    int ring_cap;
-    int exec_rows;
-    int32_t* delta_rows;
-    int32_t* n_delta;
-};
-
-// Score of every cell of a workgroup's 256-cell range.  C0 rows of the range
-// are read once per l0 (one thread per row, 64 fused multiply-adds), C1 rows
-// straight into registers (one per thread), q through a grouped sum in LDS.
-// ONLINE: a cell whose merged centroid was replaced (async_update.py:7-19) is
-// scored over its shadow row with the full 128-term chain.
-template <bool ONLINE>
-__global__ __launch_bounds__(kScoreThreads) void sel2_score_kernel(Sel2Params a) {
-    __shared__ __attribute__((aligned(16))) float qs[128];
-    __shared__ float p1[kScoreThreads + 2];
-    const int h = blockIdx.y, tid = threadIdx.x;
-    const int g0 = blockIdx.x * kScoreThreads;
-    const int g = g0 + tid;
-    const bool in = g < a.ncells;
-    const int gl = min(g0 + kScoreThreads, a.ncells) - 1;
-    const int r0 = g0 < a.ncells ? g0 / a.k1 : 0;
-    const int nr = g0 < a.ncells ? gl / a.k1 - r0 + 1 : 0;
-    // ---- loads, all issued before the first wait ----
-    uint16_t qv[kMaxGroups];
-    if (tid < 128) {
-#pragma unroll
-        for (int j = 0; j < kMaxGroups; ++j)
-            qv[j] = j < a.G ? a.q[(static_cast<int64_t>(h) * a.G + j) * 128 + tid] : 0;
-    }
-    const int l0 = in ? g / a.k1 : 0, l1 = in ? g - (g / a.k1) * a.k1 : 0;
-    const float4* c0 = reinterpret_cast<const float4*>(a.cent + (static_cast<int64_t>(h) * 2 + 0) * a.kmax * 64);
-    const float4* c1 = reinterpret_cast<const float4*>(a.cent + (static_cast<int64_t>(h) * 2 + 1) * a.kmax * 64);
-    float4 r0v[16], r1v[16];
-    const int myrow = tid < nr ? r0 + tid : 0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        r0v[i] = tid < nr ? c0[myrow * 16 + i] : make_float4(0, 0, 0, 0);
-        r1v[i] = c1[l1 * 16 + i];
-    }
-    const int cnt = in ? a.cnt[static_cast<int64_t>(h) * a.ncells + g] : 0;
-    int slot = -1;
-    if (ONLINE && a.upd_slot && in) slot = a.upd_slot[static_cast<int64_t>(h) * a.ncells + g];
-    if (tid < 128) {
-        float acc = 0.0f;   // grouped-query sum, g ascending (compute_impl.cu:80-87)
-#pragma unroll
-        for (int j = 0; j < kMaxGroups; ++j)
-            if (j < a.G) acc += bf16_to_f32(qv[j]);
-        qs[tid] = acc;
-    }
-    __syncthreads();
-    // chain over the first subspace, once per l0 of the range
-    if (tid < nr) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float4 qq = *reinterpret_cast<const float4*>(qs + 4 * i);
-            acc = __builtin_fmaf(qq.x, r0v[i].x, acc);
-            acc = __builtin_fmaf(qq.y, r0v[i].y, acc);
-            acc = __builtin_fmaf(qq.z, r0v[i].z, acc);
-            acc = __builtin_fmaf(qq.w, r0v[i].w, acc);
-        }
-        p1[tid] = acc;
-    }
-    __syncthreads();
-    // ... continued over the second subspace
-    float sc = p1[l0 - r0 >= 0 && l0 - r0 < nr ? l0 - r0 : 0];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const float4 qq = *reinterpret_cast<const float4*>(qs + 64 + 4 * i);
-        sc = __builtin_fmaf(qq.x, r1v[i].x, sc);
-        sc = __builtin_fmaf(qq.y, r1v[i].y, sc);
-        sc = __builtin_fmaf(qq.z, r1v[i].z, sc);
-        sc = __builtin_fmaf(qq.w, r1v[i].w, sc);
-    }
-    if (ONLINE && slot >= 0) {
-        // compute_impl.cu:80-101 over the replaced centroid
-        const int row = min(max(a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + min(slot, a.shadow_rows - 1)], 0),
-                            a.shadow_rows - 1);
-        const float4* sr = reinterpret_cast<const float4*>(a.shadow + (static_cast<int64_t>(h) * a.shadow_rows + row) * 128);
-        float acc = 0.0f;
-        for (int i = 0; i < 32; ++i) {
-            const float4 v = sr[i];
-            const float4 qq = *reinterpret_cast<const float4*>(qs + 4 * i);
-            acc = __builtin_fmaf(qq.x, v.x, acc);
-            acc = __builtin_fmaf(qq.y, v.y, acc);
-            acc = __builtin_fmaf(qq.z, v.z, acc);
-            acc = __builtin_fmaf(qq.w, v.w, acc);
-        }
-        sc = acc;
-    }
-    if (g < a.npad) a.keys[static_cast<int64_t>(h) * a.npad + g] = cnt > 0 ? order_key(sc) : 0u;
-}
-
-// One workgroup per head: rank (imi_rank.hpp), write the selection, then the
-// delta match when the ring is on.
-template <int E, bool RING>
-__global__ __launch_bounds__(rank::kThreads) void sel2_rank_kernel(Sel2Params a) {
-    extern __shared__ int lds[];
-    constexpr bool LATE = E > 16;   // sizes and offsets read for the placed candidates only
-    using Lay = rank::Layout<kSel2Cap>;
-    const int h = blockIdx.x, tid = threadIdx.x;
-    const uint32_t* kh = a.keys + static_cast<int64_t>(h) * a.npad;
-    const int32_t* ch = a.cnt + static_cast<int64_t>(h) * a.ncells;
-    const int32_t* oh = a.off + static_cast<int64_t>(h) * (a.ncells + 1);
-    uint32_t key[E];
-    int cnt[E], off[E];
-#pragma unroll
-    for (int j = 0; j < E / 4; ++j) {
-        const uint4 k4 = j * 4 * rank::kThreads < a.npad
-                             ? *reinterpret_cast<const uint4*>(kh + j * 4 * rank::kThreads + 4 * tid)
-                             : make_uint4(0u, 0u, 0u, 0u);
-        key[4 * j + 0] = k4.x;
-        key[4 * j + 1] = k4.y;
-        key[4 * j + 2] = k4.z;
-        key[4 * j + 3] = k4.w;
-    }
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int g = rank::item_cell(e, tid);
-        cnt[e] = (!LATE && g < a.ncells) ? ch[g] : 0;
-        off[e] = (!LATE && g < a.ncells) ? oh[g] : 0;
-    }
-    int rcode[4] = {-3, -3, -3, -3}, rrow[4] = {0, 0, 0, 0};
-    int rn = 0;
-    if (RING) {
-        rn = min(a.ring_n[h], a.ring_cap);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = 4 * tid + u;
-            if (i < a.ring_cap) {
-                rcode[u] = a.ring_cell[static_cast<int64_t>(h) * a.ring_cap + i];
-                rrow[u] = a.ring_row[static_cast<int64_t>(h) * a.ring_cap + i];
-            }
-        }
-    }
-    rank::Budget bud = a.bud;
-    if (a.head_max_tokens) bud.max_tokens = min(a.head_max_tokens[h], bud.max_tokens);
-    if (a.head_buffer_pages) bud.buffer_pages = min(a.head_buffer_pages[h], bud.buffer_pages);
-    int gid[E];   // unused in the blocked order (item_cell gives the cell)
-#pragma unroll
-    for (int e = 0; e < E; ++e) gid[e] = 0;
-    const rank::Result r = rank::rank_cells<E, kSel2Cap, LATE, rank::BLOCKED>(key, gid, cnt, off, E, ch, oh, bud, lds);
-    const int* sg = lds + Lay::kCk;
-    const int* ss = lds + Lay::kCk + kSel2Cap;
-    const int* so = lds + Lay::kSeg;
-    const int* sp = lds + Lay::kHist;
-    int32_t* out_cell = a.sel_cell + static_cast<int64_t>(h) * a.sel_cap;
-    int32_t* out_off = a.sel_offset + static_cast<int64_t>(h) * a.sel_cap;
-    int32_t* out_cnt = a.sel_count + static_cast<int64_t>(h) * a.sel_cap;
-    int32_t* out_pre = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
-    for (int i = tid; i < r.m; i += rank::kThreads) {
-        out_cell[i] = sg[i];
-        out_off[i] = so[i];
-        out_cnt[i] = ss[i];
-        out_pre[i] = sp[i];
-    }
-    if (tid == 0) {
-        out_pre[r.m] = r.n_rows;
-        a.n_sel[h] = r.m;
-        a.n_rows[h] = r.n_rows;
-    }
-    if (RING) {
-        // kept-token cells as a bitmap over global cell ids (in the candidate
-        // size / offset words, free after the ranking)
-        uint32_t* keep = reinterpret_cast<uint32_t*>(lds + Lay::kCs);
-        int* drow = lds + Lay::kCo;
-        for (int i = tid; i < (a.ncells + 31) / 32; i += rank::kThreads) keep[i] = 0u;
-        __syncthreads();
-        for (int i = tid; i < r.m_tok; i += rank::kThreads) atomicOr(&keep[sg[i] >> 5], 1u << (sg[i] & 31));
-        __syncthreads();
-        const int nd = rank::ring_match(rcode, rrow, rn, a.ncells, r.m_tok, a.bud.nprobe, a.exec_rows - r.n_rows,
-                                        keep, drow, lds + Lay::kSmall);
-        __syncthreads();
-        for (int i = tid; i < nd; i += rank::kThreads) a.delta_rows[static_cast<int64_t>(h) * a.ring_cap + i] = drow[i];
-        if (tid == 0) a.n_delta[h] = nd;
-    }
-}
 
 // ---------------------------------------------------------------- one-kernel path
 // select_kernel: one 1024-thread workgroup per KV head scores, ranks and
@@ -917,11 +709,11 @@ __global__ __launch_bounds__(256) void similarity_kernel(const uint16_t* q, cons
 int select4_validate(const imi_select_args* a);
 size_t select4_workspace_size(const imi_select_args* a);
 int select4_launch(const imi_select_args* a, hipStream_t stream);
-int sel2_npad(int ncells);
 
 // The one-kernel 2-way path applies while both codebooks fit 128 rows, a
 // 1024-thread workgroup holds every cell (16 per thread) and K' fits its
-// candidate buffer; larger shapes take the score + rank kernels.
+// candidate buffer; larger shapes take the ranking pipeline of
+// imi_select4.hip over every global cell.
 bool sel2_one_kernel(const imi_select_args* a) {
     if (a->parts != 2) return false;
     const int k0 = a->k[0], k1 = a->k[1];
@@ -966,92 +758,15 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     kmax = a->k[0] > a->k[1] ? a->k[0] : a->k[1];
     IMI_REQUIRE(a->k[0] >= 1 && a->k[1] >= 1 && kmax <= 256, IMI_ERR_UNSUPPORTED, "imi_select: k outside [1,256]");
     ncells = static_cast<int64_t>(a->k[0]) * a->k[1];
-    IMI_REQUIRE(ncells <= kSel2MaxCells, IMI_ERR_UNSUPPORTED,
-                "imi_select: k = (%d, %d) gives %lld cells, more than the %d one ranking workgroup holds", a->k[0],
-                a->k[1], static_cast<long long>(ncells), kSel2MaxCells);
+    if (!sel2_one_kernel(a)) return select4_validate(a);
     const bool rank_all = a->tile_mode || a->ring_cap > 0;
     const int kprime = rank_all ? a->nprobe : (a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages);
-    const int kp_eff = kprime < ncells ? kprime : static_cast<int>(ncells);
-    IMI_REQUIRE(kp_eff <= kSel2Cap, IMI_ERR_UNSUPPORTED, "imi_select: %d cells to rank exceed %d", kp_eff, kSel2Cap);
     IMI_REQUIRE(a->sel_cap >= kprime, IMI_ERR_INVALID, "imi_select: sel_cap %d < %d (%s)", a->sel_cap, kprime,
                 rank_all ? "nprobe" : "min(nprobe, buffer_pages)");
     return IMI_OK;
 }
 
 namespace {
-
-int sel2_fill(const imi_select_args* a, uint32_t* keys, Sel2Params* p) {
-    int64_t ncells;
-    int kmax;
-    int rc = select_validate(a, ncells, kmax);
-    if (rc) return rc;
-    *p = Sel2Params{};
-    p->q = a->query;
-    p->cent = a->centroids;
-    p->cnt = a->cell_count;
-    p->off = a->cell_offset;
-    p->H = a->kv_heads;
-    p->G = a->groups;
-    p->kmax = kmax;
-    p->k0 = a->k[0];
-    p->k1 = a->k[1];
-    p->ncells = static_cast<int>(ncells);
-    p->npad = sel2_npad(static_cast<int>(ncells));
-    p->keys = keys;
-    p->bud.nprobe = a->nprobe;
-    p->bud.max_tokens = a->max_tokens;
-    p->bud.buffer_pages = a->buffer_pages;
-    p->bud.page_size = a->page_size;
-    p->bud.tile_mode = a->tile_mode != 0;
-    p->bud.rank_all = a->tile_mode != 0 || a->ring_cap > 0;
-    p->head_max_tokens = a->head_max_tokens;
-    p->head_buffer_pages = a->head_buffer_pages;
-    p->sel_cell = a->sel_cell;
-    p->sel_offset = a->sel_offset;
-    p->sel_count = a->sel_count;
-    p->sel_prefix = a->sel_prefix;
-    p->n_sel = a->n_selected;
-    p->n_rows = a->n_rows;
-    p->sel_cap = a->sel_cap;
-    p->shadow = a->shadow;
-    p->shadow_rows = a->shadow_rows;
-    p->upd_slot = a->upd_slot;
-    p->upd_row = a->upd_row;
-    p->ring_cell = a->ring_cell;
-    p->ring_row = a->ring_row;
-    p->ring_n = a->ring_n;
-    p->ring_cap = a->ring_cap;
-    p->exec_rows = a->exec_rows;
-    p->delta_rows = a->delta_rows;
-    p->n_delta = a->n_delta;
-    return IMI_OK;
-}
-
-template <int E, bool RING>
-int launch_rank(const Sel2Params& p, hipStream_t stream) {
-    const size_t lds = static_cast<size_t>(rank::Layout<kSel2Cap>::kWords) * sizeof(int);
-    static bool attr_set = false;
-    if (!attr_set) {
-        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&sel2_rank_kernel<E, RING>),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-        attr_set = true;
-    }
-    hipLaunchKernelGGL((sel2_rank_kernel<E, RING>), dim3(p.H), dim3(rank::kThreads), lds, stream, p);
-    IMI_LAUNCH_CHECK("sel2_rank_kernel");
-    return IMI_OK;
-}
-
-template <bool RING>
-int launch_rank_e(const Sel2Params& p, hipStream_t stream) {
-    switch (p.npad / kSel2Block) {
-        case 1: return launch_rank<4, RING>(p, stream);
-        case 2: return launch_rank<8, RING>(p, stream);
-        case 3:
-        case 4: return launch_rank<16, RING>(p, stream);
-        case 5: case 6: case 7: case 8: return launch_rank<32, RING>(p, stream);
-        default: return launch_rank<64, RING>(p, stream);
-    }
-}
 
 template <int EPT, bool ONLINE>
 int launch_ept(const SelParams& p, int H, hipStream_t stream) {
@@ -1128,34 +843,11 @@ int select_one_kernel(const imi_select_args* a, int64_t ncells, int kmax, hipStr
 
 }  // namespace
 
-int sel2_npad(int ncells) {
-    // a multiple of 1024 whose 1024-cell blocks the ranking splits into 4, 8,
-    // 16, 32 or 64 items per thread
-    const int blocks = (ncells + kSel2Block - 1) / kSel2Block;
-    const int b = blocks <= 1 ? 1 : blocks <= 2 ? 2 : blocks <= 4 ? 4 : blocks <= 8 ? 8 : 16;
-    return b * kSel2Block;
-}
-
-// Workspace of the 2-way selection: the score keys of the two-kernel path,
-// nothing for the one-kernel path.
+// Workspace of a 2-way selection: nothing for the one-kernel path, the
+// ranking pipeline's otherwise.
 size_t sel2_keys_bytes(const imi_select_args* a) {
     if (sel2_one_kernel(a)) return 0;
-    return static_cast<size_t>(a->kv_heads) * sel2_npad(a->k[0] * a->k[1]) * sizeof(uint32_t);
-}
-
-// Scores of every cell into keys [H][npad] (the first kernel of the
-// two-kernel 2-way selection).
-int sel2_score_launch(const imi_select_args* a, uint32_t* keys, hipStream_t stream) {
-    Sel2Params p;
-    int rc = sel2_fill(a, keys, &p);
-    if (rc) return rc;
-    const dim3 grid(p.npad / kScoreThreads, p.H);
-    if (p.upd_slot)
-        hipLaunchKernelGGL(sel2_score_kernel<true>, grid, dim3(kScoreThreads), 0, stream, p);
-    else
-        hipLaunchKernelGGL(sel2_score_kernel<false>, grid, dim3(kScoreThreads), 0, stream, p);
-    IMI_LAUNCH_CHECK("sel2_score_kernel");
-    return IMI_OK;
+    return select4_workspace_size(a);
 }
 
 int select_launch(const imi_select_args* a, hipStream_t stream) {
@@ -1167,16 +859,8 @@ int select_launch(const imi_select_args* a, hipStream_t stream) {
                 IMI_ERR_INVALID, "imi_select: null output pointer");
     IMI_REQUIRE(a->ring_cap == 0 || (a->delta_rows && a->n_delta), IMI_ERR_INVALID,
                 "imi_select: null delta output pointer");
-    if (a->parts == 4) return select4_launch(a, stream);
-    if (sel2_one_kernel(a)) return select_one_kernel(a, ncells, kmax, stream);
-    IMI_REQUIRE(a->workspace && a->workspace_bytes >= sel2_keys_bytes(a), IMI_ERR_WORKSPACE,
-                "imi_select: workspace %zu bytes < %zu required", a->workspace_bytes, sel2_keys_bytes(a));
-    uint32_t* keys = static_cast<uint32_t*>(a->workspace);
-    rc = sel2_score_launch(a, keys, stream);
-    if (rc) return rc;
-    Sel2Params p;
-    sel2_fill(a, keys, &p);
-    return p.ring_cap > 0 ? launch_rank_e<true>(p, stream) : launch_rank_e<false>(p, stream);
+    if (a->parts == 2 && sel2_one_kernel(a)) return select_one_kernel(a, ncells, kmax, stream);
+    return select4_launch(a, stream);
 }
 
 }  // namespace imi

@@ -37,20 +37,22 @@ namespace imi {
 namespace {
 
 constexpr int kBins4 = 2048;
-constexpr int kCand4 = 4096;     // candidate capacity per head
-constexpr int kShards = 16;      // candidate counters per head (cell c counts in shard c % kShards)
-constexpr int kShardCap = kCand4 / kShards;
+constexpr int kCand4 = 8192;     // candidate capacity per head
+constexpr int kSegMax = 512;     // largest bucket ranked by counting (larger: a full sort)
+constexpr int kRingSet = 2048;   // ring-code set of the delta match (ring <= 1024 entries)
 constexpr int kK4 = 64;          // centroids per subspace the kernels hold
 constexpr int kDp4 = 32;         // subspace width (D = 128, 4 parts)
 constexpr int kMaxG4 = 8;        // query heads per KV head
 constexpr int kScoreThreads = 256;
 constexpr int kFinalThreads = 1024;
-constexpr int kSelCap4 = 2048;   // min(nprobe, buffer_pages) bound
+constexpr int kSelCap4 = kCand4;  // cells to rank (K') per head
 constexpr int kExtHeads = 1024;  // KV heads one call handles (fixed-place counters)
 constexpr int kCPT = 16;         // occupied cells per thread in the score / histogram / gather kernels
 constexpr int kCS4 = 36;         // LDS row stride of a subspace centroid (16-byte aligned rows)
 constexpr int kTripCap = 1024;   // (l0, l1, l2) prefixes a score workgroup keeps
 constexpr int kCellsPerBlock = kScoreThreads * kCPT;
+constexpr int kDenseScoreCells = kScoreThreads;   // 2-way score kernel: one global cell per thread
+constexpr int kDenseK = 256;                      // 2-way centroids per subspace the score kernel reads
 // the histogram kernel takes 8x more cells per workgroup: its global merge
 // (one atomic per non-empty bin and workgroup) is a per-workgroup cost
 constexpr int kHistCPT = 64;
@@ -65,7 +67,8 @@ struct Sel4 {
     const int32_t* csize;    // [H][cap]
     const int32_t* coff;     // [H][cap + 1]
     const int32_t* nact;     // [H]
-    int cap;
+    int cap;                 // cells listed per head (keys [H][cap])
+    int dense;               // 2-way: every global cell listed (cell index = id, n_active = cap, key 0 = empty)
     int nprobe, max_tokens, buffer_pages, page_size;
     const int32_t* head_max_tokens;    // [H] or null
     const int32_t* head_buffer_pages;  // [H] or null
@@ -81,10 +84,10 @@ struct Sel4 {
     uint32_t* hist;          // [H][kBins4]
     uint32_t* ext;           // [H][4]: max order key, ~min order key, unused, unused
     uint32_t* rpart;         // [H][nbs][2]: per-workgroup max order key and max ~order key
-    uint32_t* ccnt;          // [H][kShards]: candidates per shard (shard s: cand slots s * kShardCap ..)
-    int nbs;                 // score workgroups per head
-    uint64_t* cand;          // [H][kCand4]
-    int32_t* cidx;           // [H][kCand4]
+    uint32_t* bcur;          // [H][kBins4]: candidates placed per bucket (gather cursors)
+    int nbs;                 // score workgroups per head (range partials)
+    uint64_t* cand;          // [H][kCand4] candidate keys, grouped by bucket (best bucket first)
+    int32_t* cidx;           // [H][kCand4] their cell indices
     // online index maintenance: replaced centroids (by compact id) and the
     // delta ring
     const float* shadow;
@@ -110,8 +113,9 @@ __device__ __forceinline__ int bucket4(float s, float gmax, float inv) {
     return t < static_cast<float>(kBins4 - 1) ? static_cast<int>(t) : kBins4 - 1;
 }
 
-// occupied cells of head h, clamped to the compact array width
+// listed cells of head h, clamped to the array width
 __device__ __forceinline__ int n_active(const Sel4& a, int h) {
+    if (a.dense) return a.cap;
     const int na = a.nact[h];
     return na < 0 ? 0 : (na < a.cap ? na : a.cap);
 }
@@ -351,6 +355,123 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     }
 }
 
+// 2-way IMI over every global cell g = l0 * k1 + l1 (the shapes beyond the
+// one-kernel selection): the chain over C0[l0] once per l0 of the
+// workgroup's 256-cell range (one thread per row), continued per cell over
+// C1[l1] held in registers -- the same fused multiply-adds in the same order
+// as the chain over the merged centroid (compute_impl.cu:80-101).  Key =
+// (order key, ~g) of an occupied cell, 0 for an empty one (masked,
+// retrieval.py:357); one score range per workgroup.  ONLINE: a cell whose
+// merged centroid was replaced (async_update.py:7-19) is scored over its
+// shadow row with the full 128-term chain.
+template <bool ONLINE>
+__global__ __launch_bounds__(kScoreThreads) void sel2_dense_score_kernel(Sel4 a) {
+    __shared__ __attribute__((aligned(16))) float qs[128];
+    __shared__ float p1[kScoreThreads + 2];
+    __shared__ uint32_t red[kScoreThreads / 64][2];
+    const int h = blockIdx.y, tid = threadIdx.x;
+    const int k1 = a.k[1];
+    const int ncells = a.cap;
+    const int g0 = blockIdx.x * kDenseScoreCells;
+    const int g = g0 + tid;
+    const bool in = g < ncells;
+    const int gl = min(g0 + kDenseScoreCells, ncells) - 1;
+    const int r0 = g0 < ncells ? g0 / k1 : 0;
+    const int nr = g0 < ncells ? gl / k1 - r0 + 1 : 0;
+    // ---- loads, all issued before the first wait ----
+    uint16_t qv[kMaxG4];
+    if (tid < 128) {
+#pragma unroll
+        for (int j = 0; j < kMaxG4; ++j) qv[j] = j < a.G ? a.q[(static_cast<int64_t>(h) * a.G + j) * 128 + tid] : 0;
+    }
+    const int l0 = in ? g / k1 : 0, l1 = in ? g - (g / k1) * k1 : 0;
+    const float4* c0 = reinterpret_cast<const float4*>(a.cent + (static_cast<int64_t>(h) * 2 + 0) * a.kmax * 64);
+    const float4* c1 = reinterpret_cast<const float4*>(a.cent + (static_cast<int64_t>(h) * 2 + 1) * a.kmax * 64);
+    float4 r0v[16], r1v[16];
+    const int myrow = tid < nr ? r0 + tid : 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        r0v[i] = tid < nr ? c0[myrow * 16 + i] : make_float4(0, 0, 0, 0);
+        r1v[i] = c1[l1 * 16 + i];
+    }
+    const int cnt = in ? a.csize[static_cast<int64_t>(h) * ncells + g] : 0;
+    int slot = -1;
+    if (ONLINE && a.upd_slot && in) slot = a.upd_slot[static_cast<int64_t>(h) * ncells + g];
+    if (tid < 128) {
+        float acc = 0.0f;   // grouped-query sum, g ascending (compute_impl.cu:80-87)
+#pragma unroll
+        for (int j = 0; j < kMaxG4; ++j)
+            if (j < a.G) acc += bf16_to_f32(qv[j]);
+        qs[tid] = acc;
+    }
+    // this head's histogram starts at zero (the histogram kernel is the next launch)
+    for (int i = blockIdx.x * kScoreThreads + tid; i < kBins4; i += gridDim.x * kScoreThreads)
+        a.hist[static_cast<int64_t>(h) * kBins4 + i] = 0;
+    __syncthreads();
+    if (tid < nr) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float4 qq = *reinterpret_cast<const float4*>(qs + 4 * i);
+            acc = __builtin_fmaf(qq.x, r0v[i].x, acc);
+            acc = __builtin_fmaf(qq.y, r0v[i].y, acc);
+            acc = __builtin_fmaf(qq.z, r0v[i].z, acc);
+            acc = __builtin_fmaf(qq.w, r0v[i].w, acc);
+        }
+        p1[tid] = acc;
+    }
+    __syncthreads();
+    float sc = p1[l0 - r0 >= 0 && l0 - r0 < nr ? l0 - r0 : 0];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float4 qq = *reinterpret_cast<const float4*>(qs + 64 + 4 * i);
+        sc = __builtin_fmaf(qq.x, r1v[i].x, sc);
+        sc = __builtin_fmaf(qq.y, r1v[i].y, sc);
+        sc = __builtin_fmaf(qq.z, r1v[i].z, sc);
+        sc = __builtin_fmaf(qq.w, r1v[i].w, sc);
+    }
+    if (ONLINE && slot >= 0) {
+        const int row = min(max(a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + min(slot, a.shadow_rows - 1)], 0),
+                            a.shadow_rows - 1);
+        const float4* sr = reinterpret_cast<const float4*>(a.shadow + (static_cast<int64_t>(h) * a.shadow_rows + row) * 128);
+        float acc = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            const float4 v = sr[i];
+            const float4 qq = *reinterpret_cast<const float4*>(qs + 4 * i);
+            acc = __builtin_fmaf(qq.x, v.x, acc);
+            acc = __builtin_fmaf(qq.y, v.y, acc);
+            acc = __builtin_fmaf(qq.z, v.z, acc);
+            acc = __builtin_fmaf(qq.w, v.w, acc);
+        }
+        sc = acc;
+    }
+    const uint32_t ok = order_key(sc);
+    if (in)
+        a.keys[static_cast<int64_t>(h) * ncells + g] =
+            cnt > 0 ? (static_cast<uint64_t>(ok) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(g)) : 0ull;
+    uint32_t m1 = cnt > 0 ? ok : 0u, m2 = cnt > 0 ? ~ok : 0u;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        m1 = max(m1, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m1), o)));
+        m2 = max(m2, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m2), o)));
+    }
+    if (lane_id() == 0) {
+        red[tid >> 6][0] = m1;
+        red[tid >> 6][1] = m2;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t x1 = 0, x2 = 0;
+#pragma unroll
+        for (int w = 0; w < kScoreThreads / 64; ++w) {
+            x1 = max(x1, red[w][0]);
+            x2 = max(x2, red[w][1]);
+        }
+        a.rpart[(static_cast<int64_t>(h) * a.nbs + blockIdx.x) * 2 + 0] = x1;
+        a.rpart[(static_cast<int64_t>(h) * a.nbs + blockIdx.x) * 2 + 1] = x2;
+    }
+}
+
 // Score range of head h from the score kernel's per-workgroup partials
 // (every thread gets it; the workgroup 0 of each head also leaves it in ext
 // for the gather kernel).
@@ -392,7 +513,8 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_hist_kernel(Sel4 a) {
     __syncthreads();
     __shared__ uint32_t red2[kScoreThreads / 64 * 2];
     const int na = n_active(a, h);
-    if (blockIdx.x == 0 && tid < kShards) a.ccnt[h * kShards + tid] = 0;   // the gather kernel's counters
+    if (blockIdx.x == 0)   // the gather kernel's bucket cursors
+        for (int i = tid; i < kBins4; i += kScoreThreads) a.bcur[static_cast<int64_t>(h) * kBins4 + i] = 0;
     // every key of this thread in flight before the range reduction
     const uint64_t* keys = a.keys + static_cast<int64_t>(h) * a.cap;
     uint64_t kv[kHistCPT];
@@ -408,16 +530,19 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_hist_kernel(Sel4 a) {
 #pragma unroll
     for (int u = 0; u < kHistCPT; ++u) {
         const int c = blockIdx.x * kHistCellsPerBlock + u * kScoreThreads + tid;
-        if (c < na) atomicAdd(&lh[bucket4(key_score(kv[u]), gmax, inv)], 1u);
+        if (c < na && kv[u] != 0ull) atomicAdd(&lh[bucket4(key_score(kv[u]), gmax, inv)], 1u);   // 0: empty cell
     }
     __syncthreads();
     for (int i = tid; i < kBins4; i += kScoreThreads)
         if (lh[i]) atomicAdd(&a.hist[static_cast<int64_t>(h) * kBins4 + i], lh[i]);
 }
 
-// Bucket holding the kp-th best cell (buckets run from the best score down).
-__device__ int find_bucket(const Sel4& a, int h, int kp, int* sh) {
-    constexpr int PER = kBins4 / kScoreThreads;
+// Bucket holding the kp-th best cell (buckets run from the best score down;
+// the last bucket when fewer cells are listed) and the first candidate slot
+// of every bucket, binbase[b] = cells in buckets < b.  T threads.
+template <int T>
+__device__ int find_bucket(const Sel4& a, int h, int kp, int* sh, int* binbase) {
+    constexpr int PER = kBins4 / T;
     const int tid = threadIdx.x;
     int v[PER], loc = 0;
 #pragma unroll
@@ -428,23 +553,30 @@ __device__ int find_bucket(const Sel4& a, int h, int kp, int* sh) {
     const int incl = wave_incl_scan(loc);
     const int w = tid >> 6;
     if (lane_id() == 63) sh[w] = incl;
-    if (tid == 0) sh[8] = kBins4 - 1;
+    if (tid == 0) sh[32] = kBins4 - 1;
     __syncthreads();
-    int base = 0;
-    for (int j = 0; j < w; ++j) base += sh[j];
-    int run = base + incl - loc;
-    __syncthreads();
+    int run = incl - loc;
+    for (int j = 0; j < w; ++j) run += sh[j];
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
-        if (run < kp && run + v[u] >= kp) sh[8] = tid * PER + u;
+        binbase[tid * PER + u] = run;
+        if (run < kp && run + v[u] >= kp) sh[32] = tid * PER + u;
         run += v[u];
     }
+    if (tid == T - 1) binbase[kBins4] = run;
     __syncthreads();
-    return sh[8];
+    return sh[32];
 }
 
+// Candidates = the cells in the buckets up to the one holding the K'-th best
+// cell, written grouped by bucket: bucket b's cells occupy slots
+// [binbase[b], binbase[b + 1]) in any order (a workgroup adds its count per
+// bucket to a cursor once).  When they do not fit kCand4 slots nothing is
+// written; the final kernel then selects exactly.
 __global__ __launch_bounds__(kScoreThreads) void sel4_gather_kernel(Sel4 a) {
-    __shared__ int sh[16];
+    __shared__ int sh[40];
+    __shared__ int binbase[kBins4 + 1];
+    __shared__ int lcnt[kBins4];   // this workgroup's cells per bucket, then their first slot past binbase
     const int h = blockIdx.y, tid = threadIdx.x;
     const int na = n_active(a, h);
     const int kp = kprime(a, h, na);
@@ -457,27 +589,40 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_gather_kernel(Sel4 a) {
         const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
         kv[u] = c < na ? keys[c] : 0ull;
     }
-    const int bK = find_bucket(a, h, kp, sh);
+    for (int i = tid; i < kBins4; i += kScoreThreads) lcnt[i] = 0;
+    const int bK = find_bucket<kScoreThreads>(a, h, kp, sh, binbase);
+    if (binbase[bK + 1] > kCand4) return;
     const uint32_t okmax = a.ext[h * 4 + 0], okmin = ~a.ext[h * 4 + 1];
     const float gmax = key_score(static_cast<uint64_t>(okmax) << 32);
     const float gmin = key_score(static_cast<uint64_t>(okmin) << 32);
     const float range = gmax - gmin;
     const float inv = range > 0.0f ? static_cast<float>(kBins4) / range : 0.0f;
+    int bk[kCPT], lr[kCPT];
 #pragma unroll
     for (int u = 0; u < kCPT; ++u) {
-        const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
-        if (c < na && bucket4(key_score(kv[u]), gmax, inv) <= bK) {
-            // one of kShards counters per head, by cell index (the best cells
-            // cluster in id order): atomics on one word from every workgroup
-            // of a head serialise
-            const int shard = c & (kShards - 1);
-            const uint32_t slot = atomicAdd(&a.ccnt[h * kShards + shard], 1u);
-            if (slot < static_cast<uint32_t>(kShardCap)) {
-                const int64_t at = static_cast<int64_t>(h) * kCand4 + shard * kShardCap + slot;
-                a.cand[at] = kv[u];
-                a.cidx[at] = c;
+        bk[u] = kBins4;
+        lr[u] = -1;
+        if (kv[u] != 0ull) {
+            const int b = bucket4(key_score(kv[u]), gmax, inv);
+            if (b <= bK) {
+                bk[u] = b;
+                lr[u] = atomicAdd(&lcnt[b], 1);
             }
         }
+    }
+    __syncthreads();
+    for (int b = tid; b <= bK; b += kScoreThreads)
+        if (lcnt[b] > 0) lcnt[b] = static_cast<int>(atomicAdd(&a.bcur[static_cast<int64_t>(h) * kBins4 + b],
+                                                             static_cast<uint32_t>(lcnt[b])));
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        if (lr[u] < 0) continue;
+        const int slot = binbase[bk[u]] + lcnt[bk[u]] + lr[u];
+        if (slot >= kCand4) continue;   // only if the histogram disagreed with the keys
+        const int64_t at = static_cast<int64_t>(h) * kCand4 + slot;
+        a.cand[at] = kv[u];
+        a.cidx[at] = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
     }
 }
 
@@ -572,65 +717,119 @@ __device__ void bitonic_desc(uint64_t* sk, int* si, int N) {
     }
 }
 
+// Ring-code set of the delta match: open addressing over kRingSet slots
+// (at most kFinalThreads codes, so at most half full); returns the slot.
+__device__ __forceinline__ int ring_slot(int code) {
+    return static_cast<int>((static_cast<uint32_t>(code) * 2654435761u) >> (32 - 11)) & (kRingSet - 1);
+}
+__device__ int ring_insert(int* t, int code) {
+    int i = ring_slot(code);
+    while (true) {
+        const int prev = atomicCAS(&t[i], -1, code);
+        if (prev == -1 || prev == code) return i;
+        i = (i + 1) & (kRingSet - 1);
+    }
+}
+__device__ int ring_find(const int* t, int code) {
+    int i = ring_slot(code);
+    while (true) {
+        const int v = t[i];
+        if (v == code) return i;
+        if (v == -1) return -1;
+        i = (i + 1) & (kRingSet - 1);
+    }
+}
+
+constexpr int kRPT = kCand4 / kFinalThreads;   // ranks per thread of the budget rules
+
+// Final LDS: candidate keys and cell indices (slot order), the slot of each
+// rank, the bucket bases.
+constexpr size_t kFinalLds = static_cast<size_t>(kCand4) * (8 + 4 + 4) + (kBins4 + 1) * 4;
+
+// One workgroup per head: the candidates in rank order (within each bucket by
+// counting the better keys of the same bucket; a bitonic sort when a bucket
+// holds more than kSegMax; an exact radix select of the K'-th key when the
+// candidates did not fit), then the token and page budgets in rank order and
+// the outputs, then the delta match.
 template <bool ONLINE>
 __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
-    __shared__ uint64_t sk[kCand4];
-    __shared__ int si[kCand4];
+    extern __shared__ __attribute__((aligned(16))) uint64_t f_lds[];
+    uint64_t* sk = f_lds;                                  // [kCand4]
+    int* si = reinterpret_cast<int*>(sk + kCand4);        // [kCand4]
+    int* ord = si + kCand4;                                // [kCand4] slot of rank r
+    int* binbase = ord + kCand4;                           // [kBins4 + 1]
     __shared__ int sh[48];
     __shared__ int shk[kFinalThreads / 64];
     __shared__ int s_rows;
     __shared__ uint32_t h256[256];
-    __shared__ int s_spre[kShards + 1];
-    __shared__ int s_over;
     const int h = blockIdx.x, tid = threadIdx.x;
     const int na = n_active(a, h);
     const int kp = kprime(a, h, na);
     int32_t* prefix_out = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
-    // every candidate slot is read before the shard counts are known (one
-    // round trip for both); slots past a shard's count are ignored
-    constexpr int kSlotsPT = kCand4 / kFinalThreads;
-    uint64_t pk[kSlotsPT];
-    int pi[kSlotsPT];
+    // every candidate slot is read before the count is known (one round
+    // trip for both); slots past the count are ignored
+    uint64_t pk[kRPT];
+    int pi[kRPT];
 #pragma unroll
-    for (int u = 0; u < kSlotsPT; ++u) {
+    for (int u = 0; u < kRPT; ++u) {
         const int64_t at = static_cast<int64_t>(h) * kCand4 + tid + u * kFinalThreads;
         pk[u] = a.cand[at];
         pi[u] = a.cidx[at];
     }
-    // the gather's shard counts: prefix over the shards, overflow of any
-    if (tid < 64) {
-        const uint32_t cnt = tid < kShards ? a.ccnt[h * kShards + tid] : 0u;
-        const int v = static_cast<int>(min(cnt, static_cast<uint32_t>(kShardCap)));
-        const int incl = wave_incl_scan(v);
-        if (tid < kShards) s_spre[tid + 1] = incl;
-        if (tid == 0) s_spre[0] = 0;
-        const bool over = __builtin_amdgcn_ballot_w64(cnt > static_cast<uint32_t>(kShardCap)) != 0;
-        if (tid == 0) s_over = over ? 1 : 0;
-    }
-    __syncthreads();
-    int n = 0;   // sorted candidates in sk / si, best first
-    if (kp > 0 && !s_over) {
-        n = s_spre[kShards];
-        int N = 1;
-        while (N < n) N <<= 1;
+    const int bK = find_bucket<kFinalThreads>(a, h, kp, sh, binbase);
+    const int n_c = binbase[bK + 1];
+    int n = 0;   // ranked candidates; ord[r] = slot of rank r
+    if (kp > 0 && n_c <= kCand4) {
+        n = n_c;
 #pragma unroll
-        for (int u = 0; u < kSlotsPT; ++u) {
+        for (int u = 0; u < kRPT; ++u) {
             const int i = tid + u * kFinalThreads;
-            const int sh_ = i / kShardCap, j = i % kShardCap;
-            if (j < s_spre[sh_ + 1] - s_spre[sh_]) {
-                sk[s_spre[sh_] + j] = pk[u];
-                si[s_spre[sh_] + j] = pi[u];
+            if (i < n) {
+                sk[i] = pk[u];
+                si[i] = pi[u];
             }
         }
-        for (int i = n + tid; i < N; i += kFinalThreads) {
-            sk[i] = 0ull;
-            si[i] = -1;
-        }
+        int seg = 0;   // largest bucket among the candidates
+        for (int b = tid; b <= bK; b += kFinalThreads) seg = max(seg, binbase[b + 1] - binbase[b]);
+        seg = wave_max_i(seg);
+        if (lane_id() == 0) shk[tid >> 6] = seg;
         __syncthreads();
-        bitonic_desc(sk, si, N);
+        seg = 0;
+        for (int w = 0; w < kFinalThreads / 64; ++w) seg = max(seg, shk[w]);
+        if (seg <= kSegMax) {
+            const uint32_t okmax = a.ext[h * 4 + 0], okmin = ~a.ext[h * 4 + 1];
+            const float gmax = key_score(static_cast<uint64_t>(okmax) << 32);
+            const float gmin = key_score(static_cast<uint64_t>(okmin) << 32);
+            const float range = gmax - gmin;
+            const float inv = range > 0.0f ? static_cast<float>(kBins4) / range : 0.0f;
+#pragma unroll
+            for (int u = 0; u < kRPT; ++u) {
+                const int i = tid + u * kFinalThreads;
+                if (i < n) {
+                    const uint64_t key = pk[u];
+                    const int b = bucket4(key_score(key), gmax, inv);
+                    const int s0 = binbase[b], s1 = binbase[b + 1];
+                    int better = 0;
+                    for (int j = s0; j < s1; ++j) better += sk[j] > key ? 1 : 0;
+                    ord[min(s0 + better, kCand4 - 1)] = i;
+                }
+            }
+            __syncthreads();
+        } else {
+            int N = 1;
+            while (N < n) N <<= 1;
+            for (int i = n + tid; i < N; i += kFinalThreads) {
+                sk[i] = 0ull;
+                si[i] = -1;
+            }
+            __syncthreads();
+            bitonic_desc(sk, si, N);
+            for (int i = tid; i < n; i += kFinalThreads) ord[i] = i;
+            __syncthreads();
+        }
     } else if (kp > 0) {
         // Exact radix select of the kp-th largest key (keys are unique),
-        // then every key at or above it.
+        // then every key at or above it, sorted.
         const uint64_t* keys = a.keys + static_cast<int64_t>(h) * a.cap;
         uint64_t prefix = 0, mask = 0;
         int remaining = kp;
@@ -640,7 +839,7 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
             __syncthreads();
             for (int c = tid; c < na; c += kFinalThreads) {
                 const uint64_t key = keys[c];
-                if ((key & mask) == prefix) atomicAdd(&h256[(key >> shift) & 255u], 1u);
+                if (key != 0ull && (key & mask) == prefix) atomicAdd(&h256[(key >> shift) & 255u], 1u);
             }
             __syncthreads();
             if (tid == 0) {
@@ -665,14 +864,16 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
         __syncthreads();
         for (int c = tid; c < na; c += kFinalThreads) {
             const uint64_t key = keys[c];
-            if (key >= prefix) {
+            if (key != 0ull && key >= prefix) {
                 const int slot = atomicAdd(&sh[42], 1);
-                sk[slot] = key;
-                si[slot] = c;
+                if (slot < kCand4) {   // exactly kp keys (keys are unique)
+                    sk[slot] = key;
+                    si[slot] = c;
+                }
             }
         }
         __syncthreads();
-        n = sh[42];   // == kp
+        n = min(sh[42], kCand4);   // == kp
         int N = 1;
         while (N < n) N <<= 1;
         for (int i = n + tid; i < N; i += kFinalThreads) {
@@ -681,25 +882,32 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
         }
         __syncthreads();
         bitonic_desc(sk, si, N);
+        for (int i = tid; i < n; i += kFinalThreads) ord[i] = i;
+        __syncthreads();
     }
 
-    // budget rules in rank order over the best kp cells (ranks 2*tid, 2*tid+1)
+    // budget rules in rank order over the best kp cells: ranks kRPT*tid + u
     const int C = n < kp ? n : kp;
-    int s2[2] = {0, 0}, pg2[2] = {0, 0}, c2[2] = {-1, -1}, o2[2] = {0, 0};
+    int s2[kRPT], pg2[kRPT], o2[kRPT];
+    uint32_t g2[kRPT];
     int tsum = 0, psum = 0;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int r = 2 * tid + u;
+    for (int u = 0; u < kRPT; ++u) {
+        const int r = kRPT * tid + u;
+        s2[u] = 0;
+        o2[u] = 0;
+        g2[u] = 0;
         if (r < C) {   // size and CSR offset in one round trip
-            c2[u] = si[r];
-            s2[u] = a.csize[static_cast<int64_t>(h) * a.cap + c2[u]];
-            o2[u] = a.coff[static_cast<int64_t>(h) * (a.cap + 1) + c2[u]];
+            const int slot = min(max(ord[r], 0), kCand4 - 1);
+            const int c = min(max(si[slot], 0), a.cap - 1);
+            g2[u] = 0xFFFFFFFFu - static_cast<uint32_t>(sk[slot] & 0xFFFFFFFFull);
+            s2[u] = a.csize[static_cast<int64_t>(h) * a.cap + c];
+            o2[u] = a.coff[static_cast<int64_t>(h) * (a.cap + 1) + c];
         }
     }
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        // pages = ceil(size / page_size); a power-of-two page size (8 in every
-        // configuration) takes a shift instead of an integer division
+    for (int u = 0; u < kRPT; ++u) {
+        // pages = ceil(size / page_size); a power-of-two page size takes a shift
         pg2[u] = (a.page_size & (a.page_size - 1)) == 0 ? (s2[u] + a.page_size - 1) >> (__builtin_ctz(a.page_size))
                                                         : (s2[u] + a.page_size - 1) / a.page_size;
         if (a.tile_mode) pg2[u] = pg2[u] > head_pages(a, h) ? 1 : 0;   // cells that alone overflow
@@ -711,10 +919,10 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     block_scan2(tincl, pincl, sh, ttot, ptot);
     int texcl = tincl - tsum, pexcl = pincl - psum;
     int kept = 0, kept_tok = 0;
-    int excl_tok[2];
+    int excl_tok[kRPT];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int r = 2 * tid + u;
+    for (int u = 0; u < kRPT; ++u) {
+        const int r = kRPT * tid + u;
         excl_tok[u] = texcl;
         pexcl += pg2[u];
         const bool keep_tok = r < C && r < a.nprobe && texcl < head_tokens(a, h);
@@ -743,10 +951,10 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     int32_t* out_off = a.sel_offset + static_cast<int64_t>(h) * a.sel_cap;
     int32_t* out_cnt = a.sel_count + static_cast<int64_t>(h) * a.sel_cap;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int r = 2 * tid + u;
+    for (int u = 0; u < kRPT; ++u) {
+        const int r = kRPT * tid + u;
         if (r < m) {
-            out_cell[r] = static_cast<int32_t>(0xFFFFFFFFu - static_cast<uint32_t>(sk[r] & 0xFFFFFFFFull));
+            out_cell[r] = static_cast<int32_t>(g2[u]);
             out_off[r] = o2[u];
             out_cnt[r] = s2[u];
             prefix_out[r] = excl_tok[u];
@@ -768,25 +976,37 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     if (tid < 4) a.ext[h * 4 + tid] = 0;
     if (ONLINE && a.ring_cap > 0) {
         // Delta append (async_update.py:20-76): the ring entries whose cell
-        // is one of the m_tok cells that pass nprobe and the token budget
-        // (global ids, in si once the ranks are read), or the padding id when
-        // m_tok < nprobe, up to the execution-buffer rows left.
-        int* table = si;
-        __syncthreads();
+        // is one of the m_tok cells that pass nprobe and the token budget,
+        // or the padding id when m_tok < nprobe, up to the execution-buffer
+        // rows left.  The ring's cell codes go to a set; every kept-token
+        // cell marks its code's slot.
+        int* rtab = ord;
+        int* rhit = ord + kRingSet;
+        __syncthreads();   // ord fully read above
         const int rows_sel = m > 0 ? s_rows : 0;
-        for (int i = tid; i < kSetSize; i += kFinalThreads) table[i] = -1;
-        __syncthreads();
-        for (int r = tid; r < m_tok; r += kFinalThreads)
-            set_insert(table, static_cast<int>(0xFFFFFFFFu - static_cast<uint32_t>(sk[r] & 0xFFFFFFFFull)));
+        for (int i = tid; i < kRingSet; i += kFinalThreads) {
+            rtab[i] = -1;
+            rhit[i] = 0;
+        }
         __syncthreads();
         const int nvalid = min(a.ring_n[h], a.ring_cap);
-        bool match = false;
-        int rrow = 0;
+        int code = -3, rrow = 0, rs = -1;
         if (tid < nvalid) {
-            const int code = a.ring_cell[static_cast<int64_t>(h) * a.ring_cap + tid];
+            code = a.ring_cell[static_cast<int64_t>(h) * a.ring_cap + tid];
             rrow = a.ring_row[static_cast<int64_t>(h) * a.ring_cap + tid];
-            match = code >= 0 ? set_find(table, code) : (code == -1 && m_tok < a.nprobe);
+            if (code >= 0) rs = ring_insert(rtab, code);
         }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < kRPT; ++u) {
+            const int r = kRPT * tid + u;
+            if (r < m_tok) {
+                const int f = ring_find(rtab, static_cast<int>(g2[u]));
+                if (f >= 0) rhit[f] = 1;
+            }
+        }
+        __syncthreads();
+        const bool match = code >= 0 ? rhit[rs] != 0 : (code == -1 && m_tok < a.nprobe);
         int f = match ? 1 : 0, z = 0, tot, ztot;
         block_scan2(f, z, sh, tot, ztot);
         const int pos = f - (match ? 1 : 0);
@@ -803,11 +1023,13 @@ size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
     // call leaves them zero, so one zero-filled buffer serves calls of any
     // shape; the histogram is cleared by the score kernel of each call.
     uint32_t* ext = cv.take<uint32_t>(static_cast<size_t>(kExtHeads) * 4);
-    const int nbs = (a->compact_cap + kCellsPerBlock - 1) / kCellsPerBlock;
+    const bool dense = a->parts == 2;
+    const int cap = dense ? a->k[0] * a->k[1] : a->compact_cap;
+    const int nbs = dense ? (cap + kDenseScoreCells - 1) / kDenseScoreCells : (cap + kCellsPerBlock - 1) / kCellsPerBlock;
     uint32_t* rpart = cv.take<uint32_t>(H * static_cast<size_t>(nbs) * 2);
-    uint32_t* ccnt = cv.take<uint32_t>(H * kShards);
+    uint32_t* bcur = cv.take<uint32_t>(H * kBins4);
     uint32_t* hist = cv.take<uint32_t>(H * kBins4);
-    uint64_t* keys = cv.take<uint64_t>(H * a->compact_cap);
+    uint64_t* keys = cv.take<uint64_t>(H * static_cast<size_t>(cap));
     uint64_t* cand = cv.take<uint64_t>(H * kCand4);
     int32_t* cidx = cv.take<int32_t>(H * kCand4);
     if (p) {
@@ -815,8 +1037,10 @@ size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
         p->hist = hist;
         p->ext = ext;
         p->rpart = rpart;
-        p->ccnt = ccnt;
+        p->bcur = bcur;
         p->nbs = nbs;
+        p->cap = cap;
+        p->dense = dense ? 1 : 0;
         p->cand = cand;
         p->cidx = cidx;
     }
@@ -825,21 +1049,34 @@ size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
 
 }  // namespace
 
+// The ranking pipeline: 4-way over the occupied cells, or (parts = 2) a 2-way
+// IMI over every global cell beyond the one-kernel selection's bounds.
 int select4_validate(const imi_select_args* a) {
-    IMI_REQUIRE(a->dim == 128 && a->parts == 4, IMI_ERR_UNSUPPORTED, "imi_select: 4-way path needs D=128, parts=4");
-    IMI_REQUIRE(a->kv_heads <= kExtHeads, IMI_ERR_UNSUPPORTED, "imi_select: 4-way path handles at most %d KV heads",
-                kExtHeads);
+    const bool dense = a->parts == 2;
+    IMI_REQUIRE(a->dim == 128 && (a->parts == 4 || dense), IMI_ERR_UNSUPPORTED,
+                "imi_select: the ranking pipeline needs D=128 and parts 2 or 4");
+    IMI_REQUIRE(a->kv_heads <= kExtHeads, IMI_ERR_UNSUPPORTED, "imi_select: at most %d KV heads per call", kExtHeads);
     IMI_REQUIRE(a->groups >= 1 && a->groups <= kMaxG4, IMI_ERR_UNSUPPORTED,
                 "imi_select: %d query heads per kv head exceed %d", a->groups, kMaxG4);
-    for (int p = 0; p < 4; ++p)
-        IMI_REQUIRE(a->k[p] >= 1 && a->k[p] <= kK4, IMI_ERR_UNSUPPORTED,
-                    "imi_select: 4-way k[%d]=%d outside [1,%d]", p, a->k[p], kK4);
-    IMI_REQUIRE(a->compact_gid && a->compact_size && a->compact_offset && a->n_active && a->compact_cap > 0,
-                IMI_ERR_INVALID, "imi_select: 4-way selection needs the compact cell arrays");
+    int64_t cells_max;
+    if (dense) {
+        for (int p = 0; p < 2; ++p)
+            IMI_REQUIRE(a->k[p] >= 1 && a->k[p] <= kDenseK, IMI_ERR_UNSUPPORTED,
+                        "imi_select: 2-way k[%d]=%d outside [1,%d]", p, a->k[p], kDenseK);
+        cells_max = static_cast<int64_t>(a->k[0]) * a->k[1];
+    } else {
+        for (int p = 0; p < 4; ++p)
+            IMI_REQUIRE(a->k[p] >= 1 && a->k[p] <= kK4, IMI_ERR_UNSUPPORTED,
+                        "imi_select: 4-way k[%d]=%d outside [1,%d]", p, a->k[p], kK4);
+        IMI_REQUIRE(a->compact_gid && a->compact_size && a->compact_offset && a->n_active && a->compact_cap > 0,
+                    IMI_ERR_INVALID, "imi_select: 4-way selection needs the compact cell arrays");
+        cells_max = a->compact_cap;
+    }
     const bool rank_all = a->tile_mode || a->ring_cap > 0;
     const int kprime_max = rank_all ? a->nprobe : (a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages);
-    IMI_REQUIRE(kprime_max <= kSelCap4, IMI_ERR_UNSUPPORTED, "imi_select: %d cells to rank exceed %d", kprime_max,
-                kSelCap4);
+    const int64_t kp_eff = kprime_max < cells_max ? kprime_max : cells_max;
+    IMI_REQUIRE(kp_eff <= kSelCap4, IMI_ERR_UNSUPPORTED, "imi_select: %lld cells to rank exceed %d",
+                static_cast<long long>(kp_eff), kSelCap4);
     IMI_REQUIRE(a->sel_cap >= kprime_max, IMI_ERR_INVALID, "imi_select: sel_cap %d < %d (%s)", a->sel_cap,
                 kprime_max, rank_all ? "nprobe" : "min(nprobe, buffer_pages)");
     return IMI_OK;
@@ -867,15 +1104,15 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     p.H = a->kv_heads;
     p.G = a->groups;
     p.kmax = 0;
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < a->parts; ++i) {
         p.k[i] = a->k[i];
         p.kmax = a->k[i] > p.kmax ? a->k[i] : p.kmax;
     }
-    p.gid = a->compact_gid;
-    p.csize = a->compact_size;
-    p.coff = a->compact_offset;
-    p.nact = a->n_active;
-    p.cap = a->compact_cap;
+    const bool dense = p.dense != 0;
+    p.gid = dense ? nullptr : a->compact_gid;
+    p.csize = dense ? a->cell_count : a->compact_size;
+    p.coff = dense ? a->cell_offset : a->compact_offset;
+    p.nact = dense ? nullptr : a->n_active;
     p.nprobe = a->nprobe;
     p.max_tokens = a->max_tokens;
     p.buffer_pages = a->buffer_pages;
@@ -901,31 +1138,48 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     p.exec_rows = a->exec_rows;
     p.delta_rows = a->delta_rows;
     p.n_delta = a->n_delta;
-    const dim3 grid(p.nbs, a->kv_heads);
-    // C0..C3 rows at the padded stride, the chain prefixes per (l0, l1) pair and per triple
-    const size_t score_lds =
-        (static_cast<size_t>(4) * p.kmax * kCS4 + static_cast<size_t>(a->k[0]) * a->k[1] + kTripCap) * sizeof(float);
     const bool online = p.upd_slot || p.ring_cap > 0;
-    bool pow2 = true;
-    for (int i = 0; i < 4; ++i) pow2 = pow2 && (a->k[i] & (a->k[i] - 1)) == 0;
-    if (online && pow2)
-        hipLaunchKernelGGL((sel4_score_kernel<true, true>), grid, dim3(kScoreThreads), score_lds, stream, p);
-    else if (online)
-        hipLaunchKernelGGL((sel4_score_kernel<true, false>), grid, dim3(kScoreThreads), score_lds, stream, p);
-    else if (pow2)
-        hipLaunchKernelGGL((sel4_score_kernel<false, true>), grid, dim3(kScoreThreads), score_lds, stream, p);
-    else
-        hipLaunchKernelGGL((sel4_score_kernel<false, false>), grid, dim3(kScoreThreads), score_lds, stream, p);
-    IMI_LAUNCH_CHECK("sel4_score_kernel");
-    const dim3 grid_h((a->compact_cap + kHistCellsPerBlock - 1) / kHistCellsPerBlock, a->kv_heads);
+    if (dense) {
+        const dim3 grid_s(p.nbs, a->kv_heads);
+        if (p.upd_slot)
+            hipLaunchKernelGGL((sel2_dense_score_kernel<true>), grid_s, dim3(kScoreThreads), 0, stream, p);
+        else
+            hipLaunchKernelGGL((sel2_dense_score_kernel<false>), grid_s, dim3(kScoreThreads), 0, stream, p);
+        IMI_LAUNCH_CHECK("sel2_dense_score_kernel");
+    } else {
+        const dim3 grid(p.nbs, a->kv_heads);
+        // C0..C3 rows at the padded stride, the chain prefixes per (l0, l1) pair and per triple
+        const size_t score_lds = (static_cast<size_t>(4) * p.kmax * kCS4 + static_cast<size_t>(a->k[0]) * a->k[1] +
+                                  kTripCap) * sizeof(float);
+        bool pow2 = true;
+        for (int i = 0; i < 4; ++i) pow2 = pow2 && (a->k[i] & (a->k[i] - 1)) == 0;
+        if (online && pow2)
+            hipLaunchKernelGGL((sel4_score_kernel<true, true>), grid, dim3(kScoreThreads), score_lds, stream, p);
+        else if (online)
+            hipLaunchKernelGGL((sel4_score_kernel<true, false>), grid, dim3(kScoreThreads), score_lds, stream, p);
+        else if (pow2)
+            hipLaunchKernelGGL((sel4_score_kernel<false, true>), grid, dim3(kScoreThreads), score_lds, stream, p);
+        else
+            hipLaunchKernelGGL((sel4_score_kernel<false, false>), grid, dim3(kScoreThreads), score_lds, stream, p);
+        IMI_LAUNCH_CHECK("sel4_score_kernel");
+    }
+    const dim3 grid_h((p.cap + kHistCellsPerBlock - 1) / kHistCellsPerBlock, a->kv_heads);
     hipLaunchKernelGGL(sel4_hist_kernel, grid_h, dim3(kScoreThreads), 0, stream, p);
     IMI_LAUNCH_CHECK("sel4_hist_kernel");
-    hipLaunchKernelGGL(sel4_gather_kernel, grid, dim3(kScoreThreads), 0, stream, p);
+    const dim3 grid_g((p.cap + kCellsPerBlock - 1) / kCellsPerBlock, a->kv_heads);
+    hipLaunchKernelGGL(sel4_gather_kernel, grid_g, dim3(kScoreThreads), 0, stream, p);
     IMI_LAUNCH_CHECK("sel4_gather_kernel");
+    static bool attr_set[2] = {false, false};
+    if (!attr_set[online]) {
+        IMI_HIP_CHECK(hipFuncSetAttribute(online ? reinterpret_cast<const void*>(&sel4_final_kernel<true>)
+                                                 : reinterpret_cast<const void*>(&sel4_final_kernel<false>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kFinalLds)));
+        attr_set[online] = true;
+    }
     if (online)
-        hipLaunchKernelGGL(sel4_final_kernel<true>, dim3(a->kv_heads), dim3(kFinalThreads), 0, stream, p);
+        hipLaunchKernelGGL(sel4_final_kernel<true>, dim3(a->kv_heads), dim3(kFinalThreads), kFinalLds, stream, p);
     else
-        hipLaunchKernelGGL(sel4_final_kernel<false>, dim3(a->kv_heads), dim3(kFinalThreads), 0, stream, p);
+        hipLaunchKernelGGL(sel4_final_kernel<false>, dim3(a->kv_heads), dim3(kFinalThreads), kFinalLds, stream, p);
     IMI_LAUNCH_CHECK("sel4_final_kernel");
     return IMI_OK;
 }

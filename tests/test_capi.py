@@ -92,10 +92,13 @@ def test_select_and_decode_argument_checks(L):
     assert L.imi_select(ctypes.byref(s), None) == 1          # ... and the occupied-cell arrays
     assert "compact cell arrays" in L.imi_last_error().decode()
     s.compact_gid = s.compact_size = s.compact_offset = s.n_active = 16
+    s.compact_cap = 20000
+    s.nprobe = s.buffer_pages = 9000
+    assert L.imi_select(ctypes.byref(s), None) == 3          # top-k beyond the ranking capacity
+    assert "exceed 8192" in L.imi_last_error().decode()
     s.compact_cap = 4096
-    s.nprobe = s.buffer_pages = 3000
-    assert L.imi_select(ctypes.byref(s), None) == 3          # top-k beyond the 4-way bound
-    assert "exceed 2048" in L.imi_last_error().decode()
+    s.nprobe = s.buffer_pages = 9000                         # ... bounded by the occupied cells
+    assert L.imi_select(ctypes.byref(s), None) == 1 and "sel_cap" in L.imi_last_error().decode()
     s.nprobe = s.buffer_pages = 410
     s.sel_cell = s.sel_offset = s.sel_count = s.sel_prefix = s.n_selected = s.n_rows = 16
     need = ctypes.c_size_t()
@@ -104,10 +107,10 @@ def test_select_and_decode_argument_checks(L):
     assert "workspace" in L.imi_last_error().decode()
     s.parts = 2   # 2-way within the one-kernel bounds (k <= 128, K' <= 2048): no workspace
     assert L.imi_select_workspace_size(ctypes.byref(s), ctypes.byref(need)) == 0 and need.value == 0
-    s.k[0], s.nprobe, s.buffer_pages = 200, 3000, 3000   # beyond them: one score key per cell, padded to 1024
+    s.k[0], s.nprobe, s.buffer_pages = 200, 3000, 3000   # beyond them: the ranking pipeline's keys and candidates
     s.sel_cap = 3000
     assert L.imi_select_workspace_size(ctypes.byref(s), ctypes.byref(need)) == 0
-    assert need.value == 8 * 16 * 1024 * 4   # 12800 cells: 13 blocks, padded to 16
+    assert need.value >= 8 * (200 * 64 * 8 + 8192 * 12)   # a 64-bit key per cell, 8192 candidates per head
     s.k[0], s.nprobe, s.buffer_pages, s.sel_cap = 64, 410, 410, 410
     s.sel_cap = 100
     assert L.imi_select(ctypes.byref(s), None) == 1
@@ -222,7 +225,9 @@ def test_check_decode_limits_rejects_before_any_build(L):
     ops.check_decode_limits(8, 4, (64, 64), ops.Budget(410, 13097, 1638))
     ops.check_decode_limits(8, 4, (181, 90), ops.Budget(1638, 52000, 1638))      # 2-way k above 128
     ops.check_decode_limits(8, 4, (32, 32, 32, 32), ops.Budget(16390, 4096, 512))
-    with pytest.raises(IMIError, match="cells"):
-        ops.check_decode_limits(8, 4, (256, 128), ops.Budget(410, 13097, 1638))   # 32768 cells per head
+    ops.check_decode_limits(8, 4, (256, 256), ops.Budget(6554, 100000, 6554))  # 2-way at 1M
+    ops.check_decode_limits(8, 4, (16, 16, 16, 16), ops.Budget(6554, 100000, 2000), online=True)   # 4-way 1M, async
     with pytest.raises(IMIError, match="rank"):
-        ops.check_decode_limits(8, 4, (128, 128), ops.Budget(5000, 60000, 5000))  # K' above the ranking capacity
+        ops.check_decode_limits(8, 4, (128, 128), ops.Budget(9000, 90000, 9000))  # K' above the ranking capacity
+    with pytest.raises(IMIError, match="k"):
+        ops.check_decode_limits(8, 4, (512, 64), ops.Budget(410, 13097, 1638))    # 2-way k above 256

@@ -170,12 +170,15 @@ def _select_oracle(oracle, orc, q, out, sz, bud, exec_rows, ncells):
     return cells, rm, rtok, dr
 
 
-@pytest.mark.parametrize("ks", [(32, 32), (128, 128), (6, 6, 6, 6), (8, 8, 8, 8)])
-def test_select_with_replaced_centroids_and_delta(ops, oracle, ks):
+@pytest.mark.parametrize("ks,T", [((32, 32), 6000), ((128, 128), 6000), ((6, 6, 6, 6), 6000), ((8, 8, 8, 8), 6000),
+                                  # the 1M 4-way config's sizing (adaptive k 16, budget 0.1): nprobe 6554, all of it
+                                  # ranked for the delta match; 2-way past the one-kernel selection (k 181)
+                                  ((16, 16, 16, 16), 120000), ((181, 181), 60000)])
+def test_select_with_replaced_centroids_and_delta(ops, oracle, ks, T):
     from adaptiveimi_amd import synthetic
 
-    note(f"[online] selection ks={ks}")
-    H, T, B, G = 8, 6000, 8, 4
+    note(f"[online] selection ks={ks} T={T}")
+    H, B, G = 8, 8, 4
     keys, _, cent, out, ncells = _built(ops, H, T, ks, 71)
     upd, orc = _state(ops, oracle, out, ks, ncells, threshold=2, ring_cap=64)
     steady = _decode_keys(keys, H, 6 * B, seed=9)
@@ -187,6 +190,8 @@ def test_select_with_replaced_centroids_and_delta(ops, oracle, ks):
         orc.refresh()
     sz = oracle.sizing(T, 0.1, subspace_parts=len(ks), k_override=ks)
     bud = ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"])
+    if ks == (16, 16, 16, 16):
+        assert bud.nprobe == 6554
     compact = out if len(ks) == 4 else None
     # queries aimed at the decode keys (so replaced cells rank high) and plain ones
     qs = [(steady[:, :G].float() * 2).to(torch.bfloat16), synthetic.make_queries(keys, G, seed=4)[0]]

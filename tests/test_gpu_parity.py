@@ -341,6 +341,9 @@ def test_similarities_bit_exact(ops, oracle):
     (60000, (256, 64), 0.05, 4, 7),      # k0 = 256: score + rank kernels
     (100000, (128, 128), 0.2, 4, 8),     # K' = 2500 pages > 2048: score + rank kernels
     (50000, (200, 80), 0.3, 8, 9),       # 16000 cells, K' = 4096 nprobe < 4688 pages
+    (120000, (181, 181), 0.1, 4, 10),    # the 2-way adaptive k at 512k: 32761 cells
+    (200000, (256, 256), 0.06, 4, 11),   # ... and at 1M: 65536 cells, K' = 1500 pages
+    (150000, (128, 128), 0.45, 4, 12),   # K' = 7373 nprobe < 8438 pages: near the ranking capacity
 ])
 def test_select_bit_exact(ops, oracle, T, ks, budget, G, seed):
     note(f"[select] T={T} ks={ks} budget={budget} G={G}")
@@ -374,7 +377,8 @@ def test_select_bit_exact(ops, oracle, T, ks, budget, G, seed):
     (20000, (8, 8, 8, 8), 0.1, 8, 0),
     (30000, (16, 16, 16, 16), 0.05, 4, 1),
     (12000, (5, 7, 6, 4), 0.2, 7, 2),
-    (40000, (8, 8, 8, 8), 0.5, 4, 3),    # nprobe = 2048 < buffer_pages: the ranking capacity
+    (40000, (8, 8, 8, 8), 0.5, 4, 3),    # nprobe = 2048 < buffer_pages
+    (120000, (16, 16, 16, 16), 0.25, 4, 4),   # K' = 3750 pages < nprobe 16384
 ])
 def test_select_4way_bit_exact(ops, oracle, T, ks, budget, G, seed):
     """4-way IMI selection over the occupied cells (the reference scores the
