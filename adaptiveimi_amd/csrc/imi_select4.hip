@@ -164,25 +164,38 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     const int pair_cap = a.k[0] * a.k[1];
     float* p012 = p01 + pair_cap;
     const int h = blockIdx.y, tid = threadIdx.x;
-    const int na = n_active(a, h);
-    // the block's cells (ascending global id): their ids, loaded first
+    // the block's cells (ascending global id): their ids, loaded with the
+    // occupied-cell count (reads past it stay inside the [H][cap] arrays and
+    // are masked once the count is known)
     uint32_t gv[kCPT];
 #pragma unroll
     for (int u = 0; u < kCPT; ++u) {
         const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
-        gv[u] = c < na ? static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c]) : 0u;
+        gv[u] = c < a.cap ? static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c]) : 0u;
     }
+    const int na = n_active(a, h);
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u)
+        if (blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid >= na) gv[u] = 0u;
     const int c_first = blockIdx.x * kCellsPerBlock;
     const int c_last = min(na, c_first + kCellsPerBlock) - 1;
     const uint32_t k23 = static_cast<uint32_t>(a.k[2]) * static_cast<uint32_t>(a.k[3]);
     const uint32_t k3 = static_cast<uint32_t>(a.k[3]), k2 = static_cast<uint32_t>(a.k[2]);
-    if (tid == 0 && c_first <= c_last) {
-        const uint32_t g0 = static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c_first]);
-        const uint32_t g1 = static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c_last]);
-        s_pair[0] = static_cast<int>(kdiv<POW2>(g0, k23));
-        s_pair[1] = static_cast<int>(kdiv<POW2>(g1, k23));
-        s_trip[0] = static_cast<int>(kdiv<POW2>(g0, k3));
-        s_trip[1] = static_cast<int>(kdiv<POW2>(g1, k3));
+    // the range of (l0, l1) pairs and (l0, l1, l2) triples: from the first
+    // cell (thread 0, u = 0) and the last one (its owner), both in registers
+    if (c_first <= c_last) {
+#pragma unroll
+        for (int u = 0; u < kCPT; ++u) {
+            const int c = c_first + u * kScoreThreads + tid;
+            if (c == c_first) {
+                s_pair[0] = static_cast<int>(kdiv<POW2>(gv[u], k23));
+                s_trip[0] = static_cast<int>(kdiv<POW2>(gv[u], k3));
+            }
+            if (c == c_last) {
+                s_pair[1] = static_cast<int>(kdiv<POW2>(gv[u], k23));
+                s_trip[1] = static_cast<int>(kdiv<POW2>(gv[u], k3));
+            }
+        }
     }
     if (tid < 128) {
         uint16_t qv[kMaxG4];
@@ -194,9 +207,23 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
             if (g < a.G) acc += bf16_to_f32(qv[g]);
         qs[tid] = acc;
     }
-    for (int p = 0; p < 4; ++p) {
-        const float* cp = a.cent + (static_cast<int64_t>(h) * 4 + p) * a.kmax * kDp4;
-        for (int i = tid; i < a.k[p] * kDp4; i += kScoreThreads) cs[(p * a.kmax + i / kDp4) * kCS4 + i % kDp4] = cp[i];
+    {
+        // the four codebooks [4][kmax][32] as float4, every load in flight
+        // at once, then to LDS at the padded row stride
+        constexpr int kRowF4 = kDp4 / 4;
+        const float4* cp = reinterpret_cast<const float4*>(a.cent + static_cast<int64_t>(h) * 4 * a.kmax * kDp4);
+        const int n4 = 4 * a.kmax * kRowF4;
+        float4 cv[4 * kK4 * kRowF4 / kScoreThreads];
+#pragma unroll
+        for (int u = 0; u < 4 * kK4 * kRowF4 / kScoreThreads; ++u) {
+            const int i = tid + u * kScoreThreads;
+            cv[u] = i < n4 ? cp[i] : make_float4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4 * kK4 * kRowF4 / kScoreThreads; ++u) {
+            const int i = tid + u * kScoreThreads;
+            if (i < n4) *reinterpret_cast<float4*>(&cs[(i / kRowF4) * kCS4 + 4 * (i % kRowF4)]) = cv[u];
+        }
     }
     // this head's histogram starts at zero (the histogram kernel is the next launch)
     for (int i = blockIdx.x * kScoreThreads + tid; i < kBins4; i += gridDim.x * kScoreThreads)
