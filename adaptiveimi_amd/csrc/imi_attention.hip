@@ -16,11 +16,14 @@
 //
 // Prologue: one round trip brings q, the head's row / cell / delta counts,
 // the first kStageCap cells of its selection (row prefix and CSR offset per
-// cell) and its delta rows into registers, then LDS.  The start of every
-// non-empty cell inside the workgroup's rows is flagged with its rank, an
-// inclusive max-scan gives each row its cell, and row -> list row (or -1 -
-// steady row) goes to an LDS table.  The staged selection shares its LDS
-// with the K / V tiles, which are first written after the table is built.
+// cell) and its delta rows into registers, then LDS.  Each wave builds the
+// row table of its quarter: a 64-ary ballot search finds the cell of its
+// first selected row, the start of every later non-empty cell inside its
+// rows is flagged with its rank, an inclusive max-scan gives each row its
+// cell, and row -> list row (or -1 - steady row) goes to LDS.  The staged
+// selection shares its LDS with the K / V tiles: a workgroup barrier after
+// the tables separates the last read of the one from the first write of the
+// other.
 //
 // Streaming: a wave owns a quarter of the workgroup's rows in tiles of 16
 // and keeps two tiles in flight ahead of the one it computes.  Rows are read
@@ -219,7 +222,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
     const int64_t r1 = min(r1e, r0 + kLocCap);   // the host sizes S so that this never cuts
 
     // ---- row lookup: s_loc[i] for rows r0 + i of this split.  Each wave
-    // fills the entries of its own quarter (no workgroup barrier): a steady
+    // fills the entries of its own quarter: a steady
     // row gets -1 - its row, a delta row -1 - its ring row, a selected row j
     // the list row O[c] + j - P[c] of the cell c holding it.  The cell of the
     // wave's first selected row comes from a 64-ary search over the staged
@@ -292,7 +295,9 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
             }
         }
     }
-    wave_lds_sync();
+    // every wave is done with the staged selection before any wave writes
+    // its K / V tiles over it
+    __syncthreads();
 
     // ---- stream this wave's quarter of the rows ----
     const uint16_t* skh = a.sk + static_cast<int64_t>(h) * a.s_stride * 128;

@@ -27,6 +27,7 @@ struct IxParams {
     int32_t* hist;   // [H][kmax][nblk]
     int32_t* rank;   // [H][T]
     int32_t* cid;    // [H][ncells] compact id scratch
+    int32_t* sums;   // [H][nchunk][2] per-chunk row and occupied totals
 };
 
 __host__ __device__ inline int bits_for(int n) {
@@ -88,25 +89,126 @@ __global__ __launch_bounds__(256) void ix_count_kernel(IxParams a, int32_t* coun
     atomicAdd(&count[static_cast<int64_t>(h) * a.ncells + cell_of(a, h, t)], 1);
 }
 
+constexpr int kOffCells = 8192;                 // cells per workgroup of the offset scan
+constexpr int kOffPT = kOffCells / 256;         // 32 consecutive cells per thread
+
+// Inclusive scan of two ints over a 256-thread block; totals in tx / ty.
+__device__ __forceinline__ void block_scan2_256(int& x, int& y, int* sh, int& tx, int& ty) {
+    const int ix = wave_incl_scan(x), iy = wave_incl_scan(y);
+    const int w = threadIdx.x >> 6;
+    if (lane_id() == 63) {
+        sh[w] = ix;
+        sh[4 + w] = iy;
+    }
+    __syncthreads();
+    int bx = 0, by = 0;
+    tx = 0;
+    ty = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (j < w) {
+            bx += sh[j];
+            by += sh[4 + j];
+        }
+        tx += sh[j];
+        ty += sh[4 + j];
+    }
+    x = bx + ix;
+    y = by + iy;
+    __syncthreads();
+}
+
+// Per chunk of kOffCells global cells: the row count and the occupied cells.
+__global__ __launch_bounds__(256) void ix_chunk_sums_kernel(IxParams a, const int32_t* count, int32_t* sums,
+                                                            int nchunk) {
+    __shared__ int sh[8];
+    const int h = blockIdx.y, chunk = blockIdx.x, tid = threadIdx.x;
+    const int32_t* c = count + static_cast<int64_t>(h) * a.ncells;
+    int t = 0, o = 0;
+#pragma unroll 8
+    for (int u = 0; u < kOffPT; ++u) {
+        const int64_t g = static_cast<int64_t>(chunk) * kOffCells + u * 256 + tid;
+        const int v = g < a.ncells ? c[g] : 0;
+        t += v;
+        o += v > 0 ? 1 : 0;
+    }
+    int tt, to;
+    block_scan2_256(t, o, sh, tt, to);
+    if (tid == 0) {
+        sums[(static_cast<int64_t>(h) * nchunk + chunk) * 2 + 0] = tt;
+        sums[(static_cast<int64_t>(h) * nchunk + chunk) * 2 + 1] = to;
+    }
+}
+
 // offsets[h][g] = exclusive prefix of count (offsets[h][ncells] = T); when
 // compact metadata is requested also cid[h][g] = exclusive prefix of the
-// occupied flags and n_active[h].
-__global__ __launch_bounds__(1024) void ix_offsets_kernel(IxParams a, const int32_t* count, int32_t* offset,
-                                                          int32_t* n_active) {
-    __shared__ int sh[40];
-    const int h = blockIdx.x;
+// occupied flags and n_active[h].  One workgroup per chunk: its base is the
+// sum of the chunk totals before it, then 32 consecutive cells per thread.
+__global__ __launch_bounds__(256) void ix_offsets_kernel(IxParams a, const int32_t* count, int32_t* offset,
+                                                         int32_t* n_active, const int32_t* sums, int nchunk) {
+    __shared__ int sh[8];
+    const int h = blockIdx.y, chunk = blockIdx.x, tid = threadIdx.x;
     const int32_t* c = count + static_cast<int64_t>(h) * a.ncells;
     int32_t* o = offset + static_cast<int64_t>(h) * (a.ncells + 1);
-    for (int64_t g = threadIdx.x; g < a.ncells; g += 1024) o[g] = c[g];
-    __syncthreads();
-    const int total = block_exclusive_scan_1024(o, a.ncells, sh);
-    if (threadIdx.x == 0) o[a.ncells] = total;
-    if (a.cid == nullptr) return;
-    int32_t* id = a.cid + static_cast<int64_t>(h) * a.ncells;
-    for (int64_t g = threadIdx.x; g < a.ncells; g += 1024) id[g] = c[g] > 0 ? 1 : 0;
-    __syncthreads();
-    const int act = block_exclusive_scan_1024(id, a.ncells, sh);
-    if (threadIdx.x == 0) n_active[h] = act;
+    const int64_t g0 = static_cast<int64_t>(chunk) * kOffCells + static_cast<int64_t>(tid) * kOffPT;
+    int v[kOffPT];
+    if (g0 + kOffPT <= a.ncells && (reinterpret_cast<uintptr_t>(c + g0) & 15) == 0) {
+#pragma unroll
+        for (int u = 0; u < kOffPT / 4; ++u) {
+            const int4 q = reinterpret_cast<const int4*>(c + g0)[u];
+            v[4 * u + 0] = q.x;
+            v[4 * u + 1] = q.y;
+            v[4 * u + 2] = q.z;
+            v[4 * u + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < kOffPT; ++u) v[u] = g0 + u < a.ncells ? c[g0 + u] : 0;
+    }
+    int bt = 0, bo = 0;
+    for (int i = tid; i < chunk; i += 256) {
+        bt += sums[(static_cast<int64_t>(h) * nchunk + i) * 2 + 0];
+        bo += sums[(static_cast<int64_t>(h) * nchunk + i) * 2 + 1];
+    }
+    int btt, bot;
+    block_scan2_256(bt, bo, sh, btt, bot);
+    int lt = 0, lo = 0;
+#pragma unroll
+    for (int u = 0; u < kOffPT; ++u) {
+        lt += v[u];
+        lo += v[u] > 0 ? 1 : 0;
+    }
+    int et = lt, eo = lo, tt, to;
+    block_scan2_256(et, eo, sh, tt, to);
+    int rt = btt + et - lt, ro = bot + eo - lo;
+    int32_t* id = a.cid ? a.cid + static_cast<int64_t>(h) * a.ncells : nullptr;
+    int ov[kOffPT], iv[kOffPT];
+#pragma unroll
+    for (int u = 0; u < kOffPT; ++u) {
+        ov[u] = rt;
+        iv[u] = ro;
+        rt += v[u];
+        ro += v[u] > 0 ? 1 : 0;
+    }
+    // 16-byte stores where the row allows them (the offset rows start at
+    // h * (ncells + 1), so their alignment varies with h)
+    const bool o_vec = g0 + kOffPT <= a.ncells && (reinterpret_cast<uintptr_t>(o + g0) & 15) == 0;
+    const bool i_vec = id && g0 + kOffPT <= a.ncells && (reinterpret_cast<uintptr_t>(id + g0) & 15) == 0;
+#pragma unroll
+    for (int u = 0; u < kOffPT / 4; ++u) {
+        if (o_vec) reinterpret_cast<int4*>(o + g0)[u] = make_int4(ov[4 * u], ov[4 * u + 1], ov[4 * u + 2], ov[4 * u + 3]);
+        if (i_vec) reinterpret_cast<int4*>(id + g0)[u] = make_int4(iv[4 * u], iv[4 * u + 1], iv[4 * u + 2], iv[4 * u + 3]);
+    }
+#pragma unroll
+    for (int u = 0; u < kOffPT; ++u) {
+        if (g0 + u >= a.ncells) continue;
+        if (!o_vec) o[g0 + u] = ov[u];
+        if (id && !i_vec) id[g0 + u] = iv[u];
+    }
+    if (chunk == nchunk - 1 && tid == 0) {
+        o[a.ncells] = btt + tt;
+        if (id) n_active[h] = bot + to;
+    }
 }
 
 struct CompactOut {
@@ -120,32 +222,35 @@ struct CompactOut {
     uint8_t* mask;
 };
 
-// One wave per global cell: occupied cells write their compact slot.
+// One thread per global cell: an occupied cell writes its compact slot.
 __global__ __launch_bounds__(256) void ix_compact_fill_kernel(IxParams a, CompactOut o, const int32_t* count,
                                                               const int32_t* offset) {
     const int h = blockIdx.y;
-    const int64_t g = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (g >= a.ncells) return;
     const int cnt = count[static_cast<int64_t>(h) * a.ncells + g];
     if (cnt == 0) return;
     const int c = a.cid[static_cast<int64_t>(h) * a.ncells + g];
     const int64_t hc = static_cast<int64_t>(h) * o.n_c + c;
-    const int lane = lane_id();
-    if (lane == 0) {
-        o.gid[hc] = static_cast<int32_t>(g);
-        o.size[hc] = cnt;
-        o.offset[static_cast<int64_t>(h) * (o.n_c + 1) + c] = offset[static_cast<int64_t>(h) * (a.ncells + 1) + g];
-        if (o.mask) o.mask[hc] = 0;
-    }
-    if (!o.merged) return;
-    // merged centroid = [C_0[l0] | C_1[l1] | ...]
-    int64_t rem = g;
+    o.gid[hc] = static_cast<int32_t>(g);
+    o.size[hc] = cnt;
+    o.offset[static_cast<int64_t>(h) * (o.n_c + 1) + c] = offset[static_cast<int64_t>(h) * (a.ncells + 1) + g];
+    if (o.mask) o.mask[hc] = 0;
+}
+
+// One wave per occupied compact slot: merged centroid = [C_0[l0] | C_1[l1] | ...].
+__global__ __launch_bounds__(256) void ix_compact_merged_kernel(IxParams a, CompactOut o, const int32_t* n_active) {
+    const int h = blockIdx.y;
+    const int c = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (c >= min(n_active[h], o.n_c)) return;
+    const int64_t hc = static_cast<int64_t>(h) * o.n_c + c;
+    int64_t rem = o.gid[hc];
     int lab[4] = {0, 0, 0, 0};
     for (int p = a.P - 1; p >= 0; --p) {
         lab[p] = static_cast<int>(rem % a.k[p]);
         rem /= a.k[p];
     }
-    for (int d = lane; d < o.D; d += 64) {
+    for (int d = lane_id(); d < o.D; d += 64) {
         const int p = d / o.DP;
         o.merged[hc * o.D + d] =
             o.cent[((static_cast<int64_t>(h) * a.P + p) * a.kmax + lab[p]) * o.DP + (d - p * o.DP)];
@@ -248,6 +353,7 @@ size_t workspace_bytes(const imi_index_args* a, int kmax, int64_t ncells, IxPara
     q.hist = cv.take<int32_t>(static_cast<size_t>(a->kv_heads) * kmax * nblk);
     q.rank = cv.take<int32_t>(static_cast<size_t>(a->kv_heads) * a->n_tokens);
     q.cid = cv.take<int32_t>(static_cast<size_t>(a->kv_heads) * ncells);
+    q.sums = cv.take<int32_t>(static_cast<size_t>(a->kv_heads) * 2 * ((ncells + kOffCells - 1) / kOffCells));
     int32_t* t = cv.take<int32_t>(static_cast<size_t>(a->kv_heads) * a->n_tokens);
     if (p) *p = q;
     if (tmp) *tmp = t;
@@ -318,8 +424,12 @@ extern "C" int imi_build_index(const imi_index_args* a, imi_stream_t stream_) {
     IMI_LAUNCH_CHECK("ix_zero_kernel");
     hipLaunchKernelGGL(ix_count_kernel, dim3(p.nblk, p.H), dim3(256), 0, stream, p, a->cell_count);
     IMI_LAUNCH_CHECK("ix_count_kernel");
-    hipLaunchKernelGGL(ix_offsets_kernel, dim3(p.H), dim3(1024), 0, stream, p, a->cell_count, a->cell_offset,
-                       a->n_active);
+    const int nchunk = static_cast<int>((ncells + kOffCells - 1) / kOffCells);
+    hipLaunchKernelGGL(ix_chunk_sums_kernel, dim3(nchunk, p.H), dim3(256), 0, stream, p, a->cell_count, p.sums,
+                       nchunk);
+    IMI_LAUNCH_CHECK("ix_chunk_sums_kernel");
+    hipLaunchKernelGGL(ix_offsets_kernel, dim3(nchunk, p.H), dim3(256), 0, stream, p, a->cell_count, a->cell_offset,
+                       a->n_active, p.sums, nchunk);
     IMI_LAUNCH_CHECK("ix_offsets_kernel");
 
     if (compact) {
@@ -333,9 +443,14 @@ extern "C" int imi_build_index(const imi_index_args* a, imi_stream_t stream_) {
         o.offset = a->compact_offset;
         o.merged = a->compact_centroids;
         o.mask = a->compact_mask;
-        hipLaunchKernelGGL(ix_compact_fill_kernel, dim3(static_cast<unsigned>((ncells + 3) / 4), p.H), dim3(256), 0,
-                           stream, p, o, a->cell_count, a->cell_offset);
+        hipLaunchKernelGGL(ix_compact_fill_kernel, dim3(static_cast<unsigned>((ncells + 255) / 256), p.H), dim3(256),
+                           0, stream, p, o, a->cell_count, a->cell_offset);
         IMI_LAUNCH_CHECK("ix_compact_fill_kernel");
+        if (o.merged) {
+            hipLaunchKernelGGL(ix_compact_merged_kernel, dim3((o.n_c + 3) / 4, p.H), dim3(256), 0, stream, p, o,
+                               a->n_active);
+            IMI_LAUNCH_CHECK("ix_compact_merged_kernel");
+        }
         hipLaunchKernelGGL(ix_compact_pad_kernel, dim3((o.n_c + 256) / 256, p.H), dim3(256), 0, stream, p, o,
                            a->n_active);
         IMI_LAUNCH_CHECK("ix_compact_pad_kernel");
