@@ -45,6 +45,8 @@ def log(msg):
 WORKLOADS = {
     "config1": dict(layers=32, context=131072, kv_heads=8, groups=4, ks=(64, 64), iters=10, budget=0.1,
                     fixed_tokens=0, batch=1, sample=0),
+    "config2": dict(layers=28, context=131072, kv_heads=4, groups=7, ks=(64, 64), iters=10, budget=0.1,
+                    fixed_tokens=0, batch=4, sample=0, contexts=(32768, 65536, 98304, 131072)),
     "config3": dict(layers=16, context=262144, kv_heads=8, groups=8, ks=(32, 32, 32, 32), iters=10, budget=None,
                     fixed_tokens=4096, batch=2, sample=0),
     "config4": dict(layers=32, context=1048576, kv_heads=8, groups=4, ks=(128, 128), iters=20, budget=0.02,
@@ -79,6 +81,7 @@ def parse():
                         "known-size reference for FETCH_SIZE / WRITE_SIZE counter runs")
     args = p.parse_args()
     w = dict(WORKLOADS[args.workload])
+    w.setdefault("contexts", None)
     for name in ("layers", "context", "kv_heads", "groups", "iters", "budget"):
         if getattr(args, name) is not None:
             w[name] = getattr(args, name)
@@ -128,7 +131,10 @@ def main():
     start_ev = torch.cuda.Event(enable_timing=True)
     end_ev = torch.cuda.Event(enable_timing=True)
     keep_first = None
-    for layer in range(L):
+    head_tokens = H * T   # listed tokens over all KV heads (index-build roofline)
+    if args.contexts:
+        plans, build_ms, head_tokens = build_ragged(args, ks, static_total, static_cap, static_len, start_ev, end_ev)
+    for layer in range(0 if args.contexts else L):
         keys, values = synthetic.make_kv(H, args.context, seed=1000 + layer, device="cuda")
         mid_k = keys[:, args.static_start:args.context - args.static_end]
         mid_v = values[:, args.static_start:args.context - args.static_end]
@@ -279,7 +285,7 @@ def main():
         },
         "index_build_ms": {"per_layer_median": round(statistics.median(build_ms), 3),
                            "per_layer_min": round(min(build_ms), 3), "layers": L},
-        "index_build_roofline": build_roofline(args, H, T, ks, statistics.median(build_ms)),
+        "index_build_roofline": build_roofline(args, head_tokens, T, ks, statistics.median(build_ms)),
         "us_per_layer_step": round(ms_per_step / L * 1e3, 3),
         "attended_rows_per_layer": rows / L,
         "hbm_frac_step": round(step_gbps / HBM_PEAK_GBPS, 4),
@@ -304,6 +310,9 @@ def workload_name(args, L, H, G, ks):
     sample = f" on a {args.sample}-key sample + full assignment" if args.sample else ""
     if args.workload == "config1":
         head = f"configs[1] attention path: {L} Llama-3-8B layers"
+    elif args.workload == "config2":
+        head = (f"configs[2] attention path: {L} Qwen2.5-7B layers, ragged batch of {len(args.contexts)} sequences "
+                f"({'/'.join(str(c) for c in args.contexts)} tokens) in one launch per layer")
     elif args.workload == "config3":
         head = f"configs[3] attention path: {L}-layer Qwen2.5-72B attention slice, batch {args.batch}"
     else:
@@ -412,7 +421,70 @@ def measured_traffic(workload):
     return int(fields["traffic_bytes_per_launch"])
 
 
-def build_roofline(args, H, T, ks, build_ms):
+def build_ragged(args, ks, static_total, static_cap, static_len, start_ev, end_ev):
+    """the KV heads of several sequences of different lengths in
+    one launch per layer (sequence-major heads, each sequence's own token and
+    page budget, the lists packed in one [B*H, max_len, D] buffer).  Returns
+    the plans, the per-layer build times (every sequence's k-means and index)
+    and the listed tokens over all heads."""
+    import torch
+
+    from adaptiveimi_amd import ops, synthetic
+    from adaptiveimi_amd.sizing import decode_sizing
+
+    dev = torch.device("cuda:0")
+    Hs, G, D = args.kv_heads, args.groups, 128
+    lens = [c - static_total for c in args.contexts]
+    B = len(lens)
+    buds = []
+    for T in lens:
+        sz = decode_sizing(T, args.budget, subspace_parts=len(ks), k_override=ks)
+        buds.append(ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"]))
+    bud = ops.Budget.ragged(buds, Hs)
+    log(f"[bench] ragged: sequences {list(args.contexts)}, per-sequence max_tokens {[b.max_tokens for b in buds]}, "
+        f"buffer_pages {[b.buffer_pages for b in buds]}, nprobe {bud.nprobe}")
+    plans, build_ms = [], []
+    for layer in range(args.layers):
+        lk = torch.zeros((B * Hs, max(lens), D), dtype=torch.bfloat16, device=dev)
+        lv = torch.zeros_like(lk)
+        sk = torch.zeros((B * Hs, static_cap, D), dtype=torch.bfloat16, device=dev)
+        sv = torch.zeros_like(sk)
+        cents, counts, offsets, qs, dur = [], [], [], [], 0.0
+        for s_, ctx in enumerate(args.contexts):
+            keys, values = synthetic.make_kv(Hs, ctx, seed=1000 + 97 * layer + s_, device="cuda")
+            mid_k = keys[:, args.static_start:ctx - args.static_end]
+            mid_v = values[:, args.static_start:ctx - args.static_end]
+            hs = slice(s_ * Hs, (s_ + 1) * Hs)
+            sk[hs, :args.static_start] = keys[:, :args.static_start]
+            sk[hs, args.static_start:static_total] = keys[:, ctx - args.static_end:]
+            sv[hs, :args.static_start] = values[:, :args.static_start]
+            sv[hs, args.static_start:static_total] = values[:, ctx - args.static_end:]
+            sk[hs, static_total] = keys[:, -1]
+            sv[hs, static_total] = values[:, -1]
+            torch.cuda.synchronize()
+            start_ev.record()
+            cent, labels, _ = ops.kmeans(mid_k, list(ks), args.iters)
+            idx = ops.build_index(mid_k, mid_v, cent, labels, list(ks), compact=False, list_keys=lk[hs],
+                                  list_values=lv[hs])
+            end_ev.record()
+            torch.cuda.synchronize()
+            dur += start_ev.elapsed_time(end_ev)
+            cents.append(cent)
+            counts.append(idx["cell_count"])
+            offsets.append(idx["cell_offset"])
+            qs.append(synthetic.make_queries(mid_k, G, seed=layer * 10 + s_)[0])
+            del keys, values, mid_k, mid_v, labels
+        build_ms.append(dur)
+        plan = ops.DecodePlan(torch.cat(cents), torch.cat(counts), torch.cat(offsets), ks, bud, lk, lv, sk, sv, G,
+                              query=torch.cat(qs).contiguous())
+        plan.set_static_len(static_len)
+        plans.append(plan)
+        if layer % 7 == 6:
+            log(f"[bench] built {layer + 1}/{args.layers} layers, last build {build_ms[-1]:.2f} ms")
+    return plans, build_ms, Hs * sum(lens)
+
+
+def build_roofline(args, head_tokens, T, ks, build_ms):
     """Index-build fractions over the whole per-layer build (k-means +
     cell lists + K/V permutation, median wall time):
       E-step FLOPs = 2 T k D per Lloyd iteration per KV head (every key
@@ -424,9 +496,14 @@ def build_roofline(args, H, T, ks, build_ms):
         and V), 5 T D 2 B per KV head; against the HBM peak."""
     D = 128
     k = max(ks)
+    # per head: T listed tokens (head_tokens = their sum over the KV heads);
+    # a sampled build iterates on min(sample, T) keys, then assigns all T
+    heads = head_tokens / T
     n_it = min(args.sample, T) if args.sample else T
-    flops = 2.0 * k * D * H * (n_it * args.iters + (T if args.sample else 0))
-    nbytes = 5.0 * T * D * 2 * H
+    flops = 2.0 * k * D * heads * (n_it * args.iters + (T if args.sample else 0))
+    if args.contexts:
+        flops = 2.0 * k * D * head_tokens * args.iters
+    nbytes = 5.0 * D * 2 * head_tokens
     t = build_ms * 1e-3
     return {"estep_gflop": round(flops / 1e9, 2), "mfma_tflops": round(flops / t / 1e12, 2),
             "mfma_peak_tflops": MFMA_BF16_PEAK_TFLOPS, "mfma_frac": round(flops / t / 1e12 / MFMA_BF16_PEAK_TFLOPS, 5),

@@ -42,6 +42,12 @@ def test_other_workloads_and_overrides(monkeypatch):
     assert (a.layers, a.context, a.batch, a.groups, tuple(a.ks), a.fixed_tokens, a.budget) == \
         (16, 262144, 2, 8, (32, 32, 32, 32), 4096, None)
     assert a.cpu_baseline == 0 and a.online_layers == 0   # quoted on the default workload only
+    a = _parse(monkeypatch, ["--workload", "config2"])
+    assert (a.layers, a.kv_heads, a.groups, a.batch, tuple(a.contexts), tuple(a.ks), a.budget) == \
+        (28, 4, 7, 4, (32768, 65536, 98304, 131072), (64, 64), 0.1)
+    import bench
+
+    assert "ragged batch of 4 sequences" in bench.workload_name(a, 28, 16, 7, (64, 64))
     a = _parse(monkeypatch, ["--workload", "config4", "--layers", "2", "--k", "96"])
     assert (a.layers, a.context, tuple(a.ks), a.sample, a.budget) == (2, 1048576, (96, 96), 65536, 0.02)
 
@@ -70,7 +76,7 @@ def test_build_roofline_fields(monkeypatch):
     import bench
 
     a = _parse(monkeypatch, [])
-    r = bench.build_roofline(a, 8, 131072 - 96, (64, 64), 3.0)
+    r = bench.build_roofline(a, 8 * (131072 - 96), 131072 - 96, (64, 64), 3.0)   # listed tokens over the 8 heads
     # 2 T k D per iteration per head: 2 * 130976 * 64 * 128 * 8 * 10
     assert r["estep_gflop"] == round(2 * 130976 * 64 * 128 * 8 * 10 / 1e9, 2)
     assert r["bytes_min"] == 5 * 130976 * 128 * 2 * 8
