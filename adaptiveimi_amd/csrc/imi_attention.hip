@@ -23,7 +23,14 @@
 // cell, and row -> list row (or -1 - steady row) goes to LDS.  The staged
 // selection shares its LDS with the K / V tiles: a workgroup barrier after
 // the tables separates the last read of the one from the first write of the
-// other.
+// other.  The short form (at most kFastCap selected cells and 128 rows per
+// wave, the shapes of the decode configurations at up to 128k tokens) keeps
+// each lane's two row locations in registers (the tile loads fetch them
+// with a lane shuffle) and stages the selection apart from the tiles, so no
+// workgroup barrier separates the lookup from the first loads.  Kernel
+// arguments are ordered so that the prologue's loads depend on one 64-byte
+// argument line, and the per-head counts are read with vector loads that
+// leave with the others (one memory round trip before the lookup).
 //
 // Streaming: a wave owns a quarter of the workgroup's rows in tiles of 16
 // and keeps two tiles in flight ahead of the one it computes.  Rows are read
@@ -67,6 +74,12 @@ constexpr int kVStride = 144;        // u16 per LDS row of a wave's K / V tile (
 constexpr int kPF = 2;               // K / V tiles in flight per wave
 constexpr int kStageCap = 2048;      // selected cells staged in the prologue's first round trip
 constexpr int kStageMax = 16384;     // selected cells per head (row prefix + offset staged in LDS)
+// The short form (FAST): at most kFastCap selected cells (three entries per
+// thread in one round trip) and kFastRows rows per workgroup, so that a wave
+// holds at most 128 rows and keeps their locations in two registers.
+constexpr int kFastCap = 767;
+constexpr int kFastPad = kFastCap + 1;   // words of each staged array (the prefix has cap + 1 entries)
+constexpr int kFastRows = 4 * 128;
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
@@ -76,33 +89,53 @@ typedef __attribute__((ext_vector_type(2))) unsigned int u32x2_t;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;   // global (not flat) loads
 
+// Fields in the order the kernel first needs them: the first 64 bytes hold
+// everything the prologue's loads depend on, so that one scalar-cache line
+// (one kernel-argument round trip) starts the workgroup.
 struct DecParams {
-    const uint16_t* q;
-    const uint16_t* sk;
-    const uint16_t* sv;
-    int64_t s_stride;
-    int static_len;
-    const uint16_t* lk;
-    const uint16_t* lv;
-    int64_t list_rows;
     int H, S;
-    float scale_log2;        // scale * log2(e)
-    float* part_acc;         // [H][S][G][128]
-    float* part_ml;          // [H][S][G][2]
-    uint16_t* out;           // [H*G][128]
-    float* lse;              // [H*G] or null
-    // given selection
+    int g_cap;                 // selection capacity per head
+    uint32_t h_magic;          // floor(2^32 / H) + 1: b / H as a multiply-high
+    const uint16_t* q;
     const int32_t* g_prefix;   // [H][g_cap + 1]
     const int32_t* g_offset;   // [H][g_cap]
     const int32_t* g_nsel;     // [H]
     const int32_t* g_nrows;    // [H]
-    int g_cap;
     const int32_t* g_drows;    // [H][g_dcap] or null
+    // -- 64 bytes: what the row lookup and the first loads need
     const int32_t* g_ndelta;   // [H]
     int g_dcap;
+    int static_len;
+    double inv_S;              // 1 / S (split boundaries)
+    int s_stride;              // steady rows per head (< 2^31, checked by the host)
+    int list_rows;             // list rows per head (< 2^31, checked by the host)
+    const uint16_t* sk;
+    const uint16_t* sv;
+    const uint16_t* lk;
+    const uint16_t* lv;
+    // -- 128 bytes
+    float scale_log2;          // scale * log2(e)
     int o_base;                // LDS word of the staged offsets (after the prefix)
     int stage_words;           // LDS words shared by the staged selection and the K / V tiles
+    int fast;                  // the short form (attention_kernel<G, true>)
+    float* part_acc;           // [H][S][G][128]
+    float* part_ml;            // [H][S][G][2]
+    uint16_t* out;             // [H*G][128]
+    float* lse;                // [H*G] or null
 };
+static_assert(offsetof(DecParams, g_ndelta) == 64 && offsetof(DecParams, scale_log2) == 128,
+              "prologue fields in the first 64 bytes, lookup and load fields in the next 64");
+
+// floor(R s / S) for R < 2^32 and 0 <= s <= S <= kMaxSplit.  R s < 2^44 is
+// exact in fp64 and the rounded quotient is within 2^-8 / S of R s / S,
+// whose distance to the next integer above is 0 or at least 1 / S: the
+// truncation is exact or one below, which the check corrects.
+__device__ __forceinline__ int64_t split_floor(uint32_t R, int s, int S, double inv_S) {
+    const uint64_t n = static_cast<uint64_t>(R) * static_cast<uint32_t>(s);
+    uint64_t q = static_cast<uint64_t>(static_cast<double>(n) * inv_S);
+    if ((q + 1) * static_cast<uint64_t>(S) <= n) ++q;
+    return static_cast<int64_t>(q);
+}
 
 // Weight exp2(m - M) of a state with running max m inside a merge whose max
 // is M; an empty state (m = -inf) weighs 0 even when M is -inf too.
@@ -139,33 +172,49 @@ __device__ __forceinline__ int wave_incl_max_scan(int v) {
 }
 
 // LDS: [staged selection | K and V tiles] (stage_words), then the wave
-// partials, the row lookup and the delta rows.
+// partials, the row lookup and the delta rows; the short form keeps the
+// staged selection apart, after those.
 constexpr int kTileU16 = kWaves * 16 * kVStride;   // one of the K / V tiles of all waves
 constexpr int kTileWords = kTileU16;               // both tiles, in 32-bit words
 template <int G>
 constexpr int tail_words() {
     return kWaves * G * 128 + kWaves * G * 2 + kLocCap + kDeltaMax;
 }
+template <int G>
+constexpr int fast_words() {
+    return kTileWords + tail_words<G>() + 2 * kFastPad;
+}
 
 // One workgroup = 4 waves over its split of head h's rows [static | selected
 // | delta]; writes one partial (max, sum, unnormalised output).  The head's
 // selection (row prefix and CSR offset per cell, at most kStageCap cells in
 // the first round trip) is staged in LDS together with q and the row counts.
-template <int G>
+// FAST (at most kFastCap cells, kFastRows rows per workgroup): each lane
+// holds the locations of two of its wave's rows in registers, and the staged
+// selection does not share LDS with the tiles, so no workgroup barrier
+// separates the row lookup from the first loads.
+template <int G, bool FAST>
 __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
     extern __shared__ __attribute__((aligned(16))) int lds[];
-    int* P = lds;                                   // [g_cap + 1] row prefix of the selected cells
-    int* O = lds + a.o_base;                        // [g_cap] CSR offset of each selected cell
     uint16_t* s_k = reinterpret_cast<uint16_t*>(lds);   // the tiles reuse the staged selection's words
     uint16_t* s_v = s_k + kTileU16;
-    float* s_acc = reinterpret_cast<float*>(lds + a.stage_words);           // [4][G][128]
+    float* s_acc = reinterpret_cast<float*>(lds + (FAST ? kTileWords : a.stage_words));   // [4][G][128]
     float* s_ml = s_acc + kWaves * G * 128;                                 // [4][G][2]
     int* s_loc = reinterpret_cast<int*>(s_ml + kWaves * G * 2);             // [kLocCap]
     int* s_drow = s_loc + kLocCap;                                          // [kDeltaMax]
+    int* P = FAST ? s_drow + kDeltaMax : lds;       // [g_cap + 1] row prefix of the selected cells
+    int* O = FAST ? P + kFastPad : lds + a.o_base;  // [g_cap] CSR offset of each selected cell
 
-    const int b = blockIdx.x;
-    const int split = b / a.H;
-    const int h = (b % a.H + split) % a.H;
+    // split = b / H, h = (b % H + split) % H, by multiply-highs (exact for
+    // b * H < 2^32, which the host checks)
+    const uint32_t b = blockIdx.x;
+    const int split = a.h_magic ? static_cast<int>(__umulhi(b, a.h_magic)) : static_cast<int>(b);
+    int h = 0;
+    if (a.h_magic) {
+        h = static_cast<int>(b - static_cast<uint32_t>(split) * a.H) +
+            (split - static_cast<int>(__umulhi(static_cast<uint32_t>(split), a.h_magic)) * a.H);
+        if (h >= a.H) h -= a.H;
+    }
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lg = lane >> 4, ln = lane & 15;
 
@@ -178,12 +227,14 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
         qb[c] = *reinterpret_cast<const u32x4_t*>(a.q + (static_cast<int64_t>(h) * G + ln % G) * 128 + c * 32 + lg * 8);
     const int32_t* pre = a.g_prefix + static_cast<int64_t>(h) * (a.g_cap + 1);
     const int32_t* offg = a.g_offset + static_cast<int64_t>(h) * a.g_cap;
-    const int m_raw = a.g_nsel[h];
-    const int nrows_raw = a.g_nrows[h];
-    const int nd_raw = a.g_drows ? a.g_ndelta[h] : 0;
-    constexpr int SU = (kStageCap + kThreads) / kThreads;   // entries per thread (prefix has one more)
+    // the counts travel with the vector loads below (one round trip for all)
+    const int m_raw = vec_load_i32(a.g_nsel, h);
+    const int nrows_raw = vec_load_i32(a.g_nrows, h);
+    const int nd_raw = a.g_drows ? vec_load_i32(a.g_ndelta, h) : 0;
+    constexpr int SU = FAST ? kFastPad / kThreads : (kStageCap + kThreads) / kThreads;   // entries per thread
+    static_assert(!FAST || SU * kThreads == kFastPad, "the short form stages the prefix in SU loads per thread");
     int pv[SU], ov[SU];
-    const int c1 = min(a.g_cap, kStageCap);
+    const int c1 = min(a.g_cap, FAST ? kFastCap : kStageCap);
 #pragma unroll
     for (int u = 0; u < SU; ++u) {
         const int i = tid + u * kThreads;
@@ -204,22 +255,21 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
     }
 #pragma unroll
     for (int u = 0; u < kDeltaMax / kThreads; ++u) s_drow[tid + u * kThreads] = dv[u];
-    const int m = min(max(m_raw, 0), a.g_cap);
-    const int nrows = max(nrows_raw, 0);
-    const int nd = min(max(nd_raw, 0), a.g_dcap);
-    // selections above kStageCap cells: the rest in further round trips
-    for (int i = kStageCap + 1 + tid; i <= m; i += kThreads) P[i] = pre[i];
-    for (int i = kStageCap + tid; i < m; i += kThreads) O[i] = offg[i];
+    const int m = min(max(__builtin_amdgcn_readfirstlane(m_raw), 0), a.g_cap);
+    const int nrows = max(__builtin_amdgcn_readfirstlane(nrows_raw), 0);
+    const int nd = min(max(__builtin_amdgcn_readfirstlane(nd_raw), 0), a.g_dcap);
+    if constexpr (!FAST) {
+        // selections above kStageCap cells: the rest in further round trips
+        for (int i = kStageCap + 1 + tid; i <= m; i += kThreads) P[i] = pre[i];
+        for (int i = kStageCap + tid; i < m; i += kThreads) O[i] = offg[i];
+    }
     __syncthreads();
     const int sl = a.static_len;
-    // split boundaries floor(R s / S) in 32-bit arithmetic: R = q S + rem
-    // (R < 2^32, S <= kMaxSplit, so rem * s < 2^24)
+    // split boundaries floor(R s / S) (R < 2^32)
     const uint32_t R = static_cast<uint32_t>(sl) + static_cast<uint32_t>(nrows) + static_cast<uint32_t>(nd);
-    const uint32_t Rq = R / static_cast<uint32_t>(a.S), Rr = R % static_cast<uint32_t>(a.S);
-    const int64_t r0 = static_cast<int64_t>(Rq) * split + Rr * static_cast<uint32_t>(split) / static_cast<uint32_t>(a.S);
-    const int64_t r1e =
-        static_cast<int64_t>(Rq) * (split + 1) + Rr * static_cast<uint32_t>(split + 1) / static_cast<uint32_t>(a.S);
-    const int64_t r1 = min(r1e, r0 + kLocCap);   // the host sizes S so that this never cuts
+    const int64_t r0 = split_floor(R, split, a.S, a.inv_S);
+    const int64_t r1e = split_floor(R, split + 1, a.S, a.inv_S);
+    const int64_t r1 = min(r1e, r0 + (FAST ? kFastRows : kLocCap));   // the host sizes S so that this never cuts
 
     // ---- row lookup: s_loc[i] for rows r0 + i of this split.  Each wave
     // fills the entries of its own quarter: a steady
@@ -232,10 +282,60 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
     // the steady zone. ----
     const int nr = static_cast<int>(r1 - r0);
     const int wb = nr * wave / kWaves, we = nr * (wave + 1) / kWaves;
-    const int wn = we - wb;   // <= kLocCap / 4 = 512
-    {
-        const int lmax = max(static_cast<int>(a.list_rows) - 1, 0);
-        const int smax = static_cast<int>(a.s_stride) - 1;
+    const int wn = we - wb;   // <= kLocCap / 4 = 512 (FAST: kFastRows / 4 = 128)
+    const int lmax = max(a.list_rows - 1, 0);
+    const int smax = a.s_stride - 1;
+    // FAST: locations of rows wb + lane and wb + lane + 64, same encoding
+    // (rows past the wave's end: list row 0, never used)
+    int loc0 = 0, loc1 = 0;
+    if constexpr (FAST) {
+        const int64_t w0 = r0 + wb;
+        const int pa = static_cast<int>(min(max(sl - w0, int64_t(0)), int64_t(wn)));
+        const int pb = static_cast<int>(min(max(sl + nrows - w0, int64_t(0)), int64_t(wn)));
+        auto fixed = [&](int i) {   // steady or delta row at position i (0 otherwise)
+            if (i < pa) return -1 - static_cast<int>(w0 + i);
+            if (i >= pb && i < wn) {
+                const int d = static_cast<int>(w0 + i - sl - nrows);
+                return -1 - min(max(s_drow[min(d, kDeltaMax - 1)], 0), smax);
+            }
+            return 0;
+        };
+        loc0 = fixed(lane);
+        loc1 = fixed(lane + 64);
+        if (pb > pa) {
+            int* fl = s_loc + wave * 128;   // cell that starts at each position, else INT_MIN
+            fl[lane] = INT_MIN;
+            fl[lane + 64] = INT_MIN;
+            const int jlo = static_cast<int>(w0 + pa - sl), jhi = jlo + (pb - pa);
+            // c0 = the last cell with P[c] <= jlo (P[0] = 0 <= jlo): two
+            // ballot rounds, m <= kFastCap < 64 * 64
+            const int step = (m + 63) >> 6;
+            const uint64_t b1 = __builtin_amdgcn_ballot_w64(lane * step < m && P[lane * step] <= jlo);
+            const int base = (63 - __builtin_clzll(b1 | 1ull)) * step;
+            const uint64_t b2 = __builtin_amdgcn_ballot_w64(lane < step && base + lane < m && P[base + lane] <= jlo);
+            const int c0 = base + (63 - __builtin_clzll(b2 | 1ull));
+            wave_lds_sync();   // the INT_MIN fill precedes the flags
+            // later non-empty cells start above jlo: flag those that start below jhi
+            for (int cb = c0 + 1; cb < m; cb += 64) {
+                const int c = cb + lane;
+                const int pc = c < m ? P[c] : INT_MAX;
+                const int pn = c < m ? P[c + 1] : 0;
+                if (pc < jhi && pn > pc) fl[pa + (pc - jlo)] = c;
+                if (__builtin_amdgcn_readlane(pc, 63) >= jhi) break;
+            }
+            wave_lds_sync();
+            const int s0 = wave_incl_max_scan(fl[lane]);
+            const int s1 = max(wave_incl_max_scan(fl[lane + 64]), __builtin_amdgcn_readlane(s0, 63));
+            auto sel_loc = [&](int i, int s, int dflt) {
+                if (i < pa || i >= pb) return dflt;
+                const int c = max(s, c0);
+                const int j = jlo + (i - pa);
+                return min(max(O[c] + (j - P[c]), 0), lmax);
+            };
+            loc0 = sel_loc(lane, s0, loc0);
+            loc1 = sel_loc(lane + 64, s1, loc1);
+        }
+    } else {
         const int64_t w0 = r0 + wb;   // first row of this wave
         // positions [0, pa) steady, [pa, pb) selected, [pb, wn) delta
         const int pa = static_cast<int>(min(max(sl - w0, int64_t(0)), int64_t(wn)));
@@ -297,7 +397,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
     }
     // every wave is done with the staged selection before any wave writes
     // its K / V tiles over it
-    __syncthreads();
+    if constexpr (!FAST) __syncthreads();
 
     // ---- stream this wave's quarter of the rows ----
     const uint16_t* skh = a.sk + static_cast<int64_t>(h) * a.s_stride * 128;
@@ -321,7 +421,15 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
 #pragma unroll
             for (int it = 0; it < 4; ++it) {
                 const int jt = t * 16 + it * 4 + rg;
-                const int lr = jt < wn ? s_loc[wb + jt] : 0;
+                int lr;
+                if constexpr (FAST) {
+                    // row jt sits in lane jt % 64 of loc0 (tiles 0-3) or loc1
+                    // (tiles 4-7); every lane takes part in the shuffle
+                    const int v = __shfl(t < 4 ? loc0 : loc1, jt & 63);
+                    lr = jt < wn ? v : 0;
+                } else {
+                    lr = jt < wn ? s_loc[wb + jt] : 0;
+                }
                 const bool steady = lr < 0;
                 const int64_t roff = static_cast<int64_t>(steady ? -1 - lr : lr) * 128;
                 kb[SLOT][it] = __builtin_nontemporal_load((g_u32x4_t*)((steady ? skh : lkh) + roff + li * 8));
@@ -546,14 +654,24 @@ int64_t rows_bound(const imi_attention_args* a) {
     return srows + a->max_rows;
 }
 
+// About one workgroup per CU in all.
+int64_t splits_one_round(const imi_attention_args* a) {
+    const int64_t s = (device_cus() + a->kv_heads - 1) / a->kv_heads;
+    return s < 1 ? 1 : s;
+}
+
+// The short form when the selection fits its staging and one round of
+// workgroups keeps every split within kFastRows rows.
+bool attn_fast(const imi_attention_args* a) {
+    return a->sel_cap <= kFastCap && rows_bound(a) <= splits_one_round(a) * kFastRows;
+}
+
 // Splits per head: about one workgroup per CU in all, and enough that no
 // split holds more than kLocCap rows.
 int splits_per_head(const imi_attention_args* a) {
-    const int64_t cus = device_cus();
-    int64_t s = (cus + a->kv_heads - 1) / a->kv_heads;
+    int64_t s = splits_one_round(a);
     const int64_t need = (rows_bound(a) + kLocCap - 1) / kLocCap;
     if (s < need) s = need;
-    if (s < 1) s = 1;
     return static_cast<int>(s);
 }
 
@@ -566,6 +684,11 @@ size_t attn_workspace(const imi_attention_args* a, DecParams* p) {
         p->part_acc = acc;
         p->part_ml = ml;
         p->S = S;
+        p->inv_S = 1.0 / static_cast<double>(S);
+        p->h_magic = a->kv_heads > 1
+                         ? static_cast<uint32_t>((uint64_t(1) << 32) / static_cast<uint64_t>(a->kv_heads) + 1)
+                         : 0u;   // one head: split = b
+        p->fast = attn_fast(a) ? 1 : 0;
     }
     return cv.used();
 }
@@ -584,6 +707,8 @@ int attn_validate(const imi_attention_args* a, bool need_sel) {
                 "imi_sparse_attention: null steady zone");
     IMI_REQUIRE(a->list_keys && a->list_values && a->list_rows > 0, IMI_ERR_INVALID,
                 "imi_sparse_attention: null or empty list");
+    IMI_REQUIRE(a->list_rows < (int64_t(1) << 31) && a->steady_stride < (int64_t(1) << 31), IMI_ERR_UNSUPPORTED,
+                "imi_sparse_attention: list_rows / steady_stride must be below 2^31");
     IMI_REQUIRE(a->max_rows >= 0, IMI_ERR_INVALID, "imi_sparse_attention: max_rows must be >= 0");
     if (need_sel)
         IMI_REQUIRE(a->n_rows != nullptr, IMI_ERR_INVALID, "imi_sparse_attention: null n_rows");
@@ -603,6 +728,10 @@ int attn_validate(const imi_attention_args* a, bool need_sel) {
     IMI_REQUIRE(splits_per_head(a) <= kMaxSplit, IMI_ERR_UNSUPPORTED,
                 "imi_sparse_attention: %lld rows need more than %d splits per head",
                 static_cast<long long>(rows_bound(a)), kMaxSplit);
+    // the kernel splits its workgroup index by a 32-bit multiply-high
+    IMI_REQUIRE(static_cast<uint64_t>(a->kv_heads) * splits_per_head(a) * a->kv_heads < (uint64_t(1) << 32),
+                IMI_ERR_UNSUPPORTED, "imi_sparse_attention: %d kv heads x %d splits too large", a->kv_heads,
+                splits_per_head(a));
     return IMI_OK;
 }
 
@@ -610,11 +739,11 @@ void fill_common(const imi_attention_args* a, DecParams* p) {
     p->q = a->query;
     p->sk = a->steady_keys ? a->steady_keys : a->list_keys;   // never read when static_len = 0 and no delta rows
     p->sv = a->steady_values ? a->steady_values : a->list_values;
-    p->s_stride = a->steady_keys ? a->steady_stride : 1;
+    p->s_stride = a->steady_keys ? static_cast<int>(a->steady_stride) : 1;
     p->static_len = a->static_len;
     p->lk = a->list_keys;
     p->lv = a->list_values;
-    p->list_rows = a->list_rows;
+    p->list_rows = static_cast<int>(a->list_rows);
     p->H = a->kv_heads;
     p->scale_log2 = a->scale * 1.44269504088896340736f;
     p->out = a->out;
@@ -631,16 +760,24 @@ int stage_words(int cap) {
 
 template <int G>
 int launch_att(const DecParams& p, hipStream_t stream) {
-    const size_t lds = static_cast<size_t>(p.stage_words + tail_words<G>()) * 4;
     static bool attr_set = false;
     if (!attr_set) {
         constexpr size_t lds_max = static_cast<size_t>(2 * (kStageMax + 4) + tail_words<G>()) * 4;
-        static_assert(lds_max <= 160 * 1024, "LDS of one workgroup");
-        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<G>),
+        constexpr size_t lds_fast = static_cast<size_t>(fast_words<G>()) * 4;
+        static_assert(lds_max <= 160 * 1024 && lds_fast <= 160 * 1024, "LDS of one workgroup");
+        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<G, false>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_max)));
+        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<G, true>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_fast)));
         attr_set = true;
     }
-    hipLaunchKernelGGL((attention_kernel<G>), dim3(p.H * p.S), dim3(kThreads), lds, stream, p);
+    if (p.fast) {
+        const size_t lds = static_cast<size_t>(fast_words<G>()) * 4;
+        hipLaunchKernelGGL((attention_kernel<G, true>), dim3(p.H * p.S), dim3(kThreads), lds, stream, p);
+    } else {
+        const size_t lds = static_cast<size_t>(p.stage_words + tail_words<G>()) * 4;
+        hipLaunchKernelGGL((attention_kernel<G, false>), dim3(p.H * p.S), dim3(kThreads), lds, stream, p);
+    }
     IMI_LAUNCH_CHECK("attention_kernel");
     return IMI_OK;
 }

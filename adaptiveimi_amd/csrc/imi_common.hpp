@@ -4,6 +4,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <climits>
+#include <cstddef>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -220,6 +222,18 @@ __device__ __forceinline__ int wave_max_i(int v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o));
     return v;
+}
+
+// p[i] through a vector load.  A load at a wave-uniform address becomes a
+// scalar load, which the compiler may place after the wait for the vector
+// loads issued before it -- one more memory round trip at a kernel's start.
+// The zero offset below comes from a VGPR the compiler cannot see through,
+// so the load is a vector load scheduled with the others; readfirstlane
+// makes the value uniform again where it is used.
+__device__ __forceinline__ int vec_load_i32(const int32_t* p, int64_t i) {
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return p[i + z];
 }
 
 }  // namespace imi

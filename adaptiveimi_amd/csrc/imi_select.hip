@@ -40,39 +40,48 @@ constexpr int kCap = 2048;     // candidate capacity
 constexpr int kOvr = 64;       // replaced centroids scored per pass
 constexpr int kKeepWords = 512;  // bitmap of kept global cells (k0 * k1 <= 16384)
 
+// Fields in the order the kernel first needs them: the first 64 bytes hold
+// what the prologue's loads depend on (one kernel-argument cache line).
+// (2-way IMI at D = 128: two subspaces of 64 dims, centroid rows
+// [H][2][max(k0, k1)][64], k0 * k1 global cells).
 struct SelParams {
     const uint16_t* q;
     const float* cent;
     const int32_t* cnt;
     const int32_t* off;
-    int H, G, D, P, kmax;
-    int k[4];
-    int ncells;
-    int nprobe, max_tokens, buffer_pages, page_size;
     const int32_t* head_max_tokens;    // [H] or null
     const int32_t* head_buffer_pages;  // [H] or null
+    int k[2];                          // cells per subspace
+    int G;
+    int nprobe;
+    // -- 64 bytes: budgets, the selection outputs and the online prologue
+    int max_tokens, buffer_pages, page_size;
     int tile_mode;
-    int32_t* sel_cell;
-    int32_t* sel_offset;
-    int32_t* sel_count;
+    int sel_cap;
+    int ring_cap;
+    int exec_rows;
+    int H;
     int32_t* sel_prefix;
     int32_t* n_sel;
     int32_t* n_rows;
-    int sel_cap;
+    const int32_t* upd_slot;
+    // -- 128 bytes
+    int32_t* sel_cell;
+    int32_t* sel_offset;
+    int32_t* sel_count;
     // online index maintenance: replaced centroids and the delta ring
     const float* shadow;
     int shadow_rows;
-    const int32_t* upd_slot;
     const int32_t* upd_row;
     const int32_t* upd_n;
     const int32_t* ring_cell;
     const int32_t* ring_row;
     const int32_t* ring_n;
-    int ring_cap;
-    int exec_rows;
     int32_t* delta_rows;
     int32_t* n_delta;
 };
+static_assert(offsetof(SelParams, max_tokens) == 64 && offsetof(SelParams, sel_cell) == 128,
+              "prologue fields in the first 64 bytes, budgets and outputs in the next 64");
 
 // Block-wide inclusive scan of one int per thread (1024 threads).
 __device__ __forceinline__ int block_incl_scan(int v, int* sh, int& total) {
@@ -149,7 +158,7 @@ __device__ void delta_match(const SelParams& a, int h, int m_tok, const int* row
     const int tid = threadIdx.x, wave = tid >> 6;
     bool match = false;
     if (tid < rn)
-        match = rcode >= 0 ? (rcode < a.ncells && ((keep[rcode >> 5] >> (rcode & 31)) & 1u) != 0)
+        match = rcode >= 0 ? (rcode < a.k[0] * a.k[1] && ((keep[rcode >> 5] >> (rcode & 31)) & 1u) != 0)
                            : (rcode == -1 && m_tok < a.nprobe);
     const uint64_t bal = __builtin_amdgcn_ballot_w64(match);
     if (lane_id() == 0) wcnt[wave] = __builtin_popcountll(bal);
@@ -188,6 +197,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     const int h = blockIdx.x;
     const int tid = threadIdx.x;
     const int k0 = a.k[0], k1 = a.k[1];
+    const int ncells = k0 * k1, kmax = max(k0, k1);
+    constexpr int D = 128;
     // LDS regions: centroids during scoring, candidates afterwards
     float* c1T = reinterpret_cast<float*>(dyn);          // [DP][k1 + 1]
     float* c0s = c1T + DP * (k1 + 1);                    // [k0][DP + 1]
@@ -205,33 +216,41 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     // so one LDS read of C1[j][d] feeds EPT fused multiply-adds.
     const int R = kSelThreads / k1;
     const int jcell = tid % k1, rcell = tid / k1;
-    const int32_t* cntp = a.cnt + static_cast<int64_t>(h) * a.ncells;
-    const int32_t* offs = a.off + static_cast<int64_t>(h) * (a.ncells + 1);
+    const int32_t* cntp = a.cnt + static_cast<int64_t>(h) * ncells;
+    const int32_t* offs = a.off + static_cast<int64_t>(h) * (ncells + 1);
     // with 8 or more cells per thread the CSR offsets are read at the end,
     // for the kept cells only (holding them would spill registers)
     constexpr bool LATE_OFF = EPT >= 8;
     int sz[EPT], co_[LATE_OFF ? 1 : EPT];
+    // g = i * k1 + jcell = tid + R k1 e: an add of a uniform stride (the
+    // multiply-add form compiled to a 64-bit mad whose unused high operand
+    // was a register still being loaded, which forced a wait for the first
+    // loads before the others were issued)
+    const uint32_t gstride = static_cast<uint32_t>(R * k1);
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
         const int i = rcell + R * e;
         const bool in = rcell < R && i < k0;
-        const int g = i * k1 + jcell;
+        const uint32_t g = static_cast<uint32_t>(tid) + gstride * static_cast<uint32_t>(e);
         sz[e] = in ? cntp[g] : 0;
         if (!LATE_OFF) co_[e] = in ? offs[g] : 0;
     }
+    // this head's budgets (ragged batches), read with the other loads
+    const int hmt_raw = a.head_max_tokens ? vec_load_i32(a.head_max_tokens, h) : INT_MAX;
+    const int hbp_raw = a.head_buffer_pages ? vec_load_i32(a.head_buffer_pages, h) : INT_MAX;
     // Online index maintenance (async_update.py): the override slot of each
     // of this thread's cells (-1: merged centroid unchanged), the shadow row
     // of each of the first kOvr slots (thread t stages float4 t & 31 of slot
     // t >> 5), and this thread's delta ring entry (thread = ring index).
     const bool upd = ONLINE && a.upd_slot != nullptr;
-    const int n_upd = upd ? a.upd_n[h] : 0;
+    const int n_upd = upd ? __builtin_amdgcn_readfirstlane(vec_load_i32(a.upd_n, h)) : 0;
     int us[EPT];
     int urow[2] = {0, 0};
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
         const int i = rcell + R * e;
         const bool in = upd && rcell < R && i < k0;
-        us[e] = in ? a.upd_slot[static_cast<int64_t>(h) * a.ncells + i * k1 + jcell] : -1;
+        us[e] = in ? a.upd_slot[static_cast<int64_t>(h) * ncells + i * k1 + jcell] : -1;
     }
     if (upd) {
 #pragma unroll
@@ -242,7 +261,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     }
     const bool ring = ONLINE && a.ring_cap > 0;
     int rcode = -3, rrow = 0;
-    const int rn = ring ? min(a.ring_n[h], a.ring_cap) : 0;
+    const int rn = ring ? min(__builtin_amdgcn_readfirstlane(vec_load_i32(a.ring_n, h)), a.ring_cap) : 0;
     if (ring && tid < a.ring_cap) {
         rcode = a.ring_cell[static_cast<int64_t>(h) * a.ring_cap + tid];
         rrow = a.ring_row[static_cast<int64_t>(h) * a.ring_cap + tid];
@@ -251,8 +270,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     // stored in LDS with padded strides (conflict-free word reads): C0
     // row-major [l0][DP + 1] for the per-l0 chain, C1 transposed
     // [d][k1 + 1] so that lanes over l1 read consecutive words.
-    const float* c0 = a.cent + (static_cast<int64_t>(h) * a.P + 0) * a.kmax * DP;
-    const float* c1 = a.cent + (static_cast<int64_t>(h) * a.P + 1) * a.kmax * DP;
+    const float* c0 = a.cent + (static_cast<int64_t>(h) * 2 + 0) * kmax * DP;
+    const float* c1 = a.cent + (static_cast<int64_t>(h) * 2 + 1) * kmax * DP;
     constexpr int kV4 = 128 * DP / 4 / kSelThreads;   // float4 per thread per subspace (k <= 128)
     float4 c0v[kV4], c1v[kV4];
 #pragma unroll
@@ -262,10 +281,10 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         c1v[u] = i4 * 4 < k1 * DP ? reinterpret_cast<const float4*>(c1)[i4] : make_float4(0, 0, 0, 0);
     }
     uint16_t qv[kMaxGroups];
-    if (tid < a.D) {
+    if (tid < D) {
 #pragma unroll
         for (int g = 0; g < kMaxGroups; ++g)
-            qv[g] = g < a.G ? a.q[(static_cast<int64_t>(h) * a.G + g) * a.D + tid] : 0;
+            qv[g] = g < a.G ? a.q[(static_cast<int64_t>(h) * a.G + g) * D + tid] : 0;
     }
 #pragma unroll
     for (int u = 0; u < kV4; ++u) {
@@ -282,7 +301,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
             for (int x = 0; x < 4; ++x) c1T[(d + x) * (k1 + 1) + r] = e1[x];
         }
     }
-    if (tid < a.D) {
+    if (tid < D) {
         float acc = 0.0f;   // grouped-query sum, g ascending (compute_impl.cu:80-87)
 #pragma unroll
         for (int g = 0; g < kMaxGroups; ++g)
@@ -453,8 +472,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     const int n_valid = shv[1];
     const float gmax = shf[32], gmin = shf[33];
     // this head's budgets (ragged batches), bounded by the launch-wide ones
-    const int max_tokens = a.head_max_tokens ? min(a.head_max_tokens[h], a.max_tokens) : a.max_tokens;
-    const int buffer_pages = a.head_buffer_pages ? min(a.head_buffer_pages[h], a.buffer_pages) : a.buffer_pages;
+    const int max_tokens = min(__builtin_amdgcn_readfirstlane(hmt_raw), a.max_tokens);
+    const int buffer_pages = min(__builtin_amdgcn_readfirstlane(hbp_raw), a.buffer_pages);
     // every kept cell costs a page, except in tile mode (no running page cut);
     // the delta match needs the ranks the page cut drops too
     int kp = (a.tile_mode || a.ring_cap > 0) ? a.nprobe : (a.nprobe < buffer_pages ? a.nprobe : buffer_pages);
@@ -794,11 +813,8 @@ int select_one_kernel(const imi_select_args* a, int64_t ncells, int kmax, hipStr
     p.off = a->cell_offset;
     p.H = a->kv_heads;
     p.G = a->groups;
-    p.D = a->dim;
-    p.P = a->parts;
-    p.kmax = kmax;
-    for (int i = 0; i < 4; ++i) p.k[i] = a->k[i];
-    p.ncells = static_cast<int>(ncells);
+    p.k[0] = a->k[0];
+    p.k[1] = a->k[1];
     p.nprobe = a->nprobe;
     p.max_tokens = a->max_tokens;
     p.buffer_pages = a->buffer_pages;
