@@ -67,7 +67,7 @@ class AttentionArgs(ctypes.Structure):
         ("sel_cap", _i32), ("max_rows", _i32), ("kv_heads", _i32), ("groups", _i32), ("dim", _i32),
         ("scale", _f32), ("out", _vp), ("out_lse", _vp),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
-        ("delta_rows", _vp), ("n_delta", _vp), ("delta_cap", _i32),
+        ("delta_rows", _vp), ("n_delta", _vp), ("delta_cap", _i32), ("head_rows_bound", _vp),
     ]
 
 

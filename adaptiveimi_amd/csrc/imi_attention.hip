@@ -74,12 +74,14 @@ constexpr int kVStride = 144;        // u16 per LDS row of a wave's K / V tile (
 constexpr int kPF = 2;               // K / V tiles in flight per wave
 constexpr int kStageCap = 2048;      // selected cells staged in the prologue's first round trip
 constexpr int kStageMax = 16384;     // selected cells per head (row prefix + offset staged in LDS)
-// The short form (FAST): at most kFastCap selected cells (three entries per
-// thread in one round trip) and kFastRows rows per workgroup, so that a wave
-// holds at most 128 rows and keeps their locations in two registers.
+// The short form (NR > 0): at most kFastCap selected cells (three entries
+// per thread in one round trip) and kWaves * 64 * NR rows per workgroup, so
+// that each lane keeps the locations of NR of its wave's rows in registers.
 constexpr int kFastCap = 767;
 constexpr int kFastPad = kFastCap + 1;   // words of each staged array (the prefix has cap + 1 entries)
-constexpr int kFastRows = 4 * 128;
+constexpr int kFastNRMax = 4;            // row locations per lane (256 rows per wave)
+constexpr int kMaxRuns = 4;              // runs of heads with their own split count (ragged batches)
+constexpr int fast_rows(int nr) { return kWaves * 64 * nr; }
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
@@ -89,42 +91,52 @@ typedef __attribute__((ext_vector_type(2))) unsigned int u32x2_t;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;   // global (not flat) loads
 
-// Fields in the order the kernel first needs them: the first 64 bytes hold
-// everything the prologue's loads depend on, so that one scalar-cache line
-// (one kernel-argument round trip) starts the workgroup.
+// Fields in the order the kernel first needs them: the first 128 bytes (two
+// scalar-cache lines, fetched together) hold everything the prologue's loads
+// depend on, the next 64 what the row lookup and the first tile loads need.
+//
+// The split pass runs in runs of heads with a split count each: one run of
+// all heads, or up to kMaxRuns for a ragged batch.  Run r = (first workgroup
+// (= its first partial), first head, splits | heads << 16, floor(2^32 /
+// heads) + 1 or 0 for one head); unused runs hold (INT_MAX, H, 0, 0).
+// Workgroup b of run r takes split local / nh of head h0 + (local % nh +
+// split) % nh, local = b - first (consecutive workgroups, which the
+// dispatcher deals round robin to the XCDs, rotate over the run's heads);
+// its partial is first + (h - h0) * splits + split.
 struct DecParams {
-    int H, S;
-    int g_cap;                 // selection capacity per head
-    uint32_t h_magic;          // floor(2^32 / H) + 1: b / H as a multiply-high
+    int4 run[kMaxRuns];
+    // -- 64 bytes
     const uint16_t* q;
     const int32_t* g_prefix;   // [H][g_cap + 1]
     const int32_t* g_offset;   // [H][g_cap]
     const int32_t* g_nsel;     // [H]
     const int32_t* g_nrows;    // [H]
     const int32_t* g_drows;    // [H][g_dcap] or null
-    // -- 64 bytes: what the row lookup and the first loads need
     const int32_t* g_ndelta;   // [H]
+    int g_cap;                 // selection capacity per head
     int g_dcap;
+    // -- 128 bytes: what the row lookup and the first loads need
+    int H;
     int static_len;
-    double inv_S;              // 1 / S (split boundaries)
     int s_stride;              // steady rows per head (< 2^31, checked by the host)
     int list_rows;             // list rows per head (< 2^31, checked by the host)
     const uint16_t* sk;
     const uint16_t* sv;
     const uint16_t* lk;
     const uint16_t* lv;
-    // -- 128 bytes
     float scale_log2;          // scale * log2(e)
     int o_base;                // LDS word of the staged offsets (after the prefix)
     int stage_words;           // LDS words shared by the staged selection and the K / V tiles
-    int fast;                  // the short form (attention_kernel<G, true>)
-    float* part_acc;           // [H][S][G][128]
-    float* part_ml;            // [H][S][G][2]
+    int nr;                    // the short form's row locations per lane (0: the general form)
+    // -- 192 bytes
+    int total;                 // workgroups of the split pass (= partials)
+    float* part_acc;           // [total][G][128]
+    float* part_ml;            // [total][G][2]
     uint16_t* out;             // [H*G][128]
     float* lse;                // [H*G] or null
 };
-static_assert(offsetof(DecParams, g_ndelta) == 64 && offsetof(DecParams, scale_log2) == 128,
-              "prologue fields in the first 64 bytes, lookup and load fields in the next 64");
+static_assert(offsetof(DecParams, q) == 64 && offsetof(DecParams, H) == 128 && offsetof(DecParams, total) == 192,
+              "prologue fields in the first 128 bytes, lookup and load fields in the next 64");
 
 // floor(R s / S) for R < 2^32 and 0 <= s <= S <= kMaxSplit.  R s < 2^44 is
 // exact in fp64 and the rounded quotient is within 2^-8 / S of R s / S,
@@ -189,12 +201,14 @@ constexpr int fast_words() {
 // | delta]; writes one partial (max, sum, unnormalised output).  The head's
 // selection (row prefix and CSR offset per cell, at most kStageCap cells in
 // the first round trip) is staged in LDS together with q and the row counts.
-// FAST (at most kFastCap cells, kFastRows rows per workgroup): each lane
-// holds the locations of two of its wave's rows in registers, and the staged
-// selection does not share LDS with the tiles, so no workgroup barrier
-// separates the row lookup from the first loads.
-template <int G, bool FAST>
+// NR > 0, the short form (at most kFastCap cells, fast_rows(NR) rows per
+// workgroup): each lane holds the locations of NR of its wave's rows in
+// registers, and the staged selection does not share LDS with the tiles, so
+// no workgroup barrier separates the row lookup from the first loads.
+template <int G, int NR>
 __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
+    constexpr bool FAST = NR > 0;
+    static_assert(NR == 0 || NR == 2 || NR == 4, "two or four row locations per lane");
     extern __shared__ __attribute__((aligned(16))) int lds[];
     uint16_t* s_k = reinterpret_cast<uint16_t*>(lds);   // the tiles reuse the staged selection's words
     uint16_t* s_v = s_k + kTileU16;
@@ -205,16 +219,36 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
     int* P = FAST ? s_drow + kDeltaMax : lds;       // [g_cap + 1] row prefix of the selected cells
     int* O = FAST ? P + kFastPad : lds + a.o_base;  // [g_cap] CSR offset of each selected cell
 
-    // split = b / H, h = (b % H + split) % H, by multiply-highs (exact for
-    // b * H < 2^32, which the host checks)
+    // this workgroup's run, head and split (divisions by the run's head
+    // count as multiply-highs, exact for workgroups x heads < 2^32, which the
+    // host checks)
+    // (selects only, no branch and no indexed load).  The empty asm takes a
+    // field of each of the first three argument lines, so that the lines are
+    // fetched at once rather than one after another as the code needs them.
+    asm volatile("" ::"s"(a.run[0].x), "s"(a.q), "s"(a.H));
+    // (component by component: a select of whole int4 values went through
+    // scratch memory)
     const uint32_t b = blockIdx.x;
-    const int split = a.h_magic ? static_cast<int>(__umulhi(b, a.h_magic)) : static_cast<int>(b);
-    int h = 0;
-    if (a.h_magic) {
-        h = static_cast<int>(b - static_cast<uint32_t>(split) * a.H) +
-            (split - static_cast<int>(__umulhi(static_cast<uint32_t>(split), a.h_magic)) * a.H);
-        if (h >= a.H) h -= a.H;
+    int rx = a.run[0].x, ry = a.run[0].y, rz = a.run[0].z, rw = a.run[0].w;
+#pragma unroll
+    for (int i = 1; i < kMaxRuns; ++i) {
+        const bool in = a.run[i].x <= static_cast<int>(b);
+        rx = in ? a.run[i].x : rx;
+        ry = in ? a.run[i].y : ry;
+        rz = in ? a.run[i].z : rz;
+        rw = in ? a.run[i].w : rw;
     }
+    const int nh = rz >> 16, S_h = max(rz & 0xFFFF, 1);
+    const uint32_t local = b - static_cast<uint32_t>(rx);
+    const uint32_t mg = static_cast<uint32_t>(rw);
+    const int split = mg ? static_cast<int>(__umulhi(local, mg)) : static_cast<int>(local);
+    int hl = static_cast<int>(local - static_cast<uint32_t>(split) * nh) +
+             (split - static_cast<int>(__umulhi(static_cast<uint32_t>(split), mg)) * nh);
+    hl = hl >= nh ? hl - nh : hl;
+    hl = mg ? hl : 0;
+    const int h = ry + hl;
+    const int64_t pbase = rx + static_cast<int64_t>(hl) * S_h;   // partial of split 0 of this head
+    const double inv_S = 1.0 / static_cast<double>(S_h);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lg = lane >> 4, ln = lane & 15;
 
@@ -267,9 +301,9 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
     const int sl = a.static_len;
     // split boundaries floor(R s / S) (R < 2^32)
     const uint32_t R = static_cast<uint32_t>(sl) + static_cast<uint32_t>(nrows) + static_cast<uint32_t>(nd);
-    const int64_t r0 = split_floor(R, split, a.S, a.inv_S);
-    const int64_t r1e = split_floor(R, split + 1, a.S, a.inv_S);
-    const int64_t r1 = min(r1e, r0 + (FAST ? kFastRows : kLocCap));   // the host sizes S so that this never cuts
+    const int64_t r0 = split_floor(R, split, S_h, inv_S);
+    const int64_t r1e = split_floor(R, split + 1, S_h, inv_S);
+    const int64_t r1 = min(r1e, r0 + (FAST ? fast_rows(NR) : kLocCap));   // the host sizes S so that this never cuts
 
     // ---- row lookup: s_loc[i] for rows r0 + i of this split.  Each wave
     // fills the entries of its own quarter: a steady
@@ -282,30 +316,33 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
     // the steady zone. ----
     const int nr = static_cast<int>(r1 - r0);
     const int wb = nr * wave / kWaves, we = nr * (wave + 1) / kWaves;
-    const int wn = we - wb;   // <= kLocCap / 4 = 512 (FAST: kFastRows / 4 = 128)
+    const int wn = we - wb;   // <= kLocCap / 4 = 512 (FAST: 64 NR)
     const int lmax = max(a.list_rows - 1, 0);
     const int smax = a.s_stride - 1;
-    // FAST: locations of rows wb + lane and wb + lane + 64, same encoding
-    // (rows past the wave's end: list row 0, never used)
-    int loc0 = 0, loc1 = 0;
+    // FAST: locations of rows wb + lane + 64 r (r < NR), same encoding (rows
+    // past the wave's end: list row 0, never used)
+    constexpr int NRL = NR > 0 ? NR : 1;
+    int loc[NRL];
+#pragma unroll
+    for (int r = 0; r < NRL; ++r) loc[r] = 0;
     if constexpr (FAST) {
         const int64_t w0 = r0 + wb;
         const int pa = static_cast<int>(min(max(sl - w0, int64_t(0)), int64_t(wn)));
         const int pb = static_cast<int>(min(max(sl + nrows - w0, int64_t(0)), int64_t(wn)));
-        auto fixed = [&](int i) {   // steady or delta row at position i (0 otherwise)
-            if (i < pa) return -1 - static_cast<int>(w0 + i);
-            if (i >= pb && i < wn) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {   // steady or delta rows
+            const int i = lane + 64 * r;
+            if (i < pa) {
+                loc[r] = -1 - static_cast<int>(w0 + i);
+            } else if (i >= pb && i < wn) {
                 const int d = static_cast<int>(w0 + i - sl - nrows);
-                return -1 - min(max(s_drow[min(d, kDeltaMax - 1)], 0), smax);
+                loc[r] = -1 - min(max(s_drow[min(d, kDeltaMax - 1)], 0), smax);
             }
-            return 0;
-        };
-        loc0 = fixed(lane);
-        loc1 = fixed(lane + 64);
+        }
         if (pb > pa) {
-            int* fl = s_loc + wave * 128;   // cell that starts at each position, else INT_MIN
-            fl[lane] = INT_MIN;
-            fl[lane + 64] = INT_MIN;
+            int* fl = s_loc + wave * 64 * NR;   // cell that starts at each position, else INT_MIN
+#pragma unroll
+            for (int r = 0; r < NR; ++r) fl[lane + 64 * r] = INT_MIN;
             const int jlo = static_cast<int>(w0 + pa - sl), jhi = jlo + (pb - pa);
             // c0 = the last cell with P[c] <= jlo (P[0] = 0 <= jlo): two
             // ballot rounds, m <= kFastCap < 64 * 64
@@ -324,16 +361,17 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
                 if (__builtin_amdgcn_readlane(pc, 63) >= jhi) break;
             }
             wave_lds_sync();
-            const int s0 = wave_incl_max_scan(fl[lane]);
-            const int s1 = max(wave_incl_max_scan(fl[lane + 64]), __builtin_amdgcn_readlane(s0, 63));
-            auto sel_loc = [&](int i, int s, int dflt) {
-                if (i < pa || i >= pb) return dflt;
-                const int c = max(s, c0);
-                const int j = jlo + (i - pa);
-                return min(max(O[c] + (j - P[c]), 0), lmax);
-            };
-            loc0 = sel_loc(lane, s0, loc0);
-            loc1 = sel_loc(lane + 64, s1, loc1);
+            int carry = c0;   // the cell of the positions before this lane's
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                const int sc = max(wave_incl_max_scan(fl[lane + 64 * r]), carry);
+                carry = __builtin_amdgcn_readlane(sc, 63);
+                const int i = lane + 64 * r;
+                if (i >= pa && i < pb) {
+                    const int j = jlo + (i - pa);
+                    loc[r] = min(max(O[sc] + (j - P[sc]), 0), lmax);
+                }
+            }
         }
     } else {
         const int64_t w0 = r0 + wb;   // first row of this wave
@@ -423,9 +461,12 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
                 const int jt = t * 16 + it * 4 + rg;
                 int lr;
                 if constexpr (FAST) {
-                    // row jt sits in lane jt % 64 of loc0 (tiles 0-3) or loc1
-                    // (tiles 4-7); every lane takes part in the shuffle
-                    const int v = __shfl(t < 4 ? loc0 : loc1, jt & 63);
+                    // row jt sits in lane jt % 64 of loc[t / 4] (t / 4 is
+                    // wave-uniform); every lane takes part in the shuffle
+                    int src = loc[0];
+#pragma unroll
+                    for (int r = 1; r < NR; ++r) src = (t >> 2) == r ? loc[r] : src;
+                    const int v = __shfl(src, jt & 63);
                     lr = jt < wn ? v : 0;
                 } else {
                     lr = jt < wn ? s_loc[wb + jt] : 0;
@@ -547,7 +588,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
     __syncthreads();
     // workgroup partial (waves merged in order); an empty split writes an
     // empty state (max -inf, sum 0), which the merge weighs 0
-    const int64_t pbase = static_cast<int64_t>(h) * a.S + split;
+    const int64_t pidx = pbase + split;
     for (int o = tid; o < G * 128; o += kThreads) {
         const int g = o >> 7, d = o & 127;
         float M = -INFINITY;
@@ -560,10 +601,10 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(DecParams a) {
             L += s_ml[(w * G + g) * 2 + 1] * wt;
             A += s_acc[(w * G + g) * 128 + d] * wt;
         }
-        a.part_acc[(pbase * G + g) * 128 + d] = A;
+        a.part_acc[(pidx * G + g) * 128 + d] = A;
         if (d == 0) {
-            a.part_ml[(pbase * G + g) * 2 + 0] = M;
-            a.part_ml[(pbase * G + g) * 2 + 1] = L;
+            a.part_ml[(pidx * G + g) * 2 + 0] = M;
+            a.part_ml[(pidx * G + g) * 2 + 1] = L;
         }
     }
 }
@@ -582,10 +623,20 @@ __global__ __launch_bounds__(256) void merge_kernel(DecParams a, int G) {
     const int g = chunk >> 1;
     const int tid = threadIdx.x, q = tid >> 6, lane = tid & 63;
     const int o = chunk * 64 + lane;  // g * 128 + d
-    const int ns = a.S;
+    // this head's run: its splits and first partial (component selects)
+    int rx = a.run[0].x, ry = a.run[0].y, rz = a.run[0].z;
+#pragma unroll
+    for (int i = 1; i < kMaxRuns; ++i) {
+        const bool in = a.run[i].y <= h && a.run[i].x != INT_MAX;
+        rx = in ? a.run[i].x : rx;
+        ry = in ? a.run[i].y : ry;
+        rz = in ? a.run[i].z : rz;
+    }
+    const int ns = max(rz & 0xFFFF, 1);
+    const int64_t first = rx + static_cast<int64_t>(h - ry) * ns;
     const int64_t stride = static_cast<int64_t>(G) * 128;
-    const float* pacc = a.part_acc + static_cast<int64_t>(h) * ns * stride + o;
-    const float* pml = a.part_ml + (static_cast<int64_t>(h) * ns * G + g) * 2;
+    const float* pacc = a.part_acc + first * stride + o;
+    const float* pml = a.part_ml + (first * G + g) * 2;
     float v[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
@@ -661,9 +712,13 @@ int64_t splits_one_round(const imi_attention_args* a) {
 }
 
 // The short form when the selection fits its staging and one round of
-// workgroups keeps every split within kFastRows rows.
-bool attn_fast(const imi_attention_args* a) {
-    return a->sel_cap <= kFastCap && rows_bound(a) <= splits_one_round(a) * kFastRows;
+// workgroups keeps every split within fast_rows(NR) rows: the row
+// locations per lane, or 0 for the general form.
+int attn_nr(const imi_attention_args* a) {
+    if (a->sel_cap > kFastCap) return 0;
+    for (int nr = 2; nr <= kFastNRMax; nr += 2)
+        if (rows_bound(a) <= splits_one_round(a) * fast_rows(nr)) return nr;
+    return 0;
 }
 
 // Splits per head: about one workgroup per CU in all, and enough that no
@@ -675,20 +730,86 @@ int splits_per_head(const imi_attention_args* a) {
     return static_cast<int>(s);
 }
 
+uint32_t div_magic(int n) {   // floor(2^32 / n) + 1, or 0 for n = 1 (quotient = dividend)
+    return n > 1 ? static_cast<uint32_t>((uint64_t(1) << 32) / static_cast<uint64_t>(n) + 1) : 0u;
+}
+
+// Workgroups of the split pass.  Equal splits per head (S > 0), or, with
+// per-head row bounds that form 2..kMaxRuns runs of equal bounds (a ragged
+// batch), splits proportional to each run's bound.
+struct SplitPlan {
+    int S = 0;
+    int total = 0;   // workgroups = partials
+    int nr = 0;      // the short form's row locations per lane
+    int4 run[kMaxRuns];
+};
+
+SplitPlan split_plan(const imi_attention_args* a) {
+    SplitPlan P;
+    const int H = a->kv_heads;
+    const int64_t rb = rows_bound(a);
+    for (int r = 0; r < kMaxRuns; ++r) P.run[r] = make_int4(INT_MAX, H, 0, 0);
+    if (a->head_rows_bound && H > 1) {
+        int nruns = 0;
+        int h0[kMaxRuns];
+        int64_t B[kMaxRuns];
+        bool ok = true;
+        for (int h = 0; h < H && ok; ++h) {
+            int64_t bh = a->head_rows_bound[h];
+            bh = bh < 1 ? 1 : (bh > rb ? rb : bh);   // never above the launch-wide bound
+            if (h == 0 || bh != B[nruns - 1]) {
+                if (nruns == kMaxRuns) {
+                    ok = false;
+                } else {
+                    h0[nruns] = h;
+                    B[nruns] = bh;
+                    ++nruns;
+                }
+            }
+        }
+        if (ok && nruns > 1) {
+            int64_t tot = 0;
+            for (int r = 0; r < nruns; ++r) tot += B[r] * ((r + 1 < nruns ? h0[r + 1] : H) - h0[r]);
+            const int64_t T = device_cus() > H ? device_cus() : H;
+            int64_t wg = 0, per = 0;
+            for (int r = 0; r < nruns; ++r) {
+                const int nh = (r + 1 < nruns ? h0[r + 1] : H) - h0[r];
+                int64_t S = T * B[r] / tot;
+                const int64_t need = (B[r] + kLocCap - 1) / kLocCap;
+                S = S < need ? need : S;
+                S = S < 1 ? 1 : (S > kMaxSplit ? kMaxSplit : S);
+                P.run[r] = make_int4(static_cast<int>(wg), h0[r], static_cast<int>(S) | (nh << 16),
+                                     static_cast<int>(div_magic(nh)));
+                wg += nh * S;
+                const int64_t rows = (B[r] + S - 1) / S;
+                per = rows > per ? rows : per;
+            }
+            P.S = 0;
+            P.total = static_cast<int>(wg);
+            if (a->sel_cap <= kFastCap)
+                for (int nr = 2; nr <= kFastNRMax && P.nr == 0; nr += 2)
+                    if (per <= fast_rows(nr)) P.nr = nr;
+            return P;
+        }
+    }
+    P.S = splits_per_head(a);
+    P.total = H * P.S;
+    P.nr = attn_nr(a);
+    P.run[0] = make_int4(0, 0, P.S | (H << 16), static_cast<int>(div_magic(H)));
+    return P;
+}
+
 size_t attn_workspace(const imi_attention_args* a, DecParams* p) {
-    const int S = splits_per_head(a);
+    const SplitPlan P = split_plan(a);
     Carver cv(a->workspace);
-    float* acc = cv.take<float>(static_cast<size_t>(a->kv_heads) * S * a->groups * 128);
-    float* ml = cv.take<float>(static_cast<size_t>(a->kv_heads) * S * a->groups * 2);
+    float* acc = cv.take<float>(static_cast<size_t>(P.total) * a->groups * 128);
+    float* ml = cv.take<float>(static_cast<size_t>(P.total) * a->groups * 2);
     if (p) {
         p->part_acc = acc;
         p->part_ml = ml;
-        p->S = S;
-        p->inv_S = 1.0 / static_cast<double>(S);
-        p->h_magic = a->kv_heads > 1
-                         ? static_cast<uint32_t>((uint64_t(1) << 32) / static_cast<uint64_t>(a->kv_heads) + 1)
-                         : 0u;   // one head: split = b
-        p->fast = attn_fast(a) ? 1 : 0;
+        p->total = P.total;
+        p->nr = P.nr;
+        for (int r = 0; r < kMaxRuns; ++r) p->run[r] = P.run[r];
     }
     return cv.used();
 }
@@ -699,6 +820,7 @@ int attn_validate(const imi_attention_args* a, bool need_sel) {
     IMI_REQUIRE(a->groups == 1 || a->groups == 2 || a->groups == 4 || a->groups == 7 || a->groups == 8,
                 IMI_ERR_UNSUPPORTED, "imi_sparse_attention: %d query heads per kv head unsupported", a->groups);
     IMI_REQUIRE(a->kv_heads > 0, IMI_ERR_INVALID, "imi_sparse_attention: kv_heads must be > 0");
+    IMI_REQUIRE(a->kv_heads < 32768, IMI_ERR_UNSUPPORTED, "imi_sparse_attention: %d kv heads exceed 32767", a->kv_heads);
     IMI_REQUIRE(a->query && a->out, IMI_ERR_INVALID, "imi_sparse_attention: null query/out");
     IMI_REQUIRE(a->static_len >= 0 && a->static_len <= a->steady_stride, IMI_ERR_INVALID,
                 "imi_sparse_attention: static_len %d outside steady zone of %lld rows", a->static_len,
@@ -729,9 +851,8 @@ int attn_validate(const imi_attention_args* a, bool need_sel) {
                 "imi_sparse_attention: %lld rows need more than %d splits per head",
                 static_cast<long long>(rows_bound(a)), kMaxSplit);
     // the kernel splits its workgroup index by a 32-bit multiply-high
-    IMI_REQUIRE(static_cast<uint64_t>(a->kv_heads) * splits_per_head(a) * a->kv_heads < (uint64_t(1) << 32),
-                IMI_ERR_UNSUPPORTED, "imi_sparse_attention: %d kv heads x %d splits too large", a->kv_heads,
-                splits_per_head(a));
+    IMI_REQUIRE(static_cast<uint64_t>(split_plan(a).total) * a->kv_heads < (uint64_t(1) << 32), IMI_ERR_UNSUPPORTED,
+                "imi_sparse_attention: %d kv heads x %d workgroups too large", a->kv_heads, split_plan(a).total);
     return IMI_OK;
 }
 
@@ -765,18 +886,22 @@ int launch_att(const DecParams& p, hipStream_t stream) {
         constexpr size_t lds_max = static_cast<size_t>(2 * (kStageMax + 4) + tail_words<G>()) * 4;
         constexpr size_t lds_fast = static_cast<size_t>(fast_words<G>()) * 4;
         static_assert(lds_max <= 160 * 1024 && lds_fast <= 160 * 1024, "LDS of one workgroup");
-        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<G, false>),
+        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<G, 0>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_max)));
-        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<G, true>),
+        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<G, 2>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_fast)));
+        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<G, 4>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_fast)));
         attr_set = true;
     }
-    if (p.fast) {
-        const size_t lds = static_cast<size_t>(fast_words<G>()) * 4;
-        hipLaunchKernelGGL((attention_kernel<G, true>), dim3(p.H * p.S), dim3(kThreads), lds, stream, p);
+    const size_t lds_fast = static_cast<size_t>(fast_words<G>()) * 4;
+    if (p.nr == 2) {
+        hipLaunchKernelGGL((attention_kernel<G, 2>), dim3(p.total), dim3(kThreads), lds_fast, stream, p);
+    } else if (p.nr == 4) {
+        hipLaunchKernelGGL((attention_kernel<G, 4>), dim3(p.total), dim3(kThreads), lds_fast, stream, p);
     } else {
         const size_t lds = static_cast<size_t>(p.stage_words + tail_words<G>()) * 4;
-        hipLaunchKernelGGL((attention_kernel<G, false>), dim3(p.H * p.S), dim3(kThreads), lds, stream, p);
+        hipLaunchKernelGGL((attention_kernel<G, 0>), dim3(p.total), dim3(kThreads), lds, stream, p);
     }
     IMI_LAUNCH_CHECK("attention_kernel");
     return IMI_OK;

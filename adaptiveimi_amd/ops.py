@@ -575,6 +575,17 @@ class DecodePlan:
         t.scale = float(scale if scale is not None else 1.0 / math.sqrt(D))
         t.out = self.out.data_ptr()
         t.out_lse = _ptr(out_lse)
+        # a ragged batch: per-head row bounds (host memory, read at each call),
+        # so that the attention gives each sequence's heads splits in
+        # proportion to their budgets
+        self._head_bounds = None
+        if budget.head_buffer_pages is not None:
+            rc = update.ring_cap if update is not None else 0
+            mt = budget.head_max_tokens or [budget.max_tokens] * H
+            bounds = [t.steady_stride + bp * budget.page_size + (m if budget.tile_mode else 0) + rc
+                      for bp, m in zip(budget.head_buffer_pages, mt)]
+            self._head_bounds = (ctypes.c_int32 * H)(*bounds)
+            t.head_rows_bound = ctypes.addressof(self._head_bounds)
         need = ctypes.c_size_t()
         check(_lib.lib().imi_decode_workspace_size(ctypes.byref(a), ctypes.byref(need)), "imi_decode_workspace_size")
         self.ws = torch.zeros(max(need.value, 256), dtype=torch.uint8, device=dev)

@@ -256,6 +256,14 @@ typedef struct {
     const int32_t* delta_rows;    /* [H][delta_cap] */
     const int32_t* n_delta;       /* [H] */
     int32_t delta_cap;
+    /* Optional HOST array [H] (read during the call, not kept), NULL if
+     * absent: a bound on each head's attended rows (static + selected +
+     * delta), e.g. buffer_pages[h] * page_size + steady_stride in a ragged
+     * batch.  When the bounds differ, the split pass gives each run of equal
+     * bounds a number of workgroups per head proportional to its bound (at
+     * most 4 runs; more fall back to equal shares).  No counterpart in the
+     * reference (its decode batch is one sequence). */
+    const int32_t* head_rows_bound;
 } imi_attention_args;
 
 int imi_attention_workspace_size(const imi_attention_args* a, size_t* bytes);

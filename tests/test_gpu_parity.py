@@ -630,16 +630,19 @@ def test_config3_shape_decode_matches_oracle(ops, oracle):
     _check_attention(res, ref)
 
 
-@pytest.mark.parametrize("ks", [(32, 32), (6, 6, 6, 6)])
-def test_ragged_batch_decode_matches_oracle(ops, oracle, ks):
-    """Config 2 at reduced scale: the KV heads of four sequences of different
-    lengths (so different token and page budgets) share one selection and
-    attention launch, their lists living in one [B*H, max_len, D] buffer.
-    Every sequence must match its own batch-1 oracle step: same selected
-    cells, attention within 2e-2 + 1e-2 |ref|."""
+@pytest.mark.parametrize("ks,lens", [((32, 32), (3000, 6000, 9000, 12000)), ((6, 6, 6, 6), (3000, 6000, 9000, 12000)),
+                                     ((32, 32), (2000, 12000)), ((32, 32), (3000, 4500, 6000, 9000, 12000))])
+def test_ragged_batch_decode_matches_oracle(ops, oracle, ks, lens):
+    """Config 2 at reduced scale: the KV heads of several sequences of
+    different lengths (so different token and page budgets) share one
+    selection and attention launch, their lists living in one
+    [B*H, max_len, D] buffer.  Every sequence must match its own batch-1
+    oracle step: same selected cells, attention within 2e-2 + 1e-2 |ref|.
+    Two to four sequences take the attention's per-run split counts, five
+    fall back to equal splits per head."""
     from adaptiveimi_amd import synthetic
 
-    lens = [3000, 6000, 9000, 12000]
+    lens = list(lens)
     note(f"[ragged] lens={lens} ks={ks}")
     H, G, D, static_len = 4, 7, 128, 96
     B, cap = len(lens), max(lens)
