@@ -7,29 +7,32 @@
 // empty, so the work runs over the occupied (compact) cells that
 // imi_build_index lists in ascending global id:
 //
-//   sel4_score_kernel   16 occupied cells per thread: qsum (g ascending)
-//                       and the 128-term FMA chain over [C0[l0] | C1[l1] |
-//                       C2[l2] | C3[l3]] (the merged centroid, never
-//                       materialised), continued from prefixes shared per
-//                       (l0, l1) and (l0, l1, l2); key = (score, ~gid) so
-//                       that key order is the reference rank order; one
-//                       score range per workgroup
-//   sel4_hist_kernel    the head's range from those, then 2048 linear
-//                       buckets over it
-//   sel4_gather_kernel  the bucket holding the K'-th best cell, where
-//                       K' = min(nprobe, buffer_pages, occupied cells);
-//                       every cell in or above it becomes a candidate
-//                       (16 counters per head, by cell index)
-//   sel4_final_kernel   one workgroup per head: bitonic sort of the
-//                       candidates (or, when a counter overflows, an exact
-//                       radix select of the K'-th key), then the token and
-//                       page budgets in rank order
-//
+//   sel4_score_kernel   16 occupied cells per thread, 16384 per workgroup:
+//                       qsum (g ascending) and the 128-term FMA chain over
+//                       [C0[l0] | C1[l1] | C2[l2] | C3[l3]] (the merged
+//                       centroid, never materialised), continued from
+//                       prefixes shared per (l0, l1) and (l0, l1, l2); key =
+//                       (score, ~gid) so that key order is the reference rank
+//                       order.  Each workgroup then lists its candidates:
+//                       all its cells when they are at most K', else the
+//                       cells in the buckets up to the one holding its own
+//                       K'-th best cell (1024 linear buckets over its range),
+//                       a superset of its share of the head's K' best.
+//   sel4_final_kernel   one workgroup per head over the head's candidates:
+//                       2048 linear buckets over their range, the bucket of
+//                       the K'-th best, the candidates at or above it in LDS
+//                       grouped by bucket and ranked inside their bucket by
+//                       counting the better keys (a bitonic sort for a
+//                       bucket over 512; an exact radix select over all
+//                       candidates when more than 8192 are at or above it),
+//                       then the token and page budgets in rank order.
+// K' = min(nprobe, buffer_pages, occupied cells), or nprobe in tile mode and
+// with the delta append.
+
 // Outputs have the 2-way layout (cells in rank order, CSR offset, count,
-// exclusive row prefix, m, rows), so the gather kernel is shared.  The
-// per-head range words live at a fixed place of the workspace and the final
-// kernel zeroes them again, the score kernel clears the histogram and the
-// histogram kernel the candidate counters, so a workspace zero-filled once
+// exclusive row prefix, m, rows), so the attention kernel is shared.  The
+// per-head candidate counters live at a fixed place of the workspace and the
+// final kernel zeroes its head's again, so a workspace zero-filled once
 // serves later calls of any shape.
 #include "imi_common.hpp"
 
@@ -37,26 +40,25 @@ namespace imi {
 namespace {
 
 constexpr int kBins4 = 2048;
-constexpr int kCand4 = 8192;     // candidate capacity per head
+constexpr int kCand4 = 8192;     // candidates ranked in LDS per head
 constexpr int kSegMax = 512;     // largest bucket ranked by counting (larger: a full sort)
 constexpr int kRingSet = 2048;   // ring-code set of the delta match (ring <= 1024 entries)
 constexpr int kK4 = 64;          // centroids per subspace the kernels hold
 constexpr int kDp4 = 32;         // subspace width (D = 128, 4 parts)
 constexpr int kMaxG4 = 8;        // query heads per KV head
-constexpr int kScoreThreads = 256;
+constexpr int kScoreThreads = 256;   // 2-way score kernel
+constexpr int kScore4Threads = 1024; // 4-way score kernel
 constexpr int kFinalThreads = 1024;
 constexpr int kSelCap4 = kCand4;  // cells to rank (K') per head
 constexpr int kExtHeads = 1024;  // KV heads one call handles (fixed-place counters)
-constexpr int kCPT = 16;         // occupied cells per thread in the score / histogram / gather kernels
+constexpr int kCPT = 16;         // occupied cells per thread in the 4-way score kernel
 constexpr int kCS4 = 36;         // LDS row stride of a subspace centroid (16-byte aligned rows)
-constexpr int kTripCap = 1024;   // (l0, l1, l2) prefixes a score workgroup keeps
-constexpr int kCellsPerBlock = kScoreThreads * kCPT;
+constexpr int kTripCap = 4096;   // (l0, l1, l2) prefixes a score workgroup keeps
+constexpr int kCellsPerBlock = kScore4Threads * kCPT;
 constexpr int kDenseScoreCells = kScoreThreads;   // 2-way score kernel: one global cell per thread
 constexpr int kDenseK = 256;                      // 2-way centroids per subspace the score kernel reads
-// the histogram kernel takes 8x more cells per workgroup: its global merge
-// (one atomic per non-empty bin and workgroup) is a per-workgroup cost
-constexpr int kHistCPT = 64;
-constexpr int kHistCellsPerBlock = kScoreThreads * kHistCPT;
+constexpr int kLocBins = 1024;   // buckets of a score workgroup's own candidate cut
+constexpr int kFinalCPT = 16;    // candidates per thread the final kernel holds in registers
 
 struct Sel4 {
     const uint16_t* q;
@@ -80,14 +82,11 @@ struct Sel4 {
     int32_t* n_sel;
     int32_t* n_rows;
     int sel_cap;
-    uint64_t* keys;          // [H][cap]
-    uint32_t* hist;          // [H][kBins4]
-    uint32_t* ext;           // [H][4]: max order key, ~min order key, unused, unused
-    uint32_t* rpart;         // [H][nbs][2]: per-workgroup max order key and max ~order key
-    uint32_t* bcur;          // [H][kBins4]: candidates placed per bucket (gather cursors)
-    int nbs;                 // score workgroups per head (range partials)
-    uint64_t* cand;          // [H][kCand4] candidate keys, grouped by bucket (best bucket first)
-    int32_t* cidx;           // [H][kCand4] their cell indices
+    uint32_t* ncand;         // [kExtHeads] candidates listed per head (zero between calls)
+    uint64_t* cand;          // [H][cap] candidate keys (any order)
+    int32_t* cidx;           // [H][cap] their cell indices
+    uint32_t* rpart;         // [H][nbs][2]: per score workgroup, max order key and max ~order key of its candidates
+    int nbs;                 // score workgroups per head
     // online index maintenance: replaced centroids (by compact id) and the
     // delta ring
     const float* shadow;
@@ -149,12 +148,138 @@ __device__ __forceinline__ uint32_t kmod(uint32_t g, uint32_t k) {
     return POW2 ? g & (k - 1) : g % k;
 }
 
+// The candidates of one score workgroup (T threads, CPT keys per thread,
+// key 0 = no cell, ci = cell index): all its cells when they are at most K',
+// else the cells in the buckets up to the one holding its own K'-th best
+// cell (kLocBins linear buckets over its range; the bucket index falls as
+// the score rises, so these cells include every cell at or above that one,
+// ties included: a superset of the workgroup's share of the head's K'
+// best).  They go to the head's list at one atomic offset per workgroup, in
+// any order; the workgroup's candidate range goes to rpart.  lh: kLocBins
+// ints of LDS, zero on entry.
+template <int T, int CPT>
+__device__ void emit_candidates(const Sel4& a, int h, int kp, const uint64_t (&kv)[CPT], const int (&ci)[CPT],
+                                int* lh) {
+    constexpr int NW = T / 64;
+    __shared__ uint32_t red[NW][3];
+    __shared__ int s_bk;
+    __shared__ int s_base;
+    const int tid = threadIdx.x, w = tid >> 6;
+    // valid cells and their range (order keys)
+    int nv = 0;
+    uint32_t kmax = 0, nkmin = 0;
+#pragma unroll
+    for (int u = 0; u < CPT; ++u)
+        if (kv[u] != 0ull) {
+            const uint32_t ok = static_cast<uint32_t>(kv[u] >> 32);
+            ++nv;
+            kmax = max(kmax, ok);
+            nkmin = max(nkmin, ~ok);
+        }
+    nv = wave_sum_i(nv);
+    kmax = static_cast<uint32_t>(wave_max_i(static_cast<int>(kmax ^ 0x80000000u))) ^ 0x80000000u;
+    nkmin = static_cast<uint32_t>(wave_max_i(static_cast<int>(nkmin ^ 0x80000000u))) ^ 0x80000000u;
+    if (lane_id() == 0) {
+        red[w][0] = static_cast<uint32_t>(nv);
+        red[w][1] = kmax;
+        red[w][2] = nkmin;
+    }
+    if (tid == 0) s_bk = kp > 0 ? kLocBins : -1;   // every bucket: all cells are candidates; none
+    __syncthreads();
+    int nvb = 0;
+    uint32_t bmax = 0, bnmin = 0;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+        nvb += static_cast<int>(red[j][0]);
+        bmax = max(bmax, red[j][1]);
+        bnmin = max(bnmin, red[j][2]);
+    }
+    const float wmax = key_score(static_cast<uint64_t>(bmax) << 32);
+    const float wmin = key_score(static_cast<uint64_t>(~bnmin) << 32);
+    const float range = wmax - wmin;
+    const float inv = range > 0.0f ? static_cast<float>(kLocBins) / range : 0.0f;
+    auto bucket = [&](uint64_t key) {
+        const float t = (wmax - key_score(key)) * inv;
+        return t < static_cast<float>(kLocBins - 1) ? static_cast<int>(t) : kLocBins - 1;
+    };
+    if (nvb > kp && kp > 0) {   // workgroup-uniform
+#pragma unroll
+        for (int u = 0; u < CPT; ++u)
+            if (kv[u] != 0ull) atomicAdd(&lh[bucket(kv[u])], 1);
+        __syncthreads();
+        // the bucket holding the kp-th best: kLocBins / T buckets per thread
+        constexpr int PB = kLocBins / T;
+        int v[PB], loc = 0;
+#pragma unroll
+        for (int j = 0; j < PB; ++j) {
+            v[j] = lh[tid * PB + j];
+            loc += v[j];
+        }
+        const int incl = wave_incl_scan(loc);
+        __syncthreads();   // every histogram read is done: red is reused below
+        if (lane_id() == 63) red[w][0] = static_cast<uint32_t>(incl);
+        __syncthreads();
+        int run = incl - loc;
+        for (int j = 0; j < w; ++j) run += static_cast<int>(red[j][0]);
+#pragma unroll
+        for (int j = 0; j < PB; ++j) {
+            if (run < kp && run + v[j] >= kp) s_bk = tid * PB + j;
+            run += v[j];
+        }
+        __syncthreads();
+    }
+    const int bk = s_bk;
+    // this workgroup's candidates, their offsets and range
+    int cnt = 0;
+    uint32_t cnmin = 0;
+    bool cf[CPT];
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        cf[u] = kv[u] != 0ull && bk >= 0 && (bk >= kLocBins || bucket(kv[u]) <= bk);
+        if (cf[u]) {
+            ++cnt;
+            cnmin = max(cnmin, ~static_cast<uint32_t>(kv[u] >> 32));
+        }
+    }
+    const int cincl = wave_incl_scan(cnt);
+    cnmin = static_cast<uint32_t>(wave_max_i(static_cast<int>(cnmin ^ 0x80000000u))) ^ 0x80000000u;
+    __syncthreads();   // red is reused
+    if (lane_id() == 63) red[w][0] = static_cast<uint32_t>(cincl);
+    if (lane_id() == 0) red[w][2] = cnmin;
+    __syncthreads();
+    int before = cincl - cnt, tot = 0;
+    uint32_t cmn = 0;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+        before += j < w ? static_cast<int>(red[j][0]) : 0;
+        tot += static_cast<int>(red[j][0]);
+        cmn = max(cmn, red[j][2]);
+    }
+    if (tid == 0) {
+        s_base = tot > 0 ? static_cast<int>(atomicAdd(&a.ncand[h], static_cast<uint32_t>(tot))) : 0;
+        a.rpart[(static_cast<int64_t>(h) * a.nbs + blockIdx.x) * 2 + 0] = tot > 0 ? bmax : 0u;
+        a.rpart[(static_cast<int64_t>(h) * a.nbs + blockIdx.x) * 2 + 1] = tot > 0 ? cmn : 0u;
+    }
+    __syncthreads();
+    int pos = s_base + before;
+#pragma unroll
+    for (int u = 0; u < CPT; ++u)
+        if (cf[u]) {
+            if (pos < a.cap) {   // a head lists at most cap cells
+                a.cand[static_cast<int64_t>(h) * a.cap + pos] = kv[u];
+                a.cidx[static_cast<int64_t>(h) * a.cap + pos] = ci[u];
+            }
+            ++pos;
+        }
+}
+
 // ONLINE: replaced centroids / the delta ring (a separate instantiation).
 template <bool ONLINE, bool POW2>
-__global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
+__global__ __launch_bounds__(kScore4Threads) void sel4_score_kernel(Sel4 a) {
     __shared__ __attribute__((aligned(16))) float qs[128];
     __shared__ int s_pair[2];
     __shared__ int s_trip[2];
+    __shared__ int lh[kLocBins];   // the candidate cut's buckets
     // dynamic LDS, sized by the launch: C0..C3 rows [4][kmax][kCS4], the
     // chain over subspaces 0 and 1 per (l0, l1) pair this block uses
     // [k0 * k1], then the chain over subspaces 0..2 per (l0, l1, l2) [kTripCap]
@@ -170,13 +295,13 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     uint32_t gv[kCPT];
 #pragma unroll
     for (int u = 0; u < kCPT; ++u) {
-        const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
+        const int c = blockIdx.x * kCellsPerBlock + u * kScore4Threads + tid;
         gv[u] = c < a.cap ? static_cast<uint32_t>(a.gid[static_cast<int64_t>(h) * a.cap + c]) : 0u;
     }
     const int na = n_active(a, h);
 #pragma unroll
     for (int u = 0; u < kCPT; ++u)
-        if (blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid >= na) gv[u] = 0u;
+        if (blockIdx.x * kCellsPerBlock + u * kScore4Threads + tid >= na) gv[u] = 0u;
     const int c_first = blockIdx.x * kCellsPerBlock;
     const int c_last = min(na, c_first + kCellsPerBlock) - 1;
     const uint32_t k23 = static_cast<uint32_t>(a.k[2]) * static_cast<uint32_t>(a.k[3]);
@@ -186,7 +311,7 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     if (c_first <= c_last) {
 #pragma unroll
         for (int u = 0; u < kCPT; ++u) {
-            const int c = c_first + u * kScoreThreads + tid;
+            const int c = c_first + u * kScore4Threads + tid;
             if (c == c_first) {
                 s_pair[0] = static_cast<int>(kdiv<POW2>(gv[u], k23));
                 s_trip[0] = static_cast<int>(kdiv<POW2>(gv[u], k3));
@@ -213,21 +338,19 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
         constexpr int kRowF4 = kDp4 / 4;
         const float4* cp = reinterpret_cast<const float4*>(a.cent + static_cast<int64_t>(h) * 4 * a.kmax * kDp4);
         const int n4 = 4 * a.kmax * kRowF4;
-        float4 cv[4 * kK4 * kRowF4 / kScoreThreads];
+        float4 cv[4 * kK4 * kRowF4 / kScore4Threads];
 #pragma unroll
-        for (int u = 0; u < 4 * kK4 * kRowF4 / kScoreThreads; ++u) {
-            const int i = tid + u * kScoreThreads;
+        for (int u = 0; u < 4 * kK4 * kRowF4 / kScore4Threads; ++u) {
+            const int i = tid + u * kScore4Threads;
             cv[u] = i < n4 ? cp[i] : make_float4(0, 0, 0, 0);
         }
 #pragma unroll
-        for (int u = 0; u < 4 * kK4 * kRowF4 / kScoreThreads; ++u) {
-            const int i = tid + u * kScoreThreads;
+        for (int u = 0; u < 4 * kK4 * kRowF4 / kScore4Threads; ++u) {
+            const int i = tid + u * kScore4Threads;
             if (i < n4) *reinterpret_cast<float4*>(&cs[(i / kRowF4) * kCS4 + 4 * (i % kRowF4)]) = cv[u];
         }
     }
-    // this head's histogram starts at zero (the histogram kernel is the next launch)
-    for (int i = blockIdx.x * kScoreThreads + tid; i < kBins4; i += gridDim.x * kScoreThreads)
-        a.hist[static_cast<int64_t>(h) * kBins4 + i] = 0;
+    for (int i = tid; i < kLocBins; i += kScore4Threads) lh[i] = 0;
     __syncthreads();
     // The 128-term chain runs over C0[l0], C1[l1], C2[l2], C3[l3] in turn, so
     // its value after the first 64 terms depends on (l0, l1) only: computed
@@ -236,7 +359,7 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     const int pa = c_first <= c_last ? s_pair[0] : 0;
     // (ids out of order or out of range would only give wrong scores: both ends are clamped)
     const int npair = c_first <= c_last ? min(max(s_pair[1] - s_pair[0] + 1, 0), pair_cap) : 0;
-    for (int t = tid; t < npair; t += kScoreThreads) {
+    for (int t = tid; t < npair; t += kScore4Threads) {
         const uint32_t pt = static_cast<uint32_t>(pa + t), k1 = static_cast<uint32_t>(a.k[1]);
         const int l0 = static_cast<int>(kdiv<POW2>(pt, k1)), l1 = static_cast<int>(kmod<POW2>(pt, k1));
         float s = 0.0f;
@@ -274,7 +397,7 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
     const int ta = c_first <= c_last ? s_trip[0] : 0;
     const int ntrip = c_first <= c_last ? s_trip[1] - s_trip[0] + 1 : 0;
     if (ntrip > 0 && ntrip <= kTripCap) {
-        for (int t = tid; t < ntrip; t += kScoreThreads) {
+        for (int t = tid; t < ntrip; t += kScore4Threads) {
             const int tg = ta + t;
             float x = p01[min(max(static_cast<int>(kdiv<POW2>(tg, k2)) - pa, 0), pair_cap - 1)];
             const float* c2r = &cs[(2 * a.kmax + static_cast<int>(kmod<POW2>(tg, k2))) * kCS4];
@@ -325,11 +448,14 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
             sv[u] = __builtin_fmaf(q4.w, c4.w, sv[u]);
         }
     }
-    uint32_t okmax = 0, nokmin = 0;
+    uint64_t kv[kCPT];
+    int ci[kCPT];
 #pragma unroll
     for (int u = 0; u < kCPT; ++u) {
-        const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
-        if (c >= na) break;
+        const int c = blockIdx.x * kCellsPerBlock + u * kScore4Threads + tid;
+        ci[u] = c;
+        kv[u] = 0ull;
+        if (c >= na) continue;
         float s = sv[u];
         if (ONLINE && a.upd_slot) {
             const int us = a.upd_slot[static_cast<int64_t>(h) * a.cap + c];
@@ -350,36 +476,9 @@ __global__ __launch_bounds__(kScoreThreads) void sel4_score_kernel(Sel4 a) {
                 }
             }
         }
-        const uint32_t ok = order_key(s);
-        a.keys[static_cast<int64_t>(h) * a.cap + c] = (static_cast<uint64_t>(ok) << 32) | (0xFFFFFFFFu - gv[u]);
-        okmax = max(okmax, ok);
-        nokmin = max(nokmin, ~ok);
+        kv[u] = (static_cast<uint64_t>(order_key(s)) << 32) | (0xFFFFFFFFu - gv[u]);
     }
-    // the workgroup's range partial (max order key, max complement): a plain
-    // store, reduced by the histogram kernel (per-wave atomics on one word per
-    // head serialise when a head has 10^5 cells)
-    uint32_t m1 = okmax, m2 = nokmin;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        m1 = max(m1, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m1), o)));
-        m2 = max(m2, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m2), o)));
-    }
-    __shared__ uint32_t red[kScoreThreads / 64][2];
-    if (lane_id() == 0) {
-        red[tid >> 6][0] = m1;
-        red[tid >> 6][1] = m2;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t r1 = 0, r2 = 0;
-#pragma unroll
-        for (int w = 0; w < kScoreThreads / 64; ++w) {
-            r1 = max(r1, red[w][0]);
-            r2 = max(r2, red[w][1]);
-        }
-        a.rpart[(static_cast<int64_t>(h) * a.nbs + blockIdx.x) * 2 + 0] = r1;
-        a.rpart[(static_cast<int64_t>(h) * a.nbs + blockIdx.x) * 2 + 1] = r2;
-    }
+    emit_candidates<kScore4Threads, kCPT>(a, h, kprime(a, h, na), kv, ci, lh);
 }
 
 // 2-way IMI over every global cell g = l0 * k1 + l1 (the shapes beyond the
@@ -395,7 +494,7 @@ template <bool ONLINE>
 __global__ __launch_bounds__(kScoreThreads) void sel2_dense_score_kernel(Sel4 a) {
     __shared__ __attribute__((aligned(16))) float qs[128];
     __shared__ float p1[kScoreThreads + 2];
-    __shared__ uint32_t red[kScoreThreads / 64][2];
+    __shared__ int lh[kLocBins];   // the candidate cut's buckets
     const int h = blockIdx.y, tid = threadIdx.x;
     const int k1 = a.k[1];
     const int ncells = a.cap;
@@ -431,9 +530,7 @@ __global__ __launch_bounds__(kScoreThreads) void sel2_dense_score_kernel(Sel4 a)
             if (j < a.G) acc += bf16_to_f32(qv[j]);
         qs[tid] = acc;
     }
-    // this head's histogram starts at zero (the histogram kernel is the next launch)
-    for (int i = blockIdx.x * kScoreThreads + tid; i < kBins4; i += gridDim.x * kScoreThreads)
-        a.hist[static_cast<int64_t>(h) * kBins4 + i] = 0;
+    for (int i = tid; i < kLocBins; i += kScoreThreads) lh[i] = 0;
     __syncthreads();
     if (tid < nr) {
         float acc = 0.0f;
@@ -472,185 +569,11 @@ __global__ __launch_bounds__(kScoreThreads) void sel2_dense_score_kernel(Sel4 a)
         }
         sc = acc;
     }
-    const uint32_t ok = order_key(sc);
-    if (in)
-        a.keys[static_cast<int64_t>(h) * ncells + g] =
-            cnt > 0 ? (static_cast<uint64_t>(ok) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(g)) : 0ull;
-    uint32_t m1 = cnt > 0 ? ok : 0u, m2 = cnt > 0 ? ~ok : 0u;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        m1 = max(m1, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m1), o)));
-        m2 = max(m2, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m2), o)));
-    }
-    if (lane_id() == 0) {
-        red[tid >> 6][0] = m1;
-        red[tid >> 6][1] = m2;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t x1 = 0, x2 = 0;
-#pragma unroll
-        for (int w = 0; w < kScoreThreads / 64; ++w) {
-            x1 = max(x1, red[w][0]);
-            x2 = max(x2, red[w][1]);
-        }
-        a.rpart[(static_cast<int64_t>(h) * a.nbs + blockIdx.x) * 2 + 0] = x1;
-        a.rpart[(static_cast<int64_t>(h) * a.nbs + blockIdx.x) * 2 + 1] = x2;
-    }
-}
-
-// Score range of head h from the score kernel's per-workgroup partials
-// (every thread gets it; the workgroup 0 of each head also leaves it in ext
-// for the gather kernel).
-__device__ void head_range(const Sel4& a, int h, uint32_t* red2, float& gmax, float& gmin) {
-    const int tid = threadIdx.x;
-    uint32_t m1 = 0, m2 = 0;
-    for (int i = tid; i < a.nbs; i += kScoreThreads) {
-        m1 = max(m1, a.rpart[(static_cast<int64_t>(h) * a.nbs + i) * 2 + 0]);
-        m2 = max(m2, a.rpart[(static_cast<int64_t>(h) * a.nbs + i) * 2 + 1]);
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        m1 = max(m1, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m1), o)));
-        m2 = max(m2, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m2), o)));
-    }
-    if (lane_id() == 0) {
-        red2[(tid >> 6) * 2 + 0] = m1;
-        red2[(tid >> 6) * 2 + 1] = m2;
-    }
-    __syncthreads();
-    uint32_t r1 = 0, r2 = 0;
-#pragma unroll
-    for (int w = 0; w < kScoreThreads / 64; ++w) {
-        r1 = max(r1, red2[w * 2 + 0]);
-        r2 = max(r2, red2[w * 2 + 1]);
-    }
-    gmax = key_score(static_cast<uint64_t>(r1) << 32);
-    gmin = key_score(static_cast<uint64_t>(~r2) << 32);
-    if (blockIdx.x == 0 && tid == 0) {
-        a.ext[h * 4 + 0] = r1;
-        a.ext[h * 4 + 1] = r2;
-    }
-}
-
-__global__ __launch_bounds__(kScoreThreads) void sel4_hist_kernel(Sel4 a) {
-    __shared__ uint32_t lh[kBins4];
-    const int h = blockIdx.y, tid = threadIdx.x;
-    for (int i = tid; i < kBins4; i += kScoreThreads) lh[i] = 0;
-    __syncthreads();
-    __shared__ uint32_t red2[kScoreThreads / 64 * 2];
-    const int na = n_active(a, h);
-    if (blockIdx.x == 0)   // the gather kernel's bucket cursors
-        for (int i = tid; i < kBins4; i += kScoreThreads) a.bcur[static_cast<int64_t>(h) * kBins4 + i] = 0;
-    // every key of this thread in flight before the range reduction
-    const uint64_t* keys = a.keys + static_cast<int64_t>(h) * a.cap;
-    uint64_t kv[kHistCPT];
-#pragma unroll
-    for (int u = 0; u < kHistCPT; ++u) {
-        const int c = blockIdx.x * kHistCellsPerBlock + u * kScoreThreads + tid;
-        kv[u] = c < na ? keys[c] : 0ull;
-    }
-    float gmax, gmin;
-    head_range(a, h, red2, gmax, gmin);
-    const float range = gmax - gmin;
-    const float inv = range > 0.0f ? static_cast<float>(kBins4) / range : 0.0f;
-#pragma unroll
-    for (int u = 0; u < kHistCPT; ++u) {
-        const int c = blockIdx.x * kHistCellsPerBlock + u * kScoreThreads + tid;
-        if (c < na && kv[u] != 0ull) atomicAdd(&lh[bucket4(key_score(kv[u]), gmax, inv)], 1u);   // 0: empty cell
-    }
-    __syncthreads();
-    for (int i = tid; i < kBins4; i += kScoreThreads)
-        if (lh[i]) atomicAdd(&a.hist[static_cast<int64_t>(h) * kBins4 + i], lh[i]);
-}
-
-// Bucket holding the kp-th best cell (buckets run from the best score down;
-// the last bucket when fewer cells are listed) and the first candidate slot
-// of every bucket, binbase[b] = cells in buckets < b.  T threads.
-template <int T>
-__device__ int find_bucket(const Sel4& a, int h, int kp, int* sh, int* binbase) {
-    constexpr int PER = kBins4 / T;
-    const int tid = threadIdx.x;
-    int v[PER], loc = 0;
-#pragma unroll
-    for (int u = 0; u < PER; ++u) {
-        v[u] = static_cast<int>(a.hist[static_cast<int64_t>(h) * kBins4 + tid * PER + u]);
-        loc += v[u];
-    }
-    const int incl = wave_incl_scan(loc);
-    const int w = tid >> 6;
-    if (lane_id() == 63) sh[w] = incl;
-    if (tid == 0) sh[32] = kBins4 - 1;
-    __syncthreads();
-    int run = incl - loc;
-    for (int j = 0; j < w; ++j) run += sh[j];
-#pragma unroll
-    for (int u = 0; u < PER; ++u) {
-        binbase[tid * PER + u] = run;
-        if (run < kp && run + v[u] >= kp) sh[32] = tid * PER + u;
-        run += v[u];
-    }
-    if (tid == T - 1) binbase[kBins4] = run;
-    __syncthreads();
-    return sh[32];
-}
-
-// Candidates = the cells in the buckets up to the one holding the K'-th best
-// cell, written grouped by bucket: bucket b's cells occupy slots
-// [binbase[b], binbase[b + 1]) in any order (a workgroup adds its count per
-// bucket to a cursor once).  When they do not fit kCand4 slots nothing is
-// written; the final kernel then selects exactly.
-__global__ __launch_bounds__(kScoreThreads) void sel4_gather_kernel(Sel4 a) {
-    __shared__ int sh[40];
-    __shared__ int binbase[kBins4 + 1];
-    __shared__ int lcnt[kBins4];   // this workgroup's cells per bucket, then their first slot past binbase
-    const int h = blockIdx.y, tid = threadIdx.x;
-    const int na = n_active(a, h);
-    const int kp = kprime(a, h, na);
-    if (kp <= 0) return;
-    // every key of this thread in flight before the bucket search
-    const uint64_t* keys = a.keys + static_cast<int64_t>(h) * a.cap;
-    uint64_t kv[kCPT];
-#pragma unroll
-    for (int u = 0; u < kCPT; ++u) {
-        const int c = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
-        kv[u] = c < na ? keys[c] : 0ull;
-    }
-    for (int i = tid; i < kBins4; i += kScoreThreads) lcnt[i] = 0;
-    const int bK = find_bucket<kScoreThreads>(a, h, kp, sh, binbase);
-    if (binbase[bK + 1] > kCand4) return;
-    const uint32_t okmax = a.ext[h * 4 + 0], okmin = ~a.ext[h * 4 + 1];
-    const float gmax = key_score(static_cast<uint64_t>(okmax) << 32);
-    const float gmin = key_score(static_cast<uint64_t>(okmin) << 32);
-    const float range = gmax - gmin;
-    const float inv = range > 0.0f ? static_cast<float>(kBins4) / range : 0.0f;
-    int bk[kCPT], lr[kCPT];
-#pragma unroll
-    for (int u = 0; u < kCPT; ++u) {
-        bk[u] = kBins4;
-        lr[u] = -1;
-        if (kv[u] != 0ull) {
-            const int b = bucket4(key_score(kv[u]), gmax, inv);
-            if (b <= bK) {
-                bk[u] = b;
-                lr[u] = atomicAdd(&lcnt[b], 1);
-            }
-        }
-    }
-    __syncthreads();
-    for (int b = tid; b <= bK; b += kScoreThreads)
-        if (lcnt[b] > 0) lcnt[b] = static_cast<int>(atomicAdd(&a.bcur[static_cast<int64_t>(h) * kBins4 + b],
-                                                             static_cast<uint32_t>(lcnt[b])));
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < kCPT; ++u) {
-        if (lr[u] < 0) continue;
-        const int slot = binbase[bk[u]] + lcnt[bk[u]] + lr[u];
-        if (slot >= kCand4) continue;   // only if the histogram disagreed with the keys
-        const int64_t at = static_cast<int64_t>(h) * kCand4 + slot;
-        a.cand[at] = kv[u];
-        a.cidx[at] = blockIdx.x * kCellsPerBlock + u * kScoreThreads + tid;
-    }
+    const uint64_t kv[1] = {in && cnt > 0 ? (static_cast<uint64_t>(order_key(sc)) << 32) |
+                                                (0xFFFFFFFFu - static_cast<uint32_t>(g))
+                                          : 0ull};
+    const int ci[1] = {g};
+    emit_candidates<kScoreThreads, 1>(a, h, kprime(a, h, ncells), kv, ci, lh);
 }
 
 __device__ __forceinline__ void block_scan2(int& x, int& y, int* sh, int& tx, int& ty) {
@@ -793,29 +716,123 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     const int na = n_active(a, h);
     const int kp = kprime(a, h, na);
     int32_t* prefix_out = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
-    // every candidate slot is read before the count is known (one round
-    // trip for both); slots past the count are ignored
-    uint64_t pk[kRPT];
-    int pi[kRPT];
+    // The head's candidates: the first kFinalThreads * kFinalCPT held in
+    // registers (loaded with their count and range in one round trip), the
+    // rest, if any, streamed in batches.
+    const uint64_t* candh = a.cand + static_cast<int64_t>(h) * a.cap;
+    const int32_t* cidxh = a.cidx + static_cast<int64_t>(h) * a.cap;
+    const int nraw = vec_load_i32(reinterpret_cast<const int32_t*>(a.ncand), h);
+    uint64_t ck[kFinalCPT];
+    int cc[kFinalCPT];
 #pragma unroll
-    for (int u = 0; u < kRPT; ++u) {
-        const int64_t at = static_cast<int64_t>(h) * kCand4 + tid + u * kFinalThreads;
-        pk[u] = a.cand[at];
-        pi[u] = a.cidx[at];
+    for (int u = 0; u < kFinalCPT; ++u) {
+        const int i = tid + u * kFinalThreads;
+        ck[u] = i < a.cap ? candh[i] : 0ull;   // masked once the count is known
+        cc[u] = i < a.cap ? cidxh[i] : 0;
     }
-    const int bK = find_bucket<kFinalThreads>(a, h, kp, sh, binbase);
+    uint32_t m1 = 0, m2 = 0;
+    for (int i = tid; i < a.nbs; i += kFinalThreads) {
+        m1 = max(m1, a.rpart[(static_cast<int64_t>(h) * a.nbs + i) * 2 + 0]);
+        m2 = max(m2, a.rpart[(static_cast<int64_t>(h) * a.nbs + i) * 2 + 1]);
+    }
+    const int n1 = min(max(__builtin_amdgcn_readfirstlane(nraw), 0), a.cap);
+#pragma unroll
+    for (int u = 0; u < kFinalCPT; ++u)
+        if (tid + u * kFinalThreads >= n1) ck[u] = 0ull;
+    m1 = static_cast<uint32_t>(wave_max_i(static_cast<int>(m1 ^ 0x80000000u))) ^ 0x80000000u;
+    m2 = static_cast<uint32_t>(wave_max_i(static_cast<int>(m2 ^ 0x80000000u))) ^ 0x80000000u;
+    int* hist = ord;             // [kBins4] bucket counts
+    int* cur = ord + kBins4;     // [kBins4] gather cursors
+    if (lane_id() == 0) {
+        h256[2 * (tid >> 6)] = m1;
+        h256[2 * (tid >> 6) + 1] = m2;
+    }
+    for (int i = tid; i < kBins4; i += kFinalThreads) {
+        hist[i] = 0;
+        cur[i] = 0;
+    }
+    __syncthreads();
+    uint32_t r1 = 0, r2 = 0;
+#pragma unroll
+    for (int w = 0; w < kFinalThreads / 64; ++w) {
+        r1 = max(r1, h256[2 * w]);
+        r2 = max(r2, h256[2 * w + 1]);
+    }
+    const float gmax = key_score(static_cast<uint64_t>(r1) << 32);
+    const float gmin = key_score(static_cast<uint64_t>(~r2) << 32);
+    const float range = gmax - gmin;
+    const float inv = range > 0.0f ? static_cast<float>(kBins4) / range : 0.0f;
+    constexpr int kHeld = kFinalThreads * kFinalCPT;
+    constexpr int kBatch = 8;
+    // candidates past the held ones, kBatch loads per thread in flight
+    auto stream_rest = [&](auto fn) {
+        for (int base = kHeld; base < n1; base += kFinalThreads * kBatch) {
+            uint64_t bk[kBatch];
+            int bc[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int i = base + tid + u * kFinalThreads;
+                bk[u] = i < n1 ? candh[i] : 0ull;
+                bc[u] = i < n1 ? cidxh[i] : 0;
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (bk[u] != 0ull) fn(bk[u], bc[u]);
+        }
+    };
+    // histogram of the candidates over kBins4 linear buckets of their range
+#pragma unroll
+    for (int u = 0; u < kFinalCPT; ++u)
+        if (ck[u] != 0ull) atomicAdd(&hist[bucket4(key_score(ck[u]), gmax, inv)], 1);
+    stream_rest([&](uint64_t key, int) { atomicAdd(&hist[bucket4(key_score(key), gmax, inv)], 1); });
+    __syncthreads();
+    // bucket bK holding the kp-th best candidate (the last one when fewer),
+    // and the first slot of every bucket
+    int bK = kBins4 - 1;
+    {
+        constexpr int PER = kBins4 / kFinalThreads;
+        int v[PER], loc = 0;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            v[u] = hist[tid * PER + u];
+            loc += v[u];
+        }
+        const int incl = wave_incl_scan(loc);
+        const int w = tid >> 6;
+        if (lane_id() == 63) sh[w] = incl;
+        if (tid == 0) sh[32] = kBins4 - 1;
+        __syncthreads();
+        int run = incl - loc;
+        for (int j = 0; j < w; ++j) run += sh[j];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            binbase[tid * PER + u] = run;
+            if (run < kp && run + v[u] >= kp) sh[32] = tid * PER + u;
+            run += v[u];
+        }
+        if (tid == kFinalThreads - 1) binbase[kBins4] = run;
+        __syncthreads();
+        bK = sh[32];
+    }
     const int n_c = binbase[bK + 1];
     int n = 0;   // ranked candidates; ord[r] = slot of rank r
     if (kp > 0 && n_c <= kCand4) {
         n = n_c;
-#pragma unroll
-        for (int u = 0; u < kRPT; ++u) {
-            const int i = tid + u * kFinalThreads;
-            if (i < n) {
-                sk[i] = pk[u];
-                si[i] = pi[u];
+        // the candidates at or above bK into LDS, grouped by bucket
+        auto place = [&](uint64_t key, int c) {
+            const int b = bucket4(key_score(key), gmax, inv);
+            if (b <= bK) {
+                const int slot = binbase[b] + atomicAdd(&cur[b], 1);
+                if (slot < kCand4) {   // only if the histogram disagreed with the keys
+                    sk[slot] = key;
+                    si[slot] = c;
+                }
             }
-        }
+        };
+#pragma unroll
+        for (int u = 0; u < kFinalCPT; ++u)
+            if (ck[u] != 0ull) place(ck[u], cc[u]);
+        stream_rest(place);
         int seg = 0;   // largest bucket among the candidates
         for (int b = tid; b <= bK; b += kFinalThreads) seg = max(seg, binbase[b + 1] - binbase[b]);
         seg = wave_max_i(seg);
@@ -824,22 +841,15 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
         seg = 0;
         for (int w = 0; w < kFinalThreads / 64; ++w) seg = max(seg, shk[w]);
         if (seg <= kSegMax) {
-            const uint32_t okmax = a.ext[h * 4 + 0], okmin = ~a.ext[h * 4 + 1];
-            const float gmax = key_score(static_cast<uint64_t>(okmax) << 32);
-            const float gmin = key_score(static_cast<uint64_t>(okmin) << 32);
-            const float range = gmax - gmin;
-            const float inv = range > 0.0f ? static_cast<float>(kBins4) / range : 0.0f;
-#pragma unroll
-            for (int u = 0; u < kRPT; ++u) {
-                const int i = tid + u * kFinalThreads;
-                if (i < n) {
-                    const uint64_t key = pk[u];
-                    const int b = bucket4(key_score(key), gmax, inv);
-                    const int s0 = binbase[b], s1 = binbase[b + 1];
-                    int better = 0;
-                    for (int j = s0; j < s1; ++j) better += sk[j] > key ? 1 : 0;
-                    ord[min(s0 + better, kCand4 - 1)] = i;
-                }
+            // rank of each candidate: its bucket's first slot plus the better
+            // keys of its bucket (keys are unique)
+            for (int i = tid; i < n; i += kFinalThreads) {
+                const uint64_t key = sk[i];
+                const int b = bucket4(key_score(key), gmax, inv);
+                const int s0 = binbase[b], s1 = binbase[b + 1];
+                int better = 0;
+                for (int j = s0; j < s1; ++j) better += sk[j] > key ? 1 : 0;
+                ord[min(s0 + better, kCand4 - 1)] = i;
             }
             __syncthreads();
         } else {
@@ -855,17 +865,16 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
             __syncthreads();
         }
     } else if (kp > 0) {
-        // Exact radix select of the kp-th largest key (keys are unique),
-        // then every key at or above it, sorted.
-        const uint64_t* keys = a.keys + static_cast<int64_t>(h) * a.cap;
+        // Exact radix select of the kp-th largest candidate key (keys are
+        // unique), then every key at or above it, sorted.
         uint64_t prefix = 0, mask = 0;
         int remaining = kp;
         for (int pass = 0; pass < 8; ++pass) {
             const int shift = 8 * (7 - pass);
             for (int i = tid; i < 256; i += kFinalThreads) h256[i] = 0;
             __syncthreads();
-            for (int c = tid; c < na; c += kFinalThreads) {
-                const uint64_t key = keys[c];
+            for (int c = tid; c < n1; c += kFinalThreads) {
+                const uint64_t key = candh[c];
                 if (key != 0ull && (key & mask) == prefix) atomicAdd(&h256[(key >> shift) & 255u], 1u);
             }
             __syncthreads();
@@ -889,13 +898,13 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
         }
         if (tid == 0) sh[42] = 0;
         __syncthreads();
-        for (int c = tid; c < na; c += kFinalThreads) {
-            const uint64_t key = keys[c];
+        for (int c = tid; c < n1; c += kFinalThreads) {
+            const uint64_t key = candh[c];
             if (key != 0ull && key >= prefix) {
                 const int slot = atomicAdd(&sh[42], 1);
                 if (slot < kCand4) {   // exactly kp keys (keys are unique)
                     sk[slot] = key;
-                    si[slot] = c;
+                    si[slot] = cidxh[c];
                 }
             }
         }
@@ -999,8 +1008,8 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
         a.n_rows[h] = 0;
         prefix_out[0] = 0;
     }
-    // leave the range words zero for the next call
-    if (tid < 4) a.ext[h * 4 + tid] = 0;
+    // leave the candidate counter zero for the next call
+    if (tid == 0) a.ncand[h] = 0;
     if (ONLINE && a.ring_cap > 0) {
         // Delta append (async_update.py:20-76): the ring entries whose cell
         // is one of the m_tok cells that pass nprobe and the token budget,
@@ -1046,25 +1055,19 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
 size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
     Carver cv(a->workspace);
     const size_t H = a->kv_heads;
-    // The range/counter words sit at a fixed place for every shape and every
+    // The candidate counters sit at a fixed place for every shape and every
     // call leaves them zero, so one zero-filled buffer serves calls of any
-    // shape; the histogram is cleared by the score kernel of each call.
-    uint32_t* ext = cv.take<uint32_t>(static_cast<size_t>(kExtHeads) * 4);
+    // shape.
+    uint32_t* ncand = cv.take<uint32_t>(static_cast<size_t>(kExtHeads));
     const bool dense = a->parts == 2;
     const int cap = dense ? a->k[0] * a->k[1] : a->compact_cap;
     const int nbs = dense ? (cap + kDenseScoreCells - 1) / kDenseScoreCells : (cap + kCellsPerBlock - 1) / kCellsPerBlock;
     uint32_t* rpart = cv.take<uint32_t>(H * static_cast<size_t>(nbs) * 2);
-    uint32_t* bcur = cv.take<uint32_t>(H * kBins4);
-    uint32_t* hist = cv.take<uint32_t>(H * kBins4);
-    uint64_t* keys = cv.take<uint64_t>(H * static_cast<size_t>(cap));
-    uint64_t* cand = cv.take<uint64_t>(H * kCand4);
-    int32_t* cidx = cv.take<int32_t>(H * kCand4);
+    uint64_t* cand = cv.take<uint64_t>(H * static_cast<size_t>(cap));
+    int32_t* cidx = cv.take<int32_t>(H * static_cast<size_t>(cap));
     if (p) {
-        p->keys = keys;
-        p->hist = hist;
-        p->ext = ext;
+        p->ncand = ncand;
         p->rpart = rpart;
-        p->bcur = bcur;
         p->nbs = nbs;
         p->cap = cap;
         p->dense = dense ? 1 : 0;
@@ -1110,8 +1113,8 @@ int select4_validate(const imi_select_args* a) {
 }
 
 // Bytes at the start of the workspace that a call expects zero (the
-// fixed-place range words; every call leaves them zero again).
-size_t select4_zero_bytes() { return static_cast<size_t>(kExtHeads) * 4 * sizeof(uint32_t); }
+// fixed-place candidate counters; every call leaves them zero again).
+size_t select4_zero_bytes() { return static_cast<size_t>(kExtHeads) * sizeof(uint32_t); }
 
 size_t select4_workspace_size(const imi_select_args* a) {
     imi_select_args t = *a;
@@ -1180,22 +1183,29 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
                                   kTripCap) * sizeof(float);
         bool pow2 = true;
         for (int i = 0; i < 4; ++i) pow2 = pow2 && (a->k[i] & (a->k[i] - 1)) == 0;
+        static bool score_attr = false;
+        if (!score_attr) {   // over 64 KB of LDS with k = 64 per subspace
+            const int lds_max = static_cast<int>((4 * kK4 * kCS4 + kK4 * kK4 + kTripCap) * sizeof(float));
+            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&sel4_score_kernel<true, true>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_max));
+            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&sel4_score_kernel<true, false>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_max));
+            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&sel4_score_kernel<false, true>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_max));
+            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&sel4_score_kernel<false, false>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_max));
+            score_attr = true;
+        }
         if (online && pow2)
-            hipLaunchKernelGGL((sel4_score_kernel<true, true>), grid, dim3(kScoreThreads), score_lds, stream, p);
+            hipLaunchKernelGGL((sel4_score_kernel<true, true>), grid, dim3(kScore4Threads), score_lds, stream, p);
         else if (online)
-            hipLaunchKernelGGL((sel4_score_kernel<true, false>), grid, dim3(kScoreThreads), score_lds, stream, p);
+            hipLaunchKernelGGL((sel4_score_kernel<true, false>), grid, dim3(kScore4Threads), score_lds, stream, p);
         else if (pow2)
-            hipLaunchKernelGGL((sel4_score_kernel<false, true>), grid, dim3(kScoreThreads), score_lds, stream, p);
+            hipLaunchKernelGGL((sel4_score_kernel<false, true>), grid, dim3(kScore4Threads), score_lds, stream, p);
         else
-            hipLaunchKernelGGL((sel4_score_kernel<false, false>), grid, dim3(kScoreThreads), score_lds, stream, p);
+            hipLaunchKernelGGL((sel4_score_kernel<false, false>), grid, dim3(kScore4Threads), score_lds, stream, p);
         IMI_LAUNCH_CHECK("sel4_score_kernel");
     }
-    const dim3 grid_h((p.cap + kHistCellsPerBlock - 1) / kHistCellsPerBlock, a->kv_heads);
-    hipLaunchKernelGGL(sel4_hist_kernel, grid_h, dim3(kScoreThreads), 0, stream, p);
-    IMI_LAUNCH_CHECK("sel4_hist_kernel");
-    const dim3 grid_g((p.cap + kCellsPerBlock - 1) / kCellsPerBlock, a->kv_heads);
-    hipLaunchKernelGGL(sel4_gather_kernel, grid_g, dim3(kScoreThreads), 0, stream, p);
-    IMI_LAUNCH_CHECK("sel4_gather_kernel");
     static bool attr_set[2] = {false, false};
     if (!attr_set[online]) {
         IMI_HIP_CHECK(hipFuncSetAttribute(online ? reinterpret_cast<const void*>(&sel4_final_kernel<true>)

@@ -107,10 +107,10 @@ def test_select_and_decode_argument_checks(L):
     assert "workspace" in L.imi_last_error().decode()
     s.parts = 2   # 2-way within the one-kernel bounds (k <= 128, K' <= 2048): no workspace
     assert L.imi_select_workspace_size(ctypes.byref(s), ctypes.byref(need)) == 0 and need.value == 0
-    s.k[0], s.nprobe, s.buffer_pages = 200, 3000, 3000   # beyond them: the ranking pipeline's keys and candidates
+    s.k[0], s.nprobe, s.buffer_pages = 200, 3000, 3000   # beyond them: the ranking pipeline's candidate list
     s.sel_cap = 3000
     assert L.imi_select_workspace_size(ctypes.byref(s), ctypes.byref(need)) == 0
-    assert need.value >= 8 * (200 * 64 * 8 + 8192 * 12)   # a 64-bit key per cell, 8192 candidates per head
+    assert need.value >= 8 * 200 * 64 * 12   # room for every cell as a candidate: 64-bit key + cell index
     s.k[0], s.nprobe, s.buffer_pages, s.sel_cap = 64, 410, 410, 410
     s.sel_cap = 100
     assert L.imi_select(ctypes.byref(s), None) == 1
