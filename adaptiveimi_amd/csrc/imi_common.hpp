@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <type_traits>
 
 #include "imi_hip.h"
 
@@ -222,6 +223,24 @@ __device__ __forceinline__ int wave_max_i(int v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o));
     return v;
+}
+
+// Unsigned max over the 64 lanes on DPP row operations (no LDS round trips):
+// row shifts and row broadcasts give lane 63 the maximum, which every lane
+// then reads.  Lanes without a source contribute 0, the identity.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    auto sh = [](uint32_t x, auto ctrl_c, auto mask_c) {
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), decltype(ctrl_c)::value,
+                                                                 decltype(mask_c)::value, 0xF, false));
+    };
+    using F = std::integral_constant<int, 0xF>;
+    v = max(v, sh(v, std::integral_constant<int, 0x111>{}, F{}));
+    v = max(v, sh(v, std::integral_constant<int, 0x112>{}, F{}));
+    v = max(v, sh(v, std::integral_constant<int, 0x114>{}, F{}));
+    v = max(v, sh(v, std::integral_constant<int, 0x118>{}, F{}));
+    v = max(v, sh(v, std::integral_constant<int, 0x142>{}, std::integral_constant<int, 0xA>{}));
+    v = max(v, sh(v, std::integral_constant<int, 0x143>{}, std::integral_constant<int, 0xC>{}));
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
 }
 
 // p[i] through a vector load.  A load at a wave-uniform address becomes a

@@ -50,7 +50,7 @@ constexpr int kScoreThreads = 256;   // 2-way score kernel
 constexpr int kScore4Threads = 1024; // 4-way score kernel
 constexpr int kFinalThreads = 1024;
 constexpr int kSelCap4 = kCand4;  // cells to rank (K') per head
-constexpr int kExtHeads = 1024;  // KV heads one call handles (fixed-place counters)
+constexpr int kExtHeads = 1024;  // KV heads one call handles
 constexpr int kCPT = 16;         // occupied cells per thread in the 4-way score kernel
 constexpr int kCS4 = 36;         // LDS row stride of a subspace centroid (16-byte aligned rows)
 constexpr int kTripCap = 4096;   // (l0, l1, l2) prefixes a score workgroup keeps
@@ -59,6 +59,15 @@ constexpr int kDenseScoreCells = kScoreThreads;   // 2-way score kernel: one glo
 constexpr int kDenseK = 256;                      // 2-way centroids per subspace the score kernel reads
 constexpr int kLocBins = 1024;   // buckets of a score workgroup's own candidate cut
 constexpr int kFinalCPT = 16;    // candidates per thread the final kernel holds in registers
+constexpr int kMaxSeg = 1024;    // score workgroups per head the final kernel reads (candidate segments)
+
+// Position of candidate j of score workgroup s (= h * nbs + b) in the list.
+// A workgroup's candidates start at a staggered offset of its region
+// (region is a power of two), so that the workgroups' first candidates do
+// not all fall on the same memory channels.
+__host__ __device__ __forceinline__ int64_t cand_pos(int64_t s, int j, int region) {
+    return s * region + ((static_cast<int64_t>(s) * 520 + j) & (region - 1));
+}
 
 struct Sel4 {
     const uint16_t* q;
@@ -82,9 +91,10 @@ struct Sel4 {
     int32_t* n_sel;
     int32_t* n_rows;
     int sel_cap;
-    uint32_t* ncand;         // [kExtHeads] candidates listed per head (zero between calls)
-    uint64_t* cand;          // [H][cap] candidate keys (any order)
-    int32_t* cidx;           // [H][cap] their cell indices
+    int32_t* wcnt;           // [H][nbs] candidates of each score workgroup
+    int region;              // cells per score workgroup: workgroup b lists its candidates from b * region on
+    uint64_t* cand;          // [H][nbs * region] candidate keys (any order inside a workgroup's region)
+    int32_t* cidx;           // [H][nbs * region] their cell indices
     uint32_t* rpart;         // [H][nbs][2]: per score workgroup, max order key and max ~order key of its candidates
     int nbs;                 // score workgroups per head
     // online index maintenance: replaced centroids (by compact id) and the
@@ -155,30 +165,34 @@ __device__ __forceinline__ uint32_t kmod(uint32_t g, uint32_t k) {
 // the score rises, so these cells include every cell at or above that one,
 // ties included: a superset of the workgroup's share of the head's K'
 // best).  They go to the head's list at one atomic offset per workgroup, in
-// any order; the workgroup's candidate range goes to rpart.  lh: kLocBins
-// ints of LDS, zero on entry.
+// any order, in this workgroup's own region of the list (no atomics: a
+// contended device-scope atomic per workgroup cost several microseconds),
+// with their count in wcnt; the workgroup's candidate range goes to rpart.
+// lh: kLocBins ints of LDS, zero on entry.
 template <int T, int CPT>
 __device__ void emit_candidates(const Sel4& a, int h, int kp, const uint64_t (&kv)[CPT], const int (&ci)[CPT],
                                 int* lh) {
+    // Branch-free per-cell code throughout: the unrolled per-cell branches
+    // of a first version made this routine several times slower (each
+    // workgroup runs it once, so its code is fetched cold).
     constexpr int NW = T / 64;
     __shared__ uint32_t red[NW][3];
     __shared__ int s_bk;
-    __shared__ int s_base;
     const int tid = threadIdx.x, w = tid >> 6;
     // valid cells and their range (order keys)
     int nv = 0;
     uint32_t kmax = 0, nkmin = 0;
 #pragma unroll
-    for (int u = 0; u < CPT; ++u)
-        if (kv[u] != 0ull) {
-            const uint32_t ok = static_cast<uint32_t>(kv[u] >> 32);
-            ++nv;
-            kmax = max(kmax, ok);
-            nkmin = max(nkmin, ~ok);
-        }
+    for (int u = 0; u < CPT; ++u) {
+        const bool valid = kv[u] != 0ull;
+        const uint32_t ok = static_cast<uint32_t>(kv[u] >> 32);
+        nv += valid ? 1 : 0;
+        kmax = max(kmax, valid ? ok : 0u);
+        nkmin = max(nkmin, valid ? ~ok : 0u);
+    }
     nv = wave_sum_i(nv);
-    kmax = static_cast<uint32_t>(wave_max_i(static_cast<int>(kmax ^ 0x80000000u))) ^ 0x80000000u;
-    nkmin = static_cast<uint32_t>(wave_max_i(static_cast<int>(nkmin ^ 0x80000000u))) ^ 0x80000000u;
+    kmax = wave_max_u32(kmax);
+    nkmin = wave_max_u32(nkmin);
     if (lane_id() == 0) {
         red[w][0] = static_cast<uint32_t>(nv);
         red[w][1] = kmax;
@@ -198,14 +212,17 @@ __device__ void emit_candidates(const Sel4& a, int h, int kp, const uint64_t (&k
     const float wmin = key_score(static_cast<uint64_t>(~bnmin) << 32);
     const float range = wmax - wmin;
     const float inv = range > 0.0f ? static_cast<float>(kLocBins) / range : 0.0f;
-    auto bucket = [&](uint64_t key) {
-        const float t = (wmax - key_score(key)) * inv;
-        return t < static_cast<float>(kLocBins - 1) ? static_cast<int>(t) : kLocBins - 1;
-    };
+    int bu[CPT];   // bucket of each cell, kLocBins for no cell
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+        const float t = (wmax - key_score(kv[u])) * inv;
+        const int b = t < static_cast<float>(kLocBins - 1) ? static_cast<int>(t) : kLocBins - 1;
+        bu[u] = kv[u] != 0ull ? b : kLocBins;
+    }
     if (nvb > kp && kp > 0) {   // workgroup-uniform
 #pragma unroll
         for (int u = 0; u < CPT; ++u)
-            if (kv[u] != 0ull) atomicAdd(&lh[bucket(kv[u])], 1);
+            if (bu[u] < kLocBins) atomicAdd(&lh[bu[u]], 1);   // (one shared slot for every empty cell serialised)
         __syncthreads();
         // the bucket holding the kp-th best: kLocBins / T buckets per thread
         constexpr int PB = kLocBins / T;
@@ -228,21 +245,20 @@ __device__ void emit_candidates(const Sel4& a, int h, int kp, const uint64_t (&k
         }
         __syncthreads();
     }
-    const int bk = s_bk;
+    const int bk = s_bk < kLocBins ? s_bk : kLocBins - 1;   // bucket of the cut; -1: none
     // this workgroup's candidates, their offsets and range
     int cnt = 0;
     uint32_t cnmin = 0;
-    bool cf[CPT];
+    uint32_t cmask = 0;   // bit u: cell u is a candidate
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
-        cf[u] = kv[u] != 0ull && bk >= 0 && (bk >= kLocBins || bucket(kv[u]) <= bk);
-        if (cf[u]) {
-            ++cnt;
-            cnmin = max(cnmin, ~static_cast<uint32_t>(kv[u] >> 32));
-        }
+        const bool c = bu[u] <= bk;   // false for no cell (kLocBins) and for bk = -1
+        cmask |= c ? 1u << u : 0u;
+        cnt += c ? 1 : 0;
+        cnmin = max(cnmin, c ? ~static_cast<uint32_t>(kv[u] >> 32) : 0u);
     }
     const int cincl = wave_incl_scan(cnt);
-    cnmin = static_cast<uint32_t>(wave_max_i(static_cast<int>(cnmin ^ 0x80000000u))) ^ 0x80000000u;
+    cnmin = wave_max_u32(cnmin);
     __syncthreads();   // red is reused
     if (lane_id() == 63) red[w][0] = static_cast<uint32_t>(cincl);
     if (lane_id() == 0) red[w][2] = cnmin;
@@ -256,20 +272,18 @@ __device__ void emit_candidates(const Sel4& a, int h, int kp, const uint64_t (&k
         cmn = max(cmn, red[j][2]);
     }
     if (tid == 0) {
-        s_base = tot > 0 ? static_cast<int>(atomicAdd(&a.ncand[h], static_cast<uint32_t>(tot))) : 0;
+        a.wcnt[static_cast<int64_t>(h) * a.nbs + blockIdx.x] = tot;
         a.rpart[(static_cast<int64_t>(h) * a.nbs + blockIdx.x) * 2 + 0] = tot > 0 ? bmax : 0u;
         a.rpart[(static_cast<int64_t>(h) * a.nbs + blockIdx.x) * 2 + 1] = tot > 0 ? cmn : 0u;
     }
-    __syncthreads();
-    int pos = s_base + before;
+    // tot <= T * CPT = region; a thread's candidates in cell order
+    const int64_t sg = static_cast<int64_t>(h) * a.nbs + blockIdx.x;
 #pragma unroll
     for (int u = 0; u < CPT; ++u)
-        if (cf[u]) {
-            if (pos < a.cap) {   // a head lists at most cap cells
-                a.cand[static_cast<int64_t>(h) * a.cap + pos] = kv[u];
-                a.cidx[static_cast<int64_t>(h) * a.cap + pos] = ci[u];
-            }
-            ++pos;
+        if (cmask & (1u << u)) {
+            const int64_t pos = cand_pos(sg, before + __builtin_popcount(cmask & ((1u << u) - 1u)), a.region);
+            a.cand[pos] = kv[u];
+            a.cidx[pos] = ci[u];
         }
 }
 
@@ -716,31 +730,60 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     const int na = n_active(a, h);
     const int kp = kprime(a, h, na);
     int32_t* prefix_out = a.sel_prefix + static_cast<int64_t>(h) * (a.sel_cap + 1);
-    // The head's candidates: the first kFinalThreads * kFinalCPT held in
-    // registers (loaded with their count and range in one round trip), the
-    // rest, if any, streamed in batches.
-    const uint64_t* candh = a.cand + static_cast<int64_t>(h) * a.cap;
-    const int32_t* cidxh = a.cidx + static_cast<int64_t>(h) * a.cap;
-    const int nraw = vec_load_i32(reinterpret_cast<const int32_t*>(a.ncand), h);
+    // The head's candidates: score workgroup b listed wcnt[b] of them from
+    // b * region on.  The counts and the range partials come in one round
+    // trip; flat candidate i lies in the last segment whose start is <= i
+    // (a binary search over the starts in LDS).  The first kFinalThreads *
+    // kFinalCPT candidates are held in registers, the rest streamed in
+    // batches.
+    __shared__ int seg0[kMaxSeg + 1];
+    const int64_t hb = static_cast<int64_t>(h) * a.nbs;
+    const int cw = tid < a.nbs ? min(max(a.wcnt[hb + tid], 0), a.region) : 0;
+    uint32_t m1 = 0, m2 = 0;
+    if (tid < a.nbs) {
+        m1 = a.rpart[(hb + tid) * 2 + 0];
+        m2 = a.rpart[(hb + tid) * 2 + 1];
+    }
+    {
+        const int incl = wave_incl_scan(cw);
+        if (lane_id() == 63) sh[tid >> 6] = incl;
+        __syncthreads();
+        int before = incl - cw, tot = 0;
+        for (int j = 0; j < kFinalThreads / 64; ++j) {
+            before += j < (tid >> 6) ? sh[j] : 0;
+            tot += sh[j];
+        }
+        seg0[tid] = before;
+        if (tid == 0) seg0[kMaxSeg] = tot;
+        __syncthreads();
+    }
+    const int n1 = seg0[kMaxSeg];
+    auto cand_at = [&](int i) {   // list position of candidate i < n1
+        int lo = 0;
+#pragma unroll
+        for (int step = kMaxSeg / 2; step > 0; step >>= 1) {
+            const int mid = lo + step;
+            if (mid < a.nbs && seg0[mid] <= i) lo = mid;
+        }
+        return cand_pos(hb + lo, i - seg0[lo], a.region);
+    };
+    const uint64_t* candl = a.cand;
+    const int32_t* cidxl = a.cidx;
     uint64_t ck[kFinalCPT];
     int cc[kFinalCPT];
 #pragma unroll
     for (int u = 0; u < kFinalCPT; ++u) {
         const int i = tid + u * kFinalThreads;
-        ck[u] = i < a.cap ? candh[i] : 0ull;   // masked once the count is known
-        cc[u] = i < a.cap ? cidxh[i] : 0;
+        ck[u] = 0ull;
+        cc[u] = 0;
+        if (i < n1) {
+            const int64_t at = cand_at(i);
+            ck[u] = candl[at];
+            cc[u] = cidxl[at];
+        }
     }
-    uint32_t m1 = 0, m2 = 0;
-    for (int i = tid; i < a.nbs; i += kFinalThreads) {
-        m1 = max(m1, a.rpart[(static_cast<int64_t>(h) * a.nbs + i) * 2 + 0]);
-        m2 = max(m2, a.rpart[(static_cast<int64_t>(h) * a.nbs + i) * 2 + 1]);
-    }
-    const int n1 = min(max(__builtin_amdgcn_readfirstlane(nraw), 0), a.cap);
-#pragma unroll
-    for (int u = 0; u < kFinalCPT; ++u)
-        if (tid + u * kFinalThreads >= n1) ck[u] = 0ull;
-    m1 = static_cast<uint32_t>(wave_max_i(static_cast<int>(m1 ^ 0x80000000u))) ^ 0x80000000u;
-    m2 = static_cast<uint32_t>(wave_max_i(static_cast<int>(m2 ^ 0x80000000u))) ^ 0x80000000u;
+    m1 = wave_max_u32(m1);
+    m2 = wave_max_u32(m2);
     int* hist = ord;             // [kBins4] bucket counts
     int* cur = ord + kBins4;     // [kBins4] gather cursors
     if (lane_id() == 0) {
@@ -772,8 +815,13 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
                 const int i = base + tid + u * kFinalThreads;
-                bk[u] = i < n1 ? candh[i] : 0ull;
-                bc[u] = i < n1 ? cidxh[i] : 0;
+                bk[u] = 0ull;
+                bc[u] = 0;
+                if (i < n1) {
+                    const int64_t at = cand_at(i);
+                    bk[u] = candl[at];
+                    bc[u] = cidxl[at];
+                }
             }
 #pragma unroll
             for (int u = 0; u < kBatch; ++u)
@@ -874,7 +922,7 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
             for (int i = tid; i < 256; i += kFinalThreads) h256[i] = 0;
             __syncthreads();
             for (int c = tid; c < n1; c += kFinalThreads) {
-                const uint64_t key = candh[c];
+                const uint64_t key = candl[cand_at(c)];
                 if (key != 0ull && (key & mask) == prefix) atomicAdd(&h256[(key >> shift) & 255u], 1u);
             }
             __syncthreads();
@@ -899,12 +947,13 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
         if (tid == 0) sh[42] = 0;
         __syncthreads();
         for (int c = tid; c < n1; c += kFinalThreads) {
-            const uint64_t key = candh[c];
+            const int64_t at = cand_at(c);
+            const uint64_t key = candl[at];
             if (key != 0ull && key >= prefix) {
                 const int slot = atomicAdd(&sh[42], 1);
                 if (slot < kCand4) {   // exactly kp keys (keys are unique)
                     sk[slot] = key;
-                    si[slot] = cidxh[c];
+                    si[slot] = cidxl[at];
                 }
             }
         }
@@ -1008,8 +1057,6 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
         a.n_rows[h] = 0;
         prefix_out[0] = 0;
     }
-    // leave the candidate counter zero for the next call
-    if (tid == 0) a.ncand[h] = 0;
     if (ONLINE && a.ring_cap > 0) {
         // Delta append (async_update.py:20-76): the ring entries whose cell
         // is one of the m_tok cells that pass nprobe and the token budget,
@@ -1055,18 +1102,19 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
 size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
     Carver cv(a->workspace);
     const size_t H = a->kv_heads;
-    // The candidate counters sit at a fixed place for every shape and every
-    // call leaves them zero, so one zero-filled buffer serves calls of any
-    // shape.
-    uint32_t* ncand = cv.take<uint32_t>(static_cast<size_t>(kExtHeads));
     const bool dense = a->parts == 2;
     const int cap = dense ? a->k[0] * a->k[1] : a->compact_cap;
-    const int nbs = dense ? (cap + kDenseScoreCells - 1) / kDenseScoreCells : (cap + kCellsPerBlock - 1) / kCellsPerBlock;
+    const int region = dense ? kDenseScoreCells : kCellsPerBlock;
+    const int nbs = (cap + region - 1) / region;
+    // every score workgroup writes its count and range each call, and the
+    // final kernel reads only those: nothing has to start at zero
+    int32_t* wcnt = cv.take<int32_t>(H * static_cast<size_t>(nbs));
     uint32_t* rpart = cv.take<uint32_t>(H * static_cast<size_t>(nbs) * 2);
-    uint64_t* cand = cv.take<uint64_t>(H * static_cast<size_t>(cap));
-    int32_t* cidx = cv.take<int32_t>(H * static_cast<size_t>(cap));
+    uint64_t* cand = cv.take<uint64_t>(H * static_cast<size_t>(nbs) * region);
+    int32_t* cidx = cv.take<int32_t>(H * static_cast<size_t>(nbs) * region);
     if (p) {
-        p->ncand = ncand;
+        p->wcnt = wcnt;
+        p->region = region;
         p->rpart = rpart;
         p->nbs = nbs;
         p->cap = cap;
@@ -1102,6 +1150,10 @@ int select4_validate(const imi_select_args* a) {
                     IMI_ERR_INVALID, "imi_select: 4-way selection needs the compact cell arrays");
         cells_max = a->compact_cap;
     }
+    IMI_REQUIRE((cells_max + (dense ? kDenseScoreCells : kCellsPerBlock) - 1) / (dense ? kDenseScoreCells : kCellsPerBlock) <=
+                    kMaxSeg,
+                IMI_ERR_UNSUPPORTED, "imi_select: %lld cells per head exceed the ranking pipeline's %d score workgroups",
+                static_cast<long long>(cells_max), kMaxSeg);
     const bool rank_all = a->tile_mode || a->ring_cap > 0;
     const int kprime_max = rank_all ? a->nprobe : (a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages);
     const int64_t kp_eff = kprime_max < cells_max ? kprime_max : cells_max;
@@ -1112,9 +1164,9 @@ int select4_validate(const imi_select_args* a) {
     return IMI_OK;
 }
 
-// Bytes at the start of the workspace that a call expects zero (the
-// fixed-place candidate counters; every call leaves them zero again).
-size_t select4_zero_bytes() { return static_cast<size_t>(kExtHeads) * sizeof(uint32_t); }
+// Bytes at the start of the workspace that a call expects zero: none (each
+// call's score kernel writes every count and range its final kernel reads).
+size_t select4_zero_bytes() { return 0; }
 
 size_t select4_workspace_size(const imi_select_args* a) {
     imi_select_args t = *a;
