@@ -222,18 +222,19 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     // for the kept cells only (holding them would spill registers)
     constexpr bool LATE_OFF = EPT >= 8;
     int sz[EPT], co_[LATE_OFF ? 1 : EPT];
-    // g = i * k1 + jcell = tid + R k1 e: an add of a uniform stride (the
-    // multiply-add form compiled to a 64-bit mad whose unused high operand
-    // was a register still being loaded, which forced a wait for the first
-    // loads before the others were issued)
-    const uint32_t gstride = static_cast<uint32_t>(R * k1);
+    // cell g = i * k1 + jcell = tid + R k1 e: a wave-uniform row base plus
+    // the thread id, so each load takes the base in SGPRs and tid as a 32-bit
+    // offset.  (Index arithmetic in VGPRs compiled to 64-bit multiply-adds
+    // whose unused high operand could be a register still being loaded,
+    // which put a wait for the earlier loads before every later one.)
+    const int64_t gstride = static_cast<int64_t>(R) * k1;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
         const int i = rcell + R * e;
         const bool in = rcell < R && i < k0;
-        const uint32_t g = static_cast<uint32_t>(tid) + gstride * static_cast<uint32_t>(e);
-        sz[e] = in ? cntp[g] : 0;
-        if (!LATE_OFF) co_[e] = in ? offs[g] : 0;
+        const int32_t* crow = cntp + gstride * e;
+        sz[e] = in ? crow[static_cast<uint32_t>(tid)] : 0;
+        if (!LATE_OFF) co_[e] = in ? (offs + gstride * e)[static_cast<uint32_t>(tid)] : 0;
     }
     // this head's budgets (ragged batches), read with the other loads
     const int hmt_raw = a.head_max_tokens ? vec_load_i32(a.head_max_tokens, h) : INT_MAX;
@@ -243,7 +244,9 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     // of each of the first kOvr slots (thread t stages float4 t & 31 of slot
     // t >> 5), and this thread's delta ring entry (thread = ring index).
     const bool upd = ONLINE && a.upd_slot != nullptr;
-    const int n_upd = upd ? __builtin_amdgcn_readfirstlane(vec_load_i32(a.upd_n, h)) : 0;
+    // the counts stay in VGPRs until first use: a readfirstlane here would
+    // wait for every load issued so far
+    const int n_upd_v = upd ? vec_load_i32(a.upd_n, h) : 0;
     int us[EPT];
     int urow[2] = {0, 0};
 #pragma unroll
@@ -255,13 +258,14 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     if (upd) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int slot = (tid + u * kSelThreads) >> 5;
-            urow[u] = slot < a.shadow_rows ? a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + slot] : 0;
+            const int slot = (tid + u * kSelThreads) >> 5;   // shadow_rows >= 1 here
+            const int v = a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + min(slot, a.shadow_rows - 1)];
+            urow[u] = slot < a.shadow_rows ? v : 0;
         }
     }
     const bool ring = ONLINE && a.ring_cap > 0;
     int rcode = -3, rrow = 0;
-    const int rn = ring ? min(__builtin_amdgcn_readfirstlane(vec_load_i32(a.ring_n, h)), a.ring_cap) : 0;
+    const int rn_v = ring ? vec_load_i32(a.ring_n, h) : 0;
     if (ring && tid < a.ring_cap) {
         rcode = a.ring_cell[static_cast<int64_t>(h) * a.ring_cap + tid];
         rrow = a.ring_row[static_cast<int64_t>(h) * a.ring_cap + tid];
@@ -280,11 +284,14 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
         c0v[u] = i4 * 4 < k0 * DP ? reinterpret_cast<const float4*>(c0)[i4] : make_float4(0, 0, 0, 0);
         c1v[u] = i4 * 4 < k1 * DP ? reinterpret_cast<const float4*>(c1)[i4] : make_float4(0, 0, 0, 0);
     }
+    // the G query rows of this head: rows past G re-read row G - 1 (G >= 1)
+    // and are dropped from the sum, so the loads are unconditional and all
+    // in flight at once
     uint16_t qv[kMaxGroups];
     if (tid < D) {
+        const uint16_t* qh = a.q + static_cast<int64_t>(h) * a.G * D;
 #pragma unroll
-        for (int g = 0; g < kMaxGroups; ++g)
-            qv[g] = g < a.G ? a.q[(static_cast<int64_t>(h) * a.G + g) * D + tid] : 0;
+        for (int g = 0; g < kMaxGroups; ++g) qv[g] = qh[min(g, a.G - 1) * D + tid];
     }
 #pragma unroll
     for (int u = 0; u < kV4; ++u) {
@@ -369,6 +376,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     // slots per pass, staged in LDS after the C0 rows
     float* ovr = c0s + k0 * (DP + 1);   // [kOvr][129] replaced centroids staged in LDS
     float* ovs = ovr + kOvr * 129;      // [kOvr] their scores
+    const int n_upd = __builtin_amdgcn_readfirstlane(n_upd_v);
+    const int rn = min(__builtin_amdgcn_readfirstlane(rn_v), a.ring_cap);
     if (ONLINE && n_upd > kOvr) {
         // more than kOvr replaced cells: passes of kOvr slots before the range
         for (int base = 0; base < n_upd; base += kOvr) {
