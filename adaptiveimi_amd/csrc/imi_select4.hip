@@ -337,9 +337,12 @@ __global__ __launch_bounds__(kScore4Threads) void sel4_score_kernel(Sel4 a) {
         }
     }
     if (tid < 128) {
+        // rows past G re-read row G - 1 (G >= 1) and are dropped from the
+        // sum: unconditional loads, all in flight at once
+        const uint16_t* qh = a.q + static_cast<int64_t>(h) * a.G * 128;
         uint16_t qv[kMaxG4];
 #pragma unroll
-        for (int g = 0; g < kMaxG4; ++g) qv[g] = g < a.G ? a.q[(static_cast<int64_t>(h) * a.G + g) * 128 + tid] : 0;
+        for (int g = 0; g < kMaxG4; ++g) qv[g] = qh[min(g, a.G - 1) * 128 + tid];
         float acc = 0.0f;   // grouped-query sum, g ascending (compute_impl.cu:80-87)
 #pragma unroll
         for (int g = 0; g < kMaxG4; ++g)
@@ -462,6 +465,27 @@ __global__ __launch_bounds__(kScore4Threads) void sel4_score_kernel(Sel4 a) {
             sv[u] = __builtin_fmaf(q4.w, c4.w, sv[u]);
         }
     }
+    // replaced centroids (async_update.py:7-19): the override slots of the
+    // thread's cells, then the shadow rows of the replaced ones, each set of
+    // loads issued together (one round trip each; the second only when the
+    // wave has a replaced cell)
+    int srow[ONLINE ? kCPT : 1];
+    uint32_t rmask = 0;
+    if (ONLINE && a.upd_slot) {
+#pragma unroll
+        for (int u = 0; u < kCPT; ++u) {
+            const int c = blockIdx.x * kCellsPerBlock + u * kScore4Threads + tid;
+            srow[u] = a.upd_slot[static_cast<int64_t>(h) * a.cap + min(c, a.cap - 1)];
+            if (c < na && srow[u] >= 0) rmask |= 1u << u;
+        }
+        if (__builtin_amdgcn_ballot_w64(rmask != 0) != 0ull) {
+#pragma unroll
+            for (int u = 0; u < kCPT; ++u) {
+                const int us = min(max(srow[u], 0), a.shadow_rows - 1);
+                srow[u] = min(max(a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + us], 0), a.shadow_rows - 1);
+            }
+        }
+    }
     uint64_t kv[kCPT];
     int ci[kCPT];
 #pragma unroll
@@ -471,15 +495,10 @@ __global__ __launch_bounds__(kScore4Threads) void sel4_score_kernel(Sel4 a) {
         kv[u] = 0ull;
         if (c >= na) continue;
         float s = sv[u];
-        if (ONLINE && a.upd_slot) {
-            const int us = a.upd_slot[static_cast<int64_t>(h) * a.cap + c];
-            if (us >= 0) {
-                // replaced centroid (async_update.py:7-19): the chain over its shadow row
-                const int row = min(
-                    max(a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + min(us, a.shadow_rows - 1)], 0),
-                    a.shadow_rows - 1);
-                const float4* sr =
-                    reinterpret_cast<const float4*>(a.shadow + (static_cast<int64_t>(h) * a.shadow_rows + row) * 128);
+        if (ONLINE) {
+            if (rmask & (1u << u)) {
+                const float4* sr = reinterpret_cast<const float4*>(
+                    a.shadow + (static_cast<int64_t>(h) * a.shadow_rows + srow[u]) * 128);
                 s = 0.0f;
                 for (int d4 = 0; d4 < 32; ++d4) {
                     const float4 v = sr[d4];
@@ -521,8 +540,10 @@ __global__ __launch_bounds__(kScoreThreads) void sel2_dense_score_kernel(Sel4 a)
     // ---- loads, all issued before the first wait ----
     uint16_t qv[kMaxG4];
     if (tid < 128) {
+        // rows past G re-read row G - 1 and are dropped from the sum
+        const uint16_t* qh = a.q + static_cast<int64_t>(h) * a.G * 128;
 #pragma unroll
-        for (int j = 0; j < kMaxG4; ++j) qv[j] = j < a.G ? a.q[(static_cast<int64_t>(h) * a.G + j) * 128 + tid] : 0;
+        for (int j = 0; j < kMaxG4; ++j) qv[j] = qh[min(j, a.G - 1) * 128 + tid];
     }
     const int l0 = in ? g / k1 : 0, l1 = in ? g - (g / k1) * k1 : 0;
     const float4* c0 = reinterpret_cast<const float4*>(a.cent + (static_cast<int64_t>(h) * 2 + 0) * a.kmax * 64);
