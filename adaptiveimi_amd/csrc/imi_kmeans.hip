@@ -176,6 +176,9 @@ __global__ __launch_bounds__(256) void km_assign_kernel(KmParams a) {
 typedef __attribute__((ext_vector_type(8))) __bf16 km_bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float km_f32x4_t;
 typedef __attribute__((ext_vector_type(4))) unsigned int km_u32x4_t;
+typedef __attribute__((ext_vector_type(2))) unsigned int km_u32x2_t;
+typedef __attribute__((ext_vector_type(4))) short km_s16x4_t;
+typedef __attribute__((address_space(3))) km_s16x4_t km_lds_s16x4_t;
 
 constexpr int kScreenMaxK = 128;
 
@@ -718,16 +721,29 @@ __global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, int it
                 if (b < nb) {
                     const uint16_t* rows = reinterpret_cast<const uint16_t*>(ring[(q & 1) * NL + lw]);
                     const int cnt = (n - 64 * b) < 64 ? (n - 64 * b) : 64;
-                    if (lane < DP) {
-                        if (cnt == 64) {
-                            float v[64];
+                    if (cnt == 64) {
+                        // transposing reads: 16-lane group g takes the 4 x 16
+                        // block of members 4i..4i+3, dims 16 (g % (DP/16)) ..
+                        // +15, so lane d holds dim d of four consecutive
+                        // members per read (lanes >= DP read a copy and are
+                        // not stored); all 16 reads in flight at once
+                        const int lg = lane >> 4, ln = lane & 15;
+                        const uint16_t* base = rows + (ln >> 2) * DP + 16 * (lg % (DP / 16)) + 4 * (ln & 3);
+                        km_u32x2_t w[16];
 #pragma unroll
-                            for (int r = 0; r < 64; ++r) v[r] = bf16_to_f32(rows[r * DP + lane]);
+                        for (int i = 0; i < 16; ++i)
+                            w[i] = __builtin_bit_cast(
+                                km_u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                (km_lds_s16x4_t*)(base + 4 * i * DP)));
 #pragma unroll
-                            for (int r = 0; r < 64; ++r) acc = acc + v[r];
-                        } else {
-                            for (int r = 0; r < cnt; ++r) acc = acc + bf16_to_f32(rows[r * DP + lane]);
+                        for (int i = 0; i < 16; ++i) {
+                            acc = acc + __uint_as_float(w[i][0] << 16);
+                            acc = acc + __uint_as_float(w[i][0] & 0xFFFF0000u);
+                            acc = acc + __uint_as_float(w[i][1] << 16);
+                            acc = acc + __uint_as_float(w[i][1] & 0xFFFF0000u);
                         }
+                    } else if (lane < DP) {
+                        for (int r = 0; r < cnt; ++r) acc = acc + bf16_to_f32(rows[r * DP + lane]);
                     }
                 }
             }
