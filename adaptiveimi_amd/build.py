@@ -33,6 +33,13 @@ HIPCC_FLAGS = [
     "-Wall", "-Wno-unused-function",
 ]
 
+# Per-source additions.  k-means: matrix-core results go straight to VGPRs
+# (its E-step reads every accumulator with VALU code; the AGPR form costs one
+# copy per value).
+EXTRA_FLAGS = {
+    "imi_kmeans.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
 
 def _torch_lib_dir() -> Path:
     import torch  # noqa: F401  (only to locate the bundled HIP runtime)
@@ -62,7 +69,8 @@ def build(verbose: bool = False, jobs: int = 4, force: bool = False) -> Path:
         obj = BUILD_DIR / (src.stem + ".o")
         if not force and obj.exists() and obj.stat().st_mtime > max(src.stat().st_mtime, newest_header):
             return obj
-        cmd = [hipcc, *HIPCC_FLAGS, "-I", str(PKG.parent / "include"), "-c", str(src), "-o", str(obj)]
+        cmd = [hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-I", str(PKG.parent / "include"), "-c",
+               str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         r = subprocess.run(cmd, capture_output=True, text=True)

@@ -201,15 +201,18 @@ size_t screen_lds_bytes(int kmax) {
            4 * static_cast<size_t>(kmax) * 4 + 64;
 }
 
-template <int DP, int MAXK>
-__global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int chunks) {
+// KT > 0: every segment has k = 16 KT centroids (whole tiles, no per-tile
+// tests); KT = 0: any k <= MAXK.
+template <int DP, int MAXK, int KT>
+__global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, int chunks) {
     constexpr int KH = DP / 32;   // 32-dim K steps per subvector
+    constexpr int NCT = KT > 0 ? KT : MAXK / 16;   // centroid tiles held per lane
     extern __shared__ float smem[];
     const int seg = blockIdx.y;
     if (a.done && a.done[seg]) return;
     const int h = seg / a.P, p = seg % a.P;
-    const int k = a.k[p];
-    const int nct = (k + 15) >> 4;
+    const int k = KT > 0 ? 16 * KT : a.k[p];
+    const int nct = KT > 0 ? KT : (k + 15) >> 4;
     const int nct_max = (a.kmax + 15) >> 4;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     constexpr int CS = DP + 4;
@@ -260,8 +263,9 @@ __global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int c
         apk[e] = km_u32x4_t{w[0], w[1], w[2], w[3]};
     }
     for (int c = tid; c < nct * 16; c += 256) {
-        float sq = 0.0f;
+        float sq = INFINITY;   // padding rows of A are zero: their e(c) is +inf
         if (c < k) {
+            sq = 0.0f;
 #pragma unroll
             for (int d = 0; d < DP; ++d) sq = __builtin_fmaf(cs[c * CS + d], cs[c * CS + d], sq);
         }
@@ -272,7 +276,14 @@ __global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int c
     for (int c = lane; c < k; c += 64) ccmax = fmaxf(ccmax, ccs[c]);
     ccmax = wave_max(ccmax);
     const int nwords = (nct + 1) >> 1;          // 32-bit candidate words in use
-    const bool partial = nct * 16 > k;          // last centroid tile not full
+    // |c|^2 of the lane's accumulator rows (centroid 16 ct + 4 (lane / 16) + r)
+    // in registers for up to 4 tiles, else read from LDS per use
+    constexpr bool CCREG = NCT <= 4;
+    float ccv[CCREG ? NCT : 1][4];
+#pragma unroll
+    for (int ct = 0; ct < (CCREG ? NCT : 1); ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ccv[ct][r] = ct < nct ? ccs[ct * 16 + 4 * (lane >> 4) + r] : INFINITY;
 
     const uint16_t* kb = a.keys + h * a.hs + p * DP;
     // 256-token blocks blockIdx.x * chunks .. +chunks-1 (the prologue above is
@@ -287,22 +298,23 @@ __global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int c
     const int tw0 = blk * 256 + wave * 64;
     const int t = blk * 256 + tid;
     const bool valid = t < a.T;
+    // (tokens past T re-read token T - 1: the loads need no branches, and
+    // those lanes' results are never stored)
     km_u32x4_t bqa[4][KH];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int tt = tw0 + 16 * j + (lane & 15);
+        const int tt = min(tw0 + 16 * j + (lane & 15), a.T - 1);
 #pragma unroll
         for (int kh = 0; kh < KH; ++kh)
-            bqa[j][kh] = tt < a.T ? *reinterpret_cast<const km_u32x4_t*>(kb + static_cast<int64_t>(tt) * a.ts +
-                                                                         kh * 32 + 8 * (lane >> 4))
-                                  : km_u32x4_t{0u, 0u, 0u, 0u};
+            bqa[j][kh] = *reinterpret_cast<const km_u32x4_t*>(kb + static_cast<int64_t>(tt) * a.ts + kh * 32 +
+                                                              8 * (lane >> 4));
     }
     // the thread's own token row for the exact pass, loaded now as well
     km_u32x4_t xr[DP / 8];
+    const int tc = min(t, a.T - 1);
 #pragma unroll
     for (int i = 0; i < DP / 8; ++i)
-        xr[i] = valid ? *reinterpret_cast<const km_u32x4_t*>(kb + static_cast<int64_t>(t) * a.ts + 8 * i)
-                      : km_u32x4_t{0u, 0u, 0u, 0u};
+        xr[i] = *reinterpret_cast<const km_u32x4_t*>(kb + static_cast<int64_t>(tc) * a.ts + 8 * i);
     // screening: token tile j = tokens 16j .. 16j+15 of this wave's 64.
     // e(c) = |c|^2 - 2 x.c orders the centroids like D~ = |x|^2 + e(c).
 #pragma unroll
@@ -321,11 +333,11 @@ __global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int c
             const float own = rr == 0 ? dg[0] : rr == 1 ? dg[1] : rr == 2 ? dg[2] : dg[3];
             xs = __shfl(own, 16 * (tl >> 2) + tl);
         }
-        float ev[MAXK / 16][4];
+        float ev[NCT][4];
         float emin = INFINITY;
 #pragma unroll
-        for (int ct = 0; ct < MAXK / 16; ++ct) {
-            if (ct < nct) {
+        for (int ct = 0; ct < NCT; ++ct) {
+            if (KT > 0 || ct < nct) {
                 km_f32x4_t acc = km_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int kh = 0; kh < KH; ++kh) {
@@ -338,9 +350,8 @@ __global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int c
                 }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int c = ct * 16 + 4 * (lane >> 4) + r;
-                    float v = __builtin_fmaf(-2.0f, acc[r], ccs[c]);
-                    if (partial && ct == nct - 1 && c >= k) v = INFINITY;
+                    const float cc = CCREG ? ccv[CCREG ? ct : 0][r] : ccs[ct * 16 + 4 * (lane >> 4) + r];
+                    const float v = __builtin_fmaf(-2.0f, acc[r], cc);
                     ev[ct][r] = v;
                     emin = fminf(emin, v);
                 }
@@ -359,7 +370,7 @@ __global__ __launch_bounds__(256) void km_assign_screen_kernel(KmParams a, int c
         const float lim = all ? 3.402823466e38f : lim0;
         uint32_t m[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int ct = 0; ct < MAXK / 16; ++ct) {
+        for (int ct = 0; ct < NCT; ++ct) {
             uint32_t nib = 0u;
 #pragma unroll
             for (int r = 0; r < 4; ++r) nib |= ev[ct][r] <= lim ? (1u << r) : 0u;
@@ -808,23 +819,23 @@ size_t workspace_bytes(const imi_kmeans_args* a, int kmax, KmParams* out) {
     return cv.used();
 }
 
-template <int DP, int MAXK>
+template <int DP, int MAXK, int KT>
 int run_screen(const KmParams& p, int segs, hipStream_t stream) {
     const size_t lds = screen_lds_bytes<DP>(p.kmax);
     if (lds > 64 * 1024)
-        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_assign_screen_kernel<DP, MAXK>),
+        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_assign_screen_kernel<DP, MAXK, KT>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
     // as many workgroups as fit on the device at once, each over `chunks`
     // consecutive 256-token blocks
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, km_assign_screen_kernel<DP, MAXK>, 256, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, km_assign_screen_kernel<DP, MAXK, KT>, 256, lds) !=
             hipSuccess ||
         per_cu <= 0)
         per_cu = 1;
     const int64_t want = static_cast<int64_t>(per_cu) * device_cus();
     const int chunks = static_cast<int>(std::max<int64_t>(1, (static_cast<int64_t>(p.nblk) * segs + want - 1) / want));
     const int gx = (p.nblk + chunks - 1) / chunks;
-    hipLaunchKernelGGL((km_assign_screen_kernel<DP, MAXK>), dim3(gx, segs), dim3(256), lds, stream, p, chunks);
+    hipLaunchKernelGGL((km_assign_screen_kernel<DP, MAXK, KT>), dim3(gx, segs), dim3(256), lds, stream, p, chunks);
     IMI_LAUNCH_CHECK("km_assign_screen_kernel");
     return IMI_OK;
 }
@@ -832,7 +843,18 @@ int run_screen(const KmParams& p, int segs, hipStream_t stream) {
 template <int DP>
 int run_assign(const KmParams& p, int segs, hipStream_t stream) {
     if (p.kmax <= kScreenMaxK) {
-        return p.kmax <= 64 ? run_screen<DP, 64>(p, segs, stream) : run_screen<DP, kScreenMaxK>(p, segs, stream);
+        bool same = true;   // every subspace has kmax centroids
+        for (int q = 0; q < p.P; ++q) same = same && p.k[q] == p.kmax;
+        if (same) {
+            switch (p.kmax) {
+                case 16: return run_screen<DP, 64, 1>(p, segs, stream);
+                case 32: return run_screen<DP, 64, 2>(p, segs, stream);
+                case 64: return run_screen<DP, 64, 4>(p, segs, stream);
+                case 128: return run_screen<DP, kScreenMaxK, 8>(p, segs, stream);
+                default: break;
+            }
+        }
+        return p.kmax <= 64 ? run_screen<DP, 64, 0>(p, segs, stream) : run_screen<DP, kScreenMaxK, 0>(p, segs, stream);
     }
     const size_t lds = static_cast<size_t>(p.kmax) * DP * sizeof(float) + 4 * p.kmax * sizeof(int) + 64;
     if (lds > 64 * 1024) IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_assign_kernel<DP>),
