@@ -581,7 +581,12 @@ __global__ __launch_bounds__(pp_threads<DP>()) void km_pp_kernel(KmParams a, int
 
 // Per segment: exclusive scan of the [label][block] counts, cluster offsets,
 // empty-cluster ordinals, inertia (fixed reduction order) and the early-stop
-// test of kmeans_core.cpp:244-262.
+// test of kmeans_core.cpp:244-262.  Up to 64 counts per thread (k * nblk <=
+// 65536, 16-byte aligned) stay in registers: one read, one write, and the
+// cluster offsets come from the threads that hold them; larger segments use
+// the two-pass block scan.
+constexpr int kScanRegInts = 64;
+
 __global__ __launch_bounds__(1024) void km_scan_kernel(KmParams a, int it) {
     __shared__ int sh[40];
     __shared__ int soff[257];
@@ -591,34 +596,98 @@ __global__ __launch_bounds__(1024) void km_scan_kernel(KmParams a, int it) {
     if (a.done && a.done[seg]) return;
     const int p = seg % a.P;
     const int k = a.k[p];
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, wave = tid >> 6;
+    int32_t* hist = a.hist + static_cast<int64_t>(seg) * a.kmax * a.nblk;
+    const int n = k * a.nblk;
+    const bool reg = n <= 1024 * kScanRegInts && (n & 3) == 0 && (reinterpret_cast<uintptr_t>(hist) & 15) == 0;
+    // this thread's counts: a contiguous run of `per` (multiple of 4) ints
+    int per = (n + 1023) / 1024;
+    per = (per + 3) & ~3;
+    const int lo = min(tid * per, n), hi = min(lo + per, n);
+    typedef int __attribute__((ext_vector_type(4))) i32x4;
+    i32x4 v[kScanRegInts / 4];
+    if (reg) {
+#pragma unroll
+        for (int u = 0; u < kScanRegInts / 4; ++u)
+            v[u] = lo + 4 * u < hi ? *reinterpret_cast<const i32x4*>(hist + lo + 4 * u) : i32x4{0, 0, 0, 0};
+    }
     // inertia partials: contiguous chunk per thread, then waves in order
     const float* ip = a.ipart + static_cast<int64_t>(seg) * a.nblk;
-    const int per = (a.nblk + 1023) / 1024;
+    const int iper = (a.nblk + 1023) / 1024;
     float part = 0.0f;
-    for (int b = tid * per; b < (tid + 1) * per && b < a.nblk; ++b) part += ip[b];
+    for (int b = tid * iper; b < (tid + 1) * iper && b < a.nblk; ++b) part += ip[b];
     part = wave_sum(part);
-    if ((tid & 63) == 0) sred[tid >> 6] = part;
-    int32_t* hist = a.hist + static_cast<int64_t>(seg) * a.kmax * a.nblk;
-    block_exclusive_scan_1024(hist, static_cast<int64_t>(k) * a.nblk, sh);
+    if ((tid & 63) == 0) sred[wave] = part;
     int32_t* off = a.off + static_cast<int64_t>(seg) * (a.kmax + 1);
-    for (int c = tid; c < k; c += 1024) {
-        const int o = hist[static_cast<int64_t>(c) * a.nblk];
-        off[c] = o;
-        soff[c] = o;
+    if (reg) {
+        int local = 0;
+#pragma unroll
+        for (int u = 0; u < kScanRegInts / 4; ++u) local += (v[u][0] + v[u][1]) + (v[u][2] + v[u][3]);
+        const int incl = wave_incl_scan(local);
+        if ((tid & 63) == 63) sh[wave] = incl;
+        __syncthreads();
+        if (tid < 64) {
+            const int x = tid < 16 ? sh[tid] : 0;
+            const int sc = wave_incl_scan(x);
+            if (tid < 16) sh[16 + tid] = sc - x;
+        }
+        __syncthreads();
+        const int run0 = sh[16 + wave] + incl - local;
+        // cluster offsets: the label boundaries c * nblk inside [lo, hi)
+        for (int c = (lo + a.nblk - 1) / a.nblk; c < k && c * a.nblk < hi; ++c) {
+            const int at = c * a.nblk - lo;
+            int sum = run0;
+#pragma unroll
+            for (int u = 0; u < kScanRegInts / 4; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sum += 4 * u + e < at ? v[u][e] : 0;
+            off[c] = sum;
+            soff[c] = sum;
+        }
+        int run = run0;
+#pragma unroll
+        for (int u = 0; u < kScanRegInts / 4; ++u) {
+            if (lo + 4 * u < hi) {
+                i32x4 o;
+                o[0] = run;
+                run += v[u][0];
+                o[1] = run;
+                run += v[u][1];
+                o[2] = run;
+                run += v[u][2];
+                o[3] = run;
+                run += v[u][3];
+                *reinterpret_cast<i32x4*>(hist + lo + 4 * u) = o;
+            }
+        }
+    } else {
+        block_exclusive_scan_1024(hist, static_cast<int64_t>(n), sh);
+        for (int c = tid; c < k; c += 1024) {
+            const int o = hist[static_cast<int64_t>(c) * a.nblk];
+            off[c] = o;
+            soff[c] = o;
+        }
     }
     if (tid == 0) {
         off[k] = a.T;
         soff[k] = a.T;
     }
     __syncthreads();
+    // empty-cluster ordinals: exclusive count of empty clusters before c
+    // (k <= 256: the first four waves)
+    int empty = 0, eincl = 0;
+    if (wave < 4) {
+        empty = tid < k && soff[tid + 1] == soff[tid] ? 1 : 0;
+        eincl = wave_incl_scan(empty);
+        if ((tid & 63) == 63) sh[32 + wave] = eincl;
+    }
+    __syncthreads();
+    if (wave < 4 && tid < k) {
+        int before = 0;
+        for (int w = 0; w < wave; ++w) before += sh[32 + w];
+        a.empties[static_cast<int64_t>(seg) * a.kmax + tid] = before + eincl - empty;
+    }
     if (tid == 0) {
-        int e = 0;
-        int32_t* emp = a.empties + static_cast<int64_t>(seg) * a.kmax;
-        for (int c = 0; c < k; ++c) {
-            emp[c] = e;
-            if (soff[c + 1] == soff[c]) ++e;
-        }
         float inertia = 0.0f;
         for (int w = 0; w < 16; ++w) inertia += sred[w];
         if (a.iters) a.iters[seg] = it + 1;
@@ -633,15 +702,35 @@ __global__ __launch_bounds__(1024) void km_scan_kernel(KmParams a, int it) {
     if (tid == 0 && stop && a.done) a.done[seg] = 1;
 }
 
+// Member lists: token t of block b goes to the scanned [label][block] offset
+// plus its rank in the block.  Each thread takes one token of each of
+// kScatterBlocks consecutive blocks, so all its loads are in flight together.
+constexpr int kScatterBlocks = 4;
+
 __global__ __launch_bounds__(256) void km_scatter_kernel(KmParams a) {
-    const int seg = blockIdx.y, blk = blockIdx.x;
+    const int seg = blockIdx.y;
     if (a.done && a.done[seg]) return;
-    const int t = blk * 256 + threadIdx.x;
-    if (t >= a.T) return;
     const int64_t so = static_cast<int64_t>(seg) * a.T;
-    const int lab = a.labels[so + t];
-    const int pos = a.hist[(static_cast<int64_t>(seg) * a.kmax + lab) * a.nblk + blk] + a.rank[so + t];
-    a.sorted[so + pos] = t;
+    const int32_t* hist = a.hist + static_cast<int64_t>(seg) * a.kmax * a.nblk;
+    int lab[kScatterBlocks], rnk[kScatterBlocks];
+#pragma unroll
+    for (int u = 0; u < kScatterBlocks; ++u) {
+        const int t = (blockIdx.x * kScatterBlocks + u) * 256 + threadIdx.x;
+        const bool in = t < a.T;
+        lab[u] = in ? a.labels[so + t] : 0;
+        rnk[u] = in ? a.rank[so + t] : 0;
+    }
+    int base[kScatterBlocks];
+#pragma unroll
+    for (int u = 0; u < kScatterBlocks; ++u) {
+        const int blk = blockIdx.x * kScatterBlocks + u;
+        base[u] = blk < a.nblk ? hist[static_cast<int64_t>(lab[u]) * a.nblk + blk] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kScatterBlocks; ++u) {
+        const int t = (blockIdx.x * kScatterBlocks + u) * 256 + threadIdx.x;
+        if (t < a.T) a.sorted[so + base[u] + rnk[u]] = t;
+    }
 }
 
 // M-step, one workgroup per cluster: wave 0 keeps the chains (lane d =
@@ -945,7 +1034,8 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
         if (rc) return rc;
         hipLaunchKernelGGL(km_scan_kernel, dim3(segs), dim3(1024), 0, stream, p, it);
         IMI_LAUNCH_CHECK("km_scan_kernel");
-        hipLaunchKernelGGL(km_scatter_kernel, dim3(p.nblk, segs), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL(km_scatter_kernel, dim3((p.nblk + kScatterBlocks - 1) / kScatterBlocks, segs), dim3(256),
+                           0, stream, p);
         IMI_LAUNCH_CHECK("km_scatter_kernel");
         // Empty-cluster draws of this iteration: std::mt19937(it + 12345) with
         // uniform_int_distribution<int32_t>(0, T-1), one per empty cluster in
