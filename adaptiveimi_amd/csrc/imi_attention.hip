@@ -8,9 +8,14 @@
 // CSR list rows of the selected cells, then the matched delta-ring rows
 // (steady rows) -- with no execution buffer.
 //
-// Grid: H * S workgroups of 4 waves; workgroup b takes split s = b / H of
-// head (b + s) % H, so consecutive workgroups (which the dispatcher deals
-// round robin to the 8 XCDs) rotate over the heads.  Split s covers rows
+// Grid: workgroups of 4 waves in up to four runs of heads; run r covers
+// heads [h_r, h_r + n_r) with S_r splits each, and its workgroup l (counted
+// from the run's first) takes split l / n_r of head h_r + l % n_r, so
+// consecutive workgroups (which the dispatcher deals round robin to the 8
+// XCDs) rotate over the heads.  One run covers every head unless the host
+// passes per-head row bounds (ragged batches), where each run of
+// equal-bound heads gets splits in proportion to its bound.  The run table
+// sits in the first kernel-argument line.  Split s covers rows
 // [R s / S, R (s + 1) / S) of its head's R attended rows, so the work follows
 // the rows each head actually selected, not a bound.
 //
@@ -23,11 +28,11 @@
 // cell, and row -> list row (or -1 - steady row) goes to LDS.  The staged
 // selection shares its LDS with the K / V tiles: a workgroup barrier after
 // the tables separates the last read of the one from the first write of the
-// other.  The short form (at most kFastCap selected cells and 128 rows per
-// wave, the shapes of the decode configurations at up to 128k tokens) keeps
-// each lane's two row locations in registers (the tile loads fetch them
-// with a lane shuffle) and stages the selection apart from the tiles, so no
-// workgroup barrier separates the lookup from the first loads.  Kernel
+// other.  The short form (at most kFastCap selected cells and 64 NR rows
+// per wave, NR = 2 or 4: the decode configurations at up to 128k tokens)
+// keeps each lane's NR row locations in registers (the tile loads fetch
+// them with a lane shuffle) and stages the selection apart from the tiles,
+// so no workgroup barrier separates the lookup from the first loads.  Kernel
 // arguments are ordered so that the prologue's loads depend on one 64-byte
 // argument line, and the per-head counts are read with vector loads that
 // leave with the others (one memory round trip before the lookup).

@@ -30,10 +30,10 @@
 // with the delta append.
 
 // Outputs have the 2-way layout (cells in rank order, CSR offset, count,
-// exclusive row prefix, m, rows), so the attention kernel is shared.  The
-// per-head candidate counters live at a fixed place of the workspace and the
-// final kernel zeroes its head's again, so a workspace zero-filled once
-// serves later calls of any shape.
+// exclusive row prefix, m, rows), so the attention kernel is shared.  Each
+// score workgroup writes its candidates to its own region of the workspace
+// with its count and key range, and the final kernel reads only those: no
+// workspace bytes have to start at zero and no global atomics are used.
 #include "imi_common.hpp"
 
 namespace imi {
