@@ -740,8 +740,8 @@ __global__ __launch_bounds__(256) void km_scatter_kernel(KmParams a) {
 // loader 1 + b % 3 as its local batch b / 3; round q hands batches 3q ..
 // 3q+2 over through one of two sets of LDS slots (the loaders fill round
 // q+1 while wave 0 sums round q), one barrier per round.  Each loader keeps
-// NB local batches in flight in a register ring and the member ids NI local
-// batches ahead (the same ring discipline as a lone wave).
+// NB local batches in flight in a register ring and loads the member ids 2 NB
+// local batches ahead.
 template <int DP>
 __global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, int it, Draws draws) {
     constexpr int PARTS = DP / 8;    // 16-byte parts per row
@@ -749,7 +749,6 @@ __global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, int it
     constexpr int LPB = PARTS;       // load instructions per 64-row batch
     constexpr int NL = 3;            // loader waves
     constexpr int NB = 4;            // local batches in flight per loader
-    constexpr int NI = 2 * NB;       // local id batches in flight per loader
     __shared__ km_u32x4_t ring[2 * NL][64 * PARTS];
     const int c = blockIdx.x, seg = blockIdx.y;
     const int h = seg / a.P, p = seg % a.P;
@@ -772,40 +771,53 @@ __global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, int it
     const int nb = (n + 63) >> 6;              // 64-row batches
     const int rounds = (nb + NL - 1) / NL;     // = local batches of loader 1
     const int32_t* srt = a.sorted + static_cast<int64_t>(seg) * a.T + lo;
+    // rounds padded to whole ring cycles: the loaders' loop body is then free
+    // of branches, so the compiler's wait before each slot write counts the
+    // loads issued since that batch's (a branch around a load makes it assume
+    // the fewest, which waited for nearly every load and left one batch in
+    // flight).  Padding rounds re-read the last member's row (L2-resident)
+    // and are not summed.
+    const int rounds_pad = (rounds + NB - 1) / NB * NB;
     if (wave > 0) {
         const int lw = wave - 1;
         const int part = lane % PARTS, rsub = lane / PARTS;
-        // global batch of local batch q: NL * q + lw; rows past n read token 0
-#define KMB_ID(q) ((NL * (q) + lw) * 64 + lane < n ? srt[(NL * (q) + lw) * 64 + lane] : 0)
+        // member ids of local batch q (global batch NL q + lw); past n the
+        // last member again (a valid row, never summed: the chain adds only
+        // the first n).  No select on the loaded id: one would make the
+        // compiler wait for each id load right after issuing it.
+#define KMB_ID(q) srt[min((NL * (q) + lw) * 64 + lane, n - 1)]
 #define KMB_ROWS(idv, slot)                                                                            \
     _Pragma("unroll") for (int u = 0; u < LPB; ++u) {                                                \
         const int id_ = __shfl((idv), u * RPL + rsub);                                               \
         rr[slot][u] = *reinterpret_cast<const km_u32x4_t*>(kbase + static_cast<int64_t>(id_) * a.ts + part * 8); \
     }
-        int idr[NI];
+        // rows of local batches 0 .. NB-1 in the register ring, ids of
+        // NB .. 2NB-1 in the id ring; round q writes batch q, loads the rows
+        // of q + NB and the ids of q + 2NB
+        // (the prologue issues its loads in the loop's order -- slot j's rows,
+        // then slot j's next ids -- so the waits inside the loop are the same
+        // on entry and on the back edge)
+        int idr[NB], id0[NB];
         km_u32x4_t rr[NB][LPB];
 #pragma unroll
-        for (int j = 0; j < NI; ++j) idr[j] = KMB_ID(j);
+        for (int j = 0; j < NB; ++j) id0[j] = KMB_ID(j);
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            KMB_ROWS(idr[j], j)
+            KMB_ROWS(id0[j], j)
+            idr[j] = KMB_ID(NB + j);
+            __builtin_amdgcn_sched_barrier(0);   // keep this order (no reordering of the loads)
         }
 #pragma unroll 1
-        for (int q0 = 0; q0 < rounds; q0 += NI) {
+        for (int q0 = 0; q0 < rounds_pad; q0 += NB) {
 #pragma unroll
-            for (int jj = 0; jj < NI; ++jj) {
-                const int q = q0 + jj;
-                if (q < rounds) {
-                    const int j = jj % NB;
-                    km_u32x4_t* slot = ring[(q & 1) * NL + lw];
+            for (int j = 0; j < NB; ++j) {
+                const int q = q0 + j;
+                km_u32x4_t* slot = ring[(q & 1) * NL + lw];
 #pragma unroll
-                    for (int u = 0; u < LPB; ++u) slot[(u * RPL + rsub) * PARTS + part] = rr[j][u];
-                    if (q + NB < rounds) {
-                        KMB_ROWS(idr[(jj + NB) % NI], j)
-                    }
-                    if (q + NI < rounds) idr[jj] = KMB_ID(q + NI);
-                }
-                if (q0 + jj < rounds) __syncthreads();
+                for (int u = 0; u < LPB; ++u) slot[(u * RPL + rsub) * PARTS + part] = rr[j][u];
+                KMB_ROWS(idr[j], j)
+                idr[j] = KMB_ID(q + 2 * NB);
+                __syncthreads();
             }
         }
 #undef KMB_ID
@@ -813,8 +825,9 @@ __global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, int it
     } else {
         float acc = 0.0f;
 #pragma unroll 1
-        for (int q = 0; q < rounds; ++q) {
+        for (int q = 0; q < rounds_pad; ++q) {
             __syncthreads();   // round q's slots are filled
+            if (q >= rounds) continue;
 #pragma unroll
             for (int lw = 0; lw < NL; ++lw) {
                 const int b = NL * q + lw;
