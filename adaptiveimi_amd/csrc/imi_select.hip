@@ -685,12 +685,19 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     int32_t* out_cell = a.sel_cell + static_cast<int64_t>(h) * a.sel_cap;
     int32_t* out_off = a.sel_offset + static_cast<int64_t>(h) * a.sel_cap;
     int32_t* out_cnt = a.sel_count + static_cast<int64_t>(h) * a.sel_cap;
+    // late CSR offsets: both ranks' loads issued before either is stored
+    // (ranks past m re-read rank m - 1)
+    int offv[2] = {0, 0};
+    if (LATE_OFF && m > 0) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) offv[u] = offs[sg[min(2 * tid + u, m - 1)]];
+    }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int r = 2 * tid + u;
         if (r < m) {
             out_cell[r] = sg[r];
-            out_off[r] = LATE_OFF ? offs[sg[r]] : so[r];
+            out_off[r] = LATE_OFF ? offv[u] : so[r];
             out_cnt[r] = s2[u];
             prefix_out[r] = excl_tok[u];
         }

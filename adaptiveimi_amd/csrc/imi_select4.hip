@@ -779,12 +779,16 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
         __syncthreads();
     }
     const int n1 = seg0[kMaxSeg];
-    auto cand_at = [&](int i) {   // list position of candidate i < n1
+    // list position of candidate i < n1: the last segment start <= i, by a
+    // binary search over the nbs starts (log2 nbs dependent LDS reads; the
+    // starts past the last score workgroup all equal n1 > i, so the search
+    // needs no bound test)
+    const int top = a.nbs <= 1 ? 1 : 1 << (32 - __builtin_clz(a.nbs - 1));   // power of two >= nbs
+    auto cand_at = [&](int i) {
         int lo = 0;
-#pragma unroll
-        for (int step = kMaxSeg / 2; step > 0; step >>= 1) {
+        for (int step = top >> 1; step > 0; step >>= 1) {
             const int mid = lo + step;
-            if (mid < a.nbs && seg0[mid] <= i) lo = mid;
+            lo = seg0[mid] <= i ? mid : lo;
         }
         return cand_pos(hb + lo, i - seg0[lo], a.region);
     };
@@ -997,18 +1001,35 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     int s2[kRPT], pg2[kRPT], o2[kRPT];
     uint32_t g2[kRPT];
     int tsum = 0, psum = 0;
+    if (C > 0) {
+        // size and CSR offset of every rank in one round trip: branch-free
+        // (ranks past C re-read rank C - 1 and are masked), so the kRPT
+        // LDS lookups and loads overlap instead of running one by one
+        int cr[kRPT];
 #pragma unroll
-    for (int u = 0; u < kRPT; ++u) {
-        const int r = kRPT * tid + u;
-        s2[u] = 0;
-        o2[u] = 0;
-        g2[u] = 0;
-        if (r < C) {   // size and CSR offset in one round trip
-            const int slot = min(max(ord[r], 0), kCand4 - 1);
-            const int c = min(max(si[slot], 0), a.cap - 1);
+        for (int u = 0; u < kRPT; ++u) {
+            const int slot = min(max(ord[min(kRPT * tid + u, C - 1)], 0), kCand4 - 1);
+            cr[u] = min(max(si[slot], 0), a.cap - 1);
             g2[u] = 0xFFFFFFFFu - static_cast<uint32_t>(sk[slot] & 0xFFFFFFFFull);
-            s2[u] = a.csize[static_cast<int64_t>(h) * a.cap + c];
-            o2[u] = a.coff[static_cast<int64_t>(h) * (a.cap + 1) + c];
+        }
+#pragma unroll
+        for (int u = 0; u < kRPT; ++u) {
+            s2[u] = a.csize[static_cast<int64_t>(h) * a.cap + cr[u]];
+            o2[u] = a.coff[static_cast<int64_t>(h) * (a.cap + 1) + cr[u]];
+        }
+#pragma unroll
+        for (int u = 0; u < kRPT; ++u) {
+            const bool in = kRPT * tid + u < C;
+            s2[u] = in ? s2[u] : 0;
+            o2[u] = in ? o2[u] : 0;
+            g2[u] = in ? g2[u] : 0u;
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < kRPT; ++u) {
+            s2[u] = 0;
+            o2[u] = 0;
+            g2[u] = 0u;
         }
     }
 #pragma unroll
