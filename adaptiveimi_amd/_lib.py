@@ -87,6 +87,17 @@ class DecodeArgs(ctypes.Structure):
     _fields_ = [("sel", SelectArgs), ("attn", AttentionArgs), ("phases", _i32)]
 
 
+class HostcacheGatherArgs(ctypes.Structure):
+    _fields_ = [("host_keys", _vp), ("host_values", _vp), ("list_rows", _i64),
+                ("cache_keys", _vp), ("cache_values", _vp), ("cache_rows", _i64),
+                ("exec_keys", _vp), ("exec_values", _vp), ("exec_rows", _i64),
+                ("groups", _i32), ("max_blocks", _i32), ("block_size", _i32),
+                ("hit_ids", _vp), ("hit_sizes", _vp), ("hit_prefix", _vp), ("hit_nums", _vp),
+                ("miss_ids", _vp), ("miss_sizes", _vp), ("miss_prefix", _vp), ("miss_nums", _vp),
+                ("sel_offset", _vp), ("sel_count", _vp), ("sel_prefix", _vp), ("n_selected", _vp),
+                ("n_rows", _vp), ("sel_cap", _i32)]
+
+
 EXPORTS = {
     "imi_last_error": (ctypes.c_char_p, []),
     "imi_version": (ctypes.c_int, []),
@@ -106,6 +117,17 @@ EXPORTS = {
     "imi_update_workspace_size": (ctypes.c_int, [ctypes.POINTER(UpdateArgs), ctypes.POINTER(ctypes.c_size_t)]),
     "imi_update_assign": (ctypes.c_int, [ctypes.POINTER(UpdateArgs), _vp]),
     "imi_update_refresh": (ctypes.c_int, [ctypes.POINTER(UpdateArgs), _vp]),
+    "imi_hostcache_create": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_double,
+                                            ctypes.POINTER(_vp)]),
+    "imi_hostcache_destroy": (None, [_vp]),
+    "imi_hostcache_set_metadata": (ctypes.c_int, [_vp, _vp, _vp]),
+    "imi_hostcache_access": (ctypes.c_int, [_vp, _vp, _i32] + [_vp] * 8),
+    "imi_hostcache_update": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
+    "imi_hostcache_stats": (ctypes.c_int, [_vp, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
+    "imi_hostcache_gather": (ctypes.c_int, [ctypes.POINTER(HostcacheGatherArgs), _vp]),
+    "imi_hostcache_admit": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
+                                           _vp]),
+    "imi_host_device_pointer": (ctypes.c_int, [_vp, ctypes.POINTER(_vp)]),
 }
 
 _lib = None

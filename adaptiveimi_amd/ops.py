@@ -628,9 +628,10 @@ class DecodePlan:
         self.args.sel.exec_rows = int(exec_rows)
 
     def run(self, query: torch.Tensor, out: torch.Tensor, static_len: int, stream: Optional[int] = None,
-            exec_rows: Optional[int] = None) -> torch.Tensor:
-        """One full step on caller-owned query [H, G, D] and out [H * G, D]
-        buffers (no copies: the plan's pointers are redirected)."""
+            exec_rows: Optional[int] = None, phases: int = 3) -> torch.Tensor:
+        """One step (phases as in step(); 3 = all of it) on caller-owned query
+        [H, G, D] and out [H * G, D] buffers (no copies: the plan's pointers
+        are redirected)."""
         _as_bits(query)
         if not query.is_contiguous() or tuple(query.shape) != (self.H, self.G, self.D):
             raise ValueError(f"query must be a contiguous [{self.H}, {self.G}, {self.D}] tensor")
@@ -642,7 +643,7 @@ class DecodePlan:
         a.attn.static_len = int(static_len)
         if exec_rows is not None:
             a.sel.exec_rows = int(exec_rows)
-        a.phases = 3
+        a.phases = int(phases)
         try:
             check(self._fn(self._ref, stream if stream is not None else _stream(self.device)), "imi_decode_step")
         finally:
@@ -694,3 +695,151 @@ def dense_attention(query: torch.Tensor, steady_keys: torch.Tensor, steady_value
     a.workspace_bytes = ws.numel()
     check(_lib.lib().imi_sparse_attention(ctypes.byref(a), _stream(dev)), "imi_sparse_attention")
     return out
+
+
+def host_cache_pages(n_centroids: int, nprobe: int, pages_per_cluster: int = 2, cache_ratio: float = 0.05) -> int:
+    """GPU cache size in pages (runtime.py:48-53): round(n_centroids *
+    cache_ratio) clusters (nprobe * 3 when cache_ratio <= 0) of
+    pages_per_cluster pages, at least one."""
+    clusters = round(n_centroids * cache_ratio) if cache_ratio > 0.0 else nprobe * 3
+    return max(int(clusters) * int(pages_per_cluster), 1)
+
+
+class HostTierPlan:
+    """Decode over KV lists in pinned host memory with a GPU block cache per
+    KV head (the reference's wave buffer: wave_buffer_cpu_hotcold.cpp:54-372,
+    retrieval.py:200-290 _run_retrieval_full).  Per step: the selection runs
+    on the GPU and its ranked cells come to the host (the reference's
+    retrieval.py:377 copy); the host cache manager splits their pages into
+    hits (cache blocks) and misses (list rows in host memory); the gather
+    kernel builds the execution buffer [miss rows | hit rows] and a one-cell
+    selection over it; the host admits the missed clusters that fit; the
+    admission kernel copies them into the cache; the attention runs over
+    [steady rows | buffer].  2-way IMI without tile mode or the online update.
+
+    The lists are copied once into pinned host memory (list_keys /
+    list_values may then be freed by the caller); the device holds the
+    cache (cache_pages x page_size rows per head) and the execution buffer
+    (buffer_pages x page_size rows per head)."""
+
+    def __init__(self, centroids: torch.Tensor, cell_count: torch.Tensor, cell_offset: torch.Tensor,
+                 ks: Sequence[int], budget: Budget, list_keys: torch.Tensor, list_values: torch.Tensor,
+                 steady_keys: Optional[torch.Tensor], steady_values: Optional[torch.Tensor], groups: int,
+                 cache_pages: int, hot_ratio: float = 0.0, scale: Optional[float] = None):
+        import numpy as np
+
+        if len(ks) != 2:
+            raise ValueError("the host tier serves 2-way IMI (cells = the global cells of the CSR)")
+        if budget.tile_mode or budget.head_buffer_pages is not None:
+            raise ValueError("the host tier runs without tile mode and with one budget for every head")
+        if cache_pages < 1:
+            raise ValueError("cache_pages must be >= 1")
+        dev = _require_device(centroids, cell_count, cell_offset, list_keys, list_values)
+        H, list_rows, D = list_keys.shape
+        ps, bp = budget.page_size, budget.buffer_pages
+        self.device, self.H, self.G, self.D = dev, H, groups, D
+        self.budget, self.cache_pages = budget, int(cache_pages)
+        ncells = int(cell_count.shape[1])
+        self.pad = ncells                       # an empty cell closes each key list
+        # pinned host lists and their device mapping
+        self.h_keys = torch.empty(tuple(list_keys.shape), dtype=list_keys.dtype, pin_memory=True)
+        self.h_values = torch.empty(tuple(list_values.shape), dtype=list_values.dtype, pin_memory=True)
+        self.h_keys.copy_(list_keys)
+        self.h_values.copy_(list_values)
+        L = _lib.lib()
+        dk, dv = ctypes.c_void_p(), ctypes.c_void_p()
+        check(L.imi_host_device_pointer(ctypes.c_void_p(self.h_keys.data_ptr()), ctypes.byref(dk)),
+              "imi_host_device_pointer")
+        check(L.imi_host_device_pointer(ctypes.c_void_p(self.h_values.data_ptr()), ctypes.byref(dv)),
+              "imi_host_device_pointer")
+        self.exec_rows = bp * ps
+        self.cache_rows = self.cache_pages * ps
+        self.exec_keys = torch.zeros((H, self.exec_rows, D), dtype=torch.bfloat16, device=dev)
+        self.exec_values = torch.zeros_like(self.exec_keys)
+        self.cache_keys = torch.zeros((H, self.cache_rows, D), dtype=torch.bfloat16, device=dev)
+        self.cache_values = torch.zeros_like(self.cache_keys)
+        # the selection and the attention of one DecodePlan whose list is the buffer
+        self.plan = DecodePlan(centroids, cell_count, cell_offset, ks, budget, self.exec_keys, self.exec_values,
+                               steady_keys, steady_values, groups, scale=scale)
+        self.cap = self.plan.sel_cap
+        # host cache manager over the cells plus the empty padding cell
+        sizes = np.zeros((H, ncells + 1), np.int32)
+        offs = np.zeros((H, ncells + 2), np.int32)
+        sizes[:, :ncells] = cell_count.cpu().numpy()
+        offs[:, :ncells + 1] = cell_offset.cpu().numpy()
+        offs[:, ncells + 1] = offs[:, ncells]
+        self._h = ctypes.c_void_p()
+        check(L.imi_hostcache_create(H, ncells + 1, self.cache_pages, ps, bp, self.cap, float(hot_ratio),
+                                     ctypes.byref(self._h)), "imi_hostcache_create")
+        check(L.imi_hostcache_set_metadata(self._h, sizes.ctypes.data_as(ctypes.c_void_p),
+                                           offs.ctypes.data_as(ctypes.c_void_p)), "imi_hostcache_set_metadata")
+        # pinned host lists (8 access + 4 update arrays) and their device copies
+        n = H * bp
+        self.h_lists = torch.zeros((12, n), dtype=torch.int32, pin_memory=True)
+        self.h_nums = torch.zeros((3, 2, H), dtype=torch.int32, pin_memory=True)   # hit, miss, update counts
+        self.d_lists = torch.zeros((12, n), dtype=torch.int32, device=dev)
+        self.d_nums = torch.zeros((3, 2, H), dtype=torch.int32, device=dev)
+        self.h_sel = torch.zeros((H, self.cap), dtype=torch.int32, pin_memory=True)
+        self.h_nsel = torch.zeros(H, dtype=torch.int32, pin_memory=True)
+        self.keys = np.full((H, self.cap), self.pad, np.int64)
+        self.hits = self.misses = 0
+        sel = self.plan.selection
+        g = _lib.HostcacheGatherArgs()
+        g.host_keys, g.host_values, g.list_rows = dk.value, dv.value, list_rows
+        g.cache_keys, g.cache_values, g.cache_rows = self.cache_keys.data_ptr(), self.cache_values.data_ptr(), self.cache_rows
+        g.exec_keys, g.exec_values, g.exec_rows = self.exec_keys.data_ptr(), self.exec_values.data_ptr(), self.exec_rows
+        g.groups, g.max_blocks, g.block_size = H, bp, ps
+        row = lambda i: self.d_lists[i].data_ptr()
+        g.hit_ids, g.hit_sizes, g.hit_prefix = row(0), row(1), row(2)
+        g.miss_ids, g.miss_sizes, g.miss_prefix = row(3), row(4), row(5)
+        g.hit_nums, g.miss_nums = self.d_nums[0, 0].data_ptr(), self.d_nums[0, 1].data_ptr()
+        g.sel_offset, g.sel_count = sel["sel_offset"].data_ptr(), sel["sel_count"].data_ptr()
+        g.sel_prefix, g.n_selected, g.n_rows = sel["sel_prefix"].data_ptr(), sel["n_selected"].data_ptr(), sel["n_rows"].data_ptr()
+        g.sel_cap = self.cap
+        self._gather = g
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            _lib.lib().imi_hostcache_destroy(h)
+            self._h = None
+
+    def step(self, query: torch.Tensor, out: torch.Tensor, static_len: int) -> torch.Tensor:
+        """One decode step (host-synchronous, as the reference's)."""
+        import numpy as np
+
+        L = _lib.lib()
+        stream = _stream(self.device)
+        H, cap, bp = self.H, self.cap, self.budget.buffer_pages
+        self.plan.run(query, out, static_len, stream=stream, phases=1)          # selection
+        sel = self.plan.selection
+        self.h_sel.copy_(sel["sel_cell"], non_blocking=True)
+        self.h_nsel.copy_(sel["n_selected"], non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        cells, m = self.h_sel.numpy(), self.h_nsel.numpy()
+        keys = self.keys
+        keys.fill(self.pad)
+        live = np.arange(cap)[None, :] < np.clip(m, 0, cap)[:, None]
+        keys[live] = cells[live]
+        hl, hn = self.h_lists.numpy(), self.h_nums.numpy()
+        p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+        check(L.imi_hostcache_access(self._h, p(keys), cap, p(hl[0]), p(hl[1]), p(hl[2]), p(hn[0, 0]),
+                                     p(hl[3]), p(hl[4]), p(hl[5]), p(hn[0, 1])), "imi_hostcache_access")
+        self.d_lists[:6].copy_(self.h_lists[:6], non_blocking=True)
+        self.d_nums[0].copy_(self.h_nums[0], non_blocking=True)
+        check(L.imi_hostcache_gather(ctypes.byref(self._gather), stream), "imi_hostcache_gather")
+        hb, mbk = ctypes.c_int64(), ctypes.c_int64()
+        check(L.imi_hostcache_stats(self._h, ctypes.byref(hb), ctypes.byref(mbk)), "imi_hostcache_stats")
+        self.hits += hb.value
+        self.misses += mbk.value
+        # admission (host) while the gather runs, then its copy into the cache
+        check(L.imi_hostcache_update(self._h, p(hl[6]), p(hl[7]), p(hl[8]), p(hn[1, 0])), "imi_hostcache_update")
+        self.d_lists[6:9].copy_(self.h_lists[6:9], non_blocking=True)
+        self.d_nums[1].copy_(self.h_nums[1], non_blocking=True)
+        row = lambda i: self.d_lists[i].data_ptr()
+        check(L.imi_hostcache_admit(self.exec_keys.data_ptr(), self.exec_values.data_ptr(), self.exec_rows,
+                                    self.cache_keys.data_ptr(), self.cache_values.data_ptr(), self.cache_rows,
+                                    self.budget.page_size, H, bp, row(6), row(7), row(8),
+                                    self.d_nums[1, 0].data_ptr(), stream), "imi_hostcache_admit")
+        self.plan.run(query, out, static_len, stream=stream, phases=2)          # attention + merge
+        return out

@@ -364,6 +364,96 @@ int imi_decode_step(const imi_decode_args* a, imi_stream_t stream);
  * expect zero.  No hipMalloc / hipFree is called. */
 int imi_decode_step_noalloc(const imi_decode_args* a, imi_stream_t stream);
 
+/* ------------------------------------------------------------- host tier --
+ * KV lists in pinned host memory with a GPU block cache per KV head, for
+ * shapes whose lists exceed HBM.
+ *
+ * imi_hostcache_* is host code (no GPU call): one block-cache manager per
+ * group (KV head) with the hot / cold LRU policy of the reference's
+ * BufferManager (library/AdaptiveIMI/cpp_extensions/src/
+ * wave_buffer_cpu_hotcold.cpp:54-372): `capacity` cache blocks of
+ * `block_size` rows, a hot list of at most max(1, int(capacity * hot_ratio))
+ * blocks (hot_ratio <= 0 means the reference default 0.3; > 1 counts as 1),
+ * and at most `max_consider_blocks` blocks per access (the buffer page
+ * rule).  Replaces AdpIMI_Index::set_cluster_metadata (:850-895),
+ * batch_access (:897-929, BufferManager::batch_access :295-371) and
+ * batch_update (:931-949, BufferManager::batch_update :216-293); lists are
+ * [groups][max_consider_blocks] int32 host arrays, counts [groups]. */
+typedef struct imi_hostcache imi_hostcache;
+
+int imi_hostcache_create(int32_t groups, int32_t n_cells, int32_t capacity, int32_t block_size,
+                         int32_t max_consider_blocks, int32_t max_keys, double hot_ratio, imi_hostcache** out);
+void imi_hostcache_destroy(imi_hostcache* c);
+/* Cluster sizes [groups][n_cells] and CSR offsets [groups][n_cells + 1]
+ * (host int32); resets every group's cache to empty. */
+int imi_hostcache_set_metadata(imi_hostcache* c, const int32_t* sizes, const int32_t* offsets);
+/* keys: [groups][n_keys] host int64 cell ids in rank order (cells of size 0,
+ * e.g. the padding cell, are skipped).  hit_*: cache block id, rows, row
+ * prefix (exclusive, within the hit region); miss_*: first list row, rows,
+ * row prefix within the miss region. */
+int imi_hostcache_access(imi_hostcache* c, const int64_t* keys, int32_t n_keys, int32_t* hit_ids,
+                         int32_t* hit_sizes, int32_t* hit_prefix, int32_t* hit_nums, int32_t* miss_ids,
+                         int32_t* miss_sizes, int32_t* miss_prefix, int32_t* miss_nums);
+/* After an access: admits the missed clusters that fit (in rank order),
+ * evicting from the cold then hot tail; update_ids = the cache block each
+ * admitted block goes to, update_sizes its rows, update_prefix its first
+ * row in the miss region of the execution buffer. */
+int imi_hostcache_update(imi_hostcache* c, int32_t* update_ids, int32_t* update_sizes, int32_t* update_prefix,
+                         int32_t* update_nums);
+/* Totals over the last access: hit and miss blocks. */
+int imi_hostcache_stats(const imi_hostcache* c, int64_t* hit_blocks, int64_t* miss_blocks);
+
+/* GPU side.  Execution buffer exec_* [groups][exec_rows][128] bf16 = the
+ * miss rows (read from the pinned host lists host_* [groups][list_rows][128]
+ * through their device mapping, see imi_host_device_pointer) then the hit
+ * rows (from cache_* [groups][capacity * block_size][128]); the lists are
+ * device copies of the access outputs.  Also writes a one-cell selection
+ * per group over the buffer (sel_offset = 0, sel_count = sel_prefix[1] =
+ * n_rows = rows, n_selected = rows > 0), so imi_sparse_attention with
+ * list = exec, list_rows = exec_rows attends [steady | miss | hit] rows as
+ * the reference's concat_gather_copy (include/copy_kernel.cuh:220-335)
+ * orders them. */
+typedef struct {
+    const uint16_t* host_keys;   /* device address of pinned host memory */
+    const uint16_t* host_values;
+    int64_t list_rows;
+    const uint16_t* cache_keys;  /* device [groups][capacity * block_size][128] */
+    const uint16_t* cache_values;
+    int64_t cache_rows;          /* capacity * block_size */
+    uint16_t* exec_keys;         /* device [groups][exec_rows][128] */
+    uint16_t* exec_values;
+    int64_t exec_rows;           /* >= max_consider_blocks * block_size */
+    int32_t groups, max_blocks;  /* list width (max_consider_blocks) */
+    int32_t block_size;          /* rows per cache block */
+    const int32_t* hit_ids;      /* device copies of the access lists */
+    const int32_t* hit_sizes;
+    const int32_t* hit_prefix;
+    const int32_t* hit_nums;
+    const int32_t* miss_ids;
+    const int32_t* miss_sizes;
+    const int32_t* miss_prefix;
+    const int32_t* miss_nums;
+    int32_t* sel_offset;         /* [groups][sel_cap] outputs: the one-cell */
+    int32_t* sel_count;          /*   selection over the buffer */
+    int32_t* sel_prefix;         /* [groups][sel_cap + 1] */
+    int32_t* n_selected;         /* [groups] */
+    int32_t* n_rows;             /* [groups] */
+    int32_t sel_cap;
+} imi_hostcache_gather_args;
+
+int imi_hostcache_gather(const imi_hostcache_gather_args* a, imi_stream_t stream);
+/* Cache admission (the reference's gather_copy_scatter,
+ * include/copy_kernel.cuh:439-530): rows [update_prefix[u], + update_sizes[u])
+ * of the buffer's miss region go to cache block update_ids[u]. */
+int imi_hostcache_admit(const uint16_t* exec_keys, const uint16_t* exec_values, int64_t exec_rows,
+                        uint16_t* cache_keys, uint16_t* cache_values, int64_t cache_rows, int32_t block_size,
+                        int32_t groups, int32_t max_blocks, const int32_t* update_ids, const int32_t* update_sizes,
+                        const int32_t* update_prefix, const int32_t* update_nums, imi_stream_t stream);
+/* Device address of pinned host memory allocated by hipHostMalloc (torch
+ * pin_memory=True); no counterpart in the reference (CUDA's unified
+ * addressing hands the host pointer to the kernel). */
+int imi_host_device_pointer(const void* host, void** device);
+
 #ifdef __cplusplus
 }
 #endif
