@@ -12,7 +12,7 @@ ROOT = Path(__file__).resolve().parent.parent
 
 def declared_functions():
     text = (ROOT / "include" / "imi_hip.h").read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(imi_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|void|const char\*)\s+(imi_\w+)\s*\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")
