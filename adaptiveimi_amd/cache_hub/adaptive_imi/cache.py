@@ -14,9 +14,14 @@ What differs inside: the index is built on the GPU at prefill (k-means +
 stable CSR reorganisation, ``imi_kmeans_execute`` / ``imi_build_index``) and
 the list stays in HBM; a decode step is one ``imi_decode_step`` call (scores,
 selection with the page rule, in-place gather and attention) with no host
-round trip.  The host-tier page cache, its thread pool and the prefetch
-warm-up of the reference have no counterpart because nothing lives on the
-host; their constructor arguments are accepted and recorded.
+round trip.  By default nothing lives on the host, so the reference's
+thread pool and prefetch warm-up have no counterpart (their constructor
+arguments are accepted and recorded).  runtime_config["host_tier"] =
+{"enabled": True} keeps each layer's lists in pinned host memory instead,
+with a GPU block cache of round(n_centroids * cache_ratio) clusters of
+pages_per_cluster pages per head and the reference's hot / cold policy
+(IMI_HOTCOLD_HOT_RATIO, default 0.3): ops.HostTierPlan, for lists that do
+not fit in HBM (2-way IMI, without async_update or tile mode).
 
 Online index maintenance (runtime_config["async_update"], async_update.py)
 runs on the device as well: every `batch` decode keys of a layer are
@@ -124,7 +129,9 @@ class adpimi_cache:  # noqa: N801  (reference class name)
             "prefetch": dict(runtime_config.get("prefetch") or {}),
             "async_update": dict(runtime_config.get("async_update") or {}),
             "pipeline": dict(runtime_config.get("pipeline") or {}),
+            "host_tier": dict(runtime_config.get("host_tier") or {}),
         }
+        self.host_tier = bool(self.runtime_config["host_tier"].get("enabled", False))
         # The reference builds each layer's index on host worker threads while
         # the next layers prefill (LayerPipeline); here the build runs on a
         # side HIP stream and the first use of the index waits for it on the
@@ -409,12 +416,37 @@ class adpimi_cache:  # noqa: N801  (reference class name)
             tiles = int(os.getenv("IMI_MAX_TILES", "0") or 0) != 0
             bud = ops.Budget(self.nprobe, self.max_retrieval_tokens, self.buffer_size, self.page_size,
                              tile_mode=tiles)
+            if self.host_tier:
+                plan = self._host_plan(layer_idx, bud, upd)
+                self._plans[layer_idx] = plan
+                return plan
             plan = ops.DecodePlan(self.centroids[layer_idx], self.cell_count[layer_idx], self.cell_offset[layer_idx],
                                   self.layer_ks[layer_idx], bud, self.list_keys[layer_idx][0],
                                   self.list_values[layer_idx][0], self.steady_zone_keys[layer_idx][0],
                                   self.steady_zone_values[layer_idx][0], self.group_size,
                                   compact=self.compact_cells[layer_idx], update=upd)
             self._plans[layer_idx] = plan
+        return plan
+
+    def _host_plan(self, layer_idx: int, bud: "ops.Budget", upd) -> "ops.HostTierPlan":
+        """The layer's lists move to pinned host memory; the device holds the
+        block cache and the execution buffer (retrieval.py:200-290)."""
+        if upd is not None or bud.tile_mode or len(self.layer_ks[layer_idx]) != 2:
+            raise NotImplementedError("host_tier serves 2-way IMI without async_update or tile mode")
+        env = os.getenv("IMI_HOTCOLD_HOT_RATIO", "")
+        try:
+            ratio = float(env) if env else 0.0   # wave_buffer_cpu_hotcold.cpp:75-95
+        except ValueError:
+            ratio = 0.0
+        pages = ops.host_cache_pages(self.n_centroids, self.nprobe, self.pages_per_cluster, self.cache_ratio)
+        plan = ops.HostTierPlan(self.centroids[layer_idx], self.cell_count[layer_idx], self.cell_offset[layer_idx],
+                                self.layer_ks[layer_idx], bud, self.list_keys[layer_idx][0],
+                                self.list_values[layer_idx][0], self.steady_zone_keys[layer_idx][0],
+                                self.steady_zone_values[layer_idx][0], self.group_size, cache_pages=pages,
+                                hot_ratio=ratio)
+        # the device copies of the lists are no longer needed
+        self.list_keys[layer_idx] = None
+        self.list_values[layer_idx] = None
         return plan
 
     def ensure_layer_ready(self, layer_idx: int) -> None:
@@ -435,7 +467,10 @@ class adpimi_cache:  # noqa: N801  (reference class name)
             q = q.contiguous()
         out = torch.empty((self.batch_size, 1, self.num_heads, self.head_dim), dtype=queries.dtype,
                           device=queries.device)
-        plan.run(q, out, int(static_len), exec_rows=self.execution_stride - int(static_len))
+        if isinstance(plan, ops.HostTierPlan):
+            plan.step(q, out, int(static_len))
+        else:
+            plan.run(q, out, int(static_len), exec_rows=self.execution_stride - int(static_len))
         return out
 
     def dense_attention(self, queries, layer_idx, static_len):

@@ -257,3 +257,66 @@ def test_side_stream_build_matches_inline_build():
         outs.append(res)
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a HIP device")
+def test_host_tier_dropin_matches_oracle():
+    """runtime_config["host_tier"]: lists in pinned host memory, the GPU block
+    cache of round(n_centroids * cache_ratio) clusters x pages_per_cluster
+    pages (runtime.py:48-53); same selection and attention as the oracle."""
+    from adaptiveimi_amd import ops, synthetic
+    from adaptiveimi_amd.attn_hub.sparse_imi import imi_decode_attn
+    from oracle import oracle as orc
+
+    print("[dropin host tier] 2 layers, S=6096, ks=(32, 32), 3 decode steps", flush=True)
+    L, S, H, G, D, ks = 2, 6096, 8, 4, 128, (32, 32)
+    cache = _cache(layer_mapping={"0": DEV, "1": DEV}, max_new_length=5, max_length=6101,
+                   runtime_config={"kmeans": {"k1": 32, "k2": 32, "max_iters": 6, "early_stop_min_iter": 6,
+                                              "init": "first"},
+                                   "host_tier": {"enabled": True}})
+    kv = []
+    for layer in range(L):
+        k, v = synthetic.make_kv(H, S + 3, seed=60 + layer)
+        kv.append((k, v))
+        pk = k[:, :S].transpose(0, 1).unsqueeze(0).contiguous().to(DEV)
+        pv = v[:, :S].transpose(0, 1).unsqueeze(0).contiguous().to(DEV)
+        cache.prefill_update_kv_cache(None, pk, pv, layer, 0)
+        cache.sync(layer, 0)
+    cache.prepare_cache()
+    heads_by_layer = []
+    for layer in range(L):
+        k, v = kv[layer]
+        mid_k, mid_v = _bits(k[:, 32:S - 64]), _bits(v[:, 32:S - 64])
+        heads = []
+        for h in range(H):
+            labs, cents, _ = orc.kmeans_head(orc.bf16_to_f32(mid_k[h]), list(ks), 6, early_stop_min_iter=6)
+            r = orc.compact_reorg(labs, list(ks))
+            heads.append(dict(n_active=r["n_active"], offsets=r["offsets"], gids=r["gids"],
+                              merged=orc.merged_centroids(cents, r["gids"], list(ks)),
+                              list_keys=mid_k[h][r["perm"]], list_values=mid_v[h][r["perm"]]))
+        heads_by_layer.append(heads)
+    for step in range(3):
+        for layer in range(L):
+            k, v = kv[layer]
+            nk = k[:, S + step].reshape(1, 1, H, D).to(DEV)
+            nv = v[:, S + step].reshape(1, 1, H, D).to(DEV)
+            cache.decode_update_kv_cache(nk, nv, layer)
+            q = synthetic.make_queries(k[:, :S], G, seed=layer + 10 * (step % 2))[0]   # steps 0 and 2 repeat
+            out = imi_decode_attn(q.reshape(1, 1, H * G, D).to(DEV), nk, nv, layer, cache)
+            plan = cache._plans[layer]
+            assert isinstance(plan, ops.HostTierPlan) and cache.list_keys[layer] is None
+            static_len = cache.static_pattern_total + (1 if layer < L - 1 else 0)
+            ref, rs, rm, rrows = orc.decode_step(_bits(q), heads_by_layer[layer], _bits(cache.steady_zone_keys[layer][0]),
+                                                 _bits(cache.steady_zone_values[layer][0]), static_len,
+                                                 cache.n_centroids, cache.nprobe, cache.max_retrieval_tokens,
+                                                 cache.buffer_size)
+            assert np.array_equal(plan.h_nsel.numpy(), rm)
+            cells = plan.h_sel.numpy()
+            for h in range(H):
+                gid = heads_by_layer[layer][h]["gids"]
+                assert np.array_equal(cells[h, : rm[h]], gid[rs[h, : rm[h]]]), (layer, h)
+                assert int(plan.plan.selection["n_rows"][h]) == len(rrows[h]), (layer, h)
+            got = out.float().cpu().numpy().reshape(H, G, D)
+            assert np.all(np.abs(got - ref) <= 2e-2 + 1e-2 * np.abs(ref)), (layer, step)
+    assert all(cache._plans[layer].hits > 0 for layer in range(L))   # the repeated step hit the cache
