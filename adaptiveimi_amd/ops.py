@@ -782,7 +782,8 @@ class HostTierPlan:
         self.h_sel = torch.zeros((H, self.cap), dtype=torch.int32, pin_memory=True)
         self.h_nsel = torch.zeros(H, dtype=torch.int32, pin_memory=True)
         self.keys = np.full((H, self.cap), self.pad, np.int64)
-        self.hits = self.misses = 0
+        self.hits = self.misses = 0     # blocks over all steps
+        self.miss_rows = 0              # rows read from host memory over all steps
         sel = self.plan.selection
         g = _lib.HostcacheGatherArgs()
         g.host_keys, g.host_values, g.list_rows = dk.value, dv.value, list_rows
@@ -832,6 +833,8 @@ class HostTierPlan:
         check(L.imi_hostcache_stats(self._h, ctypes.byref(hb), ctypes.byref(mbk)), "imi_hostcache_stats")
         self.hits += hb.value
         self.misses += mbk.value
+        nm = hn[0, 1]
+        self.miss_rows += int(sum(int(hl[4][g * bp:g * bp + int(nm[g])].sum()) for g in range(H)))
         # admission (host) while the gather runs, then its copy into the cache
         check(L.imi_hostcache_update(self._h, p(hl[6]), p(hl[7]), p(hl[8]), p(hn[1, 0])), "imi_hostcache_update")
         self.d_lists[6:9].copy_(self.h_lists[6:9], non_blocking=True)

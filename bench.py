@@ -76,6 +76,9 @@ def parse():
     p.add_argument("--online-layers", type=int, default=4,
                    help="layers of the online-index-maintenance leg (async_update: batch 16, threshold 16, "
                         "512-token ring, 1024 decode keys); 0 skips it")
+    p.add_argument("--host-tier-layers", type=int, default=2,
+                   help="layers of the host-tier leg (lists in pinned host memory, GPU block cache of "
+                        "round(n_centroids * 0.05) clusters x 2 pages); 0 skips it")
     p.add_argument("--copy-probe-mb", type=int, default=0,
                    help="run a device-to-device copy of this many MiB (3 times) before the timed region, as the "
                         "known-size reference for FETCH_SIZE / WRITE_SIZE counter runs")
@@ -92,6 +95,7 @@ def parse():
     if args.workload != "config1":
         args.cpu_baseline = 0      # the CPU baseline is quoted on the default workload
         args.online_layers = 0
+        args.host_tier_layers = 0
     return args
 
 
@@ -259,6 +263,11 @@ def main():
         online = online_update_leg(args, ks, bud, static_total, capture)
         log(f"[bench] online update: {online}")
 
+    host_tier = None
+    if args.host_tier_layers > 0:
+        host_tier = host_tier_leg(args, ks, bud, static_total)
+        log(f"[bench] host tier: {host_tier}")
+
     # ----------------------------------------------------- CPU baseline
     cpu = None
     if keep_first is not None:
@@ -300,6 +309,7 @@ def main():
                                     "kernels": "attention_kernel + merge_kernel"}},
         "cpu_baseline": cpu,
         "online_update": online,
+        "host_tier": host_tier,
     }
     print(json.dumps(result), flush=True)
 
@@ -401,6 +411,71 @@ def online_update_leg(args, ks, bud, static_total, capture):
             "plain_us_per_layer_step": res["plain"][0], "plain_select_us": res["plain"][1],
             "plain_attention_merge_us": res["plain"][2],
             "replaced_cells_per_head": round(repl, 1), "delta_rows_per_head": round(drows, 1)}
+
+
+def host_tier_leg(args, ks, bud, static_total):
+    """The decode step with the lists in pinned host memory and the
+    reference's GPU block cache (wave_buffer_cpu_hotcold.cpp, sized as
+    runtime.py:48-53 with the shipped configs' cache_ratio 0.05 and
+    pages_per_cluster 2), on the first host_tier_layers layers (same seeds as
+    the main run).  Host-synchronous like the reference's step (the selected
+    cells go to the host), so it is timed on the host clock: the first step
+    of each layer (every page a miss) and 10 steps with the same query after
+    it (hits where the cache holds the cells)."""
+    import time
+
+    import torch
+
+    from adaptiveimi_amd import ops, synthetic
+
+    dev = torch.device("cuda:0")
+    H, G, D, NL = args.kv_heads, args.groups, 128, args.host_tier_layers
+    ncells = ks[0] * ks[1]
+    cache_pages = ops.host_cache_pages(ncells + 1, bud.nprobe)
+    static_cap = static_total + 8
+    plans, cold, warm = [], [], []
+    for layer in range(NL):
+        keys, values = synthetic.make_kv(H, args.context, seed=1000 + layer, device="cuda")
+        mid_k = keys[:, args.static_start:args.context - args.static_end]
+        mid_v = values[:, args.static_start:args.context - args.static_end]
+        cent, labels, _ = ops.kmeans(mid_k, list(ks), args.iters)
+        idx = ops.build_index(mid_k, mid_v, cent, labels, list(ks), compact=False)
+        sk = torch.zeros((H, static_cap, D), dtype=torch.bfloat16, device=dev)
+        sv = torch.zeros_like(sk)
+        sk[:, :args.static_start] = keys[:, :args.static_start]
+        sk[:, args.static_start:static_total] = keys[:, args.context - args.static_end:]
+        sv[:, :static_total] = torch.cat([values[:, :args.static_start], values[:, args.context - args.static_end:]], 1)
+        q = synthetic.make_queries(mid_k, G, seed=layer)[0].contiguous()
+        pl = ops.HostTierPlan(cent, idx["cell_count"], idx["cell_offset"], ks, bud, idx["list_keys"],
+                              idx["list_values"], sk, sv, G, cache_pages=cache_pages)
+        plans.append((pl, q, sk, sv, cent, idx["cell_count"], idx["cell_offset"]))
+        del keys, values, mid_k, mid_v, labels, idx
+    out = torch.empty((H * G, D), dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    hits = misses = mrows = 0
+    for pl, q, *_ in plans:
+        t0 = time.perf_counter()
+        pl.step(q, out, static_total)
+        torch.cuda.synchronize()
+        cold.append((time.perf_counter() - t0) * 1e6)
+        h0, m0, r0 = pl.hits, pl.misses, pl.miss_rows
+        for _ in range(10):
+            t0 = time.perf_counter()
+            pl.step(q, out, static_total)
+            torch.cuda.synchronize()
+            warm.append((time.perf_counter() - t0) * 1e6)
+        hits += pl.hits - h0
+        misses += pl.misses - m0
+        mrows += pl.miss_rows - r0
+    warm_us = sorted(warm)[len(warm) // 2]
+    miss_rows = mrows / (10 * NL)
+    return {"layers": NL, "cache_pages": cache_pages, "buffer_pages": bud.buffer_pages,
+            "cold_us_per_layer_step": round(sorted(cold)[len(cold) // 2], 1),
+            "warm_us_per_layer_step": round(warm_us, 1),
+            "warm_hit_block_fraction": round(hits / max(hits + misses, 1), 4),
+            "warm_miss_rows_per_layer_step": round(miss_rows, 1),
+            "warm_miss_gbps": round(miss_rows * 512 / (warm_us * 1e-6) / 1e9, 2),
+            "clock": "host wall clock around each synchronous step"}
 
 
 def measured_traffic(workload):
