@@ -743,7 +743,7 @@ __global__ __launch_bounds__(256) void km_scatter_kernel(KmParams a) {
 // NB local batches in flight in a register ring and loads the member ids 2 NB
 // local batches ahead.
 template <int DP>
-__global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, int it, Draws draws) {
+__global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, Draws draws) {
     constexpr int PARTS = DP / 8;    // 16-byte parts per row
     constexpr int RPL = 64 / PARTS;  // rows per load instruction
     constexpr int LPB = PARTS;       // load instructions per 64-row batch
@@ -1058,9 +1058,9 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
         std::uniform_int_distribution<int32_t> dist(0, a->n_tokens - 1);
         for (int e = 0; e < kmax; ++e) dr.v[e] = dist(rng);
         if (dp == 64)
-            hipLaunchKernelGGL(km_update_block_kernel<64>, dim3(kmax, segs), dim3(256), 0, stream, p, it, dr);
+            hipLaunchKernelGGL(km_update_block_kernel<64>, dim3(kmax, segs), dim3(256), 0, stream, p, dr);
         else
-            hipLaunchKernelGGL(km_update_block_kernel<32>, dim3(kmax, segs), dim3(256), 0, stream, p, it, dr);
+            hipLaunchKernelGGL(km_update_block_kernel<32>, dim3(kmax, segs), dim3(256), 0, stream, p, dr);
         IMI_LAUNCH_CHECK("km_update_block_kernel");
     }
     return IMI_OK;

@@ -821,7 +821,7 @@ int launch_ept(const SelParams& p, int H, hipStream_t stream) {
     return IMI_OK;
 }
 
-int select_one_kernel(const imi_select_args* a, int64_t ncells, int kmax, hipStream_t stream) {
+int select_one_kernel(const imi_select_args* a, hipStream_t stream) {
     SelParams p;
     p.q = a->query;
     p.cent = a->centroids;
@@ -891,7 +891,7 @@ int select_launch(const imi_select_args* a, hipStream_t stream) {
                 IMI_ERR_INVALID, "imi_select: null output pointer");
     IMI_REQUIRE(a->ring_cap == 0 || (a->delta_rows && a->n_delta), IMI_ERR_INVALID,
                 "imi_select: null delta output pointer");
-    if (a->parts == 2 && sel2_one_kernel(a)) return select_one_kernel(a, ncells, kmax, stream);
+    if (a->parts == 2 && sel2_one_kernel(a)) return select_one_kernel(a, stream);
     return select4_launch(a, stream);
 }
 

@@ -315,7 +315,7 @@ __global__ __launch_bounds__(kScore4Threads) void sel4_score_kernel(Sel4 a) {
     const int na = n_active(a, h);
 #pragma unroll
     for (int u = 0; u < kCPT; ++u)
-        if (blockIdx.x * kCellsPerBlock + u * kScore4Threads + tid >= na) gv[u] = 0u;
+        if (static_cast<int>(blockIdx.x) * kCellsPerBlock + u * kScore4Threads + tid >= na) gv[u] = 0u;
     const int c_first = blockIdx.x * kCellsPerBlock;
     const int c_last = min(na, c_first + kCellsPerBlock) - 1;
     const uint32_t k23 = static_cast<uint32_t>(a.k[2]) * static_cast<uint32_t>(a.k[3]);
