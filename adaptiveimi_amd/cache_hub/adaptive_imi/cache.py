@@ -23,6 +23,11 @@ pages_per_cluster pages per head and the reference's hot / cold policy
 (IMI_HOTCOLD_HOT_RATIO, default 0.3): ops.HostTierPlan, for lists that do
 not fit in HBM (2-way IMI, without async_update or tile mode).
 
+subspace_parts = 0 builds an IVF index (kmeans_core.cpp:503-595: one
+k-means over the 128 dims per KV head, k = runtime kmeans.k1 or
+round(T / 16), at most 4096) whose clusters are the cells of the same
+selection and attention path (without async_update or host_tier).
+
 Online index maintenance (runtime_config["async_update"], async_update.py)
 runs on the device as well: every `batch` decode keys of a layer are
 assigned to clusters and enter the delta ring (imi_update_assign, at
@@ -102,8 +107,6 @@ class adpimi_cache:  # noqa: N801  (reference class name)
             raise ValueError("num_heads must be a multiple of num_key_value_heads")
         if subspace_parts not in (0, 2, 4):
             raise ValueError("subspace_parts must be 0, 2 or 4")
-        if subspace_parts == 0:
-            raise NotImplementedError("IVF indexing (subspace_parts=0) is not implemented on this path")
 
         self.device_list = sorted(set(self.layer_mapping.values()),
                                   key=lambda x: (x.split(":")[0], int(x.split(":")[1]) if ":" in x else 0))
@@ -149,6 +152,8 @@ class adpimi_cache:  # noqa: N801  (reference class name)
             raise ValueError("async_update: batch must be at most 64 and at most delta_tokens")
         if self.async_update_enabled and self.async_update_delta_tokens > 1024:
             raise ValueError("async_update: delta_tokens must be at most 1024")
+        if self.async_update_enabled and subspace_parts == 0:
+            raise NotImplementedError("async_update is not available for IVF indexing (subspace_parts=0)")
         self._updates: List[Optional[ops.OnlineUpdate]] = [None] * layer_num
         self._upd_count = [0] * layer_num
         self._upd_pending: List[Optional[int]] = [None] * layer_num   # decode step of an unapplied refresh
@@ -212,18 +217,21 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         self.valid_lengths_dict: Dict[str, torch.Tensor] = {}
 
     # ------------------------------------------------------------ prefill --
+    def _k_names(self) -> Sequence[str]:
+        """Runtime k knobs by index type; IVF takes its cluster count from
+        k1 (layer_pipeline.cpp:1142-1148)."""
+        return {0: ("k1",), 2: ("k1", "k2")}.get(self.subspace_parts, ("k1", "k2", "k3", "k4"))
+
     def _layer_ks(self, n_tokens: int) -> List[int]:
         cfg = self.runtime_config["kmeans"]
-        names = ("k1", "k2") if self.subspace_parts == 2 else ("k1", "k2", "k3", "k4")
-        ks = [int(cfg.get(n, 0) or 0) for n in names]
+        ks = [int(cfg.get(n, 0) or 0) for n in self._k_names()]
         if all(k > 0 for k in ks):   # layer_pipeline.cpp:1137-1156
             return ks
         return adaptive_k(n_tokens, int(cfg.get("target_cluster_size", 16)), self.subspace_parts)
 
     def _decode_budget(self, ks: Sequence[int]) -> Dict[str, int]:
         """runtime.py:31-63 with this cache's list capacity and budget."""
-        names = ("k1", "k2") if self.subspace_parts == 2 else ("k1", "k2", "k3", "k4")
-        explicit = all(int(self.runtime_config["kmeans"].get(n, 0) or 0) > 0 for n in names)
+        explicit = all(int(self.runtime_config["kmeans"].get(n, 0) or 0) > 0 for n in self._k_names())
         return decode_sizing(self.list_capacity, self.retrieval_budget, self.subspace_parts, self.buffer_cluster_num,
                              self.page_size, k_override=ks if explicit else None)
 

@@ -11,7 +11,9 @@
 // The cell order is produced by an LSD sort with one stable counting pass per
 // subspace label (last subspace first), which yields tokens ordered by
 // (l0, l1, ..., token) = (global cell id, token): the reference's CSR order,
-// because compact ids are ranks of global ids.
+// because compact ids are ranks of global ids.  IVF (one subspace, the
+// cluster label is the cell id; build_compact_reorg_input_ivf, 178-231) is
+// the one-pass case.
 #include "imi_common.hpp"
 #include "imi_sort.hpp"
 
@@ -36,8 +38,11 @@ __host__ __device__ inline int bits_for(int n) {
     return b;
 }
 
+constexpr int kIvfMaxK = 4096;   // IVF clusters per head
+
+template <int NB>
 __global__ __launch_bounds__(256) void ix_rank_kernel(IxParams a, int p, const int32_t* in) {
-    __shared__ int wcnt[4 * 256];
+    __shared__ int wcnt[4 * NB];
     const int h = blockIdx.y, blk = blockIdx.x;
     const int pos = blk * 256 + threadIdx.x;
     const bool valid = pos < a.T;
@@ -316,16 +321,18 @@ int validate(const imi_index_args* a, int& kmax, int64_t& ncells) {
                 IMI_ERR_INVALID, "imi_build_index: null pointer argument");
     IMI_REQUIRE(a->kv_heads > 0 && a->n_tokens > 0, IMI_ERR_INVALID, "imi_build_index: empty input");
     IMI_REQUIRE(a->dim == 128, IMI_ERR_UNSUPPORTED, "imi_build_index: head_dim must be 128 (got %d)", a->dim);
-    IMI_REQUIRE(a->parts == 2 || a->parts == 4, IMI_ERR_UNSUPPORTED, "imi_build_index: parts must be 2 or 4");
+    IMI_REQUIRE(a->parts == 1 || a->parts == 2 || a->parts == 4, IMI_ERR_UNSUPPORTED,
+                "imi_build_index: parts must be 1 (IVF), 2 or 4");
     IMI_REQUIRE(a->list_rows >= a->n_tokens, IMI_ERR_INVALID, "imi_build_index: list_rows %lld < n_tokens %d",
                 static_cast<long long>(a->list_rows), a->n_tokens);
     IMI_REQUIRE((a->token_stride % 8) == 0 && (a->head_stride % 8) == 0, IMI_ERR_INVALID,
                 "imi_build_index: strides must be multiples of 8 elements");
     kmax = 0;
     ncells = 1;
+    const int kcap = a->parts == 1 ? kIvfMaxK : 256;
     for (int p = 0; p < a->parts; ++p) {
-        IMI_REQUIRE(a->k[p] >= 1 && a->k[p] <= 256, IMI_ERR_UNSUPPORTED, "imi_build_index: k[%d]=%d outside [1,256]",
-                    p, a->k[p]);
+        IMI_REQUIRE(a->k[p] >= 1 && a->k[p] <= kcap, IMI_ERR_UNSUPPORTED, "imi_build_index: k[%d]=%d outside [1,%d]",
+                    p, a->k[p], kcap);
         kmax = a->k[p] > kmax ? a->k[p] : kmax;
         ncells *= a->k[p];
     }
@@ -409,7 +416,10 @@ extern "C" int imi_build_index(const imi_index_args* a, imi_stream_t stream_) {
     for (int pass = 0; pass < a->parts; ++pass) {
         const int part = a->parts - 1 - pass;
         int32_t* out = ((a->parts - 1 - pass) % 2 == 0) ? a->perm : scratch;
-        hipLaunchKernelGGL(ix_rank_kernel, dim3(p.nblk, p.H), dim3(256), 0, stream, p, part, in);
+        if (a->k[part] <= 256)
+            hipLaunchKernelGGL(ix_rank_kernel<256>, dim3(p.nblk, p.H), dim3(256), 0, stream, p, part, in);
+        else
+            hipLaunchKernelGGL(ix_rank_kernel<kIvfMaxK>, dim3(p.nblk, p.H), dim3(256), 0, stream, p, part, in);
         IMI_LAUNCH_CHECK("ix_rank_kernel");
         hipLaunchKernelGGL(ix_scan_kernel, dim3(p.H), dim3(1024), 0, stream, p, part);
         IMI_LAUNCH_CHECK("ix_scan_kernel");

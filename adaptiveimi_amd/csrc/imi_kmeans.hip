@@ -8,6 +8,9 @@
 //                          1.0f/size; empty cluster <- x[uniform draw])
 //   executor     384-501 (one independent run per (head, subspace))
 //
+// IVF (KmeansExecutorIVF, 503-595) is the one-subspace case: P = 1, Dp = 128,
+// k up to kIvfMaxK, kmeans++ with seed 42.
+//
 // Work layout: every kernel covers all H*P (head, subspace) segments at once.
 // E-step (k <= 128): distances are screened on the matrix cores (bf16 MFMA
 // with the centroids split into hi + lo bf16 parts, under a proven rounding
@@ -56,6 +59,9 @@ struct KmParams {
 struct Draws {
     int32_t v[256];  // uniform draws for the empty clusters of one iteration
 };
+
+constexpr int kDraws = 256;      // empty-cluster draws one launch carries
+constexpr int kIvfMaxK = 4096;   // IVF clusters per head
 
 __host__ __device__ inline int bits_for(int n) {
     int b = 0;
@@ -151,6 +157,75 @@ __global__ __launch_bounds__(256) void km_assign_kernel(KmParams a) {
     if (a.hist == nullptr) return;
 
     // inertia partial of this block (fixed reduction order)
+    float part = wave_sum(valid ? best : 0.0f);
+    if (lane_id() == 0) red[tid >> 6] = part;
+    const int r = block_digit_rank(arg, valid, k, bits_for(k), wcnt,
+                                   a.hist + static_cast<int64_t>(seg) * a.kmax * a.nblk, a.nblk, blk);
+    if (valid) a.rank[static_cast<int64_t>(seg) * a.T + t] = r;
+    if (tid == 0) a.ipart[static_cast<int64_t>(seg) * a.nblk + blk] = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// E-step of the IVF index (Dp = 128, k up to kIvfMaxK): the centroids pass
+// through LDS in tiles of kTileC rows; the exact reference distance to every
+// centroid, c ascending, strict '<'.  Outputs as km_assign_kernel.
+constexpr int kTileC = 64;
+
+template <int DP>
+size_t tiled_lds_bytes(int kmax) {
+    return static_cast<size_t>(kTileC) * DP * sizeof(float) + 4 * static_cast<size_t>(kmax) * sizeof(int) + 64;
+}
+
+template <int DP>
+__global__ __launch_bounds__(256) void km_assign_tiled_kernel(KmParams a) {
+    extern __shared__ float smem[];
+    const int seg = blockIdx.y, blk = blockIdx.x;
+    if (a.done && a.done[seg]) return;
+    const int h = seg / a.P, p = seg % a.P;
+    const int k = a.k[p];
+    const int tid = threadIdx.x;
+    float* cs = smem;                                              // [kTileC][DP]
+    int* wcnt = reinterpret_cast<int*>(smem + kTileC * DP);        // [4][kmax]
+    float* red = reinterpret_cast<float*>(wcnt + 4 * a.kmax);      // [4]
+    const float4* cg = reinterpret_cast<const float4*>(a.cent + static_cast<int64_t>(seg) * a.kmax * DP);
+
+    const int t = blk * 256 + tid;
+    const bool valid = t < a.T;
+    float x[DP];
+    {
+        // past the end: row T - 1 again (a valid row; its label is not stored)
+        const uint4* src = reinterpret_cast<const uint4*>(a.keys + h * a.hs +
+                                                          static_cast<int64_t>(valid ? t : a.T - 1) * a.ts + p * DP);
+#pragma unroll
+        for (int i = 0; i < DP / 8; ++i) {
+            const uint4 v = src[i];
+            x[8 * i + 0] = bf16_lo(v.x); x[8 * i + 1] = bf16_hi(v.x);
+            x[8 * i + 2] = bf16_lo(v.y); x[8 * i + 3] = bf16_hi(v.y);
+            x[8 * i + 4] = bf16_lo(v.z); x[8 * i + 5] = bf16_hi(v.z);
+            x[8 * i + 6] = bf16_lo(v.w); x[8 * i + 7] = bf16_hi(v.w);
+        }
+    }
+    float best = 3.402823466e38f;  // FLT_MAX
+    int arg = 0;
+    for (int c0 = 0; c0 < k; c0 += kTileC) {
+        const int nc = min(kTileC, k - c0);
+        __syncthreads();   // the previous tile is read
+        for (int i = tid; i < nc * (DP / 4); i += 256)
+            reinterpret_cast<float4*>(cs)[i] = cg[static_cast<int64_t>(c0) * (DP / 4) + i];
+        __syncthreads();
+#pragma unroll 1
+        for (int c = 0; c < nc; ++c) {
+            const float dist = l2_lanes8<DP>(x, cs + c * DP);
+            if (dist < best) {
+                best = dist;
+                arg = c0 + c;
+            }
+        }
+    }
+    if (valid) {
+        a.labels[static_cast<int64_t>(seg) * a.T + t] = arg;
+        if (a.mind) a.mind[static_cast<int64_t>(seg) * a.T + t] = best;
+    }
+    if (a.hist == nullptr) return;
     float part = wave_sum(valid ? best : 0.0f);
     if (lane_id() == 0) red[tid >> 6] = part;
     const int r = block_digit_rank(arg, valid, k, bits_for(k), wcnt,
@@ -447,9 +522,11 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
 // block scan; otherwise one thread replays the sequential loops.
 struct PpDraws {
     int32_t first;
+    int32_t c0, c1;      // picks c0 .. c1 - 1 in this launch (c0 >= 1)
     int32_t pad;
-    double canon[256];   // canon[c] for pick c (index 0 unused)
+    double canon[256];   // canon[c - c0] for pick c
 };
+constexpr int kPpChunk = 256;   // picks per launch
 
 __device__ __forceinline__ long long pp_units(float m, int emin_eff) {
     const uint32_t u = __float_as_uint(m);
@@ -460,14 +537,14 @@ __device__ __forceinline__ long long pp_units(float m, int emin_eff) {
 }
 
 template <int DP>
-constexpr int pp_threads() { return DP == 64 ? 512 : 1024; }   // keeps x[DP] in registers
+constexpr int pp_threads() { return DP == 128 ? 256 : (DP == 64 ? 512 : 1024); }   // keeps x[DP] in registers
 
 template <int DP>
 __global__ __launch_bounds__(pp_threads<DP>()) void km_pp_kernel(KmParams a, int p, PpDraws dr) {
     constexpr int TPB = pp_threads<DP>();
     constexpr int NW = TPB / 64;
     __shared__ __attribute__((aligned(16))) float cur[DP];
-    __shared__ int s_emin, s_emax, s_sel;
+    __shared__ int s_emin, s_emax, s_sel[2];
     __shared__ long long s_part[NW];
     const int h = blockIdx.x, tid = threadIdx.x;
     const int seg = h * a.P + p;
@@ -475,21 +552,29 @@ __global__ __launch_bounds__(pp_threads<DP>()) void km_pp_kernel(KmParams a, int
     float* md = reinterpret_cast<float*>(a.rank) + static_cast<int64_t>(seg) * T;
     float* cent = a.cent + static_cast<int64_t>(seg) * a.kmax * DP;
     const uint16_t* xb = a.keys + static_cast<int64_t>(h) * a.hs + p * DP;
-    if (tid < DP) {
-        const float v = bf16_to_f32(xb[static_cast<int64_t>(dr.first) * a.ts + tid]);
-        cur[tid] = v;
-        cent[tid] = v;
+    if (dr.c0 == 1) {   // first launch: the first pick, no distances yet
+        if (tid < DP) {
+            const float v = bf16_to_f32(xb[static_cast<int64_t>(dr.first) * a.ts + tid]);
+            cur[tid] = v;
+            cent[tid] = v;
+        }
+        for (int i = tid; i < T; i += TPB) md[i] = 3.402823466e38f;
+    } else if (tid < DP) {   // later launches: the previous pick, distances in md
+        cur[tid] = cent[static_cast<int64_t>(dr.c0 - 1) * DP + tid];
     }
-    for (int i = tid; i < T; i += TPB) md[i] = 3.402823466e38f;
     const int chunk = (T + TPB - 1) / TPB;
     const int i0 = tid * chunk, i1 = min(T, i0 + chunk);
     int logT = 0;
     while ((1ll << logT) < static_cast<long long>(T)) ++logT;
-    for (int c = 1; c < k; ++c) {
+    // s_sel alternates by pick: the waves that read pick c's selection after
+    // the last barrier of its iteration may still be reading it while thread 0
+    // resets the slot of pick c + 1
+    for (int c = dr.c0; c < dr.c1 && c < k; ++c) {
+        const int sb = c & 1;
         if (tid == 0) {
             s_emin = 0x7FFFFFFF;
             s_emax = 0;
-            s_sel = T;
+            s_sel[sb] = T;
         }
         __syncthreads();   // cur, md and the LDS scalars are ready
         int emin = 0x7FFFFFFF, emax = 0;
@@ -544,20 +629,20 @@ __global__ __launch_bounds__(pp_threads<DP>()) void km_pp_kernel(KmParams a, int
             }
             const double scale = ldexp(1.0, emin_eff - 150);
             const double total = static_cast<double>(total_u) * scale;
-            const double target = dr.canon[c] * total + 0.0;
+            const double target = dr.canon[c - dr.c0] * total + 0.0;
             const double tu = target / scale;
             long long run = base + incl - sum;
             for (int i = i0; i < i1; ++i) {
                 run += pp_units(md[i], emin_eff);
                 if (static_cast<double>(run) >= tu) {
-                    atomicMin(&s_sel, i);
+                    atomicMin(&s_sel[sb], i);
                     break;
                 }
             }
         } else if (tid == 0) {
             double tw = 0.0;
             for (int i = 0; i < T; ++i) tw += static_cast<double>(md[i]);
-            const double target = dr.canon[c] * tw + 0.0;
+            const double target = dr.canon[c - dr.c0] * tw + 0.0;
             double cs = 0.0;
             int sel = 0;
             for (int i = 0; i < T; ++i) {
@@ -567,11 +652,11 @@ __global__ __launch_bounds__(pp_threads<DP>()) void km_pp_kernel(KmParams a, int
                     break;
                 }
             }
-            s_sel = sel;
+            s_sel[sb] = sel;
         }
         __syncthreads();   // selection known; every read of cur is done
-        if (tid < DP) {   // wave 0 only: tid 0 resets s_sel after these reads
-            const int sel = s_sel < T ? s_sel : 0;
+        if (tid < DP) {
+            const int sel = s_sel[sb] < T ? s_sel[sb] : 0;
             const float v = bf16_to_f32(xb[static_cast<int64_t>(sel) * a.ts + tid]);
             cur[tid] = v;
             cent[static_cast<int64_t>(c) * DP + tid] = v;
@@ -589,7 +674,7 @@ constexpr int kScanRegInts = 64;
 
 __global__ __launch_bounds__(1024) void km_scan_kernel(KmParams a, int it) {
     __shared__ int sh[40];
-    __shared__ int soff[257];
+    __shared__ int soff[kIvfMaxK + 1];
     __shared__ float sred[16];
     __shared__ int stop;
     const int seg = blockIdx.x;
@@ -673,19 +758,24 @@ __global__ __launch_bounds__(1024) void km_scan_kernel(KmParams a, int it) {
         soff[k] = a.T;
     }
     __syncthreads();
-    // empty-cluster ordinals: exclusive count of empty clusters before c
-    // (k <= 256: the first four waves)
-    int empty = 0, eincl = 0;
-    if (wave < 4) {
-        empty = tid < k && soff[tid + 1] == soff[tid] ? 1 : 0;
-        eincl = wave_incl_scan(empty);
-        if ((tid & 63) == 63) sh[32 + wave] = eincl;
-    }
-    __syncthreads();
-    if (wave < 4 && tid < k) {
-        int before = 0;
-        for (int w = 0; w < wave; ++w) before += sh[32 + w];
-        a.empties[static_cast<int64_t>(seg) * a.kmax + tid] = before + eincl - empty;
+    // empty-cluster ordinals: exclusive count of empty clusters before c,
+    // 256 clusters at a time on the first four waves
+    for (int c0 = 0, carry = 0; c0 < k; c0 += 256) {
+        const int c = c0 + tid;
+        int empty = 0, eincl = 0;
+        if (wave < 4) {
+            empty = c < k && soff[c + 1] == soff[c] ? 1 : 0;
+            eincl = wave_incl_scan(empty);
+            if ((tid & 63) == 63) sh[32 + wave] = eincl;
+        }
+        __syncthreads();
+        if (wave < 4 && c < k) {
+            int before = carry;
+            for (int w = 0; w < wave; ++w) before += sh[32 + w];
+            a.empties[static_cast<int64_t>(seg) * a.kmax + c] = before + eincl - empty;
+        }
+        carry += (sh[32] + sh[33]) + (sh[34] + sh[35]);
+        __syncthreads();
     }
     if (tid == 0) {
         float inertia = 0.0f;
@@ -748,7 +838,8 @@ __global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, Draws 
     constexpr int RPL = 64 / PARTS;  // rows per load instruction
     constexpr int LPB = PARTS;       // load instructions per 64-row batch
     constexpr int NL = 3;            // loader waves
-    constexpr int NB = 4;            // local batches in flight per loader
+    constexpr int NB = DP > 64 ? 2 : 4;   // local batches in flight per loader (register ring)
+    constexpr int HALVES = DP > 64 ? DP / 64 : 1;   // dims per chain lane
     __shared__ km_u32x4_t ring[2 * NL][64 * PARTS];
     const int c = blockIdx.x, seg = blockIdx.y;
     const int h = seg / a.P, p = seg % a.P;
@@ -760,10 +851,11 @@ __global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, Draws 
     const uint16_t* kbase = a.keys + h * a.hs + p * DP;
     float* dst = a.cent + (static_cast<int64_t>(seg) * a.kmax + c) * DP;
     if (hi == lo) {
-        if (wave == 0 && lane < DP) {
-            const int e = a.empties[static_cast<int64_t>(seg) * a.kmax + c];
+        // empty ordinals past this launch's draws: km_reseed_kernel
+        const int e = a.empties[static_cast<int64_t>(seg) * a.kmax + c];
+        if (wave == 0 && e < kDraws) {
             const int tok = draws.v[e];
-            dst[lane] = bf16_to_f32(kbase[static_cast<int64_t>(tok) * a.ts + lane]);
+            for (int d = lane; d < DP; d += 64) dst[d] = bf16_to_f32(kbase[static_cast<int64_t>(tok) * a.ts + d]);
         }
         return;
     }
@@ -823,7 +915,9 @@ __global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, Draws 
 #undef KMB_ID
 #undef KMB_ROWS
     } else {
-        float acc = 0.0f;
+        float acc[HALVES];
+#pragma unroll
+        for (int hh = 0; hh < HALVES; ++hh) acc[hh] = 0.0f;
 #pragma unroll 1
         for (int q = 0; q < rounds_pad; ++q) {
             __syncthreads();   // round q's slots are filled
@@ -839,30 +933,57 @@ __global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, Draws 
                         // block of members 4i..4i+3, dims 16 (g % (DP/16)) ..
                         // +15, so lane d holds dim d of four consecutive
                         // members per read (lanes >= DP read a copy and are
-                        // not stored); all 16 reads in flight at once
+                        // not stored); all 16 reads in flight at once.  DP =
+                        // 128: a second pass over dims 64..127.
                         const int lg = lane >> 4, ln = lane & 15;
-                        const uint16_t* base = rows + (ln >> 2) * DP + 16 * (lg % (DP / 16)) + 4 * (ln & 3);
-                        km_u32x2_t w[16];
 #pragma unroll
-                        for (int i = 0; i < 16; ++i)
-                            w[i] = __builtin_bit_cast(
-                                km_u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                                (km_lds_s16x4_t*)(base + 4 * i * DP)));
+                        for (int hh = 0; hh < HALVES; ++hh) {
+                            const uint16_t* base =
+                                rows + (ln >> 2) * DP + 64 * hh + 16 * (lg % (DP / 16)) + 4 * (ln & 3);
+                            km_u32x2_t w[16];
 #pragma unroll
-                        for (int i = 0; i < 16; ++i) {
-                            acc = acc + __uint_as_float(w[i][0] << 16);
-                            acc = acc + __uint_as_float(w[i][0] & 0xFFFF0000u);
-                            acc = acc + __uint_as_float(w[i][1] << 16);
-                            acc = acc + __uint_as_float(w[i][1] & 0xFFFF0000u);
+                            for (int i = 0; i < 16; ++i)
+                                w[i] = __builtin_bit_cast(
+                                    km_u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                    (km_lds_s16x4_t*)(base + 4 * i * DP)));
+#pragma unroll
+                            for (int i = 0; i < 16; ++i) {
+                                acc[hh] = acc[hh] + __uint_as_float(w[i][0] << 16);
+                                acc[hh] = acc[hh] + __uint_as_float(w[i][0] & 0xFFFF0000u);
+                                acc[hh] = acc[hh] + __uint_as_float(w[i][1] << 16);
+                                acc[hh] = acc[hh] + __uint_as_float(w[i][1] & 0xFFFF0000u);
+                            }
                         }
-                    } else if (lane < DP) {
-                        for (int r = 0; r < cnt; ++r) acc = acc + bf16_to_f32(rows[r * DP + lane]);
+                    } else {
+#pragma unroll
+                        for (int hh = 0; hh < HALVES; ++hh)
+                            if (64 * hh + lane < DP)
+                                for (int r = 0; r < cnt; ++r)
+                                    acc[hh] = acc[hh] + bf16_to_f32(rows[r * DP + 64 * hh + lane]);
                     }
                 }
             }
         }
-        if (lane < DP) dst[lane] = acc * (1.0f / static_cast<float>(n));
+#pragma unroll
+        for (int hh = 0; hh < HALVES; ++hh)
+            if (64 * hh + lane < DP) dst[64 * hh + lane] = acc[hh] * (1.0f / static_cast<float>(n));
     }
+}
+
+// Empty clusters whose ordinal falls in [e0, e0 + kDraws): the draws of
+// that slice (clusters beyond kDraws empty ones only occur when k > kDraws).
+__global__ __launch_bounds__(64) void km_reseed_kernel(KmParams a, Draws draws, int e0) {
+    const int c = blockIdx.x, seg = blockIdx.y;
+    const int h = seg / a.P, p = seg % a.P;
+    if (c >= a.k[p]) return;
+    if (a.done && a.done[seg]) return;
+    const int32_t* off = a.off + static_cast<int64_t>(seg) * (a.kmax + 1);
+    if (off[c + 1] != off[c]) return;
+    const int e = a.empties[static_cast<int64_t>(seg) * a.kmax + c] - e0;
+    if (e < 0 || e >= kDraws) return;
+    const uint16_t* row = a.keys + h * a.hs + p * a.DP + static_cast<int64_t>(draws.v[e]) * a.ts;
+    float* dst = a.cent + (static_cast<int64_t>(seg) * a.kmax + c) * a.DP;
+    for (int d = threadIdx.x; d < a.DP; d += 64) dst[d] = bf16_to_f32(row[d]);
 }
 
 __global__ void km_reset_kernel(KmParams a) {
@@ -878,18 +999,19 @@ int validate(const imi_kmeans_args* a, int& kmax, int& dp) {
     IMI_REQUIRE(a->keys && a->centroids && a->labels, IMI_ERR_INVALID, "imi_kmeans: null pointer argument");
     IMI_REQUIRE(a->kv_heads > 0 && a->n_tokens > 0, IMI_ERR_INVALID, "imi_kmeans: empty input (H=%d T=%d)",
                 a->kv_heads, a->n_tokens);
-    IMI_REQUIRE(a->parts == 2 || a->parts == 4, IMI_ERR_UNSUPPORTED, "imi_kmeans: parts must be 2 or 4 (got %d)",
-                a->parts);
+    IMI_REQUIRE(a->parts == 1 || a->parts == 2 || a->parts == 4, IMI_ERR_UNSUPPORTED,
+                "imi_kmeans: parts must be 1 (IVF), 2 or 4 (got %d)", a->parts);
     IMI_REQUIRE(a->dim % a->parts == 0, IMI_ERR_INVALID, "imi_kmeans: dim %d not divisible by parts %d", a->dim,
                 a->parts);
     dp = a->dim / a->parts;
-    IMI_REQUIRE(dp == 32 || dp == 64, IMI_ERR_UNSUPPORTED, "imi_kmeans: subspace width %d unsupported (32 or 64)",
-                dp);
+    IMI_REQUIRE(dp == 32 || dp == 64 || (a->parts == 1 && dp == 128), IMI_ERR_UNSUPPORTED,
+                "imi_kmeans: subspace width %d unsupported (32 or 64; 128 for IVF)", dp);
     IMI_REQUIRE(a->max_iters >= 1, IMI_ERR_INVALID, "imi_kmeans: max_iters must be >= 1");
+    const int kcap = a->parts == 1 ? kIvfMaxK : 256;
     kmax = 0;
     for (int p = 0; p < a->parts; ++p) {
-        IMI_REQUIRE(a->k[p] >= 1 && a->k[p] <= 256, IMI_ERR_UNSUPPORTED, "imi_kmeans: k[%d]=%d outside [1,256]", p,
-                    a->k[p]);
+        IMI_REQUIRE(a->k[p] >= 1 && a->k[p] <= kcap, IMI_ERR_UNSUPPORTED, "imi_kmeans: k[%d]=%d outside [1,%d]", p,
+                    a->k[p], kcap);
         kmax = a->k[p] > kmax ? a->k[p] : kmax;
     }
     IMI_REQUIRE(a->init_mode >= 0 && a->init_mode <= 2, IMI_ERR_INVALID,
@@ -944,6 +1066,15 @@ int run_screen(const KmParams& p, int segs, hipStream_t stream) {
 
 template <int DP>
 int run_assign(const KmParams& p, int segs, hipStream_t stream) {
+    if constexpr (DP == 128) {
+        const size_t lds = tiled_lds_bytes<DP>(p.kmax);
+        if (lds > 64 * 1024)
+            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_assign_tiled_kernel<DP>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+        hipLaunchKernelGGL(km_assign_tiled_kernel<DP>, dim3(p.nblk, segs), dim3(256), lds, stream, p);
+        IMI_LAUNCH_CHECK("km_assign_tiled_kernel");
+        return IMI_OK;
+    }
     if (p.kmax <= kScreenMaxK) {
         bool same = true;   // every subspace has kmax centroids
         for (int q = 0; q < p.P; ++q) same = same && p.k[q] == p.kmax;
@@ -1028,22 +1159,35 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
     } else if (a->init_mode == 2) {
         // kmeans++ seeds 42, 43, 44, 45 by subspace, the same for every head
         // (kmeans_core.cpp:459, 469)
+        // (IVF: seed 42, kmeans_core.cpp:548-556); picks in launches of
+        // kPpChunk, the distances carried over in the workspace
         for (int part = 0; part < a->parts; ++part) {
             PpDraws dr{};
             std::mt19937_64 rng(static_cast<uint64_t>(42 + part));
             std::uniform_int_distribution<int32_t> first(0, a->n_tokens - 1);
             dr.first = first(rng);
-            for (int c = 1; c < a->k[part]; ++c)
-                dr.canon[c] = std::generate_canonical<double, std::numeric_limits<double>::digits>(rng);
-            if (dp == 64)
-                hipLaunchKernelGGL(km_pp_kernel<64>, dim3(a->kv_heads), dim3(pp_threads<64>()), 0, stream, p, part, dr);
-            else
-                hipLaunchKernelGGL(km_pp_kernel<32>, dim3(a->kv_heads), dim3(pp_threads<32>()), 0, stream, p, part, dr);
-            IMI_LAUNCH_CHECK("km_pp_kernel");
+            const int kp = a->k[part];
+            for (int c0 = 1; c0 == 1 || c0 < kp; c0 += kPpChunk) {
+                dr.c0 = c0;
+                dr.c1 = std::min(kp, c0 + kPpChunk);
+                for (int c = c0; c < dr.c1; ++c)
+                    dr.canon[c - c0] = std::generate_canonical<double, std::numeric_limits<double>::digits>(rng);
+                if (dp == 128)
+                    hipLaunchKernelGGL(km_pp_kernel<128>, dim3(a->kv_heads), dim3(pp_threads<128>()), 0, stream, p,
+                                       part, dr);
+                else if (dp == 64)
+                    hipLaunchKernelGGL(km_pp_kernel<64>, dim3(a->kv_heads), dim3(pp_threads<64>()), 0, stream, p,
+                                       part, dr);
+                else
+                    hipLaunchKernelGGL(km_pp_kernel<32>, dim3(a->kv_heads), dim3(pp_threads<32>()), 0, stream, p,
+                                       part, dr);
+                IMI_LAUNCH_CHECK("km_pp_kernel");
+            }
         }
     }
     for (int it = 0; it < a->max_iters; ++it) {
-        rc = dp == 64 ? run_assign<64>(p, segs, stream) : run_assign<32>(p, segs, stream);
+        rc = dp == 128 ? run_assign<128>(p, segs, stream)
+                       : (dp == 64 ? run_assign<64>(p, segs, stream) : run_assign<32>(p, segs, stream));
         if (rc) return rc;
         hipLaunchKernelGGL(km_scan_kernel, dim3(segs), dim3(1024), 0, stream, p, it);
         IMI_LAUNCH_CHECK("km_scan_kernel");
@@ -1056,12 +1200,20 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
         Draws dr;
         std::mt19937 rng(static_cast<unsigned>(it + 12345));
         std::uniform_int_distribution<int32_t> dist(0, a->n_tokens - 1);
-        for (int e = 0; e < kmax; ++e) dr.v[e] = dist(rng);
-        if (dp == 64)
+        for (int e = 0; e < std::min(kmax, kDraws); ++e) dr.v[e] = dist(rng);
+        if (dp == 128)
+            hipLaunchKernelGGL(km_update_block_kernel<128>, dim3(kmax, segs), dim3(256), 0, stream, p, dr);
+        else if (dp == 64)
             hipLaunchKernelGGL(km_update_block_kernel<64>, dim3(kmax, segs), dim3(256), 0, stream, p, dr);
         else
             hipLaunchKernelGGL(km_update_block_kernel<32>, dim3(kmax, segs), dim3(256), 0, stream, p, dr);
         IMI_LAUNCH_CHECK("km_update_block_kernel");
+        // the draws of empty ordinals kDraws and up (IVF, k > kDraws)
+        for (int e0 = kDraws; e0 < kmax; e0 += kDraws) {
+            for (int e = e0; e < std::min(kmax, e0 + kDraws); ++e) dr.v[e - e0] = dist(rng);
+            hipLaunchKernelGGL(km_reseed_kernel, dim3(kmax, segs), dim3(64), 0, stream, p, dr, e0);
+            IMI_LAUNCH_CHECK("km_reseed_kernel");
+        }
     }
     return IMI_OK;
 }
@@ -1102,5 +1254,6 @@ extern "C" int imi_kmeans_assign(const uint16_t* keys, int64_t head_stride, int6
     p.mind = mind;
     p.nblk = (n_tokens + 255) / 256;
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    if (dp == 128) return run_assign<128>(p, kv_heads * parts, stream);
     return dp == 64 ? run_assign<64>(p, kv_heads * parts, stream) : run_assign<32>(p, kv_heads * parts, stream);
 }

@@ -22,6 +22,7 @@
 //                      kernel of one cell per thread and many workgroups
 //                      per head, a histogram, the candidates, the ranks and
 //                      budgets in one workgroup per head.
+// An IVF index (parts = 1) always takes the ranking pipeline.
 #include "imi_common.hpp"
 
 namespace imi {
@@ -765,8 +766,8 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     IMI_REQUIRE(a->groups <= kMaxGroups, IMI_ERR_UNSUPPORTED, "imi_select: %d query heads per kv head exceed %d",
                 a->groups, kMaxGroups);
     IMI_REQUIRE(a->dim == 128, IMI_ERR_UNSUPPORTED, "imi_select: head_dim must be 128");
-    IMI_REQUIRE(a->parts == 2 || a->parts == 4, IMI_ERR_UNSUPPORTED, "imi_select: parts must be 2 or 4 (got %d)",
-                a->parts);
+    IMI_REQUIRE(a->parts == 1 || a->parts == 2 || a->parts == 4, IMI_ERR_UNSUPPORTED,
+                "imi_select: parts must be 1 (IVF), 2 or 4 (got %d)", a->parts);
     if (a->ring_cap != 0) {
         IMI_REQUIRE(a->ring_cap > 0 && a->ring_cap <= kRingCap, IMI_ERR_UNSUPPORTED,
                     "imi_select: ring_cap %d outside [1, %d]", a->ring_cap, kRingCap);
@@ -777,12 +778,12 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     if (a->upd_slot)
         IMI_REQUIRE(a->shadow && a->upd_row && a->upd_n && a->shadow_rows > 0, IMI_ERR_INVALID,
                     "imi_select: replaced centroids need shadow, shadow_rows, upd_row and upd_n");
-    if (a->parts == 4) {
+    if (a->parts != 2) {
         IMI_REQUIRE(a->page_size > 0 && a->nprobe > 0 && a->max_tokens > 0 && a->buffer_pages > 0, IMI_ERR_INVALID,
                     "imi_select: budgets must be positive");
         kmax = 0;
         ncells = 1;
-        for (int p = 0; p < 4; ++p) {
+        for (int p = 0; p < a->parts; ++p) {
             kmax = a->k[p] > kmax ? a->k[p] : kmax;
             ncells *= a->k[p];
         }

@@ -57,6 +57,7 @@ constexpr int kTripCap = 4096;   // (l0, l1, l2) prefixes a score workgroup keep
 constexpr int kCellsPerBlock = kScore4Threads * kCPT;
 constexpr int kDenseScoreCells = kScoreThreads;   // 2-way score kernel: one global cell per thread
 constexpr int kDenseK = 256;                      // 2-way centroids per subspace the score kernel reads
+constexpr int kIvfMaxK = 4096;                    // IVF clusters per head
 constexpr int kLocBins = 1024;   // buckets of a score workgroup's own candidate cut
 constexpr int kFinalCPT = 16;    // candidates per thread the final kernel holds in registers
 constexpr int kMaxSeg = 1024;    // score workgroups per head the final kernel reads (candidate segments)
@@ -79,7 +80,7 @@ struct Sel4 {
     const int32_t* coff;     // [H][cap + 1]
     const int32_t* nact;     // [H]
     int cap;                 // cells listed per head (keys [H][cap])
-    int dense;               // 2-way: every global cell listed (cell index = id, n_active = cap, key 0 = empty)
+    int dense;               // 2-way and IVF: every global cell listed (cell index = id, n_active = cap, key 0 = empty)
     int nprobe, max_tokens, buffer_pages, page_size;
     const int32_t* head_max_tokens;    // [H] or null
     const int32_t* head_buffer_pages;  // [H] or null
@@ -603,6 +604,55 @@ __global__ __launch_bounds__(kScoreThreads) void sel2_dense_score_kernel(Sel4 a)
             acc = __builtin_fmaf(qq.w, v.w, acc);
         }
         sc = acc;
+    }
+    const uint64_t kv[1] = {in && cnt > 0 ? (static_cast<uint64_t>(order_key(sc)) << 32) |
+                                                (0xFFFFFFFFu - static_cast<uint32_t>(g))
+                                          : 0ull};
+    const int ci[1] = {g};
+    emit_candidates<kScoreThreads, 1>(a, h, kprime(a, h, ncells), kv, ci, lh);
+}
+
+// IVF (one 128-dim space): one cluster per thread, the 128-term chain of
+// compute_impl.cu:80-101 over its centroid, keys as in
+// sel2_dense_score_kernel (0 for an empty cluster).
+__global__ __launch_bounds__(kScoreThreads) void sel1_score_kernel(Sel4 a) {
+    __shared__ __attribute__((aligned(16))) float qs[128];
+    __shared__ int lh[kLocBins];   // the candidate cut's buckets
+    const int h = blockIdx.y, tid = threadIdx.x;
+    const int ncells = a.cap;
+    const int g = blockIdx.x * kDenseScoreCells + tid;
+    const bool in = g < ncells;
+    // ---- loads, all issued before the first wait ----
+    uint16_t qv[kMaxG4];
+    if (tid < 128) {
+        // rows past G re-read row G - 1 and are dropped from the sum
+        const uint16_t* qh = a.q + static_cast<int64_t>(h) * a.G * 128;
+#pragma unroll
+        for (int j = 0; j < kMaxG4; ++j) qv[j] = qh[min(j, a.G - 1) * 128 + tid];
+    }
+    const float4* cr =
+        reinterpret_cast<const float4*>(a.cent + (static_cast<int64_t>(h) * a.kmax + (in ? g : 0)) * 128);
+    float4 r[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) r[i] = cr[i];
+    const int cnt = in ? a.csize[static_cast<int64_t>(h) * ncells + g] : 0;
+    if (tid < 128) {
+        float acc = 0.0f;   // grouped-query sum, g ascending (compute_impl.cu:80-87)
+#pragma unroll
+        for (int j = 0; j < kMaxG4; ++j)
+            if (j < a.G) acc += bf16_to_f32(qv[j]);
+        qs[tid] = acc;
+    }
+    for (int i = tid; i < kLocBins; i += kScoreThreads) lh[i] = 0;
+    __syncthreads();
+    float sc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const float4 qq = *reinterpret_cast<const float4*>(qs + 4 * i);
+        sc = __builtin_fmaf(qq.x, r[i].x, sc);
+        sc = __builtin_fmaf(qq.y, r[i].y, sc);
+        sc = __builtin_fmaf(qq.z, r[i].z, sc);
+        sc = __builtin_fmaf(qq.w, r[i].w, sc);
     }
     const uint64_t kv[1] = {in && cnt > 0 ? (static_cast<uint64_t>(order_key(sc)) << 32) |
                                                 (0xFFFFFFFFu - static_cast<uint32_t>(g))
@@ -1144,8 +1194,8 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
 size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
     Carver cv(a->workspace);
     const size_t H = a->kv_heads;
-    const bool dense = a->parts == 2;
-    const int cap = dense ? a->k[0] * a->k[1] : a->compact_cap;
+    const bool dense = a->parts <= 2;
+    const int cap = a->parts == 1 ? a->k[0] : (dense ? a->k[0] * a->k[1] : a->compact_cap);
     const int region = dense ? kDenseScoreCells : kCellsPerBlock;
     const int nbs = (cap + region - 1) / region;
     // every score workgroup writes its count and range each call, and the
@@ -1170,16 +1220,23 @@ size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
 }  // namespace
 
 // The ranking pipeline: 4-way over the occupied cells, or (parts = 2) a 2-way
-// IMI over every global cell beyond the one-kernel selection's bounds.
+// IMI over every global cell beyond the one-kernel selection's bounds, or
+// (parts = 1) the IVF clusters.
 int select4_validate(const imi_select_args* a) {
-    const bool dense = a->parts == 2;
+    const bool dense = a->parts == 1 || a->parts == 2;
     IMI_REQUIRE(a->dim == 128 && (a->parts == 4 || dense), IMI_ERR_UNSUPPORTED,
-                "imi_select: the ranking pipeline needs D=128 and parts 2 or 4");
+                "imi_select: the ranking pipeline needs D=128 and parts 1, 2 or 4");
     IMI_REQUIRE(a->kv_heads <= kExtHeads, IMI_ERR_UNSUPPORTED, "imi_select: at most %d KV heads per call", kExtHeads);
     IMI_REQUIRE(a->groups >= 1 && a->groups <= kMaxG4, IMI_ERR_UNSUPPORTED,
                 "imi_select: %d query heads per kv head exceed %d", a->groups, kMaxG4);
     int64_t cells_max;
-    if (dense) {
+    if (a->parts == 1) {
+        IMI_REQUIRE(a->k[0] >= 1 && a->k[0] <= kIvfMaxK, IMI_ERR_UNSUPPORTED, "imi_select: IVF k=%d outside [1,%d]",
+                    a->k[0], kIvfMaxK);
+        IMI_REQUIRE(!a->upd_slot && a->ring_cap == 0, IMI_ERR_UNSUPPORTED,
+                    "imi_select: the online index update is not available for IVF");
+        cells_max = a->k[0];
+    } else if (dense) {
         for (int p = 0; p < 2; ++p)
             IMI_REQUIRE(a->k[p] >= 1 && a->k[p] <= kDenseK, IMI_ERR_UNSUPPORTED,
                         "imi_select: 2-way k[%d]=%d outside [1,%d]", p, a->k[p], kDenseK);
@@ -1263,7 +1320,10 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     p.delta_rows = a->delta_rows;
     p.n_delta = a->n_delta;
     const bool online = p.upd_slot || p.ring_cap > 0;
-    if (dense) {
+    if (a->parts == 1) {
+        hipLaunchKernelGGL(sel1_score_kernel, dim3(p.nbs, a->kv_heads), dim3(kScoreThreads), 0, stream, p);
+        IMI_LAUNCH_CHECK("sel1_score_kernel");
+    } else if (dense) {
         const dim3 grid_s(p.nbs, a->kv_heads);
         if (p.upd_slot)
             hipLaunchKernelGGL((sel2_dense_score_kernel<true>), grid_s, dim3(kScoreThreads), 0, stream, p);

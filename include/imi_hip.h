@@ -14,7 +14,8 @@
  *   centroids    fp32 [H][P][kmax][Dp]   (subspace centroids)
  *   labels       int32 [H][P][T]          (subspace labels)
  *   cell index   global cell id g = ((l0 * k1 + l1) * k2 + l2) * k3 + l3
- *                (mixed radix, reorganize_core.cpp:33-35, 112-118)
+ *                (mixed radix, reorganize_core.cpp:33-35, 112-118); IVF
+ *                (P = 1, Dp = D): g = the cluster label
  *   cell_count / cell_offset   int32 [H][ncells] / [H][ncells + 1]: CSR over
  *                global cell ids (empty cells have count 0)
  *   list_keys / list_values    bf16 [H][list_stride_rows][D]: rows in CSR order
@@ -65,8 +66,10 @@ typedef struct {
     int32_t kv_heads;         /* H */
     int32_t n_tokens;         /* T */
     int32_t dim;              /* D (128) */
-    int32_t parts;            /* P: 2 or 4 (IMI subspaces) */
-    int32_t k[4];             /* centroids per subspace, each in [1, 256] */
+    int32_t parts;            /* P: 2 or 4 (IMI subspaces), or 1 (IVF: one
+                                 128-dim space, kmeans_core.cpp:503-595) */
+    int32_t k[4];             /* centroids per subspace, each in [1, 256]
+                                 (IVF: [1, 4096]) */
     int32_t max_iters;        /* >= 1 */
     float tol;                /* absolute inertia tolerance */
     int32_t early_stop_min_iter; /* early stop disabled when > max_iters */

@@ -52,7 +52,7 @@ def test_cache_rejects_what_the_reference_rejects():
     with pytest.raises(ValueError, match="input length"):
         _cache(input_length=0)
     with pytest.raises(NotImplementedError, match="IVF"):
-        _cache(subspace_parts=0)
+        _cache(subspace_parts=0, runtime_config={"async_update": {"enabled": True}})
 
 
 def test_async_update_config():
@@ -121,7 +121,7 @@ def _bits(t):
 
 @pytest.mark.gpu
 @pytest.mark.skipif(not gpu_available(), reason="needs a HIP device")
-@pytest.mark.parametrize("ks", [(32, 32), (6, 6, 6, 6), (8, 8, 8, 8)])
+@pytest.mark.parametrize("ks", [(32, 32), (6, 6, 6, 6), (8, 8, 8, 8), (375,)])   # (375,): IVF, k = round(6000 / 16)
 def test_model_shaped_prefill_and_decode_match_oracle(ks):
     from adaptiveimi_amd import synthetic
     from adaptiveimi_amd.attn_hub.sparse_imi import imi_decode_attn
@@ -131,7 +131,8 @@ def test_model_shaped_prefill_and_decode_match_oracle(ks):
     L, S, H, G, D = 2, 6096, 8, 4, 128
     kcfg = {f"k{i + 1}": k for i, k in enumerate(ks)}
     kcfg.update(max_iters=6, early_stop_min_iter=6, init="first")
-    cache = _cache(layer_mapping={"0": DEV, "1": DEV}, subspace_parts=len(ks), runtime_config={"kmeans": kcfg})
+    cache = _cache(layer_mapping={"0": DEV, "1": DEV}, subspace_parts=len(ks) if len(ks) > 1 else 0,
+                   runtime_config={"kmeans": kcfg})
     kv = []
     for layer in range(L):
         k, v = synthetic.make_kv(H, S + 2, seed=40 + layer)
