@@ -106,6 +106,34 @@ __device__ __forceinline__ float l2_lanes8(const float (&x)[DP], const float* cr
     return t;
 }
 
+// The same distance with the row still in its bf16 load registers (each
+// 16-byte part holds dims i .. i+7 of lanes 0..7): no float copy of the row,
+// for kernels that keep many rows in flight.
+template <int DP>
+__device__ __forceinline__ float l2_lanes8_bf16(const uint4 (&v)[DP / 8], const float* cr) {
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < DP / 8; ++i) {
+        const float4 c0 = *reinterpret_cast<const float4*>(cr + 8 * i);
+        const float4 c1 = *reinterpret_cast<const float4*>(cr + 8 * i + 4);
+        float d;
+        d = bf16_lo(v[i].x) - c0.x; acc[0] = __builtin_fmaf(d, d, acc[0]);
+        d = bf16_hi(v[i].x) - c0.y; acc[1] = __builtin_fmaf(d, d, acc[1]);
+        d = bf16_lo(v[i].y) - c0.z; acc[2] = __builtin_fmaf(d, d, acc[2]);
+        d = bf16_hi(v[i].y) - c0.w; acc[3] = __builtin_fmaf(d, d, acc[3]);
+        d = bf16_lo(v[i].z) - c1.x; acc[4] = __builtin_fmaf(d, d, acc[4]);
+        d = bf16_hi(v[i].z) - c1.y; acc[5] = __builtin_fmaf(d, d, acc[5]);
+        d = bf16_lo(v[i].w) - c1.z; acc[6] = __builtin_fmaf(d, d, acc[6]);
+        d = bf16_hi(v[i].w) - c1.w; acc[7] = __builtin_fmaf(d, d, acc[7]);
+    }
+    float t = acc[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) t = t + acc[j];
+    return t;
+}
+
 // E-step over one block of 256 tokens of one segment.
 template <int DP>
 __global__ __launch_bounds__(256) void km_assign_kernel(KmParams a) {
@@ -537,7 +565,7 @@ __device__ __forceinline__ long long pp_units(float m, int emin_eff) {
 }
 
 template <int DP>
-constexpr int pp_threads() { return DP == 128 ? 256 : (DP == 64 ? 512 : 1024); }   // keeps x[DP] in registers
+constexpr int pp_threads() { return DP == 32 ? 1024 : 512; }   // keeps x[DP] (DP = 128: the raw row) in registers
 
 template <int DP>
 __global__ __launch_bounds__(pp_threads<DP>()) void km_pp_kernel(KmParams a, int p, PpDraws dr) {
@@ -578,18 +606,27 @@ __global__ __launch_bounds__(pp_threads<DP>()) void km_pp_kernel(KmParams a, int
         }
         __syncthreads();   // cur, md and the LDS scalars are ready
         int emin = 0x7FFFFFFF, emax = 0;
+#pragma unroll 1
         for (int i = tid; i < T; i += TPB) {
-            float x[DP];
             const uint16_t* row = xb + static_cast<int64_t>(i) * a.ts;
+            float dist;
+            if constexpr (DP == 128) {
+                uint4 v[DP / 8];
 #pragma unroll
-            for (int d = 0; d < DP; d += 8) {
-                const uint4 v = *reinterpret_cast<const uint4*>(row + d);
-                x[d + 0] = bf16_lo(v.x); x[d + 1] = bf16_hi(v.x);
-                x[d + 2] = bf16_lo(v.y); x[d + 3] = bf16_hi(v.y);
-                x[d + 4] = bf16_lo(v.z); x[d + 5] = bf16_hi(v.z);
-                x[d + 6] = bf16_lo(v.w); x[d + 7] = bf16_hi(v.w);
+                for (int d = 0; d < DP / 8; ++d) v[d] = reinterpret_cast<const uint4*>(row)[d];
+                dist = l2_lanes8_bf16<DP>(v, cur);
+            } else {
+                float x[DP];
+#pragma unroll
+                for (int d = 0; d < DP; d += 8) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(row + d);
+                    x[d + 0] = bf16_lo(v.x); x[d + 1] = bf16_hi(v.x);
+                    x[d + 2] = bf16_lo(v.y); x[d + 3] = bf16_hi(v.y);
+                    x[d + 4] = bf16_lo(v.z); x[d + 5] = bf16_hi(v.z);
+                    x[d + 6] = bf16_lo(v.w); x[d + 7] = bf16_hi(v.w);
+                }
+                dist = l2_lanes8<DP>(x, cur);
             }
-            const float dist = l2_lanes8<DP>(x, cur);
             float m = md[i];
             if (dist < m) {
                 m = dist;
