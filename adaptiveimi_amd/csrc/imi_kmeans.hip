@@ -49,6 +49,7 @@ struct KmParams {
     float* prev;       // [seg]
     int32_t* done;     // [seg] or null
     int32_t* iters;    // [seg] or null
+    void* ppstats;     // kmeans++ block statistics [seg][T / kPpRows] (init_mode 2)
     int nblk;
     int max_iters;
     float tol;
@@ -535,170 +536,272 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
 }
 
 // ---------------------------------------------------------------- kmeans++
-// kmeans_plusplus_init_inplace (kmeans_core.cpp:138-186), one workgroup per
-// (head, subspace).  The random draws do not depend on the data: the host
-// replays std::mt19937_64(seed) for the first index
-// (uniform_int_distribution<int32_t>(0, T-1)) and for one
+// kmeans_plusplus_init_inplace (kmeans_core.cpp:138-186) for every (head,
+// subspace) segment at once, two launches per pick.  The random draws do not
+// depend on the data: the host replays std::mt19937_64(seed) for the first
+// index (uniform_int_distribution<int32_t>(0, T-1)) and for one
 // generate_canonical<double, 53> per pick, which is what
 // uniform_real_distribution<double>(0, total) consumes; target = canon *
-// total.  min_dists are updated with the reference distance.  The reference
-// sums them sequentially in double (total, then the running sum that picks
-// the first index with cumsum >= target).  When every value is a multiple
-// of the smallest value's ulp and the total stays below 2^53 such units (the
-// exponent spread is checked per pick), no partial sum rounds, so the
-// sequential doubles equal exact integer prefix sums, computed here with a
-// block scan; otherwise one thread replays the sequential loops.
-struct PpDraws {
-    int32_t first;
-    int32_t c0, c1;      // picks c0 .. c1 - 1 in this launch (c0 >= 1)
-    int32_t pad;
-    double canon[256];   // canon[c - c0] for pick c
-};
-constexpr int kPpChunk = 256;   // picks per launch
+// total.  The reference sums the min distances sequentially in double (the
+// total, then the running sum that picks the first index with cumsum >=
+// target).  When every value is a multiple of the smallest value's ulp and
+// the total stays below 2^53 such units (the exponent spread is checked per
+// pick), no partial sum rounds, so the sequential doubles equal exact
+// integer prefix sums, which any blocking of the rows reproduces; otherwise
+// one thread replays the sequential loops.
+//   km_pp_dist_kernel  (blocks of kPpRows rows x segments): each row's min
+//                      distance to the picks so far (reference distance to
+//                      the previous pick), then the block's exponent range
+//                      and its sum in units of its own smallest exponent
+//   km_pp_pick_kernel  (one workgroup per segment): the segment's range and
+//                      total, the block that reaches the target, the row
+//                      inside it; writes the pick's centroid row
+constexpr int kPpRPT = 4;                 // consecutive rows per thread
+constexpr int kPpRows = 256 * kPpRPT;     // rows per distance block
 
-__device__ __forceinline__ long long pp_units(float m, int emin_eff) {
+struct PpBlock {                 // per (segment, block)
+    unsigned long long units;    // sum of its values in units of 2^(emin - 150)
+    int emin, emax;              // exponent range of its non-zero values (emin = INT_MAX: none)
+};
+
+struct PpPick {
+    int c;                       // pick index
+    int first[4];                // c == 0: the first row, per subspace
+    double canon[4];             // c >= 1: canon of pick c, per subspace
+};
+
+// value m in units of 2^(emin_eff - 150) (m a multiple of that unit when the
+// segment passes the exactness test; shifts past 63 only occur when it fails)
+__device__ __forceinline__ unsigned long long pp_units(float m, int emin_eff) {
     const uint32_t u = __float_as_uint(m);
     const int e = static_cast<int>((u >> 23) & 0xFFu);
-    const long long mant = static_cast<long long>(u & 0x7FFFFFu) | (e > 0 ? (1ll << 23) : 0ll);
-    const int e_eff = e > 0 ? e : 1;
-    return mant << (e_eff - emin_eff);
+    const unsigned long long mant = static_cast<unsigned long long>(u & 0x7FFFFFu) | (e > 0 ? (1ull << 23) : 0ull);
+    const int sh = (e > 0 ? e : 1) - emin_eff;
+    return (mant == 0 || sh < 0 || sh > 63) ? 0ull : mant << sh;
+}
+
+__device__ __forceinline__ int pp_exp(float m) {
+    const int e = static_cast<int>((__float_as_uint(m) >> 23) & 0xFFu);
+    return e > 0 ? e : 1;
+}
+
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ long long wave_incl_scan_ll(long long v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const long long y = __shfl_up(v, o);
+        if (lane_id() >= o) v += y;
+    }
+    return v;
+}
+
+// 256-thread exclusive scan of one long long per thread; the total to all
+__device__ __forceinline__ long long block_excl_scan_ll(long long v, long long* sh, long long& total) {
+    const long long incl = wave_incl_scan_ll(v);
+    const int w = threadIdx.x >> 6;
+    if (lane_id() == 63) sh[w] = incl;
+    __syncthreads();
+    long long base = 0;
+    total = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (j < w) base += sh[j];
+        total += sh[j];
+    }
+    __syncthreads();
+    return base + incl - v;
 }
 
 template <int DP>
-constexpr int pp_threads() { return DP == 32 ? 1024 : 512; }   // keeps x[DP] (DP = 128: the raw row) in registers
+__global__ __launch_bounds__(256) void km_pp_dist_kernel(KmParams a, int c, PpBlock* stats, int nbp) {
+    __shared__ __attribute__((aligned(16))) float cur[DP];
+    __shared__ int s_e[2][4];
+    __shared__ long long s_u[4];
+    const int seg = blockIdx.y, b = blockIdx.x, tid = threadIdx.x;
+    const int h = seg / a.P, p = seg % a.P;
+    if (c >= a.k[p]) return;
+    const int T = a.T;
+    float* md = reinterpret_cast<float*>(a.rank) + static_cast<int64_t>(seg) * T;
+    const uint16_t* xb = a.keys + static_cast<int64_t>(h) * a.hs + p * DP;
+    if (tid < DP / 4)
+        reinterpret_cast<float4*>(cur)[tid] =
+            reinterpret_cast<const float4*>(a.cent + (static_cast<int64_t>(seg) * a.kmax + c - 1) * DP)[tid];
+    const int r0 = b * kPpRows + tid * kPpRPT;
+    float prev[kPpRPT];
+#pragma unroll
+    for (int j = 0; j < kPpRPT; ++j)   // c == 1: no distances yet (FLT_MAX)
+        prev[j] = (c > 1 && r0 + j < T) ? md[r0 + j] : 3.402823466e38f;
+    __syncthreads();   // cur ready
+    float m[kPpRPT];
+    int emin = 0x7FFFFFFF, emax = 0;
+#pragma unroll 1
+    for (int j = 0; j < kPpRPT; ++j) {
+        const int i = min(r0 + j, T - 1);
+        uint4 v[DP / 8];
+        const uint4* row = reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(i) * a.ts);
+#pragma unroll
+        for (int d = 0; d < DP / 8; ++d) v[d] = row[d];
+        const float dist = l2_lanes8_bf16<DP>(v, cur);
+        float mm = prev[j];
+        if (dist < mm) mm = dist;
+        m[j] = r0 + j < T ? mm : 0.0f;
+        if (r0 + j < T) md[r0 + j] = mm;
+        if (m[j] > 0.0f) {
+            emin = min(emin, pp_exp(m[j]));
+            emax = max(emax, pp_exp(m[j]));
+        }
+    }
+    const int w = tid >> 6;
+    emin = wave_min_i(emin);
+    emax = wave_max_i(emax);
+    if (lane_id() == 0) {
+        s_e[0][w] = emin;
+        s_e[1][w] = emax;
+    }
+    __syncthreads();
+    const int be = min(min(s_e[0][0], s_e[0][1]), min(s_e[0][2], s_e[0][3]));
+    const int bx = max(max(s_e[1][0], s_e[1][1]), max(s_e[1][2], s_e[1][3]));
+    unsigned long long u = 0;
+    if (be != 0x7FFFFFFF) {
+#pragma unroll
+        for (int j = 0; j < kPpRPT; ++j) u += pp_units(m[j], be);
+    }
+    const long long us = wave_incl_scan_ll(static_cast<long long>(u));
+    if (lane_id() == 63) s_u[w] = us;
+    __syncthreads();
+    if (tid == 0) {
+        PpBlock o;
+        o.units = static_cast<unsigned long long>(((s_u[0] + s_u[1]) + s_u[2]) + s_u[3]);
+        o.emin = be;
+        o.emax = bx;
+        stats[static_cast<int64_t>(seg) * nbp + b] = o;
+    }
+}
 
 template <int DP>
-__global__ __launch_bounds__(pp_threads<DP>()) void km_pp_kernel(KmParams a, int p, PpDraws dr) {
-    constexpr int TPB = pp_threads<DP>();
-    constexpr int NW = TPB / 64;
-    __shared__ __attribute__((aligned(16))) float cur[DP];
-    __shared__ int s_emin, s_emax, s_sel[2];
-    __shared__ long long s_part[NW];
-    const int h = blockIdx.x, tid = threadIdx.x;
-    const int seg = h * a.P + p;
-    const int T = a.T, k = a.k[p];
-    float* md = reinterpret_cast<float*>(a.rank) + static_cast<int64_t>(seg) * T;
-    float* cent = a.cent + static_cast<int64_t>(seg) * a.kmax * DP;
+__global__ __launch_bounds__(256) void km_pp_pick_kernel(KmParams a, PpPick pk, const PpBlock* stats, int nbp) {
+    __shared__ int s_e[2][4];
+    __shared__ long long s_sc[4];
+    __shared__ int s_blk, s_sel;
+    __shared__ long long s_base;
+    const int seg = blockIdx.x, tid = threadIdx.x;
+    const int h = seg / a.P, p = seg % a.P;
+    const int c = pk.c;
+    if (c >= a.k[p]) return;
+    const int T = a.T;
     const uint16_t* xb = a.keys + static_cast<int64_t>(h) * a.hs + p * DP;
-    if (dr.c0 == 1) {   // first launch: the first pick, no distances yet
-        if (tid < DP) {
-            const float v = bf16_to_f32(xb[static_cast<int64_t>(dr.first) * a.ts + tid]);
-            cur[tid] = v;
-            cent[tid] = v;
-        }
-        for (int i = tid; i < T; i += TPB) md[i] = 3.402823466e38f;
-    } else if (tid < DP) {   // later launches: the previous pick, distances in md
-        cur[tid] = cent[static_cast<int64_t>(dr.c0 - 1) * DP + tid];
-    }
-    const int chunk = (T + TPB - 1) / TPB;
-    const int i0 = tid * chunk, i1 = min(T, i0 + chunk);
-    int logT = 0;
-    while ((1ll << logT) < static_cast<long long>(T)) ++logT;
-    // s_sel alternates by pick: the waves that read pick c's selection after
-    // the last barrier of its iteration may still be reading it while thread 0
-    // resets the slot of pick c + 1
-    for (int c = dr.c0; c < dr.c1 && c < k; ++c) {
-        const int sb = c & 1;
+    int sel;
+    if (c == 0) {
+        sel = pk.first[p];
+    } else {
+        const float* md = reinterpret_cast<const float*>(a.rank) + static_cast<int64_t>(seg) * T;
+        const PpBlock* st = stats + static_cast<int64_t>(seg) * nbp;
         if (tid == 0) {
-            s_emin = 0x7FFFFFFF;
-            s_emax = 0;
-            s_sel[sb] = T;
+            s_blk = nbp;
+            s_sel = T;
         }
-        __syncthreads();   // cur, md and the LDS scalars are ready
+        // this thread's consecutive blocks
+        const int per = (nbp + 255) / 256;
+        const int b0 = min(tid * per, nbp), b1 = min(b0 + per, nbp);
         int emin = 0x7FFFFFFF, emax = 0;
-#pragma unroll 1
-        for (int i = tid; i < T; i += TPB) {
-            const uint16_t* row = xb + static_cast<int64_t>(i) * a.ts;
-            float dist;
-            if constexpr (DP == 128) {
-                uint4 v[DP / 8];
-#pragma unroll
-                for (int d = 0; d < DP / 8; ++d) v[d] = reinterpret_cast<const uint4*>(row)[d];
-                dist = l2_lanes8_bf16<DP>(v, cur);
-            } else {
-                float x[DP];
-#pragma unroll
-                for (int d = 0; d < DP; d += 8) {
-                    const uint4 v = *reinterpret_cast<const uint4*>(row + d);
-                    x[d + 0] = bf16_lo(v.x); x[d + 1] = bf16_hi(v.x);
-                    x[d + 2] = bf16_lo(v.y); x[d + 3] = bf16_hi(v.y);
-                    x[d + 4] = bf16_lo(v.z); x[d + 5] = bf16_hi(v.z);
-                    x[d + 6] = bf16_lo(v.w); x[d + 7] = bf16_hi(v.w);
-                }
-                dist = l2_lanes8<DP>(x, cur);
-            }
-            float m = md[i];
-            if (dist < m) {
-                m = dist;
-                md[i] = m;
-            }
-            if (m > 0.0f) {
-                const int e = static_cast<int>((__float_as_uint(m) >> 23) & 0xFFu);
-                const int ee = e > 0 ? e : 1;
-                emin = min(emin, ee);
-                emax = max(emax, ee);
-            }
+        for (int bb = b0; bb < b1; ++bb) {
+            emin = min(emin, st[bb].emin);
+            emax = max(emax, st[bb].emax);
         }
-        if (emin != 0x7FFFFFFF) atomicMin(&s_emin, emin);
-        if (emax != 0) atomicMax(&s_emax, emax);
-        __syncthreads();   // md complete, exponent range known
-        const int e_lo = s_emin, e_hi = s_emax;
+        const int w = tid >> 6;
+        emin = wave_min_i(emin);
+        emax = wave_max_i(emax);
+        if (lane_id() == 0) {
+            s_e[0][w] = emin;
+            s_e[1][w] = emax;
+        }
+        __syncthreads();
+        const int e_lo = min(min(s_e[0][0], s_e[0][1]), min(s_e[0][2], s_e[0][3]));
+        const int e_hi = max(max(s_e[1][0], s_e[1][1]), max(s_e[1][2], s_e[1][3]));
+        int logT = 0;
+        while ((1ll << logT) < static_cast<long long>(T)) ++logT;
         const bool any = e_lo != 0x7FFFFFFF;
         const bool exact = !any || (e_hi - e_lo) + 24 + logT <= 53;
         if (exact) {
             const int emin_eff = any ? e_lo : 1;
-            long long sum = 0;
-            for (int i = i0; i < i1; ++i) sum += pp_units(md[i], emin_eff);
-            // block exclusive scan of the chunk sums (thread order = index order)
-            long long incl = sum;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const long long y = __shfl_up(incl, o);
-                if (lane_id() >= o) incl += y;
-            }
-            const int w = tid >> 6;
-            if (lane_id() == 63) s_part[w] = incl;
-            __syncthreads();
-            long long base = 0, total_u = 0;
-            for (int j = 0; j < NW; ++j) {
-                if (j < w) base += s_part[j];
-                total_u += s_part[j];
-            }
+            long long mine = 0;
+            for (int bb = b0; bb < b1; ++bb)
+                if (st[bb].emin != 0x7FFFFFFF)
+                    mine += static_cast<long long>(st[bb].units << (st[bb].emin - emin_eff));
+            long long total_u;
+            const long long base = block_excl_scan_ll(mine, s_sc, total_u);
             const double scale = ldexp(1.0, emin_eff - 150);
             const double total = static_cast<double>(total_u) * scale;
-            const double target = dr.canon[c - dr.c0] * total + 0.0;
+            const double target = pk.canon[p] * total + 0.0;
             const double tu = target / scale;
-            long long run = base + incl - sum;
-            for (int i = i0; i < i1; ++i) {
-                run += pp_units(md[i], emin_eff);
-                if (static_cast<double>(run) >= tu) {
-                    atomicMin(&s_sel[sb], i);
+            // the first block whose inclusive prefix reaches the target
+            long long run = base;
+            for (int bb = b0; bb < b1; ++bb) {
+                const long long ub =
+                    st[bb].emin != 0x7FFFFFFF ? static_cast<long long>(st[bb].units << (st[bb].emin - emin_eff)) : 0;
+                if (static_cast<double>(run + ub) >= tu) {
+                    atomicMin(&s_blk, bb);
                     break;
+                }
+                run += ub;
+            }
+            __syncthreads();
+            const int blk = s_blk;
+            if (blk < nbp) {
+                // the exclusive prefix of that block, from the thread that holds it
+                if (blk >= b0 && blk < b1) {
+                    long long r = base;
+                    for (int bb = b0; bb < blk; ++bb)
+                        if (st[bb].emin != 0x7FFFFFFF)
+                            r += static_cast<long long>(st[bb].units << (st[bb].emin - emin_eff));
+                    s_base = r;
+                }
+                __syncthreads();
+                // rows of that block: kPpRPT consecutive rows per thread, as the distance kernel
+                const int r0 = blk * kPpRows + tid * kPpRPT;
+                long long uj[kPpRPT];
+                long long ut = 0;
+#pragma unroll
+                for (int j = 0; j < kPpRPT; ++j) {
+                    uj[j] = r0 + j < T ? static_cast<long long>(pp_units(md[r0 + j], emin_eff)) : 0;
+                    ut += uj[j];
+                }
+                long long tot;
+                long long rr = s_base + block_excl_scan_ll(ut, s_sc, tot);
+#pragma unroll
+                for (int j = 0; j < kPpRPT; ++j) {
+                    rr += uj[j];
+                    if (r0 + j < T && static_cast<double>(rr) >= tu) {
+                        atomicMin(&s_sel, r0 + j);
+                        break;
+                    }
                 }
             }
         } else if (tid == 0) {
             double tw = 0.0;
             for (int i = 0; i < T; ++i) tw += static_cast<double>(md[i]);
-            const double target = dr.canon[c - dr.c0] * tw + 0.0;
+            const double target = pk.canon[p] * tw + 0.0;
             double cs = 0.0;
-            int sel = 0;
+            int pick = 0;
             for (int i = 0; i < T; ++i) {
                 cs += static_cast<double>(md[i]);
                 if (cs >= target) {
-                    sel = i;
+                    pick = i;
                     break;
                 }
             }
-            s_sel[sb] = sel;
+            s_sel = pick;
         }
-        __syncthreads();   // selection known; every read of cur is done
-        if (tid < DP) {
-            const int sel = s_sel[sb] < T ? s_sel[sb] : 0;
-            const float v = bf16_to_f32(xb[static_cast<int64_t>(sel) * a.ts + tid]);
-            cur[tid] = v;
-            cent[static_cast<int64_t>(c) * DP + tid] = v;
-        }
+        __syncthreads();
+        sel = s_sel < T ? s_sel : 0;
     }
+    float* dst = a.cent + (static_cast<int64_t>(seg) * a.kmax + c) * DP;
+    for (int d = tid; d < DP; d += 256) dst[d] = bf16_to_f32(xb[static_cast<int64_t>(sel) * a.ts + d]);
 }
 
 // Per segment: exclusive scan of the [label][block] counts, cluster offsets,
@@ -1076,6 +1179,11 @@ size_t workspace_bytes(const imi_kmeans_args* a, int kmax, KmParams* out) {
     p.empties = cv.take<int32_t>(static_cast<size_t>(segs) * kmax);
     p.prev = cv.take<float>(segs);
     p.done = cv.take<int32_t>(segs);
+    if (a->init_mode == 2) {
+        const int nbp = (a->n_tokens + kPpRows - 1) / kPpRows;
+        PpBlock* st = cv.take<PpBlock>(static_cast<size_t>(segs) * nbp);
+        if (out) p.ppstats = st;
+    }
     if (out) *out = p;
     return cv.used();
 }
@@ -1195,31 +1303,40 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
         IMI_LAUNCH_CHECK("km_init_first_kernel");
     } else if (a->init_mode == 2) {
         // kmeans++ seeds 42, 43, 44, 45 by subspace, the same for every head
-        // (kmeans_core.cpp:459, 469)
-        // (IVF: seed 42, kmeans_core.cpp:548-556); picks in launches of
-        // kPpChunk, the distances carried over in the workspace
+        // (kmeans_core.cpp:459, 469; IVF: seed 42, kmeans_core.cpp:548-556);
+        // every segment's pick c in one pair of launches
+        PpPick pk{};
+        std::vector<double> canon[4];
         for (int part = 0; part < a->parts; ++part) {
-            PpDraws dr{};
             std::mt19937_64 rng(static_cast<uint64_t>(42 + part));
             std::uniform_int_distribution<int32_t> first(0, a->n_tokens - 1);
-            dr.first = first(rng);
-            const int kp = a->k[part];
-            for (int c0 = 1; c0 == 1 || c0 < kp; c0 += kPpChunk) {
-                dr.c0 = c0;
-                dr.c1 = std::min(kp, c0 + kPpChunk);
-                for (int c = c0; c < dr.c1; ++c)
-                    dr.canon[c - c0] = std::generate_canonical<double, std::numeric_limits<double>::digits>(rng);
+            pk.first[part] = first(rng);
+            canon[part].assign(a->k[part], 0.0);
+            for (int c = 1; c < a->k[part]; ++c)
+                canon[part][c] = std::generate_canonical<double, std::numeric_limits<double>::digits>(rng);
+        }
+        const int nbp = (a->n_tokens + kPpRows - 1) / kPpRows;
+        PpBlock* st = static_cast<PpBlock*>(p.ppstats);
+        for (int c = 0; c < kmax; ++c) {
+            if (c > 0) {
+                const dim3 grid(nbp, segs);
                 if (dp == 128)
-                    hipLaunchKernelGGL(km_pp_kernel<128>, dim3(a->kv_heads), dim3(pp_threads<128>()), 0, stream, p,
-                                       part, dr);
+                    hipLaunchKernelGGL(km_pp_dist_kernel<128>, grid, dim3(256), 0, stream, p, c, st, nbp);
                 else if (dp == 64)
-                    hipLaunchKernelGGL(km_pp_kernel<64>, dim3(a->kv_heads), dim3(pp_threads<64>()), 0, stream, p,
-                                       part, dr);
+                    hipLaunchKernelGGL(km_pp_dist_kernel<64>, grid, dim3(256), 0, stream, p, c, st, nbp);
                 else
-                    hipLaunchKernelGGL(km_pp_kernel<32>, dim3(a->kv_heads), dim3(pp_threads<32>()), 0, stream, p,
-                                       part, dr);
-                IMI_LAUNCH_CHECK("km_pp_kernel");
+                    hipLaunchKernelGGL(km_pp_dist_kernel<32>, grid, dim3(256), 0, stream, p, c, st, nbp);
+                IMI_LAUNCH_CHECK("km_pp_dist_kernel");
             }
+            pk.c = c;
+            for (int part = 0; part < a->parts; ++part) pk.canon[part] = c < a->k[part] ? canon[part][c] : 0.0;
+            if (dp == 128)
+                hipLaunchKernelGGL(km_pp_pick_kernel<128>, dim3(segs), dim3(256), 0, stream, p, pk, st, nbp);
+            else if (dp == 64)
+                hipLaunchKernelGGL(km_pp_pick_kernel<64>, dim3(segs), dim3(256), 0, stream, p, pk, st, nbp);
+            else
+                hipLaunchKernelGGL(km_pp_pick_kernel<32>, dim3(segs), dim3(256), 0, stream, p, pk, st, nbp);
+            IMI_LAUNCH_CHECK("km_pp_pick_kernel");
         }
     }
     for (int it = 0; it < a->max_iters; ++it) {
