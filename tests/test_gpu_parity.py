@@ -631,9 +631,11 @@ def test_config3_shape_decode_matches_oracle(ops, oracle):
 
 
 @pytest.mark.parametrize("ks,lens", [((32, 32), (3000, 6000, 9000, 12000)), ((6, 6, 6, 6), (3000, 6000, 9000, 12000)),
-                                     ((32, 32), (2000, 12000)), ((32, 32), (3000, 4500, 6000, 9000, 12000))])
+                                     ((32, 32), (2000, 12000)), ((32, 32), (3000, 4500, 6000, 9000, 12000)),
+                                     # configs[2] at its own lengths (32k-128k, 64 x 64, 16 KV heads, GQA 7)
+                                     ((64, 64), (32768 - 96, 65536 - 96, 98304 - 96, 131072 - 96))])
 def test_ragged_batch_decode_matches_oracle(ops, oracle, ks, lens):
-    """Config 2 at reduced scale: the KV heads of several sequences of
+    """Config 2 (reduced lengths, and its own 32k-128k): the KV heads of several sequences of
     different lengths (so different token and page budgets) share one
     selection and attention launch, their lists living in one
     [B*H, max_len, D] buffer.  Every sequence must match its own batch-1
