@@ -639,14 +639,27 @@ __global__ __launch_bounds__(256) void km_pp_dist_kernel(KmParams a, int c, PpBl
     __syncthreads();   // cur ready
     float m[kPpRPT];
     int emin = 0x7FFFFFFF, emax = 0;
-#pragma unroll 1
-    for (int j = 0; j < kPpRPT; ++j) {
-        const int i = min(r0 + j, T - 1);
-        uint4 v[DP / 8];
-        const uint4* row = reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(i) * a.ts);
+    // every row's loads in flight at once up to 64 dims (DP = 128: one row
+    // at a time, the registers of four rows would not fit)
+    constexpr int NRF = DP <= 64 ? kPpRPT : 1;
+    uint4 v[NRF][DP / 8];
 #pragma unroll
-        for (int d = 0; d < DP / 8; ++d) v[d] = row[d];
-        const float dist = l2_lanes8_bf16<DP>(v, cur);
+    for (int j = 0; j < NRF; ++j) {
+        const uint4* row = reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(min(r0 + j, T - 1)) * a.ts);
+#pragma unroll
+        for (int d = 0; d < DP / 8; ++d) v[j][d] = row[d];
+    }
+#pragma unroll
+    for (int j = 0; j < kPpRPT; ++j) {
+        if constexpr (NRF == 1) {
+            if (j > 0) {
+                const uint4* row =
+                    reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(min(r0 + j, T - 1)) * a.ts);
+#pragma unroll
+                for (int d = 0; d < DP / 8; ++d) v[0][d] = row[d];
+            }
+        }
+        const float dist = l2_lanes8_bf16<DP>(v[NRF == 1 ? 0 : j], cur);
         float mm = prev[j];
         if (dist < mm) mm = dist;
         m[j] = r0 + j < T ? mm : 0.0f;

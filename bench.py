@@ -68,6 +68,8 @@ def parse():
     p.add_argument("--groups", type=int, default=None)
     p.add_argument("--k", type=int, default=None, help="centroids per subspace")
     p.add_argument("--iters", type=int, default=None)
+    p.add_argument("--kmeans-init", choices=("first", "kmeans++"), default="first",
+                   help="index-build seeding: the first k keys (BASELINE) or the reference's kmeans++")
     p.add_argument("--budget", type=float, default=None)
     p.add_argument("--cpu-baseline", type=int, default=1)
     p.add_argument("--cpu-seconds", type=float, default=40.0,
@@ -153,9 +155,9 @@ def main():
         torch.cuda.synchronize()
         start_ev.record()
         if args.sample:
-            cent, labels, _ = ops.kmeans_sampled(mid_k, list(ks), args.iters, args.sample)
+            cent, labels, _ = ops.kmeans_sampled(mid_k, list(ks), args.iters, args.sample, init=args.kmeans_init)
         else:
-            cent, labels, _ = ops.kmeans(mid_k, list(ks), args.iters)
+            cent, labels, _ = ops.kmeans(mid_k, list(ks), args.iters, init=args.kmeans_init)
         if parts == 4:   # selection over the occupied cells (compact ids)
             idx = ops.build_index(mid_k, mid_v, cent, labels, list(ks), compact=True, merged=False,
                                   n_centroids=min(T, ncells) + 1)
@@ -290,7 +292,7 @@ def main():
             "workload": workload_name(args, L, H, G, ks),
             "layers": L, "context": args.context, "kv_heads": H, "q_heads": H * G, "static_window": static_total,
             "nprobe": bud.nprobe, "max_tokens": bud.max_tokens, "buffer_pages": bud.buffer_pages,
-            "hip_graph": graph is not None,
+            "hip_graph": graph is not None, "kmeans_init": args.kmeans_init,
         },
         "index_build_ms": {"per_layer_median": round(statistics.median(build_ms), 3),
                            "per_layer_min": round(min(build_ms), 3), "layers": L},
