@@ -26,7 +26,7 @@ not fit in HBM (2-way IMI, without async_update or tile mode).
 subspace_parts = 0 builds an IVF index (kmeans_core.cpp:503-595: one
 k-means over the 128 dims per KV head, k = runtime kmeans.k1 or
 round(T / 16), at most 4096) whose clusters are the cells of the same
-selection and attention path (without async_update or host_tier).
+selection and attention path, async_update included (not host_tier).
 
 Online index maintenance (runtime_config["async_update"], async_update.py)
 runs on the device as well: every `batch` decode keys of a layer are
@@ -152,8 +152,6 @@ class adpimi_cache:  # noqa: N801  (reference class name)
             raise ValueError("async_update: batch must be at most 64 and at most delta_tokens")
         if self.async_update_enabled and self.async_update_delta_tokens > 1024:
             raise ValueError("async_update: delta_tokens must be at most 1024")
-        if self.async_update_enabled and subspace_parts == 0:
-            raise NotImplementedError("async_update is not available for IVF indexing (subspace_parts=0)")
         self._updates: List[Optional[ops.OnlineUpdate]] = [None] * layer_num
         self._upd_count = [0] * layer_num
         self._upd_pending: List[Optional[int]] = [None] * layer_num   # decode step of an unapplied refresh

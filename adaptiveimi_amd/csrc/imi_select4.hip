@@ -614,7 +614,9 @@ __global__ __launch_bounds__(kScoreThreads) void sel2_dense_score_kernel(Sel4 a)
 
 // IVF (one 128-dim space): one cluster per thread, the 128-term chain of
 // compute_impl.cu:80-101 over its centroid, keys as in
-// sel2_dense_score_kernel (0 for an empty cluster).
+// sel2_dense_score_kernel (0 for an empty cluster).  ONLINE: a cluster
+// whose centroid was replaced is scored over its shadow row instead.
+template <bool ONLINE>
 __global__ __launch_bounds__(kScoreThreads) void sel1_score_kernel(Sel4 a) {
     __shared__ __attribute__((aligned(16))) float qs[128];
     __shared__ int lh[kLocBins];   // the candidate cut's buckets
@@ -630,8 +632,15 @@ __global__ __launch_bounds__(kScoreThreads) void sel1_score_kernel(Sel4 a) {
 #pragma unroll
         for (int j = 0; j < kMaxG4; ++j) qv[j] = qh[min(j, a.G - 1) * 128 + tid];
     }
+    int slot = -1;
+    if (ONLINE && a.upd_slot && in) slot = a.upd_slot[static_cast<int64_t>(h) * ncells + g];
     const float4* cr =
         reinterpret_cast<const float4*>(a.cent + (static_cast<int64_t>(h) * a.kmax + (in ? g : 0)) * 128);
+    if (ONLINE && slot >= 0) {
+        const int row = min(max(a.upd_row[static_cast<int64_t>(h) * a.shadow_rows + min(slot, a.shadow_rows - 1)], 0),
+                            a.shadow_rows - 1);
+        cr = reinterpret_cast<const float4*>(a.shadow + (static_cast<int64_t>(h) * a.shadow_rows + row) * 128);
+    }
     float4 r[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) r[i] = cr[i];
@@ -1233,8 +1242,6 @@ int select4_validate(const imi_select_args* a) {
     if (a->parts == 1) {
         IMI_REQUIRE(a->k[0] >= 1 && a->k[0] <= kIvfMaxK, IMI_ERR_UNSUPPORTED, "imi_select: IVF k=%d outside [1,%d]",
                     a->k[0], kIvfMaxK);
-        IMI_REQUIRE(!a->upd_slot && a->ring_cap == 0, IMI_ERR_UNSUPPORTED,
-                    "imi_select: the online index update is not available for IVF");
         cells_max = a->k[0];
     } else if (dense) {
         for (int p = 0; p < 2; ++p)
@@ -1321,7 +1328,10 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     p.n_delta = a->n_delta;
     const bool online = p.upd_slot || p.ring_cap > 0;
     if (a->parts == 1) {
-        hipLaunchKernelGGL(sel1_score_kernel, dim3(p.nbs, a->kv_heads), dim3(kScoreThreads), 0, stream, p);
+        if (p.upd_slot)
+            hipLaunchKernelGGL(sel1_score_kernel<true>, dim3(p.nbs, a->kv_heads), dim3(kScoreThreads), 0, stream, p);
+        else
+            hipLaunchKernelGGL(sel1_score_kernel<false>, dim3(p.nbs, a->kv_heads), dim3(kScoreThreads), 0, stream, p);
         IMI_LAUNCH_CHECK("sel1_score_kernel");
     } else if (dense) {
         const dim3 grid_s(p.nbs, a->kv_heads);

@@ -51,8 +51,6 @@ def test_cache_rejects_what_the_reference_rejects():
         _cache(subspace_parts=3)
     with pytest.raises(ValueError, match="input length"):
         _cache(input_length=0)
-    with pytest.raises(NotImplementedError, match="IVF"):
-        _cache(subspace_parts=0, runtime_config={"async_update": {"enabled": True}})
 
 
 def test_async_update_config():

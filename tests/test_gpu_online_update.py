@@ -93,7 +93,7 @@ def _compare_state(upd, orc, out, four, ncells):
         assert (uslot[h] >= 0).sum() == len(rep)
 
 
-@pytest.mark.parametrize("ks", [(32, 32), (6, 6, 6, 6), (8, 8, 8, 8)])   # (8,8,8,8): power-of-two digit path
+@pytest.mark.parametrize("ks", [(32, 32), (6, 6, 6, 6), (8, 8, 8, 8), (300,)])   # (8,8,8,8): power-of-two digits; (300,): IVF
 def test_update_kernels_match_oracle(ops, oracle, ks):
     note(f"[online] update kernels ks={ks}")
     H, T, B = 8, 5000, 8
@@ -173,7 +173,8 @@ def _select_oracle(oracle, orc, q, out, sz, bud, exec_rows, ncells):
 @pytest.mark.parametrize("ks,T", [((32, 32), 6000), ((128, 128), 6000), ((6, 6, 6, 6), 6000), ((8, 8, 8, 8), 6000),
                                   # the 1M 4-way config's sizing (adaptive k 16, budget 0.1): nprobe 6554, all of it
                                   # ranked for the delta match; 2-way past the one-kernel selection (k 181)
-                                  ((16, 16, 16, 16), 120000), ((181, 181), 60000)])
+                                  ((16, 16, 16, 16), 120000), ((181, 181), 60000),
+                                  ((375,), 6000)])   # IVF
 def test_select_with_replaced_centroids_and_delta(ops, oracle, ks, T):
     from adaptiveimi_amd import synthetic
 
@@ -302,7 +303,8 @@ def test_decode_step_online_matches_oracle(ops, oracle):
 
 
 @pytest.mark.parametrize("ks,steps,batch,thr,ring", [((32, 32), 14, 4, 2, 24), ((6, 6, 6, 6), 14, 4, 2, 24),
-                                                      ((8, 8, 8, 8), 14, 4, 2, 24), ((32, 32), 50, 16, 3, 40)])
+                                                      ((8, 8, 8, 8), 14, 4, 2, 24), ((32, 32), 50, 16, 3, 40),
+                                                      ((256,), 14, 4, 2, 24)])   # (256,): IVF
 def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, thr, ring):
     """The drop-in with async_update on, driven like model_hub drives it,
     against a step-by-step oracle replay (update applied at the next step);
@@ -321,7 +323,7 @@ def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, t
                          layer_mapping={"0": DEV, "1": DEV}, max_new_length=steps + 1, input_length=S,
                          static_pattern_start=32, static_pattern_end=64, core=4, pages_per_cluster=2,
                          retrieval_budget=0.1, cache_ratio=0.05, buffer_cluster_num=32, prefill_bsz=1, num_gpus=1,
-                         model_size=8, subspace_parts=len(ks),
+                         model_size=8, subspace_parts=len(ks) if len(ks) > 1 else 0,
                          runtime_config={"kmeans": kcfg, "async_update": {"enabled": True, "batch": batch,
                                                                           "threshold": thr, "delta_tokens": ring}})
     kv = []

@@ -75,12 +75,14 @@ def test_ivf_library_limits(L):
     assert "4096" in L.imi_last_error().decode()
     # subspaces of 2 / 4 keep their 256 limit
     assert L.imi_kmeans_workspace_size(ctypes.byref(_kargs(2, 300)), ctypes.byref(need)) != 0
-    # selection: IVF through the ranking pipeline; no online update
+    # selection: IVF through the ranking pipeline, with or without the online update
     a = _lib.SelectArgs(query=16, centroids=16, cell_count=16, cell_offset=16, kv_heads=2, groups=4, dim=128,
                         parts=1, nprobe=10, max_tokens=100, buffer_pages=20, page_size=8, tile_mode=0)
     a.k[0] = 100
     a.sel_cap = 10
     assert L.imi_select_workspace_size(ctypes.byref(a), ctypes.byref(need)) == 0 and need.value > 0
     a.ring_cap, a.ring_cell, a.ring_row, a.ring_n = 1, 16, 16, 16
+    assert L.imi_select_workspace_size(ctypes.byref(a), ctypes.byref(need)) == 0
+    a.k[0] = 4097
     assert L.imi_select_workspace_size(ctypes.byref(a), ctypes.byref(need)) != 0
     assert "IVF" in L.imi_last_error().decode()
