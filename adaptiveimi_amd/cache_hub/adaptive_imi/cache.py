@@ -21,12 +21,12 @@ arguments are accepted and recorded).  runtime_config["host_tier"] =
 with a GPU block cache of round(n_centroids * cache_ratio) clusters of
 pages_per_cluster pages per head and the reference's hot / cold policy
 (IMI_HOTCOLD_HOT_RATIO, default 0.3): ops.HostTierPlan, for lists that do
-not fit in HBM (2-way IMI, without async_update or tile mode).
+not fit in HBM (2-way IMI or IVF, without async_update or tile mode).
 
 subspace_parts = 0 builds an IVF index (kmeans_core.cpp:503-595: one
 k-means over the 128 dims per KV head, k = runtime kmeans.k1 or
 round(T / 16), at most 4096) whose clusters are the cells of the same
-selection and attention path, async_update included (not host_tier).
+selection and attention path, async_update and host_tier included.
 
 Online index maintenance (runtime_config["async_update"], async_update.py)
 runs on the device as well: every `batch` decode keys of a layer are
@@ -437,8 +437,8 @@ class adpimi_cache:  # noqa: N801  (reference class name)
     def _host_plan(self, layer_idx: int, bud: "ops.Budget", upd) -> "ops.HostTierPlan":
         """The layer's lists move to pinned host memory; the device holds the
         block cache and the execution buffer (retrieval.py:200-290)."""
-        if upd is not None or bud.tile_mode or len(self.layer_ks[layer_idx]) != 2:
-            raise NotImplementedError("host_tier serves 2-way IMI without async_update or tile mode")
+        if upd is not None or bud.tile_mode or len(self.layer_ks[layer_idx]) not in (1, 2):
+            raise NotImplementedError("host_tier serves 2-way IMI and IVF without async_update or tile mode")
         env = os.getenv("IMI_HOTCOLD_HOT_RATIO", "")
         try:
             ratio = float(env) if env else 0.0   # wave_buffer_cpu_hotcold.cpp:75-95

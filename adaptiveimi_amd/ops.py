@@ -715,7 +715,7 @@ class HostTierPlan:
     kernel builds the execution buffer [miss rows | hit rows] and a one-cell
     selection over it; the host admits the missed clusters that fit; the
     admission kernel copies them into the cache; the attention runs over
-    [steady rows | buffer].  2-way IMI without tile mode or the online update.
+    [steady rows | buffer].  2-way IMI or IVF, without tile mode or the online update.
 
     The lists are copied once into pinned host memory (list_keys /
     list_values may then be freed by the caller); the device holds the
@@ -728,8 +728,8 @@ class HostTierPlan:
                  cache_pages: int, hot_ratio: float = 0.0, scale: Optional[float] = None):
         import numpy as np
 
-        if len(ks) != 2:
-            raise ValueError("the host tier serves 2-way IMI (cells = the global cells of the CSR)")
+        if len(ks) not in (1, 2):
+            raise ValueError("the host tier serves 2-way IMI and IVF (cells = the global cells of the CSR)")
         if budget.tile_mode or budget.head_buffer_pages is not None:
             raise ValueError("the host tier runs without tile mode and with one budget for every head")
         if cache_pages < 1:

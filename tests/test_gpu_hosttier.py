@@ -23,7 +23,8 @@ def bits(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("T,ks,G,cache_pages,ratio", [(12000, (32, 32), 4, 60, 0.0), (9000, (16, 16), 8, 400, 0.5)])
+@pytest.mark.parametrize("T,ks,G,cache_pages,ratio", [(12000, (32, 32), 4, 60, 0.0), (9000, (16, 16), 8, 400, 0.5),
+                                                       (9000, (560,), 4, 200, 0.3)])   # (560,): IVF
 def test_host_tier_decode_matches(T, ks, G, cache_pages, ratio):
     from adaptiveimi_amd import ops, synthetic
     from oracle import hostcache as O
