@@ -69,7 +69,7 @@ def parse():
     p.add_argument("--k", type=int, default=None, help="centroids per subspace")
     p.add_argument("--iters", type=int, default=None)
     p.add_argument("--kmeans-init", choices=("first", "kmeans++"), default="first",
-                   help="index-build seeding: the first k keys (BASELINE) or the reference's kmeans++")
+                   help="index-build seeding: the first k keys (as BASELINE.json specifies) or the reference's kmeans++")
     p.add_argument("--budget", type=float, default=None)
     p.add_argument("--cpu-baseline", type=int, default=1)
     p.add_argument("--cpu-seconds", type=float, default=40.0,
