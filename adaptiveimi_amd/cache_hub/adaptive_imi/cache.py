@@ -18,10 +18,16 @@ round trip.  By default nothing lives on the host, so the reference's
 thread pool and prefetch warm-up have no counterpart (their constructor
 arguments are accepted and recorded).  runtime_config["host_tier"] =
 {"enabled": True} keeps each layer's lists in pinned host memory instead,
-with a GPU block cache of round(n_centroids * cache_ratio) clusters of
-pages_per_cluster pages per head and the reference's hot / cold policy
-(IMI_HOTCOLD_HOT_RATIO, default 0.3): ops.HostTierPlan, for lists that do
-not fit in HBM (2-way IMI or IVF, without async_update or tile mode).
+as the reference always does (indexing.py:98-107): each layer's build
+writes its lists to a device buffer that an asynchronous copy moves to the
+pinned lists and that is freed at once, so the device never holds more than
+one layer's lists.  Decode then runs with a GPU block cache of
+round(n_centroids * cache_ratio) clusters of pages_per_cluster pages per
+head and the reference's hot / cold policy (IMI_HOTCOLD_HOT_RATIO, default
+0.3): ops.HostTierPlan, for lists that do not fit in HBM (2-way, 4-way IMI
+or IVF, async_update included; not with tile mode).  A host-tier step
+synchronises with the host (its selected cells go to the cache manager), so
+it cannot be captured in a graph.
 
 subspace_parts = 0 builds an IVF index (kmeans_core.cpp:503-595: one
 k-means over the 128 dims per KV head, k = runtime kmeans.k1 or
@@ -208,6 +214,8 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         self.compact_meta: List[Optional[Dict[str, torch.Tensor]]] = [None] * layer_num
         self.list_keys: List[Optional[torch.Tensor]] = [None] * layer_num      # [1, H, list_capacity, D]
         self.list_values: List[Optional[torch.Tensor]] = [None] * layer_num
+        # host tier: each layer's lists in pinned host memory ([H, rows, D] keys, values)
+        self.host_lists: List[Optional[tuple]] = [None] * layer_num
         self._plans: List[Optional[ops.DecodePlan]] = [None] * layer_num
         # the reference's execution-buffer views; the gather here reads rows in place
         self.execution_buffer_keys_dict: Dict[str, torch.Tensor] = {}
@@ -239,6 +247,8 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         rank for the 4-way path)."""
         sz = self._decode_budget(ks)
         tiles = int(os.getenv("IMI_MAX_TILES", "0") or 0) != 0
+        if tiles and self.host_tier:
+            raise NotImplementedError("host_tier runs without tile mode (IMI_MAX_TILES)")
         bud = ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"], self.page_size, tile_mode=tiles)
         ops.check_decode_limits(self.batch_groups, self.group_size, ks, bud, online=self.async_update_enabled)
 
@@ -273,6 +283,16 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         idx = ops.build_index(middle_k, middle_v, cent, labels, ks, list_keys=lk[0], list_values=lv[0],
                               compact=four_way or online, merged=online,
                               n_centroids=min(T, ncells) + 1 if four_way else ncells + 1)
+        if self.host_tier:
+            # the lists go to pinned host memory on this (the build's) stream;
+            # the device buffer is freed now, and the allocator hands its block
+            # to the next build on the same stream only after this copy
+            hk = torch.empty((H, rows, D), dtype=middle_k.dtype, pin_memory=True)
+            hv = torch.empty_like(hk, pin_memory=True)
+            hk.copy_(lk[0], non_blocking=True)
+            hv.copy_(lv[0], non_blocking=True)
+            self.host_lists[layer_idx] = (hk, hv)
+            lk = lv = None
         self.compact_cells[layer_idx] = (
             {n: idx[n] for n in ("n_active", "compact_gid", "compact_size", "compact_offset")} if four_way else None)
         self.compact_meta[layer_idx] = (
@@ -435,25 +455,21 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         return plan
 
     def _host_plan(self, layer_idx: int, bud: "ops.Budget", upd) -> "ops.HostTierPlan":
-        """The layer's lists move to pinned host memory; the device holds the
+        """Decode over the layer's pinned host lists; the device holds the
         block cache and the execution buffer (retrieval.py:200-290)."""
-        if upd is not None or bud.tile_mode or len(self.layer_ks[layer_idx]) not in (1, 2):
-            raise NotImplementedError("host_tier serves 2-way IMI and IVF without async_update or tile mode")
+        if bud.tile_mode:
+            raise NotImplementedError("host_tier runs without tile mode (IMI_MAX_TILES)")
         env = os.getenv("IMI_HOTCOLD_HOT_RATIO", "")
         try:
             ratio = float(env) if env else 0.0   # wave_buffer_cpu_hotcold.cpp:75-95
         except ValueError:
             ratio = 0.0
         pages = ops.host_cache_pages(self.n_centroids, self.nprobe, self.pages_per_cluster, self.cache_ratio)
-        plan = ops.HostTierPlan(self.centroids[layer_idx], self.cell_count[layer_idx], self.cell_offset[layer_idx],
-                                self.layer_ks[layer_idx], bud, self.list_keys[layer_idx][0],
-                                self.list_values[layer_idx][0], self.steady_zone_keys[layer_idx][0],
+        hk, hv = self.host_lists[layer_idx]
+        return ops.HostTierPlan(self.centroids[layer_idx], self.cell_count[layer_idx], self.cell_offset[layer_idx],
+                                self.layer_ks[layer_idx], bud, hk, hv, self.steady_zone_keys[layer_idx][0],
                                 self.steady_zone_values[layer_idx][0], self.group_size, cache_pages=pages,
-                                hot_ratio=ratio)
-        # the device copies of the lists are no longer needed
-        self.list_keys[layer_idx] = None
-        self.list_values[layer_idx] = None
-        return plan
+                                hot_ratio=ratio, compact=self.compact_cells[layer_idx], update=upd)
 
     def ensure_layer_ready(self, layer_idx: int) -> None:
         if not self.layer_ready[layer_idx]:
@@ -474,7 +490,7 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         out = torch.empty((self.batch_size, 1, self.num_heads, self.head_dim), dtype=queries.dtype,
                           device=queries.device)
         if isinstance(plan, ops.HostTierPlan):
-            plan.step(q, out, int(static_len))
+            plan.step(q, out, int(static_len), exec_rows=self.execution_stride - int(static_len))
         else:
             plan.run(q, out, int(static_len), exec_rows=self.execution_stride - int(static_len))
         return out
@@ -509,7 +525,9 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         return None, None
 
     def capture_cuda_graph(self):
-        """runtime.py:9 (a no-op there too); decode steps are graph-capturable."""
+        """runtime.py:9 (a no-op there too).  HBM-resident decode steps are
+        graph-capturable; host-tier steps are not (each one hands its
+        selected cells to the host cache manager)."""
         return None
 
     # ----------------------------------------------------------- lifecycle --
@@ -597,6 +615,7 @@ class adpimi_cache:  # noqa: N801  (reference class name)
         self._upd_pending = [None] * n
         self.list_keys = [None] * n
         self.list_values = [None] * n
+        self.host_lists = [None] * n
         self.layer_ks = [None] * n
         self.layer_ready = [False] * n
 

@@ -301,6 +301,18 @@ int imi_hostcache_access(imi_hostcache* c, const int64_t* keys, int32_t n_keys, 
                 IMI_ERR_INVALID, "imi_hostcache_access: null argument");
     IMI_REQUIRE(n_keys >= 0 && n_keys <= c->max_keys, IMI_ERR_INVALID,
                 "imi_hostcache_access: %d keys outside [0, %d]", n_keys, c->max_keys);
+    // every key of every group is checked before any output or cache state
+    // changes; a rejected call also forgets the previous access's hit and
+    // miss lists, so that an update after it admits and touches nothing
+    for (int64_t i = 0; i < static_cast<int64_t>(c->groups) * n_keys; ++i) {
+        if (keys[i] >= 0 && keys[i] < c->n_cells) continue;
+        for (auto& gr : c->g) {
+            gr.hit_keys.clear();
+            gr.miss_keys.clear();
+        }
+        IMI_REQUIRE(false, IMI_ERR_INVALID, "imi_hostcache_access: cell %lld outside [0, %d) (group %lld)",
+                    static_cast<long long>(keys[i]), c->n_cells, static_cast<long long>(i / n_keys));
+    }
     const int mb = c->max_consider;
     for (int gi = 0; gi < c->groups; ++gi) {
         auto& gr = c->g[gi];
@@ -314,8 +326,6 @@ int imi_hostcache_access(imi_hostcache* c, const int64_t* keys, int32_t n_keys, 
         int nh = 0, nm = 0, hrow = 0, mrow = 0, consider = 0;
         for (int i = 0; i < n_keys; ++i) {
             const int64_t key = k[i];
-            IMI_REQUIRE(key >= 0 && key < c->n_cells, IMI_ERR_INVALID,
-                        "imi_hostcache_access: cell %lld outside [0, %d)", static_cast<long long>(key), c->n_cells);
             auto& cell = gr.cells[key];
             if (cell.blocks == 0 || cell.last == 0) continue;
             consider += cell.blocks;

@@ -715,37 +715,54 @@ class HostTierPlan:
     kernel builds the execution buffer [miss rows | hit rows] and a one-cell
     selection over it; the host admits the missed clusters that fit; the
     admission kernel copies them into the cache; the attention runs over
-    [steady rows | buffer].  2-way IMI or IVF, without tile mode or the online update.
+    [steady rows | buffer | matched delta-ring rows].
 
-    The lists are copied once into pinned host memory (list_keys /
-    list_values may then be freed by the caller); the device holds the
-    cache (cache_pages x page_size rows per head) and the execution buffer
-    (buffer_pages x page_size rows per head)."""
+    Cells: the global cells of the CSR for a 2-way IMI and IVF; for a 4-way
+    IMI (``compact``, the occupied cells of build_index) the manager keeps
+    the occupied cells by compact id and the host maps each selected global
+    id to its compact id (the reference's clusters are its compact cells).
+    ``update``: the online index update (async_update.py), whose replaced
+    centroids the selection scores and whose matched ring tokens (steady
+    rows) are attended after the buffer.  Not with tile mode.
+
+    list_keys / list_values: pinned host tensors [H, rows, D], used in place
+    (the drop-in cache writes each layer's lists there during its build), or
+    device tensors, copied once into pinned host memory.  The device holds
+    the cache (cache_pages x page_size rows per head) and the execution
+    buffer (buffer_pages x page_size rows per head)."""
 
     def __init__(self, centroids: torch.Tensor, cell_count: torch.Tensor, cell_offset: torch.Tensor,
                  ks: Sequence[int], budget: Budget, list_keys: torch.Tensor, list_values: torch.Tensor,
                  steady_keys: Optional[torch.Tensor], steady_values: Optional[torch.Tensor], groups: int,
-                 cache_pages: int, hot_ratio: float = 0.0, scale: Optional[float] = None):
+                 cache_pages: int, hot_ratio: float = 0.0, scale: Optional[float] = None,
+                 compact: Optional[Dict[str, torch.Tensor]] = None, update: Optional[OnlineUpdate] = None):
         import numpy as np
 
-        if len(ks) not in (1, 2):
-            raise ValueError("the host tier serves 2-way IMI and IVF (cells = the global cells of the CSR)")
+        if len(ks) not in (1, 2, 4):
+            raise ValueError("the host tier serves IVF, 2-way and 4-way IMI")
+        if len(ks) == 4 and compact is None:
+            raise ValueError("a 4-way host tier needs the occupied cells (build_index compact outputs)")
         if budget.tile_mode or budget.head_buffer_pages is not None:
             raise ValueError("the host tier runs without tile mode and with one budget for every head")
         if cache_pages < 1:
             raise ValueError("cache_pages must be >= 1")
-        dev = _require_device(centroids, cell_count, cell_offset, list_keys, list_values)
+        dev = _require_device(centroids, cell_count, cell_offset)
         H, list_rows, D = list_keys.shape
+        if tuple(list_values.shape) != (H, list_rows, D):
+            raise ValueError("list_keys and list_values must have the same [H, rows, D] shape")
         ps, bp = budget.page_size, budget.buffer_pages
         self.device, self.H, self.G, self.D = dev, H, groups, D
         self.budget, self.cache_pages = budget, int(cache_pages)
-        ncells = int(cell_count.shape[1])
-        self.pad = ncells                       # an empty cell closes each key list
-        # pinned host lists and their device mapping
-        self.h_keys = torch.empty(tuple(list_keys.shape), dtype=list_keys.dtype, pin_memory=True)
-        self.h_values = torch.empty(tuple(list_values.shape), dtype=list_values.dtype, pin_memory=True)
-        self.h_keys.copy_(list_keys)
-        self.h_values.copy_(list_values)
+        # pinned host lists (taken as they are when already pinned) and their device mapping
+        host = [t if (not t.is_cuda and t.is_pinned() and t.is_contiguous()) else None
+                for t in (list_keys, list_values)]
+        if host[0] is None or host[1] is None:
+            host = [torch.empty((H, list_rows, D), dtype=t.dtype, pin_memory=True) for t in (list_keys, list_values)]
+            host[0].copy_(list_keys)
+            host[1].copy_(list_values)
+        self.h_keys, self.h_values = host
+        _as_bits(self.h_keys)
+        _as_bits(self.h_values)
         L = _lib.lib()
         dk, dv = ctypes.c_void_p(), ctypes.c_void_p()
         check(L.imi_host_device_pointer(ctypes.c_void_p(self.h_keys.data_ptr()), ctypes.byref(dk)),
@@ -760,16 +777,34 @@ class HostTierPlan:
         self.cache_values = torch.zeros_like(self.cache_keys)
         # the selection and the attention of one DecodePlan whose list is the buffer
         self.plan = DecodePlan(centroids, cell_count, cell_offset, ks, budget, self.exec_keys, self.exec_values,
-                               steady_keys, steady_values, groups, scale=scale)
+                               steady_keys, steady_values, groups, scale=scale, compact=compact, update=update)
         self.cap = self.plan.sel_cap
-        # host cache manager over the cells plus the empty padding cell
-        sizes = np.zeros((H, ncells + 1), np.int32)
-        offs = np.zeros((H, ncells + 2), np.int32)
-        sizes[:, :ncells] = cell_count.cpu().numpy()
-        offs[:, :ncells + 1] = cell_offset.cpu().numpy()
-        offs[:, ncells + 1] = offs[:, ncells]
+        # the manager's cells: sizes and CSR offsets per head, then one empty
+        # padding cell that closes each key list
+        if compact is not None:
+            na = compact["n_active"].cpu().numpy().astype(np.int64)
+            n = int(na.max()) if na.size else 0
+            self._gids = compact["compact_gid"].cpu().numpy()
+            self._na = na
+            csz = compact["compact_size"].cpu().numpy()
+            coff = compact["compact_offset"].cpu().numpy()
+            sizes = np.zeros((H, n + 1), np.int32)
+            offs = np.zeros((H, n + 2), np.int32)
+            for h in range(H):
+                sizes[h, :na[h]] = csz[h, :na[h]]
+                offs[h, :na[h] + 1] = coff[h, :na[h] + 1]
+                offs[h, na[h] + 1:] = coff[h, na[h]]
+        else:
+            self._gids = None
+            n = int(cell_count.shape[1])
+            sizes = np.zeros((H, n + 1), np.int32)
+            offs = np.zeros((H, n + 2), np.int32)
+            sizes[:, :n] = cell_count.cpu().numpy()
+            offs[:, :n + 1] = cell_offset.cpu().numpy()
+            offs[:, n + 1] = offs[:, n]
+        self.pad = n
         self._h = ctypes.c_void_p()
-        check(L.imi_hostcache_create(H, ncells + 1, self.cache_pages, ps, bp, self.cap, float(hot_ratio),
+        check(L.imi_hostcache_create(H, n + 1, self.cache_pages, ps, bp, self.cap, float(hot_ratio),
                                      ctypes.byref(self._h)), "imi_hostcache_create")
         check(L.imi_hostcache_set_metadata(self._h, sizes.ctypes.data_as(ctypes.c_void_p),
                                            offs.ctypes.data_as(ctypes.c_void_p)), "imi_hostcache_set_metadata")
@@ -805,14 +840,17 @@ class HostTierPlan:
             _lib.lib().imi_hostcache_destroy(h)
             self._h = None
 
-    def step(self, query: torch.Tensor, out: torch.Tensor, static_len: int) -> torch.Tensor:
-        """One decode step (host-synchronous, as the reference's)."""
+    def step(self, query: torch.Tensor, out: torch.Tensor, static_len: int,
+             exec_rows: Optional[int] = None) -> torch.Tensor:
+        """One decode step (host-synchronous, as the reference's).  exec_rows:
+        execution-buffer rows left after the static rows, the bound of the
+        delta append (with the online update)."""
         import numpy as np
 
         L = _lib.lib()
         stream = _stream(self.device)
         H, cap, bp = self.H, self.cap, self.budget.buffer_pages
-        self.plan.run(query, out, static_len, stream=stream, phases=1)          # selection
+        self.plan.run(query, out, static_len, stream=stream, phases=1, exec_rows=exec_rows)   # selection
         sel = self.plan.selection
         self.h_sel.copy_(sel["sel_cell"], non_blocking=True)
         self.h_nsel.copy_(sel["n_selected"], non_blocking=True)
@@ -820,8 +858,13 @@ class HostTierPlan:
         cells, m = self.h_sel.numpy(), self.h_nsel.numpy()
         keys = self.keys
         keys.fill(self.pad)
-        live = np.arange(cap)[None, :] < np.clip(m, 0, cap)[:, None]
-        keys[live] = cells[live]
+        if self._gids is None:
+            live = np.arange(cap)[None, :] < np.clip(m, 0, cap)[:, None]
+            keys[live] = cells[live]
+        else:   # 4-way: selected global ids -> compact ids (occupied cells in ascending global id)
+            for h in range(H):
+                mh = int(np.clip(m[h], 0, cap))
+                keys[h, :mh] = np.searchsorted(self._gids[h, :self._na[h]], cells[h, :mh])
         hl, hn = self.h_lists.numpy(), self.h_nums.numpy()
         p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
         check(L.imi_hostcache_access(self._h, p(keys), cap, p(hl[0]), p(hl[1]), p(hl[2]), p(hn[0, 0]),
@@ -844,5 +887,5 @@ class HostTierPlan:
                                     self.cache_keys.data_ptr(), self.cache_values.data_ptr(), self.cache_rows,
                                     self.budget.page_size, H, bp, row(6), row(7), row(8),
                                     self.d_nums[1, 0].data_ptr(), stream), "imi_hostcache_admit")
-        self.plan.run(query, out, static_len, stream=stream, phases=2)          # attention + merge
+        self.plan.run(query, out, static_len, stream=stream, phases=2, exec_rows=exec_rows)   # attention + merge
         return out

@@ -319,3 +319,51 @@ def test_host_tier_dropin_matches_oracle():
             got = out.float().cpu().numpy().reshape(H, G, D)
             assert np.all(np.abs(got - ref) <= 2e-2 + 1e-2 * np.abs(ref)), (layer, step)
     assert all(cache._plans[layer].hits > 0 for layer in range(L))   # the repeated step hit the cache
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a HIP device")
+def test_host_tier_keeps_lists_off_the_device():
+    """With the host tier each layer's lists go to pinned host memory during
+    its build (indexing.py:98-107 keeps them in host memory from the start),
+    so after the prefill of every layer the device holds none of them: the
+    allocated device memory grows by the per-layer metadata only, while the
+    HBM-resident cache holds every layer's lists."""
+    from adaptiveimi_amd import synthetic
+
+    print("[dropin host tier] device memory after prefill, 3 layers", flush=True)
+    L, S, H, D = 3, 6096, 8, 128
+    kv = [synthetic.make_kv(H, S, seed=90 + layer) for layer in range(L)]
+    list_bytes = 2 * H * (S - 96) * D * 2      # one layer's keys + values
+
+    def prefill(host):
+        cache = _cache(layer_mapping={str(i): DEV for i in range(L)}, layer_num=L,
+                       runtime_config={"kmeans": {"k1": 32, "k2": 32, "max_iters": 3, "early_stop_min_iter": 3,
+                                                  "init": "first"},
+                                       "host_tier": {"enabled": host}})
+        torch.cuda.synchronize()
+        before = torch.cuda.memory_allocated()
+        for layer in range(L):
+            k, v = kv[layer]
+            pk = k.transpose(0, 1).unsqueeze(0).contiguous().to(DEV)
+            pv = v.transpose(0, 1).unsqueeze(0).contiguous().to(DEV)
+            cache.prefill_update_kv_cache(None, pk, pv, layer, 0)
+            cache.sync(layer, 0)
+            del pk, pv
+        torch.cuda.synchronize()
+        return cache, torch.cuda.memory_allocated() - before
+
+    hbm, grown_hbm = prefill(False)      # also warms the shared k-means / index workspaces
+    assert grown_hbm >= L * list_bytes
+    del hbm
+    host, grown_host = prefill(True)
+    assert grown_host < list_bytes // 4, (grown_host, list_bytes)
+    for layer in range(L):
+        hk, hv = host.host_lists[layer]
+        assert host.list_keys[layer] is None and hk.is_pinned() and hv.is_pinned()
+        # the pinned lists hold the permuted rows of the middle keys
+        k, v = kv[layer]
+        perm = host.token_perm[layer].cpu().long()
+        mid_k, mid_v = k[:, 32:S - 64], v[:, 32:S - 64]
+        for h in (0, H - 1):
+            assert torch.equal(hk[h], mid_k[h, perm[h]]) and torch.equal(hv[h], mid_v[h, perm[h]])

@@ -24,7 +24,8 @@ def bits(t: torch.Tensor) -> np.ndarray:
 
 
 @pytest.mark.parametrize("T,ks,G,cache_pages,ratio", [(12000, (32, 32), 4, 60, 0.0), (9000, (16, 16), 8, 400, 0.5),
-                                                       (9000, (560,), 4, 200, 0.3)])   # (560,): IVF
+                                                       (9000, (560,), 4, 200, 0.3),   # (560,): IVF
+                                                       (12000, (8, 8, 8, 8), 4, 150, 0.0)])   # 4-way: compact cells
 def test_host_tier_decode_matches(T, ks, G, cache_pages, ratio):
     from adaptiveimi_amd import ops, synthetic
     from oracle import hostcache as O
@@ -35,21 +36,37 @@ def test_host_tier_decode_matches(T, ks, G, cache_pages, ratio):
     keys, values = synthetic.make_kv(H, T, seed=41)
     kd, vd = keys.to(DEV), values.to(DEV)
     cent, labels, _ = ops.kmeans(kd, list(ks), 3)
-    idx = ops.build_index(kd, vd, cent, labels, list(ks), n_centroids=int(np.prod(ks)) + 1)
+    four = len(ks) == 4
+    ncells = int(np.prod(ks))
+    idx = ops.build_index(kd, vd, cent, labels, list(ks), n_centroids=min(T, ncells) + 1 if four else ncells + 1)
+    compact = {n: idx[n] for n in ("n_active", "compact_gid", "compact_size", "compact_offset")} if four else None
     sk, sv = synthetic.make_kv(H, static_len + 8, seed=7)
     sk, sv = sk.to(DEV), sv.to(DEV)
-    sz = orc.sizing(T, 0.1, k_override=ks)
+    sz = orc.sizing(T, 0.1, subspace_parts=len(ks) if len(ks) > 1 else 0, k_override=ks)
     bud = ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"])
     plan = ops.DecodePlan(cent, idx["cell_count"], idx["cell_offset"], ks, bud, idx["list_keys"],
-                          idx["list_values"], sk, sv, G)
-    host = ops.HostTierPlan(cent, idx["cell_count"], idx["cell_offset"], ks, bud, idx["list_keys"],
-                            idx["list_values"], sk, sv, G, cache_pages=cache_pages, hot_ratio=ratio)
+                          idx["list_values"], sk, sv, G, compact=compact)
+    # the lists handed over in pinned host memory, as the drop-in cache does
+    hk = torch.empty(tuple(idx["list_keys"].shape), dtype=torch.bfloat16, pin_memory=True)
+    hv = torch.empty_like(hk, pin_memory=True)
+    hk.copy_(idx["list_keys"])
+    hv.copy_(idx["list_values"])
+    host = ops.HostTierPlan(cent, idx["cell_count"], idx["cell_offset"], ks, bud, hk, hv, sk, sv, G,
+                            cache_pages=cache_pages, hot_ratio=ratio, compact=compact)
+    assert host.h_keys.data_ptr() == hk.data_ptr()   # used in place
     lk, lv = bits(idx["list_keys"]), bits(idx["list_values"])
-    counts = idx["cell_count"].cpu().numpy()
-    offs = idx["cell_offset"].cpu().numpy()
-    ncells, ps = counts.shape[1], bud.page_size
-    groups = [O.Group(list(counts[h]) + [0], list(offs[h]) + [offs[h][-1]], cache_pages, ps, bud.buffer_pages,
-                      ratio) for h in range(H)]
+    ps = bud.page_size
+    if four:   # the manager's cells are the occupied cells by compact id
+        na = idx["n_active"].cpu().numpy()
+        csz, coff = idx["compact_size"].cpu().numpy(), idx["compact_offset"].cpu().numpy()
+        groups = [O.Group(list(csz[h, :na[h]]) + [0] * (host.pad + 1 - na[h]),
+                          list(coff[h, :na[h] + 1]) + [coff[h, na[h]]] * (host.pad + 1 - na[h]),
+                          cache_pages, ps, bud.buffer_pages, ratio) for h in range(H)]
+    else:
+        counts = idx["cell_count"].cpu().numpy()
+        offs = idx["cell_offset"].cpu().numpy()
+        groups = [O.Group(list(counts[h]) + [0], list(offs[h]) + [offs[h][-1]], cache_pages, ps, bud.buffer_pages,
+                          ratio) for h in range(H)]
     out_h = torch.empty((H * G, 128), dtype=torch.bfloat16, device=DEV)
     out_r = torch.empty_like(out_h)
     hits = 0

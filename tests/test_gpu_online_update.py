@@ -302,20 +302,23 @@ def test_decode_step_online_matches_oracle(ops, oracle):
     assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)), float(err.max())
 
 
-@pytest.mark.parametrize("ks,steps,batch,thr,ring", [((32, 32), 14, 4, 2, 24), ((6, 6, 6, 6), 14, 4, 2, 24),
-                                                      ((8, 8, 8, 8), 14, 4, 2, 24), ((32, 32), 50, 16, 3, 40),
-                                                      ((256,), 14, 4, 2, 24)])   # (256,): IVF
-def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, thr, ring):
+@pytest.mark.parametrize("ks,steps,batch,thr,ring,host", [
+    ((32, 32), 14, 4, 2, 24, False), ((6, 6, 6, 6), 14, 4, 2, 24, False), ((8, 8, 8, 8), 14, 4, 2, 24, False),
+    ((32, 32), 50, 16, 3, 40, False), ((256,), 14, 4, 2, 24, False),   # (256,): IVF
+    # the host tier (lists in pinned host memory, GPU block cache) with the update
+    # on: the reference's shipped 1M configuration is a 4-way index with async_update
+    ((8, 8, 8, 8), 14, 4, 2, 24, True), ((32, 32), 50, 16, 3, 40, True)])
+def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, thr, ring, host):
     """The drop-in with async_update on, driven like model_hub drives it,
     against a step-by-step oracle replay (update applied at the next step);
-    the last case uses the reference's batch of 16 keys over three batches
-    with a ring that wraps."""
+    the 50-step cases use the reference's batch of 16 keys over three batches
+    with a ring that wraps.  host: the same with runtime_config["host_tier"]."""
     from adaptiveimi_amd import synthetic
     from adaptiveimi_amd.attn_hub.sparse_imi import imi_decode_attn
     from adaptiveimi_amd.cache_hub.adaptive_imi import adpimi_cache
 
     L, S, H, G, D = 2, 4096, 8, 4, 128
-    note(f"[online] drop-in ks={ks} {steps} decode steps")
+    note(f"[online] drop-in ks={ks} {steps} decode steps host_tier={host}")
     kcfg = {f"k{i + 1}": k for i, k in enumerate(ks)}
     kcfg.update(max_iters=3, early_stop_min_iter=3, init="first")
     cache = adpimi_cache(valid_start=[0], layer_num=L, batch_size=1, max_length=S + steps + 1,
@@ -325,7 +328,8 @@ def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, t
                          retrieval_budget=0.1, cache_ratio=0.05, buffer_cluster_num=32, prefill_bsz=1, num_gpus=1,
                          model_size=8, subspace_parts=len(ks) if len(ks) > 1 else 0,
                          runtime_config={"kmeans": kcfg, "async_update": {"enabled": True, "batch": batch,
-                                                                          "threshold": thr, "delta_tokens": ring}})
+                                                                          "threshold": thr, "delta_tokens": ring},
+                                         "host_tier": {"enabled": host}})
     kv = []
     for layer in range(L):
         k, v = synthetic.make_kv(H, S, seed=50 + layer)
@@ -333,11 +337,15 @@ def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, t
         cache.prefill_update_kv_cache(None, k.transpose(0, 1).unsqueeze(0).contiguous().to(DEV),
                                       v.transpose(0, 1).unsqueeze(0).contiguous().to(DEV), layer, 0)
     cache.prepare_cache()
+    torch.cuda.synchronize()   # the host tier's list copies are done
     ncells = int(np.prod(ks))
     # oracle twins of each layer's index (from the device build, whose parity
     # is tested on its own) and update state
     twins = []
     for layer in range(L):
+        lists = cache.host_lists[layer] if host else (cache.list_keys[layer][0], cache.list_values[layer][0])
+        if host:
+            assert cache.list_keys[layer] is None and not lists[0].is_cuda
         meta = cache.compact_meta[layer]
         sizes = meta["compact_size"].cpu().numpy()
         offs = np.zeros((H, sizes.shape[1] + 1), np.int64)
@@ -347,7 +355,7 @@ def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, t
         orc = oracle.OnlineUpdateOracle(meta["compact_centroids"].cpu().numpy(), sizes, cache.padding_cluster_id,
                                         thr, ring)
         twins.append(dict(sizes=sizes, offs=offs, mask=mask, orc=orc, count=0, pending=None,
-                          lk=bits(cache.list_keys[layer][0]), lv=bits(cache.list_values[layer][0])))
+                          lk=bits(lists[0]), lv=bits(lists[1])))
     assert cache.padding_cluster_id == ncells
     g = torch.Generator().manual_seed(7)
     appended = 0
@@ -375,12 +383,19 @@ def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, t
                 tw["orc"].refresh()
                 tw["pending"] = None
             exec_rows = cache.execution_stride - static_len
-            ref, _, rm, _, dr = oracle.decode_step_online(
+            ref, _, rm, rrows, dr = oracle.decode_step_online(
                 bits(q), tw["sizes"], tw["offs"], tw["mask"], tw["lk"],
                 tw["lv"], bits(cache.steady_zone_keys[layer][0]), bits(cache.steady_zone_values[layer][0]),
                 static_len, tw["orc"], cache.nprobe, cache.max_retrieval_tokens, cache.buffer_size, exec_rows)
-            sel = cache._plans[layer].selection
-            assert np.array_equal(sel["n_selected"].cpu().numpy(), rm), (step, layer)
+            plan = cache._plans[layer]
+            if host:   # the buffer's one-cell selection replaced the ranked one in the workspace
+                assert isinstance(plan, ops.HostTierPlan)
+                sel = plan.plan.selection
+                assert np.array_equal(plan.h_nsel.numpy(), rm), (step, layer)
+                assert np.array_equal(sel["n_rows"].cpu().numpy(), [len(r) for r in rrows]), (step, layer)
+            else:
+                sel = plan.selection
+                assert np.array_equal(sel["n_selected"].cpu().numpy(), rm), (step, layer)
             assert [int(x) for x in sel["n_delta"].cpu().numpy()] == [len(d) for d in dr], (step, layer)
             appended += sum(len(d) for d in dr)
             got = out.float().cpu().numpy().reshape(H, G, D)
@@ -391,3 +406,5 @@ def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, t
                 upd = cache._updates[layer]
                 assert np.array_equal(upd.shadow.cpu().numpy(), twins[layer]["orc"].shadow)
     assert appended > 0
+    if host:
+        assert all(cache._plans[layer].hits > 0 for layer in range(L))

@@ -234,14 +234,35 @@ def test_kmeans_early_stop_semantics(ops, oracle):
     assert torch.equal(lab2, labels)
 
 
-def test_reciprocal_is_correctly_rounded(ops):
-    """The M-step multiplies by 1.0f/size; HIP division must round exactly
-    like the host's IEEE division for every size up to 2^20."""
-    note("[recip] 1/n")
-    n = torch.arange(1, 1 << 20, device=DEV, dtype=torch.float32)
-    gpu = (1.0 / n).cpu().numpy()
-    ref = (np.float32(1.0) / np.arange(1, 1 << 20, dtype=np.float32))
-    assert np.array_equal(gpu, ref)
+def test_mstep_reciprocal_over_cluster_sizes(ops, oracle):
+    """The M-step's sum * (1.0f / size) (kmeans_core.cpp:280-290) on the GPU
+    for 127 different cluster sizes and one of several thousand: every member
+    of cluster c repeats the same row, so the sums are exact in any order
+    and the centroids differ from those rows only through the rounding of
+    1/size and of the product -- compared bit for bit with the oracle's host
+    arithmetic after one Lloyd iteration from the rows themselves."""
+    note("[mstep] 1/size over cluster sizes")
+    k = 128
+    sizes = np.arange(1, k + 1)
+    sizes[-1] = 5000
+    T = int(sizes.sum())
+    rng = np.random.default_rng(12)
+    rows = np.zeros((k, 128), np.float32)
+    for c in range(k):   # distinct rows far apart (integers, exact in bf16)
+        rows[c] = rng.integers(-40, 41, size=128) + 97 * (c % 3)
+        rows[c, c % 128] += 200.0
+    lab = np.repeat(np.arange(k), sizes)
+    rng.shuffle(lab)
+    keys = torch.from_numpy(rows[lab]).to(torch.bfloat16).unsqueeze(0).contiguous()
+    init = torch.from_numpy(np.stack([rows[:, :64], rows[:, 64:]])[None]).contiguous()
+    cent, labels, _ = ops.kmeans(keys.to(DEV), [k, k], 1, init_centroids=init.to(DEV))
+    kf = oracle.bf16_to_f32(bits(keys))
+    labs, cents, _ = oracle.kmeans_head(kf[0], [k, k], 1, init="given",
+                                        init_centroids=[rows[:, :64], rows[:, 64:]])
+    for p in range(2):
+        assert np.array_equal(labels.cpu().numpy()[0, p], lab), p
+        assert np.array_equal(labs[p], lab), p
+        assert np.array_equal(cent.cpu().numpy()[0, p], cents[p]), p
 
 
 # ---------------------------------------------------------- cell index ----
@@ -630,6 +651,86 @@ def test_config3_shape_decode_matches_oracle(ops, oracle):
     _check_attention(res, ref)
 
 
+def test_config4_build_and_decode_match_oracle(ops, oracle):
+    """configs[4] per KV head at its own size: 1,048,480 listed tokens, IMI
+    2 x 128 centroids, 20 Lloyd iterations on the evenly strided
+    65,536-key sample, then every key assigned to the final centroids
+    (kmeans_core.cpp:190-314 on the sample, the E-step 222-242 over all
+    keys); the index (reorganize_core.cpp:18-311) and one decode step at
+    budget 0.02 (runtime.py:31-63: nprobe 328, max_tokens 20969, 2622
+    pages).  Centroids, the full 1M assignment, the CSR, the permutation,
+    the list rows and the selected cells are bit-exact with the oracle;
+    attention within 2e-2 abs + 1e-2 rel."""
+    from adaptiveimi_amd import synthetic
+
+    H, G, ks, iters, sample, budget = 2, 4, (128, 128), 20, 65536, 0.02
+    T = 1048576 - 96
+    note(f"[config4] H={H} T={T} ks={ks} iters={iters} sample={sample} budget={budget}")
+    keys, values = _kv(H, T, seed=444)
+    kd, vd = keys.to(DEV), values.to(DEV)
+    cent, labels, _ = ops.kmeans_sampled(kd, list(ks), iters, sample)
+    ncells = ks[0] * ks[1]
+    out = ops.build_index(kd, vd, cent, labels, list(ks), n_centroids=ncells + 1)
+    torch.cuda.synchronize()
+    step = -(-T // sample)
+    assert step == 16 and len(range(0, T, step)) == 65530
+    kf = keys.float().numpy()   # exact bf16 widen
+    kb, vb = bits(keys), bits(values)
+    sl = oracle.subspace_slices(128, 2)
+    cg, lg = cent.cpu().numpy(), labels.cpu().numpy()
+    perm, cnt, off = out["perm"].cpu().numpy(), out["cell_count"].cpu().numpy(), out["cell_offset"].cpu().numpy()
+    heads = []
+    for h in range(H):
+        _, rc, it = oracle.kmeans_head(kf[h, ::step], list(ks), iters)
+        assert it == [iters, iters]
+        labs = []
+        for p in range(2):
+            assert np.array_equal(cg[h, p, : ks[p]], rc[p]), (h, p)
+            lab, _, _ = oracle.estep(np.ascontiguousarray(kf[h][:, sl[p]]), rc[p])
+            assert np.array_equal(lg[h, p], lab), (h, p)
+            labs.append(lab)
+        r = oracle.compact_reorg(labs, list(ks))
+        na = r["n_active"]
+        assert int(out["n_active"][h]) == na
+        assert np.array_equal(out["compact_gid"][h, :na].cpu().numpy(), r["gids"]), h
+        assert np.array_equal(out["compact_offset"][h, : na + 1].cpu().numpy(), r["offsets"]), h
+        assert np.array_equal(perm[h], r["perm"]), h
+        full_cnt = np.zeros(ncells, np.int32)
+        full_cnt[r["gids"]] = np.diff(r["offsets"])
+        assert np.array_equal(cnt[h], full_cnt), h
+        assert off[h, 0] == 0 and np.array_equal(np.diff(off[h]), full_cnt), h
+        # list rows = the permuted keys / values, compared on the device
+        ph = out["perm"][h].long()
+        assert torch.equal(out["list_keys"][h], kd[h, ph]) and torch.equal(out["list_values"][h], vd[h, ph]), h
+        heads.append(dict(n_active=na, offsets=r["offsets"], merged=oracle.merged_centroids(rc, r["gids"], list(ks)),
+                          list_keys=kb[h][r["perm"]], list_values=vb[h][r["perm"]], gids=r["gids"]))
+    del kf
+    sz = oracle.sizing(T, budget, k_override=ks)
+    bud = ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"])
+    assert (bud.nprobe, bud.max_tokens, bud.buffer_pages) == (328, 20969, 2622)
+    static_len = 97
+    sk, sv = synthetic.make_kv(H, static_len + 8, seed=79)
+    plan = ops.DecodePlan(cent, out["cell_count"], out["cell_offset"], ks, bud, out["list_keys"],
+                          out["list_values"], sk.to(DEV), sv.to(DEV), G)
+    plan.set_static_len(static_len)
+    q = synthetic.make_queries(keys, G, seed=7)[0]
+    plan.query.copy_(q.to(DEV))
+    res = plan.step().clone()
+    torch.cuda.synchronize()
+    ref, rs, rm, rrows = oracle.decode_step(bits(q), heads, bits(sk), bits(sv), static_len, sz["n_centroids"],
+                                            bud.nprobe, bud.max_tokens, bud.buffer_pages)
+    sel = plan.selection
+    assert np.array_equal(sel["n_selected"].cpu().numpy(), rm)
+    cells, nrows = sel["sel_cell"].cpu().numpy(), sel["n_rows"].cpu().numpy()
+    for h in range(H):
+        assert np.array_equal(cells[h, : rm[h]], heads[h]["gids"][rs[h, : rm[h]]]), h
+        assert nrows[h] == len(rrows[h]), h
+    note(f"[config4] selected cells {rm.tolist()}, rows {nrows.tolist()}")
+    # nprobe binds (328 cells of ~53 rows stay under max_tokens and the pages)
+    assert (rm == bud.nprobe).all() and (nrows < bud.max_tokens).all() and (nrows > 10000).all(), (rm, nrows)
+    _check_attention(res, ref)
+
+
 @pytest.mark.parametrize("ks,lens", [((32, 32), (3000, 6000, 9000, 12000)), ((6, 6, 6, 6), (3000, 6000, 9000, 12000)),
                                      ((32, 32), (2000, 12000)), ((32, 32), (3000, 4500, 6000, 9000, 12000)),
                                      # configs[2] at its own lengths (32k-128k, 64 x 64, 16 KV heads, GQA 7)
@@ -870,3 +971,47 @@ def test_select_refinement_paths(ops, oracle, case):
         for h in range(H):
             assert np.array_equal(sel["sel_cell"].cpu().numpy()[h, : m[h]], gids[h][rs[h, : rm[h]]]), h
         assert np.array_equal(sel["n_rows"].cpu().numpy(), rtok)
+
+
+@pytest.mark.parametrize("ks", [(64, 64), (128, 128), (32, 32)])
+def test_select_screen_across_offsets(ops, oracle, ks):
+    """The selection screens cells by p1[l0] + q1[l1] with a rounding bound
+    and computes exact chains for the candidates only, falling back to every
+    cell's chain when the score range is narrow next to the bound.  A common
+    offset added to every centroid grows the scores' magnitude (hence the
+    bound) at a fixed spread, so the sweep crosses from the screened ranking
+    into the fallback; 6 queries per offset, every selection bit-exact with
+    the oracle's exhaustive ranking."""
+    note(f"[select] screen across offsets ks={ks}")
+    H, T = 4, 30000
+    keys, values = _kv(H, T, seed=23)
+    kd, vd = keys.to(DEV), values.to(DEV)
+    cent0, labels, _ = ops.kmeans(kd, list(ks), 3)
+    out = ops.build_index(kd, vd, cent0, labels, list(ks), n_centroids=ks[0] * ks[1] + 1)
+    gids = out["compact_gid"].cpu().numpy()
+    size, mask = out["compact_size"].cpu().numpy(), out["compact_mask"].cpu().numpy()
+    na = out["n_active"].cpu().numpy()
+    from adaptiveimi_amd import synthetic
+
+    qs = synthetic.make_queries(keys, 4, seed=9, n_queries=6)
+    u = torch.randn((2, 64), generator=torch.Generator().manual_seed(1)).to(DEV)
+    bud = ops.Budget(round(ks[0] * ks[1] * 0.1), int(0.1 * T), -(-int(0.1 * T) // 8))
+    for off in (0.0, 3.0, 30.0, 300.0, 3000.0, 3e4):
+        cent = cent0.clone()
+        cent[:, :, : max(ks)] += off * u[None, :, None, :]
+        merged = np.zeros((H, ks[0] * ks[1] + 1, 128), np.float32)
+        cc = cent.cpu().numpy()
+        for h in range(H):
+            merged[h, : na[h]] = oracle.merged_centroids([cc[h, 0, : ks[0]], cc[h, 1, : ks[1]]], gids[h, : na[h]],
+                                                         list(ks))
+        for n in range(qs.shape[0]):
+            q = qs[n]
+            sel = ops.select(q.to(DEV), cent, out["cell_count"], out["cell_offset"], ks, bud)
+            sc = oracle.scores(bits(q), merged)
+            rs, rm, rtok = oracle.select(sc, size, mask, bud.nprobe, bud.max_tokens, bud.buffer_pages)
+            m = sel["n_selected"].cpu().numpy()
+            assert np.array_equal(m, rm), (off, n)
+            cells = sel["sel_cell"].cpu().numpy()
+            for h in range(H):
+                assert np.array_equal(cells[h, : m[h]], gids[h][rs[h, : rm[h]]]), (off, n, h)
+            assert np.array_equal(sel["n_rows"].cpu().numpy(), rtok), (off, n)

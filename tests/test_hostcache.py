@@ -174,3 +174,29 @@ def test_library_rejects_bad_arguments(L):
         assert L.imi_hostcache_access(h, _p(keys), 5, *map(_p, lists)) == 1
     finally:
         L.imi_hostcache_destroy(h)
+    # two groups: a bad key in the second group rejects the whole access
+    # before the first group's outputs or lists change, and an update after
+    # the rejection admits nothing
+    _lib.check(L.imi_hostcache_create(2, 4, 4, 2, 4, 4, 0.3, ctypes.byref(h)), "create")
+    try:
+        sizes = np.array([2, 2, 2, 0] * 2, np.int32)
+        offsets = np.array([0, 2, 4, 6, 6] * 2, np.int32)
+        _lib.check(L.imi_hostcache_set_metadata(h, _p(sizes), _p(offsets)), "set_metadata")
+        lists = _lists(4, 2) + _lists(4, 2)
+        good = np.array([0, 1, 2, 1], np.int64)
+        _lib.check(L.imi_hostcache_access(h, _p(good), 2, *map(_p, lists)), "access")
+        assert lists[7].tolist() == [2, 2]   # misses per group (nothing cached yet)
+        for a in lists:
+            a.fill(-5)
+        bad = np.array([0, 1, 2, 9], np.int64)
+        assert L.imi_hostcache_access(h, _p(bad), 2, *map(_p, lists)) == 1
+        assert "outside" in L.imi_last_error().decode()
+        assert all((a == -5).all() for a in lists)
+        upd = _lists(4, 2)
+        _lib.check(L.imi_hostcache_update(h, *map(_p, upd)), "update")
+        assert upd[3].tolist() == [0, 0]
+        # a valid access afterwards still sees an empty cache
+        _lib.check(L.imi_hostcache_access(h, _p(good), 2, *map(_p, lists)), "access")
+        assert lists[3].tolist() == [0, 0] and lists[7].tolist() == [2, 2]
+    finally:
+        L.imi_hostcache_destroy(h)
