@@ -139,6 +139,7 @@ struct DecParams {
     float* part_ml;            // [total][G][2]
     uint16_t* out;             // [H*G][128]
     float* lse;                // [H*G] or null
+    int fixed_nt;              // tiles per wave of the fixed-grid split pass, 0: row-balanced
 };
 static_assert(offsetof(DecParams, q) == 64 && offsetof(DecParams, H) == 128 && offsetof(DecParams, total) == 192,
               "prologue fields in the first 128 bytes, lookup and load fields in the next 64");
@@ -702,6 +703,294 @@ __global__ __launch_bounds__(256) void merge_kernel(DecParams a, int G) {
     }
 }
 
+
+// ------------------------------------------------- fixed-grid split pass
+// The decode step's split pass when every head has the same row bound and at
+// most kFixedCap selected cells (the selection of imi_select: every cell
+// holds at least one row): workgroup b takes split b / H of head
+// (b % H + split) % H and the rows [split * 64 NT, + 64 NT) of that head's
+// [static | selected | delta] rows, NT tiles of 16 rows per wave, the tile
+// loop unrolled at compile time.  The head's selection is staged in LDS in
+// one round trip; each wave finds the cell of its first row with two ballot
+// rounds over the staged prefix, flags the window offsets where the next
+// cells start and counts the flags up to each row.  A split past the head's
+// rows writes an empty partial (max -inf, sum 0), which the merge weighs 0.
+// At configs[1] this form runs the split pass in 12.4 us against 13.3 us for
+// the row-balanced form (whose per-split ranges follow the rows each head
+// actually selected, for ragged batches and larger shapes).
+constexpr int kFixedCap = 2048;   // selected cells per head the fixed grid stages
+
+__device__ __forceinline__ int popc_upto(uint64_t lo, uint64_t hi, int i) {   // set bits at positions 0..i
+    if (i < 64) return __builtin_popcountll(lo & (~0ull >> (63 - i)));
+    return __builtin_popcountll(lo) + __builtin_popcountll(hi & (~0ull >> (127 - i)));
+}
+
+template <int G, int NT, bool DELTA>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void fixed_attention_kernel(
+    DecParams a) {
+    constexpr int RW = NT * 16;                 // rows per wave
+    constexpr int NRL = (RW + 63) / 64;         // row locations per lane
+    static_assert(NRL <= 2, "the row lookup covers windows of at most 128 rows");
+    constexpr int SU = (kFixedCap + kThreads) / kThreads;
+    constexpr int DU = kDeltaMax / kThreads;
+    __shared__ float s_acc[kWaves][G][128];
+    __shared__ float s_ml[kWaves][G][2];
+    __shared__ int s_pre[kFixedCap + 1];
+    __shared__ int s_off[kFixedCap];
+    __shared__ int s_drow[DELTA ? kDeltaMax : 1];
+    __shared__ int s_flag[kWaves][NRL * 64];
+    __shared__ __attribute__((aligned(16))) uint16_t s_v[kWaves][16 * kVStride];
+    __shared__ __attribute__((aligned(16))) uint16_t s_k[kWaves][16 * kVStride];
+
+    const int b = blockIdx.x;
+    const int H = a.H, S = a.run[0].z & 0xFFFF;
+    const int split = b / H;
+    const int h = (b % H + split) % H;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lg = lane >> 4, ln = lane & 15;
+    const int row0 = split * (64 * NT) + wave * RW;
+
+    // one round trip: q (as the MFMA B operand: column ln = query ln % G,
+    // dims 32c + 8lg ..), the row and cell counts, the head's selection (row
+    // prefix and CSR offset per cell) and its delta rows
+    u32x4_t qb[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        qb[c] = *reinterpret_cast<const u32x4_t*>(a.q + (static_cast<int64_t>(h) * G + ln % G) * 128 + c * 32 + lg * 8);
+    const int nrows_raw = vec_load_i32(a.g_nrows, h);
+    const int m_raw = vec_load_i32(a.g_nsel, h);
+    const int nd_raw = DELTA ? vec_load_i32(a.g_ndelta, h) : 0;
+    {
+        const int32_t* pre = a.g_prefix + static_cast<int64_t>(h) * (a.g_cap + 1);
+        const int32_t* off = a.g_offset + static_cast<int64_t>(h) * a.g_cap;
+        int pv[SU], ov[SU];
+#pragma unroll
+        for (int u = 0; u < SU; ++u) {
+            const int i = tid + u * kThreads;
+            pv[u] = i <= a.g_cap ? pre[i] : 0;
+            ov[u] = i < a.g_cap ? off[i] : 0;
+        }
+        int dv[DELTA ? DU : 1];
+        if constexpr (DELTA) {
+#pragma unroll
+            for (int u = 0; u < DU; ++u) {
+                const int i = tid + u * kThreads;
+                dv[u] = i < a.g_dcap ? a.g_drows[static_cast<int64_t>(h) * a.g_dcap + i] : 0;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SU; ++u) {
+            const int i = tid + u * kThreads;
+            if (i <= a.g_cap) s_pre[i] = pv[u];
+            if (i < a.g_cap) s_off[i] = ov[u];
+        }
+        if constexpr (DELTA) {
+#pragma unroll
+            for (int u = 0; u < DU; ++u) s_drow[tid + u * kThreads] = dv[u];
+        }
+    }
+    __syncthreads();
+    const int nrows = max(__builtin_amdgcn_readfirstlane(nrows_raw), 0);
+    const int m = min(max(__builtin_amdgcn_readfirstlane(m_raw), 0), a.g_cap);
+    const int nd = DELTA ? min(max(__builtin_amdgcn_readfirstlane(nd_raw), 0), a.g_dcap) : 0;
+    const int sl = a.static_len;
+    // rows: [static_len steady rows | nrows list rows | nd delta rows (steady)]
+    const int N = sl + nrows + nd;
+    const int64_t pidx = static_cast<int64_t>(h) * S + split;
+    if (split * (64 * NT) >= N) {   // no rows in this split: an empty partial
+        for (int o = tid; o < G * 128; o += kThreads) a.part_acc[pidx * G * 128 + o] = 0.0f;
+        if (tid < G) {
+            a.part_ml[(pidx * G + tid) * 2 + 0] = -INFINITY;
+            a.part_ml[(pidx * G + tid) * 2 + 1] = 0.0f;
+        }
+        return;
+    }
+
+    // list row of window row i (rows row0 + i, i = lane + 64 r): the cell c0
+    // holding the wave's first list row j0 comes from two ballot rounds over
+    // the staged prefix, the window offsets where the following cells start
+    // are flagged, and the flags are counted up to each row.  Locations are
+    // clamped to the list; a delta row gets -1 - its steady row (clamped to
+    // the steady zone).
+    int loc[NRL];
+    {
+        const int j0 = max(row0 - sl, 0);
+        int c0 = 0;
+        if (m > 1) {
+            const int step = (m + 63) >> 6;   // <= 32 cells per lane sample
+            const int cs = lane * step;
+            const uint64_t b1 = __builtin_amdgcn_ballot_w64(cs < m && s_pre[cs] <= j0);
+            const int base = (63 - __builtin_clzll(b1 | 1ull)) * step;
+            const int cc = base + lane;
+            const uint64_t b2 = __builtin_amdgcn_ballot_w64(lane < step && cc < m && s_pre[cc] <= j0);
+            c0 = base + (63 - __builtin_clzll(b2 | 1ull));
+        }
+        int* fl = s_flag[wave];
+#pragma unroll
+        for (int r = 0; r < NRL; ++r) fl[lane + 64 * r] = 0;
+        wave_lds_sync();
+#pragma unroll
+        for (int r = 0; r < NRL; ++r) {
+            const int c = c0 + 1 + lane + 64 * r;
+            if (c < m) {
+                const int o = s_pre[c] - j0;
+                if (o > 0 && o < NRL * 64) fl[o] = 1;
+            }
+        }
+        wave_lds_sync();
+        uint64_t fm[2] = {0ull, 0ull};
+#pragma unroll
+        for (int r = 0; r < NRL; ++r) fm[r] = __builtin_amdgcn_ballot_w64(fl[lane + 64 * r] != 0);
+        const int lmax = max(a.list_rows - 1, 0);
+#pragma unroll
+        for (int r = 0; r < NRL; ++r) {
+            const int j = row0 + lane + 64 * r - sl;
+            int l = 0;
+            if (j >= 0 && j < nrows) {
+                const int c = c0 + popc_upto(fm[0], fm[1], j - j0);
+                l = min(max(s_off[c] + (j - s_pre[c]), 0), lmax);
+            } else if (DELTA && j >= nrows && j < nrows + nd) {
+                l = -1 - min(max(s_drow[j - nrows], 0), a.s_stride - 1);
+            }
+            loc[r] = l;
+        }
+    }
+
+    const uint16_t* skh = a.sk + static_cast<int64_t>(h) * a.s_stride * 128;
+    const uint16_t* svh = a.sv + static_cast<int64_t>(h) * a.s_stride * 128;
+    const uint16_t* lkh = a.lk + static_cast<int64_t>(h) * a.list_rows * 128;
+    const uint16_t* lvh = a.lv + static_cast<int64_t>(h) * a.list_rows * 128;
+    f32x4_t acc[8];   // acc[d][r] = O[query slot 4lg + r][dim 16d + ln]
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[d] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_own = -INFINITY, l_own = 0.0f;   // softmax state of query slot ln
+    uint16_t* sv = s_v[wave];
+    uint16_t* sk = s_k[wave];
+    if (row0 < N) {
+        // tile t: rows t*16 + 4it + rg, 16 lanes x 16 bytes per row; rows past
+        // N read list row 0 (in bounds) and are masked below
+        const int rg = lane >> 4, li = lane & 15;
+        u32x4_t kb[2][4], vb[2][4];
+        auto load = [&](int t, int slot) {
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int jt = t * 16 + it * 4 + rg;
+                const int n = row0 + jt;
+                const int lr = __shfl(loc[(t * 16) >> 6], jt & 63);
+                const bool st = n < sl;
+                const bool dl = DELTA && !st && n < N && lr < 0;   // delta row: steady row -1 - lr
+                const int64_t roff =
+                    (st ? static_cast<int64_t>(n) : static_cast<int64_t>(dl ? -1 - lr : (n < N ? lr : 0))) * 128;
+                kb[slot][it] = __builtin_nontemporal_load((g_u32x4_t*)((st || dl ? skh : lkh) + roff + li * 8));
+                vb[slot][it] = __builtin_nontemporal_load((g_u32x4_t*)((st || dl ? svh : lvh) + roff + li * 8));
+            }
+        };
+        load(0, 0);
+        if (NT > 1) load(1, 1);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int slot = t & 1;
+            // K and V tiles -> LDS, row-major [token][dim]; K comes back in
+            // the MFMA A layout (lane -> token ln, dims 32c + 8lg)
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                *reinterpret_cast<u32x4_t*>(sv + (4 * it + rg) * kVStride + li * 8) = vb[slot][it];
+                *reinterpret_cast<u32x4_t*>(sk + (4 * it + rg) * kVStride + li * 8) = kb[slot][it];
+            }
+            wave_lds_sync();
+            u32x4_t ka[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) ka[c] = *reinterpret_cast<const u32x4_t*>(sk + ln * kVStride + c * 32 + lg * 8);
+            f32x4_t s4 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                s4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka[c]),
+                                                             __builtin_bit_cast(bf16x8_t, qb[c]), s4, 0, 0, 0);
+            if (t + 2 < NT) load(t + 2, slot);
+            float s[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[i] = (row0 + t * 16 + 4 * lg + i < N) ? s4[i] * a.scale_log2 : -INFINITY;
+            float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+            tm = fmaxf(tm, xor16(tm));
+            tm = fmaxf(tm, xor32(tm));
+            const float mn = fmaxf(m_own, tm);
+            const float corr = wexp(m_own, mn);
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[i] = wexp(s[i], mn);   // 0 for masked rows
+            l_own = l_own * corr + ((p[0] + p[1]) + (p[2] + p[3]));
+            m_own = mn;
+            if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
+                // O row 4lg + r belongs to query slot 4lg + r: its factor sits
+                // in lane 16lg + 4lg + r (any lane of that slot would do)
+                float cr[4];
+                if (4 % G == 0) {
+                    cr[0] = dpp_f32<0x00>(corr);
+                    cr[1] = dpp_f32<0x55>(corr);
+                    cr[2] = dpp_f32<0xAA>(corr);
+                    cr[3] = dpp_f32<0xFF>(corr);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 16 * lg + 4 * lg + r);
+                }
+#pragma unroll
+                for (int d = 0; d < 8; ++d) {
+                    acc[d][0] *= cr[0];
+                    acc[d][1] *= cr[1];
+                    acc[d][2] *= cr[2];
+                    acc[d][3] *= cr[3];
+                }
+            }
+            u32x2_t pa;
+            pa.x = pack_bf16(p[0], p[1]);
+            pa.y = pack_bf16(p[2], p[3]);
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                // lane (lg, ln) gets V[token 4lg + e][dim 16d + ln], e = 0..3
+                const s16x4_t vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4_t*)(sv + (4 * lg + (ln >> 2)) * kVStride + d * 16 + 4 * (ln & 3)));
+                acc[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, pa), vt, acc[d], 0,
+                                                                   0, 0);
+            }
+            wave_lds_sync();
+        }
+    }
+    // sum over the four lane groups (different tokens, shared max)
+    l_own += xor16(l_own);
+    l_own += xor32(l_own);
+    // query g: O row g (lane group g / 4, register g % 4), state of slot g
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        if (lg == g / 4) {
+#pragma unroll
+            for (int d = 0; d < 8; ++d) s_acc[wave][g][d * 16 + ln] = acc[d][g % 4];
+        }
+    if (lg == 0 && ln < G) {
+        s_ml[wave][ln][0] = m_own;
+        s_ml[wave][ln][1] = l_own;
+    }
+    __syncthreads();
+    // workgroup partial (waves merged in order)
+    for (int o = tid; o < G * 128; o += kThreads) {
+        const int g = o >> 7, d = o & 127;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_ml[w][g][0]);
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float wt = wexp(s_ml[w][g][0], M);
+            L += s_ml[w][g][1] * wt;
+            A += s_acc[w][g][d] * wt;
+        }
+        a.part_acc[(pidx * G + g) * 128 + d] = A;
+        if (d == 0) {
+            a.part_ml[(pidx * G + g) * 2 + 0] = M;
+            a.part_ml[(pidx * G + g) * 2 + 1] = L;
+        }
+    }
+}
+
 // Rows one split may hold for any call of this shape: any static_len up to
 // steady_stride (so one workspace and one captured launch shape stay valid
 // while the steady zone grows), the selected rows, the delta rows.
@@ -746,14 +1035,36 @@ struct SplitPlan {
     int S = 0;
     int total = 0;   // workgroups = partials
     int nr = 0;      // the short form's row locations per lane
+    int fixed_nt = 0;   // tiles per wave of the fixed grid (0: row-balanced)
     int4 run[kMaxRuns];
 };
 
-SplitPlan split_plan(const imi_attention_args* a) {
+// Tiles per wave of the fixed-grid split pass: the fewest in [4, 8] whose
+// grid (64 NT rows per workgroup) fits the CUs in one round, or 0.  Only for
+// selections made by imi_select (fixed_ok: every selected cell holds a row)
+// with one row bound for every head.
+int fixed_tiles(const imi_attention_args* a, bool fixed_ok) {
+    if (!fixed_ok || a->sel_cap > kFixedCap) return 0;
+    if (a->head_rows_bound)
+        for (int h = 1; h < a->kv_heads; ++h)
+            if (a->head_rows_bound[h] != a->head_rows_bound[0]) return 0;
+    const int64_t rb = rows_bound(a);
+    for (int nt = 4; nt <= 8; ++nt)
+        if (static_cast<int64_t>(a->kv_heads) * ((rb + 64 * nt - 1) / (64 * nt)) <= device_cus()) return nt;
+    return 0;
+}
+
+SplitPlan split_plan(const imi_attention_args* a, bool fixed_ok = false) {
     SplitPlan P;
     const int H = a->kv_heads;
     const int64_t rb = rows_bound(a);
     for (int r = 0; r < kMaxRuns; ++r) P.run[r] = make_int4(INT_MAX, H, 0, 0);
+    if ((P.fixed_nt = fixed_tiles(a, fixed_ok)) > 0) {
+        P.S = static_cast<int>((rb + 64 * P.fixed_nt - 1) / (64 * P.fixed_nt));
+        P.total = H * P.S;
+        P.run[0] = make_int4(0, 0, P.S | (H << 16), static_cast<int>(div_magic(H)));
+        return P;
+    }
     if (a->head_rows_bound && H > 1) {
         int nruns = 0;
         int h0[kMaxRuns];
@@ -804,8 +1115,8 @@ SplitPlan split_plan(const imi_attention_args* a) {
     return P;
 }
 
-size_t attn_workspace(const imi_attention_args* a, DecParams* p) {
-    const SplitPlan P = split_plan(a);
+size_t attn_workspace(const imi_attention_args* a, DecParams* p, bool fixed_ok = false) {
+    const SplitPlan P = split_plan(a, fixed_ok);
     Carver cv(a->workspace);
     float* acc = cv.take<float>(static_cast<size_t>(P.total) * a->groups * 128);
     float* ml = cv.take<float>(static_cast<size_t>(P.total) * a->groups * 2);
@@ -814,6 +1125,7 @@ size_t attn_workspace(const imi_attention_args* a, DecParams* p) {
         p->part_ml = ml;
         p->total = P.total;
         p->nr = P.nr;
+        p->fixed_nt = P.fixed_nt;
         for (int r = 0; r < kMaxRuns; ++r) p->run[r] = P.run[r];
     }
     return cv.used();
@@ -900,7 +1212,22 @@ int launch_att(const DecParams& p, hipStream_t stream) {
         attr_set = true;
     }
     const size_t lds_fast = static_cast<size_t>(fast_words<G>()) * 4;
-    if (p.nr == 2) {
+    if (p.fixed_nt > 0) {
+        const bool delta = p.g_drows != nullptr;
+        auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(p.total), dim3(kThreads), 0, stream, p); };
+        switch (p.fixed_nt * 2 + (delta ? 1 : 0)) {
+            case 8: go(fixed_attention_kernel<G, 4, false>); break;
+            case 9: go(fixed_attention_kernel<G, 4, true>); break;
+            case 10: go(fixed_attention_kernel<G, 5, false>); break;
+            case 11: go(fixed_attention_kernel<G, 5, true>); break;
+            case 12: go(fixed_attention_kernel<G, 6, false>); break;
+            case 13: go(fixed_attention_kernel<G, 6, true>); break;
+            case 14: go(fixed_attention_kernel<G, 7, false>); break;
+            case 15: go(fixed_attention_kernel<G, 7, true>); break;
+            case 16: go(fixed_attention_kernel<G, 8, false>); break;
+            default: go(fixed_attention_kernel<G, 8, true>); break;
+        }
+    } else if (p.nr == 2) {
         hipLaunchKernelGGL((attention_kernel<G, 2>), dim3(p.total), dim3(kThreads), lds_fast, stream, p);
     } else if (p.nr == 4) {
         hipLaunchKernelGGL((attention_kernel<G, 4>), dim3(p.total), dim3(kThreads), lds_fast, stream, p);
@@ -933,10 +1260,11 @@ int attn_run(const DecParams& p, int groups, hipStream_t stream, int kernels) {
     return IMI_OK;
 }
 
-// Attention over a selection held in global memory.
-int attn_launch_given(const imi_attention_args* a, hipStream_t stream, int kernels) {
+// Attention over a selection held in global memory (fixed_ok: made by
+// imi_select, so every selected cell holds a row).
+int attn_launch_given(const imi_attention_args* a, hipStream_t stream, int kernels, bool fixed_ok = false) {
     DecParams p{};
-    attn_workspace(a, &p);
+    attn_workspace(a, &p, fixed_ok);
     fill_common(a, &p);
     p.g_prefix = a->sel_prefix;
     p.g_offset = a->sel_offset;
@@ -1015,7 +1343,7 @@ DecodeLayout decode_layout(const imi_decode_args* a, void* ws) {
     L.zero_at = L.sel_ws;
     imi_attention_args t = a->attn;
     t.workspace = nullptr;
-    L.attn_bytes = attn_workspace(&t, nullptr);
+    L.attn_bytes = attn_workspace(&t, nullptr, true);
     L.attn_ws = cv.take<char>(L.attn_bytes);
     L.total = cv.used();
     return L;
@@ -1097,7 +1425,7 @@ int decode_run(const imi_decode_args* a, void* ws, hipStream_t stream) {
     t.delta_rows = s.ring_cap > 0 ? s.delta_rows : nullptr;
     t.n_delta = s.ring_cap > 0 ? s.n_delta : nullptr;
     t.delta_cap = s.ring_cap > 0 ? s.ring_cap : 0;
-    return attn_launch_given(&t, stream, kernels);
+    return attn_launch_given(&t, stream, kernels, true);
 }
 }  // namespace
 
