@@ -55,6 +55,7 @@ struct KmParams {
     float tol;
     int es_min;
     float es_rel;
+    int exact;         // the E-step's distances are read (min distances or the early-stop inertia)
 };
 
 struct Draws {
@@ -110,8 +111,8 @@ __device__ __forceinline__ float l2_lanes8(const float (&x)[DP], const float* cr
 // The same distance with the row still in its bf16 load registers (each
 // 16-byte part holds dims i .. i+7 of lanes 0..7): no float copy of the row,
 // for kernels that keep many rows in flight.
-template <int DP>
-__device__ __forceinline__ float l2_lanes8_bf16(const uint4 (&v)[DP / 8], const float* cr) {
+template <int DP, typename V>
+__device__ __forceinline__ float l2_lanes8_bf16(const V (&v)[DP / 8], const float* cr) {
     float acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
@@ -285,6 +286,7 @@ typedef __attribute__((ext_vector_type(4))) short km_s16x4_t;
 typedef __attribute__((address_space(3))) km_s16x4_t km_lds_s16x4_t;
 
 constexpr int kScreenMaxK = 128;
+constexpr int kScreenQueue = 64;   // queued exact passes per 256-token block
 
 __device__ __forceinline__ uint32_t xor16_u(uint32_t v) { return __float_as_uint(xor16(__uint_as_float(v))); }
 __device__ __forceinline__ uint32_t xor32_u(uint32_t v) { return __float_as_uint(xor32(__uint_as_float(v))); }
@@ -302,12 +304,12 @@ size_t screen_lds_bytes(int kmax) {
     constexpr int KH = DP / 32;
     const size_t nct = (kmax + 15) / 16;
     return static_cast<size_t>(kmax) * (DP + 4) * 4 + nct * KH * 2 * 64 * 16 + nct * 16 * 4 + 256 * 2 * 8 +
-           4 * static_cast<size_t>(kmax) * 4 + 64;
+           4 * static_cast<size_t>(kmax) * 4 + 16 + (kScreenQueue + 1) * 4;
 }
 
 // KT > 0: every segment has k = 16 KT centroids (whole tiles, no per-tile
 // tests); KT = 0: any k <= MAXK.
-template <int DP, int MAXK, int KT>
+template <int DP, int MAXK, int KT, bool EXACT>
 __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, int chunks) {
     constexpr int KH = DP / 32;   // 32-dim K steps per subvector
     constexpr int NCT = KT > 0 ? KT : MAXK / 16;   // centroid tiles held per lane
@@ -326,6 +328,8 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
     uint64_t* cmask = reinterpret_cast<uint64_t*>(ccs + nct_max * 16);      // [256][2] candidate bits
     int* wcnt = reinterpret_cast<int*>(cmask + 256 * 2);                     // [4][kmax]
     float* red = reinterpret_cast<float*>(wcnt + 4 * a.kmax);               // [4]
+    int* qtok = reinterpret_cast<int*>(red + 4);                            // [kScreenQueue] queued tokens
+    int* qcnt = qtok + kScreenQueue;                                        // queue length
 
     const float* cg = a.cent + static_cast<int64_t>(seg) * a.kmax * DP;
     {
@@ -343,6 +347,7 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
             if (i < k * DP) *reinterpret_cast<float4*>(cs + (i / DP) * CS + i % DP) = v[u];
         }
     }
+    if (tid == 0) *qcnt = 0;
     __syncthreads();
     // A operands: lane l of tile ct holds centroid 16ct + l%16, dims
     // 32kh + 8(l/16) .. +7 (v_mfma_f32_16x16x32_bf16 A layout)
@@ -414,11 +419,13 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
                                                               8 * (lane >> 4));
     }
     // the thread's own token row for the exact pass, loaded now as well
-    km_u32x4_t xr[DP / 8];
-    const int tc = min(t, a.T - 1);
+    km_u32x4_t xr[EXACT ? DP / 8 : 1];
+    if constexpr (EXACT) {
+        const int tc = min(t, a.T - 1);
 #pragma unroll
-    for (int i = 0; i < DP / 8; ++i)
-        xr[i] = *reinterpret_cast<const km_u32x4_t*>(kb + static_cast<int64_t>(tc) * a.ts + 8 * i);
+        for (int i = 0; i < DP / 8; ++i)
+            xr[i] = *reinterpret_cast<const km_u32x4_t*>(kb + static_cast<int64_t>(tc) * a.ts + 8 * i);
+    }
     // screening: token tile j = tokens 16j .. 16j+15 of this wave's 64.
     // e(c) = |c|^2 - 2 x.c orders the centroids like D~ = |x|^2 + e(c).
 #pragma unroll
@@ -495,38 +502,79 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
     }
     km_wave_lds_sync();
 
-    // exact reference distance to the candidates, one token per thread
-    float x[DP];
-#pragma unroll
-    for (int i = 0; i < DP / 8; ++i) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            x[8 * i + 2 * w] = bf16_lo(xr[i][w]);
-            x[8 * i + 2 * w + 1] = bf16_hi(xr[i][w]);
-        }
-    }
     float best = 3.402823466e38f;  // FLT_MAX
     int arg = 0;
+    if constexpr (EXACT) {
+        // exact reference distance to every candidate of the thread's token
 #pragma unroll
-    for (int w = 0; w < 2; ++w) {
-        uint64_t mm = cmask[tid * 2 + w];
-        while (mm) {
-            const int c = 64 * w + __builtin_ctzll(mm);
-            mm &= mm - 1;
-            const float dist = l2_lanes8<DP>(x, cs + c * CS);
-            if (dist < best) {
-                best = dist;
-                arg = c;
+        for (int w = 0; w < 2; ++w) {
+            uint64_t mm = cmask[tid * 2 + w];
+            while (mm) {
+                const int c = 64 * w + __builtin_ctzll(mm);
+                mm &= mm - 1;
+                const float dist = l2_lanes8_bf16<DP>(xr, cs + c * CS);
+                if (dist < best) {
+                    best = dist;
+                    arg = c;
+                }
             }
         }
+    } else {
+        // No distance is read: a lone candidate is the reference's label (the
+        // bound above).  Tokens with several candidates (a few percent, but
+        // in most waves) queue up, and the first wave runs all their exact
+        // passes instead of every wave running its own.
+        const uint64_t m0 = cmask[tid * 2], m1 = cmask[tid * 2 + 1];
+        arg = m0 ? __builtin_ctzll(m0) : (m1 ? 64 + __builtin_ctzll(m1) : 0);
+        const bool multi = valid && __popcll(m0) + __popcll(m1) > 1;
+        const uint64_t bal = __ballot(multi);
+        int slot = 0;
+        if (bal) {
+            int base = 0;
+            if (lane == 0) base = atomicAdd(qcnt, __popcll(bal));
+            slot = __shfl(base, 0) + __popcll(bal & lanemask_lt());
+        }
+        if (multi && slot < kScreenQueue) qtok[slot] = tid;
+        __syncthreads();
+        const int nq = min(*qcnt, kScreenQueue);
+        // the exact pass of block token tk (its row re-read: it is in L2)
+        auto exact_label = [&](int tk) {
+            km_u32x4_t xq[DP / 8];
+#pragma unroll
+            for (int i = 0; i < DP / 8; ++i)
+                xq[i] = *reinterpret_cast<const km_u32x4_t*>(kb + static_cast<int64_t>(blk * 256 + tk) * a.ts + 8 * i);
+            float qb = 3.402823466e38f;
+            int qa = 0;
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                uint64_t mm = cmask[tk * 2 + w];
+                while (mm) {
+                    const int c = 64 * w + __builtin_ctzll(mm);
+                    mm &= mm - 1;
+                    const float dist = l2_lanes8_bf16<DP>(xq, cs + c * CS);
+                    if (dist < qb) {
+                        qb = dist;
+                        qa = c;
+                    }
+                }
+            }
+            return qa;
+        };
+        // the queued tokens on the first threads (the label replaces the
+        // token in its slot); past the queue's end a token runs its own pass
+        if (tid < nq) qtok[tid] = exact_label(qtok[tid]);
+        if (multi && slot >= kScreenQueue) arg = exact_label(tid);
+        __syncthreads();
+        if (multi && slot < kScreenQueue) arg = qtok[slot];
+        if (tid == 0) *qcnt = 0;   // read by every thread before the barrier above
     }
     if (valid) {
         a.labels[static_cast<int64_t>(seg) * a.T + t] = arg;
-        if (a.mind) a.mind[static_cast<int64_t>(seg) * a.T + t] = best;
+        if (EXACT && a.mind) a.mind[static_cast<int64_t>(seg) * a.T + t] = best;
     }
     if (a.hist == nullptr) continue;
 
-    float part = wave_sum(valid ? best : 0.0f);
+    float part = EXACT ? wave_sum(valid ? best : 0.0f) : 0.0f;
     if (lane_id() == 0) red[tid >> 6] = part;
     const int r = block_digit_rank(arg, valid, k, bits_for(k), wcnt,
                                    a.hist + static_cast<int64_t>(seg) * a.kmax * a.nblk, a.nblk, blk);
@@ -1201,25 +1249,33 @@ size_t workspace_bytes(const imi_kmeans_args* a, int kmax, KmParams* out) {
     return cv.used();
 }
 
-template <int DP, int MAXK, int KT>
-int run_screen(const KmParams& p, int segs, hipStream_t stream) {
+template <int DP, int MAXK, int KT, bool EXACT>
+int launch_screen(const KmParams& p, int segs, hipStream_t stream) {
     const size_t lds = screen_lds_bytes<DP>(p.kmax);
+    const void* fn = reinterpret_cast<const void*>(&km_assign_screen_kernel<DP, MAXK, KT, EXACT>);
     if (lds > 64 * 1024)
-        IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_assign_screen_kernel<DP, MAXK, KT>),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+        IMI_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
     // as many workgroups as fit on the device at once, each over `chunks`
     // consecutive 256-token blocks
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, km_assign_screen_kernel<DP, MAXK, KT>, 256, lds) !=
-            hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, km_assign_screen_kernel<DP, MAXK, KT, EXACT>, 256,
+                                                     lds) != hipSuccess ||
         per_cu <= 0)
         per_cu = 1;
     const int64_t want = static_cast<int64_t>(per_cu) * device_cus();
     const int chunks = static_cast<int>(std::max<int64_t>(1, (static_cast<int64_t>(p.nblk) * segs + want - 1) / want));
     const int gx = (p.nblk + chunks - 1) / chunks;
-    hipLaunchKernelGGL((km_assign_screen_kernel<DP, MAXK, KT>), dim3(gx, segs), dim3(256), lds, stream, p, chunks);
+    hipLaunchKernelGGL((km_assign_screen_kernel<DP, MAXK, KT, EXACT>), dim3(gx, segs), dim3(256), lds, stream, p,
+                       chunks);
     IMI_LAUNCH_CHECK("km_assign_screen_kernel");
     return IMI_OK;
+}
+
+// EXACT: the distances are read (min distances or the early-stop inertia)
+template <int DP, int MAXK, int KT>
+int run_screen(const KmParams& p, int segs, hipStream_t stream) {
+    return p.exact ? launch_screen<DP, MAXK, KT, true>(p, segs, stream)
+                   : launch_screen<DP, MAXK, KT, false>(p, segs, stream);
 }
 
 template <int DP>
@@ -1232,8 +1288,7 @@ int run_assign(const KmParams& p, int segs, hipStream_t stream) {
         hipLaunchKernelGGL(km_assign_tiled_kernel<DP>, dim3(p.nblk, segs), dim3(256), lds, stream, p);
         IMI_LAUNCH_CHECK("km_assign_tiled_kernel");
         return IMI_OK;
-    }
-    if (p.kmax <= kScreenMaxK) {
+    } else if (p.kmax <= kScreenMaxK) {
         bool same = true;   // every subspace has kmax centroids
         for (int q = 0; q < p.P; ++q) same = same && p.k[q] == p.kmax;
         if (same) {
@@ -1353,6 +1408,8 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
         }
     }
     for (int it = 0; it < a->max_iters; ++it) {
+        // the inertia of iteration it enters the stop tests of it and it + 1
+        p.exact = early_stop && it + 2 >= std::max(a->early_stop_min_iter, 1) ? 1 : 0;
         rc = dp == 128 ? run_assign<128>(p, segs, stream)
                        : (dp == 64 ? run_assign<64>(p, segs, stream) : run_assign<32>(p, segs, stream));
         if (rc) return rc;
@@ -1419,6 +1476,7 @@ extern "C" int imi_kmeans_assign(const uint16_t* keys, int64_t head_stride, int6
     p.cent = const_cast<float*>(centroids);
     p.labels = labels;
     p.mind = mind;
+    p.exact = mind != nullptr ? 1 : 0;
     p.nblk = (n_tokens + 255) / 256;
     hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
     if (dp == 128) return run_assign<128>(p, kv_heads * parts, stream);

@@ -114,9 +114,10 @@ def kmeans(keys: torch.Tensor, ks: Sequence[int], max_iters: int, tol: float = 5
     return cent, labels, iters
 
 
-def kmeans_assign(keys: torch.Tensor, centroids: torch.Tensor, ks: Sequence[int]):
+def kmeans_assign(keys: torch.Tensor, centroids: torch.Tensor, ks: Sequence[int], with_distance: bool = True):
     """One E-step with given centroids [H, P, kmax, D/P] (kmeans_core.cpp:222-242).
-    Returns (labels i32 [H, P, T], min distance f32 [H, P, T])."""
+    Returns (labels i32 [H, P, T], min distance f32 [H, P, T]); the distance
+    is None with ``with_distance=False`` (the labels alone are cheaper)."""
     dev = _require_device(keys, centroids)
     _as_bits(keys)
     H, T, D = keys.shape
@@ -124,9 +125,10 @@ def kmeans_assign(keys: torch.Tensor, centroids: torch.Tensor, ks: Sequence[int]
     hs, ts = _head_token_strides(keys)
     cent = centroids.to(torch.float32).contiguous()
     labels = torch.empty((H, P, T), dtype=torch.int32, device=dev)
-    mind = torch.empty((H, P, T), dtype=torch.float32, device=dev)
+    mind = torch.empty((H, P, T), dtype=torch.float32, device=dev) if with_distance else None
     check(_lib.lib().imi_kmeans_assign(keys.data_ptr(), hs, ts, H, T, D, P, ctypes.cast(_ks(ks), ctypes.c_void_p),
-                                       cent.data_ptr(), labels.data_ptr(), mind.data_ptr(), _stream(dev)),
+                                       cent.data_ptr(), labels.data_ptr(),
+                                       mind.data_ptr() if with_distance else None, _stream(dev)),
           "imi_kmeans_assign")
     return labels, mind
 
@@ -144,7 +146,7 @@ def kmeans_sampled(keys: torch.Tensor, ks: Sequence[int], max_iters: int, sample
     H, T, D = keys.shape
     step = max(1, -(-T // int(sample_tokens)))
     cent, _, iters = kmeans(keys[:, ::step], ks, max_iters, **kw)
-    labels, _ = kmeans_assign(keys, cent, ks)
+    labels, _ = kmeans_assign(keys, cent, ks, with_distance=False)
     return cent, labels, iters
 
 

@@ -65,6 +65,9 @@ def test_assign_bit_exact(ops, oracle, T, k, parts, integer):
             ref, rmind, _ = oracle.estep(sub, cent[h, p])
             assert np.array_equal(labels[h, p], ref), (h, p)
             assert np.array_equal(mind[h, p], rmind), (h, p)
+    # labels only: lone screen candidates skip the exact distance
+    lab2, none = ops.kmeans_assign(keys.to(DEV), torch.from_numpy(cent).to(DEV), [k] * parts, with_distance=False)
+    assert none is None and np.array_equal(lab2.cpu().numpy(), labels)
 
 
 @pytest.mark.parametrize("T,k,iters", [(4096, 64, 10), (2500, 32, 6), (300, 64, 4)])
@@ -200,11 +203,13 @@ def _exact_cluster_keys(H, k=4, per=64, seed=0):
 
 
 @pytest.mark.parametrize("min_iter,rel_tol,tol", [(1, 1e-6, 0.0), (2, 0.0, 0.0), (1, 0.9, 0.0), (5, 0.0, 0.0),
-                                                  (1, 0.0, 1e9)])
+                                                  (7, 0.0, 0.0), (1, 0.0, 1e9)])
 def test_kmeans_early_stop_matches_oracle(ops, oracle, min_iter, rel_tol, tol):
     """kmeans_core.cpp:244-262 on data whose inertia is exact in any order, so
     the GPU's summation order cannot move the stop: the iteration count, the
-    labels and the centroids equal the oracle's."""
+    labels and the centroids equal the oracle's.  The E-step skips the
+    distances of lone screen candidates in the iterations before
+    min_iter - 1, whose inertia no stop test reads (min_iter 5 and 7)."""
     note(f"[kmeans] early stop min_iter={min_iter} rel_tol={rel_tol} tol={tol}")
     H, k = 2, 4
     keys = _exact_cluster_keys(H, k)
