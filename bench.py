@@ -677,7 +677,8 @@ def cpu_baseline(first, ks, bud, static_len, seconds, iters):
     build_ms = statistics.median(build) * 1e3
     return {"value": round(1.0 / dec_s, 2), "unit": "decode steps/s per layer", "cores": cores, "kind": "port",
             "sample": f"layer 0 of the same workload: {len(dec)} decode steps ({H} KV heads, scores + selection + "
-                      f"fp32 attention, OpenMP on {cores} cores), median; {len(build)} full index builds of the "
+                      f"fp32 attention, AVX2 + OpenMP on {cores} cores, each K/V row read once for its "
+                      f"{first['q'].shape[1]} query heads), median; {len(build)} full index builds of the "
                       f"layer ({H} heads x {len(ks)} subspaces, {iters} Lloyd iterations, {max_conc} concurrent "
                       f"runs x {tpp} threads as the reference splits them, compaction, K/V permutation), median",
             "decode_us_per_layer_median": round(dec_s * 1e6, 1), "decode_runs": len(dec),

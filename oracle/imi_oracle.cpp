@@ -402,96 +402,4 @@ void orc_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, int6
     }
 }
 
-// CPU BASELINE (timed by bench.py's cpu_baseline leg, not a checker): one
-// decode step of every KV head as the reference's path computes it --
-// query-group sum and the fp32 FMA score chain (compute_impl.cu:62-103), the
-// mask (retrieval.py:357), top-nprobe + token rule (retrieval.py:295-303),
-// page rule (wave_buffer_cpu_hotcold.cpp:303-371), gather of [static rows |
-// selected rows] (copy_kernel.cuh:220-335) and softmax attention in fp32 --
-// with OpenMP over (head, cell) for the scores, over heads for the
-// selection and over (head, query) for the attention.
-//   q [H][G][D] bf16, cent [H][N][D] fp32 (merged, padded), sizes / masked /
-//   offsets [H][N(+1)], lk / lv [H][L][D] bf16, sk / sv [H][S][D] bf16;
-//   out [H][G][D] fp32; m [H] cells selected.
-void orc_decode_step_f32(const uint16_t* q, const float* cent, const int32_t* sizes, const uint8_t* masked,
-                         const int32_t* offsets, int H, int G, int N, int D, const uint16_t* lk,
-                         const uint16_t* lv, int64_t L, const uint16_t* sk, const uint16_t* sv, int64_t S,
-                         int static_len, int nprobe, int max_tokens, int buffer_pages, int page_size,
-                         float scale, float* out, int32_t* m_out) {
-    std::vector<float> qs((size_t)H * D), sc((size_t)H * N);
-    for (int h = 0; h < H; ++h)
-        for (int d = 0; d < D; ++d) {
-            float a = 0.0f;
-            for (int g = 0; g < G; ++g) a += bf16_bits_to_f32(q[((int64_t)h * G + g) * D + d]);
-            qs[(size_t)h * D + d] = a;
-        }
-#pragma omp parallel for schedule(static)
-    for (int64_t hc = 0; hc < (int64_t)H * N; ++hc) {
-        const int h = (int)(hc / N);
-        const float* cp = cent + hc * D;
-        const float* qh = qs.data() + (size_t)h * D;
-        float s = 0.0f;
-        for (int d = 0; d < D; ++d) s = std::fmaf(qh[d], cp[d], s);
-        sc[hc] = masked[hc] ? -std::numeric_limits<float>::infinity() : s;
-    }
-    std::vector<std::vector<int64_t>> rows(H);
-#pragma omp parallel for schedule(dynamic, 1)
-    for (int h = 0; h < H; ++h) {
-        const float* s = sc.data() + (size_t)h * N;
-        const int32_t* sz = sizes + (int64_t)h * N;
-        const int k = std::min(nprobe, N);
-        std::vector<int32_t> idx(N);
-        for (int c = 0; c < N; ++c) idx[c] = c;
-        std::partial_sort(idx.begin(), idx.begin() + k, idx.end(), [&](int32_t a, int32_t b) {
-            return s[a] > s[b] || (s[a] == s[b] && a < b);
-        });
-        int32_t cum = 0;
-        int pages = 0, cnt = 0;
-        std::vector<int64_t>& r = rows[h];
-        for (int i = 0; i < static_len; ++i) r.push_back(-1 - i);
-        for (int i = 0; i < k; ++i) {
-            const int32_t c = idx[i], size = sz[c];
-            cum += size;
-            if (!(size > 0 && (cum - size) < max_tokens)) continue;
-            pages += (size + page_size - 1) / page_size;
-            if (pages > buffer_pages) break;
-            ++cnt;
-            for (int32_t t = offsets[(int64_t)h * (N + 1) + c]; t < offsets[(int64_t)h * (N + 1) + c + 1]; ++t)
-                r.push_back(t);
-        }
-        m_out[h] = cnt;
-    }
-#pragma omp parallel for schedule(dynamic, 1)
-    for (int hg = 0; hg < H * G; ++hg) {
-        const int h = hg / G;
-        const uint16_t* qp = q + (int64_t)hg * D;
-        float qf[512];
-        for (int d = 0; d < D; ++d) qf[d] = bf16_bits_to_f32(qp[d]);
-        const std::vector<int64_t>& r = rows[h];
-        std::vector<float> p(r.size());
-        float mx = -std::numeric_limits<float>::infinity();
-        auto row_ptr = [&](int64_t x, const uint16_t* list, const uint16_t* steady) {
-            return x < 0 ? steady + ((int64_t)h * S + (-1 - x)) * D : list + ((int64_t)h * L + x) * D;
-        };
-        for (size_t i = 0; i < r.size(); ++i) {
-            const uint16_t* kp = row_ptr(r[i], lk, sk);
-            float a = 0.0f;
-            for (int d = 0; d < D; ++d) a += qf[d] * bf16_bits_to_f32(kp[d]);
-            p[i] = a * scale;
-            mx = std::max(mx, p[i]);
-        }
-        float* o = out + (int64_t)hg * D;
-        for (int d = 0; d < D; ++d) o[d] = 0.0f;
-        float den = 0.0f;
-        for (size_t i = 0; i < r.size(); ++i) {
-            const float w = std::exp(p[i] - mx);
-            den += w;
-            const uint16_t* vp = row_ptr(r[i], lv, sv);
-            for (int d = 0; d < D; ++d) o[d] += w * bf16_bits_to_f32(vp[d]);
-        }
-        if (den > 0.0f)
-            for (int d = 0; d < D; ++d) o[d] /= den;
-    }
-}
-
 }  // extern "C"

@@ -40,6 +40,7 @@ import numpy as np
 
 _HERE = Path(__file__).resolve().parent
 _LIB_PATH = _HERE / "liboracle.so"
+_BASE_PATH = _HERE / "libcpudecode.so"
 _lib = None
 
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -51,9 +52,12 @@ _u8p = ctypes.POINTER(ctypes.c_uint8)
 
 
 def build(force: bool = False) -> Path:
-    """Compile liboracle.so with oracle/Makefile."""
-    if force or not _LIB_PATH.exists() or _LIB_PATH.stat().st_mtime < (_HERE / "imi_oracle.cpp").stat().st_mtime:
-        subprocess.run(["make", "-B" if force else "-s", "-C", str(_HERE)], check=True)
+    """Compile liboracle.so (the checker) and libcpudecode.so (the CPU
+    baseline) with oracle/Makefile."""
+    stale = any(not lib_.exists() or lib_.stat().st_mtime < (_HERE / src).stat().st_mtime
+                for lib_, src in ((_LIB_PATH, "imi_oracle.cpp"), (_BASE_PATH, "cpu_decode.cpp")))
+    if force or stale:
+        subprocess.run(["make", "-B" if force else "-s", "-C", str(_HERE), "all"], check=True)
     return _LIB_PATH
 
 
@@ -88,11 +92,6 @@ def lib():
         L.orc_mt32_outputs.argtypes = [ctypes.c_uint32, ctypes.c_int64, ctypes.POINTER(ctypes.c_uint32)]
         L.orc_mt64_outputs.restype = None
         L.orc_mt64_outputs.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.POINTER(ctypes.c_uint64)]
-        L.orc_decode_step_f32.restype = None
-        L.orc_decode_step_f32.argtypes = [_u16p, _f32p, _i32p, _u8p, _i32p, ctypes.c_int, ctypes.c_int,
-                                          ctypes.c_int, ctypes.c_int, _u16p, _u16p, ctypes.c_int64, _u16p, _u16p,
-                                          ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                          ctypes.c_int, ctypes.c_float, _f32p, _i32p]
         L.orc_attention.restype = None
         L.orc_attention.argtypes = [_u16p, _u16p, _u16p, ctypes.c_int64, _i64p, _i32p, ctypes.c_int64,
                                     ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_double, _f64p]
@@ -484,15 +483,35 @@ def decode_step(q_bits: np.ndarray, heads: List[dict], steady_k: np.ndarray, ste
     return out, sel, m, rows
 
 
+_base = None
+
+
+def base_lib():
+    """libcpudecode.so: the CPU baseline's own vectorized build."""
+    global _base
+    if _base is None:
+        build()
+        L = ctypes.CDLL(str(_BASE_PATH))
+        L.cpu_decode_step_f32.restype = None
+        L.cpu_decode_step_f32.argtypes = [_u16p, _f32p, _i32p, _u8p, _i32p, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_int, _u16p, _u16p, ctypes.c_int64, _u16p, _u16p,
+                                          ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_float, _f32p, _i32p]
+        _base = L
+    return _base
+
+
 class DecodeBaselineF32:
     """CPU BASELINE, not a checker: the decode step of every KV head in fp32
-    with OpenMP (orc_decode_step_f32), on metadata padded once
-    (pad_metadata).  list_keys / values: [H, L, D] bf16 bits; steady_k / v:
-    [H, S, D] bf16 bits."""
+    (cpu_decode_step_f32, AVX2 + OpenMP: each K/V row read once for the G
+    queries of its KV head, row chunks over the threads), on metadata padded
+    once (pad_metadata).  list_keys / values: [H, L, D] bf16 bits;
+    steady_k / v: [H, S, D] bf16 bits."""
 
     def __init__(self, heads: List[dict], list_keys: np.ndarray, list_values: np.ndarray, steady_k: np.ndarray,
                  steady_v: np.ndarray, n_centroids: int, D: int = 128):
         self.sizes, self.offsets, self.cent, mask = pad_metadata(heads, n_centroids, D)
+        self.cent_t = np.ascontiguousarray(self.cent.transpose(0, 2, 1))   # [H, D, N]
         self.mask = np.ascontiguousarray(mask, np.uint8)
         self.lk = np.ascontiguousarray(list_keys, np.uint16)
         self.lv = np.ascontiguousarray(list_values, np.uint16)
@@ -507,7 +526,9 @@ class DecodeBaselineF32:
         out = np.empty((self.H, G, self.D), np.float32)
         m = np.empty(self.H, np.int32)
         sc = 1.0 / math.sqrt(self.D) if scale is None else scale
-        lib().orc_decode_step_f32(_p(q_bits, _u16p), _p(self.cent, _f32p), _p(self.sizes, _i32p),
+        if G > 16 or self.D % 8 or self.D > 256:
+            raise ValueError("the CPU baseline takes G <= 16 and D a multiple of 8 up to 256")
+        base_lib().cpu_decode_step_f32(_p(q_bits, _u16p), _p(self.cent_t, _f32p), _p(self.sizes, _i32p),
                                   _p(self.mask, _u8p), _p(self.offsets, _i32p), self.H, G, self.N, self.D,
                                   _p(self.lk, _u16p), _p(self.lv, _u16p), self.lk.shape[1], _p(self.sk, _u16p),
                                   _p(self.sv, _u16p), self.sk.shape[1], static_len, nprobe, max_tokens,
