@@ -81,6 +81,9 @@ def parse():
     p.add_argument("--host-tier-layers", type=int, default=2,
                    help="layers of the host-tier leg (lists in pinned host memory, GPU block cache of "
                         "round(n_centroids * 0.05) clusters x 2 pages); 0 skips it")
+    p.add_argument("--config3-layers", type=int, default=2,
+                   help="layers of the configs[3] leg (4-way 32^4 IMI, 2 x 8 KV heads at 262,144 tokens, GQA 8, "
+                        "fixed 4,096-token budget): step and selection per layer; 0 skips it")
     p.add_argument("--copy-probe-mb", type=int, default=0,
                    help="run a device-to-device copy of this many MiB (3 times) before the timed region, as the "
                         "known-size reference for FETCH_SIZE / WRITE_SIZE counter runs")
@@ -98,6 +101,7 @@ def parse():
         args.cpu_baseline = 0      # the CPU baseline is quoted on the default workload
         args.online_layers = 0
         args.host_tier_layers = 0
+        args.config3_layers = 0
     return args
 
 
@@ -270,6 +274,11 @@ def main():
         host_tier = host_tier_leg(args, ks, bud, static_total)
         log(f"[bench] host tier: {host_tier}")
 
+    config3 = None
+    if args.config3_layers > 0:
+        config3 = config3_leg(args, capture)
+        log(f"[bench] configs[3] leg: {config3}")
+
     # ----------------------------------------------------- CPU baseline
     cpu = None
     if keep_first is not None:
@@ -312,6 +321,7 @@ def main():
         "cpu_baseline": cpu,
         "online_update": online,
         "host_tier": host_tier,
+        "config3": config3,
     }
     print(json.dumps(result), flush=True)
 
@@ -413,6 +423,75 @@ def online_update_leg(args, ks, bud, static_total, capture):
             "plain_us_per_layer_step": res["plain"][0], "plain_select_us": res["plain"][1],
             "plain_attention_merge_us": res["plain"][2],
             "replaced_cells_per_head": round(repl, 1), "delta_rows_per_head": round(drows, 1)}
+
+
+def config3_leg(args, capture):
+    """The configs[3] decode step (the reference's default 4-way IMI, 32^4
+    cells, over a batch of 2 sequences x 8 KV heads at 262,144 tokens, GQA 8,
+    fixed 4,096-token budget) on config3_layers layers: per layer-step time
+    of the graphed step, and per launch of the selection alone (graph of the
+    selection phase of every layer), as the main run times configs[1]."""
+    import torch
+
+    from adaptiveimi_amd import ops, synthetic
+    from adaptiveimi_amd.sizing import decode_sizing
+
+    w = WORKLOADS["config3"]
+    dev = torch.device("cuda:0")
+    H, G, D, NL = w["kv_heads"] * w["batch"], w["groups"], 128, args.config3_layers
+    ks = tuple(w["ks"])
+    static_total = args.static_start + args.static_end
+    T = w["context"] - static_total
+    sz = decode_sizing(T, w["fixed_tokens"] / T, subspace_parts=len(ks), k_override=ks)
+    bud = ops.Budget(sz["nprobe"], w["fixed_tokens"], max(32, -(-w["fixed_tokens"] // sz["page_size"])))
+    static_cap, static_len = static_total + 256, static_total + 1
+    ncells = min(T, math.prod(ks))
+    plans = []
+    for layer in range(NL):
+        keys, values = synthetic.make_kv(H, w["context"], seed=3000 + layer, device="cuda")
+        mid_k = keys[:, args.static_start:w["context"] - args.static_end]
+        mid_v = values[:, args.static_start:w["context"] - args.static_end]
+        sk = torch.zeros((H, static_cap, D), dtype=torch.bfloat16, device=dev)
+        sv = torch.zeros_like(sk)
+        sk[:, :static_total] = torch.cat([keys[:, :args.static_start], keys[:, w["context"] - args.static_end:]], 1)
+        sv[:, :static_total] = torch.cat([values[:, :args.static_start],
+                                          values[:, w["context"] - args.static_end:]], 1)
+        sk[:, static_total] = keys[:, -1]
+        sv[:, static_total] = values[:, -1]
+        cent, labels, _ = ops.kmeans(mid_k, list(ks), w["iters"], init=args.kmeans_init)
+        idx = ops.build_index(mid_k, mid_v, cent, labels, list(ks), compact=True, merged=False,
+                              n_centroids=ncells + 1)
+        q = synthetic.make_queries(mid_k, G, seed=layer)[0]
+        plan = ops.DecodePlan(cent, idx["cell_count"], idx["cell_offset"], ks, bud, idx["list_keys"],
+                              idx["list_values"], sk, sv, G, query=q.contiguous(), compact=idx)
+        plan.set_static_len(static_len)
+        plans.append(plan)
+        del keys, values, mid_k, mid_v, labels
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def per_layer_us(fn, reps):
+        g = capture(fn)
+        g.replay()
+        torch.cuda.synchronize()
+        ev0.record()
+        for _ in range(reps):
+            g.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) * 1e3 / (reps * NL)
+
+    reps = max(args.steps, 5)
+    step_us = per_layer_us(lambda: [p.step() for p in plans], reps)
+    sel_us = per_layer_us(lambda: [p.step(phases=1) for p in plans], reps)
+    rows = sum(int(p.selection["n_rows"].sum().item()) for p in plans) / NL
+    del plans
+    torch.cuda.empty_cache()
+    return {"layers": NL, "kv_heads": H, "q_heads": H * G, "context": w["context"], "ks": list(ks),
+            "nprobe": bud.nprobe, "max_tokens": bud.max_tokens, "buffer_pages": bud.buffer_pages,
+            "us_per_layer_step": round(step_us, 2), "select_us": round(sel_us, 2),
+            "attended_rows_per_layer": rows,
+            "clock": "HIP events around graphs of every layer's step (or its selection phase)"}
 
 
 def host_tier_leg(args, ks, bud, static_total):
