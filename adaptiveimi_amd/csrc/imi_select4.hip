@@ -53,8 +53,10 @@ constexpr int kSelCap4 = kCand4;  // cells to rank (K') per head
 constexpr int kExtHeads = 1024;  // KV heads one call handles
 constexpr int kCPT = 16;         // occupied cells per thread in the 4-way score kernel
 constexpr int kCS4 = 36;         // LDS row stride of a subspace centroid (16-byte aligned rows)
-constexpr int kTripCap = 4096;   // (l0, l1, l2) prefixes a score workgroup keeps
+constexpr int kTripCap = 8192;   // (l0, l1, l2) prefixes a score workgroup keeps
 constexpr int kCellsPerBlock = kScore4Threads * kCPT;
+constexpr int kFastCand = 2048;  // screened pass: candidates a score workgroup scores exactly
+constexpr size_t kFastLds = static_cast<size_t>(kFastCand) * 12 + 2 * kK4 * 4;   // their (x0, gid, cell), d3 and A
 constexpr int kDenseScoreCells = kScoreThreads;   // 2-way score kernel: one global cell per thread
 constexpr int kDenseK = 256;                      // 2-way centroids per subspace the score kernel reads
 constexpr int kIvfMaxK = 4096;                    // IVF clusters per head
@@ -111,6 +113,7 @@ struct Sel4 {
     int exec_rows;
     int32_t* delta_rows;
     int32_t* n_delta;
+    int fast4;               // the 4-way score kernel has LDS for its screened pass
 };
 
 __device__ __forceinline__ float key_score(uint64_t key) {
@@ -288,8 +291,248 @@ __device__ void emit_candidates(const Sel4& a, int h, int kp, const uint64_t (&k
         }
 }
 
+// Screened candidate cut of a 4-way score workgroup (no online update,
+// K' <= 1024).  Each cell's score is the
+// chain continued from its triple prefix x0 over C3[l3]; its approximation
+// fl(x0 + d3[l3]), with d3 the same chain from zero, differs from it by at
+// most gamma_66 (|x0| + A[l3]) (A = sum |q c| over the 32 terms; u = 2^-24,
+// one rounding per fused multiply-add, the chains' errors plus the final
+// add).  E = 2^-16 (max |x0| + max A) + 1e-30 bounds that with a 4x margin
+// and covers subnormal results.  A threshold L with K' approximate scores at
+// or above it (from the threads' largest approximate scores) has K' exact
+// scores at or above L - E: the workgroup's K'-th best exact score is
+// >= L - E, and each of its cells that can be among the head's K' best has
+// an approximate score >= L - 2E.  Those cells (a few percent) get the exact chain and are
+// listed with their keys; every other cell is skipped.  Returns false
+// (workgroup-uniform) when the bound is not finite or more than kFastCand
+// cells pass: the caller then scores every cell.
+template <bool POW2>
+__device__ bool screened_cut(const Sel4& a, int h, int kp, int c_first, int na, const uint32_t (&gv)[kCPT],
+                             const float (&sv)[kCPT], uint32_t k3, float* fx0, uint32_t* fgid, int* fci,
+                             const float* fd3, const float* fa3, uint32_t (*s_fw)[3], const float* qs,
+                             const float* cs, int* lh) {
+    constexpr int NW = kScore4Threads / 64;
+    const int tid = threadIdx.x, w = tid >> 6, lane = lane_id();
+    if (kp > kScore4Threads) return false;   // (per-head budgets beyond the host's bound)
+    if (kp <= 0) {   // no cells to rank: no candidates
+        if (tid == 0) {
+            const int64_t sg = static_cast<int64_t>(h) * a.nbs + blockIdx.x;
+            a.wcnt[sg] = 0;
+            a.rpart[sg * 2 + 0] = 0u;
+            a.rpart[sg * 2 + 1] = 0u;
+        }
+        return true;
+    }
+    uint32_t xmb = 0;   // non-negative floats (NaN above inf) as their bits
+#pragma unroll
+    for (int j = 0; j < NW; ++j) xmb = max(xmb, s_fw[j][0]);
+    const float E = 0x1p-16f * (__uint_as_float(xmb) + fa3[0] * 1.0001f) + 1e-30f;   // fa3[0]: the largest A
+    const bool ok = E < 1e30f;   // false for inf and NaN
+    // Each thread's largest approximate key stands for one of its cells:
+    // the smallest thread maximum L among the threads in the buckets that
+    // reach K' (a 1024-bucket histogram of the thread maxima) has K' cells at
+    // or above it, whatever the buckets' rounding.
+    uint32_t tmax = 0;
+    bool any = false;
+    float ap[kCPT];   // approximate scores
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        const bool in = c_first + u * kScore4Threads + tid < na;
+        ap[u] = in ? sv[u] + fd3[kmod<POW2>(gv[u], k3)] : -INFINITY;
+        if (in) tmax = max(tmax, order_key(ap[u]));
+        any = any || in;
+    }
+    {
+        const uint32_t hi = wave_max_u32(any ? tmax : 0u);
+        const uint32_t nlo = wave_max_u32(any ? ~tmax : 0u);
+        if (lane == 0) {
+            s_fw[w][1] = hi;
+            s_fw[w][2] = nlo;
+        }
+    }
+    __syncthreads();
+    uint32_t khi = 0, knlo = 0;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+        khi = max(khi, s_fw[j][1]);
+        knlo = max(knlo, s_fw[j][2]);
+    }
+    const float fhi = key_score(static_cast<uint64_t>(khi) << 32);
+    const float flo = key_score(static_cast<uint64_t>(~knlo) << 32);
+    const float span = fhi - flo;
+    const float inv = span > 0.0f ? static_cast<float>(kLocBins) / span : 0.0f;
+    int bt = kLocBins;   // no bucket
+    if (any) {
+        const float t = (fhi - key_score(static_cast<uint64_t>(tmax) << 32)) * inv;
+        bt = t < static_cast<float>(kLocBins - 1) ? (t > 0.0f ? static_cast<int>(t) : 0) : kLocBins - 1;
+        atomicAdd(&lh[bt], 1);
+    }
+    __syncthreads();
+    {
+        // bucket bk where the count reaches kp (one bucket per thread)
+        constexpr int PB = kLocBins / kScore4Threads;
+        static_assert(PB == 1, "one bucket per thread");
+        const int v = lh[tid];
+        const int incl = wave_incl_scan(v);
+        if (lane == 63) s_fw[w][1] = static_cast<uint32_t>(incl);
+        __syncthreads();
+        int run = incl - v;
+        for (int j = 0; j < w; ++j) run += static_cast<int>(s_fw[j][1]);
+        if (run < kp && run + v >= kp) s_fw[0][2] = static_cast<uint32_t>(tid);   // one writer
+        if (tid == kScore4Threads - 1 && run + v < kp) s_fw[0][2] = static_cast<uint32_t>(kLocBins);   // fewer than kp
+        __syncthreads();
+    }
+    const int bk = static_cast<int>(s_fw[0][2]);
+    uint32_t lmin = bt <= bk && any ? tmax : 0xFFFFFFFFu;
+    lmin = ~wave_max_u32(~lmin);
+    if (lane == 0) s_fw[w][1] = lmin;   // (the scan's totals were read before the last barrier)
+    __syncthreads();
+    uint32_t L = 0xFFFFFFFFu;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) L = min(L, s_fw[j][1]);
+    if (bk >= kLocBins) L = 0u;   // fewer than kp thread maxima: every cell
+    float thr = -INFINITY;        // L = 0: every cell passes
+    if (L != 0u) {
+        const float lf = key_score(static_cast<uint64_t>(L) << 32);
+        thr = lf - (2.0f * E + fabsf(lf) * 0x1p-20f);   // the margin covers the subtraction's rounding
+    }
+    // the cells that pass, listed in LDS in thread order (a block scan of the
+    // per-thread counts)
+    uint32_t cm = 0;
+    int cnt = 0;
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        const bool c = c_first + u * kScore4Threads + tid < na && ap[u] >= thr;
+        cm |= c ? 1u << u : 0u;
+        cnt += c ? 1 : 0;
+    }
+    const int incl = wave_incl_scan(cnt);
+    if (lane == 63) s_fw[w][2] = static_cast<uint32_t>(incl);
+    __syncthreads();
+    int before = incl - cnt, total = 0;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+        before += j < w ? static_cast<int>(s_fw[j][2]) : 0;
+        total += static_cast<int>(s_fw[j][2]);
+    }
+    if (!ok || total > kFastCand) return false;
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u)
+        if (cm & (1u << u)) {
+            const int pos = before + __builtin_popcount(cm & ((1u << u) - 1u));
+            fx0[pos] = sv[u];
+            fgid[pos] = gv[u];
+            fci[pos] = c_first + u * kScore4Threads + tid;
+        }
+    __syncthreads();
+    const int64_t sg = static_cast<int64_t>(h) * a.nbs + blockIdx.x;
+    uint32_t kmx = 0, knm = 0;
+    for (int j = tid; j < total; j += kScore4Threads) {
+        float x = fx0[j];
+        const uint32_t g = fgid[j];
+        const float* c3r = &cs[(3 * a.kmax + static_cast<int>(kmod<POW2>(g, k3))) * kCS4];
+#pragma unroll 2
+        for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
+            const float4 q4 = *reinterpret_cast<const float4*>(&qs[3 * kDp4 + 4 * d4]);
+            const float4 c4 = *reinterpret_cast<const float4*>(&c3r[4 * d4]);
+            x = __builtin_fmaf(q4.x, c4.x, x);
+            x = __builtin_fmaf(q4.y, c4.y, x);
+            x = __builtin_fmaf(q4.z, c4.z, x);
+            x = __builtin_fmaf(q4.w, c4.w, x);
+        }
+        const uint32_t ok32 = order_key(x);
+        const int64_t pos = cand_pos(sg, j, a.region);
+        a.cand[pos] = (static_cast<uint64_t>(ok32) << 32) | (0xFFFFFFFFu - g);
+        a.cidx[pos] = fci[j];
+        kmx = max(kmx, ok32);
+        knm = max(knm, ~ok32);
+    }
+    kmx = wave_max_u32(kmx);
+    knm = wave_max_u32(knm);
+    if (lane == 0) {
+        s_fw[w][0] = kmx;
+        s_fw[w][1] = knm;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t m1 = 0, m2 = 0;
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+            m1 = max(m1, s_fw[j][0]);
+            m2 = max(m2, s_fw[j][1]);
+        }
+        a.wcnt[sg] = total;
+        a.rpart[sg * 2 + 0] = total > 0 ? m1 : 0u;
+        a.rpart[sg * 2 + 1] = total > 0 ? m2 : 0u;
+    }
+    return true;
+}
+
+// Every cell of the workgroup as a candidate, scored exactly: the chain
+// from sv (through C2) over C3[l3] (the screened cut's fallback).
+template <bool POW2>
+__device__ void dense_emit(const Sel4& a, int h, int c_first, int na, const uint32_t (&gv)[kCPT],
+                           const float (&sv)[kCPT], uint32_t k3, uint32_t (*s_fw)[3], const float* qs,
+                           const float* cs) {
+    constexpr int NW = kScore4Threads / 64;
+    const int tid = threadIdx.x, w = tid >> 6, lane = lane_id();
+    const int64_t sg = static_cast<int64_t>(h) * a.nbs + blockIdx.x;
+    float x[kCPT];
+    int r3[kCPT];
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        x[u] = sv[u];
+        r3[u] = (3 * a.kmax + static_cast<int>(kmod<POW2>(gv[u], k3))) * kCS4;
+    }
+#pragma unroll 1
+    for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
+        const float4 q4 = *reinterpret_cast<const float4*>(&qs[3 * kDp4 + 4 * d4]);
+#pragma unroll
+        for (int u = 0; u < kCPT; ++u) {
+            const float4 c4 = *reinterpret_cast<const float4*>(&cs[r3[u] + 4 * d4]);
+            x[u] = __builtin_fmaf(q4.x, c4.x, x[u]);
+            x[u] = __builtin_fmaf(q4.y, c4.y, x[u]);
+            x[u] = __builtin_fmaf(q4.z, c4.z, x[u]);
+            x[u] = __builtin_fmaf(q4.w, c4.w, x[u]);
+        }
+    }
+    uint32_t kmx = 0, knm = 0;
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        const int loc = u * kScore4Threads + tid;
+        if (c_first + loc < na) {
+            const uint32_t o = order_key(x[u]);
+            const int64_t pos = cand_pos(sg, loc, a.region);
+            a.cand[pos] = (static_cast<uint64_t>(o) << 32) | (0xFFFFFFFFu - gv[u]);
+            a.cidx[pos] = c_first + loc;
+            kmx = max(kmx, o);
+            knm = max(knm, ~o);
+        }
+    }
+    kmx = wave_max_u32(kmx);
+    knm = wave_max_u32(knm);
+    __syncthreads();   // s_fw was read by every thread
+    if (lane == 0) {
+        s_fw[w][0] = kmx;
+        s_fw[w][1] = knm;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t m1 = 0, m2 = 0;
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+            m1 = max(m1, s_fw[j][0]);
+            m2 = max(m2, s_fw[j][1]);
+        }
+        const int n = max(min(na - c_first, kCellsPerBlock), 0);
+        a.wcnt[sg] = n;
+        a.rpart[sg * 2 + 0] = n > 0 ? m1 : 0u;
+        a.rpart[sg * 2 + 1] = n > 0 ? m2 : 0u;
+    }
+}
+
 // ONLINE: replaced centroids / the delta ring (a separate instantiation).
-template <bool ONLINE, bool POW2>
+template <bool ONLINE, bool POW2, bool FAST>
 __global__ __launch_bounds__(kScore4Threads) void sel4_score_kernel(Sel4 a) {
     __shared__ __attribute__((aligned(16))) float qs[128];
     __shared__ int s_pair[2];
@@ -303,6 +546,15 @@ __global__ __launch_bounds__(kScore4Threads) void sel4_score_kernel(Sel4 a) {
     float* p01 = s_dyn4 + 4 * a.kmax * kCS4;
     const int pair_cap = a.k[0] * a.k[1];
     float* p012 = p01 + pair_cap;
+    // screened pass (fast4): the candidates' chain prefix, global id and
+    // cell index, and per l3 the chain over C3 from zero (d3) and the sum
+    // of |q c| (A)
+    float* fx0 = p012 + kTripCap;                                   // [kFastCand]
+    uint32_t* fgid = reinterpret_cast<uint32_t*>(fx0 + kFastCand);  // [kFastCand]
+    int* fci = reinterpret_cast<int*>(fgid + kFastCand);            // [kFastCand]
+    float* fd3 = reinterpret_cast<float*>(fci + kFastCand);         // [kK4]
+    float* fa3 = fd3 + kK4;                                         // [kK4]
+    __shared__ uint32_t s_fw[kScore4Threads / 64][3];
     const int h = blockIdx.y, tid = threadIdx.x;
     // the block's cells (ascending global id): their ids, loaded with the
     // occupied-cell count (reads past it stay inside the [H][cap] arrays and
@@ -369,6 +621,17 @@ __global__ __launch_bounds__(kScore4Threads) void sel4_score_kernel(Sel4 a) {
         }
     }
     for (int i = tid; i < kLocBins; i += kScore4Threads) lh[i] = 0;
+    // no occupied cells here (a head with fewer than the grid covers): the
+    // check waits for the count, so it comes after every load is issued
+    if (c_first > c_last) {
+        if (tid == 0) {
+            const int64_t sg = static_cast<int64_t>(h) * a.nbs + blockIdx.x;
+            a.wcnt[sg] = 0;
+            a.rpart[sg * 2 + 0] = 0u;
+            a.rpart[sg * 2 + 1] = 0u;
+        }
+        return;
+    }
     __syncthreads();
     // The 128-term chain runs over C0[l0], C1[l1], C2[l2], C3[l3] in turn, so
     // its value after the first 64 terms depends on (l0, l1) only: computed
@@ -409,9 +672,6 @@ __global__ __launch_bounds__(kScore4Threads) void sel4_score_kernel(Sel4 a) {
     // through C2 is also computed once per triple, and cells continue over
     // C3 only.
     float sv[kCPT];
-    int r3[kCPT];   // LDS offsets of the rows C3[l3]
-#pragma unroll
-    for (int u = 0; u < kCPT; ++u) r3[u] = (3 * a.kmax + static_cast<int>(kmod<POW2>(gv[u], k3))) * kCS4;
     const int ta = c_first <= c_last ? s_trip[0] : 0;
     const int ntrip = c_first <= c_last ? s_trip[1] - s_trip[0] + 1 : 0;
     if (ntrip > 0 && ntrip <= kTripCap) {
@@ -454,6 +714,45 @@ __global__ __launch_bounds__(kScore4Threads) void sel4_score_kernel(Sel4 a) {
             }
         }
     }
+    if constexpr (FAST) {
+        // sv: every cell's chain through C2.  The largest |prefix|, and per
+        // l3 the chain over C3 from zero (d3) and the sum of |q c| (A), for
+        // the screened cut; the cells it cannot settle are scored exactly.
+        uint32_t xm = 0;   // fp32 bits of a non-negative value (NaN above inf)
+#pragma unroll
+        for (int u = 0; u < kCPT; ++u)
+            if (c_first + u * kScore4Threads + tid < na) xm = max(xm, __float_as_uint(fabsf(sv[u])));
+        xm = wave_max_u32(xm);
+        if (lane_id() == 0) s_fw[tid >> 6][0] = xm;
+        if (tid < 64) {   // wave 0: one l3 per lane (k3 <= 64), and the largest A
+            float am = 0.0f;
+            if (tid < static_cast<int>(k3)) {
+                const float* c3r = &cs[(3 * a.kmax + tid) * kCS4];
+                float d = 0.0f;
+#pragma unroll 2
+                for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
+                    const float4 q4 = *reinterpret_cast<const float4*>(&qs[3 * kDp4 + 4 * d4]);
+                    const float4 c4 = *reinterpret_cast<const float4*>(&c3r[4 * d4]);
+                    d = __builtin_fmaf(q4.x, c4.x, d);
+                    d = __builtin_fmaf(q4.y, c4.y, d);
+                    d = __builtin_fmaf(q4.z, c4.z, d);
+                    d = __builtin_fmaf(q4.w, c4.w, d);
+                    am += fabsf(q4.x * c4.x) + fabsf(q4.y * c4.y) + fabsf(q4.z * c4.z) + fabsf(q4.w * c4.w);
+                }
+                fd3[tid] = d;
+            }
+            const uint32_t amb = wave_max_u32(__float_as_uint(am));   // NaN above inf
+            if (tid == 0) fa3[0] = __uint_as_float(amb);
+        }
+        __syncthreads();
+        const int kp = kprime(a, h, na);
+        if (!screened_cut<POW2>(a, h, kp, c_first, na, gv, sv, k3, fx0, fgid, fci, fd3, fa3, s_fw, qs, cs, lh))
+            dense_emit<POW2>(a, h, c_first, na, gv, sv, k3, s_fw, qs, cs);
+        return;
+    }
+    int r3[kCPT];   // LDS offsets of the rows C3[l3]
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) r3[u] = (3 * a.kmax + static_cast<int>(kmod<POW2>(gv[u], k3))) * kCS4;
 #pragma unroll 1
     for (int d4 = 0; d4 < kDp4 / 4; ++d4) {
         const float4 q4 = *reinterpret_cast<const float4*>(&qs[3 * kDp4 + 4 * d4]);
@@ -1343,31 +1642,43 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     } else {
         const dim3 grid(p.nbs, a->kv_heads);
         // C0..C3 rows at the padded stride, the chain prefixes per (l0, l1) pair and per triple
+        // (+ the screened pass's candidates and per-l3 tables: without the
+        // online update and for K' <= 64 per wave)
+        const bool rank_all = a->tile_mode || a->ring_cap > 0;
+        const int kprime_max = rank_all ? a->nprobe : (a->nprobe < a->buffer_pages ? a->nprobe : a->buffer_pages);
+        const bool fast = !online && kprime_max <= kScore4Threads;
+        p.fast4 = fast ? 1 : 0;
         const size_t score_lds = (static_cast<size_t>(4) * p.kmax * kCS4 + static_cast<size_t>(a->k[0]) * a->k[1] +
-                                  kTripCap) * sizeof(float);
+                                  kTripCap) * sizeof(float) +
+                                 (fast ? kFastLds : 0);
         bool pow2 = true;
         for (int i = 0; i < 4; ++i) pow2 = pow2 && (a->k[i] & (a->k[i] - 1)) == 0;
         static bool score_attr = false;
         if (!score_attr) {   // over 64 KB of LDS with k = 64 per subspace
-            const int lds_max = static_cast<int>((4 * kK4 * kCS4 + kK4 * kK4 + kTripCap) * sizeof(float));
-            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&sel4_score_kernel<true, true>),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_max));
-            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&sel4_score_kernel<true, false>),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_max));
-            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&sel4_score_kernel<false, true>),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_max));
-            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&sel4_score_kernel<false, false>),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_max));
+            const int lds_max = static_cast<int>((4 * kK4 * kCS4 + kK4 * kK4 + kTripCap) * sizeof(float) + kFastLds);
+            const void* fns[6] = {reinterpret_cast<const void*>(&sel4_score_kernel<true, true, false>),
+                                  reinterpret_cast<const void*>(&sel4_score_kernel<true, false, false>),
+                                  reinterpret_cast<const void*>(&sel4_score_kernel<false, true, false>),
+                                  reinterpret_cast<const void*>(&sel4_score_kernel<false, false, false>),
+                                  reinterpret_cast<const void*>(&sel4_score_kernel<false, true, true>),
+                                  reinterpret_cast<const void*>(&sel4_score_kernel<false, false, true>)};
+            for (const void* f : fns)
+                IMI_HIP_CHECK(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds_max));
             score_attr = true;
         }
+        const dim3 blk(kScore4Threads);
         if (online && pow2)
-            hipLaunchKernelGGL((sel4_score_kernel<true, true>), grid, dim3(kScore4Threads), score_lds, stream, p);
+            hipLaunchKernelGGL((sel4_score_kernel<true, true, false>), grid, blk, score_lds, stream, p);
         else if (online)
-            hipLaunchKernelGGL((sel4_score_kernel<true, false>), grid, dim3(kScore4Threads), score_lds, stream, p);
+            hipLaunchKernelGGL((sel4_score_kernel<true, false, false>), grid, blk, score_lds, stream, p);
+        else if (fast && pow2)
+            hipLaunchKernelGGL((sel4_score_kernel<false, true, true>), grid, blk, score_lds, stream, p);
+        else if (fast)
+            hipLaunchKernelGGL((sel4_score_kernel<false, false, true>), grid, blk, score_lds, stream, p);
         else if (pow2)
-            hipLaunchKernelGGL((sel4_score_kernel<false, true>), grid, dim3(kScore4Threads), score_lds, stream, p);
+            hipLaunchKernelGGL((sel4_score_kernel<false, true, false>), grid, blk, score_lds, stream, p);
         else
-            hipLaunchKernelGGL((sel4_score_kernel<false, false>), grid, dim3(kScore4Threads), score_lds, stream, p);
+            hipLaunchKernelGGL((sel4_score_kernel<false, false, false>), grid, blk, score_lds, stream, p);
         IMI_LAUNCH_CHECK("sel4_score_kernel");
     }
     static bool attr_set[2] = {false, false};
