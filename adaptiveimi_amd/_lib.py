@@ -68,6 +68,7 @@ class AttentionArgs(ctypes.Structure):
         ("scale", _f32), ("out", _vp), ("out_lse", _vp),
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("delta_rows", _vp), ("n_delta", _vp), ("delta_cap", _i32), ("head_rows_bound", _vp),
+        ("rows_hint", _i32),
     ]
 
 

@@ -1049,6 +1049,7 @@ int fixed_tiles(const imi_attention_args* a, bool fixed_ok) {
         for (int h = 1; h < a->kv_heads; ++h)
             if (a->head_rows_bound[h] != a->head_rows_bound[0]) return 0;
     const int64_t rb = rows_bound(a);
+    if (a->rows_hint > 0 && 2 * static_cast<int64_t>(a->rows_hint) < rb) return 0;   // mostly empty windows
     for (int nt = 4; nt <= 8; ++nt)
         if (static_cast<int64_t>(a->kv_heads) * ((rb + 64 * nt - 1) / (64 * nt)) <= device_cus()) return nt;
     return 0;

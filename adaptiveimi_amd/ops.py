@@ -526,6 +526,29 @@ def sparse_attention(query: torch.Tensor, steady_keys: Optional[torch.Tensor], s
     return (out, lse) if return_lse else out
 
 
+def _rows_hint(cell_count: torch.Tensor, compact: Optional[Dict[str, torch.Tensor]], budget: "Budget",
+               steady_rows: int) -> int:
+    """Expected attended rows per head, for the attention's choice of split
+    pass only (one device sync, at plan time): cells of the index's mean
+    occupied size, as many as nprobe, the token rule and the page rule allow
+    (wave_buffer_cpu_hotcold.cpp:303-371), plus the steady zone; the largest
+    over the heads.  0 (unknown) in tile mode."""
+    if budget.tile_mode:
+        return 0
+    if compact is not None:
+        rows = compact["compact_size"].sum(1).double()
+        occ = compact["n_active"].double()
+    else:
+        rows = cell_count.sum(1).double()
+        occ = (cell_count > 0).sum(1).double()
+    mean = (rows / occ.clamp(min=1)).clamp(min=1).cpu().tolist()
+    est = 0.0
+    for m in mean:
+        cells = min(budget.nprobe, budget.buffer_pages // max(1, math.ceil(m / budget.page_size)))
+        est = max(est, min(budget.max_tokens + m, cells * m))
+    return int(min(est + steady_rows, 2 ** 30))
+
+
 class DecodePlan:
     """Pre-built arguments of imi_decode_step for one layer: only the query,
     output and static_len change between steps, so a step costs one ctypes
@@ -588,6 +611,7 @@ class DecodePlan:
                       for bp, m in zip(budget.head_buffer_pages, mt)]
             self._head_bounds = (ctypes.c_int32 * H)(*bounds)
             t.head_rows_bound = ctypes.addressof(self._head_bounds)
+        t.rows_hint = _rows_hint(cell_count, compact, budget, t.steady_stride)
         need = ctypes.c_size_t()
         check(_lib.lib().imi_decode_workspace_size(ctypes.byref(a), ctypes.byref(need)), "imi_decode_workspace_size")
         self.ws = torch.zeros(max(need.value, 256), dtype=torch.uint8, device=dev)

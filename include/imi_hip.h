@@ -267,6 +267,13 @@ typedef struct {
      * most 4 runs; more fall back to equal shares).  No counterpart in the
      * reference (its decode batch is one sequence). */
     const int32_t* head_rows_bound;
+    /* Optional expected attended rows per head (0 = unknown), e.g. the
+     * page rule over cells of the index's mean size.  A decode step takes
+     * the fixed-window split pass only when the hint is at least half the
+     * row bound: with far fewer rows, a few windows would hold them all.
+     * Never a bound and never read by the kernels.  No counterpart in the
+     * reference. */
+    int32_t rows_hint;
 } imi_attention_args;
 
 int imi_attention_workspace_size(const imi_attention_args* a, size_t* bytes);
