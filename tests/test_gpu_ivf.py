@@ -46,7 +46,8 @@ def _kv(H, T, seed=0, integer=False):
     return synthetic.make_kv(H, T, seed=seed)
 
 
-@pytest.mark.parametrize("T,k,integer", [(1500, 100, False), (1200, 700, False), (1000, 300, True)])
+@pytest.mark.parametrize("T,k,integer", [(1500, 100, False), (1200, 700, False), (1000, 300, True),
+                                           (6000, 4096, False), (5000, 4096, True)])   # the 4096-cluster limit
 def test_ivf_assign_bit_exact(ops, oracle, T, k, integer):
     """E-step over 128 dims with the centroids streamed through LDS in tiles
     (kmeans_core.cpp:222-242)."""
@@ -73,6 +74,7 @@ def test_ivf_assign_bit_exact(ops, oracle, T, k, integer):
     (2000, 900, 2, "first", 700),     # 699 identical first rows: > 256 clusters re-seeded in iteration 0
     (3000, 300, 2, "kmeans++", 0),    # picks 1-256 and 257-299 in two launches
     (1800, 520, 2, "kmeans++", 0),    # three launches
+    (6000, 4096, 2, "first", 0),      # the 4096-cluster limit (kIvfMaxK): 64 LDS tiles, 16 draw batches
 ])
 def test_ivf_kmeans_bit_exact(ops, oracle, T, k, iters, init, dup):
     """KmeansExecutorIVF (kmeans_core.cpp:503-595): labels and centroids equal
