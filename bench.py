@@ -314,7 +314,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": measured_traffic(workload_name(args, L, H, G, ks)),
-                     "kernel": "attention_kernel (gather + GQA split-K attention)",
+                     "kernel": "attention split pass: gather + GQA split-K attention (fixed_attention_kernel, "
+                               "fixed row windows, at configs[1]; attention_kernel, row-balanced, elsewhere)",
                      "bytes_per_launch": int(bytes_per_layer),
                      "with_merge": {"achieved": round(achieved_am, 1), "frac": round(achieved_am / HBM_PEAK_GBPS, 4),
                                     "kernels": "attention_kernel + merge_kernel"}},
@@ -560,11 +561,11 @@ def host_tier_leg(args, ks, bud, static_total):
 
 
 def measured_traffic(workload):
-    """HBM bytes per attention_kernel launch from the committed counter
+    """HBM bytes per split-pass launch from the committed counter
     summary of this exact workload (FETCH_SIZE + WRITE_SIZE per dispatch,
     each scaled by what the counter reads for a copy of known size), or
     None when no summary of this workload is committed."""
-    f = ROOT / "profiles" / "attention_kernel_traffic_config1.md"
+    f = ROOT / "profiles" / "fixed_attention_kernel_traffic_config1.md"
     if not f.exists():
         return None
     fields = {}
