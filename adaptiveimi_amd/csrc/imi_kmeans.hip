@@ -665,6 +665,8 @@ __device__ __forceinline__ long long block_excl_scan_ll(long long v, long long* 
     return base + incl - v;
 }
 
+typedef unsigned int __attribute__((ext_vector_type(4))) pp_u32x4_t;
+
 template <int DP>
 __global__ __launch_bounds__(256) void km_pp_dist_kernel(KmParams a, int c, PpBlock* stats, int nbp) {
     __shared__ __attribute__((aligned(16))) float cur[DP];
@@ -679,39 +681,46 @@ __global__ __launch_bounds__(256) void km_pp_dist_kernel(KmParams a, int c, PpBl
     if (tid < DP / 4)
         reinterpret_cast<float4*>(cur)[tid] =
             reinterpret_cast<const float4*>(a.cent + (static_cast<int64_t>(seg) * a.kmax + c - 1) * DP)[tid];
-    const int r0 = b * kPpRows + tid * kPpRPT;
+    // rows r0 + 256 j + tid (j < kPpRPT) for the thread; each round of 256
+    // rows is loaded coalesced (consecutive lanes read consecutive 16-byte
+    // chunks, so one wave instruction covers whole rows) and staged in LDS,
+    // from which each thread takes its own row
+    constexpr int CH = DP / 8;   // 16-byte chunks per row
+    extern __shared__ pp_u32x4_t s_rows[];   // [256][CH + 1]
+    const int r0 = b * kPpRows;
     float prev[kPpRPT];
 #pragma unroll
-    for (int j = 0; j < kPpRPT; ++j)   // c == 1: no distances yet (FLT_MAX)
-        prev[j] = (c > 1 && r0 + j < T) ? md[r0 + j] : 3.402823466e38f;
-    __syncthreads();   // cur ready
+    for (int j = 0; j < kPpRPT; ++j) {   // c == 1: no distances yet (FLT_MAX)
+        const int r = r0 + 256 * j + tid;
+        prev[j] = (c > 1 && r < T) ? md[r] : 3.402823466e38f;
+    }
     float m[kPpRPT];
     int emin = 0x7FFFFFFF, emax = 0;
-    // every row's loads in flight at once up to 64 dims (DP = 128: one row
-    // at a time, the registers of four rows would not fit)
-    constexpr int NRF = DP <= 64 ? kPpRPT : 1;
-    uint4 v[NRF][DP / 8];
-#pragma unroll
-    for (int j = 0; j < NRF; ++j) {
-        const uint4* row = reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(min(r0 + j, T - 1)) * a.ts);
-#pragma unroll
-        for (int d = 0; d < DP / 8; ++d) v[j][d] = row[d];
-    }
 #pragma unroll
     for (int j = 0; j < kPpRPT; ++j) {
-        if constexpr (NRF == 1) {
-            if (j > 0) {
-                const uint4* row =
-                    reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(min(r0 + j, T - 1)) * a.ts);
+        pp_u32x4_t ld[CH];
 #pragma unroll
-                for (int d = 0; d < DP / 8; ++d) v[0][d] = row[d];
-            }
+        for (int k = 0; k < CH; ++k) {
+            const int f = tid + 256 * k, row = f / CH, ch = f % CH;
+            const int r = min(r0 + 256 * j + row, T - 1);
+            ld[k] = reinterpret_cast<const pp_u32x4_t*>(xb + static_cast<int64_t>(r) * a.ts)[ch];
         }
-        const float dist = l2_lanes8_bf16<DP>(v[NRF == 1 ? 0 : j], cur);
+        if (j > 0) __syncthreads();   // the previous round's rows are read
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const int f = tid + 256 * k, row = f / CH, ch = f % CH;
+            s_rows[row * (CH + 1) + ch] = ld[k];
+        }
+        __syncthreads();   // (and cur, before the first round)
+        pp_u32x4_t v[CH];
+#pragma unroll
+        for (int k = 0; k < CH; ++k) v[k] = s_rows[tid * (CH + 1) + k];
+        const int r = r0 + 256 * j + tid;
+        const float dist = l2_lanes8_bf16<DP>(v, cur);
         float mm = prev[j];
         if (dist < mm) mm = dist;
-        m[j] = r0 + j < T ? mm : 0.0f;
-        if (r0 + j < T) md[r0 + j] = mm;
+        m[j] = r < T ? mm : 0.0f;
+        if (r < T) md[r] = mm;
         if (m[j] > 0.0f) {
             emin = min(emin, pp_exp(m[j]));
             emax = max(emax, pp_exp(m[j]));
@@ -1385,15 +1394,21 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
         }
         const int nbp = (a->n_tokens + kPpRows - 1) / kPpRows;
         PpBlock* st = static_cast<PpBlock*>(p.ppstats);
+        if (dp == 128)   // 68 KB of LDS per workgroup
+            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_pp_dist_kernel<128>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              static_cast<int>(256 * 17 * 16)));
         for (int c = 0; c < kmax; ++c) {
             if (c > 0) {
                 const dim3 grid(nbp, segs);
+                // LDS: one round of 256 rows at a padded stride
+                const size_t lds = static_cast<size_t>(256) * (dp / 8 + 1) * 16;
                 if (dp == 128)
-                    hipLaunchKernelGGL(km_pp_dist_kernel<128>, grid, dim3(256), 0, stream, p, c, st, nbp);
+                    hipLaunchKernelGGL(km_pp_dist_kernel<128>, grid, dim3(256), lds, stream, p, c, st, nbp);
                 else if (dp == 64)
-                    hipLaunchKernelGGL(km_pp_dist_kernel<64>, grid, dim3(256), 0, stream, p, c, st, nbp);
+                    hipLaunchKernelGGL(km_pp_dist_kernel<64>, grid, dim3(256), lds, stream, p, c, st, nbp);
                 else
-                    hipLaunchKernelGGL(km_pp_dist_kernel<32>, grid, dim3(256), 0, stream, p, c, st, nbp);
+                    hipLaunchKernelGGL(km_pp_dist_kernel<32>, grid, dim3(256), lds, stream, p, c, st, nbp);
                 IMI_LAUNCH_CHECK("km_pp_dist_kernel");
             }
             pk.c = c;
