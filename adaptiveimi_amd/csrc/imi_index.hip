@@ -87,11 +87,21 @@ __global__ void ix_zero_kernel(int32_t* x, int64_t n) {
         x[i] = 0;
 }
 
-__global__ __launch_bounds__(256) void ix_count_kernel(IxParams a, int32_t* count) {
+// Cell counts over the tokens in cell order (perm = the stable cell sort):
+// equal cells are contiguous, so each wave adds one count per run of equal
+// cells (one atomic per run instead of one per token).
+__global__ __launch_bounds__(256) void ix_count_kernel(IxParams a, const int32_t* perm, int32_t* count) {
     const int h = blockIdx.y;
-    const int t = blockIdx.x * 256 + threadIdx.x;
-    if (t >= a.T) return;
-    atomicAdd(&count[static_cast<int64_t>(h) * a.ncells + cell_of(a, h, t)], 1);
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int lane = lane_id();
+    const int64_t c = i < a.T ? cell_of(a, h, perm[static_cast<int64_t>(h) * a.T + i]) : -1;
+    const int64_t cp = __shfl(c, lane > 0 ? lane - 1 : 0);
+    const uint64_t starts = __builtin_amdgcn_ballot_w64(lane == 0 || c != cp);
+    if (c >= 0 && (lane == 0 || c != cp)) {
+        const uint64_t after = lane < 63 ? starts >> (lane + 1) : 0ull;
+        const int len = after ? __builtin_ctzll(after) + 1 : 64 - lane;
+        atomicAdd(&count[static_cast<int64_t>(h) * a.ncells + c], len);
+    }
 }
 
 constexpr int kOffCells = 8192;                 // cells per workgroup of the offset scan
@@ -434,7 +444,7 @@ extern "C" int imi_build_index(const imi_index_args* a, imi_stream_t stream_) {
     hipLaunchKernelGGL(ix_zero_kernel, dim3(static_cast<unsigned>((cells_total + 255) / 256 < 65535 ? (cells_total + 255) / 256 : 65535)),
                        dim3(256), 0, stream, a->cell_count, cells_total);
     IMI_LAUNCH_CHECK("ix_zero_kernel");
-    hipLaunchKernelGGL(ix_count_kernel, dim3(p.nblk, p.H), dim3(256), 0, stream, p, a->cell_count);
+    hipLaunchKernelGGL(ix_count_kernel, dim3(p.nblk, p.H), dim3(256), 0, stream, p, a->perm, a->cell_count);
     IMI_LAUNCH_CHECK("ix_count_kernel");
     const int nchunk = static_cast<int>((ncells + kOffCells - 1) / kOffCells);
     hipLaunchKernelGGL(ix_chunk_sums_kernel, dim3(nchunk, p.H), dim3(256), 0, stream, p, a->cell_count, p.sums,
