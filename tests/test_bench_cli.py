@@ -59,7 +59,7 @@ def test_traffic_comes_from_the_committed_summary_of_the_same_workload(monkeypat
 
     a = _parse(monkeypatch, [])
     name = bench.workload_name(a, 32, 8, 4, tuple(a.ks))
-    f = ROOT / "profiles" / "attention_kernel_traffic_config1.md"
+    f = ROOT / "profiles" / "fixed_attention_kernel_traffic_config1.md"
     assert bench.measured_traffic(name + " (other)") is None
     if not f.exists():
         assert bench.measured_traffic(name) is None
