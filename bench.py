@@ -84,6 +84,13 @@ def parse():
     p.add_argument("--config3-layers", type=int, default=2,
                    help="layers of the configs[3] leg (4-way 32^4 IMI, 2 x 8 KV heads at 262,144 tokens, GQA 8, "
                         "fixed 4,096-token budget): step and selection per layer; 0 skips it")
+    p.add_argument("--e2e-layers", type=int, default=32,
+                   help="end-to-end leg: a random-init Llama-3-8B-shaped model of this many layers prefills "
+                        "--e2e-context tokens through the drop-in cache (index built on the side stream during "
+                        "the prefill) and decodes --e2e-decode tokens greedily (0: skip; configs[1] only)")
+    p.add_argument("--e2e-context", type=int, default=131072)
+    p.add_argument("--e2e-decode", type=int, default=256)
+    p.add_argument("--e2e-only", action="store_true", help="run only the end-to-end leg and print its JSON")
     p.add_argument("--copy-probe-mb", type=int, default=0,
                    help="run a device-to-device copy of this many MiB (3 times) before the timed region, as the "
                         "known-size reference for FETCH_SIZE / WRITE_SIZE counter runs")
@@ -102,6 +109,8 @@ def parse():
         args.online_layers = 0
         args.host_tier_layers = 0
         args.config3_layers = 0
+        if not args.e2e_only:
+            args.e2e_layers = 0
     return args
 
 
@@ -119,6 +128,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.e2e_only:
+        print(json.dumps({"e2e": e2e_leg(args)}), flush=True)
+        return
     H, G, D, L = args.kv_heads * args.batch, args.groups, 128, args.layers   # H: KV heads of every sequence
     static_total = args.static_start + args.static_end
     T = args.context - static_total
@@ -279,6 +291,17 @@ def main():
         config3 = config3_leg(args, capture)
         log(f"[bench] configs[3] leg: {config3}")
 
+    used_graph = graph is not None
+    e2e = None
+    if args.e2e_layers > 0:
+        del plans, graph
+        torch.cuda.empty_cache()
+        try:
+            e2e = e2e_leg(args)
+        except (RuntimeError, ValueError) as exc:   # reported in the line; the decode-path figures stand
+            e2e = {"error": f"{type(exc).__name__}: {exc}"[:300]}
+        log(f"[bench] end-to-end leg: {e2e}")
+
     # ----------------------------------------------------- CPU baseline
     cpu = None
     if keep_first is not None:
@@ -301,7 +324,7 @@ def main():
             "workload": workload_name(args, L, H, G, ks),
             "layers": L, "context": args.context, "kv_heads": H, "q_heads": H * G, "static_window": static_total,
             "nprobe": bud.nprobe, "max_tokens": bud.max_tokens, "buffer_pages": bud.buffer_pages,
-            "hip_graph": graph is not None, "kmeans_init": args.kmeans_init,
+            "hip_graph": used_graph, "kmeans_init": args.kmeans_init,
         },
         "index_build_ms": {"per_layer_median": round(statistics.median(build_ms), 3),
                            "per_layer_min": round(min(build_ms), 3), "layers": L},
@@ -323,6 +346,7 @@ def main():
         "online_update": online,
         "host_tier": host_tier,
         "config3": config3,
+        "e2e": e2e,
     }
     print(json.dumps(result), flush=True)
 
@@ -342,6 +366,187 @@ def workload_name(args, L, H, G, ks):
         head = f"configs[4] attention path: {L} Llama-3-8B layers"
     return (f"{head} ({H} KV heads, GQA {G}, d128) at {args.context} tokens, IMI {imi}, {args.iters} Lloyd "
             f"iters{sample}, {budget}")
+
+
+def e2e_leg(args):
+    """End-to-end configs[1]: a random-init Llama-3-8B-shaped
+    model (hidden 4096, 32 q / 8 KV heads, head_dim 128, FFN 14336, vocab
+    128256, N(0, 0.02) bf16 weights, RMSNorm, rotate-half RoPE theta 500000)
+    prefills a prompt of uniform random token ids and decodes greedily, with
+    the drop-in cache driven as model_hub does (prefill.py:33-105: per layer
+    prefill_update_kv_cache, prefill attention over the returned K / V, sync;
+    base.py:324-350, 407-499: prepare_cache, then per layer
+    decode_update_kv_cache + imi_decode_attn).  The cache takes the reference
+    JSON's settings (config/Llama-3-8B-Instruct-Gradient-1048k.json: static
+    32 + 64, pages_per_cluster 2, cache_ratio 0.05, budget 0.1, 32 buffer
+    clusters, 20 Lloyd iterations, kmeans++ seeding) with BASELINE's IMI 2 x
+    64, or at 1M tokens 2 x 128 on a 65536-key sample.  Each
+    layer's index build runs on the cache's side stream while the following
+    layers prefill.  The same prefill without the cache gives the build time
+    the prefill does not hide.  Prefill attention is torch's flash SDPA (the
+    reference uses flash_attn; out of this build's scope); the model's GEMMs
+    are torch's."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from adaptiveimi_amd import ops
+    from adaptiveimi_amd.attn_hub.sparse_imi import imi_decode_attn
+    from adaptiveimi_amd.cache_hub.adaptive_imi import adpimi_cache
+
+    dev = torch.device("cuda:0")
+    L, S, steps = args.e2e_layers, args.e2e_context, args.e2e_decode
+    HID, HQ, HKV, D, FFN, VOC = 4096, 32, 8, 128, 14336, 128256
+    eps, theta, chunk = 1e-5, 500000.0, 16384
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(7)
+
+    def w(*shape):
+        return torch.randn(shape, generator=g, device=dev, dtype=bf).mul_(0.02)
+
+    embed, lm_head, norm = w(VOC, HID), w(VOC, HID), torch.ones(HID, dtype=bf, device=dev)
+    layers = [dict(wqkv=w((HQ + 2 * HKV) * D, HID), wo=w(HID, HQ * D), w13=w(2 * FFN, HID), w2=w(HID, FFN),
+                   ln1=torch.ones(HID, dtype=bf, device=dev), ln2=torch.ones(HID, dtype=bf, device=dev))
+              for _ in range(L)]
+    # RoPE angles of every position in fp64, kept as fp32 cos / sin tables
+    inv = theta ** (-torch.arange(0, D // 2, dtype=torch.float64, device=dev) * 2.0 / D)
+    ang = torch.arange(S + steps, dtype=torch.float64, device=dev)[:, None] * inv[None, :]
+    cos_t, sin_t = ang.cos().float(), ang.sin().float()
+    del ang
+
+    def rms(x, wt):
+        return F.rms_norm(x, (HID,), wt, eps)
+
+    def rope(x, pos):   # x [n, heads, D], pos [n]
+        c, s_ = cos_t[pos][:, None, :], sin_t[pos][:, None, :]
+        x1, x2 = x[..., : D // 2].float(), x[..., D // 2:].float()
+        return torch.cat([x1 * c - x2 * s_, x2 * c + x1 * s_], dim=-1).to(bf)
+
+    def qkv_of(x, W, pos):
+        n = x.shape[0]
+        q = torch.empty((n, HQ, D), dtype=bf, device=dev)
+        k = torch.empty((n, HKV, D), dtype=bf, device=dev)
+        v = torch.empty((n, HKV, D), dtype=bf, device=dev)
+        for s0 in range(0, n, chunk):
+            e = min(n, s0 + chunk)
+            t = rms(x[s0:e], W["ln1"]) @ W["wqkv"].t()
+            q[s0:e] = rope(t[:, : HQ * D].view(e - s0, HQ, D), pos[s0:e])
+            k[s0:e] = rope(t[:, HQ * D: (HQ + HKV) * D].view(e - s0, HKV, D), pos[s0:e])
+            v[s0:e] = t[:, (HQ + HKV) * D:].view(e - s0, HKV, D)
+        return q, k, v
+
+    def mlp_(x, W):   # x += MLP(rms(x)), in token chunks
+        for s0 in range(0, x.shape[0], chunk):
+            e = min(x.shape[0], s0 + chunk)
+            gu = rms(x[s0:e], W["ln2"]) @ W["w13"].t()
+            x[s0:e] += (F.silu(gu[:, :FFN]) * gu[:, FFN:]) @ W["w2"].t()
+
+    def logits_argmax(x):
+        return (rms(x, norm) @ lm_head.t()).float().argmax(-1)
+
+    def prefill(ids, cache, nl):
+        n = ids.shape[0]
+        pos = torch.arange(n, device=dev)
+        x = embed[ids]
+        for li in range(nl):
+            W = layers[li]
+            q, k, v = qkv_of(x, W, pos)
+            kk, vv = k[None], v[None]                          # [1, S, H, D]
+            if cache is not None:
+                kk, vv = cache.prefill_update_kv_cache(q[None], kk, vv, li, 0)
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                o = F.scaled_dot_product_attention(q.transpose(0, 1)[None].contiguous(),
+                                                   kk.transpose(1, 2).contiguous(), vv.transpose(1, 2).contiguous(),
+                                                   is_causal=True, enable_gqa=True)
+            del q, k, v, kk, vv
+            x += o[0].transpose(0, 1).reshape(n, HQ * D) @ W["wo"].t()
+            del o
+            if cache is not None:
+                cache.sync(li, 0)
+            mlp_(x, W)
+        return logits_argmax(x[-1:])
+
+    def decode(tok, pos, cache):
+        x = embed[tok]
+        for li, W in enumerate(layers):
+            t = rms(x, W["ln1"]) @ W["wqkv"].t()
+            q = rope(t[:, : HQ * D].view(1, HQ, D), pos)
+            k = rope(t[:, HQ * D: (HQ + HKV) * D].view(1, HKV, D), pos)
+            kk, vv = k.view(1, 1, HKV, D), t[:, (HQ + HKV) * D:].view(1, 1, HKV, D)
+            cache.decode_update_kv_cache(kk, vv, li)
+            o = imi_decode_attn(q.view(1, 1, HQ, D), kk, vv, li, cache)
+            x = x + o.view(1, HQ * D) @ W["wo"].t()
+            mlp_(x, W)
+        return logits_argmax(x)
+
+    four_m = S > 524288
+    kcfg = {"k1": 128, "k2": 128, "sample_keys": 65536} if four_m else {"k1": 64, "k2": 64}
+    kcfg.update(max_iters=20, tol=5e-4, early_stop_min_iter=20, early_stop_rel_tol=5e-4, init="kmeans++")
+    ids = torch.randint(0, VOC, (S,), generator=g, device=dev)
+    log(f"[e2e] {L} layers, {S}-token prompt, {steps} decode tokens; warm-up prefill of one layer")
+    prefill(ids, None, 1)          # kernel selection / code loading of every prefill op
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    prefill(ids, None, L)
+    torch.cuda.synchronize()
+    plain_s = time.perf_counter() - t0
+    log(f"[e2e] prefill without the index: {plain_s:.3f} s")
+    torch.cuda.empty_cache()
+    cache = adpimi_cache(valid_start=[0], layer_num=L, batch_size=1, max_length=S + steps, num_key_value_heads=HKV,
+                         num_heads=HQ, head_dim=D, dtype=bf, layer_mapping={str(i): "cuda:0" for i in range(L)},
+                         max_new_length=steps, input_length=S, static_pattern_start=32, static_pattern_end=64,
+                         core=22, pages_per_cluster=2, retrieval_budget=0.02 if four_m else 0.1, cache_ratio=0.05,
+                         buffer_cluster_num=32, prefill_bsz=1, num_gpus=1, model_size=8, subspace_parts=2,
+                         runtime_config={"kmeans": kcfg})
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    tok = prefill(ids, cache, L)
+    cache.prepare_cache()
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    log(f"[e2e] prefill with the index build: {prefill_s:.3f} s")
+    # the same build alone (layer 0's listed keys and values as the input)
+    lk0, lv0 = cache.list_keys[0][0, :, : cache.list_capacity], cache.list_values[0][0, :, : cache.list_capacity]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    alone = []
+    for _ in range(3):
+        e0.record()
+        km = dict(tol=5e-4, early_stop_min_iter=20, early_stop_rel_tol=5e-4, init="kmeans++")
+        if four_m:
+            cent, lab, _ = ops.kmeans_sampled(lk0, [kcfg["k1"], kcfg["k2"]], 20, kcfg["sample_keys"], **km)
+        else:
+            cent, lab, _ = ops.kmeans(lk0, [kcfg["k1"], kcfg["k2"]], 20, **km)
+        ops.build_index(lk0, lv0, cent, lab, [kcfg["k1"], kcfg["k2"]], compact=False)
+        e1.record()
+        torch.cuda.synchronize()
+        alone.append(e0.elapsed_time(e1))
+    del lk0, lv0, cent, lab
+    pos = torch.arange(S, S + steps, device=dev)
+    out = [tok]
+    t0 = time.perf_counter()
+    for i in range(steps - 1):
+        tok = decode(tok, pos[i:i + 1], cache)
+        out.append(tok)
+    torch.cuda.synchronize()
+    decode_s = time.perf_counter() - t0
+    ntok = steps - 1
+    toks = torch.cat(out).tolist()
+    res = {"model": "random-init Llama-3-8B shape (hidden 4096, 32 q / 8 KV heads, d128, FFN 14336, vocab 128256)",
+           "layers": L, "context": S, "decode_tokens": steps, "imi": "2x128, 65536-key sample" if four_m else "2x64",
+           "budget": 0.02 if four_m else 0.1, "kmeans": "kmeans++ seeding, 20 Lloyd iterations",
+           "prefill_s": round(prefill_s, 3), "prefill_without_index_s": round(plain_s, 3),
+           "exposed_index_build_ms_per_layer": round((prefill_s - plain_s) * 1e3 / L, 2),
+           "index_build_alone_ms_per_layer": round(min(alone), 2),
+           "decode_ms_per_token": round(decode_s * 1e3 / max(ntok, 1), 3),
+           "decode_tokens_per_s": round(ntok / decode_s, 2) if ntok else None,
+           "end2end_s": round(prefill_s + decode_s, 3), "nprobe": cache.nprobe,
+           "max_tokens": cache.max_retrieval_tokens, "buffer_pages": cache.buffer_size,
+           "first_tokens": toks[:8], "distinct_tokens": len(set(toks)),
+           "clock": "host wall clock with device synchronisation around the prefill (index build included) and "
+                    "around the decode loop (eager launches)"}
+    del cache, layers, embed, lm_head
+    torch.cuda.empty_cache()
+    return res
 
 
 def online_update_leg(args, ks, bud, static_total, capture):
