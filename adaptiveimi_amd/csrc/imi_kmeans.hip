@@ -304,7 +304,14 @@ size_t screen_lds_bytes(int kmax) {
     constexpr int KH = DP / 32;
     const size_t nct = (kmax + 15) / 16;
     return static_cast<size_t>(kmax) * (DP + 4) * 4 + nct * KH * 2 * 64 * 16 + nct * 16 * 4 + 256 * 2 * 8 +
-           4 * static_cast<size_t>(kmax) * 4 + 16 + (kScreenQueue + 1) * 4;
+           kScreenQueue * 8 + 4 * static_cast<size_t>(kmax) * 4 + 16 + (kScreenQueue + 1) * 4 +
+           (kScreenQueue + 1) * 4;
+}
+
+// Row shift left by K inside a row of 16 lanes: lane i gets lane i + K's value.
+template <int K>
+__device__ __forceinline__ float dpp_row_shl(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + K, 0xF, 0xF, false));
 }
 
 // KT > 0: every segment has k = 16 KT centroids (whole tiles, no per-tile
@@ -326,10 +333,12 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
     km_u32x4_t* apk = reinterpret_cast<km_u32x4_t*>(cs + a.kmax * CS);      // [nct][KH][hi,lo][64 lanes]
     float* ccs = reinterpret_cast<float*>(apk + nct_max * KH * 2 * 64);     // [nct * 16]
     uint64_t* cmask = reinterpret_cast<uint64_t*>(ccs + nct_max * 16);      // [256][2] candidate bits
-    int* wcnt = reinterpret_cast<int*>(cmask + 256 * 2);                     // [4][kmax]
+    uint64_t* qbest = cmask + 256 * 2;                                      // [kScreenQueue] (distance, centroid)
+    int* wcnt = reinterpret_cast<int*>(qbest + kScreenQueue);               // [4][kmax]
     float* red = reinterpret_cast<float*>(wcnt + 4 * a.kmax);               // [4]
     int* qtok = reinterpret_cast<int*>(red + 4);                            // [kScreenQueue] queued tokens
     int* qcnt = qtok + kScreenQueue;                                        // queue length
+    int* qoff = qcnt + 1;                                                   // [kScreenQueue + 1] first pair
 
     const float* cg = a.cent + static_cast<int64_t>(seg) * a.kmax * DP;
     {
@@ -522,8 +531,8 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
     } else {
         // No distance is read: a lone candidate is the reference's label (the
         // bound above).  Tokens with several candidates (a few percent, but
-        // in most waves) queue up, and the first wave runs all their exact
-        // passes instead of every wave running its own.
+        // in most waves) queue up; their (token, candidate) distances are
+        // spread over the block, 8 lanes per pair.
         const uint64_t m0 = cmask[tid * 2], m1 = cmask[tid * 2 + 1];
         arg = m0 ? __builtin_ctzll(m0) : (m1 ? 64 + __builtin_ctzll(m1) : 0);
         const bool multi = valid && __popcll(m0) + __popcll(m1) > 1;
@@ -537,7 +546,72 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
         if (multi && slot < kScreenQueue) qtok[slot] = tid;
         __syncthreads();
         const int nq = min(*qcnt, kScreenQueue);
-        // the exact pass of block token tk (its row re-read: it is in L2)
+        if (wave == 0) {
+            // the pairs of queued token i are [qoff[i], qoff[i + 1])
+            int n = 0;
+            if (lane < nq) {
+                const int tk = qtok[lane];
+                n = __popcll(cmask[tk * 2]) + __popcll(cmask[tk * 2 + 1]);
+                qbest[lane] = ~0ull;
+            }
+            const int incl = wave_incl_scan(n);
+            if (lane < kScreenQueue) qoff[lane] = incl - n;
+            if (lane == 63) qoff[kScreenQueue] = incl;
+        }
+        __syncthreads();
+        {
+            // Pair p on lanes 8 (p % 8) .. +7 of wave (p / 8) % 4: lane part j
+            // sums dims j, j + 8, .. in ascending order (the reference's
+            // lane j), the group adds the eight sums left to right on its
+            // first lane (row shifts inside the 16-lane row), and an LDS
+            // minimum over (distance bits, centroid) keeps the smallest
+            // distance below FLT_MAX and, among equal ones, the lowest
+            // centroid: the reference's strict < over ascending centroids.
+            const int npairs = qoff[kScreenQueue];
+            const int part = lane & 7;
+#pragma unroll 1
+            for (int p0 = 0; p0 < npairs; p0 += 32) {
+                const int pr = p0 + wave * 8 + (lane >> 3);
+                float acc = 0.0f;
+                int qi = 0, c = 0;
+                if (pr < npairs) {
+                    for (int step = 32; step > 0; step >>= 1)
+                        if (qi + step < nq && qoff[qi + step] <= pr) qi += step;
+                    const int tk = qtok[qi];
+                    int r = pr - qoff[qi];
+                    const uint64_t w0 = cmask[tk * 2], w1 = cmask[tk * 2 + 1];
+                    const int n0 = __popcll(w0);
+                    uint64_t mm = r < n0 ? w0 : w1;
+                    const int cb = r < n0 ? 0 : 64;
+                    r = r < n0 ? r : r - n0;
+                    for (int i = 0; i < r; ++i) mm &= mm - 1;
+                    c = cb + __builtin_ctzll(mm);
+                    const uint16_t* xr = kb + static_cast<int64_t>(blk * 256 + tk) * a.ts + part;
+                    uint16_t xv[DP / 8];
+#pragma unroll
+                    for (int i = 0; i < DP / 8; ++i) xv[i] = xr[8 * i];
+                    const float* cr = cs + c * CS + part;
+#pragma unroll
+                    for (int i = 0; i < DP / 8; ++i) {
+                        const float d = bf16_to_f32(xv[i]) - cr[8 * i];
+                        acc = __builtin_fmaf(d, d, acc);
+                    }
+                }
+                float t = acc;
+                t = t + dpp_row_shl<1>(acc);
+                t = t + dpp_row_shl<2>(acc);
+                t = t + dpp_row_shl<3>(acc);
+                t = t + dpp_row_shl<4>(acc);
+                t = t + dpp_row_shl<5>(acc);
+                t = t + dpp_row_shl<6>(acc);
+                t = t + dpp_row_shl<7>(acc);
+                if (pr < npairs && part == 0 && t < 3.402823466e38f)
+                    atomicMin(reinterpret_cast<unsigned long long*>(&qbest[qi]),
+                              (static_cast<unsigned long long>(__float_as_uint(t)) << 32) | static_cast<uint32_t>(c));
+            }
+        }
+        // past the queue's end a token runs its own exact pass (its row
+        // re-read: it is in L2)
         auto exact_label = [&](int tk) {
             km_u32x4_t xq[DP / 8];
 #pragma unroll
@@ -560,12 +634,12 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
             }
             return qa;
         };
-        // the queued tokens on the first threads (the label replaces the
-        // token in its slot); past the queue's end a token runs its own pass
-        if (tid < nq) qtok[tid] = exact_label(qtok[tid]);
         if (multi && slot >= kScreenQueue) arg = exact_label(tid);
         __syncthreads();
-        if (multi && slot < kScreenQueue) arg = qtok[slot];
+        if (multi && slot < kScreenQueue) {
+            const uint64_t b = qbest[slot];   // no distance below FLT_MAX: label 0, as the reference's loop
+            arg = b == ~0ull ? 0 : static_cast<int>(static_cast<uint32_t>(b));
+        }
         if (tid == 0) *qcnt = 0;   // read by every thread before the barrier above
     }
     if (valid) {
