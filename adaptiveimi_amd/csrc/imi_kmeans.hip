@@ -56,6 +56,13 @@ struct KmParams {
     int es_min;
     float es_rel;
     int exact;         // the E-step's distances are read (min distances or the early-stop inertia)
+    // Block member lists (no km_scan / km_scatter pass): the E-step writes each
+    // block's tokens in label order to `rank` ([seg][T], position blk * 256 +
+    // the token's place in its block) and the block's row of label offsets to
+    // loff ([seg][nblk][kmax + 1]: first place of each label, then the
+    // block's token count); the M-step finds its members from its label's
+    // pair of offsets in every row.  Null: the scanned member lists.
+    int32_t* loff;
 };
 
 struct Draws {
@@ -63,6 +70,7 @@ struct Draws {
 };
 
 constexpr int kDraws = 256;      // empty-cluster draws one launch carries
+constexpr int kLocalMaxBlk = 512;   // blocks (T <= 131072) of the block member lists
 constexpr int kIvfMaxK = 4096;   // IVF clusters per head
 
 __host__ __device__ inline int bits_for(int n) {
@@ -339,6 +347,10 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
     int* qtok = reinterpret_cast<int*>(red + 4);                            // [kScreenQueue] queued tokens
     int* qcnt = qtok + kScreenQueue;                                        // queue length
     int* qoff = qcnt + 1;                                                   // [kScreenQueue + 1] first pair
+    // the block rank's label offsets reuse the queue's slots, which are read
+    // before its first barrier ([kmax] <= 2 * kScreenQueue ints, [4])
+    int* lofs = reinterpret_cast<int*>(qbest);
+    int* lwsum = qoff;
 
     const float* cg = a.cent + static_cast<int64_t>(seg) * a.kmax * DP;
     {
@@ -650,9 +662,16 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
 
     float part = EXACT ? wave_sum(valid ? best : 0.0f) : 0.0f;
     if (lane_id() == 0) red[tid >> 6] = part;
-    const int r = block_digit_rank(arg, valid, k, bits_for(k), wcnt,
-                                   a.hist + static_cast<int64_t>(seg) * a.kmax * a.nblk, a.nblk, blk);
-    if (valid) a.rank[static_cast<int64_t>(seg) * a.T + t] = r;
+    if (a.loff) {
+        // block member lists: the token at its place in the block's label order
+        const int pos = block_digit_pos(arg, valid, k, bits_for(k), wcnt, lofs, lwsum,
+                                        a.loff + (static_cast<int64_t>(seg) * a.nblk + blk) * (a.kmax + 1));
+        if (valid) a.rank[static_cast<int64_t>(seg) * a.T + blk * 256 + pos] = t;
+    } else {
+        const int r = block_digit_rank(arg, valid, k, bits_for(k), wcnt,
+                                       a.hist + static_cast<int64_t>(seg) * a.kmax * a.nblk, a.nblk, blk);
+        if (valid) a.rank[static_cast<int64_t>(seg) * a.T + t] = r;
+    }
     if (tid == 0) a.ipart[static_cast<int64_t>(seg) * a.nblk + blk] = ((red[0] + red[1]) + red[2]) + red[3];
     }
 }
@@ -1125,28 +1144,94 @@ __global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, Draws 
     constexpr int NB = DP > 64 ? 2 : 4;   // local batches in flight per loader (register ring)
     constexpr int HALVES = DP > 64 ? DP / 64 : 1;   // dims per chain lane
     __shared__ km_u32x4_t ring[2 * NL][64 * PARTS];
+    // block member lists: the label's exclusive prefix over the blocks, its
+    // first place in each block, the waves' member counts
+    __shared__ int s_pref[kLocalMaxBlk];
+    __shared__ int s_lof[kLocalMaxBlk];
+    __shared__ int s_wt[4];
     const int c = blockIdx.x, seg = blockIdx.y;
     const int h = seg / a.P, p = seg % a.P;
     if (c >= a.k[p]) return;
     if (a.done && a.done[seg]) return;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int32_t* off = a.off + static_cast<int64_t>(seg) * (a.kmax + 1);
-    const int lo = off[c], hi = off[c + 1];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint16_t* kbase = a.keys + h * a.hs + p * DP;
     float* dst = a.cent + (static_cast<int64_t>(seg) * a.kmax + c) * DP;
-    if (hi == lo) {
-        // empty ordinals past this launch's draws: km_reseed_kernel
-        const int e = a.empties[static_cast<int64_t>(seg) * a.kmax + c];
+    const bool local = a.loff != nullptr;
+    int lo = 0, n = 0;
+    if (local) {
+        // this label's first place and count in every block (nblk <= 512:
+        // two blocks per thread, their offset pairs loaded together), then
+        // the prefix of the counts
+        const int32_t* rows = a.loff + static_cast<int64_t>(seg) * a.nblk * (a.kmax + 1) + c;
+        int cv[kLocalMaxBlk / 256], lv[kLocalMaxBlk / 256];
+#pragma unroll
+        for (int u = 0; u < kLocalMaxBlk / 256; ++u) {
+            const int b = min(2 * tid + u, a.nblk - 1);
+            lv[u] = rows[static_cast<int64_t>(b) * (a.kmax + 1)];
+            cv[u] = rows[static_cast<int64_t>(b) * (a.kmax + 1) + 1];
+        }
+#pragma unroll
+        for (int u = 0; u < kLocalMaxBlk / 256; ++u) cv[u] = 2 * tid + u < a.nblk ? cv[u] - lv[u] : 0;
+        const int run = cv[0] + cv[1];
+        const int incl = wave_incl_scan(run);
+        if (lane == 63) s_wt[wave] = incl;
+        __syncthreads();
+        int before = incl - run;
+        for (int w = 0; w < wave; ++w) before += s_wt[w];
+        if (2 * tid < a.nblk) {
+            s_pref[2 * tid] = before;
+            s_lof[2 * tid] = lv[0];
+        }
+        if (2 * tid + 1 < a.nblk) {
+            s_pref[2 * tid + 1] = before + cv[0];
+            s_lof[2 * tid + 1] = lv[1];
+        }
+        __syncthreads();
+        n = (s_wt[0] + s_wt[1]) + (s_wt[2] + s_wt[3]);
+    } else {
+        const int32_t* off = a.off + static_cast<int64_t>(seg) * (a.kmax + 1);
+        lo = off[c];
+        n = off[c + 1] - lo;
+    }
+    if (n == 0) {
+        int e;
+        if (local) {
+            // the empty ordinal: labels below c whose block counts are all zero
+            // (every thread sums one label's column, in parallel over labels)
+            __shared__ int s_emp;
+            if (tid == 0) s_emp = 0;
+            __syncthreads();
+            for (int c2 = tid; c2 < c; c2 += 256) {
+                const int32_t* r2 = a.loff + static_cast<int64_t>(seg) * a.nblk * (a.kmax + 1) + c2;
+                int sum = 0;
+                for (int b = 0; b < a.nblk; ++b) sum += r2[static_cast<int64_t>(b) * (a.kmax + 1) + 1] - r2[static_cast<int64_t>(b) * (a.kmax + 1)];
+                if (sum == 0) atomicAdd(&s_emp, 1);
+            }
+            __syncthreads();
+            e = s_emp;
+        } else {
+            e = a.empties[static_cast<int64_t>(seg) * a.kmax + c];   // past this launch's draws: km_reseed_kernel
+        }
         if (wave == 0 && e < kDraws) {
             const int tok = draws.v[e];
             for (int d = lane; d < DP; d += 64) dst[d] = bf16_to_f32(kbase[static_cast<int64_t>(tok) * a.ts + d]);
         }
         return;
     }
-    const int n = hi - lo;
     const int nb = (n + 63) >> 6;              // 64-row batches
     const int rounds = (nb + NL - 1) / NL;     // = local batches of loader 1
     const int32_t* srt = a.sorted + static_cast<int64_t>(seg) * a.T + lo;
+    const int32_t* lst = a.rank + static_cast<int64_t>(seg) * a.T;
+    // member j: the block holding it (the last one whose prefix is <= j) and
+    // its place there
+    auto member = [&](int j) {
+        if (!local) return srt[j];
+        int b = 0;
+#pragma unroll
+        for (int step = kLocalMaxBlk / 2; step > 0; step >>= 1)
+            b = (b + step < a.nblk && s_pref[b + step] <= j) ? b + step : b;
+        return lst[b * 256 + s_lof[b] + (j - s_pref[b])];
+    };
     // rounds padded to whole ring cycles: the loaders' loop body is then free
     // of branches, so the compiler's wait before each slot write counts the
     // loads issued since that batch's (a branch around a load makes it assume
@@ -1161,7 +1246,7 @@ __global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, Draws 
         // last member again (a valid row, never summed: the chain adds only
         // the first n).  No select on the loaded id: one would make the
         // compiler wait for each id load right after issuing it.
-#define KMB_ID(q) srt[min((NL * (q) + lw) * 64 + lane, n - 1)]
+#define KMB_ID(q) member(min((NL * (q) + lw) * 64 + lane, n - 1))
 #define KMB_ROWS(idv, slot)                                                                            \
     _Pragma("unroll") for (int u = 0; u < LPB; ++u) {                                                \
         const int id_ = __shfl((idv), u * RPL + rsub);                                               \
@@ -1275,7 +1360,7 @@ __global__ void km_reset_kernel(KmParams a) {
     if (seg >= a.H * a.P) return;
     a.prev[seg] = 3.402823466e38f;
     if (a.done) a.done[seg] = 0;
-    if (a.iters) a.iters[seg] = 0;
+    if (a.iters) a.iters[seg] = a.loff ? a.max_iters : 0;   // no km_scan counts them without early stop
 }
 
 int validate(const imi_kmeans_args* a, int& kmax, int& dp) {
@@ -1323,6 +1408,7 @@ size_t workspace_bytes(const imi_kmeans_args* a, int kmax, KmParams* out) {
     p.empties = cv.take<int32_t>(static_cast<size_t>(segs) * kmax);
     p.prev = cv.take<float>(segs);
     p.done = cv.take<int32_t>(segs);
+    p.loff = cv.take<int32_t>(static_cast<size_t>(segs) * nblk * (kmax + 1));
     if (a->init_mode == 2) {
         const int nbp = (a->n_tokens + kPpRows - 1) / kPpRows;
         PpBlock* st = cv.take<PpBlock>(static_cast<size_t>(segs) * nbp);
@@ -1446,6 +1532,11 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
     const int segs = a->kv_heads * a->parts;
     const bool early_stop = a->early_stop_min_iter <= a->max_iters;
     if (!early_stop) p.done = nullptr;  // no test can fire: skip the flag reads
+    // Block member lists instead of km_scan + km_scatter: without early stop
+    // (nothing reads the inertia), with the screened E-step (subspaces of at
+    // most 64 dims, k <= 128) and at most kLocalMaxBlk blocks.
+    const bool local = !early_stop && dp <= 64 && kmax <= kScreenMaxK && p.nblk <= kLocalMaxBlk;
+    if (!local) p.loff = nullptr;
 
     hipLaunchKernelGGL(km_reset_kernel, dim3((segs + 63) / 64), dim3(64), 0, stream, p);
     IMI_LAUNCH_CHECK("km_reset_kernel");
@@ -1502,11 +1593,13 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
         rc = dp == 128 ? run_assign<128>(p, segs, stream)
                        : (dp == 64 ? run_assign<64>(p, segs, stream) : run_assign<32>(p, segs, stream));
         if (rc) return rc;
-        hipLaunchKernelGGL(km_scan_kernel, dim3(segs), dim3(1024), 0, stream, p, it);
-        IMI_LAUNCH_CHECK("km_scan_kernel");
-        hipLaunchKernelGGL(km_scatter_kernel, dim3((p.nblk + kScatterBlocks - 1) / kScatterBlocks, segs), dim3(256),
-                           0, stream, p);
-        IMI_LAUNCH_CHECK("km_scatter_kernel");
+        if (!local) {
+            hipLaunchKernelGGL(km_scan_kernel, dim3(segs), dim3(1024), 0, stream, p, it);
+            IMI_LAUNCH_CHECK("km_scan_kernel");
+            hipLaunchKernelGGL(km_scatter_kernel, dim3((p.nblk + kScatterBlocks - 1) / kScatterBlocks, segs),
+                               dim3(256), 0, stream, p);
+            IMI_LAUNCH_CHECK("km_scatter_kernel");
+        }
         // Empty-cluster draws of this iteration: std::mt19937(it + 12345) with
         // uniform_int_distribution<int32_t>(0, T-1), one per empty cluster in
         // ascending cluster order (kmeans_core.cpp:299-311).

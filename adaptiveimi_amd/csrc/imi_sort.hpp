@@ -42,6 +42,55 @@ __device__ __forceinline__ int block_digit_rank(int digit, bool valid, int nbins
     return valid ? wcnt[wave * nbins + digit] + in_wave : 0;
 }
 
+// The same ranks as positions in the block's digit-sorted order: the item's
+// rank plus the count of smaller digits in the block (lofs, LDS of nbins
+// ints).  The block's row of digit offsets goes to loff_row[0 .. nbins - 1]
+// and its item count to loff_row[nbins] (one contiguous store per block).
+// nbins <= 256; `wsum` is LDS of 4 ints.
+__device__ __forceinline__ int block_digit_pos(int digit, bool valid, int nbins, int nbits, int* wcnt, int* lofs,
+                                               int* wsum, int32_t* loff_row) {
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    for (int i = tid; i < 4 * nbins; i += kSortBlock) wcnt[i] = 0;
+    __syncthreads();
+    const uint64_t active = __ballot(valid);
+    const uint64_t peers = match_peers(static_cast<uint32_t>(digit), nbits, active);
+    const int in_wave = __popcll(peers & lanemask_lt());
+    if (valid && in_wave == 0) wcnt[wave * nbins + digit] = __popcll(peers);
+    __syncthreads();
+    int run = 0;   // digit tid's count in this block
+    if (tid < nbins) {
+        for (int w = 0; w < 4; ++w) {
+            const int t = wcnt[w * nbins + tid];
+            wcnt[w * nbins + tid] = run;
+            run += t;
+        }
+    }
+    if (nbins <= 64) {   // one wave holds every digit: no cross-wave step
+        if (wave == 0) {
+            const int incl = wave_incl_scan(run);
+            if (tid < nbins) {
+                lofs[tid] = incl - run;
+                loff_row[tid] = incl - run;
+            }
+            if (tid == 63) loff_row[nbins] = incl;
+        }
+    } else {
+        const int incl = wave_incl_scan(run);
+        if ((tid & 63) == 63) wsum[wave] = incl;
+        __syncthreads();
+        int before = incl - run;
+        for (int w = 0; w < wave; ++w) before += wsum[w];
+        if (tid < nbins) {
+            lofs[tid] = before;
+            loff_row[tid] = before;
+        }
+        if (tid == 255) loff_row[nbins] = before + run;
+    }
+    __syncthreads();
+    return valid ? lofs[digit] + wcnt[wave * nbins + digit] + in_wave : 0;
+}
+
 // Exclusive scan, in place, of n ints by one 1024-thread block.  `sh` is LDS
 // of at least 33 ints.  Returns the total on every thread.  Each thread owns a
 // contiguous chunk; when n is a multiple of 4 and data 16-byte aligned the
