@@ -704,6 +704,51 @@ __global__ __launch_bounds__(256) void merge_kernel(DecParams a, int G) {
 }
 
 
+// The merge for heads of at most SMAX (32 or 64) splits: one wave per (head,
+// query head, 64 dims), no LDS and no barrier.  Lane s holds split s's (max,
+// sum), the split weights come from one wave max and one wave sum, and each
+// lane (one output dim) adds its partials in split order with the weights
+// read lane by lane (deterministic).  Loads and adds are unconditional:
+// splits past the head's count re-read its last partial and weigh 0.
+constexpr int kMergeWaveSplits = 64;
+
+template <int SMAX>
+__global__ __launch_bounds__(64) void merge_wave_kernel(DecParams a, int G) {
+    const int h = blockIdx.y, chunk = blockIdx.x;
+    const int g = chunk >> 1;
+    const int lane = threadIdx.x;
+    const int o = chunk * 64 + lane;   // g * 128 + d
+    int rx = a.run[0].x, ry = a.run[0].y, rz = a.run[0].z;
+#pragma unroll
+    for (int i = 1; i < kMaxRuns; ++i) {
+        const bool in = a.run[i].y <= h && a.run[i].x != INT_MAX;
+        rx = in ? a.run[i].x : rx;
+        ry = in ? a.run[i].y : ry;
+        rz = in ? a.run[i].z : rz;
+    }
+    const int ns = min(max(rz & 0xFFFF, 1), SMAX);
+    const int64_t first = rx + static_cast<int64_t>(h - ry) * ns;
+    const int64_t stride = static_cast<int64_t>(G) * 128;
+    const float* pacc = a.part_acc + first * stride + o;
+    const float* pml = a.part_ml + (first * G + g) * 2;
+    float v[SMAX];
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) v[s] = pacc[min(s, ns - 1) * stride];
+    const int sl = min(lane, ns - 1);
+    const float pm0 = pml[static_cast<int64_t>(sl) * G * 2];
+    const float pl0 = pml[static_cast<int64_t>(sl) * G * 2 + 1];
+    const float pm = lane < ns ? pm0 : -INFINITY;
+    const float M = wave_max(pm);
+    const float w = wexp(pm, M);   // 0 past ns and for empty splits
+    const float L = wave_sum(lane < ns ? pl0 * w : 0.0f);
+    float A = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SMAX; ++s) A = __builtin_fmaf(v[s], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), s)), A);
+    a.out[static_cast<int64_t>(h) * G * 128 + o] = f32_to_bf16(L > 0.0f ? A / L : 0.0f);
+    if (a.lse && lane == 0 && (chunk & 1) == 0)
+        a.lse[static_cast<int64_t>(h) * G + g] = L > 0.0f ? (M + log2f(L)) * 0.69314718055994530942f : -INFINITY;
+}
+
 // ------------------------------------------------- fixed-grid split pass
 // The decode step's split pass when every head has the same row bound and at
 // most kFixedCap selected cells (the selection of imi_select: every cell
@@ -1255,8 +1300,20 @@ int attn_run(const DecParams& p, int groups, hipStream_t stream, int kernels) {
         if (rc) return rc;
     }
     if (kernels & 2) {
-        hipLaunchKernelGGL(merge_kernel, dim3(2 * groups, p.H), dim3(256), 0, stream, p, groups);
-        IMI_LAUNCH_CHECK("merge_kernel");
+        int smax = 0;   // the most splits of any head
+        for (int r = 0; r < kMaxRuns; ++r)
+            if (p.run[r].x != INT_MAX) smax = std::max(smax, p.run[r].z & 0xFFFF);
+        if (smax <= 32) {
+            hipLaunchKernelGGL(merge_wave_kernel<32>, dim3(2 * groups, p.H), dim3(64), 0, stream, p, groups);
+            IMI_LAUNCH_CHECK("merge_wave_kernel");
+        } else if (smax <= kMergeWaveSplits) {
+            hipLaunchKernelGGL(merge_wave_kernel<kMergeWaveSplits>, dim3(2 * groups, p.H), dim3(64), 0, stream, p,
+                               groups);
+            IMI_LAUNCH_CHECK("merge_wave_kernel");
+        } else {
+            hipLaunchKernelGGL(merge_kernel, dim3(2 * groups, p.H), dim3(256), 0, stream, p, groups);
+            IMI_LAUNCH_CHECK("merge_kernel");
+        }
     }
     return IMI_OK;
 }
