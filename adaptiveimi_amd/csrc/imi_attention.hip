@@ -79,6 +79,11 @@ constexpr int kVStride = 144;        // u16 per LDS row of a wave's K / V tile (
 constexpr int kPF = 2;               // K / V tiles in flight per wave
 constexpr int kStageCap = 2048;      // selected cells staged in the prologue's first round trip
 constexpr int kStageMax = 16384;     // selected cells per head (row prefix + offset staged in LDS)
+constexpr int kStageMax16 = 12288;   // the same for 16 query heads per KV head (larger wave partials)
+// query heads per KV head with their own kernels (the 16 columns of the
+// matrix-core tile hold query n mod G in column n, so any G <= 16 fits)
+constexpr bool groups_supported(int g) { return (g >= 1 && g <= 8) || g == 16; }
+constexpr int stage_max(int g) { return g > 8 ? kStageMax16 : kStageMax; }
 // The short form (NR > 0): at most kFastCap selected cells (three entries
 // per thread in one round trip) and kWaves * 64 * NR rows per workgroup, so
 // that each lane keeps the locations of NR of its wave's rows in registers.
@@ -1180,8 +1185,8 @@ size_t attn_workspace(const imi_attention_args* a, DecParams* p, bool fixed_ok =
 int attn_validate(const imi_attention_args* a, bool need_sel) {
     IMI_REQUIRE(a != nullptr, IMI_ERR_INVALID, "imi_sparse_attention: null args");
     IMI_REQUIRE(a->dim == 128, IMI_ERR_UNSUPPORTED, "imi_sparse_attention: head_dim must be 128");
-    IMI_REQUIRE(a->groups == 1 || a->groups == 2 || a->groups == 4 || a->groups == 7 || a->groups == 8,
-                IMI_ERR_UNSUPPORTED, "imi_sparse_attention: %d query heads per kv head unsupported", a->groups);
+    IMI_REQUIRE(groups_supported(a->groups), IMI_ERR_UNSUPPORTED,
+                "imi_sparse_attention: %d query heads per kv head unsupported (1..8 or 16)", a->groups);
     IMI_REQUIRE(a->kv_heads > 0, IMI_ERR_INVALID, "imi_sparse_attention: kv_heads must be > 0");
     IMI_REQUIRE(a->kv_heads < 32768, IMI_ERR_UNSUPPORTED, "imi_sparse_attention: %d kv heads exceed 32767", a->kv_heads);
     IMI_REQUIRE(a->query && a->out, IMI_ERR_INVALID, "imi_sparse_attention: null query/out");
@@ -1208,8 +1213,8 @@ int attn_validate(const imi_attention_args* a, bool need_sel) {
             IMI_REQUIRE(a->n_delta != nullptr, IMI_ERR_INVALID, "imi_sparse_attention: null n_delta");
     }
     IMI_REQUIRE(a->sel_cap >= 0, IMI_ERR_INVALID, "imi_sparse_attention: sel_cap must be >= 0");
-    IMI_REQUIRE(a->sel_cap <= kStageMax, IMI_ERR_UNSUPPORTED, "imi_sparse_attention: sel_cap %d above %d",
-                a->sel_cap, kStageMax);
+    IMI_REQUIRE(a->sel_cap <= stage_max(a->groups), IMI_ERR_UNSUPPORTED, "imi_sparse_attention: sel_cap %d above %d",
+                a->sel_cap, stage_max(a->groups));
     IMI_REQUIRE(splits_per_head(a) <= kMaxSplit, IMI_ERR_UNSUPPORTED,
                 "imi_sparse_attention: %lld rows need more than %d splits per head",
                 static_cast<long long>(rows_bound(a)), kMaxSplit);
@@ -1246,7 +1251,7 @@ template <int G>
 int launch_att(const DecParams& p, hipStream_t stream) {
     static bool attr_set = false;
     if (!attr_set) {
-        constexpr size_t lds_max = static_cast<size_t>(2 * (kStageMax + 4) + tail_words<G>()) * 4;
+        constexpr size_t lds_max = static_cast<size_t>(2 * (stage_max(G) + 4) + tail_words<G>()) * 4;
         constexpr size_t lds_fast = static_cast<size_t>(fast_words<G>()) * 4;
         static_assert(lds_max <= 160 * 1024 && lds_fast <= 160 * 1024, "LDS of one workgroup");
         IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attention_kernel<G, 0>),
@@ -1293,9 +1298,13 @@ int attn_run(const DecParams& p, int groups, hipStream_t stream, int kernels) {
         switch (groups) {
             case 1: rc = launch_att<1>(p, stream); break;
             case 2: rc = launch_att<2>(p, stream); break;
+            case 3: rc = launch_att<3>(p, stream); break;
             case 4: rc = launch_att<4>(p, stream); break;
+            case 5: rc = launch_att<5>(p, stream); break;
+            case 6: rc = launch_att<6>(p, stream); break;
             case 7: rc = launch_att<7>(p, stream); break;
-            default: rc = launch_att<8>(p, stream); break;
+            case 8: rc = launch_att<8>(p, stream); break;
+            default: rc = launch_att<16>(p, stream); break;   // groups_supported: 16
         }
         if (rc) return rc;
     }
@@ -1423,8 +1432,8 @@ int decode_validate(const imi_decode_args* a) {
                               (a->sel.ring_cap > 0 ? a->sel.ring_cap : 0);
     IMI_REQUIRE(a->attn.max_rows >= need_rows, IMI_ERR_INVALID, "imi_decode_step: max_rows %d < %lld selectable rows",
                 a->attn.max_rows, static_cast<long long>(need_rows));
-    IMI_REQUIRE(a->sel.sel_cap <= kStageMax, IMI_ERR_UNSUPPORTED, "imi_decode_step: sel_cap %d above %d",
-                a->sel.sel_cap, kStageMax);
+    IMI_REQUIRE(a->sel.sel_cap <= stage_max(a->sel.groups), IMI_ERR_UNSUPPORTED,
+                "imi_decode_step: sel_cap %d above %d", a->sel.sel_cap, stage_max(a->sel.groups));
     int64_t nc;
     int km;
     int rc = select_validate(&a->sel, nc, km);

@@ -77,6 +77,21 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     return static_cast<uint16_t>(u >> 16);
 }
 
+// Element `col` of the G (<= 16) query rows of one KV head (row stride 128):
+// rows past G re-read row G - 1, so the loads carry no per-row test and are
+// all in flight at once; the upper eight only when G > 8 (a uniform branch).
+__device__ __forceinline__ void load_group_rows(const uint16_t* qh, int G, int col, uint16_t (&qv)[16]) {
+#pragma unroll
+    for (int g = 0; g < 8; ++g) qv[g] = qh[min(g, G - 1) * 128 + col];
+    if (G > 8) {
+#pragma unroll
+        for (int g = 8; g < 16; ++g) qv[g] = qh[min(g, G - 1) * 128 + col];
+    } else {
+#pragma unroll
+        for (int g = 8; g < 16; ++g) qv[g] = 0;
+    }
+}
+
 // fp32 -> uint32 whose unsigned order equals the float order (NaN-free input).
 __device__ __forceinline__ uint32_t order_key(float f) {
     uint32_t u = __float_as_uint(f);

@@ -29,7 +29,7 @@ namespace imi {
 
 namespace {
 
-constexpr int kMaxGroups = 8;  // query heads per KV head
+constexpr int kMaxGroups = 16;  // query heads per KV head
 constexpr int kRingCap = 1024; // delta ring entries (4 per thread)
 
 // ---------------------------------------------------------------- one-kernel path
@@ -291,8 +291,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(SelParams a) {
     uint16_t qv[kMaxGroups];
     if (tid < D) {
         const uint16_t* qh = a.q + static_cast<int64_t>(h) * a.G * D;
-#pragma unroll
-        for (int g = 0; g < kMaxGroups; ++g) qv[g] = qh[min(g, a.G - 1) * D + tid];
+        load_group_rows(qh, a.G, tid, qv);
     }
 #pragma unroll
     for (int u = 0; u < kV4; ++u) {

@@ -45,7 +45,7 @@ constexpr int kSegMax = 512;     // largest bucket ranked by counting (larger: a
 constexpr int kRingSet = 2048;   // ring-code set of the delta match (ring <= 1024 entries)
 constexpr int kK4 = 64;          // centroids per subspace the kernels hold
 constexpr int kDp4 = 32;         // subspace width (D = 128, 4 parts)
-constexpr int kMaxG4 = 8;        // query heads per KV head
+constexpr int kMaxG4 = 16;       // query heads per KV head
 constexpr int kScoreThreads = 256;   // 2-way score kernel
 constexpr int kScore4Threads = 1024; // 4-way score kernel
 constexpr int kFinalThreads = 1024;
@@ -594,8 +594,7 @@ __global__ __launch_bounds__(kScore4Threads) void sel4_score_kernel(Sel4 a) {
         // sum: unconditional loads, all in flight at once
         const uint16_t* qh = a.q + static_cast<int64_t>(h) * a.G * 128;
         uint16_t qv[kMaxG4];
-#pragma unroll
-        for (int g = 0; g < kMaxG4; ++g) qv[g] = qh[min(g, a.G - 1) * 128 + tid];
+        load_group_rows(qh, a.G, tid, qv);
         float acc = 0.0f;   // grouped-query sum, g ascending (compute_impl.cu:80-87)
 #pragma unroll
         for (int g = 0; g < kMaxG4; ++g)
@@ -842,8 +841,7 @@ __global__ __launch_bounds__(kScoreThreads) void sel2_dense_score_kernel(Sel4 a)
     if (tid < 128) {
         // rows past G re-read row G - 1 and are dropped from the sum
         const uint16_t* qh = a.q + static_cast<int64_t>(h) * a.G * 128;
-#pragma unroll
-        for (int j = 0; j < kMaxG4; ++j) qv[j] = qh[min(j, a.G - 1) * 128 + tid];
+        load_group_rows(qh, a.G, tid, qv);
     }
     const int l0 = in ? g / k1 : 0, l1 = in ? g - (g / k1) * k1 : 0;
     const float4* c0 = reinterpret_cast<const float4*>(a.cent + (static_cast<int64_t>(h) * 2 + 0) * a.kmax * 64);
@@ -928,8 +926,7 @@ __global__ __launch_bounds__(kScoreThreads) void sel1_score_kernel(Sel4 a) {
     if (tid < 128) {
         // rows past G re-read row G - 1 and are dropped from the sum
         const uint16_t* qh = a.q + static_cast<int64_t>(h) * a.G * 128;
-#pragma unroll
-        for (int j = 0; j < kMaxG4; ++j) qv[j] = qh[min(j, a.G - 1) * 128 + tid];
+        load_group_rows(qh, a.G, tid, qv);
     }
     int slot = -1;
     if (ONLINE && a.upd_slot && in) slot = a.upd_slot[static_cast<int64_t>(h) * ncells + g];

@@ -131,9 +131,10 @@ def test_select_and_decode_argument_checks(L):
     assert L.imi_decode_step(ctypes.byref(d), None) == 1
     assert "phases" in L.imi_last_error().decode()
     d.phases = 0
-    d.attn.groups = 5
-    d.sel.groups = 5
-    assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == 3
+    for g, rc in ((5, 0), (6, 0), (16, 0), (9, 3), (17, 3)):   # 1..8 and 16 query heads per KV head
+        d.attn.groups = g
+        d.sel.groups = g
+        assert L.imi_decode_workspace_size(ctypes.byref(d), ctypes.byref(need)) == rc, g
 
 
 def test_online_update_argument_checks(L):

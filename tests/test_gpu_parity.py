@@ -561,6 +561,9 @@ def _check_attention(out, ref):
     (20000, (32, 32), 4, 96, True, 0.1),
     (100000, (128, 128), 4, 96, False, 0.2),   # score + rank kernels; over 2048 selected cells per head
     (131072 - 96, (64, 64), 4, 97, False, 0.1),   # configs[1], the bench shape: nprobe 410, 1638 pages
+    # GQA groups of other model shapes: Qwen2.5-14B / 32B (5), Qwen2-1.5B (6), Llama-3.1-405B (16), and 3
+    (12000, (32, 32), 5, 96, False, 0.1), (8000, (32, 32), 6, 33, False, 0.1), (16000, (32, 32), 16, 96, False, 0.1),
+    (7000, (32, 32), 3, 0, False, 0.1), (20000, (32, 32), 16, 96, True, 0.1),
 ])
 def test_decode_step_matches_oracle(ops, oracle, T, ks, G, static_len, tiles, budget):
     note(f"[decode] T={T} ks={ks} G={G} static={static_len} tiles={tiles} budget={budget}")
