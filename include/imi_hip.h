@@ -160,7 +160,7 @@ typedef struct {
     const float* centroids;   /* device [H][P][kmax][Dp] */
     const int32_t* cell_count;  /* device [H][ncells] */
     const int32_t* cell_offset; /* device [H][ncells + 1] */
-    int32_t kv_heads, groups, dim, parts;
+    int32_t kv_heads, groups, dim, parts;   /* groups (G): 1..16 */
     int32_t k[4];
     int32_t nprobe, max_tokens, buffer_pages, page_size;
     /* outputs (device) */
@@ -248,7 +248,7 @@ typedef struct {
     const int32_t* n_rows;
     int32_t sel_cap;
     int32_t max_rows;             /* bound on n_rows (buffer_pages * page_size) */
-    int32_t kv_heads, groups, dim;
+    int32_t kv_heads, groups, dim;   /* groups (G): 1..8 or 16 */
     float scale;                  /* softmax scale (1/sqrt(D)) */
     uint16_t* out;                /* device bf16 [H*G][D] */
     float* out_lse;               /* device fp32 [H*G] natural-log LSE, may be NULL */
