@@ -690,13 +690,16 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
 // pick), no partial sum rounds, so the sequential doubles equal exact
 // integer prefix sums, which any blocking of the rows reproduces; otherwise
 // one thread replays the sequential loops.
-//   km_pp_dist_kernel  (blocks of kPpRows rows x segments): each row's min
-//                      distance to the picks so far (reference distance to
-//                      the previous pick), then the block's exponent range
-//                      and its sum in units of its own smallest exponent
-//   km_pp_pick_kernel  (one workgroup per segment): the segment's range and
-//                      total, the block that reaches the target, the row
-//                      inside it; writes the pick's centroid row
+//   km_pp_step_kernel  (launch c >= 1; blocks of kPpRows rows x segments):
+//                      pick c - 1 (the first row, or found from launch
+//                      c - 1's block statistics and minima), written by the
+//                      segment's block 0; then each row's min distance to
+//                      the picks 0..c-1, and the block's exponent range and
+//                      its sum in units of its own smallest exponent
+//   km_pp_pick_kernel  (one workgroup per segment): the last pick
+// Every block finds the pick itself (a few KB of statistics and one block's
+// minima), so no launch separates a pick from the next distance pass; the
+// minima and statistics alternate between two buffers for that reason.
 constexpr int kPpRPT = 4;                 // consecutive rows per thread
 constexpr int kPpRows = 256 * kPpRPT;     // rows per distance block
 
@@ -705,11 +708,6 @@ struct PpBlock {                 // per (segment, block)
     int emin, emax;              // exponent range of its non-zero values (emin = INT_MAX: none)
 };
 
-struct PpPick {
-    int c;                       // pick index
-    int first[4];                // c == 0: the first row, per subspace
-    double canon[4];             // c >= 1: canon of pick c, per subspace
-};
 
 // value m in units of 2^(emin_eff - 150) (m a multiple of that unit when the
 // segment passes the exactness test; shifts past 63 only occur when it fails)
@@ -760,123 +758,233 @@ __device__ __forceinline__ long long block_excl_scan_ll(long long v, long long* 
 
 typedef unsigned int __attribute__((ext_vector_type(4))) pp_u32x4_t;
 
-template <int DP>
-__global__ __launch_bounds__(256) void km_pp_dist_kernel(KmParams a, int c, PpBlock* stats, int nbp) {
-    __shared__ __attribute__((aligned(16))) float cur[DP];
-    __shared__ int s_e[2][4];
-    __shared__ long long s_u[4];
-    const int seg = blockIdx.y, b = blockIdx.x, tid = threadIdx.x;
-    const int h = seg / a.P, p = seg % a.P;
-    if (c >= a.k[p]) return;
-    const int T = a.T;
-    float* md = reinterpret_cast<float*>(a.rank) + static_cast<int64_t>(seg) * T;
-    const uint16_t* xb = a.keys + static_cast<int64_t>(h) * a.hs + p * DP;
-    if (tid < DP / 4)
-        reinterpret_cast<float4*>(cur)[tid] =
-            reinterpret_cast<const float4*>(a.cent + (static_cast<int64_t>(seg) * a.kmax + c - 1) * DP)[tid];
-    // rows r0 + 256 j + tid (j < kPpRPT) for the thread; each round of 256
-    // rows is loaded coalesced (consecutive lanes read consecutive 16-byte
-    // chunks, so one wave instruction covers whole rows) and staged in LDS,
-    // from which each thread takes its own row
-    constexpr int CH = DP / 8;   // 16-byte chunks per row
-    extern __shared__ pp_u32x4_t s_rows[];   // [256][CH + 1]
-    const int r0 = b * kPpRows;
-    float prev[kPpRPT];
-#pragma unroll
-    for (int j = 0; j < kPpRPT; ++j) {   // c == 1: no distances yet (FLT_MAX)
-        const int r = r0 + 256 * j + tid;
-        prev[j] = (c > 1 && r < T) ? md[r] : 3.402823466e38f;
+struct PpShared {
+    int e[2][4];
+    long long sc[4];
+    int blk, sel;
+    long long base;
+};
+
+// Row of pick c >= 1 of one segment (all 256 threads; the row to every
+// thread) from the minima md and block statistics st the distance pass of
+// pick c wrote: the segment's exponent range and, when every partial sum is
+// exact in double, the block and then the row whose integer prefix sum
+// reaches the target; otherwise thread 0 replays the reference's sequential
+// double sums (kmeans_core.cpp:160-181).
+__device__ int pp_pick_row(const float* md, const PpBlock* st, int nbp, int T, double canon, PpShared& sh) {
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        sh.blk = nbp;
+        sh.sel = T;
     }
-    float m[kPpRPT];
+    // this thread's consecutive blocks
+    const int per = (nbp + 255) / 256;
+    const int b0 = min(tid * per, nbp), b1 = min(b0 + per, nbp);
     int emin = 0x7FFFFFFF, emax = 0;
-#pragma unroll
-    for (int j = 0; j < kPpRPT; ++j) {
-        pp_u32x4_t ld[CH];
-#pragma unroll
-        for (int k = 0; k < CH; ++k) {
-            const int f = tid + 256 * k, row = f / CH, ch = f % CH;
-            const int r = min(r0 + 256 * j + row, T - 1);
-            ld[k] = reinterpret_cast<const pp_u32x4_t*>(xb + static_cast<int64_t>(r) * a.ts)[ch];
-        }
-        if (j > 0) __syncthreads();   // the previous round's rows are read
-#pragma unroll
-        for (int k = 0; k < CH; ++k) {
-            const int f = tid + 256 * k, row = f / CH, ch = f % CH;
-            s_rows[row * (CH + 1) + ch] = ld[k];
-        }
-        __syncthreads();   // (and cur, before the first round)
-        pp_u32x4_t v[CH];
-#pragma unroll
-        for (int k = 0; k < CH; ++k) v[k] = s_rows[tid * (CH + 1) + k];
-        const int r = r0 + 256 * j + tid;
-        const float dist = l2_lanes8_bf16<DP>(v, cur);
-        float mm = prev[j];
-        if (dist < mm) mm = dist;
-        m[j] = r < T ? mm : 0.0f;
-        if (r < T) md[r] = mm;
-        if (m[j] > 0.0f) {
-            emin = min(emin, pp_exp(m[j]));
-            emax = max(emax, pp_exp(m[j]));
-        }
+    for (int bb = b0; bb < b1; ++bb) {
+        emin = min(emin, st[bb].emin);
+        emax = max(emax, st[bb].emax);
     }
     const int w = tid >> 6;
     emin = wave_min_i(emin);
     emax = wave_max_i(emax);
     if (lane_id() == 0) {
-        s_e[0][w] = emin;
-        s_e[1][w] = emax;
+        sh.e[0][w] = emin;
+        sh.e[1][w] = emax;
     }
     __syncthreads();
-    const int be = min(min(s_e[0][0], s_e[0][1]), min(s_e[0][2], s_e[0][3]));
-    const int bx = max(max(s_e[1][0], s_e[1][1]), max(s_e[1][2], s_e[1][3]));
-    unsigned long long u = 0;
-    if (be != 0x7FFFFFFF) {
+    const int e_lo = min(min(sh.e[0][0], sh.e[0][1]), min(sh.e[0][2], sh.e[0][3]));
+    const int e_hi = max(max(sh.e[1][0], sh.e[1][1]), max(sh.e[1][2], sh.e[1][3]));
+    int logT = 0;
+    while ((1ll << logT) < static_cast<long long>(T)) ++logT;
+    const bool any = e_lo != 0x7FFFFFFF;
+    const bool exact = !any || (e_hi - e_lo) + 24 + logT <= 53;
+    if (exact) {
+        const int emin_eff = any ? e_lo : 1;
+        long long mine = 0;
+        for (int bb = b0; bb < b1; ++bb)
+            if (st[bb].emin != 0x7FFFFFFF)
+                mine += static_cast<long long>(st[bb].units << (st[bb].emin - emin_eff));
+        long long total_u;
+        const long long base = block_excl_scan_ll(mine, sh.sc, total_u);
+        const double scale = ldexp(1.0, emin_eff - 150);
+        const double total = static_cast<double>(total_u) * scale;
+        const double target = canon * total + 0.0;
+        const double tu = target / scale;
+        // the first block whose inclusive prefix reaches the target
+        long long run = base;
+        for (int bb = b0; bb < b1; ++bb) {
+            const long long ub =
+                st[bb].emin != 0x7FFFFFFF ? static_cast<long long>(st[bb].units << (st[bb].emin - emin_eff)) : 0;
+            if (static_cast<double>(run + ub) >= tu) {
+                atomicMin(&sh.blk, bb);
+                break;
+            }
+            run += ub;
+        }
+        __syncthreads();
+        const int blk = sh.blk;
+        if (blk < nbp) {
+            // the exclusive prefix of that block, from the thread that holds it
+            if (blk >= b0 && blk < b1) {
+                long long r = base;
+                for (int bb = b0; bb < blk; ++bb)
+                    if (st[bb].emin != 0x7FFFFFFF)
+                        r += static_cast<long long>(st[bb].units << (st[bb].emin - emin_eff));
+                sh.base = r;
+            }
+            __syncthreads();
+            // rows of that block: kPpRPT consecutive rows per thread, as the distance pass
+            const int r0 = blk * kPpRows + tid * kPpRPT;
+            long long uj[kPpRPT];
+            long long ut = 0;
 #pragma unroll
-        for (int j = 0; j < kPpRPT; ++j) u += pp_units(m[j], be);
+            for (int j = 0; j < kPpRPT; ++j) {
+                uj[j] = r0 + j < T ? static_cast<long long>(pp_units(md[r0 + j], emin_eff)) : 0;
+                ut += uj[j];
+            }
+            long long tot;
+            long long rr = sh.base + block_excl_scan_ll(ut, sh.sc, tot);
+#pragma unroll
+            for (int j = 0; j < kPpRPT; ++j) {
+                rr += uj[j];
+                if (r0 + j < T && static_cast<double>(rr) >= tu) {
+                    atomicMin(&sh.sel, r0 + j);
+                    break;
+                }
+            }
+        }
+    } else if (tid == 0) {
+        double tw = 0.0;
+        for (int i = 0; i < T; ++i) tw += static_cast<double>(md[i]);
+        const double target = canon * tw + 0.0;
+        double cs = 0.0;
+        int pick = 0;
+        for (int i = 0; i < T; ++i) {
+            cs += static_cast<double>(md[i]);
+            if (cs >= target) {
+                pick = i;
+                break;
+            }
+        }
+        sh.sel = pick;
     }
-    const long long us = wave_incl_scan_ll(static_cast<long long>(u));
-    if (lane_id() == 63) s_u[w] = us;
     __syncthreads();
-    if (tid == 0) {
-        PpBlock o;
-        o.units = static_cast<unsigned long long>(((s_u[0] + s_u[1]) + s_u[2]) + s_u[3]);
-        o.emin = be;
-        o.emax = bx;
-        stats[static_cast<int64_t>(seg) * nbp + b] = o;
-    }
+    return sh.sel < T ? sh.sel : 0;
 }
 
+struct PpStep {
+    int c;                       // launch index: pick c - 1, distances to it
+    int nbp;                     // blocks per segment
+    int nsub;                    // blocks per workgroup
+    int first[4];                // the first row, per subspace
+    double canon[4];             // canon of pick c - 1 (c >= 2), per subspace
+    const float* md_in;          // [seg][T] minima of launch c - 1
+    float* md_out;               // [seg][T]
+    const PpBlock* st_in;        // [seg][nbp] statistics of launch c - 1
+    PpBlock* st_out;
+};
+
 template <int DP>
-__global__ __launch_bounds__(256) void km_pp_pick_kernel(KmParams a, PpPick pk, const PpBlock* stats, int nbp) {
+__global__ __launch_bounds__(256) void km_pp_step_kernel(KmParams a, PpStep ps) {
+    __shared__ __attribute__((aligned(16))) float cur[DP];
     __shared__ int s_e[2][4];
-    __shared__ long long s_sc[4];
-    __shared__ int s_blk, s_sel;
-    __shared__ long long s_base;
-    const int seg = blockIdx.x, tid = threadIdx.x;
+    __shared__ long long s_u[4];
+    __shared__ PpShared sh;
+    // one round of 256 rows at a padded stride
+    constexpr int CH = DP / 8;   // 16-byte chunks per row
+    extern __shared__ __attribute__((aligned(16))) pp_u32x4_t s_rows[];   // [256][CH + 1]
+    const int nb = ps.nbp, c = ps.c, nsub = ps.nsub;
+    const int seg = blockIdx.y, wb = blockIdx.x, tid = threadIdx.x;
     const int h = seg / a.P, p = seg % a.P;
-    const int c = pk.c;
-    if (c >= a.k[p]) return;
+    if (c - 1 >= a.k[p]) return;
+    const bool dist = c < a.k[p];   // false: pick c - 1 is the segment's last
+    if (!dist && wb != 0) return;
     const int T = a.T;
+    const float* mdi = ps.md_in + static_cast<int64_t>(seg) * T;
+    float* mdo = ps.md_out + static_cast<int64_t>(seg) * T;
     const uint16_t* xb = a.keys + static_cast<int64_t>(h) * a.hs + p * DP;
-    int sel;
-    if (c == 0) {
-        sel = pk.first[p];
-    } else {
-        const float* md = reinterpret_cast<const float*>(a.rank) + static_cast<int64_t>(seg) * T;
-        const PpBlock* st = stats + static_cast<int64_t>(seg) * nbp;
-        if (tid == 0) {
-            s_blk = nbp;
-            s_sel = T;
+    const int blk0 = wb * nsub, blk1 = min(blk0 + nsub, nb);
+    // Block bk: rows bk * kPpRows + 256 j + tid (j < kPpRPT) for the thread;
+    // each round of 256 rows is loaded coalesced (consecutive lanes read
+    // consecutive 16-byte chunks, so one wave instruction covers whole rows)
+    // and staged in LDS, from which each thread takes its own row.  The first
+    // block's previous minima and first round do not depend on the pick:
+    // they are loaded before it.
+    float prev[kPpRPT];
+    pp_u32x4_t ld[CH];
+    if (dist) {
+        const int r0 = blk0 * kPpRows;
+#pragma unroll
+        for (int j = 0; j < kPpRPT; ++j) {   // c == 1: no distances yet (FLT_MAX)
+            const int r = r0 + 256 * j + tid;
+            prev[j] = (c > 1 && r < T) ? mdi[r] : 3.402823466e38f;
         }
-        // this thread's consecutive blocks
-        const int per = (nbp + 255) / 256;
-        const int b0 = min(tid * per, nbp), b1 = min(b0 + per, nbp);
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const int f = tid + 256 * k, row = f / CH, ch = f % CH;
+            const int r = min(r0 + row, T - 1);
+            ld[k] = reinterpret_cast<const pp_u32x4_t*>(xb + static_cast<int64_t>(r) * a.ts)[ch];
+        }
+    }
+    const int sel = c == 1 ? ps.first[p]
+                           : pp_pick_row(mdi, ps.st_in + static_cast<int64_t>(seg) * nb, nb, T, ps.canon[p], sh);
+    if (tid < CH) {
+        const pp_u32x4_t v = reinterpret_cast<const pp_u32x4_t*>(xb + static_cast<int64_t>(sel) * a.ts)[tid];
+        const float4 f0 = make_float4(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y));
+        const float4 f1 = make_float4(bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w));
+        reinterpret_cast<float4*>(cur)[2 * tid] = f0;
+        reinterpret_cast<float4*>(cur)[2 * tid + 1] = f1;
+        if (wb == 0) {
+            float4* dst = reinterpret_cast<float4*>(a.cent + (static_cast<int64_t>(seg) * a.kmax + c - 1) * DP);
+            dst[2 * tid] = f0;
+            dst[2 * tid + 1] = f1;
+        }
+    }
+    if (!dist) return;
+    const int w = tid >> 6;
+    for (int bk = blk0; bk < blk1; ++bk) {
+        const int r0 = bk * kPpRows;
+        if (bk > blk0) {
+#pragma unroll
+            for (int j = 0; j < kPpRPT; ++j) {
+                const int r = r0 + 256 * j + tid;
+                prev[j] = (c > 1 && r < T) ? mdi[r] : 3.402823466e38f;
+            }
+        }
+        float m[kPpRPT];
         int emin = 0x7FFFFFFF, emax = 0;
-        for (int bb = b0; bb < b1; ++bb) {
-            emin = min(emin, st[bb].emin);
-            emax = max(emax, st[bb].emax);
+#pragma unroll
+        for (int j = 0; j < kPpRPT; ++j) {
+            if (j > 0 || bk > blk0) {
+#pragma unroll
+                for (int k = 0; k < CH; ++k) {
+                    const int f = tid + 256 * k, row = f / CH, ch = f % CH;
+                    const int r = min(r0 + 256 * j + row, T - 1);
+                    ld[k] = reinterpret_cast<const pp_u32x4_t*>(xb + static_cast<int64_t>(r) * a.ts)[ch];
+                }
+                __syncthreads();   // the previous round's rows are read
+            }
+#pragma unroll
+            for (int k = 0; k < CH; ++k) {
+                const int f = tid + 256 * k, row = f / CH, ch = f % CH;
+                s_rows[row * (CH + 1) + ch] = ld[k];
+            }
+            __syncthreads();   // (and cur, before the first round)
+            pp_u32x4_t v[CH];
+#pragma unroll
+            for (int k = 0; k < CH; ++k) v[k] = s_rows[tid * (CH + 1) + k];
+            const int r = r0 + 256 * j + tid;
+            const float d = l2_lanes8_bf16<DP>(v, cur);
+            float mm = prev[j];
+            if (d < mm) mm = d;
+            m[j] = r < T ? mm : 0.0f;
+            if (r < T) mdo[r] = mm;
+            if (m[j] > 0.0f) {
+                emin = min(emin, pp_exp(m[j]));
+                emax = max(emax, pp_exp(m[j]));
+            }
         }
-        const int w = tid >> 6;
         emin = wave_min_i(emin);
         emax = wave_max_i(emax);
         if (lane_id() == 0) {
@@ -884,85 +992,40 @@ __global__ __launch_bounds__(256) void km_pp_pick_kernel(KmParams a, PpPick pk, 
             s_e[1][w] = emax;
         }
         __syncthreads();
-        const int e_lo = min(min(s_e[0][0], s_e[0][1]), min(s_e[0][2], s_e[0][3]));
-        const int e_hi = max(max(s_e[1][0], s_e[1][1]), max(s_e[1][2], s_e[1][3]));
-        int logT = 0;
-        while ((1ll << logT) < static_cast<long long>(T)) ++logT;
-        const bool any = e_lo != 0x7FFFFFFF;
-        const bool exact = !any || (e_hi - e_lo) + 24 + logT <= 53;
-        if (exact) {
-            const int emin_eff = any ? e_lo : 1;
-            long long mine = 0;
-            for (int bb = b0; bb < b1; ++bb)
-                if (st[bb].emin != 0x7FFFFFFF)
-                    mine += static_cast<long long>(st[bb].units << (st[bb].emin - emin_eff));
-            long long total_u;
-            const long long base = block_excl_scan_ll(mine, s_sc, total_u);
-            const double scale = ldexp(1.0, emin_eff - 150);
-            const double total = static_cast<double>(total_u) * scale;
-            const double target = pk.canon[p] * total + 0.0;
-            const double tu = target / scale;
-            // the first block whose inclusive prefix reaches the target
-            long long run = base;
-            for (int bb = b0; bb < b1; ++bb) {
-                const long long ub =
-                    st[bb].emin != 0x7FFFFFFF ? static_cast<long long>(st[bb].units << (st[bb].emin - emin_eff)) : 0;
-                if (static_cast<double>(run + ub) >= tu) {
-                    atomicMin(&s_blk, bb);
-                    break;
-                }
-                run += ub;
-            }
-            __syncthreads();
-            const int blk = s_blk;
-            if (blk < nbp) {
-                // the exclusive prefix of that block, from the thread that holds it
-                if (blk >= b0 && blk < b1) {
-                    long long r = base;
-                    for (int bb = b0; bb < blk; ++bb)
-                        if (st[bb].emin != 0x7FFFFFFF)
-                            r += static_cast<long long>(st[bb].units << (st[bb].emin - emin_eff));
-                    s_base = r;
-                }
-                __syncthreads();
-                // rows of that block: kPpRPT consecutive rows per thread, as the distance kernel
-                const int r0 = blk * kPpRows + tid * kPpRPT;
-                long long uj[kPpRPT];
-                long long ut = 0;
+        const int be = min(min(s_e[0][0], s_e[0][1]), min(s_e[0][2], s_e[0][3]));
+        const int bx = max(max(s_e[1][0], s_e[1][1]), max(s_e[1][2], s_e[1][3]));
+        unsigned long long u = 0;
+        if (be != 0x7FFFFFFF) {
 #pragma unroll
-                for (int j = 0; j < kPpRPT; ++j) {
-                    uj[j] = r0 + j < T ? static_cast<long long>(pp_units(md[r0 + j], emin_eff)) : 0;
-                    ut += uj[j];
-                }
-                long long tot;
-                long long rr = s_base + block_excl_scan_ll(ut, s_sc, tot);
-#pragma unroll
-                for (int j = 0; j < kPpRPT; ++j) {
-                    rr += uj[j];
-                    if (r0 + j < T && static_cast<double>(rr) >= tu) {
-                        atomicMin(&s_sel, r0 + j);
-                        break;
-                    }
-                }
-            }
-        } else if (tid == 0) {
-            double tw = 0.0;
-            for (int i = 0; i < T; ++i) tw += static_cast<double>(md[i]);
-            const double target = pk.canon[p] * tw + 0.0;
-            double cs = 0.0;
-            int pick = 0;
-            for (int i = 0; i < T; ++i) {
-                cs += static_cast<double>(md[i]);
-                if (cs >= target) {
-                    pick = i;
-                    break;
-                }
-            }
-            s_sel = pick;
+            for (int j = 0; j < kPpRPT; ++j) u += pp_units(m[j], be);
         }
+        const long long us = wave_incl_scan_ll(static_cast<long long>(u));
+        if (lane_id() == 63) s_u[w] = us;
         __syncthreads();
-        sel = s_sel < T ? s_sel : 0;
+        if (tid == 0) {
+            PpBlock o;
+            o.units = static_cast<unsigned long long>(((s_u[0] + s_u[1]) + s_u[2]) + s_u[3]);
+            o.emin = be;
+            o.emax = bx;
+            ps.st_out[static_cast<int64_t>(seg) * nb + bk] = o;
+        }
     }
+}
+
+// The last pick c of every segment with k == c + 1 (c == 0: the first row)
+// from the minima and statistics of launch c.
+template <int DP>
+__global__ __launch_bounds__(256) void km_pp_pick_kernel(KmParams a, PpStep ps) {
+    __shared__ PpShared sh;
+    const int seg = blockIdx.x, tid = threadIdx.x;
+    const int h = seg / a.P, p = seg % a.P;
+    const int c = ps.c;
+    if (c >= a.k[p]) return;
+    const int T = a.T, nb = ps.nbp;
+    const uint16_t* xb = a.keys + static_cast<int64_t>(h) * a.hs + p * DP;
+    const int sel = c == 0 ? ps.first[p]
+                           : pp_pick_row(ps.md_in + static_cast<int64_t>(seg) * T,
+                                         ps.st_in + static_cast<int64_t>(seg) * nb, nb, T, ps.canon[p], sh);
     float* dst = a.cent + (static_cast<int64_t>(seg) * a.kmax + c) * DP;
     for (int d = tid; d < DP; d += 256) dst[d] = bf16_to_f32(xb[static_cast<int64_t>(sel) * a.ts + d]);
 }
@@ -1411,7 +1474,7 @@ size_t workspace_bytes(const imi_kmeans_args* a, int kmax, KmParams* out) {
     p.loff = cv.take<int32_t>(static_cast<size_t>(segs) * nblk * (kmax + 1));
     if (a->init_mode == 2) {
         const int nbp = (a->n_tokens + kPpRows - 1) / kPpRows;
-        PpBlock* st = cv.take<PpBlock>(static_cast<size_t>(segs) * nbp);
+        PpBlock* st = cv.take<PpBlock>(static_cast<size_t>(2) * segs * nbp);   // two launches' worth
         if (out) p.ppstats = st;
     }
     if (out) *out = p;
@@ -1547,45 +1610,70 @@ extern "C" int imi_kmeans_execute(const imi_kmeans_args* a, imi_stream_t stream_
         // kmeans++ seeds 42, 43, 44, 45 by subspace, the same for every head
         // (kmeans_core.cpp:459, 469; IVF: seed 42, kmeans_core.cpp:548-556);
         // every segment's pick c in one pair of launches
-        PpPick pk{};
+        PpStep ps{};
         std::vector<double> canon[4];
         for (int part = 0; part < a->parts; ++part) {
             std::mt19937_64 rng(static_cast<uint64_t>(42 + part));
             std::uniform_int_distribution<int32_t> first(0, a->n_tokens - 1);
-            pk.first[part] = first(rng);
+            ps.first[part] = first(rng);
             canon[part].assign(a->k[part], 0.0);
             for (int c = 1; c < a->k[part]; ++c)
                 canon[part][c] = std::generate_canonical<double, std::numeric_limits<double>::digits>(rng);
         }
         const int nbp = (a->n_tokens + kPpRows - 1) / kPpRows;
+        ps.nbp = nbp;
         PpBlock* st = static_cast<PpBlock*>(p.ppstats);
+        // minima and statistics alternate between two buffers (the member
+        // lists' `rank` and `sorted`, free until the first E-step)
+        float* md[2] = {reinterpret_cast<float*>(p.rank), reinterpret_cast<float*>(p.sorted)};
+        PpBlock* sts[2] = {st, st + static_cast<size_t>(segs) * nbp};
+        const size_t lds = static_cast<size_t>(256) * (dp / 8 + 1) * 16;
         if (dp == 128)   // 68 KB of LDS per workgroup
-            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_pp_dist_kernel<128>),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                                              static_cast<int>(256 * 17 * 16)));
-        for (int c = 0; c < kmax; ++c) {
-            if (c > 0) {
-                const dim3 grid(nbp, segs);
-                // LDS: one round of 256 rows at a padded stride
-                const size_t lds = static_cast<size_t>(256) * (dp / 8 + 1) * 16;
-                if (dp == 128)
-                    hipLaunchKernelGGL(km_pp_dist_kernel<128>, grid, dim3(256), lds, stream, p, c, st, nbp);
-                else if (dp == 64)
-                    hipLaunchKernelGGL(km_pp_dist_kernel<64>, grid, dim3(256), lds, stream, p, c, st, nbp);
-                else
-                    hipLaunchKernelGGL(km_pp_dist_kernel<32>, grid, dim3(256), lds, stream, p, c, st, nbp);
-                IMI_LAUNCH_CHECK("km_pp_dist_kernel");
-            }
-            pk.c = c;
-            for (int part = 0; part < a->parts; ++part) pk.canon[part] = c < a->k[part] ? canon[part][c] : 0.0;
+            IMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&km_pp_step_kernel<128>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+        // one resident round of workgroups, each over nsub consecutive blocks
+        int per_cu = 0;
+        const void* fn = dp == 128 ? reinterpret_cast<const void*>(&km_pp_step_kernel<128>)
+                                   : (dp == 64 ? reinterpret_cast<const void*>(&km_pp_step_kernel<64>)
+                                               : reinterpret_cast<const void*>(&km_pp_step_kernel<32>));
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds) != hipSuccess || per_cu <= 0)
+            per_cu = 1;
+        const int64_t want = static_cast<int64_t>(per_cu) * device_cus();
+        ps.nsub = static_cast<int>(std::max<int64_t>(1, (static_cast<int64_t>(nbp) * segs + want - 1) / want));
+        const int nbw = (nbp + ps.nsub - 1) / ps.nsub;
+        // launch c (1 <= c < kmax): pick c - 1 and the distances to it
+        for (int c = 1; c < kmax; ++c) {
+            ps.c = c;
+            for (int part = 0; part < a->parts; ++part)
+                ps.canon[part] = c - 1 >= 1 && c - 1 < a->k[part] ? canon[part][c - 1] : 0.0;
+            ps.md_in = md[(c - 1) & 1];
+            ps.md_out = md[c & 1];
+            ps.st_in = sts[(c - 1) & 1];
+            ps.st_out = sts[c & 1];
+            const dim3 grid(nbw, segs);
             if (dp == 128)
-                hipLaunchKernelGGL(km_pp_pick_kernel<128>, dim3(segs), dim3(256), 0, stream, p, pk, st, nbp);
+                hipLaunchKernelGGL(km_pp_step_kernel<128>, grid, dim3(256), lds, stream, p, ps);
             else if (dp == 64)
-                hipLaunchKernelGGL(km_pp_pick_kernel<64>, dim3(segs), dim3(256), 0, stream, p, pk, st, nbp);
+                hipLaunchKernelGGL(km_pp_step_kernel<64>, grid, dim3(256), lds, stream, p, ps);
             else
-                hipLaunchKernelGGL(km_pp_pick_kernel<32>, dim3(segs), dim3(256), 0, stream, p, pk, st, nbp);
-            IMI_LAUNCH_CHECK("km_pp_pick_kernel");
+                hipLaunchKernelGGL(km_pp_step_kernel<32>, grid, dim3(256), lds, stream, p, ps);
+            IMI_LAUNCH_CHECK("km_pp_step_kernel");
         }
+        // the last pick of the segments with kmax centroids
+        const int c = kmax - 1;
+        ps.c = c;
+        for (int part = 0; part < a->parts; ++part) ps.canon[part] = c >= 1 && c < a->k[part] ? canon[part][c] : 0.0;
+        ps.md_in = md[c & 1];
+        ps.st_in = sts[c & 1];
+        ps.md_out = nullptr;
+        ps.st_out = nullptr;
+        if (dp == 128)
+            hipLaunchKernelGGL(km_pp_pick_kernel<128>, dim3(segs), dim3(256), 0, stream, p, ps);
+        else if (dp == 64)
+            hipLaunchKernelGGL(km_pp_pick_kernel<64>, dim3(segs), dim3(256), 0, stream, p, ps);
+        else
+            hipLaunchKernelGGL(km_pp_pick_kernel<32>, dim3(segs), dim3(256), 0, stream, p, ps);
+        IMI_LAUNCH_CHECK("km_pp_pick_kernel");
     }
     for (int it = 0; it < a->max_iters; ++it) {
         // the inertia of iteration it enters the stop tests of it and it + 1

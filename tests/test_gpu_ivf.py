@@ -8,7 +8,7 @@ merged centroid, which for IVF is the centroid itself; retrieval.py:295-303;
 wave_buffer_cpu_hotcold.cpp:303-371).
 
 Bit-exact: E-step labels and distances, full Lloyd runs (first-k and
-kmeans++ initialisation, kmeans++ picks over several launches, more than 256
+kmeans++ initialisation (one launch per pick), more than 256
 empty clusters re-seeded in one iteration), cell order, CSR, permutation,
 selected cells and row totals.  Attention within 2e-2 abs / 1e-2 rel.
 """
@@ -72,8 +72,8 @@ def test_ivf_assign_bit_exact(ops, oracle, T, k, integer):
     (3000, 200, 4, "first", 0),
     (2500, 600, 3, "first", 0),
     (2000, 900, 2, "first", 700),     # 699 identical first rows: > 256 clusters re-seeded in iteration 0
-    (3000, 300, 2, "kmeans++", 0),    # picks 1-256 and 257-299 in two launches
-    (1800, 520, 2, "kmeans++", 0),    # three launches
+    (3000, 300, 2, "kmeans++", 0),    # 300 picks
+    (1800, 520, 2, "kmeans++", 0),    # 520 picks
     (6000, 4096, 2, "first", 0),      # the 4096-cluster limit (kIvfMaxK): 64 LDS tiles, 16 draw batches
 ])
 def test_ivf_kmeans_bit_exact(ops, oracle, T, k, iters, init, dup):

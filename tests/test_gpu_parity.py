@@ -88,7 +88,8 @@ def test_kmeans_full_run_bit_exact(ops, oracle, T, k, iters):
             assert np.array_equal(cent[h, p], cents[p]), (h, p)
 
 
-@pytest.mark.parametrize("T,ks,iters", [(3000, (32, 32), 4), (2049, (16, 16, 16, 16), 3), (700, (64, 64), 2)])
+@pytest.mark.parametrize("T,ks,iters", [(3000, (32, 32), 4), (2049, (16, 16, 16, 16), 3), (700, (64, 64), 2),
+                                         (2500, (40, 24), 2), (1100, (1, 8), 1)])
 def test_kmeans_plusplus_bit_exact(ops, oracle, T, ks, iters):
     """kmeans++ initialisation (kmeans_core.cpp:138-186, seeds 42 + subspace):
     the GPU picks the same rows as the oracle, which runs the reference's
