@@ -1354,6 +1354,43 @@ __global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, Draws 
         for (int q = 0; q < rounds_pad; ++q) {
             __syncthreads();   // round q's slots are filled
             if (q >= rounds) continue;
+            if (HALVES == 1 && NL * 64 * (q + 1) <= n) {
+                // a full round (three batches of 64 members): the next batch's
+                // reads are issued before the current batch's additions, and
+                // the widening of value j + 1 is scheduled between the adds of
+                // j - 1 and j, so no add waits on the instruction before it
+                const int lg = lane >> 4, ln = lane & 15;
+                const int boff = (ln >> 2) * DP + 16 * (lg % (DP / 16)) + 4 * (ln & 3);
+                km_u32x2_t w[2][16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    w[0][i] = __builtin_bit_cast(
+                        km_u32x2_t,
+                        __builtin_amdgcn_ds_read_tr16_b64_v4i16((km_lds_s16x4_t*)(reinterpret_cast<const uint16_t*>(
+                                                                    ring[(q & 1) * NL]) + boff + 4 * i * DP)));
+#pragma unroll
+                for (int lw = 0; lw < NL; ++lw) {
+                    if (lw + 1 < NL) {
+#pragma unroll
+                        for (int i = 0; i < 16; ++i)
+                            w[(lw + 1) & 1][i] = __builtin_bit_cast(
+                                km_u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                (km_lds_s16x4_t*)(reinterpret_cast<const uint16_t*>(
+                                                                      ring[(q & 1) * NL + lw + 1]) + boff + 4 * i * DP)));
+                    }
+                    float f[64];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        f[4 * i] = __uint_as_float(w[lw & 1][i][0] << 16);
+                        f[4 * i + 1] = __uint_as_float(w[lw & 1][i][0] & 0xFFFF0000u);
+                        f[4 * i + 2] = __uint_as_float(w[lw & 1][i][1] << 16);
+                        f[4 * i + 3] = __uint_as_float(w[lw & 1][i][1] & 0xFFFF0000u);
+                    }
+#pragma unroll
+                    for (int j = 0; j < 64; ++j) acc[0] = acc[0] + f[j];
+                }
+                continue;
+            }
 #pragma unroll
             for (int lw = 0; lw < NL; ++lw) {
                 const int b = NL * q + lw;
