@@ -739,6 +739,210 @@ __global__ __launch_bounds__(256) void similarity_kernel(const uint16_t* q, cons
     out[static_cast<int64_t>(h) * out_stride + c] = s;
 }
 
+// ---- Tile mode with the delta append (retrieval.py:480-509) ----
+//
+// The reference attends tile after tile, each through its own execution
+// buffer, and appends the delta entries that match a tile after that tile's
+// rows (async_update.py:41-76).  Here every tile is attended in the one pass
+// over the union of the tiles, so only the delta list has to follow the
+// tiles: per tile t of head h, the valid ring entries (index order) whose
+// cell is one of the tile's cells -- or the padding id, when the head took
+// fewer cells into tile t than the head that took most, so that its row of
+// the tile tensor is padded -- up to the buffer rows the tile's cells leave.
+// Tiles are each head's greedy runs of its ranked cells that fit the page
+// budget (_build_cluster_tiles, retrieval.py:30-112); the tile count of the
+// call is the most any head has.  Two launches after the selection:
+//   tile_ends_kernel   (one workgroup per head) the end rank of every tile
+//   tile_delta_kernel  (one workgroup per head) the cross-head tile sizes
+//                      where a padding entry exists, and the delta list
+// A padding entry can match several tiles, and the reference then attends
+// its row once per such tile; the list keeps every repeat up to ring_cap
+// rows per head.
+constexpr int kTileRanks = 8192;   // ranks the tiles of a head cover (>= any K')
+constexpr int kTileSet = 2048;     // ring-code set (ring <= 1024 entries)
+
+struct TileDeltaParams {
+    int H, sel_cap;
+    const int32_t* sel_cell;
+    const int32_t* sel_count;
+    const int32_t* sel_prefix;
+    const int32_t* n_sel;
+    int page_size, buffer_pages;
+    const int32_t* head_buffer_pages;
+    const int32_t* ring_cell;
+    const int32_t* ring_row;
+    const int32_t* ring_n;
+    int ring_cap, exec_rows;
+    int32_t* delta_rows;
+    int32_t* n_delta;
+    int32_t* tile_end;   // [H][sel_cap] scratch
+    int32_t* n_tiles;    // [H] scratch
+};
+
+__device__ __forceinline__ int tile_block_max(int v, int* sh) {
+    v = wave_max_i(v);
+    if (lane_id() == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    int r = sh[0];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) r = max(r, sh[w]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ int tile_block_min(int v, int* sh) {
+    return -tile_block_max(-v, sh);
+}
+
+__global__ __launch_bounds__(1024) void tile_ends_kernel(TileDeltaParams a) {
+    __shared__ int P[kTileRanks];          // inclusive page prefix over the ranks
+    __shared__ uint16_t nxt[kTileRanks];   // end of the tile that starts at each rank
+    __shared__ int sh[80];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int m = min(max(a.n_sel[h], 0), min(a.sel_cap, kTileRanks));
+    const int B = a.head_buffer_pages ? min(a.head_buffer_pages[h], a.buffer_pages) : a.buffer_pages;
+    const int32_t* cnt = a.sel_count + static_cast<int64_t>(h) * a.sel_cap;
+    constexpr int RPT = kTileRanks / 1024;
+    int pg[RPT], sum = 0;
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) {
+        const int r = RPT * tid + u;
+        const int sz = r < m ? cnt[r] : 0;
+        pg[u] = sz > 0 ? max((sz + a.page_size - 1) / a.page_size, 1) : 0;
+        sum += pg[u];
+    }
+    int incl = sum, dummy = 0, tot, dtot;
+    block_incl_scan2(incl, dummy, sh, tot, dtot);
+    int run = incl - sum;
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) {
+        run += pg[u];
+        P[RPT * tid + u] = run;
+    }
+    __syncthreads();
+    // the tile that starts at rank s ends before the first rank whose
+    // prefix exceeds the pages before s plus the budget (every rank below m
+    // fits alone: the selection stops at the first cell that does not)
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) {
+        const int s0 = RPT * tid + u;
+        if (s0 < m) {
+            const int lim = (s0 > 0 ? P[s0 - 1] : 0) + B;
+            int lo = s0, hi = m;   // first e in [s0, m] with P[e] > lim (m: none)
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (P[mid] > lim) hi = mid;
+                else lo = mid + 1;
+            }
+            nxt[s0] = static_cast<uint16_t>(max(lo, s0 + 1));
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int32_t* ends = a.tile_end + static_cast<int64_t>(h) * a.sel_cap;
+        int t = 0;
+        for (int s0 = 0; s0 < m; s0 = nxt[s0]) ends[t++] = nxt[s0];
+        a.n_tiles[h] = t;
+    }
+}
+
+__device__ __forceinline__ int tile_slot(int code) {
+    return static_cast<int>((static_cast<uint32_t>(code) * 2654435761u) >> 21) & (kTileSet - 1);
+}
+
+__global__ __launch_bounds__(1024) void tile_delta_kernel(TileDeltaParams a) {
+    __shared__ int te[kTileRanks];     // this head's tile ends
+    __shared__ int rtab[kTileSet];     // ring-code set
+    __shared__ int rtile[kTileSet];    // tile of each code (-1: in no tile)
+    __shared__ int sh[80];
+    const int h = blockIdx.x, tid = threadIdx.x, wave = tid >> 6;
+    const int sc = a.sel_cap;
+    const int m = min(max(a.n_sel[h], 0), min(sc, kTileRanks));
+    const int nh = min(a.n_tiles[h], m);
+    int nt = 0;
+    for (int i = tid; i < a.H; i += 1024) nt = max(nt, a.n_tiles[i]);
+    for (int t = tid; t < nh; t += 1024) te[t] = a.tile_end[static_cast<int64_t>(h) * sc + t];
+    for (int i = tid; i < kTileSet; i += 1024) {
+        rtab[i] = -1;
+        rtile[i] = -1;
+    }
+    nt = tile_block_max(nt, sh);   // (its barriers also publish te and the cleared set)
+    const int rn = min(max(a.ring_n[h], 0), a.ring_cap);
+    int code = -3, rrow = 0, slot = -1;
+    if (tid < rn) {
+        code = a.ring_cell[static_cast<int64_t>(h) * a.ring_cap + tid];
+        rrow = a.ring_row[static_cast<int64_t>(h) * a.ring_cap + tid];
+    }
+    if (code >= 0) {
+        int i = tile_slot(code);
+        while (true) {
+            const int prev = atomicCAS(&rtab[i], -1, code);
+            if (prev == -1 || prev == code) break;
+            i = (i + 1) & (kTileSet - 1);
+        }
+        slot = i;
+    }
+    __syncthreads();
+    // the tile of each ranked cell whose code the ring holds
+    for (int r = tid; r < m; r += 1024) {
+        const int c = a.sel_cell[static_cast<int64_t>(h) * sc + r];
+        int i = tile_slot(c);
+        while (rtab[i] != c && rtab[i] != -1) i = (i + 1) & (kTileSet - 1);
+        if (rtab[i] == c) {
+            int lo = 0, hi = nh - 1;   // the first tile that ends past r
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (te[mid] > r) hi = mid;
+                else lo = mid + 1;
+            }
+            rtile[i] = lo;
+        }
+    }
+    const bool padc = code == -1;
+    const int npad = tile_block_max(padc ? 1 : 0, sh);   // any padding entry (its barriers publish rtile)
+    const int my_t = slot >= 0 ? rtile[slot] : -1;
+    const int32_t* pre = a.sel_prefix + static_cast<int64_t>(h) * (sc + 1);
+    int base = 0;
+    // every tile when a padding entry can match, else only the tiles holding matches
+    int t = npad > 0 ? 0 : tile_block_min(my_t >= 0 ? my_t : INT_MAX, sh);
+    while (t < nt) {
+        const int s_t = t == 0 ? 0 : (t - 1 < nh ? te[t - 1] : m);
+        const int e_t = t < nh ? te[t] : m;
+        const int rows_t = e_t > s_t ? pre[e_t] - pre[s_t] : 0;
+        bool pad = false;
+        if (npad > 0) {   // padded row: another head took more cells into tile t
+            int mt = 0;
+            for (int i = tid; i < a.H; i += 1024) {
+                const int ni = a.n_tiles[i];
+                if (t < ni) {
+                    const int32_t* ei = a.tile_end + static_cast<int64_t>(i) * sc;
+                    mt = max(mt, ei[t] - (t > 0 ? ei[t - 1] : 0));
+                }
+            }
+            mt = tile_block_max(mt, sh);
+            pad = e_t - s_t < mt;
+        }
+        const bool match = my_t == t || (padc && pad);
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(match);
+        if (lane_id() == 0) sh[wave] = __builtin_popcountll(bal);
+        __syncthreads();
+        int before = 0, cnt = 0;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) {
+            cnt += sh[w];
+            before += w < wave ? sh[w] : 0;
+        }
+        const int pos = before + __builtin_popcountll(bal & lanemask_lt());
+        const int app = min(cnt, max(a.exec_rows - rows_t, 0));
+        if (match && pos < app && base + pos < a.ring_cap)
+            a.delta_rows[static_cast<int64_t>(h) * a.ring_cap + base + pos] = rrow;
+        base += app;
+        __syncthreads();   // sh is reused
+        t = npad > 0 ? t + 1 : tile_block_min(my_t > t ? my_t : INT_MAX, sh);
+    }
+    if (tid == 0) a.n_delta[h] = min(base, a.ring_cap);
+}
+
 }  // namespace
 
 int select4_validate(const imi_select_args* a);
@@ -770,7 +974,6 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     if (a->ring_cap != 0) {
         IMI_REQUIRE(a->ring_cap > 0 && a->ring_cap <= kRingCap, IMI_ERR_UNSUPPORTED,
                     "imi_select: ring_cap %d outside [1, %d]", a->ring_cap, kRingCap);
-        IMI_REQUIRE(!a->tile_mode, IMI_ERR_UNSUPPORTED, "imi_select: the delta append is not available in tile mode");
         IMI_REQUIRE(a->ring_cell && a->ring_row && a->ring_n, IMI_ERR_INVALID, "imi_select: null delta ring");
         IMI_REQUIRE(a->exec_rows >= 0, IMI_ERR_INVALID, "imi_select: exec_rows must be >= 0");
     }
@@ -853,7 +1056,7 @@ int select_one_kernel(const imi_select_args* a, hipStream_t stream) {
     p.ring_cell = a->ring_cell;
     p.ring_row = a->ring_row;
     p.ring_n = a->ring_n;
-    p.ring_cap = a->ring_cap;
+    p.ring_cap = a->tile_mode ? 0 : a->ring_cap;   // tile mode: the tile launches append the delta
     p.exec_rows = a->exec_rows;
     p.delta_rows = a->delta_rows;
     p.n_delta = a->n_delta;
@@ -875,10 +1078,45 @@ int select_one_kernel(const imi_select_args* a, hipStream_t stream) {
 
 }  // namespace
 
-// Workspace of a 2-way selection: nothing for the one-kernel path, the
-// ranking pipeline's otherwise.
+// Scratch of the tile-mode delta append: the tile ends of every head and
+// their counts (tile mode with a delta ring only).
+size_t tile_delta_bytes(const imi_select_args* a) {
+    if (!(a->tile_mode && a->ring_cap > 0)) return 0;
+    return (static_cast<size_t>(a->kv_heads) * (a->sel_cap + 1)) * sizeof(int32_t) + 256;
+}
+
+int tile_delta_launch(const imi_select_args* a, void* scratch, hipStream_t stream) {
+    TileDeltaParams t{};
+    t.H = a->kv_heads;
+    t.sel_cap = a->sel_cap;
+    t.sel_cell = a->sel_cell;
+    t.sel_count = a->sel_count;
+    t.sel_prefix = a->sel_prefix;
+    t.n_sel = a->n_selected;
+    t.page_size = a->page_size;
+    t.buffer_pages = a->buffer_pages;
+    t.head_buffer_pages = a->head_buffer_pages;
+    t.ring_cell = a->ring_cell;
+    t.ring_row = a->ring_row;
+    t.ring_n = a->ring_n;
+    t.ring_cap = a->ring_cap;
+    t.exec_rows = a->exec_rows;
+    t.delta_rows = a->delta_rows;
+    t.n_delta = a->n_delta;
+    const uintptr_t p0 = (reinterpret_cast<uintptr_t>(scratch) + 255) & ~static_cast<uintptr_t>(255);
+    t.tile_end = reinterpret_cast<int32_t*>(p0);
+    t.n_tiles = t.tile_end + static_cast<size_t>(a->kv_heads) * a->sel_cap;
+    hipLaunchKernelGGL(tile_ends_kernel, dim3(a->kv_heads), dim3(1024), 0, stream, t);
+    IMI_LAUNCH_CHECK("tile_ends_kernel");
+    hipLaunchKernelGGL(tile_delta_kernel, dim3(a->kv_heads), dim3(1024), 0, stream, t);
+    IMI_LAUNCH_CHECK("tile_delta_kernel");
+    return IMI_OK;
+}
+
+// Workspace of a 2-way selection: for the one-kernel path only the tile-mode
+// delta scratch, the ranking pipeline's otherwise.
 size_t sel2_keys_bytes(const imi_select_args* a) {
-    if (sel2_one_kernel(a)) return 0;
+    if (sel2_one_kernel(a)) return tile_delta_bytes(a);
     return select4_workspace_size(a);
 }
 
@@ -891,7 +1129,14 @@ int select_launch(const imi_select_args* a, hipStream_t stream) {
                 IMI_ERR_INVALID, "imi_select: null output pointer");
     IMI_REQUIRE(a->ring_cap == 0 || (a->delta_rows && a->n_delta), IMI_ERR_INVALID,
                 "imi_select: null delta output pointer");
-    if (a->parts == 2 && sel2_one_kernel(a)) return select_one_kernel(a, stream);
+    if (a->parts == 2 && sel2_one_kernel(a)) {
+        if (a->tile_mode && a->ring_cap > 0)
+            IMI_REQUIRE(a->workspace && a->workspace_bytes >= tile_delta_bytes(a), IMI_ERR_WORKSPACE,
+                        "imi_select: workspace %zu bytes < %zu required", a->workspace_bytes, tile_delta_bytes(a));
+        rc = select_one_kernel(a, stream);
+        if (rc || !(a->tile_mode && a->ring_cap > 0)) return rc;
+        return tile_delta_launch(a, a->workspace, stream);
+    }
     return select4_launch(a, stream);
 }
 

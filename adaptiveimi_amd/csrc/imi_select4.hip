@@ -37,6 +37,10 @@
 #include "imi_common.hpp"
 
 namespace imi {
+
+size_t tile_delta_bytes(const imi_select_args* a);
+int tile_delta_launch(const imi_select_args* a, void* scratch, hipStream_t stream);
+
 namespace {
 
 constexpr int kBins4 = 2048;
@@ -73,6 +77,7 @@ __host__ __device__ __forceinline__ int64_t cand_pos(int64_t s, int j, int regio
 }
 
 struct Sel4 {
+    void* tile_scr;          // scratch of the tile-mode delta append (null: none)
     const uint16_t* q;
     const float* cent;       // [H][4][kmax][32]
     int H, G, kmax;
@@ -1509,7 +1514,10 @@ size_t sel4_workspace(const imi_select_args* a, Sel4* p) {
     uint32_t* rpart = cv.take<uint32_t>(H * static_cast<size_t>(nbs) * 2);
     uint64_t* cand = cv.take<uint64_t>(H * static_cast<size_t>(nbs) * region);
     int32_t* cidx = cv.take<int32_t>(H * static_cast<size_t>(nbs) * region);
+    const size_t tb = tile_delta_bytes(a);
+    char* tscr = tb > 0 ? cv.take<char>(tb) : nullptr;
     if (p) {
+        p->tile_scr = tscr;
         p->wcnt = wcnt;
         p->region = region;
         p->rpart = rpart;
@@ -1622,6 +1630,8 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     p.exec_rows = a->exec_rows;
     p.delta_rows = a->delta_rows;
     p.n_delta = a->n_delta;
+    const bool tile_delta = a->tile_mode && a->ring_cap > 0;
+    if (tile_delta) p.ring_cap = 0;   // the tile launches append the delta
     const bool online = p.upd_slot || p.ring_cap > 0;
     if (a->parts == 1) {
         if (p.upd_slot)
@@ -1690,6 +1700,7 @@ int select4_launch(const imi_select_args* a, hipStream_t stream) {
     else
         hipLaunchKernelGGL(sel4_final_kernel<false>, dim3(a->kv_heads), dim3(kFinalThreads), kFinalLds, stream, p);
     IMI_LAUNCH_CHECK("sel4_final_kernel");
+    if (tile_delta) return tile_delta_launch(a, p.tile_scr, stream);
     return IMI_OK;
 }
 

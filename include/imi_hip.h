@@ -209,8 +209,13 @@ typedef struct {
      * reference's `selected` (the cells that pass nprobe and the token
      * budget, before the page cut, plus the padding id when fewer than
      * nprobe pass) are appended after the selected rows, in ring index
-     * order, up to exec_rows - n_rows.  ring_cap 0 = off; not with
-     * tile_mode; sel_cap must then cover nprobe. */
+     * order, up to exec_rows - n_rows.  With tile_mode (retrieval.py:
+     * 480-509) the append follows the tiles: per tile, the entries of the
+     * tile's cells -- and the padding entries where the head's row of the
+     * tile is padded, i.e. it took fewer cells into the tile than the head
+     * that took most -- up to exec_rows minus the rows of the tile's cells;
+     * a padding entry can then repeat, and delta_rows keeps the first
+     * ring_cap rows.  ring_cap 0 = off; sel_cap must then cover nprobe. */
     const int32_t* ring_cell;       /* [H][ring_cap] match code (imi_update_args) */
     const int32_t* ring_row;        /* [H][ring_cap] steady row of each entry */
     const int32_t* ring_n;          /* [H] valid entries (ring index 0 ..) */
@@ -220,7 +225,8 @@ typedef struct {
     int32_t* n_delta;               /* out [H] */
 } imi_select_args;
 
-/* Workspace imi_select needs (0 for 2-way IMI). */
+/* Workspace imi_select needs (0 for 2-way IMI within the one-kernel
+ * selection, except tile mode with the delta append: its tile scratch). */
 int imi_select_workspace_size(const imi_select_args* a, size_t* bytes);
 int imi_select(const imi_select_args* a, imi_stream_t stream);
 

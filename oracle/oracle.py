@@ -422,6 +422,49 @@ def select_tiles(sc: np.ndarray, sizes: np.ndarray, mask: np.ndarray, nprobe: in
     return sel, m, tok
 
 
+def build_cluster_tiles(sel: np.ndarray, counts: np.ndarray, sizes: np.ndarray, buffer_pages: int, page_size: int,
+                        padding_id: int) -> List[np.ndarray]:
+    """_build_cluster_tiles (retrieval.py:30-112) over every head at once.
+    sel [H, nprobe]: cells in rank order, the first counts[h] of them
+    selected (the rest ignored); sizes [H, n]: cell sizes.  Each tile is an
+    [H, max_take] array: head h's next run of cells that fits buffer_pages
+    pages, padded with padding_id where the head took fewer than the head
+    that took most.  A head stops at a cell whose own pages exceed
+    buffer_pages (it can join no tile)."""
+    sel = np.asarray(sel, np.int64)
+    H, nprobe = sel.shape
+    counts = np.asarray(counts, np.int64)
+    pos = np.arange(nprobe)[None, :]
+    ids = np.where(pos < counts[:, None], sel, padding_id)
+    szs = np.zeros((H, nprobe), np.int64)
+    for h in range(H):
+        live = ids[h] != padding_id
+        szs[h, live] = sizes[h, ids[h, live]]
+    pages = np.where(szs > 0, np.maximum((szs + page_size - 1) // page_size, 1), 0)
+    prefix = np.cumsum(pages, axis=1)
+    offs = np.zeros(H, np.int64)
+    tiles = []
+    while np.any(offs < counts):
+        valid = offs < counts
+        start = np.where(offs > 0, prefix[np.arange(H), np.maximum(offs - 1, 0)], 0)
+        rel = prefix - start[:, None]
+        cand = (pos >= offs[:, None]) & (pos < counts[:, None]) & (rel <= buffer_pages)
+        take = cand.sum(axis=1)
+        force = valid & (take == 0)
+        cur_pages = pages[np.arange(H), np.minimum(offs, nprobe - 1)]
+        take = np.where(force & (cur_pages <= buffer_pages), 1, take)
+        take = np.minimum(take, counts - offs)
+        mt = int(take.max())
+        if mt <= 0:
+            break
+        tile = np.full((H, mt), padding_id, np.int64)
+        for h in range(H):
+            tile[h, : take[h]] = ids[h, offs[h]: offs[h] + take[h]]
+        tiles.append(tile)
+        offs = offs + take
+    return tiles
+
+
 def selected_rows(sel: np.ndarray, m: np.ndarray, offsets: np.ndarray) -> List[np.ndarray]:
     """CSR rows of the selected cells per head, in rank order."""
     out = []
@@ -625,10 +668,26 @@ class OnlineUpdateOracle:
         return out[: max(exec_rows - rows_sel, 0)]
 
 
+    def delta_rows_tiles(self, h: int, tiles: Sequence[np.ndarray], exec_rows: int, sizes_h: np.ndarray) -> List[int]:
+        """async_update.py:41-76 once per tile, as retrieval.py:480-509 calls
+        it: for each tile (build_cluster_tiles, padded with the padding id)
+        the ring entries (index order, the first n valid) whose cluster is in
+        head h's row of the tile -- the padding id included when that row is
+        padded -- at most exec_rows minus the rows of that row's cells.  An
+        entry can be appended once per tile it matches."""
+        out = []
+        for tile in tiles:
+            ids = set(int(c) for c in tile[h])
+            rows_t = int(sum(int(sizes_h[c]) for c in tile[h] if int(c) != self.padding_id))
+            got = [int(self.ring_row[h, p]) for p in range(int(self.n[h])) if int(self.ring_id[h, p]) in ids]
+            out += got[: max(exec_rows - rows_t, 0)]
+        return out
+
+
 def decode_step_online(q_bits: np.ndarray, sizes: np.ndarray, offsets: np.ndarray, mask: np.ndarray,
                        list_keys: np.ndarray, list_values: np.ndarray, steady_k: np.ndarray, steady_v: np.ndarray,
                        static_len: int, upd: OnlineUpdateOracle, nprobe: int, max_tokens: int, buffer_pages: int,
-                       exec_rows: int, page_size: int = 8):
+                       exec_rows: int, page_size: int = 8, tile_mode: bool = False):
     """sparse_attention with the async update on (retrieval.py:320-447 with
     async_update.py:7-76): scores over the current centroids (the shadow),
     selection, execution buffer [static rows | selected rows | delta rows]
@@ -637,11 +696,17 @@ def decode_step_online(q_bits: np.ndarray, sizes: np.ndarray, offsets: np.ndarra
     m, list rows per head, delta steady rows per head)."""
     H, G, D = q_bits.shape
     sc = scores(q_bits, upd.shadow)
-    sel, m, _ = select(sc, sizes, mask, nprobe, max_tokens, buffer_pages, page_size)
     big = np.iinfo(np.int32).max // 2
     sel_t, m_t, _ = select(sc, sizes, mask, nprobe, max_tokens, big, page_size)
-    rows = selected_rows(sel, m, offsets)
-    drows = [upd.delta_rows(h, sel_t[h, : m_t[h]], nprobe, exec_rows, len(rows[h])) for h in range(H)]
+    if tile_mode:   # retrieval.py:452-527: every tile, its delta rows, LSE-merged
+        sel, m, _ = select_tiles(sc, sizes, mask, nprobe, max_tokens, buffer_pages, page_size)
+        rows = selected_rows(sel, m, offsets)
+        tiles = build_cluster_tiles(sel_t, m_t, sizes, buffer_pages, page_size, upd.padding_id)
+        drows = [upd.delta_rows_tiles(h, tiles, exec_rows, sizes[h]) for h in range(H)]
+    else:
+        sel, m, _ = select(sc, sizes, mask, nprobe, max_tokens, buffer_pages, page_size)
+        rows = selected_rows(sel, m, offsets)
+        drows = [upd.delta_rows(h, sel_t[h, : m_t[h]], nprobe, exec_rows, len(rows[h])) for h in range(H)]
     width = max(static_len + len(rows[h]) + len(drows[h]) for h in range(H))
     ek = np.zeros((H, max(width, 1), D), np.uint16)
     ev = np.zeros_like(ek)

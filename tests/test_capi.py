@@ -158,21 +158,28 @@ def test_online_update_argument_checks(L):
     u.ring_cap, u.delta_sums = 512, None
     assert L.imi_update_refresh(ctypes.byref(u), None) == 1
     assert "null state" in L.imi_last_error().decode()
-    # selection: the delta append is not available in tile mode, needs the ring
-    # and must rank all of nprobe
+    # selection: the delta append needs the ring and must rank all of nprobe;
+    # in tile mode it needs the workspace of its tile scratch (the one-kernel
+    # selection needs none otherwise)
     s = SelectArgs(query=16, centroids=16, cell_count=16, cell_offset=16, kv_heads=8, groups=4, dim=128, parts=2,
                    nprobe=410, max_tokens=3276, buffer_pages=300, page_size=8, sel_cap=300, ring_cap=512,
                    tile_mode=1)
     s.k[0] = s.k[1] = 64
-    assert L.imi_select(ctypes.byref(s), None) == 3
-    assert "tile mode" in L.imi_last_error().decode()
-    s.tile_mode = 0
     assert L.imi_select(ctypes.byref(s), None) == 1
     assert "delta ring" in L.imi_last_error().decode()
     s.ring_cell = s.ring_row = s.ring_n = 16
     assert L.imi_select(ctypes.byref(s), None) == 1
     assert "sel_cap 300 < 410 (nprobe)" in L.imi_last_error().decode()
     s.sel_cap = 410
+    assert L.imi_select_workspace_size(ctypes.byref(s), ctypes.byref(need)) == 0 and need.value >= 8 * 411 * 4
+    s.sel_cell = s.sel_offset = s.sel_count = s.sel_prefix = s.n_selected = s.n_rows = 16
+    s.delta_rows = s.n_delta = 16
+    assert L.imi_select(ctypes.byref(s), None) == 4
+    assert "workspace" in L.imi_last_error().decode()
+    s.tile_mode = 0
+    assert L.imi_select_workspace_size(ctypes.byref(s), ctypes.byref(need)) == 0 and need.value == 0
+    s.sel_cell = s.sel_offset = s.sel_count = s.sel_prefix = s.n_selected = s.n_rows = None
+    s.delta_rows = s.n_delta = None
     s.upd_slot = 16
     assert L.imi_select(ctypes.byref(s), None) == 1
     assert "shadow" in L.imi_last_error().decode()

@@ -221,6 +221,73 @@ def test_select_with_replaced_centroids_and_delta(ops, oracle, ks, T):
     assert hit_replaced > 0, "no replaced centroid was selected: the test covers nothing"
 
 
+def _pad_ring(upd, orc, ncells, seed, per_head=6):
+    """Turn a few valid ring entries of every head into padding entries (the
+    padding id, match code -1), on the GPU state and its oracle twin."""
+    rng = np.random.default_rng(seed)
+    torch.cuda.synchronize()
+    rc = upd.ring_cell.cpu().numpy()
+    for h in range(rc.shape[0]):
+        n = int(orc.n[h])
+        for p in rng.choice(n, min(per_head, n), replace=False):
+            orc.ring_id[h, p] = ncells
+            rc[h, p] = -1
+    upd.ring_cell.copy_(torch.from_numpy(rc).to(DEV))
+
+
+@pytest.mark.parametrize("ks,T", [((32, 32), 6000), ((181, 181), 60000), ((8, 8, 8, 8), 6000), ((375,), 6000)])
+def test_select_tile_mode_with_delta(ops, oracle, ks, T):
+    """Tile mode with the delta append (retrieval.py:480-509): per tile, the
+    ring entries of the tile's cells and -- where the head's row of the tile
+    is padded -- the padding entries, each tile's list cut at the buffer rows
+    its cells leave; checked against the oracle's literal tile builder and
+    per-tile append, with page budgets that make several tiles."""
+    from adaptiveimi_amd import synthetic
+
+    note(f"[online] tile-mode delta ks={ks} T={T}")
+    H, B, G, cap = 8, 8, 4, 64
+    keys, _, cent, out, ncells = _built(ops, H, T, ks, 71)
+    upd, orc = _state(ops, oracle, out, ks, ncells, threshold=2, ring_cap=cap)
+    steady = _decode_keys(keys, H, 6 * B, seed=9)
+    sd = steady.to(DEV)
+    for b in range(6):
+        upd.assign(sd, b * B, B)
+        orc.assign(bits(steady[:, b * B:(b + 1) * B]), list(range(b * B, (b + 1) * B)))
+        upd.refresh(B)
+        orc.refresh()
+    _pad_ring(upd, orc, ncells, seed=3)
+    sizes = out["compact_size"].cpu().numpy()
+    mask = out["compact_mask"].cpu().numpy()
+    gid = out["compact_gid"].cpu().numpy()
+    sz = oracle.sizing(T, 0.1, subspace_parts=len(ks), k_override=ks)
+    compact = out if len(ks) == 4 else None
+    qs = [(steady[:, :G].float() * 2).to(torch.bfloat16), synthetic.make_queries(keys, G, seed=4)[0]]
+    big = np.iinfo(np.int32).max // 2
+    several = 0
+    for bp in (max(6, sz["buffer_pages"] // 6), sz["buffer_pages"]):
+        bud = ops.Budget(sz["nprobe"], sz["max_tokens"], bp, tile_mode=True)
+        for qi, q in enumerate(qs):
+            sc = oracle.scores(bits(q), orc.shadow)
+            rs, rm, rtok = oracle.select_tiles(sc, sizes, mask, bud.nprobe, bud.max_tokens, bp)
+            st, mt, _ = oracle.select(sc, sizes, mask, bud.nprobe, bud.max_tokens, big)
+            tiles = oracle.build_cluster_tiles(st, mt, sizes, bp, bud.page_size, ncells)
+            several += len(tiles) > 1
+            for er in (10 ** 6, bp * bud.page_size - 30, bp * bud.page_size // 2):
+                sel = ops.select(q.to(DEV), cent, out["cell_count"], out["cell_offset"], ks, bud, compact=compact,
+                                 update=upd, exec_rows=er)
+                m = sel["n_selected"].cpu().numpy()
+                assert np.array_equal(m, rm), (bp, qi, er)
+                got = sel["sel_cell"].cpu().numpy()
+                nd = sel["n_delta"].cpu().numpy()
+                drow = sel["delta_rows"].cpu().numpy()
+                assert np.array_equal(sel["n_rows"].cpu().numpy(), rtok)
+                for h in range(H):
+                    assert np.array_equal(got[h, : m[h]], gid[h][rs[h, : rm[h]]]), (bp, qi, h)
+                    want = orc.delta_rows_tiles(h, tiles, er, sizes[h])[:cap]
+                    assert list(drow[h, : nd[h]]) == want, (bp, qi, h, er)
+    assert several > 0, "no call made more than one tile"
+
+
 def test_select_many_replaced_centroids(ops, oracle):
     """More than 64 replaced centroids in a head (the selection then scores
     them in several passes of 64): threshold 1 and batches of 64 keys drawn
@@ -259,8 +326,9 @@ def test_select_many_replaced_centroids(ops, oracle):
         assert np.array_equal(sel["n_rows"].cpu().numpy(), rtok)
 
 
-def test_decode_step_online_matches_oracle(ops, oracle):
-    note("[online] decode step")
+@pytest.mark.parametrize("tile", [False, True])
+def test_decode_step_online_matches_oracle(ops, oracle, tile):
+    note(f"[online] decode step tile={tile}")
     H, T, B, G, ks = 8, 9000, 8, 4, (32, 32)
     keys, values, cent, out, ncells = _built(ops, H, T, ks, 81)
     upd, orc = _state(ops, oracle, out, ks, ncells, threshold=2, ring_cap=48)
@@ -276,8 +344,11 @@ def test_decode_step_online_matches_oracle(ops, oracle):
         orc.assign(bits(sk[:, r0:r0 + B]), list(range(r0, r0 + B)))
         upd.refresh(B)
         orc.refresh()
+    if tile:
+        _pad_ring(upd, orc, ncells, seed=4, per_head=3)
     sz = oracle.sizing(T, 0.1, k_override=ks)
-    bud = ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"])
+    bp = sz["buffer_pages"] // 5 if tile else sz["buffer_pages"]   # tile mode: several tiles
+    bud = ops.Budget(sz["nprobe"], sz["max_tokens"], bp, tile_mode=tile)
     plan = ops.DecodePlan(cent, out["cell_count"], out["cell_offset"], ks, bud, out["list_keys"],
                           out["list_values"], skd, svd, G, update=upd)
     exec_rows = bud.buffer_pages * bud.page_size + 64
@@ -291,10 +362,11 @@ def test_decode_step_online_matches_oracle(ops, oracle):
     ref, rs, rm, rows, dr = oracle.decode_step_online(bits(q), sizes, offs, out["compact_mask"].cpu().numpy(),
                                                       bits(out["list_keys"]), bits(out["list_values"]), bits(sk),
                                                       bits(sv), static_len, orc, bud.nprobe, bud.max_tokens,
-                                                      bud.buffer_pages, exec_rows)
+                                                      bud.buffer_pages, exec_rows, tile_mode=tile)
     sel = plan.selection
     assert np.array_equal(sel["n_selected"].cpu().numpy(), rm)
     nd = sel["n_delta"].cpu().numpy()
+    assert max(len(d) for d in dr) <= upd.ring_cap, "the oracle's list would be cut: the case checks less"
     assert [int(x) for x in nd] == [len(d) for d in dr]
     assert sum(len(d) for d in dr) > 0, "no delta row was appended"
     got = res.float().cpu().numpy().reshape(H, G, 128)
@@ -302,13 +374,17 @@ def test_decode_step_online_matches_oracle(ops, oracle):
     assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)), float(err.max())
 
 
-@pytest.mark.parametrize("ks,steps,batch,thr,ring,host", [
-    ((32, 32), 14, 4, 2, 24, False), ((6, 6, 6, 6), 14, 4, 2, 24, False), ((8, 8, 8, 8), 14, 4, 2, 24, False),
-    ((32, 32), 50, 16, 3, 40, False), ((256,), 14, 4, 2, 24, False),   # (256,): IVF
+@pytest.mark.parametrize("ks,steps,batch,thr,ring,host,tiles", [
+    ((32, 32), 14, 4, 2, 24, False, False), ((6, 6, 6, 6), 14, 4, 2, 24, False, False),
+    ((8, 8, 8, 8), 14, 4, 2, 24, False, False),
+    ((32, 32), 50, 16, 3, 40, False, False), ((256,), 14, 4, 2, 24, False, False),   # (256,): IVF
     # the host tier (lists in pinned host memory, GPU block cache) with the update
     # on: the reference's shipped 1M configuration is a 4-way index with async_update
-    ((8, 8, 8, 8), 14, 4, 2, 24, True), ((32, 32), 50, 16, 3, 40, True)])
-def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, thr, ring, host):
+    ((8, 8, 8, 8), 14, 4, 2, 24, True, False), ((32, 32), 50, 16, 3, 40, True, False),
+    # tile mode (IMI_MAX_TILES != 0) with the per-tile delta append
+    ((32, 32), 14, 4, 2, 24, False, True), ((8, 8, 8, 8), 14, 4, 2, 24, False, True)])
+def test_cache_with_async_update_matches_oracle(ops, oracle, monkeypatch, ks, steps, batch, thr, ring, host,
+                                                tiles):
     """The drop-in with async_update on, driven like model_hub drives it,
     against a step-by-step oracle replay (update applied at the next step);
     the 50-step cases use the reference's batch of 16 keys over three batches
@@ -321,6 +397,7 @@ def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, t
     note(f"[online] drop-in ks={ks} {steps} decode steps host_tier={host}")
     kcfg = {f"k{i + 1}": k for i, k in enumerate(ks)}
     kcfg.update(max_iters=3, early_stop_min_iter=3, init="first")
+    monkeypatch.setenv("IMI_MAX_TILES", "4" if tiles else "0")
     cache = adpimi_cache(valid_start=[0], layer_num=L, batch_size=1, max_length=S + steps + 1,
                          num_key_value_heads=H, num_heads=H * G, head_dim=D, dtype=torch.bfloat16,
                          layer_mapping={"0": DEV, "1": DEV}, max_new_length=steps + 1, input_length=S,
@@ -386,7 +463,8 @@ def test_cache_with_async_update_matches_oracle(ops, oracle, ks, steps, batch, t
             ref, _, rm, rrows, dr = oracle.decode_step_online(
                 bits(q), tw["sizes"], tw["offs"], tw["mask"], tw["lk"],
                 tw["lv"], bits(cache.steady_zone_keys[layer][0]), bits(cache.steady_zone_values[layer][0]),
-                static_len, tw["orc"], cache.nprobe, cache.max_retrieval_tokens, cache.buffer_size, exec_rows)
+                static_len, tw["orc"], cache.nprobe, cache.max_retrieval_tokens, cache.buffer_size, exec_rows,
+                tile_mode=tiles)
             plan = cache._plans[layer]
             if host:   # the buffer's one-cell selection replaced the ranked one in the workspace
                 assert isinstance(plan, ops.HostTierPlan)

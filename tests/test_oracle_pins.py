@@ -440,6 +440,70 @@ def test_select_tiles_matches_literal_tiles(oracle, seed):
             assert sum((int(sizes[b, c]) + page - 1) // page for c in cells) <= buffer_pages
 
 
+def _tile_delta_literal(tiles, ring_ids, ring_rows, ring_n, cluster_sizes, pad, exec_rows):
+    """retrieval.py:480-509 with _append_delta_to_execution (async_update.py:
+    41-76) in torch ops: per tile, valid_lengths = the rows of the tile's
+    cells, then the matching valid ring entries up to the buffer's end."""
+    B, cap = ring_ids.shape
+    out = [[] for _ in range(B)]
+    positions = torch.arange(cap).unsqueeze(0)
+    valid_mask = positions < ring_n.unsqueeze(1)
+    for tile in tiles:
+        sizes = torch.gather(cluster_sizes.to(torch.int64), 1, tile.clamp_max(pad))
+        valid_lengths = torch.where(tile == pad, 0, sizes).sum(dim=1)
+        match = (ring_ids.unsqueeze(-1) == tile.unsqueeze(1)).any(dim=-1) & valid_mask
+        for b in range(B):
+            if not torch.any(match[b]):
+                continue
+            rows = ring_rows[b, match[b]]
+            start = int(valid_lengths[b].item())
+            if start >= exec_rows:
+                continue
+            out[b] += rows[: exec_rows - start].tolist()
+    return out
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_tile_delta_matches_literal(oracle, seed):
+    """The oracle's tile builder and per-tile delta append against the
+    reference's loops in torch ops, with ring entries on tiled cells, on
+    unselected cells and on the padding id (which matches every tile where
+    a head took fewer cells than another)."""
+    rng = np.random.default_rng(700 + seed)
+    B, N, page = 4, 300, 8
+    sizes = rng.integers(1, 60, (B, N)).astype(np.int32)
+    mask = np.zeros((B, N), bool)
+    buffer_pages = int(rng.integers(3, 12))
+    big = rng.random((B, N)) < 0.03
+    sizes[big] = rng.integers(page * buffer_pages + 1, page * buffer_pages + 90, int(big.sum()))
+    sc = rng.standard_normal((B, N)).astype(np.float32)
+    nprobe = int(rng.integers(20, 120))
+    max_tokens = int(rng.integers(200, 3000))
+    sims = torch.from_numpy(sc)
+    cs = torch.from_numpy(np.concatenate([sizes, np.zeros((B, 1), np.int32)], 1))
+    tiles_lit = _tiles_literal(sims, cs, N, nprobe, max_tokens, buffer_pages, page)
+    bigp = np.iinfo(np.int32).max // 2
+    sel_t, m_t, _ = oracle.select(sc, sizes, mask, nprobe, max_tokens, bigp, page)
+    tiles = oracle.build_cluster_tiles(sel_t, m_t, sizes, buffer_pages, page, N)
+    assert len(tiles) == len(tiles_lit)
+    for t, tl in zip(tiles, tiles_lit):
+        assert np.array_equal(t, tl.numpy())
+    cap = 48
+    upd = oracle.OnlineUpdateOracle(np.zeros((B, N + 1, 4), np.float32), np.zeros((B, N + 1), np.int64), N, 2, cap)
+    for b in range(B):
+        pool = [int(c) for c in sel_t[b, : m_t[b]]] or [0]
+        for p in range(cap):
+            u = rng.random()
+            upd.ring_id[b, p] = pool[rng.integers(len(pool))] if u < 0.5 else (N if u < 0.7 else rng.integers(N))
+            upd.ring_row[b, p] = 1000 * b + p
+        upd.n[b] = rng.integers(0, cap + 1)
+    for exec_rows in (10 ** 6, 4 * buffer_pages, 8 * buffer_pages + 5):   # the last two truncate
+        lit = _tile_delta_literal(tiles_lit, torch.from_numpy(upd.ring_id), torch.from_numpy(upd.ring_row),
+                                  torch.from_numpy(upd.n), cs, N, exec_rows)
+        for b in range(B):
+            assert upd.delta_rows_tiles(b, tiles, exec_rows, sizes[b]) == lit[b], (b, exec_rows)
+
+
 # ------------------------------------------------------ CPU baseline step ----
 
 def test_cpu_baseline_step_matches_oracle_decode(oracle):
