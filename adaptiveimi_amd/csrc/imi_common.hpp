@@ -111,6 +111,12 @@ inline int device_cus() {
     return cached[dev];
 }
 
+// Centroids per subspace of a 2-way or 4-way IMI: the k-means E-step holds
+// k x 64 fp32 rows in LDS (132 KB at 512), the 2-way ranking pipeline scores
+// k * k <= 1024 x 256 cells per head.  512 covers the reference's adaptive k
+// (layer_pipeline.cpp:177-228) up to 4M tokens.
+constexpr int kImiMaxK = 512;
+
 // ------------------------------------------------- LDS set of cell ids --
 // Open-addressing set of non-negative ints in a kSetSize-int LDS table
 // (empty = -1), filled at most half: inserts and lookups always end.

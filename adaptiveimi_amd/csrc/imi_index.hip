@@ -341,7 +341,7 @@ int validate(const imi_index_args* a, int& kmax, int64_t& ncells) {
                 "imi_build_index: strides must be multiples of 8 elements");
     kmax = 0;
     ncells = 1;
-    const int kcap = a->parts == 1 ? kIvfMaxK : 256;
+    const int kcap = a->parts == 1 ? kIvfMaxK : kImiMaxK;
     for (int p = 0; p < a->parts; ++p) {
         IMI_REQUIRE(a->k[p] >= 1 && a->k[p] <= kcap, IMI_ERR_UNSUPPORTED, "imi_build_index: k[%d]=%d outside [1,%d]",
                     p, a->k[p], kcap);

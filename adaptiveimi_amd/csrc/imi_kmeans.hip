@@ -1476,7 +1476,7 @@ int validate(const imi_kmeans_args* a, int& kmax, int& dp) {
     IMI_REQUIRE(dp == 32 || dp == 64 || (a->parts == 1 && dp == 128), IMI_ERR_UNSUPPORTED,
                 "imi_kmeans: subspace width %d unsupported (32 or 64; 128 for IVF)", dp);
     IMI_REQUIRE(a->max_iters >= 1, IMI_ERR_INVALID, "imi_kmeans: max_iters must be >= 1");
-    const int kcap = a->parts == 1 ? kIvfMaxK : 256;
+    const int kcap = a->parts == 1 ? kIvfMaxK : kImiMaxK;
     kmax = 0;
     for (int p = 0; p < a->parts; ++p) {
         IMI_REQUIRE(a->k[p] >= 1 && a->k[p] <= kcap, IMI_ERR_UNSUPPORTED, "imi_kmeans: k[%d]=%d outside [1,%d]", p,

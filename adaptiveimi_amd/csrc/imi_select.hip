@@ -994,7 +994,8 @@ int select_validate(const imi_select_args* a, int64_t& ncells, int& kmax) {
     IMI_REQUIRE(a->page_size > 0 && a->nprobe > 0 && a->max_tokens > 0 && a->buffer_pages > 0, IMI_ERR_INVALID,
                 "imi_select: budgets must be positive");
     kmax = a->k[0] > a->k[1] ? a->k[0] : a->k[1];
-    IMI_REQUIRE(a->k[0] >= 1 && a->k[1] >= 1 && kmax <= 256, IMI_ERR_UNSUPPORTED, "imi_select: k outside [1,256]");
+    IMI_REQUIRE(a->k[0] >= 1 && a->k[1] >= 1 && kmax <= kImiMaxK, IMI_ERR_UNSUPPORTED, "imi_select: k outside [1,%d]",
+                kImiMaxK);
     ncells = static_cast<int64_t>(a->k[0]) * a->k[1];
     if (!sel2_one_kernel(a)) return select4_validate(a);
     const bool rank_all = a->tile_mode || a->ring_cap > 0;

@@ -62,7 +62,7 @@ constexpr int kCellsPerBlock = kScore4Threads * kCPT;
 constexpr int kFastCand = 2048;  // screened pass: candidates a score workgroup scores exactly
 constexpr size_t kFastLds = static_cast<size_t>(kFastCand) * 12 + 2 * kK4 * 4;   // their (x0, gid, cell), d3 and A
 constexpr int kDenseScoreCells = kScoreThreads;   // 2-way score kernel: one global cell per thread
-constexpr int kDenseK = 256;                      // 2-way centroids per subspace the score kernel reads
+constexpr int kDenseK = kImiMaxK;                 // 2-way centroids per subspace (k0 * k1 <= kMaxSeg * 256 cells)
 constexpr int kIvfMaxK = 4096;                    // IVF clusters per head
 constexpr int kLocBins = 1024;   // buckets of a score workgroup's own candidate cut
 constexpr int kFinalCPT = 16;    // candidates per thread the final kernel holds in registers

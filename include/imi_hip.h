@@ -68,7 +68,7 @@ typedef struct {
     int32_t dim;              /* D (128) */
     int32_t parts;            /* P: 2 or 4 (IMI subspaces), or 1 (IVF: one
                                  128-dim space, kmeans_core.cpp:503-595) */
-    int32_t k[4];             /* centroids per subspace, each in [1, 256]
+    int32_t k[4];             /* centroids per subspace, each in [1, 512]
                                  (IVF: [1, 4096]) */
     int32_t max_iters;        /* >= 1 */
     float tol;                /* absolute inertia tolerance */

@@ -54,7 +54,7 @@ def _kmeans_args(**over):
 @pytest.mark.parametrize("over,code,text", [
     (dict(parts=3), 3, "parts"),
     (dict(k=(0, 64)), 3, "k[0]"),
-    (dict(k=(300, 64)), 3, "k[0]"),
+    (dict(k=(513, 64)), 3, "k[0]"),
     (dict(n_tokens=0), 1, "empty"),
     (dict(n_tokens=32), 1, "first-k"),
     (dict(max_iters=0), 1, "max_iters"),
@@ -234,8 +234,10 @@ def test_check_decode_limits_rejects_before_any_build(L):
     ops.check_decode_limits(8, 4, (181, 90), ops.Budget(1638, 52000, 1638))      # 2-way k above 128
     ops.check_decode_limits(8, 4, (32, 32, 32, 32), ops.Budget(16390, 4096, 512))
     ops.check_decode_limits(8, 4, (256, 256), ops.Budget(6554, 100000, 6554))  # 2-way at 1M
+    ops.check_decode_limits(8, 4, (362, 362), ops.Budget(2621, 41943, 5243))   # 2-way at 2M, budget 0.02
+    ops.check_decode_limits(8, 4, (512, 512), ops.Budget(5243, 83886, 10486))  # 2-way at 4M, budget 0.02
     ops.check_decode_limits(8, 4, (16, 16, 16, 16), ops.Budget(6554, 100000, 2000), online=True)   # 4-way 1M, async
     with pytest.raises(IMIError, match="rank"):
         ops.check_decode_limits(8, 4, (128, 128), ops.Budget(9000, 90000, 9000))  # K' above the ranking capacity
     with pytest.raises(IMIError, match="k"):
-        ops.check_decode_limits(8, 4, (512, 64), ops.Budget(410, 13097, 1638))    # 2-way k above 256
+        ops.check_decode_limits(8, 4, (513, 64), ops.Budget(410, 13097, 1638))    # 2-way k above 512

@@ -44,7 +44,8 @@ def _kv(H, T, seed=0, integer=False):
 
 @pytest.mark.parametrize("T,k,parts,integer", [(3000, 64, 2, False), (1000, 16, 2, True), (2049, 32, 4, False),
                                                 (777, 7, 2, False),
-                                                (1000, 128, 2, False), (1500, 128, 2, True)])   # configs[4]: k = 128
+                                                (1000, 128, 2, False), (1500, 128, 2, True),    # configs[4]: k = 128
+                                                (3000, 362, 2, False), (2000, 512, 2, True)])   # 2M / 4M adaptive k
 def test_assign_bit_exact(ops, oracle, T, k, parts, integer):
     note(f"[assign] T={T} k={k} parts={parts} integer={integer}")
     H = 4
@@ -70,7 +71,8 @@ def test_assign_bit_exact(ops, oracle, T, k, parts, integer):
     assert none is None and np.array_equal(lab2.cpu().numpy(), labels)
 
 
-@pytest.mark.parametrize("T,k,iters", [(4096, 64, 10), (2500, 32, 6), (300, 64, 4)])
+@pytest.mark.parametrize("T,k,iters", [(4096, 64, 10), (2500, 32, 6), (300, 64, 4),
+                                       (6000, 362, 3)])   # the 2-way adaptive k at 2M tokens
 def test_kmeans_full_run_bit_exact(ops, oracle, T, k, iters):
     """First-k init, no early stop: labels AND centroids equal the oracle's
     Lloyd run with threads_per_phase = 1 (kmeans_core.cpp:190-314)."""
@@ -273,7 +275,7 @@ def test_mstep_reciprocal_over_cluster_sizes(ops, oracle):
 
 # ---------------------------------------------------------- cell index ----
 
-@pytest.mark.parametrize("T,ks", [(5000, (32, 32)), (4096, (64, 64)), (3001, (8, 4, 8, 4))])
+@pytest.mark.parametrize("T,ks", [(5000, (32, 32)), (4096, (64, 64)), (3001, (8, 4, 8, 4)), (20000, (512, 300))])
 def test_build_index_bit_exact(ops, oracle, T, ks):
     note(f"[index] T={T} ks={ks}")
     H = 4
@@ -371,6 +373,8 @@ def test_similarities_bit_exact(ops, oracle):
     (120000, (181, 181), 0.1, 4, 10),    # the 2-way adaptive k at 512k: 32761 cells
     (200000, (256, 256), 0.06, 4, 11),   # ... and at 1M: 65536 cells, K' = 1500 pages
     (150000, (128, 128), 0.45, 4, 12),   # K' = 7373 nprobe < 8438 pages: near the ranking capacity
+    (300000, (362, 362), 0.02, 4, 13),   # the 2-way adaptive k at 2M tokens: 131044 cells
+    (300000, (512, 512), 0.02, 4, 14),   # ... and at 4M: 262144 cells, the k cap
 ])
 def test_select_bit_exact(ops, oracle, T, ks, budget, G, seed):
     note(f"[select] T={T} ks={ks} budget={budget} G={G}")

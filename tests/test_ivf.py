@@ -73,8 +73,10 @@ def test_ivf_library_limits(L):
     big.n_tokens = 5000
     assert L.imi_kmeans_workspace_size(ctypes.byref(big), ctypes.byref(need)) != 0
     assert "4096" in L.imi_last_error().decode()
-    # subspaces of 2 / 4 keep their 256 limit
-    assert L.imi_kmeans_workspace_size(ctypes.byref(_kargs(2, 300)), ctypes.byref(need)) != 0
+    # subspaces of 2 / 4 keep their 512 limit
+    assert L.imi_kmeans_workspace_size(ctypes.byref(_kargs(2, 512)), ctypes.byref(need)) == 0
+    assert L.imi_kmeans_workspace_size(ctypes.byref(_kargs(2, 513)), ctypes.byref(need)) != 0
+    assert "512" in L.imi_last_error().decode()
     # selection: IVF through the ranking pipeline, with or without the online update
     a = _lib.SelectArgs(query=16, centroids=16, cell_count=16, cell_offset=16, kv_heads=2, groups=4, dim=128,
                         parts=1, nprobe=10, max_tokens=100, buffer_pages=20, page_size=8, tile_mode=0)
