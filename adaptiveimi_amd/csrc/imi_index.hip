@@ -290,9 +290,13 @@ __global__ __launch_bounds__(256) void ix_compact_pad_kernel(IxParams a, Compact
 
 // list[h][pos] = src[h][perm[h][pos]] for keys and values; 16 lanes per
 // 256-byte row, 16 rows per wave with every load issued before any store.
-// (32 rows per wave, twice the loads in flight, ran at 3.1 TB/s even on the
-// identity permutation; 16 rows copy at the plain device copy's 5.4 TB/s.)
+// Loads and stores are non-temporal (each byte is touched once) and the
+// loads unconditional (rows past T re-read token 0 and are not stored): 1.07
+// GB per layer at configs[1] in ~150 us, against ~237 us with cached,
+// predicated loads and stores.  (32 rows per wave, twice the loads in
+// flight, ran at 3.1 TB/s even on the identity permutation.)
 constexpr int kPermRowsPerWave = 16;
+typedef unsigned int ix_u32x4_t __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256) void ix_permute_kernel(const uint16_t* keys, const uint16_t* values, int64_t hs,
                                                          int64_t ts, int T, const int32_t* perm, uint16_t* lk,
@@ -304,24 +308,21 @@ __global__ __launch_bounds__(256) void ix_permute_kernel(const uint16_t* keys, c
     const int my = base + lane;
     const int tok = (lane < kPermRowsPerWave && my < T) ? perm[static_cast<int64_t>(h) * T + my] : 0;
     constexpr int IT = kPermRowsPerWave / 4;
-    uint4 kv[IT], vv[IT];
+    ix_u32x4_t kv[IT], vv[IT];
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
-        const int j = it * 4 + rg;
-        const int t = __shfl(tok, j);
-        if (base + j < T) {
-            const int64_t so = h * hs + static_cast<int64_t>(t) * ts + li * 8;
-            kv[it] = *reinterpret_cast<const uint4*>(keys + so);
-            vv[it] = *reinterpret_cast<const uint4*>(values + so);
-        }
+        const int t = __shfl(tok, it * 4 + rg);
+        const int64_t so = h * hs + static_cast<int64_t>(t) * ts + li * 8;
+        kv[it] = __builtin_nontemporal_load(reinterpret_cast<const ix_u32x4_t*>(keys + so));
+        vv[it] = __builtin_nontemporal_load(reinterpret_cast<const ix_u32x4_t*>(values + so));
     }
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
         const int pos = base + it * 4 + rg;
         if (pos < T) {
             const int64_t dofs = (static_cast<int64_t>(h) * list_rows + pos) * 128 + li * 8;
-            *reinterpret_cast<uint4*>(lk + dofs) = kv[it];
-            *reinterpret_cast<uint4*>(lv + dofs) = vv[it];
+            __builtin_nontemporal_store(kv[it], reinterpret_cast<ix_u32x4_t*>(lk + dofs));
+            __builtin_nontemporal_store(vv[it], reinterpret_cast<ix_u32x4_t*>(lv + dofs));
         }
     }
 }
