@@ -1204,7 +1204,11 @@ __global__ __launch_bounds__(256) void km_update_block_kernel(KmParams a, Draws 
     constexpr int RPL = 64 / PARTS;  // rows per load instruction
     constexpr int LPB = PARTS;       // load instructions per 64-row batch
     constexpr int NL = 3;            // loader waves
-    constexpr int NB = DP > 64 ? 2 : 4;   // local batches in flight per loader (register ring)
+    // local batches in flight per loader (register ring).  Two: every
+    // workgroup fills its ring at the start, and with four the burst (~75 MB
+    // at configs[1]) delayed the first rounds of the largest clusters, whose
+    // chains set the kernel's length (79.9 -> 71.4 us per M-step).
+    constexpr int NB = 2;
     constexpr int HALVES = DP > 64 ? DP / 64 : 1;   // dims per chain lane
     __shared__ km_u32x4_t ring[2 * NL][64 * PARTS];
     // block member lists: the label's exclusive prefix over the blocks, its

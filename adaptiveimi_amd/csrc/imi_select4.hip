@@ -1119,11 +1119,30 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
     // batches.
     __shared__ int seg0[kMaxSeg + 1];
     const int64_t hb = static_cast<int64_t>(h) * a.nbs;
-    const int cw = tid < a.nbs ? min(max(a.wcnt[hb + tid], 0), a.region) : 0;
+    int cw = tid < a.nbs ? min(max(a.wcnt[hb + tid], 0), a.region) : 0;
     uint32_t m1 = 0, m2 = 0;
     if (tid < a.nbs) {
         m1 = a.rpart[(hb + tid) * 2 + 0];
         m2 = a.rpart[(hb + tid) * 2 + 1];
+    }
+    // A score workgroup that listed at least kp candidates holds kp cells at
+    // or above its lowest candidate, so the head's kp-th best key is at or
+    // above the highest such lowest score, lb (order-key bits): a candidate
+    // below lb cannot rank, and a workgroup whose best cell is below lb is
+    // skipped whole.  The range of the candidates left starts at lb.
+    uint32_t lb = (kp > 0 && cw >= kp) ? ~m2 : 0u;
+    lb = wave_max_u32(lb);
+    if (lane_id() == 0) shk[tid >> 6] = static_cast<int>(lb);
+    __syncthreads();
+    lb = 0u;
+#pragma unroll
+    for (int w = 0; w < kFinalThreads / 64; ++w) lb = max(lb, static_cast<uint32_t>(shk[w]));
+    if (m1 < lb) {
+        cw = 0;
+        m1 = 0u;
+        m2 = 0u;
+    } else {
+        m2 = min(m2, ~lb);
     }
     {
         const int incl = wave_incl_scan(cw);
@@ -1167,6 +1186,9 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
             cc[u] = cidxl[at];
         }
     }
+#pragma unroll
+    for (int u = 0; u < kFinalCPT; ++u)
+        if (static_cast<uint32_t>(ck[u] >> 32) < lb) ck[u] = 0ull;
     m1 = wave_max_u32(m1);
     m2 = wave_max_u32(m2);
     int* hist = ord;             // [kBins4] bucket counts
@@ -1210,7 +1232,7 @@ __global__ __launch_bounds__(kFinalThreads) void sel4_final_kernel(Sel4 a) {
             }
 #pragma unroll
             for (int u = 0; u < kBatch; ++u)
-                if (bk[u] != 0ull) fn(bk[u], bc[u]);
+                if (bk[u] != 0ull && static_cast<uint32_t>(bk[u] >> 32) >= lb) fn(bk[u], bc[u]);
         }
     };
     // histogram of the candidates over kBins4 linear buckets of their range
