@@ -413,7 +413,7 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
 #pragma unroll
     for (int ct = 0; ct < (CCREG ? NCT : 1); ++ct)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ccv[ct][r] = ct < nct ? ccs[ct * 16 + 4 * (lane >> 4) + r] : INFINITY;
+        for (int r = 0; r < 4; ++r) ccv[ct][r] = ct < nct ? -0.5f * ccs[ct * 16 + 4 * (lane >> 4) + r] : -INFINITY;
 
     const uint16_t* kb = a.keys + h * a.hs + p * DP;
     // 256-token blocks blockIdx.x * chunks .. +chunks-1 (the prologue above is
@@ -448,7 +448,10 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
             xr[i] = *reinterpret_cast<const km_u32x4_t*>(kb + static_cast<int64_t>(tc) * a.ts + 8 * i);
     }
     // screening: token tile j = tokens 16j .. 16j+15 of this wave's 64.
-    // e(c) = |c|^2 - 2 x.c orders the centroids like D~ = |x|^2 + e(c).
+    // f(c) = x.c - |c|^2 / 2 = -e(c) / 2 with e(c) = |c|^2 - 2 x.c, which
+    // orders the centroids like D~ = |x|^2 + e(c) (largest f first): the
+    // matrix cores start each tile's accumulator at -|c|^2 / 2 (halving is
+    // exact but for subnormals, which the absolute term of the bound covers).
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const km_u32x4_t* bq = bqa[j];
@@ -466,11 +469,14 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
             xs = __shfl(own, 16 * (tl >> 2) + tl);
         }
         float ev[NCT][4];
-        float emin = INFINITY;
+        float emax = -INFINITY;
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) {
             if (KT > 0 || ct < nct) {
-                km_f32x4_t acc = km_f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                km_f32x4_t acc;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[r] = CCREG ? ccv[CCREG ? ct : 0][r] : -0.5f * ccs[ct * 16 + 4 * (lane >> 4) + r];
 #pragma unroll
                 for (int kh = 0; kh < KH; ++kh) {
                     const km_u32x4_t ah = apk[((ct * KH + kh) * 2 + 0) * 64 + lane];
@@ -482,30 +488,29 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
                 }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float cc = CCREG ? ccv[CCREG ? ct : 0][r] : ccs[ct * 16 + 4 * (lane >> 4) + r];
-                    const float v = __builtin_fmaf(-2.0f, acc[r], cc);
-                    ev[ct][r] = v;
-                    emin = fminf(emin, v);
+                    ev[ct][r] = acc[r];
+                    emax = fmaxf(emax, acc[r]);
                 }
             } else {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) ev[ct][r] = INFINITY;
+                for (int r = 0; r < 4; ++r) ev[ct][r] = -INFINITY;
             }
         }
-        emin = fminf(emin, xor16(emin));
-        emin = fminf(emin, xor32(emin));
-        // candidates: e(c) <= min e + 2E; non-finite or huge magnitudes make
-        // every finite e a candidate (the exhaustive E-step)
+        emax = fmaxf(emax, xor16(emax));
+        emax = fmaxf(emax, xor32(emax));
+        // candidates: e(c) <= min e + 2E, i.e. f(c) >= max f - E; non-finite
+        // or huge magnitudes make every finite f a candidate (the exhaustive
+        // E-step)
         const float mag = xs + ccmax;
-        const float lim0 = emin + 2.0f * (0x1p-12f * mag + 1e-30f);
-        const bool all = !(mag <= 1e37f) || !(lim0 < INFINITY);
-        const float lim = all ? 3.402823466e38f : lim0;
+        const float lim0 = emax - (0x1p-12f * mag + 1e-30f);
+        const bool all = !(mag <= 1e37f) || !(lim0 > -INFINITY);
+        const float lim = all ? -3.402823466e38f : lim0;
         uint32_t m[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) {
             uint32_t nib = 0u;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) nib |= ev[ct][r] <= lim ? (1u << r) : 0u;
+            for (int r = 0; r < 4; ++r) nib |= ev[ct][r] >= lim ? (1u << r) : 0u;
             m[ct >> 1] |= nib << ((ct & 1) * 16 + 4 * (lane >> 4));
         }
 #pragma unroll
