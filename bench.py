@@ -8,7 +8,9 @@ budget 0.1.  One step = the retrieval + gather + attention of every layer for
 one decode token; the metric is decode steps/s per layer.
 
 Prints ONE JSON line (rank 0).  Index-build time, per-kernel durations,
-roofline and the CPU baseline are fields of the same line.
+roofline and the CPU baseline are fields of the same line, and so are the
+legs on other shapes: online index maintenance, the host tier, a configs[3]
+and a configs[4] slice (two layers each) and the end-to-end model run.
 
 `--workload config3` / `config4` run the same measurement on the other
 single-GPU configurations of BASELINE.json (their parity cases are in the
@@ -84,6 +86,10 @@ def parse():
     p.add_argument("--config3-layers", type=int, default=2,
                    help="layers of the configs[3] leg (4-way 32^4 IMI, 2 x 8 KV heads at 262,144 tokens, GQA 8, "
                         "fixed 4,096-token budget): step and selection per layer; 0 skips it")
+    p.add_argument("--config4-layers", type=int, default=2,
+                   help="layers of the configs[4] leg (2 x 128 IMI at 1,048,576 tokens, 8 KV heads, GQA 4, "
+                        "20 Lloyd iterations on a 65,536-key sample then one full assignment, budget 0.02): "
+                        "index build, step and selection per layer; 0 skips it")
     p.add_argument("--e2e-layers", type=int, default=32,
                    help="end-to-end leg: a random-init Llama-3-8B-shaped model of this many layers prefills "
                         "--e2e-context tokens through the drop-in cache (index built on the side stream during "
@@ -109,6 +115,7 @@ def parse():
         args.online_layers = 0
         args.host_tier_layers = 0
         args.config3_layers = 0
+        args.config4_layers = 0
         if not args.e2e_only:
             args.e2e_layers = 0
     return args
@@ -291,6 +298,11 @@ def main():
         config3 = config3_leg(args, capture)
         log(f"[bench] configs[3] leg: {config3}")
 
+    config4 = None
+    if args.config4_layers > 0:
+        config4 = config4_leg(args, capture)
+        log(f"[bench] configs[4] leg: {config4}")
+
     used_graph = graph is not None
     e2e = None
     if args.e2e_layers > 0:
@@ -346,6 +358,7 @@ def main():
         "online_update": online,
         "host_tier": host_tier,
         "config3": config3,
+        "config4": config4,
         "e2e": e2e,
     }
     print(json.dumps(result), flush=True)
@@ -698,6 +711,84 @@ def config3_leg(args, capture):
             "us_per_layer_step": round(step_us, 2), "select_us": round(sel_us, 2),
             "attended_rows_per_layer": rows,
             "clock": "HIP events around graphs of every layer's step (or its selection phase)"}
+
+
+def config4_leg(args, capture):
+    """The configs[4] index build and decode step (2 x 128 IMI over 8 KV heads
+    at 1,048,576 tokens, GQA 4: 20 Lloyd iterations on an evenly strided
+    65,536-key sample, then one assignment of every key, budget 0.02) on
+    config4_layers layers: the build per layer on HIP events around it, and
+    per layer-step times of graphs of every layer's step and of its
+    selection and split-pass phases, as the main run times configs[1]."""
+    import torch
+
+    from adaptiveimi_amd import ops, synthetic
+    from adaptiveimi_amd.sizing import decode_sizing
+
+    w = WORKLOADS["config4"]
+    dev = torch.device("cuda:0")
+    H, G, D, NL = w["kv_heads"], w["groups"], 128, args.config4_layers
+    ks = tuple(w["ks"])
+    static_total = args.static_start + args.static_end
+    T = w["context"] - static_total
+    sz = decode_sizing(T, w["budget"], subspace_parts=len(ks), k_override=ks)
+    bud = ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"])
+    static_cap, static_len = static_total + 256, static_total + 1
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    plans, build_ms = [], []
+    for layer in range(NL):
+        keys, values = synthetic.make_kv(H, w["context"], seed=4000 + layer, device="cuda")
+        mid_k = keys[:, args.static_start:w["context"] - args.static_end]
+        mid_v = values[:, args.static_start:w["context"] - args.static_end]
+        sk = torch.zeros((H, static_cap, D), dtype=torch.bfloat16, device=dev)
+        sv = torch.zeros_like(sk)
+        sk[:, :static_total] = torch.cat([keys[:, :args.static_start], keys[:, w["context"] - args.static_end:]], 1)
+        sv[:, :static_total] = torch.cat([values[:, :args.static_start],
+                                          values[:, w["context"] - args.static_end:]], 1)
+        sk[:, static_total] = keys[:, -1]
+        sv[:, static_total] = values[:, -1]
+        torch.cuda.synchronize()
+        e0.record()
+        cent, labels, _ = ops.kmeans_sampled(mid_k, list(ks), w["iters"], w["sample"], init=args.kmeans_init)
+        idx = ops.build_index(mid_k, mid_v, cent, labels, list(ks), compact=False)
+        e1.record()
+        torch.cuda.synchronize()
+        build_ms.append(e0.elapsed_time(e1))
+        q = synthetic.make_queries(mid_k, G, seed=layer)[0]
+        plan = ops.DecodePlan(cent, idx["cell_count"], idx["cell_offset"], ks, bud, idx["list_keys"],
+                              idx["list_values"], sk, sv, G, query=q.contiguous())
+        plan.set_static_len(static_len)
+        plans.append(plan)
+        del keys, values, mid_k, mid_v, labels
+    torch.cuda.synchronize()
+
+    def per_layer_us(fn, reps):
+        g = capture(fn)
+        g.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * NL)
+
+    reps = max(args.steps, 5)
+    step_us = per_layer_us(lambda: [p.step() for p in plans], reps)
+    sel_us = per_layer_us(lambda: [p.step(phases=1) for p in plans], reps)
+    split_us = per_layer_us(lambda: [p.step(phases=4) for p in plans], reps)
+    rows = sum(int(p.selection["n_rows"].sum().item()) + H * static_len for p in plans) / NL
+    del plans
+    torch.cuda.empty_cache()
+    gbps = rows * 2 * D * 2 / (split_us * 1e-6) / 1e9
+    return {"layers": NL, "kv_heads": H, "q_heads": H * G, "context": w["context"], "ks": list(ks),
+            "kmeans": f"{w['iters']} Lloyd iterations on a {w['sample']}-key sample, then every key",
+            "nprobe": bud.nprobe, "max_tokens": bud.max_tokens, "buffer_pages": bud.buffer_pages,
+            "index_build_ms_per_layer": round(statistics.median(build_ms), 2),
+            "us_per_layer_step": round(step_us, 2), "select_us": round(sel_us, 2),
+            "split_pass_us": round(split_us, 2), "attended_rows_per_layer": rows,
+            "split_pass_hbm_frac": round(gbps / 8000.0, 4),
+            "clock": "HIP events around each build and around graphs of every layer's step (or one phase)"}
 
 
 def host_tier_leg(args, ks, bud, static_total):
