@@ -31,6 +31,8 @@ def test_default_workload_is_the_north_star(monkeypatch):
     assert (a.layers, a.context, a.kv_heads, a.groups, tuple(a.ks), a.iters, a.budget) == \
         (32, 131072, 8, 4, (64, 64), 10, 0.1)
     assert a.cpu_baseline == 1 and a.online_layers == 4
+    # the legs on the other shapes ride in the default line, two layers each
+    assert (a.config3_layers, a.config4_layers, a.host_tier_layers) == (2, 2, 2)
     # the end-to-end configs[1] leg: 32 layers, 131072-token prompt, 256 decode tokens
     assert (a.e2e_layers, a.e2e_context, a.e2e_decode) == (32, 131072, 256)
     import bench
@@ -44,6 +46,7 @@ def test_other_workloads_and_overrides(monkeypatch):
     assert (a.layers, a.context, a.batch, a.groups, tuple(a.ks), a.fixed_tokens, a.budget) == \
         (16, 262144, 2, 8, (32, 32, 32, 32), 4096, None)
     assert a.cpu_baseline == 0 and a.online_layers == 0 and a.e2e_layers == 0   # quoted on the default workload only
+    assert a.config3_layers == 0 and a.config4_layers == 0 and a.host_tier_layers == 0
     a = _parse(monkeypatch, ["--workload", "config2"])
     assert (a.layers, a.kv_heads, a.groups, a.batch, tuple(a.contexts), tuple(a.ks), a.budget) == \
         (28, 4, 7, 4, (32768, 65536, 98304, 131072), (64, 64), 0.1)
