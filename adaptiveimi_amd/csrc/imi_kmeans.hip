@@ -511,6 +511,12 @@ __global__ __launch_bounds__(256, 4) void km_assign_screen_kernel(KmParams a, in
             uint32_t nib = 0u;
 #pragma unroll
             for (int r = 0; r < 4; ++r) nib |= ev[ct][r] >= lim ? (1u << r) : 0u;
+            if (all) {
+                // every real centroid: past 1e37 the screen's products and
+                // norms can overflow to inf or NaN where a distance does not
+                const int c0 = 16 * ct + 4 * (lane >> 4);
+                nib = KT > 0 ? 0xFu : (c0 >= k ? 0u : (k - c0 >= 4 ? 0xFu : (1u << (k - c0)) - 1u));
+            }
             m[ct >> 1] |= nib << ((ct & 1) * 16 + 4 * (lane >> 4));
         }
 #pragma unroll

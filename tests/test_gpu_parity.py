@@ -71,6 +71,34 @@ def test_assign_bit_exact(ops, oracle, T, k, parts, integer):
     assert none is None and np.array_equal(lab2.cpu().numpy(), labels)
 
 
+@pytest.mark.parametrize("log2_scale", [40, 60, -60, -70])
+def test_assign_bit_exact_extreme_magnitudes(ops, oracle, log2_scale):
+    """Keys and centroids scaled by 2^s (exact in bf16 and fp32): 2^40 keeps
+    the screen's bound finite; 2^60 puts |x|^2 + max |c|^2 past 1e37, where
+    every centroid is a candidate; 2^-60 and 2^-70 make the matrix-core
+    screen values and the halved |c|^2 subnormal, where the bound's absolute
+    term takes over.  Labels and minimum distances equal the oracle's."""
+    note(f"[assign-scale] 2^{log2_scale}")
+    H, T, k, parts = 2, 2000, 64, 2
+    keys, _ = _kv(H, T, seed=31)
+    scale = 2.0 ** log2_scale
+    keys = (keys.float() * scale).to(torch.bfloat16)
+    rng = np.random.default_rng(31)
+    Dp = 128 // parts
+    cent = (rng.standard_normal((H, parts, k, Dp)) * 2 * scale).astype(np.float32)
+    labels, mind = ops.kmeans_assign(keys.to(DEV), torch.from_numpy(cent).to(DEV), [k] * parts)
+    labels, mind = labels.cpu().numpy(), mind.cpu().numpy()
+    kf = oracle.bf16_to_f32(bits(keys))
+    for h in range(H):
+        for p in range(parts):
+            sub = np.ascontiguousarray(kf[h][:, p * Dp:(p + 1) * Dp])
+            ref, rmind, _ = oracle.estep(sub, cent[h, p])
+            assert np.array_equal(labels[h, p], ref), (h, p)
+            assert np.array_equal(mind[h, p].view(np.uint32), rmind.view(np.uint32)), (h, p)
+    lab2, _ = ops.kmeans_assign(keys.to(DEV), torch.from_numpy(cent).to(DEV), [k] * parts, with_distance=False)
+    assert np.array_equal(lab2.cpu().numpy(), labels)
+
+
 @pytest.mark.parametrize("T,k,iters", [(4096, 64, 10), (2500, 32, 6), (300, 64, 4),
                                        (6000, 362, 3)])   # the 2-way adaptive k at 2M tokens
 def test_kmeans_full_run_bit_exact(ops, oracle, T, k, iters):
