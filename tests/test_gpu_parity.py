@@ -138,6 +138,27 @@ def test_kmeans_plusplus_bit_exact(ops, oracle, T, ks, iters):
             assert np.array_equal(labels[h, p], labs[p]), (h, p)
 
 
+@pytest.mark.parametrize("init,log2_scale", [("first", 60), ("first", 62), ("first", -70),
+                                              ("kmeans++", 60), ("kmeans++", 62), ("kmeans++", -70)])
+def test_kmeans_extreme_magnitudes(ops, oracle, init, log2_scale):
+    """Whole Lloyd runs on keys scaled by 2^s: at 2^60 and 2^62 squared
+    norms and some distances overflow (the E-step's every-centroid path, the
+    kmeans++ sums past the exact-integer test), at 2^-70 the distances are
+    subnormal.  Labels and centroids equal the oracle's bit for bit."""
+    note(f"[kmeans-scale] init={init} 2^{log2_scale}")
+    H, T, k, iters = 2, 1500, 32, 3
+    keys, _ = _kv(H, T, seed=41)
+    keys = (keys.float() * 2.0 ** log2_scale).to(torch.bfloat16)
+    cent, labels, _ = ops.kmeans(keys.to(DEV), [k, k], iters, init=init)
+    cent, labels = cent.cpu().numpy(), labels.cpu().numpy()
+    kf = oracle.bf16_to_f32(bits(keys))
+    for h in range(H):
+        labs, cents, _ = oracle.kmeans_head(kf[h], [k, k], iters, init=init, mstep_threads=1)
+        for p in range(2):
+            assert np.array_equal(labels[h, p], labs[p]), (h, p)
+            assert np.array_equal(cent[h, p, :k].view(np.uint32), np.asarray(cents[p], np.float32).view(np.uint32)), (h, p)
+
+
 def test_kmeans_plusplus_init_only_with_duplicates(ops, oracle):
     """Initial centroids alone (one Lloyd iteration is compared through its
     labels) on data with many duplicate rows, so min distances of 0 occur and
