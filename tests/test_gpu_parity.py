@@ -661,6 +661,43 @@ def test_decode_step_matches_oracle(ops, oracle, T, ks, G, static_len, tiles, bu
     _check_attention(res, ref)
 
 
+@pytest.mark.parametrize("log2_scale", [-40, 4, 12])
+def test_decode_step_scaled_queries(ops, oracle, log2_scale):
+    """Queries scaled by 2^s: tiny scores (2^-40), a sharp softmax (2^4)
+    and one whose logits reach ~1e8 (2^12, a single dominant row per query):
+    the selection stays bit-exact and the attention within tolerance."""
+    note(f"[decode-scale] 2^{log2_scale}")
+    from adaptiveimi_amd import synthetic
+
+    H, T, ks, G, static_len = 4, 12000, (32, 32), 4, 96
+    keys, values, cent, out = _index(ops, H, T, ks, 55)
+    sk, sv = synthetic.make_kv(H, static_len + 8, seed=78)
+    sz = oracle.sizing(T, 0.1, k_override=ks)
+    bud = ops.Budget(sz["nprobe"], sz["max_tokens"], sz["buffer_pages"])
+    plan = ops.DecodePlan(cent, out["cell_count"], out["cell_offset"], ks, bud, out["list_keys"],
+                          out["list_values"], sk.to(DEV), sv.to(DEV), G)
+    plan.set_static_len(static_len)
+    q = (synthetic.make_queries(keys, G, seed=5)[0].float() * 2.0 ** log2_scale).to(torch.bfloat16)
+    plan.query.copy_(q.to(DEV))
+    res = plan.step().clone()
+    torch.cuda.synchronize()
+    heads = []
+    for h in range(H):
+        na = int(out["n_active"][h])
+        heads.append(dict(n_active=na, offsets=out["compact_offset"][h, : na + 1].cpu().numpy(),
+                          merged=out["compact_centroids"][h, :na].cpu().numpy(),
+                          list_keys=bits(out["list_keys"][h]), list_values=bits(out["list_values"][h])))
+    ref, rs, rm, rrows = oracle.decode_step(bits(q), heads, bits(sk), bits(sv), static_len, sz["n_centroids"],
+                                            bud.nprobe, bud.max_tokens, bud.buffer_pages)
+    sel = plan.selection
+    assert np.array_equal(sel["n_selected"].cpu().numpy(), rm)
+    gids = out["compact_gid"].cpu().numpy()
+    cells = sel["sel_cell"].cpu().numpy()
+    for h in range(H):
+        assert np.array_equal(cells[h, : rm[h]], gids[h][rs[h, : rm[h]]]), h
+    _check_attention(res, ref)
+
+
 def test_config3_shape_decode_matches_oracle(ops, oracle):
     """configs[3] per sequence: 4-way IMI with 32 centroids per subspace (a
     1,048,576-cell space), 262,048 listed tokens per KV head (over 200k
