@@ -832,6 +832,8 @@ def test_config4_build_and_decode_match_oracle(ops, oracle):
 
 @pytest.mark.parametrize("ks,lens", [((32, 32), (3000, 6000, 9000, 12000)), ((6, 6, 6, 6), (3000, 6000, 9000, 12000)),
                                      ((32, 32), (2000, 12000)), ((32, 32), (3000, 4500, 6000, 9000, 12000)),
+                                     # a 40:1 length ratio, and seven sequences of close lengths
+                                     ((32, 32), (1500, 60000)), ((16, 16), (1200, 1300, 1400, 1500, 1600, 1700, 1800)),
                                      # configs[2] at its own lengths (32k-128k, 64 x 64, 16 KV heads, GQA 7)
                                      ((64, 64), (32768 - 96, 65536 - 96, 98304 - 96, 131072 - 96))])
 def test_ragged_batch_decode_matches_oracle(ops, oracle, ks, lens):
